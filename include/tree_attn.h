@@ -1,0 +1,146 @@
+/* tree_attn.h — C ABI of the MI355X tree-attention engine (gfx950, HIP).
+ *
+ * Every pointer argument is a DEVICE pointer allocated and owned by the caller
+ * unless stated otherwise; `stream` is a hipStream_t passed as void*. Calls
+ * only enqueue work on `stream` (no host synchronisation, no allocation: the
+ * caller supplies every workspace). Arguments are validated on the host before
+ * any HIP call; a failed check returns a negative TT_E_* code and launches
+ * nothing. No C++ exception crosses this boundary. The library keeps no
+ * mutable global state.
+ *
+ * Visibility model. A problem has n_q query tokens (the DFS-packed tokens of
+ * one tree or one partition) and n_keys = n_past + n_q keys: first the
+ * gateway ("past") keys, then the query tokens themselves. Key j is visible to
+ * query i iff  key_lo[j] <= i < key_hi[j]. For the tree's own tokens this is
+ * the closed form of the reference's dense mask, mask[i,j] <=> j <= i < h[j]
+ * with h[j] the exclusive end of the subtree of j's node; a gateway key is
+ * visible to every query or to none.
+ */
+#ifndef TREE_ATTN_H
+#define TREE_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    TT_OK = 0,
+    TT_E_ARG = -1,          /* bad size, null pointer, stride or layout */
+    TT_E_UNSUPPORTED = -2,  /* dtype / head_dim / head ratio not built */
+    TT_E_HIP = -3,          /* a HIP launch failed */
+    TT_E_WORKSPACE = -4     /* workspace or plan buffer too small */
+};
+
+enum { TT_DTYPE_F32 = 0, TT_DTYPE_BF16 = 1 };
+
+/* Device-side status bits written by tt_meta_build / tt_keys_build. */
+enum {
+    TT_STATUS_BAD_LEN = 1,      /* a node with length < 1 */
+    TT_STATUS_BAD_PARENT = 2,   /* parent not in [-1, self) (not DFS pre-order) */
+    TT_STATUS_BAD_TOTAL = 4,    /* sum of node lengths != n_tokens */
+    TT_STATUS_BAD_BIAS = 8      /* a gateway bias that is neither 0 nor -inf */
+};
+
+int tt_abi_version(void);
+const char* tt_strerror(int code);
+
+/* ---- (1) DFS metadata -----------------------------------------------------
+ * Replaces build_dfs_tree_info (dfs_tree_forward.py:91-184): depth-based
+ * positions (:113-139) and, instead of the dense [N,N] mask (:161-172), the
+ * per-token subtree horizon h. Also the per-partition position offset of
+ * tree_grad_hybrid.py:307-310 (pos_offset).
+ * Input: node_len[n_nodes], node_parent[n_nodes] in DFS pre-order
+ * (parent < child, -1 for a root). Output (int32):
+ *   node_start[n], node_off[n] (sum of ancestor lengths), node_hend[n]
+ *   (exclusive end token of the node's subtree), pos[T] = pos_offset +
+ *   node_off + offset-in-node, node_of[T], horizon[T] = node_hend[node_of].
+ * status: one device int32, OR-ed with TT_STATUS_* bits (caller zeroes it).
+ */
+size_t tt_meta_workspace_bytes(int32_t n_nodes);
+int tt_meta_build(const int32_t* node_len, const int32_t* node_parent, int32_t n_nodes,
+                  int32_t n_tokens, int32_t pos_offset,
+                  int32_t* node_start, int32_t* node_off, int32_t* node_hend,
+                  int32_t* pos, int32_t* node_of, int32_t* horizon, int32_t* status,
+                  void* ws, size_t ws_bytes, void* stream);
+
+/* Per-key visible query intervals for [gateway | own] keys. Replaces the
+ * additive mask assembly of tree_grad_hybrid.py:312-317 and
+ * dfs_tree_forward.py:548-550: past_bias[j] (0 or -inf, float32, may be NULL
+ * when n_past == 0) -> [0, n_q) or empty; own key j -> [j, horizon[j]). */
+int tt_keys_build(const float* past_bias, int32_t n_past, const int32_t* horizon, int32_t n_q,
+                  int32_t* key_lo, int32_t* key_hi, int32_t* status, void* stream);
+
+/* Dense expansion mask[i, j] = key_lo[j] <= i < key_hi[j] as uint8 [n_q, n_keys]:
+ * the reference's attn_mask_bool (dfs_tree_forward.py:161-172) for
+ * compatibility and parity checks; the attention path never builds it. */
+int tt_meta_dense_mask(const int32_t* key_lo, const int32_t* key_hi, int32_t n_keys, int32_t n_q,
+                       uint8_t* mask, void* stream);
+
+/* ---- tile plan -------------------------------------------------------------
+ * Block-sparsity map of the (query block x key tile) grid: empty tiles are
+ * skipped, full tiles run unmasked, partial tiles apply the interval test in
+ * the tile. Opaque device buffer; its first 8 bytes hold the uint64 count of
+ * visible (query, key) pairs per head, P = sum_j |[lo_j,hi_j) & [0,n_q)|. */
+size_t tt_plan_bytes(int32_t n_q, int32_t n_keys);
+int tt_plan_build(const int32_t* key_lo, const int32_t* key_hi, int32_t n_keys, int32_t n_q,
+                  void* plan, size_t plan_bytes, void* stream);
+
+/* ---- (2)+(3) tree-masked GQA attention -------------------------------------
+ * Replaces repeat_kv + F.scaled_dot_product_attention(attn_mask=dense) and its
+ * autograd backward (transformers integrations/sdpa_attention.py:79-175,
+ * models/qwen3/modeling_qwen3.py:173-207) as called from Qwen3Attention
+ * (models/qwen3/modeling_qwen3.py:262-276), and GatewayCache.update's cat of
+ * gateway KV with new KV (tree_grad_ckpt_opath.py:92-114): the gateway is
+ * the `k_past/v_past` segment, read in place. */
+typedef struct tt_tensor {
+    const void* ptr;        /* element [t][h][d] at ptr + t*stride_tok + h*stride_head + d */
+    int64_t stride_tok;     /* in elements */
+    int64_t stride_head;    /* in elements */
+} tt_tensor;
+
+typedef struct tt_attn_problem {
+    int32_t dtype;          /* TT_DTYPE_BF16 or TT_DTYPE_F32; every tensor has it */
+    int32_t n_q;            /* query tokens (= own keys) */
+    int32_t n_past;         /* gateway keys, 0 for none */
+    int32_t n_heads_q;      /* Hq */
+    int32_t n_heads_kv;     /* Hkv, Hq % Hkv == 0 (GQA: q head h reads kv head h / (Hq/Hkv)) */
+    int32_t head_dim;       /* 128 */
+    float scale;            /* softmax scale, head_dim ** -0.5 in Qwen3 */
+    int32_t reserved;
+    tt_tensor q, k, v;      /* q: n_q x Hq; k, v: n_q x Hkv */
+    tt_tensor k_past, v_past; /* n_past x Hkv; ignored when n_past == 0 */
+    const int32_t* key_lo;  /* [n_past + n_q] */
+    const int32_t* key_hi;
+    const void* plan;       /* built by tt_plan_build for (key_lo, key_hi) */
+    size_t plan_bytes;
+} tt_attn_problem;
+
+/* o: [n_q, Hq, head_dim] contiguous, problem dtype; lse: [Hq, n_q] float32
+ * (natural-log softmax normaliser, saved for the backward). */
+int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* stream);
+
+/* Backward for upstream gradient d_o (n_q x Hq, strides given). Writes
+ * dq [n_q,Hq,D], dk/dv [n_q,Hkv,D] (contiguous, problem dtype, overwritten).
+ * Gateway gradients are ADDED in float32 to dk_past_acc/dv_past_acc
+ * [n_past, Hkv, D] contiguous (the fp32 hook accumulation of
+ * tree_grad_hybrid.py:220-225, kept on the device); pass NULL to drop them.
+ * Deterministic: no atomics, every output element has one writer. */
+size_t tt_attn_bwd_workspace_bytes(const tt_attn_problem* p);
+int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_tensor d_o,
+                void* dq, void* dk, void* dv, float* dk_past_acc, float* dv_past_acc,
+                void* ws, size_t ws_bytes, void* stream);
+
+/* ---- device self-test ----------------------------------------------------
+ * No counterpart in the reference. Runs one v_mfma_f32_32x32x16_bf16 with the
+ * operand and accumulator lane layout the bf16 kernels assume:
+ * d[32x32] = a[32x16] @ b[16x32], all row-major (a, b bf16; d float32). */
+int tt_selftest_mfma32(const void* a, const void* b, float* d, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TREE_ATTN_H */

@@ -1,0 +1,99 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+header declares, and rejects bad arguments on the host before any launch."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from tree_training_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    src = open(os.path.join(ROOT, "include", "tree_attn.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(tt_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_exports_match_header():
+    lib = _lib.lib()
+    declared = header_symbols()
+    assert declared == sorted(_lib.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_version_and_strerror():
+    lib = _lib.lib()
+    assert lib.tt_abi_version() == _lib.ABI_VERSION
+    for code in (0, -1, -2, -3, -4, -99):
+        assert lib.tt_strerror(code)
+
+
+def _problem(**kw):
+    p = _lib.TTAttnProblem(dtype=_lib.TT_DTYPE_BF16, n_q=100, n_past=0, n_heads_q=32, n_heads_kv=8,
+                           head_dim=128, scale=128 ** -0.5, reserved=0,
+                           q=_lib.TTTensor(16, 32 * 128, 128), k=_lib.TTTensor(16, 8 * 128, 128),
+                           v=_lib.TTTensor(16, 8 * 128, 128), k_past=_lib.TTTensor(None, 128, 128),
+                           v_past=_lib.TTTensor(None, 128, 128), key_lo=16, key_hi=16, plan=16,
+                           plan_bytes=_lib.lib().tt_plan_bytes(100, 100))
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("head_dim", 64, _lib.TT_E_UNSUPPORTED),
+    ("dtype", 7, _lib.TT_E_UNSUPPORTED),
+    ("n_heads_kv", 5, _lib.TT_E_UNSUPPORTED),
+    ("n_q", 0, _lib.TT_E_ARG),
+    ("scale", float("nan"), _lib.TT_E_ARG),
+    ("scale", -1.0, _lib.TT_E_ARG),
+    ("plan_bytes", 10, _lib.TT_E_WORKSPACE),
+    ("key_lo", None, _lib.TT_E_ARG),
+    ("n_past", 3, _lib.TT_E_ARG),            # past segment without pointers
+])
+def test_attn_fwd_validation(field, value, code):
+    lib = _lib.lib()
+    p = _problem(**{field: value})
+    assert lib.tt_attn_fwd(ctypes.byref(p), ctypes.c_void_p(16), ctypes.c_void_p(16), None) == code
+
+
+def test_attn_stride_and_alignment_validation():
+    lib = _lib.lib()
+    p = _problem(q=_lib.TTTensor(16, 100, 128))         # stride not a multiple of 8
+    assert lib.tt_attn_fwd(ctypes.byref(p), ctypes.c_void_p(16), ctypes.c_void_p(16), None) == _lib.TT_E_ARG
+    p = _problem(q=_lib.TTTensor(18, 32 * 128, 128))    # not 16-byte aligned
+    assert lib.tt_attn_fwd(ctypes.byref(p), ctypes.c_void_p(16), ctypes.c_void_p(16), None) == _lib.TT_E_ARG
+    p = _problem()
+    assert lib.tt_attn_fwd(ctypes.byref(p), None, ctypes.c_void_p(16), None) == _lib.TT_E_ARG
+
+
+def test_bwd_validation():
+    lib = _lib.lib()
+    p = _problem()
+    ws = lib.tt_attn_bwd_workspace_bytes(ctypes.byref(p))
+    assert ws >= 32 * 100 * 4
+    d_o = _lib.TTTensor(16, 32 * 128, 128)
+    V = ctypes.c_void_p(16)
+    # one gateway accumulator without the other
+    assert lib.tt_attn_bwd(ctypes.byref(p), V, V, d_o, V, V, V, V, None, V, ws, None) == _lib.TT_E_ARG
+    # workspace too small
+    assert lib.tt_attn_bwd(ctypes.byref(p), V, V, d_o, V, V, V, None, None, V, 8, None) == _lib.TT_E_WORKSPACE
+
+
+def test_meta_and_plan_validation():
+    lib = _lib.lib()
+    V = ctypes.c_void_p(16)
+    assert lib.tt_meta_build(V, V, 0, 5, 0, V, V, V, V, V, V, V, V, 1 << 20, None) == _lib.TT_E_ARG
+    assert lib.tt_meta_build(V, V, 3, 2, 0, V, V, V, V, V, V, V, V, 1 << 20, None) == _lib.TT_E_ARG
+    assert lib.tt_meta_build(V, V, 3, 9, 0, V, V, V, V, V, V, V, V, 4, None) == _lib.TT_E_WORKSPACE
+    assert lib.tt_meta_build(V, V, 3, 9, -1, V, V, V, V, V, V, V, V, 1 << 20, None) == _lib.TT_E_ARG
+    assert lib.tt_keys_build(None, 4, V, 9, V, V, V, None) == _lib.TT_E_ARG
+    assert lib.tt_plan_build(V, V, 5, 9, V, 1 << 20, None) == _lib.TT_E_ARG     # fewer keys than queries
+    assert lib.tt_plan_build(V, V, 9, 9, V, 8, None) == _lib.TT_E_WORKSPACE
+    assert lib.tt_plan_bytes(0, 5) == 0
+    assert lib.tt_meta_workspace_bytes(0) == 0
+    assert lib.tt_meta_dense_mask(V, V, 4, 70000, V, None) == _lib.TT_E_UNSUPPORTED

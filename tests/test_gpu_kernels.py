@@ -1,0 +1,193 @@
+"""GPU parity of the HIP kernels against the CPU oracle (through the C ABI)."""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention import attn_bwd, attn_fwd, key_interval_mask, max_rel
+from oracle.tree_meta import mask_from_horizon, meta_closed_form
+from tests.conftest import load_golden
+from tree_training_amd import workloads
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+HQ, HKV, D = 32, 8, 128
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _meta(lens, par, pos_offset=0):
+    from tree_training_amd.meta import TreeMetaDevice
+    return TreeMetaDevice(lens, par, pos_offset=pos_offset, device=DEV, validate=True)
+
+
+# --------------------------------------------------------------------------- MFMA layout
+def test_mfma_layout_selftest():
+    import ctypes
+    from tree_training_amd._lib import lib
+    from tree_training_amd.meta import _ptr, _stream
+    say("selftest mfma32")
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(32, 16, generator=g).bfloat16()
+    b = torch.randn(16, 32, generator=g).bfloat16()
+    da, db = a.to(DEV), b.to(DEV)
+    d = torch.empty(32, 32, device=DEV)
+    assert lib().tt_selftest_mfma32(_ptr(da), _ptr(db), _ptr(d), _stream(torch.device(DEV))) == 0
+    torch.cuda.synchronize()
+    ref = a.float() @ b.float()
+    assert torch.allclose(d.cpu(), ref, atol=1e-4, rtol=1e-4), (d.cpu() - ref).abs().max()
+
+
+# --------------------------------------------------------------------------- metadata
+def test_meta_c1_fixture():
+    spec = load_golden("c1_tree.json")
+    lens = [n["len"] for n in spec["nodes"]]
+    par = [n["parent"] for n in spec["nodes"]]
+    m = _meta(lens, par)
+    assert m.pos.cpu().tolist() == spec["dfs_pos_ids"]
+    assert m.node_hend.cpu().tolist() == spec["chunk_horizon"]
+    assert m.node_start.cpu().tolist() == [b[0] for b in spec["chunk_boundaries"]]
+    from tree_training_amd.meta import KeyPlan
+    kp = KeyPlan(m.horizon, validate=True)
+    assert kp.visible_pairs() == spec["nnz"]
+    cf = meta_closed_form(lens, par)
+    assert np.array_equal(kp.dense_mask().cpu().numpy(), mask_from_horizon(cf["horizon"]))
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_meta_random_forests(seed):
+    lens, par = workloads.random_forest(seed, node_len=(1, 70))
+    say(f"meta random forest seed={seed} n={len(lens)} T={sum(lens)}")
+    off = (seed * 37) % 100
+    m = _meta(lens, par, pos_offset=off)
+    ref = meta_closed_form(lens, par, pos_offset=off)
+    assert np.array_equal(m.pos.cpu().numpy(), ref["pos"])
+    assert np.array_equal(m.horizon.cpu().numpy(), ref["horizon"])
+    assert np.array_equal(m.node_of.cpu().numpy(), ref["node_of"])
+    assert np.array_equal(m.node_off.cpu().numpy(), ref["node_off"])
+
+
+@pytest.mark.parametrize("name", ["agent16k", "rollout48k", "chain", "star"])
+def test_meta_large(name):
+    topo = {
+        "agent16k": lambda: workloads.agent_tree(0),
+        "rollout48k": lambda: workloads.rollout_tree(0),
+        "chain": lambda: ([3] * 3000, [-1] + list(range(2999))),
+        "star": lambda: ([5] + [2] * 5000, [-1] + [0] * 5000),
+    }[name]()
+    lens, par = topo
+    say(f"meta large {name} n={len(lens)} T={sum(lens)}")
+    m = _meta(lens, par)
+    ref = meta_closed_form(lens, par)
+    assert np.array_equal(m.pos.cpu().numpy(), ref["pos"])
+    assert np.array_equal(m.horizon.cpu().numpy(), ref["horizon"])
+    from tree_training_amd.meta import KeyPlan
+    kp = KeyPlan(m.horizon)
+    assert kp.visible_pairs() == workloads.visible_pairs(topo) == int((ref["pos"] + 1).sum())
+
+
+def test_meta_rejects_bad_input():
+    from tree_training_amd.meta import TreeMetaDevice
+    with pytest.raises(ValueError):
+        TreeMetaDevice([2, 3], [-1, 1], device=DEV, validate=True)   # parent not before child
+    with pytest.raises(ValueError):
+        TreeMetaDevice([2, 0, 1], [-1, 0, 0], device=DEV, validate=True)  # empty node
+
+
+# --------------------------------------------------------------------------- attention
+def _qkv(T, Lp, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    # transformers layout: [1, H, T, D] views of token-major storage
+    q = torch.randn(1, T, HQ, D, generator=g).to(dtype)
+    k = torch.randn(1, T, HKV, D, generator=g).to(dtype)
+    v = torch.randn(1, T, HKV, D, generator=g).to(dtype)
+    do = torch.randn(1, T, HQ, D, generator=g).to(dtype)
+    kp = torch.randn(1, Lp, HKV, D, generator=g).to(dtype) if Lp else None
+    vp = torch.randn(1, Lp, HKV, D, generator=g).to(dtype) if Lp else None
+    return q, k, v, do, kp, vp
+
+
+def _run(lens, par, dtype, seed=0, past_vis=None):
+    from tree_training_amd.attention import attn_backward, attn_forward
+    from tree_training_amd.meta import KeyPlan
+    T = sum(lens)
+    Lp = 0 if past_vis is None else len(past_vis)
+    q, k, v, do, kp, vp = _qkv(T, Lp, dtype, seed)
+    m = _meta(lens, par)
+    bias = None
+    if Lp:
+        bias = torch.tensor([0.0 if b else -math.inf for b in past_vis], device=DEV)
+    plan = KeyPlan(m.horizon, bias, validate=True)
+    tr = lambda x: None if x is None else x.to(DEV).transpose(1, 2)
+    scale = D ** -0.5
+    acc = None
+    if Lp:
+        acc = (torch.zeros(Lp, HKV, D, device=DEV), torch.zeros(Lp, HKV, D, device=DEV))
+    o, lse = attn_forward(tr(q), tr(k), tr(v), plan, scale, tr(kp), tr(vp))
+    dq, dk, dv = attn_backward(tr(q), tr(k), tr(v), plan, scale, o, lse, do.to(DEV), tr(kp), tr(vp), acc)
+    torch.cuda.synchronize()
+    # oracle on the same (rounded) inputs, fp64
+    cf = meta_closed_form(lens, par)
+    lo = ([0] * Lp) + list(range(T))
+    hi = ([T if b else 0 for b in (past_vis or [])]) + list(cf["horizon"])
+    mask = key_interval_mask(lo, hi, T)
+    f64 = lambda x: x[0].double().numpy()
+    kk = f64(k) if not Lp else np.concatenate([f64(kp), f64(k)], axis=0)
+    vv = f64(v) if not Lp else np.concatenate([f64(vp), f64(v)], axis=0)
+    ro, rlse = attn_fwd(f64(q), kk, vv, mask, scale)
+    rdq, rdk, rdv = attn_bwd(f64(q), kk, vv, mask, scale, f64(do))
+    out = dict(o=(ro, o.float().cpu().numpy()), lse=(rlse, lse.cpu().numpy()),
+               dq=(rdq, dq.float().cpu().numpy()), dk=(rdk[Lp:], dk.float().cpu().numpy()),
+               dv=(rdv[Lp:], dv.float().cpu().numpy()))
+    if Lp:
+        out["dk_past"] = (rdk[:Lp], acc[0].cpu().numpy())
+        out["dv_past"] = (rdv[:Lp], acc[1].cpu().numpy())
+    return out
+
+
+TOL = {torch.bfloat16: 2e-2, torch.float32: 1e-5}
+
+CASES = {
+    "c1": ([3, 4, 3, 4, 5, 3, 3, 4, 4, 3, 4, 3, 4], [-1, 0, 1, 2, 3, 3, 2, 6, -1, 8, 9, 8, 11]),
+    "single_token": ([1], [-1]),
+    "chain_ragged": ([37, 100, 5, 211], [-1, 0, 1, 2]),
+    "wide": ([130] + [67] * 9, [-1] + [0] * 9),
+    "forest7": workloads.random_forest(7, node_len=(1, 90)),
+    "agent_small": workloads.agent_tree(3, max_tokens=1500),
+}
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("case", list(CASES))
+def test_attention_parity(case, dtype):
+    lens, par = CASES[case]
+    say(f"attention parity case={case} dtype={dtype} T={sum(lens)}")
+    res = _run(lens, par, dtype, seed=sum(map(ord, case)))
+    tol = TOL[dtype]
+    for name, (ref, got) in res.items():
+        if name == "lse":
+            assert np.abs(ref - got).max() < (2e-2 if dtype == torch.bfloat16 else 1e-5), name
+            continue
+        r = max_rel(ref, got)
+        assert r < tol, f"{name}: max_rel {r:.3e} >= {tol}"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_attention_gateway(dtype):
+    lens, par = [40, 70, 33], [-1, 0, 0]
+    rng = np.random.default_rng(5)
+    past_vis = [bool(x) for x in (rng.random(150) < 0.6)]
+    say(f"attention gateway dtype={dtype} Lp={len(past_vis)}")
+    res = _run(lens, par, dtype, seed=11, past_vis=past_vis)
+    tol = TOL[dtype]
+    for name, (ref, got) in res.items():
+        if name == "lse":
+            continue
+        r = max_rel(ref, got)
+        assert r < tol, f"{name}: max_rel {r:.3e} >= {tol}"

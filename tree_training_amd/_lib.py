@@ -1,0 +1,102 @@
+"""ctypes binding of the C ABI in include/tree_attn.h.
+
+The shared library is built in-tree (``python -m tree_training_amd.build``)
+into ``tree_training_amd/lib/libtree_attn.so``. Loading fails loudly when it is
+missing: there is no CPU fallback for any entry point.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libtree_attn.so")
+
+TT_OK = 0
+TT_E_ARG = -1
+TT_E_UNSUPPORTED = -2
+TT_E_HIP = -3
+TT_E_WORKSPACE = -4
+TT_DTYPE_F32 = 0
+TT_DTYPE_BF16 = 1
+TT_STATUS_BAD_LEN = 1
+TT_STATUS_BAD_PARENT = 2
+TT_STATUS_BAD_TOTAL = 4
+TT_STATUS_BAD_BIAS = 8
+
+ABI_VERSION = 1
+
+# Every symbol include/tree_attn.h declares, for the export check.
+EXPORTS = (
+    "tt_abi_version", "tt_strerror", "tt_meta_workspace_bytes", "tt_meta_build", "tt_keys_build",
+    "tt_meta_dense_mask", "tt_plan_bytes", "tt_plan_build", "tt_attn_fwd",
+    "tt_attn_bwd_workspace_bytes", "tt_attn_bwd", "tt_selftest_mfma32",
+)
+
+
+class TTTensor(ctypes.Structure):
+    _fields_ = [("ptr", ctypes.c_void_p), ("stride_tok", ctypes.c_int64), ("stride_head", ctypes.c_int64)]
+
+
+class TTAttnProblem(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("n_q", ctypes.c_int32), ("n_past", ctypes.c_int32),
+        ("n_heads_q", ctypes.c_int32), ("n_heads_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("scale", ctypes.c_float), ("reserved", ctypes.c_int32),
+        ("q", TTTensor), ("k", TTTensor), ("v", TTTensor), ("k_past", TTTensor), ("v_past", TTTensor),
+        ("key_lo", ctypes.c_void_p), ("key_hi", ctypes.c_void_p), ("plan", ctypes.c_void_p),
+        ("plan_bytes", ctypes.c_size_t),
+    ]
+
+
+class TreeAttnError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def _declare(lib):
+    P, I32, SZ, VP = ctypes.c_void_p, ctypes.c_int32, ctypes.c_size_t, ctypes.c_void_p
+    sig = {
+        "tt_abi_version": (ctypes.c_int, []),
+        "tt_strerror": (ctypes.c_char_p, [ctypes.c_int]),
+        "tt_meta_workspace_bytes": (SZ, [I32]),
+        "tt_meta_build": (ctypes.c_int, [P, P, I32, I32, I32, P, P, P, P, P, P, P, P, SZ, VP]),
+        "tt_keys_build": (ctypes.c_int, [P, I32, P, I32, P, P, P, VP]),
+        "tt_meta_dense_mask": (ctypes.c_int, [P, P, I32, I32, P, VP]),
+        "tt_plan_bytes": (SZ, [I32, I32]),
+        "tt_plan_build": (ctypes.c_int, [P, P, I32, I32, P, SZ, VP]),
+        "tt_attn_fwd": (ctypes.c_int, [ctypes.POINTER(TTAttnProblem), P, P, VP]),
+        "tt_attn_bwd_workspace_bytes": (SZ, [ctypes.POINTER(TTAttnProblem)]),
+        "tt_attn_bwd": (ctypes.c_int, [ctypes.POINTER(TTAttnProblem), P, P, TTTensor, P, P, P, P, P, P, SZ,
+                                       VP]),
+        "tt_selftest_mfma32": (ctypes.c_int, [P, P, P, VP]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def lib():
+    """Loads the HIP library (once). Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise TreeAttnError(
+                f"{LIB_PATH} is missing: build it with `python -m tree_training_amd.build` "
+                "(the tree-attention path has no CPU fallback)")
+        l = ctypes.CDLL(LIB_PATH)
+        _declare(l)
+        v = l.tt_abi_version()
+        if v != ABI_VERSION:
+            raise TreeAttnError(f"libtree_attn ABI {v} != expected {ABI_VERSION}; rebuild the library")
+        _lib = l
+    return _lib
+
+
+def check(rc: int, what: str):
+    if rc != TT_OK:
+        msg = lib().tt_strerror(rc).decode()
+        raise TreeAttnError(f"{what} failed: {msg} (code {rc})")

@@ -1,0 +1,173 @@
+"""Tree-masked GQA attention as a torch.autograd.Function over the HIP kernels.
+
+Drop-in replacement for the attention core the reference hands to
+transformers — ``repeat_kv`` + ``F.scaled_dot_product_attention`` with the dense
+additive tree mask, and autograd's backward of it (transformers
+integrations/sdpa_attention.py:79-175 as called by Qwen3Attention,
+models/qwen3/modeling_qwen3.py:262-276) — plus the gateway concatenation of
+``GatewayCache.update`` (tree_grad_ckpt_opath.py:92-114): the gateway K/V are
+a second key segment read in place.
+
+Layouts follow transformers: q [1, Hq, N, D], k/v [1, Hkv, N, D] (any strides
+with D contiguous), output [1, N, Hq, D] contiguous. Gateway K/V are
+[1, Hkv, Lp, D]. When ``gate_acc`` is given, gateway gradients are added in
+float32 to ``gate_acc = (acc_k, acc_v)`` ([Lp, Hkv, D] each) on the device and
+no gradient is returned for the gateway tensors — the contract of the fp32
+hooks of tree_grad_hybrid.py:220-225, without the host round trip.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+
+from ._lib import (TT_DTYPE_BF16, TT_DTYPE_F32, TreeAttnError, TTAttnProblem, TTTensor, check, lib)
+from .meta import KeyPlan, _ptr, _stream
+
+_DTYPES = {torch.bfloat16: TT_DTYPE_BF16, torch.float32: TT_DTYPE_F32}
+
+
+def _layout(x: torch.Tensor, tok_dim: int, head_dim: int) -> Tuple[torch.Tensor, int, int]:
+    """4-D tensor with a contiguous last (head-dim) axis -> (tensor,
+    stride_tok, stride_head) in elements; copies only when the kernels' 16-byte
+    vector alignment would not hold. Strides of size-1 axes are never used."""
+    if x.dim() != 4 or x.shape[0] != 1:
+        raise TreeAttnError(f"expected a 4-D tensor with batch 1, got shape {tuple(x.shape)}")
+
+    def stride(t, d):
+        return t.stride(d) if t.shape[d] > 1 else t.shape[3]
+
+    def ok(t):
+        return (t.stride(3) == 1 and t.data_ptr() % 16 == 0
+                and all(stride(t, d) % 8 == 0 and stride(t, d) >= t.shape[3] for d in (tok_dim, head_dim)))
+
+    if not ok(x):
+        x = x.contiguous()
+    return x, stride(x, tok_dim), stride(x, head_dim)
+
+
+def _hf_view(x: torch.Tensor) -> Tuple[torch.Tensor, int, int]:
+    """[1, H, T, D] (transformers layout)."""
+    return _layout(x, 2, 1)
+
+
+def _tok_view(x: torch.Tensor) -> Tuple[torch.Tensor, int, int]:
+    """[1, T, H, D] (attention-output layout)."""
+    return _layout(x, 1, 2)
+
+
+class _Problem:
+    """Builds the C problem struct for one call (keeps tensors alive)."""
+
+    def __init__(self, q, k, v, kp, vp, plan: KeyPlan, scale: float):
+        if q.dtype not in _DTYPES:
+            raise TreeAttnError(f"unsupported dtype {q.dtype}; the engine is built for bf16 and fp32")
+        for t in (k, v, kp, vp):
+            if t is not None and t.dtype != q.dtype:
+                raise TreeAttnError("q, k, v and gateway tensors must share one dtype")
+        q, qst, qsh = _hf_view(q)
+        k, kst, ksh = _hf_view(k)
+        v, vst, vsh = _hf_view(v)
+        n_past = 0
+        kpt = vpt = TTTensor(None, 128, 128)
+        if kp is not None:
+            kp, kpst, kpsh = _hf_view(kp)
+            vp, vpst, vpsh = _hf_view(vp)
+            n_past = kp.shape[2]
+            kpt = TTTensor(kp.data_ptr(), kpst, kpsh)
+            vpt = TTTensor(vp.data_ptr(), vpst, vpsh)
+        N, Hq, D = q.shape[2], q.shape[1], q.shape[3]
+        if k.shape[2] != N or v.shape[2] != N:
+            raise TreeAttnError("k/v must have the same token count as q (own segment)")
+        if n_past != plan.n_past or N != plan.n_q:
+            raise TreeAttnError(f"plan built for n_q={plan.n_q}, n_past={plan.n_past}; "
+                                f"got n_q={N}, n_past={n_past}")
+        self.keep = (q, k, v, kp, vp, plan)
+        self.N, self.Hq, self.Hkv, self.D, self.n_past = N, Hq, k.shape[1], D, n_past
+        self.dtype = q.dtype
+        self.s = TTAttnProblem(
+            dtype=_DTYPES[q.dtype], n_q=N, n_past=n_past, n_heads_q=Hq, n_heads_kv=k.shape[1],
+            head_dim=D, scale=float(scale), reserved=0,
+            q=TTTensor(q.data_ptr(), qst, qsh), k=TTTensor(k.data_ptr(), kst, ksh),
+            v=TTTensor(v.data_ptr(), vst, vsh), k_past=kpt, v_past=vpt,
+            key_lo=plan.key_lo.data_ptr(), key_hi=plan.key_hi.data_ptr(), plan=plan.plan.data_ptr(),
+            plan_bytes=plan.plan_bytes)
+
+
+def attn_forward(q, k, v, plan: KeyPlan, scale: float, k_past=None, v_past=None):
+    """Returns (o [N, Hq, D], lse [Hq, N] float32)."""
+    pb = _Problem(q, k, v, k_past, v_past, plan, scale)
+    o = torch.empty((pb.N, pb.Hq, pb.D), dtype=pb.dtype, device=q.device)
+    lse = torch.empty((pb.Hq, pb.N), dtype=torch.float32, device=q.device)
+    check(lib().tt_attn_fwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), _stream(q.device)), "tt_attn_fwd")
+    return o, lse
+
+
+def attn_backward(q, k, v, plan: KeyPlan, scale: float, o, lse, d_o, k_past=None, v_past=None,
+                  gate_acc=None):
+    """Returns (dq [N,Hq,D], dk [N,Hkv,D], dv [N,Hkv,D]); gateway grads are
+    added to ``gate_acc`` when given."""
+    pb = _Problem(q, k, v, k_past, v_past, plan, scale)
+    dev = q.device
+    d_o = d_o.reshape(1, pb.N, pb.Hq, pb.D) if d_o.dim() != 4 else d_o
+    d_o, dst, dsh = _tok_view(d_o)
+    dq = torch.empty((pb.N, pb.Hq, pb.D), dtype=pb.dtype, device=dev)
+    dk = torch.empty((pb.N, pb.Hkv, pb.D), dtype=pb.dtype, device=dev)
+    dv = torch.empty((pb.N, pb.Hkv, pb.D), dtype=pb.dtype, device=dev)
+    ws_bytes = lib().tt_attn_bwd_workspace_bytes(ctypes.byref(pb.s))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    acc_k = acc_v = None
+    if gate_acc is not None and pb.n_past > 0:
+        acc_k, acc_v = gate_acc
+        for a in (acc_k, acc_v):
+            if a.dtype != torch.float32 or not a.is_contiguous() or a.numel() != pb.n_past * pb.Hkv * pb.D:
+                raise TreeAttnError("gateway accumulators must be contiguous float32 [Lp, Hkv, D]")
+    rc = lib().tt_attn_bwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), TTTensor(d_o.data_ptr(), dst, dsh),
+                           _ptr(dq), _ptr(dk), _ptr(dv), _ptr(acc_k), _ptr(acc_v), _ptr(ws), ws_bytes,
+                           _stream(dev))
+    check(rc, "tt_attn_bwd")
+    return dq, dk, dv
+
+
+class TreeAttnFunction(torch.autograd.Function):
+    """Autograd node of one tree-attention call; re-entrant under repeated
+    ``backward(retain_graph=True)`` with partial upstream gradients."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, k_past, v_past, plan, scale, gate_acc):
+        o, lse = attn_forward(q, k, v, plan, scale, k_past, v_past)
+        ctx.save_for_backward(q, k, v, k_past, v_past, o, lse)
+        ctx.plan, ctx.scale, ctx.gate_acc = plan, scale, gate_acc
+        return o.view(1, *o.shape)
+
+    @staticmethod
+    def backward(ctx, g_o):
+        q, k, v, k_past, v_past, o, lse = ctx.saved_tensors
+        N, Hq, D = o.shape
+        Hkv = k.shape[1]
+        gate_acc = ctx.gate_acc
+        need_past = k_past is not None and (ctx.needs_input_grad[3] or ctx.needs_input_grad[4])
+        own_acc = None
+        if k_past is not None and gate_acc is None and need_past:
+            Lp = k_past.shape[2]
+            own_acc = (torch.zeros((Lp, Hkv, D), dtype=torch.float32, device=q.device),
+                       torch.zeros((Lp, Hkv, D), dtype=torch.float32, device=q.device))
+        dq, dk, dv = attn_backward(q, k, v, ctx.plan, ctx.scale, o, lse, g_o, k_past, v_past,
+                                   gate_acc if gate_acc is not None else own_acc)
+        dq = dq.view(1, N, Hq, D).transpose(1, 2)
+        dk = dk.view(1, N, Hkv, D).transpose(1, 2)
+        dv = dv.view(1, N, Hkv, D).transpose(1, 2)
+        dkp = dvp = None
+        if own_acc is not None:
+            Lp = k_past.shape[2]
+            dkp = own_acc[0].to(k_past.dtype).view(1, Lp, Hkv, D).transpose(1, 2)
+            dvp = own_acc[1].to(v_past.dtype).view(1, Lp, Hkv, D).transpose(1, 2)
+        return dq, dk, dv, dkp, dvp, None, None, None
+
+
+def tree_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: KeyPlan, scale: float,
+                   k_past: Optional[torch.Tensor] = None, v_past: Optional[torch.Tensor] = None,
+                   gate_acc=None) -> torch.Tensor:
+    """Tree-masked attention: returns [1, N, Hq, D] (the HF attention output)."""
+    return TreeAttnFunction.apply(q, k, v, k_past, v_past, plan, float(scale), gate_acc)

@@ -1,0 +1,173 @@
+// extern "C" entry points: host-side validation, then enqueue-only launches.
+#include <math.h>
+
+#include "tt_common.h"
+#include "tt_internal.h"
+
+namespace {
+
+constexpr int kAbiVersion = 1;
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Validates a problem and fills the kernels' view of it.
+int make_dev(const tt_attn_problem* p, AttnDev* a) {
+    if (!p) return TT_E_ARG;
+    if (p->dtype != TT_DTYPE_BF16 && p->dtype != TT_DTYPE_F32) return TT_E_UNSUPPORTED;
+    if (p->head_dim != 128) return TT_E_UNSUPPORTED;
+    if (p->n_q < 1 || p->n_past < 0 || p->n_heads_q < 1 || p->n_heads_kv < 1) return TT_E_ARG;
+    if (p->n_heads_q % p->n_heads_kv != 0) return TT_E_UNSUPPORTED;
+    if (p->n_heads_q > 65535 || p->n_heads_kv > 65535) return TT_E_ARG;
+    if ((int64_t)p->n_q + p->n_past > 0x3fffffff) return TT_E_ARG;
+    if (!(p->scale > 0.0f) || !isfinite(p->scale)) return TT_E_ARG;
+    if (!p->q.ptr || !p->k.ptr || !p->v.ptr || !p->key_lo || !p->key_hi || !p->plan) return TT_E_ARG;
+    if (p->n_past > 0 && (!p->k_past.ptr || !p->v_past.ptr)) return TT_E_ARG;
+    const int n_keys = p->n_q + p->n_past;
+    if (p->plan_bytes < tt_plan_bytes_impl(p->n_q, n_keys)) return TT_E_WORKSPACE;
+    // bf16 kernels read 16-byte vectors: 8-element granularity for strides.
+    const int64_t gran = p->dtype == TT_DTYPE_BF16 ? 8 : 1;
+    const size_t ealign = p->dtype == TT_DTYPE_BF16 ? 16 : 4;
+    const tt_tensor* ts[5] = {&p->q, &p->k, &p->v, &p->k_past, &p->v_past};
+    const int nt = p->n_past > 0 ? 5 : 3;
+    for (int i = 0; i < nt; ++i) {
+        const tt_tensor* t = ts[i];
+        if (t->stride_tok < 128 || t->stride_head < 128 || (t->stride_tok % gran) || (t->stride_head % gran))
+            return TT_E_ARG;
+        if (!aligned(t->ptr, ealign)) return TT_E_ARG;
+    }
+    a->q = p->q.ptr; a->q_st = p->q.stride_tok; a->q_sh = p->q.stride_head;
+    a->k = p->k.ptr; a->k_st = p->k.stride_tok; a->k_sh = p->k.stride_head;
+    a->v = p->v.ptr; a->v_st = p->v.stride_tok; a->v_sh = p->v.stride_head;
+    a->kp = p->n_past > 0 ? p->k_past.ptr : nullptr;
+    a->kp_st = p->k_past.stride_tok; a->kp_sh = p->k_past.stride_head;
+    a->vp = p->n_past > 0 ? p->v_past.ptr : nullptr;
+    a->vp_st = p->v_past.stride_tok; a->vp_sh = p->v_past.stride_head;
+    a->key_lo = p->key_lo;
+    a->key_hi = p->key_hi;
+    a->n_q = p->n_q;
+    a->n_past = p->n_past;
+    a->n_keys = n_keys;
+    a->hq = p->n_heads_q;
+    a->hkv = p->n_heads_kv;
+    a->rep = p->n_heads_q / p->n_heads_kv;
+    a->n_qb = tt_cdiv(p->n_q, TT_BQ);
+    a->n_kt = tt_cdiv(n_keys, TT_BK);
+    a->scale = p->scale;
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(p->plan);
+    a->row_cnt = reinterpret_cast<const int32_t*>(base + TT_PLAN_HDR);
+    a->row_list = a->row_cnt + a->n_qb;
+    return TT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tt_abi_version(void) { return kAbiVersion; }
+
+const char* tt_strerror(int code) {
+    switch (code) {
+        case TT_OK: return "ok";
+        case TT_E_ARG: return "invalid argument (size, null pointer, stride or alignment)";
+        case TT_E_UNSUPPORTED: return "unsupported configuration (dtype, head_dim != 128, or Hq % Hkv != 0)";
+        case TT_E_HIP: return "HIP kernel launch failed";
+        case TT_E_WORKSPACE: return "workspace or plan buffer too small";
+        default: return "unknown tree-attention error";
+    }
+}
+
+size_t tt_meta_workspace_bytes(int32_t n_nodes) { return tt_meta_ws_bytes_impl(n_nodes); }
+
+int tt_meta_build(const int32_t* node_len, const int32_t* node_parent, int32_t n_nodes, int32_t n_tokens,
+                  int32_t pos_offset, int32_t* node_start, int32_t* node_off, int32_t* node_hend, int32_t* pos,
+                  int32_t* node_of, int32_t* horizon, int32_t* status, void* ws, size_t ws_bytes,
+                  void* stream) {
+    if (n_nodes < 1 || n_tokens < n_nodes || n_tokens > 0x3fffffff || pos_offset < 0) return TT_E_ARG;
+    if (!node_len || !node_parent || !node_start || !node_off || !node_hend || !pos || !horizon || !status ||
+        !ws)
+        return TT_E_ARG;
+    if (ws_bytes < tt_meta_ws_bytes_impl(n_nodes)) return TT_E_WORKSPACE;
+    return tt_meta_build_impl(node_len, node_parent, n_nodes, n_tokens, pos_offset, node_start, node_off,
+                              node_hend, pos, node_of, horizon, status, ws, (hipStream_t)stream);
+}
+
+int tt_keys_build(const float* past_bias, int32_t n_past, const int32_t* horizon, int32_t n_q, int32_t* key_lo,
+                  int32_t* key_hi, int32_t* status, void* stream) {
+    if (n_q < 1 || n_past < 0 || (int64_t)n_q + n_past > 0x3fffffff) return TT_E_ARG;
+    if ((n_past > 0 && !past_bias) || !horizon || !key_lo || !key_hi || !status) return TT_E_ARG;
+    return tt_keys_build_impl(past_bias, n_past, horizon, n_q, key_lo, key_hi, status, (hipStream_t)stream);
+}
+
+int tt_meta_dense_mask(const int32_t* key_lo, const int32_t* key_hi, int32_t n_keys, int32_t n_q, uint8_t* mask,
+                       void* stream) {
+    if (n_keys < 1 || n_q < 1 || !key_lo || !key_hi || !mask) return TT_E_ARG;
+    if (n_q > 65535) return TT_E_UNSUPPORTED;   // one grid row per query
+    return tt_dense_mask_impl(key_lo, key_hi, n_keys, n_q, mask, (hipStream_t)stream);
+}
+
+size_t tt_plan_bytes(int32_t n_q, int32_t n_keys) {
+    if (n_q < 1 || n_keys < 1) return 0;
+    return tt_plan_bytes_impl(n_q, n_keys);
+}
+
+int tt_plan_build(const int32_t* key_lo, const int32_t* key_hi, int32_t n_keys, int32_t n_q, void* plan,
+                  size_t plan_bytes, void* stream) {
+    if (n_q < 1 || n_keys < n_q || n_keys > 0x3fffffff || !key_lo || !key_hi || !plan) return TT_E_ARG;
+    if (plan_bytes < tt_plan_bytes_impl(n_q, n_keys)) return TT_E_WORKSPACE;
+    return tt_plan_build_impl(key_lo, key_hi, n_keys, n_q, plan, (hipStream_t)stream);
+}
+
+int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* stream) {
+    AttnDev a;
+    int rc = make_dev(p, &a);
+    if (rc != TT_OK) return rc;
+    if (!o || !lse) return TT_E_ARG;
+    if (p->dtype == TT_DTYPE_BF16) {
+        if (!aligned(o, 16)) return TT_E_ARG;
+        return tt_fwd_bf16_launch(a, o, lse, (hipStream_t)stream);
+    }
+    return tt_fwd_f32_launch(a, o, lse, (hipStream_t)stream);
+}
+
+size_t tt_attn_bwd_workspace_bytes(const tt_attn_problem* p) {
+    if (!p || p->n_q < 1 || p->n_heads_q < 1) return 0;
+    return (size_t)p->n_heads_q * (size_t)p->n_q * sizeof(float) + 256;
+}
+
+int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_tensor d_o, void* dq, void* dk,
+                void* dv, float* dk_past_acc, float* dv_past_acc, void* ws, size_t ws_bytes, void* stream) {
+    AttnDev a;
+    int rc = make_dev(p, &a);
+    if (rc != TT_OK) return rc;
+    if (!o || !lse || !d_o.ptr || !dq || !dk || !dv || !ws) return TT_E_ARG;
+    if ((dk_past_acc == nullptr) != (dv_past_acc == nullptr)) return TT_E_ARG;
+    if (ws_bytes < tt_attn_bwd_workspace_bytes(p)) return TT_E_WORKSPACE;
+    const int64_t gran = p->dtype == TT_DTYPE_BF16 ? 8 : 1;
+    const size_t ealign = p->dtype == TT_DTYPE_BF16 ? 16 : 4;
+    if (d_o.stride_tok < 128 || d_o.stride_head < 128 || (d_o.stride_tok % gran) || (d_o.stride_head % gran))
+        return TT_E_ARG;
+    if (!aligned(d_o.ptr, ealign) || !aligned(o, ealign) || !aligned(dq, ealign) || !aligned(dk, ealign) ||
+        !aligned(dv, ealign) || !aligned(ws, 4))
+        return TT_E_ARG;
+    BwdDev b;
+    b.o = o;
+    b.lse = lse;
+    b.dout = d_o.ptr;
+    b.do_st = d_o.stride_tok;
+    b.do_sh = d_o.stride_head;
+    b.dq = dq;
+    b.dk = dk;
+    b.dv = dv;
+    b.dk_acc = p->n_past > 0 ? dk_past_acc : nullptr;
+    b.dv_acc = p->n_past > 0 ? dv_past_acc : nullptr;
+    b.delta = reinterpret_cast<float*>(ws);
+    if (p->dtype == TT_DTYPE_BF16) return tt_bwd_bf16_launch(a, b, (hipStream_t)stream);
+    return tt_bwd_f32_launch(a, b, (hipStream_t)stream);
+}
+
+int tt_selftest_mfma32(const void* a, const void* b, float* d, void* stream) {
+    if (!a || !b || !d || !aligned(a, 2) || !aligned(b, 2) || !aligned(d, 4)) return TT_E_ARG;
+    return tt_selftest_mfma_launch(a, b, d, (hipStream_t)stream);
+}
+
+}  // extern "C"

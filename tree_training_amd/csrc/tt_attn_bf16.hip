@@ -1,0 +1,546 @@
+// Tree-masked GQA flash attention for gfx950, bf16 in / fp32 accumulate.
+//
+// Forward and dQ pass (query-major): a workgroup owns TT_BQ = 128 queries of
+// one q head; each of its four waves keeps 32 queries in registers and walks
+// the non-empty key tiles of the plan. Scores are computed transposed,
+// S^T = K Q^T with v_mfma_f32_32x32x16_bf16, so a lane owns one query column:
+// the online-softmax row max needs a single cross-half exchange and the
+// probabilities feed O^T = V^T P^T straight from the accumulators. V (and K
+// for dQ) is staged in LDS transposed ([d][key]) so every MFMA operand is a
+// pair of 8-byte LDS reads.
+//
+// dK/dV pass (key-major): a workgroup owns TT_BKB = 128 keys of one kv head;
+// each wave keeps K and V of 32 keys as MFMA operands and dK, dV of those
+// keys in fp32 accumulators, and walks the contiguous range of queries that
+// can see them (for a DFS-packed tree, [first key, subtree end)) for the
+// Hq/Hkv q heads of the group. Q and dO blocks are staged natural and
+// transposed. No atomics: each output element has exactly one writer.
+//
+// Visibility: key j is seen by query i iff key_lo[j] <= i < key_hi[j]; the
+// plan marks each (query block, key tile) empty (skipped), full (no mask) or
+// partial (interval test per element).
+#include "tt_common.h"
+#include "tt_internal.h"
+
+namespace {
+
+typedef __bf16 bf16;
+
+constexpr int D = 128;
+constexpr int KS = D + 8;          // natural [key][d] row stride (elements): 272 B
+constexpr int VS = TT_BK + 8;      // transposed [d][key] row stride: 144 B
+constexpr int TS = TT_BQB + 8;     // transposed [d][query] row stride: 80 B
+
+__device__ __forceinline__ bf16x8 zero8() {
+    bf16x8 z;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) z[i] = (bf16)0.0f;
+    return z;
+}
+
+__device__ __forceinline__ const bf16* key_row(const AttnDev& a, int kk, int g, bool isv) {
+    if (kk < a.n_past) {
+        return isv ? (const bf16*)a.vp + kk * a.vp_st + g * a.vp_sh
+                   : (const bf16*)a.kp + kk * a.kp_st + g * a.kp_sh;
+    }
+    const int64_t t = kk - a.n_past;
+    return isv ? (const bf16*)a.v + t * a.v_st + g * a.v_sh : (const bf16*)a.k + t * a.k_st + g * a.k_sh;
+}
+
+// Natural [64 keys][D] tile: thread t loads key t/4, d in [32*(t%4), +32).
+__device__ __forceinline__ void load_keys_natural(const AttnDev& a, int kt, int g, bool isv, bf16* dst) {
+    const int t = threadIdx.x;
+    const int kr = t >> 2, seg = (t & 3) * 32;
+    const int kk = kt * TT_BK + kr;
+    bf16x8 x[4];
+    if (kk < a.n_keys) {
+        const bf16* src = key_row(a, kk, g, isv) + seg;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = *(const bf16x8*)(src + 8 * i);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = zero8();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *(bf16x8*)(dst + kr * KS + seg + 8 * i) = x[i];
+}
+
+// Transposed [D][64 keys] tile: thread t loads keys 4*(t/16)..+3 at
+// d in [8*(t%16), +8) and writes eight 4-key rows.
+__device__ __forceinline__ void load_keys_transposed(const AttnDev& a, int kt, int g, bool isv, bf16* dst) {
+    const int t = threadIdx.x;
+    const int dc = (t & 15) * 8, kg = (t >> 4) * 4;
+    bf16x8 x[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int kk = kt * TT_BK + kg + i;
+        x[i] = (kk < a.n_keys) ? *(const bf16x8*)(key_row(a, kk, g, isv) + dc) : zero8();
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        bf16x4 w;
+        w[0] = x[0][e]; w[1] = x[1][e]; w[2] = x[2][e]; w[3] = x[3][e];
+        *(bf16x4*)(dst + (dc + e) * VS + kg) = w;
+    }
+}
+
+__device__ __forceinline__ void load_key_bounds(const AttnDev& a, int kt, int* s_lo, int* s_hi) {
+    const int t = threadIdx.x;
+    if (t < TT_BK) {
+        const int kk = kt * TT_BK + t;
+        s_lo[t] = kk < a.n_keys ? a.key_lo[kk] : 0;
+        s_hi[t] = kk < a.n_keys ? a.key_hi[kk] : 0;
+    }
+}
+
+// Lane's 32 query-column scores -> -inf where the key is invisible.
+__device__ __forceinline__ void mask_scores(f32x16 (&s)[2], const int* s_lo, const int* s_hi, int qi, int half) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+        for (int grp = 0; grp < 4; ++grp) {
+            const int k0 = 32 * b + 8 * grp + 4 * half;
+            const i32x4 lo = *(const i32x4*)(s_lo + k0);
+            const i32x4 hi = *(const i32x4*)(s_hi + k0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const bool vis = lo[e] <= qi && qi < hi[e];
+                s[b][4 * grp + e] = vis ? s[b][4 * grp + e] : -INFINITY;
+            }
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------
+// forward
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void fwd_bf16_kernel(AttnDev a, bf16* __restrict__ out, float* __restrict__ lse) {
+    __shared__ __attribute__((aligned(16))) bf16 Ks[TT_BK * KS];
+    __shared__ __attribute__((aligned(16))) bf16 Vt[D * VS];
+    __shared__ __attribute__((aligned(16))) int s_lo[TT_BK];
+    __shared__ __attribute__((aligned(16))) int s_hi[TT_BK];
+
+    const int qb = blockIdx.x, h = blockIdx.y, g = h / a.rep;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int col = lane & 31, half = lane >> 5;
+    const int qi = qb * TT_BQ + wave * 32 + col;
+    const float c = a.scale * TT_LOG2E;
+
+    bf16x8 qa[8];
+    if (qi < a.n_q) {
+        const bf16* qp = (const bf16*)a.q + qi * a.q_st + h * a.q_sh + 8 * half;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) qa[t] = *(const bf16x8*)(qp + 16 * t);
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) qa[t] = zero8();
+    }
+
+    f32x16 o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = (f32x16){};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    const int cnt = a.row_cnt[qb];
+    const int* list = a.row_list + (size_t)qb * a.n_kt;
+    for (int it = 0; it < cnt; ++it) {
+        const int ent = list[it];
+        const int kt = ent >> 1;
+        const bool full = ent & 1;
+        __syncthreads();
+        load_keys_natural(a, kt, g, false, Ks);
+        load_keys_transposed(a, kt, g, true, Vt);
+        load_key_bounds(a, kt, s_lo, s_hi);
+        __syncthreads();
+
+        f32x16 s[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            s[b] = (f32x16){};
+            const bf16* kr = Ks + (32 * b + col) * KS + 8 * half;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) s[b] = mfma32(*(const bf16x8*)(kr + 16 * t), qa[t], s[b]);
+        }
+        if (!full) mask_scores(s, s_lo, s_hi, qi, half);
+
+        float mx = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx * c);
+        const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+        const float alpha = fast_exp2(m_run - m_use);
+        float psum = 0.0f;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = fast_exp2(fmaf(s[b][r], c, -m_use));
+                s[b][r] = p;
+                psum += p;
+            }
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db) o[db] *= alpha;
+        }
+
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const f32x16& pb = s[st >> 1];
+            const int r0 = 8 * (st & 1);
+            const bf16x8 pk = pack8(pb[r0 + 0], pb[r0 + 1], pb[r0 + 2], pb[r0 + 3], pb[r0 + 4], pb[r0 + 5],
+                                    pb[r0 + 6], pb[r0 + 7]);
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const bf16* vr = Vt + (32 * db + col) * VS + 16 * st + 4 * half;
+                const bf16x8 va = cat44(*(const bf16x4*)vr, *(const bf16x4*)(vr + 8));
+                o[db] = mfma32(va, pk, o[db]);
+            }
+        }
+    }
+
+    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    if (qi < a.n_q) {
+        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        bf16* op = out + ((size_t)qi * a.hq + h) * D;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int grp = 0; grp < 4; ++grp) {
+                bf16x4 w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[e] = (bf16)(o[db][4 * grp + e] * inv);
+                *(bf16x4*)(op + 32 * db + 8 * grp + 4 * half) = w;
+            }
+        if (half == 0) {
+            const float m_fin = (m_run == -INFINITY) ? 0.0f : m_run;
+            lse[(size_t)h * a.n_q + qi] = l_tot > 0.0f ? (m_fin + __log2f(l_tot)) * TT_LN2 : -INFINITY;
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------
+// backward: delta = rowsum(dO * O)
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void bwd_delta_bf16_kernel(AttnDev a, BwdDev b) {
+    const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int sub = threadIdx.x & 15;
+    const int total = a.n_q * a.hq;
+    float acc = 0.0f;
+    int i = 0, h = 0;
+    if (row < total) {
+        i = row / a.hq;
+        h = row - i * a.hq;
+        const bf16x8 ov = *(const bf16x8*)((const bf16*)b.o + ((size_t)i * a.hq + h) * D + 8 * sub);
+        const bf16x8 dv = *(const bf16x8*)((const bf16*)b.dout + i * b.do_st + h * b.do_sh + 8 * sub);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += (float)ov[e] * (float)dv[e];
+    }
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+    if (row < total && sub == 0) b.delta[(size_t)h * a.n_q + i] = acc;
+}
+
+// ----------------------------------------------------------------------------
+// backward: dQ (query-major, same tiling as the forward)
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void bwd_dq_bf16_kernel(AttnDev a, BwdDev bw) {
+    __shared__ __attribute__((aligned(16))) bf16 Ks[TT_BK * KS];
+    __shared__ __attribute__((aligned(16))) bf16 Vs[TT_BK * KS];
+    __shared__ __attribute__((aligned(16))) bf16 Kt[D * VS];
+    __shared__ __attribute__((aligned(16))) int s_lo[TT_BK];
+    __shared__ __attribute__((aligned(16))) int s_hi[TT_BK];
+
+    const int qb = blockIdx.x, h = blockIdx.y, g = h / a.rep;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int col = lane & 31, half = lane >> 5;
+    const int qi = qb * TT_BQ + wave * 32 + col;
+    const float c = a.scale * TT_LOG2E;
+
+    bf16x8 qa[8], da[8];
+    float lse2 = INFINITY, dlt = 0.0f;
+    if (qi < a.n_q) {
+        const bf16* qp = (const bf16*)a.q + qi * a.q_st + h * a.q_sh + 8 * half;
+        const bf16* dp = (const bf16*)bw.dout + qi * bw.do_st + h * bw.do_sh + 8 * half;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            qa[t] = *(const bf16x8*)(qp + 16 * t);
+            da[t] = *(const bf16x8*)(dp + 16 * t);
+        }
+        lse2 = bw.lse[(size_t)h * a.n_q + qi] * TT_LOG2E;
+        dlt = bw.delta[(size_t)h * a.n_q + qi];
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) { qa[t] = zero8(); da[t] = zero8(); }
+    }
+
+    f32x16 dq[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dq[i] = (f32x16){};
+
+    const int cnt = a.row_cnt[qb];
+    const int* list = a.row_list + (size_t)qb * a.n_kt;
+    for (int it = 0; it < cnt; ++it) {
+        const int ent = list[it];
+        const int kt = ent >> 1;
+        const bool full = ent & 1;
+        __syncthreads();
+        load_keys_natural(a, kt, g, false, Ks);
+        load_keys_natural(a, kt, g, true, Vs);
+        load_keys_transposed(a, kt, g, false, Kt);
+        load_key_bounds(a, kt, s_lo, s_hi);
+        __syncthreads();
+
+        f32x16 s[2], dp[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            s[b] = (f32x16){};
+            dp[b] = (f32x16){};
+            const bf16* kr = Ks + (32 * b + col) * KS + 8 * half;
+            const bf16* vr = Vs + (32 * b + col) * KS + 8 * half;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                s[b] = mfma32(*(const bf16x8*)(kr + 16 * t), qa[t], s[b]);
+                dp[b] = mfma32(*(const bf16x8*)(vr + 16 * t), da[t], dp[b]);
+            }
+        }
+        if (!full) mask_scores(s, s_lo, s_hi, qi, half);
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = fast_exp2(fmaf(s[b][r], c, -lse2));
+                s[b][r] = p * (dp[b][r] - dlt);   // dS^T
+            }
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const f32x16& sb = s[st >> 1];
+            const int r0 = 8 * (st & 1);
+            const bf16x8 pk = pack8(sb[r0 + 0], sb[r0 + 1], sb[r0 + 2], sb[r0 + 3], sb[r0 + 4], sb[r0 + 5],
+                                    sb[r0 + 6], sb[r0 + 7]);
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const bf16* kr = Kt + (32 * db + col) * VS + 16 * st + 4 * half;
+                const bf16x8 ka = cat44(*(const bf16x4*)kr, *(const bf16x4*)(kr + 8));
+                dq[db] = mfma32(ka, pk, dq[db]);
+            }
+        }
+    }
+
+    if (qi < a.n_q) {
+        bf16* op = (bf16*)bw.dq + ((size_t)qi * a.hq + h) * D;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int grp = 0; grp < 4; ++grp) {
+                bf16x4 w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[e] = (bf16)(dq[db][4 * grp + e] * a.scale);
+                *(bf16x4*)(op + 32 * db + 8 * grp + 4 * half) = w;
+            }
+    }
+}
+
+// ----------------------------------------------------------------------------
+// backward: dK, dV (key-major)
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void bwd_dkdv_bf16_kernel(AttnDev a, BwdDev bw) {
+    __shared__ __attribute__((aligned(16))) bf16 Qs[TT_BQB * KS];
+    __shared__ __attribute__((aligned(16))) bf16 Ds[TT_BQB * KS];
+    __shared__ __attribute__((aligned(16))) bf16 Qt[D * TS];
+    __shared__ __attribute__((aligned(16))) bf16 Dt[D * TS];
+    __shared__ __attribute__((aligned(16))) float s_lse[TT_BQB];
+    __shared__ __attribute__((aligned(16))) float s_dlt[TT_BQB];
+    __shared__ int s_rng[2];
+
+    const int kb = blockIdx.x, g = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int col = lane & 31, half = lane >> 5;
+    const int kk = kb * TT_BKB + wave * 32 + col;   // this lane's key (MFMA column)
+    const float c = a.scale * TT_LOG2E;
+
+    int lo = 0, hi = 0;
+    bf16x8 kbv[8], vbv[8];
+    if (kk < a.n_keys) {
+        lo = max(a.key_lo[kk], 0);
+        hi = min(a.key_hi[kk], a.n_q);
+        const bf16* kp = key_row(a, kk, g, false) + 8 * half;
+        const bf16* vp = key_row(a, kk, g, true) + 8 * half;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            kbv[t] = *(const bf16x8*)(kp + 16 * t);
+            vbv[t] = *(const bf16x8*)(vp + 16 * t);
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) { kbv[t] = zero8(); vbv[t] = zero8(); }
+    }
+    if (lo >= hi) { lo = a.n_q; hi = 0; }      // invisible key: neutral for min/max
+    const int w_lo = wave_min_i(lo), w_hi = wave_max_i(hi);
+    const int w_maxlo = wave_max_i(lo < hi ? lo : -1), w_minhi = wave_min_i(lo < hi ? hi : -1);
+    const bool w_all_vis = wave_min_i((kk < a.n_keys && lo < hi) ? 1 : 0) == 1;
+
+    if (threadIdx.x == 0) { s_rng[0] = a.n_q; s_rng[1] = 0; }
+    __syncthreads();
+    if (lane == 0) { atomicMin(&s_rng[0], w_lo); atomicMax(&s_rng[1], w_hi); }
+    __syncthreads();
+    const int q_begin = (s_rng[0] / TT_BQB) * TT_BQB, q_end = s_rng[1];
+
+    f32x16 dk[4], dv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { dk[i] = (f32x16){}; dv[i] = (f32x16){}; }
+
+    for (int q0 = q_begin; q0 < q_end; q0 += TT_BQB) {
+        const int q1 = min(q0 + TT_BQB, a.n_q);
+        const bool active = (q0 < w_hi) && (q1 > w_lo);
+        const bool full = w_all_vis && (w_maxlo <= q0) && (w_minhi >= q1);
+        for (int hh = 0; hh < a.rep; ++hh) {
+            const int h = g * a.rep + hh;
+            __syncthreads();
+            {   // stage Q (threads 0..127) and dO (128..255), natural and transposed
+                const int t = threadIdx.x & 127;
+                const bool isd = threadIdx.x >= 128;
+                const int dc = (t & 15) * 8, rg = (t >> 4) * 4;
+                bf16x8 x[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int qq = q0 + rg + i;
+                    if (qq < a.n_q) {
+                        const bf16* src = isd ? (const bf16*)bw.dout + qq * bw.do_st + h * bw.do_sh
+                                              : (const bf16*)a.q + qq * a.q_st + h * a.q_sh;
+                        x[i] = *(const bf16x8*)(src + dc);
+                    } else {
+                        x[i] = zero8();
+                    }
+                }
+                bf16* nat = isd ? Ds : Qs;
+                bf16* tr = isd ? Dt : Qt;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) *(bf16x8*)(nat + (rg + i) * KS + dc) = x[i];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    bf16x4 w;
+                    w[0] = x[0][e]; w[1] = x[1][e]; w[2] = x[2][e]; w[3] = x[3][e];
+                    *(bf16x4*)(tr + (dc + e) * TS + rg) = w;
+                }
+                if (threadIdx.x < TT_BQB) {
+                    const int qq = q0 + threadIdx.x;
+                    s_lse[threadIdx.x] = qq < a.n_q ? bw.lse[(size_t)h * a.n_q + qq] * TT_LOG2E : INFINITY;
+                } else if (threadIdx.x >= 64 && threadIdx.x < 64 + TT_BQB) {
+                    const int qq = q0 + threadIdx.x - 64;
+                    s_dlt[threadIdx.x - 64] = qq < a.n_q ? bw.delta[(size_t)h * a.n_q + qq] : 0.0f;
+                }
+            }
+            __syncthreads();
+            if (!active) continue;
+
+            // S = Q K^T and dP = dO V^T: rows = queries, lane = key column.
+            f32x16 s = (f32x16){}, dp = (f32x16){};
+            const bf16* qr = Qs + col * KS + 8 * half;
+            const bf16* dr = Ds + col * KS + 8 * half;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                s = mfma32(*(const bf16x8*)(qr + 16 * t), kbv[t], s);
+                dp = mfma32(*(const bf16x8*)(dr + 16 * t), vbv[t], dp);
+            }
+#pragma unroll
+            for (int grp = 0; grp < 4; ++grp) {
+                const int r0 = 8 * grp + 4 * half;
+                const f32x4 l2 = *(const f32x4*)(s_lse + r0);
+                const f32x4 dl = *(const f32x4*)(s_dlt + r0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int qq = q0 + r0 + e;
+                    float p = fast_exp2(fmaf(s[4 * grp + e], c, -l2[e]));
+                    if (!full) p = (lo <= qq && qq < hi) ? p : 0.0f;
+                    s[4 * grp + e] = p;                         // P
+                    dp[4 * grp + e] = p * (dp[4 * grp + e] - dl[e]);  // dS
+                }
+            }
+            // dV += P^T dO, dK += dS^T Q: contraction over the 32 queries.
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                const int r0 = 8 * st;
+                const bf16x8 pa = pack8(s[r0 + 0], s[r0 + 1], s[r0 + 2], s[r0 + 3], s[r0 + 4], s[r0 + 5],
+                                        s[r0 + 6], s[r0 + 7]);
+                const bf16x8 sa = pack8(dp[r0 + 0], dp[r0 + 1], dp[r0 + 2], dp[r0 + 3], dp[r0 + 4],
+                                        dp[r0 + 5], dp[r0 + 6], dp[r0 + 7]);
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    const bf16* dtr = Dt + (32 * db + col) * TS + 16 * st + 4 * half;
+                    const bf16* qtr = Qt + (32 * db + col) * TS + 16 * st + 4 * half;
+                    const bf16x8 dob = cat44(*(const bf16x4*)dtr, *(const bf16x4*)(dtr + 8));
+                    const bf16x8 qbb = cat44(*(const bf16x4*)qtr, *(const bf16x4*)(qtr + 8));
+                    dv[db] = mfma32(pa, dob, dv[db]);
+                    dk[db] = mfma32(sa, qbb, dk[db]);
+                }
+            }
+        }
+    }
+
+    // Epilogue: rows of dk/dv = this wave's keys, columns = d.
+    const int kbase = kb * TT_BKB + wave * 32;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int key = kbase + acc_row(r, half);
+        if (key >= a.n_keys) continue;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const int d = 32 * db + col;
+            const float gk = dk[db][r] * a.scale, gv = dv[db][r];
+            if (key < a.n_past) {
+                if (bw.dk_acc) {
+                    const size_t idx = ((size_t)key * a.hkv + g) * D + d;
+                    bw.dk_acc[idx] += gk;
+                    bw.dv_acc[idx] += gv;
+                }
+            } else {
+                const size_t idx = ((size_t)(key - a.n_past) * a.hkv + g) * D + d;
+                ((bf16*)bw.dk)[idx] = (bf16)gk;
+                ((bf16*)bw.dv)[idx] = (bf16)gv;
+            }
+        }
+    }
+}
+
+// Device self-test of the MFMA lane layout every bf16 kernel above relies on:
+// D = A[32x16] * B[16x32] (row-major bf16), written back through acc_row().
+__global__ __launch_bounds__(64) void selftest_mfma_kernel(const bf16* __restrict__ A, const bf16* __restrict__ B,
+                                                           float* __restrict__ Dm) {
+    const int lane = threadIdx.x, col = lane & 31, half = lane >> 5;
+    bf16x8 av, bv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        av[e] = A[col * 16 + 8 * half + e];
+        bv[e] = B[(8 * half + e) * 32 + col];
+    }
+    const f32x16 acc = mfma32(av, bv, (f32x16){});
+#pragma unroll
+    for (int r = 0; r < 16; ++r) Dm[acc_row(r, half) * 32 + col] = acc[r];
+}
+
+}  // namespace
+
+int tt_selftest_mfma_launch(const void* a, const void* b, float* d, hipStream_t s) {
+    hipLaunchKernelGGL(selftest_mfma_kernel, dim3(1), dim3(64), 0, s, (const bf16*)a, (const bf16*)b, d);
+    return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
+}
+
+int tt_fwd_bf16_launch(const AttnDev& a, void* o, float* lse, hipStream_t s) {
+    hipLaunchKernelGGL(fwd_bf16_kernel, dim3(a.n_qb, a.hq), dim3(256), 0, s, a, (bf16*)o, lse);
+    return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
+}
+
+int tt_bwd_bf16_launch(const AttnDev& a, const BwdDev& b, hipStream_t s) {
+    const int rows = a.n_q * a.hq;
+    hipLaunchKernelGGL(bwd_delta_bf16_kernel, dim3(tt_cdiv(rows, 16)), dim3(256), 0, s, a, b);
+    if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+    hipLaunchKernelGGL(bwd_dq_bf16_kernel, dim3(a.n_qb, a.hq), dim3(256), 0, s, a, b);
+    if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+    hipLaunchKernelGGL(bwd_dkdv_bf16_kernel, dim3(tt_cdiv(a.n_keys, TT_BKB), a.hkv), dim3(256), 0, s, a, b);
+    return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
+}

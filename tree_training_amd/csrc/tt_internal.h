@@ -1,0 +1,52 @@
+// Internal launchers shared between the translation units of the library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/tree_attn.h"
+
+// Device-side view of a tt_attn_problem (passed to kernels by value).
+struct AttnDev {
+    const void* q; int64_t q_st, q_sh;
+    const void* k; int64_t k_st, k_sh;
+    const void* v; int64_t v_st, v_sh;
+    const void* kp; int64_t kp_st, kp_sh;
+    const void* vp; int64_t vp_st, vp_sh;
+    const int32_t* key_lo;
+    const int32_t* key_hi;
+    const int32_t* row_cnt;   // plan: per query block, number of key tiles
+    const int32_t* row_list;  // plan: per query block, (kt << 1) | full
+    int n_q, n_past, n_keys, hq, hkv, rep, n_qb, n_kt;
+    float scale;
+};
+
+struct BwdDev {
+    const void* o;            // [n_q, hq, 128] contiguous
+    const float* lse;         // [hq, n_q]
+    const void* dout; int64_t do_st, do_sh;
+    void* dq;                 // [n_q, hq, 128]
+    void* dk;                 // [n_q, hkv, 128]
+    void* dv;
+    float* dk_acc;            // [n_past, hkv, 128] fp32 (+=), may be null
+    float* dv_acc;
+    float* delta;             // workspace [hq, n_q]: rowsum(dO * O)
+};
+
+size_t tt_meta_ws_bytes_impl(int n);
+int tt_meta_build_impl(const int32_t* len, const int32_t* par, int n, int T, int pos_offset, int32_t* start,
+                       int32_t* off, int32_t* hend, int32_t* pos, int32_t* node_of, int32_t* horizon,
+                       int32_t* status, void* ws, hipStream_t s);
+int tt_keys_build_impl(const float* bias, int n_past, const int32_t* horizon, int n_q, int32_t* key_lo,
+                       int32_t* key_hi, int32_t* status, hipStream_t s);
+int tt_dense_mask_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys, int n_q, uint8_t* mask,
+                       hipStream_t s);
+size_t tt_plan_bytes_impl(int n_q, int n_keys);
+int tt_plan_build_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys, int n_q, void* plan,
+                       hipStream_t s);
+
+int tt_fwd_bf16_launch(const AttnDev& a, void* o, float* lse, hipStream_t s);
+int tt_bwd_bf16_launch(const AttnDev& a, const BwdDev& b, hipStream_t s);
+int tt_fwd_f32_launch(const AttnDev& a, void* o, float* lse, hipStream_t s);
+int tt_bwd_f32_launch(const AttnDev& a, const BwdDev& b, hipStream_t s);
+int tt_selftest_mfma_launch(const void* a, const void* b, float* d, hipStream_t s);

@@ -1,0 +1,284 @@
+// DFS tree metadata, per-key visibility intervals and the block-sparsity plan.
+//
+// Replaces build_dfs_tree_info (dfs_tree_forward.py:91-184) and the dense
+// additive-mask assembly (dfs_tree_forward.py:548-550, tree_grad_hybrid.py:312-317).
+// Node-level work (prefix sums over node lengths, ancestor offsets by pointer
+// jumping, subtree ends by a sparse-table next-smaller-or-equal-depth search)
+// runs in one workgroup; token-level work (positions, node ids, horizons) runs
+// one thread per token. All of it is integer work bound by launch latency and
+// HBM, never by arithmetic.
+#include "tt_common.h"
+#include "tt_internal.h"
+
+namespace {
+
+constexpr int kNodeThreads = 1024;
+
+__host__ __device__ inline int sparse_levels(int n) {
+    int L = 1;
+    while ((1 << L) <= n) ++L;   // levels r = 0..L-1 with 2^r <= n
+    return L;
+}
+
+__global__ __launch_bounds__(kNodeThreads) void meta_nodes_kernel(
+    const int32_t* __restrict__ len, const int32_t* __restrict__ par, int n, int T,
+    int32_t* __restrict__ start, int32_t* __restrict__ off, int32_t* __restrict__ hend,
+    int32_t* __restrict__ status, int32_t* __restrict__ ws) {
+    __shared__ int s_scan[kNodeThreads];
+    __shared__ int s_carry;
+    __shared__ int s_err;
+    const int tid = threadIdx.x;
+    int32_t* anc0 = ws;
+    int32_t* anc1 = ws + n;
+    int32_t* offb1 = ws + 2 * n;
+    int32_t* dep0 = ws + 3 * n;
+    int32_t* dep1 = ws + 4 * n;
+    int32_t* st = ws + 5 * n;   // sparse-table levels 1..L-1, n ints each
+    if (tid == 0) { s_carry = 0; s_err = 0; }
+    __syncthreads();
+
+    // 1. exclusive prefix sum of node lengths -> node_start; validate input.
+    for (int base = 0; base < n; base += kNodeThreads) {
+        const int i = base + tid;
+        int v = 0;
+        if (i < n) {
+            v = len[i];
+            int p = par[i];
+            if (v < 1) atomicOr(&s_err, TT_STATUS_BAD_LEN);
+            if (p < -1 || p >= i) atomicOr(&s_err, TT_STATUS_BAD_PARENT);
+        }
+        s_scan[tid] = v;
+        __syncthreads();
+        for (int o = 1; o < kNodeThreads; o <<= 1) {
+            int t = tid >= o ? s_scan[tid - o] : 0;
+            __syncthreads();
+            s_scan[tid] += t;
+            __syncthreads();
+        }
+        if (i < n) start[i] = s_carry + s_scan[tid] - v;
+        __syncthreads();
+        if (tid == kNodeThreads - 1) s_carry += s_scan[tid];
+        __syncthreads();
+    }
+    if (tid == 0 && s_carry != T) atomicOr(&s_err, TT_STATUS_BAD_TOTAL);
+
+    // 2. pointer jumping: off = sum of ancestor lengths, dep = ancestor count.
+    for (int i = tid; i < n; i += kNodeThreads) {
+        int p = par[i];
+        if (p < -1 || p >= i) p = -1;   // flagged above; keep the walk in bounds
+        anc0[i] = p;
+        off[i] = p >= 0 ? len[p] : 0;
+        dep0[i] = p >= 0 ? 1 : 0;
+    }
+    __syncthreads();
+    int32_t* a_cur = anc0; int32_t* a_nxt = anc1;
+    int32_t* o_cur = off;  int32_t* o_nxt = offb1;
+    int32_t* d_cur = dep0; int32_t* d_nxt = dep1;
+    for (;;) {
+        int any = 0;
+        for (int i = tid; i < n; i += kNodeThreads) {
+            int a = a_cur[i];
+            if (a >= 0) {
+                o_nxt[i] = o_cur[i] + o_cur[a];
+                d_nxt[i] = d_cur[i] + d_cur[a];
+                int aa = a_cur[a];
+                a_nxt[i] = aa;
+                any |= (aa >= 0);
+            } else {
+                o_nxt[i] = o_cur[i];
+                d_nxt[i] = d_cur[i];
+                a_nxt[i] = -1;
+            }
+        }
+        any = __syncthreads_or(any);
+        int32_t* t;
+        t = a_cur; a_cur = a_nxt; a_nxt = t;
+        t = o_cur; o_cur = o_nxt; o_nxt = t;
+        t = d_cur; d_cur = d_nxt; d_nxt = t;
+        if (!any) break;
+    }
+    if (o_cur != off) {
+        for (int i = tid; i < n; i += kNodeThreads) off[i] = o_cur[i];
+    }
+    __syncthreads();
+
+    // 3. subtree end = first later node whose depth <= own depth (pre-order).
+    const int L = sparse_levels(n);
+    for (int r = 1; r < L; ++r) {
+        const int32_t* prev = (r == 1) ? d_cur : st + (size_t)(r - 2) * n;
+        int32_t* cur = st + (size_t)(r - 1) * n;
+        const int w = 1 << r, hw = w >> 1;
+        for (int i = tid; i + w <= n; i += kNodeThreads) cur[i] = min(prev[i], prev[i + hw]);
+        __syncthreads();
+    }
+    for (int c = tid; c < n; c += kNodeThreads) {
+        const int thr = d_cur[c];
+        int i = c + 1;
+        for (int r = L - 1; r >= 0; --r) {
+            const int w = 1 << r;
+            if (i + w <= n) {
+                const int32_t* lev = (r == 0) ? d_cur : st + (size_t)(r - 1) * n;
+                if (lev[i] > thr) i += w;
+            }
+        }
+        hend[c] = (i < n) ? start[i] : T;
+    }
+    if (tid == 0 && s_err) atomicOr(status, s_err);
+}
+
+__global__ void meta_tokens_kernel(const int32_t* __restrict__ start, const int32_t* __restrict__ off,
+                                   const int32_t* __restrict__ hend, int n, int T, int pos_offset,
+                                   int32_t* __restrict__ pos, int32_t* __restrict__ node_of,
+                                   int32_t* __restrict__ horizon) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= T) return;
+    int lo = 0, hi = n - 1;          // largest c with start[c] <= i
+    while (lo < hi) {
+        int mid = (lo + hi + 1) >> 1;
+        if (start[mid] <= i) lo = mid; else hi = mid - 1;
+    }
+    pos[i] = pos_offset + off[lo] + (i - start[lo]);
+    if (node_of) node_of[i] = lo;
+    horizon[i] = hend[lo];
+}
+
+__global__ void keys_kernel(const float* __restrict__ bias, int n_past, const int32_t* __restrict__ horizon,
+                            int n_q, int32_t* __restrict__ key_lo, int32_t* __restrict__ key_hi,
+                            int32_t* __restrict__ status) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= n_past + n_q) return;
+    if (j < n_past) {
+        const float b = bias[j];
+        int vis = 0;
+        if (b == 0.0f) vis = 1;
+        else if (!(__builtin_isinf(b) && b < 0.0f)) atomicOr(status, TT_STATUS_BAD_BIAS);
+        key_lo[j] = 0;
+        key_hi[j] = vis ? n_q : 0;
+    } else {
+        const int jj = j - n_past;
+        key_lo[j] = jj;
+        key_hi[j] = horizon[jj];
+    }
+}
+
+__global__ void dense_mask_kernel(const int32_t* __restrict__ key_lo, const int32_t* __restrict__ key_hi,
+                                  int n_keys, int n_q, uint8_t* __restrict__ mask) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    const int i = blockIdx.y;
+    if (j >= n_keys || i >= n_q) return;
+    mask[(size_t)i * n_keys + j] = (key_lo[j] <= i && i < key_hi[j]) ? 1 : 0;
+}
+
+__global__ void plan_header_kernel(uint8_t* plan, int n_qb, int n_kt) {
+    if (threadIdx.x == 0) {
+        *reinterpret_cast<unsigned long long*>(plan) = 0ull;
+        reinterpret_cast<int32_t*>(plan)[2] = n_qb;
+        reinterpret_cast<int32_t*>(plan)[3] = n_kt;
+    }
+}
+
+__global__ void plan_pairs_kernel(const int32_t* __restrict__ key_lo, const int32_t* __restrict__ key_hi,
+                                  int n_keys, int n_q, unsigned long long* __restrict__ pairs) {
+    __shared__ unsigned long long s_sum;
+    if (threadIdx.x == 0) s_sum = 0;
+    __syncthreads();
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    long long c = 0;
+    if (j < n_keys) {
+        int a = max(key_lo[j], 0), b = min(key_hi[j], n_q);
+        c = b > a ? (long long)(b - a) : 0;
+    }
+    atomicAdd(&s_sum, (unsigned long long)c);
+    __syncthreads();
+    if (threadIdx.x == 0 && s_sum) atomicAdd(pairs, s_sum);
+}
+
+__global__ void plan_classify_kernel(const int32_t* __restrict__ key_lo, const int32_t* __restrict__ key_hi,
+                                     int n_keys, int n_q, int n_qb, int n_kt, uint8_t* __restrict__ cls) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n_qb * n_kt) return;
+    const int qb = idx / n_kt, kt = idx - qb * n_kt;
+    const int i0 = qb * TT_BQ, i1 = min(i0 + TT_BQ, n_q);
+    bool any = false, all = true;
+    for (int j = kt * TT_BK; j < kt * TT_BK + TT_BK; ++j) {
+        if (j >= n_keys) { all = false; continue; }
+        const int lo = key_lo[j], hi = key_hi[j];
+        if (max(lo, i0) < min(hi, i1)) any = true;
+        if (!(lo <= i0 && hi >= i1)) all = false;
+    }
+    cls[idx] = any ? (all ? 2 : 1) : 0;
+}
+
+// One wave per query block: compacts the non-empty key tiles, ascending.
+__global__ void plan_compact_kernel(const uint8_t* __restrict__ cls, int n_qb, int n_kt,
+                                    int32_t* __restrict__ row_cnt, int32_t* __restrict__ row_list) {
+    const int row = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+    const int lane = threadIdx.x & 63;
+    if (row >= n_qb) return;
+    int cnt = 0;
+    const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int base = 0; base < n_kt; base += 64) {
+        const int kt = base + lane;
+        const int c = kt < n_kt ? cls[(size_t)row * n_kt + kt] : 0;
+        const unsigned long long m = __ballot(c != 0);
+        if (c) row_list[(size_t)row * n_kt + cnt + __popcll(m & below)] = (kt << 1) | (c == 2 ? 1 : 0);
+        cnt += __popcll(m);
+    }
+    if (lane == 0) row_cnt[row] = cnt;
+}
+
+}  // namespace
+
+size_t tt_meta_ws_bytes_impl(int n) {
+    if (n <= 0) return 0;
+    return (size_t)(5 + sparse_levels(n)) * (size_t)n * sizeof(int32_t) + 256;
+}
+
+int tt_meta_build_impl(const int32_t* len, const int32_t* par, int n, int T, int pos_offset,
+                       int32_t* start, int32_t* off, int32_t* hend, int32_t* pos, int32_t* node_of,
+                       int32_t* horizon, int32_t* status, void* ws, hipStream_t s) {
+    hipLaunchKernelGGL(meta_nodes_kernel, dim3(1), dim3(kNodeThreads), 0, s, len, par, n, T, start, off,
+                       hend, status, reinterpret_cast<int32_t*>(ws));
+    if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+    hipLaunchKernelGGL(meta_tokens_kernel, dim3(tt_cdiv(T, 256)), dim3(256), 0, s, start, off, hend, n, T,
+                       pos_offset, pos, node_of, horizon);
+    return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
+}
+
+int tt_keys_build_impl(const float* bias, int n_past, const int32_t* horizon, int n_q, int32_t* key_lo,
+                       int32_t* key_hi, int32_t* status, hipStream_t s) {
+    const int nk = n_past + n_q;
+    hipLaunchKernelGGL(keys_kernel, dim3(tt_cdiv(nk, 256)), dim3(256), 0, s, bias, n_past, horizon, n_q,
+                       key_lo, key_hi, status);
+    return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
+}
+
+int tt_dense_mask_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys, int n_q, uint8_t* mask,
+                       hipStream_t s) {
+    hipLaunchKernelGGL(dense_mask_kernel, dim3(tt_cdiv(n_keys, 256), n_q), dim3(256), 0, s, key_lo, key_hi,
+                       n_keys, n_q, mask);
+    return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
+}
+
+size_t tt_plan_bytes_impl(int n_q, int n_keys) {
+    const size_t n_qb = (size_t)tt_cdiv(n_q, TT_BQ), n_kt = (size_t)tt_cdiv(n_keys, TT_BK);
+    size_t b = TT_PLAN_HDR + 4 * n_qb + 4 * n_qb * n_kt + n_qb * n_kt;
+    return (b + 255) & ~(size_t)255;
+}
+
+int tt_plan_build_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys, int n_q, void* plan,
+                       hipStream_t s) {
+    const int n_qb = tt_cdiv(n_q, TT_BQ), n_kt = tt_cdiv(n_keys, TT_BK);
+    uint8_t* base = reinterpret_cast<uint8_t*>(plan);
+    int32_t* row_cnt = reinterpret_cast<int32_t*>(base + TT_PLAN_HDR);
+    int32_t* row_list = row_cnt + n_qb;
+    uint8_t* cls = reinterpret_cast<uint8_t*>(row_list + (size_t)n_qb * n_kt);
+    hipLaunchKernelGGL(plan_header_kernel, dim3(1), dim3(64), 0, s, base, n_qb, n_kt);
+    hipLaunchKernelGGL(plan_pairs_kernel, dim3(tt_cdiv(n_keys, 256)), dim3(256), 0, s, key_lo, key_hi, n_keys,
+                       n_q, reinterpret_cast<unsigned long long*>(base));
+    hipLaunchKernelGGL(plan_classify_kernel, dim3(tt_cdiv(n_qb * n_kt, 256)), dim3(256), 0, s, key_lo, key_hi,
+                       n_keys, n_q, n_qb, n_kt, cls);
+    hipLaunchKernelGGL(plan_compact_kernel, dim3(tt_cdiv(n_qb, 4)), dim3(256), 0, s, cls, n_qb, n_kt, row_cnt,
+                       row_list);
+    return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
+}
