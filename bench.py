@@ -1,0 +1,270 @@
+#!/usr/bin/env python3
+"""Tree-attention forward + backward benchmark on one MI355X.
+
+Workload (default ``agent16k``): the synthetic agent-trajectory tree (depth 6,
+branching U{2,3,4}, node lengths U{64..512}, DFS-packed, capped at 16,384
+tokens; seed 0) through one Qwen3-4B-shaped GQA attention layer (32 q heads,
+8 kv heads, head_dim 128), bf16, q/k/v/dO ~ N(0,1) seeded, resident in HBM.
+One step = DFS metadata + tile plan + tree-attention forward + full backward
+(dQ, dK, dV) over the whole packed tree, each through the C ABI.
+
+Metric: useful TFLOP/s = 12 * d * Hq * P / t_step, with P the number of
+ancestor-visible (query, key) pairs per head (flash recompute not counted),
+plus packed tokens/s. The dominant kernel's roofline figure is measured live
+with HIP events on the launch stream; the CPU baseline times the dense-mask
+restatement of the reference path (additive mask + repeat_kv + SDPA + autograd)
+on a bounded sample on the host cores.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload agent16k|gateway16k|rollout48k]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+HQ, HKV, D = 32, 8, 128
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="agent16k", choices=["agent16k", "gateway16k", "rollout48k"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-runs", type=int, default=3)
+    return ap.parse_args()
+
+
+def build_workload(name):
+    from tree_training_amd import workloads
+    if name == "rollout48k":
+        return workloads.rollout_tree(0)
+    return workloads.agent_tree(0)
+
+
+def gateway_split(topo, max_tokens=4096):
+    """Partitions of the tree (tree_grad_hybrid.partition_tree) with their
+    inherited gateway visibility, as (node_len, parent, past_visible, pos_off)."""
+    from tree_training_amd.tree import TreeNode
+    from tree_training_amd.hybrid import hybrid_plan
+    from tree_training_amd.workloads import forest_from_topology
+    roots, _ = forest_from_topology(topo, TreeNode)
+    return hybrid_plan(roots, max_tokens)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the tree-attention path has no multi-GPU mode in this build "
+              "(see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from tree_training_amd import _lib
+    from tree_training_amd.attention import _Problem, attn_forward
+    from tree_training_amd.meta import KeyPlan, TreeMetaDevice, _ptr, _stream
+    from tree_training_amd.workloads import visible_pairs
+    import ctypes
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    topo = build_workload(args.workload)
+    lens, par = topo
+    T = sum(lens)
+    P = visible_pairs(topo)
+    g = torch.Generator(device=dev).manual_seed(0)
+    bf = torch.bfloat16
+    # token-major storage viewed as [1, H, T, D] (transformers layout)
+    q = torch.randn(1, T, HQ, D, device=dev, generator=g, dtype=bf).transpose(1, 2)
+    k = torch.randn(1, T, HKV, D, device=dev, generator=g, dtype=bf).transpose(1, 2)
+    v = torch.randn(1, T, HKV, D, device=dev, generator=g, dtype=bf).transpose(1, 2)
+    do = torch.randn(1, T, HQ, D, device=dev, generator=g, dtype=bf)
+    scale = D ** -0.5
+    lib = _lib.lib()
+    stream = torch.cuda.current_stream(dev)
+
+    segments = None
+    if args.workload == "gateway16k":
+        segments = []
+        for part in gateway_split(topo):
+            n, lp = part["n_tokens"], part["past_len"]
+            seg = dict(part)
+            seg["q"] = torch.randn(1, n, HQ, D, device=dev, generator=g, dtype=bf).transpose(1, 2)
+            seg["k"] = torch.randn(1, n, HKV, D, device=dev, generator=g, dtype=bf).transpose(1, 2)
+            seg["v"] = torch.randn(1, n, HKV, D, device=dev, generator=g, dtype=bf).transpose(1, 2)
+            seg["do"] = torch.randn(1, n, HQ, D, device=dev, generator=g, dtype=bf)
+            if lp:
+                seg["kp"] = torch.randn(1, HKV, lp, D, device=dev, generator=g, dtype=bf)
+                seg["vp"] = torch.randn(1, HKV, lp, D, device=dev, generator=g, dtype=bf)
+                seg["acc"] = (torch.zeros(lp, HKV, D, device=dev), torch.zeros(lp, HKV, D, device=dev))
+                seg["bias_dev"] = seg["bias"].to(dev)
+            segments.append(seg)
+
+    def run_problem(lens_, par_, qq, kk, vv, dd, kp=None, vp=None, bias=None, acc=None, ev=None, pos_off=0):
+        meta = TreeMetaDevice(lens_, par_, pos_offset=pos_off, device=dev)
+        plan = KeyPlan(meta.horizon, bias)
+        pb = _Problem(qq, kk, vv, kp, vp, plan, scale)
+        N = pb.N
+        o = torch.empty((N, HQ, D), dtype=bf, device=dev)
+        lse = torch.empty((HQ, N), dtype=torch.float32, device=dev)
+        dq = torch.empty((N, HQ, D), dtype=bf, device=dev)
+        dk = torch.empty((N, HKV, D), dtype=bf, device=dev)
+        dv = torch.empty((N, HKV, D), dtype=bf, device=dev)
+        ws_bytes = lib.tt_attn_bwd_workspace_bytes(ctypes.byref(pb.s))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        st = _stream(dev)
+        from tree_training_amd.attention import _tok_view
+        dd, dst, dsh = _tok_view(dd)
+        dt = _lib.TTTensor(dd.data_ptr(), dst, dsh)
+        ak, av = (acc if acc is not None else (None, None))
+
+        def rec(i):
+            if ev is not None:
+                ev[i].record(stream)
+        rec(0)
+        _lib.check(lib.tt_attn_fwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), st), "fwd")
+        rec(1)
+        pb.s.bwd_parts = _lib.TT_BWD_DELTA
+        _lib.check(lib.tt_attn_bwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), dt, _ptr(dq), _ptr(dk), _ptr(dv),
+                                   _ptr(ak), _ptr(av), _ptr(ws), ws_bytes, st), "bwd delta")
+        rec(2)
+        pb.s.bwd_parts = _lib.TT_BWD_DQ
+        _lib.check(lib.tt_attn_bwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), dt, _ptr(dq), _ptr(dk), _ptr(dv),
+                                   _ptr(ak), _ptr(av), _ptr(ws), ws_bytes, st), "bwd dq")
+        rec(3)
+        pb.s.bwd_parts = _lib.TT_BWD_DKDV
+        _lib.check(lib.tt_attn_bwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), dt, _ptr(dq), _ptr(dk), _ptr(dv),
+                                   _ptr(ak), _ptr(av), _ptr(ws), ws_bytes, st), "bwd dkdv")
+        rec(4)
+        return o, dq, dk, dv
+
+    def step(ev=None):
+        if segments is None:
+            run_problem(lens, par, q, k, v, do, ev=ev)
+            return
+        for seg in segments:   # partitions in creation order (parents first)
+            run_problem(seg["node_len"], seg["parent"], seg["q"], seg["k"], seg["v"], seg["do"],
+                        seg.get("kp"), seg.get("vp"), seg.get("bias_dev"), seg.get("acc"),
+                        ev=None, pos_off=seg["pos_offset"])
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    start_ev = torch.cuda.Event(enable_timing=True)
+    end_ev = torch.cuda.Event(enable_timing=True)
+    start_ev.record(stream)
+    for i in range(args.steps):
+        step(evs[i] if segments is None else None)
+    end_ev.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = start_ev.elapsed_time(end_ev) / args.steps
+
+    flops = 12.0 * D * HQ * P
+    tflops = flops / (ms_step * 1e-3) / 1e12
+    tokens_s = T / (ms_step * 1e-3)
+    kernels = {}
+    roofline = None
+    if segments is None:
+        names = ["fwd_bf16_kernel", "bwd_delta_bf16_kernel", "bwd_dq_bf16_kernel", "bwd_dkdv_bf16_kernel"]
+        useful = [4.0 * D * HQ * P, 0.0, 4.0 * D * HQ * P, 4.0 * D * HQ * P]
+        for j, name in enumerate(names):
+            ms = statistics.mean(e[j].elapsed_time(e[j + 1]) for e in evs)
+            kernels[name] = {"ms": round(ms, 4),
+                             "useful_tflops": round(useful[j] / (ms * 1e-3) / 1e12, 2) if useful[j] else None}
+        dom = max((n for n in names if kernels[n]["useful_tflops"]), key=lambda n: kernels[n]["ms"])
+        ach = kernels[dom]["useful_tflops"]
+        roofline = {"bound": "mfma", "kernel": dom, "achieved": ach, "peak": PEAK_BF16_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                    "flops_per_launch": useful[names.index(dom)]}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(topo, args.cpu_runs)
+
+    line = {
+        "metric": "tree-attn fwd+bwd useful TFLOP/s (16K-token DFS tree, bf16)",
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded topology and N(0,1) q/k/v/dO)",
+        "config": {"workload": args.workload, "packed_tokens": T, "visible_pairs_per_head": P,
+                   "n_nodes": len(lens), "heads_q": HQ, "heads_kv": HKV, "head_dim": D,
+                   "layer": "one Qwen3-4B-shaped GQA attention layer", "parallelism": "single GPU"},
+        "tokens_per_s": round(tokens_s, 1),
+        "frac_of_bf16_peak": round(tflops / PEAK_BF16_TFLOPS, 4),
+        "wall_s_timed": round(wall, 3),
+        "kernels": kernels,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(topo, runs):
+    """Dense-mask restatement of the reference path on the host cores, on one
+    kv-head group (4 q heads + 1 kv head) of the same tree: median of ``runs``
+    fwd+bwd after one warm-up. Reported in the metric's unit (useful TFLOP/s
+    for the sampled heads)."""
+    import torch
+    from oracle.dense_path import additive_mask, dense_fwd_bwd
+    from oracle.tree_meta import mask_from_horizon, meta_closed_form
+    from tree_training_amd.workloads import visible_pairs
+    cores = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    lens, par = topo
+    m = meta_closed_form(lens, par)
+    T = m["T"]
+    P = visible_pairs(topo)
+    t0 = time.perf_counter()
+    am = additive_mask(torch.from_numpy(mask_from_horizon(m["horizon"])), torch.bfloat16)
+    t_mask = time.perf_counter() - t0
+    g = torch.Generator().manual_seed(0)
+    hq = HQ // HKV
+    q = torch.randn(1, hq, T, D, generator=g).bfloat16()
+    k = torch.randn(1, 1, T, D, generator=g).bfloat16()
+    v = torch.randn(1, 1, T, D, generator=g).bfloat16()
+    do = torch.randn(1, T, hq, D, generator=g).bfloat16()
+    times = []
+    for i in range(runs + 1):
+        t0 = time.perf_counter()
+        dense_fwd_bwd(q, k, v, am, D ** -0.5, do)
+        dt = time.perf_counter() - t0
+        if i:
+            times.append(dt)
+    t = statistics.median(times)
+    useful = 12.0 * D * hq * P
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(useful / t / 1e12, 5), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"1 of 8 kv-head groups (4 q heads) of the full {T}-token tree, dense additive mask + "
+                      f"repeat_kv + SDPA fwd+bwd in bf16 (torch CPU), median of {runs} after 1 warm-up",
+            "seconds_per_sample": round(t, 3), "mask_build_s": round(t_mask, 3),
+            "tokens_per_s_full_layer": round(T / (t * HKV), 1), "cpu_model": model}
+
+
+if __name__ == "__main__":
+    main()

@@ -36,6 +36,14 @@ enum {
 
 enum { TT_DTYPE_F32 = 0, TT_DTYPE_BF16 = 1 };
 
+/* Parts of the backward (tt_attn_problem.bwd_parts); they must run in this
+ * order, each after the previous one on the same stream. */
+enum {
+    TT_BWD_DELTA = 1,   /* rowsum(dO * O) into the workspace */
+    TT_BWD_DQ = 2,      /* dQ (reads the workspace) */
+    TT_BWD_DKDV = 4     /* dK, dV and gateway accumulation (reads the workspace) */
+};
+
 /* Device-side status bits written by tt_meta_build / tt_keys_build. */
 enum {
     TT_STATUS_BAD_LEN = 1,      /* a node with length < 1 */
@@ -109,7 +117,7 @@ typedef struct tt_attn_problem {
     int32_t n_heads_kv;     /* Hkv, Hq % Hkv == 0 (GQA: q head h reads kv head h / (Hq/Hkv)) */
     int32_t head_dim;       /* 128 */
     float scale;            /* softmax scale, head_dim ** -0.5 in Qwen3 */
-    int32_t reserved;
+    int32_t bwd_parts;      /* tt_attn_bwd only: OR of TT_BWD_* (0 = all parts) */
     tt_tensor q, k, v;      /* q: n_q x Hq; k, v: n_q x Hkv */
     tt_tensor k_past, v_past; /* n_past x Hkv; ignored when n_past == 0 */
     const int32_t* key_lo;  /* [n_past + n_q] */

@@ -84,3 +84,28 @@ def c1_spec():
 @pytest.fixture
 def q1_spec():
     return load_golden("q1_chain.json")
+
+
+def qwen3_config(shape="tiny", layers=2, vocab=1000):
+    """Random-init Qwen3 configs: 'tiny' (hidden 512, 4 q / 2 kv heads) or
+    'qwen3_4b' (hidden 2560, 32 q / 8 kv heads, intermediate 9728); head_dim
+    128, RoPE theta 1e6, RMSNorm eps 1e-6 as in Qwen3-4B."""
+    from transformers import Qwen3Config
+    if shape == "qwen3_4b":
+        dims = dict(hidden_size=2560, intermediate_size=9728, num_attention_heads=32, num_key_value_heads=8)
+    else:
+        dims = dict(hidden_size=512, intermediate_size=1024, num_attention_heads=4, num_key_value_heads=2)
+    return Qwen3Config(vocab_size=vocab, num_hidden_layers=layers, head_dim=128, rope_theta=1e6,
+                       rms_norm_eps=1e-6, max_position_embeddings=8192, tie_word_embeddings=False,
+                       attention_dropout=0.0, **dims)
+
+
+def make_qwen3(shape="tiny", layers=2, seed=0):
+    import torch
+    from transformers import Qwen3ForCausalLM
+    torch.manual_seed(seed)
+    cfg = qwen3_config(shape, layers)
+    cfg._attn_implementation = "eager"
+    m = Qwen3ForCausalLM(cfg).float()
+    m.train()
+    return m

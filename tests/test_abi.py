@@ -34,7 +34,7 @@ def test_version_and_strerror():
 
 def _problem(**kw):
     p = _lib.TTAttnProblem(dtype=_lib.TT_DTYPE_BF16, n_q=100, n_past=0, n_heads_q=32, n_heads_kv=8,
-                           head_dim=128, scale=128 ** -0.5, reserved=0,
+                           head_dim=128, scale=128 ** -0.5, bwd_parts=0,
                            q=_lib.TTTensor(16, 32 * 128, 128), k=_lib.TTTensor(16, 8 * 128, 128),
                            v=_lib.TTTensor(16, 8 * 128, 128), k_past=_lib.TTTensor(None, 128, 128),
                            v_past=_lib.TTTensor(None, 128, 128), key_lo=16, key_hi=16, plan=16,

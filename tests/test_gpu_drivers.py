@@ -1,0 +1,155 @@
+"""GPU parity of the drop-in drivers (dfs_tree_forward, tree_grad_ckpt_sequential,
+tree_grad_hybrid) on random-init Qwen3 models against the CPU oracle of the
+reference's dense-mask path, run in float64."""
+import copy
+import sys
+
+import pytest
+import torch
+
+from oracle.attention import max_rel
+from oracle.model_path import dense_leaf_logits, sequential_param_grads
+from tests.conftest import forest_from_spec, load_golden, make_qwen3
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _tree(name):
+    from tree_training_amd.tree import TreeNode
+    spec = load_golden({"c1": "c1_tree.json", "q1": "q1_chain.json"}[name])
+    roots, nodes = forest_from_spec(spec["nodes"], TreeNode)
+    leaves = [n for n in nodes if not n.children]
+    return roots, leaves
+
+
+def _labels(leaves, seed=99, vocab=1000):
+    g = torch.Generator().manual_seed(seed)
+    return {id(n): torch.randint(1, vocab, (len(n.token_ids),), generator=g) for n in leaves}
+
+
+def _grads(model, run):
+    acc, hs = {}, []
+    for name, p in model.named_parameters():
+        def hook(g, name=name):
+            g = g.detach().cpu().double()
+            acc[name] = acc[name] + g if name in acc else g.clone()
+        hs.append(p.register_hook(hook))
+    try:
+        model.zero_grad(set_to_none=True)
+        run()
+        torch.cuda.synchronize()
+    finally:
+        for h in hs:
+            h.remove()
+    return acc
+
+
+def _max_rel_params(ref, new):
+    assert set(ref) == set(new), set(ref) ^ set(new)
+    return max(max_rel(ref[k].numpy(), new[k].numpy()) for k in ref)
+
+
+def _loss_fn(labels, n_leaves):
+    import torch.nn.functional as F
+
+    def fn(logits, node):
+        return F.cross_entropy(logits[0], labels[id(node)].to(logits.device)) / n_leaves
+    return fn
+
+
+def test_c1_qwen3_4b_layer_forward_fp32():
+    """Config 1: the 47-token two-root tree through one Qwen3-4B-shaped layer."""
+    from tree_training_amd.dfs_tree_forward import dfs_tree_forward
+    say("c1 qwen3-4b-shaped layer forward fp32")
+    base = make_qwen3("qwen3_4b", layers=1)
+    ref_model = copy.deepcopy(base).double()
+    model = base.to(DEV)
+    roots, _ = _tree("c1")
+    res = dfs_tree_forward(model, roots)
+    ref_logits, _ = dense_leaf_logits(ref_model, roots)
+    assert len(res.leaf_logits) == len(ref_logits) == 5
+    worst = max(max_rel(r.detach().numpy(), o.detach().cpu().double().numpy())
+                for r, o in zip(ref_logits, res.leaf_logits))
+    assert worst < 1e-5, worst
+    assert res.info.dfs_pos_ids == load_golden("c1_tree.json")["dfs_pos_ids"]
+
+
+def test_c1_qwen3_4b_layer_sequential_grads_fp32():
+    from tree_training_amd.ckpt import tree_grad_ckpt_sequential
+    say("c1 qwen3-4b-shaped layer sequential grads fp32")
+    base = make_qwen3("qwen3_4b", layers=1)
+    ref_model = copy.deepcopy(base).double()
+    model = base.to(DEV)
+    roots, leaves = _tree("c1")
+    labels = _labels(leaves)
+    ref = sequential_param_grads(ref_model, roots, labels, len(leaves))
+    new = _grads(model, lambda: tree_grad_ckpt_sequential(model, roots, _loss_fn(labels, len(leaves))))
+    r = _max_rel_params(ref, new)
+    say(f"  max_rel {r:.3e}")
+    assert r < 1e-5, r
+
+
+@pytest.mark.parametrize("max_tokens", [1000, 20, 10])
+def test_hybrid_grads_fp32(max_tokens):
+    from tree_training_amd.hybrid import tree_grad_hybrid
+    say(f"hybrid fp32 max_tokens={max_tokens}")
+    base = make_qwen3("tiny", layers=2)
+    ref_model = copy.deepcopy(base).double()
+    model = base.to(DEV)
+    roots, leaves = _tree("c1")
+    labels = _labels(leaves)
+    ref = sequential_param_grads(ref_model, roots, labels, len(leaves))
+    new = _grads(model, lambda: tree_grad_hybrid(model, roots, _loss_fn(labels, len(leaves)), max_tokens))
+    r = _max_rel_params(ref, new)
+    say(f"  max_rel {r:.3e}")
+    assert r < 1e-5, r
+
+
+def test_hybrid_chain_inherited_bias_equals_whole_tree():
+    """Two-level partition chain: with the inherited gateway bias the hybrid
+    run equals the whole tree; the reference's literal bias does not."""
+    from tree_training_amd.hybrid import tree_grad_hybrid
+    say("hybrid q1 chain inherited vs legacy")
+    base = make_qwen3("tiny", layers=2)
+    ref_model = copy.deepcopy(base).double()
+    model = base.to(DEV)
+    roots, leaves = _tree("q1")
+    labels = _labels(leaves)
+    ref = sequential_param_grads(ref_model, roots, labels, len(leaves))
+    fn = _loss_fn(labels, len(leaves))
+    inh = _grads(model, lambda: tree_grad_hybrid(model, roots, fn, 6))
+    leg = _grads(model, lambda: tree_grad_hybrid(model, roots, fn, 6, legacy_gateway_bias=True))
+    r_inh, r_leg = _max_rel_params(ref, inh), _max_rel_params(ref, leg)
+    say(f"  inherited {r_inh:.3e} legacy {r_leg:.3e}")
+    assert r_inh < 1e-5
+    assert r_leg > 1e-3
+
+
+def test_sequential_and_hybrid_bf16():
+    """bf16 model: hybrid vs sequential (the reference's own differential test,
+    threshold 5e-2 from verify_hybrid.py:143), and sequential vs the fp64 oracle."""
+    from tree_training_amd.ckpt import tree_grad_ckpt_sequential
+    from tree_training_amd.hybrid import tree_grad_hybrid
+    say("bf16 sequential / hybrid")
+    base = make_qwen3("tiny", layers=2)
+    model = base.to(DEV).to(torch.bfloat16)
+    ref_model = copy.deepcopy(model).cpu().double()
+    roots, leaves = _tree("c1")
+    labels = _labels(leaves)
+    fn = _loss_fn(labels, len(leaves))
+    seq = _grads(model, lambda: tree_grad_ckpt_sequential(model, roots, fn))
+    ref = sequential_param_grads(ref_model, roots, labels, len(leaves))
+    r_ref = _max_rel_params(ref, seq)
+    say(f"  sequential bf16 vs fp64 oracle {r_ref:.3e}")
+    assert r_ref < 5e-2
+    for mt in (1000, 20, 10):
+        hyb = _grads(model, lambda: tree_grad_hybrid(model, roots, fn, mt))
+        r = _max_rel_params(seq, hyb)
+        say(f"  hybrid bf16 max_tokens={mt} vs sequential {r:.3e}")
+        assert r < 5e-2

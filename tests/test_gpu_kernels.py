@@ -153,6 +153,17 @@ def _run(lens, par, dtype, seed=0, past_vis=None):
 
 TOL = {torch.bfloat16: 2e-2, torch.float32: 1e-5}
 
+
+def check_close(name, ref, got, tol):
+    """max_rel (verify_hybrid.py:129-132) against the tolerance; a reference
+    that is exactly zero up to rounding (e.g. dQ of a query with one visible
+    key) is compared in absolute terms instead."""
+    if np.abs(ref).max() < 1e-9:
+        assert np.abs(got).max() < tol, f"{name}: |got| {np.abs(got).max():.3e} for a zero reference"
+        return
+    r = max_rel(ref, got)
+    assert r < tol, f"{name}: max_rel {r:.3e} >= {tol}"
+
 CASES = {
     "c1": ([3, 4, 3, 4, 5, 3, 3, 4, 4, 3, 4, 3, 4], [-1, 0, 1, 2, 3, 3, 2, 6, -1, 8, 9, 8, 11]),
     "single_token": ([1], [-1]),
@@ -174,8 +185,7 @@ def test_attention_parity(case, dtype):
         if name == "lse":
             assert np.abs(ref - got).max() < (2e-2 if dtype == torch.bfloat16 else 1e-5), name
             continue
-        r = max_rel(ref, got)
-        assert r < tol, f"{name}: max_rel {r:.3e} >= {tol}"
+        check_close(name, ref, got, tol)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
@@ -189,5 +199,4 @@ def test_attention_gateway(dtype):
     for name, (ref, got) in res.items():
         if name == "lse":
             continue
-        r = max_rel(ref, got)
-        assert r < tol, f"{name}: max_rel {r:.3e} >= {tol}"
+        check_close(name, ref, got, tol)

@@ -1,0 +1,168 @@
+"""Host-side logic of the drop-in API (no GPU): DFS flattening, partitioning,
+gateway metadata, GatewayCache semantics, transformers integration seams."""
+import math
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.partition import hybrid_schedule, partition_tree_literal
+from oracle.tree_meta import build_dfs_tree_info_literal
+from tests.conftest import Node, forest_from_spec, make_qwen3
+from tests.test_oracle_meta import random_forest
+from tree_training_amd import hybrid as H
+from tree_training_amd.gateway import GatewayCache
+from tree_training_amd.tree import TreeNode, build_dfs_tree_info
+
+
+def test_tree_node_api():
+    r = TreeNode([1, 2, 3])
+    c = r.add_child([4])
+    assert c in r.children and not r.is_leaf and c.is_leaf
+    assert TreeNode([5]).children == []
+
+
+def test_host_fields_match_literal(c1_spec):
+    for seed in range(30):
+        rng = random.Random(seed)
+        roots = random_forest(rng, n_roots=rng.randint(1, 3)) if seed else forest_from_spec(c1_spec["nodes"])[0]
+        lit = build_dfs_tree_info_literal(roots)
+        info = build_dfs_tree_info(roots)
+        assert info.dfs_token_ids == lit["dfs_token_ids"]
+        assert info.chunk_boundaries == lit["chunk_boundaries"]
+        assert info.chunk_parent_map == lit["chunk_parent_map"]
+        assert info.leaf_chunk_ids == lit["leaf_chunk_ids"]
+        assert [id(n) for n in info.leaf_nodes] == [id(n) for n in lit["leaf_nodes"]]
+        assert (info.N, info.n_chunks) == (lit["N"], lit["n_chunks"])
+        # node depth offsets equal the first position of each chunk
+        assert info.node_off == [lit["dfs_pos_ids"][s] for s, _ in lit["chunk_boundaries"]]
+
+
+def test_deep_chain_is_iterative():
+    root = TreeNode([1])
+    n = root
+    for _ in range(5000):
+        n = n.add_child([2])
+    info = build_dfs_tree_info([root])
+    assert info.N == 5001 and info.leaf_chunk_ids == [5000]
+    parts = H.partition_tree([root], 100)
+    assert [p.token_count for p in parts] == [100] * 50 + [1]
+
+
+def test_empty_node_rejected():
+    r = TreeNode([1])
+    r.add_child([])
+    with pytest.raises(ValueError):
+        build_dfs_tree_info([r])
+
+
+def test_no_gpu_fails_loudly():
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    from tree_training_amd._lib import TreeAttnError
+    info = build_dfs_tree_info([TreeNode([1, 2])])
+    with pytest.raises(TreeAttnError):
+        info.dfs_pos_ids
+
+
+def test_partition_tree_matches_oracle(c1_spec):
+    for mt, want in c1_spec["partitions"].items():
+        roots, _ = forest_from_spec(c1_spec["nodes"], TreeNode)
+        parts = H.partition_tree(roots, int(mt))
+        assert [p.token_count for p in parts] == want["sizes"]
+    rng = random.Random(5)
+    for trial in range(80):
+        roots = random_forest(rng, n_roots=rng.randint(1, 3), max_depth=6, max_len=7)
+        budget = rng.randint(1, 30)
+        a = H.partition_tree(roots, budget)
+        b = partition_tree_literal(roots, budget)
+        assert len(a) == len(b)
+        for pa, pb in zip(a, b):
+            assert [id(n) for n in pa.dfs_nodes] == [id(n) for n in pb.dfs_nodes]
+            assert pa.cut_node_set == pb.cut_node_set
+            assert pa.leaf_node_set == pb.leaf_node_set
+            assert pa.token_count == pb.token_count
+            assert (pa.parent is None) == (pb.parent is None)
+            assert id(pa.parent_cut_node) == id(pb.parent_cut_node)
+
+
+@pytest.mark.parametrize("legacy", [True, False])
+def test_hybrid_plan_gateways_match_oracle(legacy, c1_spec, q1_spec):
+    cases = [(forest_from_spec(c1_spec["nodes"], TreeNode)[0], mt) for mt in (1000, 20, 10)]
+    cases.append((forest_from_spec(q1_spec["nodes"], TreeNode)[0], q1_spec["max_tokens"]))
+    rng = random.Random(9)
+    for _ in range(40):
+        cases.append((random_forest(rng, n_roots=rng.randint(1, 2), max_depth=6, max_len=6), rng.randint(2, 16)))
+    for roots, mt in cases:
+        ours = H.hybrid_plan(roots, mt, legacy=legacy)
+        ref = hybrid_schedule(roots, mt, legacy=legacy)
+        assert len(ours) == len(ref)
+        for o, r in zip(ours, ref):
+            assert o["pos_offset"] == r["pos_offset"]
+            assert o["n_tokens"] == r["info"]["N"]
+            if r["gateway"] is None:
+                assert o["past_len"] == 0
+                continue
+            assert o["past_len"] == r["gateway"]["total"]
+            assert [math.isfinite(x) for x in o["bias"].tolist()] == [math.isfinite(x) for x in r["gateway"]["bias"]]
+
+
+def test_gateway_cache_reference_mode():
+    gk = torch.randn(1, 2, 3, 4, requires_grad=True)
+    gv = torch.randn(1, 2, 3, 4, requires_grad=True)
+    c = GatewayCache([(gk, gv), (None, None)])
+    k, v = torch.randn(1, 2, 5, 4), torch.randn(1, 2, 5, 4)
+    fk, fv = c.update(k, v, 0)
+    assert fk.shape == (1, 2, 8, 4) and torch.equal(fk[:, :, :3], gk.detach()) and torch.equal(fv[:, :, 3:], v)
+    fk1, _ = c.update(k, v, 1)
+    assert fk1 is k
+    assert c.get_seq_length(0) == 3 and c.get_seq_length(1) == 0 and c.get_seq_length(7) == 0
+    assert c.get_mask_sizes(torch.arange(5), 0) == (8, 0)
+    assert c.get_mask_sizes(5, 0) == (8, 0)
+    assert set(c._full_kv) == {0, 1}
+
+
+def test_gateway_cache_segmented_mode():
+    gk = torch.randn(1, 2, 3, 4)
+    gv = torch.randn(1, 2, 3, 4)
+    c = GatewayCache([(gk, gv)], segmented=True)
+    k, v = torch.randn(1, 2, 5, 4), torch.randn(1, 2, 5, 4)
+    rk, rv = c.update(k, v, 0)
+    assert rk is k and rv is v                      # no concatenation on the hot path
+    assert c.gate(0)[0] is gk
+    fk, fv = c._full_kv[0]                          # still available on demand
+    assert torch.equal(fk, torch.cat([gk, k], -2)) and 0 in c._full_kv
+    child, raws, gates, accs = c.make_child_gates()
+    assert isinstance(child, GatewayCache)
+
+
+def test_gateway_cache_child_gates_fp32_hooks():
+    k = torch.randn(1, 1, 4, 2, requires_grad=True)
+    c = GatewayCache([])
+    fk, fv = c.update(k * 1.0, k * 2.0, 0)
+    child, raws, gates, accs = c.make_child_gates()
+    (gates[0].sum() * 3).backward()
+    assert accs[0][0].dtype == torch.float32 and torch.allclose(accs[0][0], torch.full((1, 1, 4, 2), 3.0))
+    assert torch.count_nonzero(gates[0].grad) == 0   # hook returns zeros, as the reference's
+
+
+def test_transformers_passes_tree_ctx_to_attention():
+    """The seam the engine relies on: a registered attention function gets the
+    model kwargs and no dense mask is built for an unregistered-mask name."""
+    from transformers import AttentionInterface
+    seen = {}
+
+    def fake_attention(module, q, k, v, mask, scaling=None, dropout=0.0, **kw):
+        seen.setdefault("ctx", kw.get("tree_ctx"))
+        seen.setdefault("mask", mask)
+        seen["layers"] = seen.get("layers", 0) + 1
+        out = torch.zeros(q.shape[0], q.shape[2], q.shape[1], q.shape[3], dtype=q.dtype)
+        return out, None
+
+    AttentionInterface.register("tree_probe", fake_attention)
+    m = make_qwen3("tiny", layers=2)
+    m.config._attn_implementation = "tree_probe"
+    marker = object()
+    m(input_ids=torch.tensor([[1, 2, 3]]), position_ids=torch.tensor([[0, 1, 1]]), tree_ctx=marker)
+    assert seen["ctx"] is marker and seen["mask"] is None and seen["layers"] == 2

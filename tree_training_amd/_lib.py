@@ -19,6 +19,9 @@ TT_E_HIP = -3
 TT_E_WORKSPACE = -4
 TT_DTYPE_F32 = 0
 TT_DTYPE_BF16 = 1
+TT_BWD_DELTA = 1
+TT_BWD_DQ = 2
+TT_BWD_DKDV = 4
 TT_STATUS_BAD_LEN = 1
 TT_STATUS_BAD_PARENT = 2
 TT_STATUS_BAD_TOTAL = 4
@@ -42,7 +45,7 @@ class TTAttnProblem(ctypes.Structure):
     _fields_ = [
         ("dtype", ctypes.c_int32), ("n_q", ctypes.c_int32), ("n_past", ctypes.c_int32),
         ("n_heads_q", ctypes.c_int32), ("n_heads_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32),
-        ("scale", ctypes.c_float), ("reserved", ctypes.c_int32),
+        ("scale", ctypes.c_float), ("bwd_parts", ctypes.c_int32),
         ("q", TTTensor), ("k", TTTensor), ("v", TTTensor), ("k_past", TTTensor), ("v_past", TTTensor),
         ("key_lo", ctypes.c_void_p), ("key_hi", ctypes.c_void_p), ("plan", ctypes.c_void_p),
         ("plan_bytes", ctypes.c_size_t),

@@ -10,10 +10,11 @@ a second key segment read in place.
 
 Layouts follow transformers: q [1, Hq, N, D], k/v [1, Hkv, N, D] (any strides
 with D contiguous), output [1, N, Hq, D] contiguous. Gateway K/V are
-[1, Hkv, Lp, D]. When ``gate_acc`` is given, gateway gradients are added in
-float32 to ``gate_acc = (acc_k, acc_v)`` ([Lp, Hkv, D] each) on the device and
-no gradient is returned for the gateway tensors — the contract of the fp32
-hooks of tree_grad_hybrid.py:220-225, without the host round trip.
+[1, Hkv, Lp, D]. When a gateway accumulator is given, gateway gradients are
+added to it in float32 on the device and no gradient is returned for the
+gateway tensors — the contract of the fp32 hooks of tree_grad_hybrid.py:220-225
+(accumulate in fp32, suppress the low-precision ``.grad``), without the host
+round trip.
 """
 from __future__ import annotations
 
@@ -88,7 +89,7 @@ class _Problem:
         self.dtype = q.dtype
         self.s = TTAttnProblem(
             dtype=_DTYPES[q.dtype], n_q=N, n_past=n_past, n_heads_q=Hq, n_heads_kv=k.shape[1],
-            head_dim=D, scale=float(scale), reserved=0,
+            head_dim=D, scale=float(scale), bwd_parts=0,
             q=TTTensor(q.data_ptr(), qst, qsh), k=TTTensor(k.data_ptr(), kst, ksh),
             v=TTTensor(v.data_ptr(), vst, vsh), k_past=kpt, v_past=vpt,
             key_lo=plan.key_lo.data_ptr(), key_hi=plan.key_hi.data_ptr(), plan=plan.plan.data_ptr(),
@@ -147,27 +148,35 @@ class TreeAttnFunction(torch.autograd.Function):
         N, Hq, D = o.shape
         Hkv = k.shape[1]
         gate_acc = ctx.gate_acc
-        need_past = k_past is not None and (ctx.needs_input_grad[3] or ctx.needs_input_grad[4])
-        own_acc = None
-        if k_past is not None and gate_acc is None and need_past:
-            Lp = k_past.shape[2]
-            own_acc = (torch.zeros((Lp, Hkv, D), dtype=torch.float32, device=q.device),
+        acc = None
+        own_acc = False
+        if k_past is not None:
+            if gate_acc is not None:
+                gate_acc.touched = True
+                acc = (gate_acc.k, gate_acc.v)
+            elif ctx.needs_input_grad[3] or ctx.needs_input_grad[4]:
+                Lp = k_past.shape[2]
+                acc = (torch.zeros((Lp, Hkv, D), dtype=torch.float32, device=q.device),
                        torch.zeros((Lp, Hkv, D), dtype=torch.float32, device=q.device))
-        dq, dk, dv = attn_backward(q, k, v, ctx.plan, ctx.scale, o, lse, g_o, k_past, v_past,
-                                   gate_acc if gate_acc is not None else own_acc)
+                own_acc = True
+        dq, dk, dv = attn_backward(q, k, v, ctx.plan, ctx.scale, o, lse, g_o, k_past, v_past, acc)
         dq = dq.view(1, N, Hq, D).transpose(1, 2)
         dk = dk.view(1, N, Hkv, D).transpose(1, 2)
         dv = dv.view(1, N, Hkv, D).transpose(1, 2)
         dkp = dvp = None
-        if own_acc is not None:
+        if own_acc:
             Lp = k_past.shape[2]
-            dkp = own_acc[0].to(k_past.dtype).view(1, Lp, Hkv, D).transpose(1, 2)
-            dvp = own_acc[1].to(v_past.dtype).view(1, Lp, Hkv, D).transpose(1, 2)
+            dkp = acc[0].to(k_past.dtype).view(1, Lp, Hkv, D).transpose(1, 2)
+            dvp = acc[1].to(v_past.dtype).view(1, Lp, Hkv, D).transpose(1, 2)
         return dq, dk, dv, dkp, dvp, None, None, None
 
 
 def tree_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: KeyPlan, scale: float,
                    k_past: Optional[torch.Tensor] = None, v_past: Optional[torch.Tensor] = None,
                    gate_acc=None) -> torch.Tensor:
-    """Tree-masked attention: returns [1, N, Hq, D] (the HF attention output)."""
+    """Tree-masked attention: returns [1, N, Hq, D] (the HF attention output).
+
+    ``gate_acc`` (a ``gateway.GatewayAccumulator``) receives the gateway
+    gradients in float32; without it, gateway tensors that require grad get
+    their gradient through autograd in their own dtype."""
     return TreeAttnFunction.apply(q, k, v, k_past, v_past, plan, float(scale), gate_acc)

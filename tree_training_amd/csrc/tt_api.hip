@@ -161,6 +161,8 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
     b.dk_acc = p->n_past > 0 ? dk_past_acc : nullptr;
     b.dv_acc = p->n_past > 0 ? dv_past_acc : nullptr;
     b.delta = reinterpret_cast<float*>(ws);
+    if (p->bwd_parts & ~(TT_BWD_DELTA | TT_BWD_DQ | TT_BWD_DKDV)) return TT_E_ARG;
+    b.parts = p->bwd_parts ? p->bwd_parts : (TT_BWD_DELTA | TT_BWD_DQ | TT_BWD_DKDV);
     if (p->dtype == TT_DTYPE_BF16) return tt_bwd_bf16_launch(a, b, (hipStream_t)stream);
     return tt_bwd_f32_launch(a, b, (hipStream_t)stream);
 }

@@ -537,10 +537,17 @@ int tt_fwd_bf16_launch(const AttnDev& a, void* o, float* lse, hipStream_t s) {
 
 int tt_bwd_bf16_launch(const AttnDev& a, const BwdDev& b, hipStream_t s) {
     const int rows = a.n_q * a.hq;
-    hipLaunchKernelGGL(bwd_delta_bf16_kernel, dim3(tt_cdiv(rows, 16)), dim3(256), 0, s, a, b);
-    if (hipGetLastError() != hipSuccess) return TT_E_HIP;
-    hipLaunchKernelGGL(bwd_dq_bf16_kernel, dim3(a.n_qb, a.hq), dim3(256), 0, s, a, b);
-    if (hipGetLastError() != hipSuccess) return TT_E_HIP;
-    hipLaunchKernelGGL(bwd_dkdv_bf16_kernel, dim3(tt_cdiv(a.n_keys, TT_BKB), a.hkv), dim3(256), 0, s, a, b);
-    return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
+    if (b.parts & TT_BWD_DELTA) {
+        hipLaunchKernelGGL(bwd_delta_bf16_kernel, dim3(tt_cdiv(rows, 16)), dim3(256), 0, s, a, b);
+        if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+    }
+    if (b.parts & TT_BWD_DQ) {
+        hipLaunchKernelGGL(bwd_dq_bf16_kernel, dim3(a.n_qb, a.hq), dim3(256), 0, s, a, b);
+        if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+    }
+    if (b.parts & TT_BWD_DKDV) {
+        hipLaunchKernelGGL(bwd_dkdv_bf16_kernel, dim3(tt_cdiv(a.n_keys, TT_BKB), a.hkv), dim3(256), 0, s, a, b);
+        if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+    }
+    return TT_OK;
 }

@@ -142,10 +142,17 @@ int tt_fwd_f32_launch(const AttnDev& a, void* o, float* lse, hipStream_t s) {
 }
 
 int tt_bwd_f32_launch(const AttnDev& a, const BwdDev& b, hipStream_t s) {
-    hipLaunchKernelGGL(bwd_delta_f32_kernel, dim3(a.n_q, a.hq), dim3(64), 0, s, a, b);
-    if (hipGetLastError() != hipSuccess) return TT_E_HIP;
-    hipLaunchKernelGGL(bwd_dq_f32_kernel, dim3(a.n_q, a.hq), dim3(64), 0, s, a, b);
-    if (hipGetLastError() != hipSuccess) return TT_E_HIP;
-    hipLaunchKernelGGL(bwd_dkdv_f32_kernel, dim3(a.n_keys, a.hkv), dim3(64), 0, s, a, b);
-    return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
+    if (b.parts & TT_BWD_DELTA) {
+        hipLaunchKernelGGL(bwd_delta_f32_kernel, dim3(a.n_q, a.hq), dim3(64), 0, s, a, b);
+        if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+    }
+    if (b.parts & TT_BWD_DQ) {
+        hipLaunchKernelGGL(bwd_dq_f32_kernel, dim3(a.n_q, a.hq), dim3(64), 0, s, a, b);
+        if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+    }
+    if (b.parts & TT_BWD_DKDV) {
+        hipLaunchKernelGGL(bwd_dkdv_f32_kernel, dim3(a.n_keys, a.hkv), dim3(64), 0, s, a, b);
+        if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+    }
+    return TT_OK;
 }

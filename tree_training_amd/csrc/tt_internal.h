@@ -31,6 +31,7 @@ struct BwdDev {
     float* dk_acc;            // [n_past, hkv, 128] fp32 (+=), may be null
     float* dv_acc;
     float* delta;             // workspace [hq, n_q]: rowsum(dO * O)
+    int parts;                // OR of TT_BWD_* (never 0 here)
 };
 
 size_t tt_meta_ws_bytes_impl(int n);

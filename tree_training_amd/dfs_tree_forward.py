@@ -1,0 +1,66 @@
+"""Single-pass DFS tree forward — drop-in for dfs_tree_forward.py Parts 7-8.
+
+``dfs_tree_forward(model, roots, dtype=None)`` runs one forward over the whole
+DFS-packed forest and returns per-leaf logit views (dfs_tree_forward.py:513-576).
+Instead of a dense [1,1,N,N] additive mask the model runs with the
+``"tree_hip"`` attention implementation: positions come straight from the GPU
+metadata kernel and every layer shares one tile plan.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import List, Optional
+
+import torch
+import torch.nn.functional as F
+
+from .hf_adapter import TreeAttnContext, tree_attention_mode
+from .tree import DFSTreeInfo, TreeNode, build_dfs_tree_info
+
+
+@dataclass
+class DFSTreeResult:
+    """Output of dfs_tree_forward (dfs_tree_forward.py:474-506).
+
+    leaf_logits : list of [1, Lc, V] views into the single forward's logits, DFS order
+    leaf_nodes  : the leaf TreeNodes (same order)
+    info        : DFSTreeInfo
+    """
+    leaf_logits: List[torch.Tensor]
+    leaf_nodes: List[TreeNode]
+    info: DFSTreeInfo
+
+    def total_loss(self, labels: List[torch.Tensor]) -> torch.Tensor:
+        """Sum of per-leaf cross entropies (labels[i]: [Lc] LongTensor)."""
+        if len(labels) != len(self.leaf_logits):
+            raise AssertionError(f"Expected {len(self.leaf_logits)} label tensors, got {len(labels)}")
+        return sum(F.cross_entropy(lg.squeeze(0), lab.to(lg.device))
+                   for lg, lab in zip(self.leaf_logits, labels))
+
+
+def run_tree_model(model, info: DFSTreeInfo, dev, pos_offset: int = 0, cache=None, accumulators=None,
+                   past_bias: Optional[torch.Tensor] = None):
+    """One model forward over a DFS-packed forest (or partition) with tree
+    attention. Returns the model output."""
+    meta = info.device_meta(dev, pos_offset)
+    plan = info.key_plan(dev, past_bias, pos_offset)
+    ids_t = torch.tensor([info.dfs_token_ids], device=dev)
+    pos_t = meta.pos.long().unsqueeze(0)
+    ctx = TreeAttnContext(plan=plan, cache=cache, accumulators=accumulators)
+    with tree_attention_mode(model):
+        return model(input_ids=ids_t, attention_mask=None, position_ids=pos_t,
+                     past_key_values=cache, use_cache=cache is not None, tree_ctx=ctx)
+
+
+def dfs_tree_forward(model, roots: List[TreeNode], dtype: Optional[torch.dtype] = None) -> DFSTreeResult:
+    """One DFS-packed forward over a forest (dfs_tree_forward.py:513-576).
+
+    ``dtype`` is accepted for signature compatibility; it only set the dense
+    mask's dtype in the reference, and no dense mask is built here.
+    """
+    dev = next(model.parameters()).device
+    info = build_dfs_tree_info(roots)
+    out = run_tree_model(model, info, dev)
+    logits = out.logits
+    leaf_logits = [logits[:, s:e, :] for s, e in (info.chunk_boundaries[c] for c in info.leaf_chunk_ids)]
+    return DFSTreeResult(leaf_logits=leaf_logits, leaf_nodes=info.leaf_nodes, info=info)
