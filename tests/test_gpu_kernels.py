@@ -171,6 +171,8 @@ CASES = {
     "wide": ([130] + [67] * 9, [-1] + [0] * 9),
     "forest7": workloads.random_forest(7, node_len=(1, 90)),
     "agent_small": workloads.agent_tree(3, max_tokens=1500),
+    # key tiles whose visible query range exceeds one dK/dV work item (split + fp32 sums)
+    "long_prompt": ([2600, 300, 250, 410], [-1, 0, 0, 0]),
 }
 
 
@@ -189,10 +191,13 @@ def test_attention_parity(case, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
-def test_attention_gateway(dtype):
-    lens, par = [40, 70, 33], [-1, 0, 0]
+@pytest.mark.parametrize("shape", ["short", "split"])
+def test_attention_gateway(dtype, shape):
+    # "split": the gateway keys are seen by more queries than one dK/dV work item covers
+    lens, par, n_past = {"short": ([40, 70, 33], [-1, 0, 0], 150),
+                         "split": ([1200, 900, 700], [-1, 0, 0], 300)}[shape]
     rng = np.random.default_rng(5)
-    past_vis = [bool(x) for x in (rng.random(150) < 0.6)]
+    past_vis = [bool(x) for x in (rng.random(n_past) < 0.6)]
     say(f"attention gateway dtype={dtype} Lp={len(past_vis)}")
     res = _run(lens, par, dtype, seed=11, past_vis=past_vis)
     tol = TOL[dtype]

@@ -53,9 +53,17 @@ int make_dev(const tt_attn_problem* p, AttnDev* a) {
     a->n_qb = tt_cdiv(p->n_q, TT_BQ);
     a->n_kt = tt_cdiv(n_keys, TT_BK);
     a->scale = p->scale;
+    const PlanLayout L(p->n_q, n_keys);
+    a->n_kb = L.n_kb;
     const uint8_t* base = reinterpret_cast<const uint8_t*>(p->plan);
-    a->row_cnt = reinterpret_cast<const int32_t*>(base + TT_PLAN_HDR);
-    a->row_list = a->row_cnt + a->n_qb;
+    a->row_cnt = reinterpret_cast<const int32_t*>(base + L.row_cnt);
+    a->row_order = reinterpret_cast<const int32_t*>(base + L.row_order);
+    a->row_list = reinterpret_cast<const int32_t*>(base + L.row_list);
+    a->kb_qlo = reinterpret_cast<const int32_t*>(base + L.kb_qlo);
+    a->kb_qhi = reinterpret_cast<const int32_t*>(base + L.kb_qhi);
+    a->kb_order = reinterpret_cast<const int32_t*>(base + L.kb_order);
+    a->kb_base = reinterpret_cast<const int32_t*>(base + L.kb_base);
+    a->n_items = reinterpret_cast<const int32_t*>(base) + 5;
     return TT_OK;
 }
 
@@ -129,9 +137,19 @@ int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* stream) {
     return tt_fwd_f32_launch(a, o, lse, (hipStream_t)stream);
 }
 
+// Workspace: delta [Hq, n_q] fp32, then (bf16 problems) the fp32 dK and dV
+// sums of key tiles whose query range is split over several work items,
+// [n_keys, Hkv, head_dim] each.
+static size_t delta_bytes(const tt_attn_problem* p) {
+    return ((size_t)p->n_heads_q * (size_t)p->n_q * sizeof(float) + 255) & ~(size_t)255;
+}
+
 size_t tt_attn_bwd_workspace_bytes(const tt_attn_problem* p) {
-    if (!p || p->n_q < 1 || p->n_heads_q < 1) return 0;
-    return (size_t)p->n_heads_q * (size_t)p->n_q * sizeof(float) + 256;
+    if (!p || p->n_q < 1 || p->n_heads_q < 1 || p->n_heads_kv < 1 || p->n_past < 0) return 0;
+    size_t b = delta_bytes(p);
+    if (p->dtype == TT_DTYPE_BF16)
+        b += 2 * (size_t)(p->n_q + p->n_past) * (size_t)p->n_heads_kv * 128 * sizeof(float);
+    return b;
 }
 
 int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_tensor d_o, void* dq, void* dk,
@@ -161,6 +179,11 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
     b.dk_acc = p->n_past > 0 ? dk_past_acc : nullptr;
     b.dv_acc = p->n_past > 0 ? dv_past_acc : nullptr;
     b.delta = reinterpret_cast<float*>(ws);
+    b.dk_ws = b.dv_ws = nullptr;
+    if (p->dtype == TT_DTYPE_BF16) {
+        b.dk_ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + delta_bytes(p));
+        b.dv_ws = b.dk_ws + (size_t)a.n_keys * a.hkv * 128;
+    }
     if (p->bwd_parts & ~(TT_BWD_DELTA | TT_BWD_DQ | TT_BWD_DKDV)) return TT_E_ARG;
     b.parts = p->bwd_parts ? p->bwd_parts : (TT_BWD_DELTA | TT_BWD_DQ | TT_BWD_DKDV);
     if (p->dtype == TT_DTYPE_BF16) return tt_bwd_bf16_launch(a, b, (hipStream_t)stream);

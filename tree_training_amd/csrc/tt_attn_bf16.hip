@@ -7,14 +7,19 @@
 // the online-softmax row max needs a single cross-half exchange and the
 // probabilities feed O^T = V^T P^T straight from the accumulators. V (and K
 // for dQ) is staged in LDS transposed ([d][key]) so every MFMA operand is a
-// pair of 8-byte LDS reads.
+// pair of 8-byte LDS reads. Tiles are software-pipelined: the next tile's
+// global loads are in flight (in registers) while the current tile computes
+// out of the other LDS stage; one barrier per tile.
 //
 // dK/dV pass (key-major): a workgroup owns TT_BKB = 128 keys of one kv head;
 // each wave keeps K and V of 32 keys as MFMA operands and dK, dV of those
-// keys in fp32 accumulators, and walks the contiguous range of queries that
-// can see them (for a DFS-packed tree, [first key, subtree end)) for the
-// Hq/Hkv q heads of the group. Q and dO blocks are staged natural and
-// transposed. No atomics: each output element has exactly one writer.
+// keys in fp32 accumulators, and walks a range of queries that can see them
+// (for a DFS-packed tree the range is contiguous: [first key, subtree end))
+// for the Hq/Hkv q heads of the group, with Q and dO blocks staged natural and
+// transposed, double-buffered. Ranges longer than TT_QCH queries are split
+// into several work items; a persistent grid walks the items widest-first.
+// Unsplit tiles write dK/dV directly; split tiles add fp32 partial sums into a
+// workspace that a finalize pass converts.
 //
 // Visibility: key j is seen by query i iff key_lo[j] <= i < key_hi[j]; the
 // plan marks each (query block, key tile) empty (skipped), full (no mask) or
@@ -47,35 +52,45 @@ __device__ __forceinline__ const bf16* key_row(const AttnDev& a, int kk, int g, 
     return isv ? (const bf16*)a.v + t * a.v_st + g * a.v_sh : (const bf16*)a.k + t * a.k_st + g * a.k_sh;
 }
 
-// Natural [64 keys][D] tile: thread t loads key t/4, d in [32*(t%4), +32).
-__device__ __forceinline__ void load_keys_natural(const AttnDev& a, int kt, int g, bool isv, bf16* dst) {
-    const int t = threadIdx.x;
-    const int kr = t >> 2, seg = (t & 3) * 32;
-    const int kk = kt * TT_BK + kr;
-    bf16x8 x[4];
-    if (kk < a.n_keys) {
-        const bf16* src = key_row(a, kk, g, isv) + seg;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) x[i] = *(const bf16x8*)(src + 8 * i);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) x[i] = zero8();
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *(bf16x8*)(dst + kr * KS + seg + 8 * i) = x[i];
-}
+// Per-thread slice of a 64-key tile: keys kg..kg+3 (kg = 4*(t/16)) at head
+// dims dc..dc+7 (dc = 8*(t%16)); 16 lanes cover one 256-byte key row.
+struct TileRegs {
+    bf16x8 k[4];
+    bf16x8 v[4];
+    int lo, hi;
+};
 
-// Transposed [D][64 keys] tile: thread t loads keys 4*(t/16)..+3 at
-// d in [8*(t%16), +8) and writes eight 4-key rows.
-__device__ __forceinline__ void load_keys_transposed(const AttnDev& a, int kt, int g, bool isv, bf16* dst) {
+__device__ __forceinline__ void fetch_tile(const AttnDev& a, int kt, int g, TileRegs& r) {
     const int t = threadIdx.x;
     const int dc = (t & 15) * 8, kg = (t >> 4) * 4;
-    bf16x8 x[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int kk = kt * TT_BK + kg + i;
-        x[i] = (kk < a.n_keys) ? *(const bf16x8*)(key_row(a, kk, g, isv) + dc) : zero8();
+        if (kk < a.n_keys) {
+            r.k[i] = *(const bf16x8*)(key_row(a, kk, g, false) + dc);
+            r.v[i] = *(const bf16x8*)(key_row(a, kk, g, true) + dc);
+        } else {
+            r.k[i] = zero8();
+            r.v[i] = zero8();
+        }
     }
+    if (t < TT_BK) {
+        const int kk = kt * TT_BK + t;
+        r.lo = kk < a.n_keys ? a.key_lo[kk] : 0;
+        r.hi = kk < a.n_keys ? a.key_hi[kk] : 0;
+    }
+}
+
+__device__ __forceinline__ void store_natural(const bf16x8 (&x)[4], bf16* dst) {
+    const int t = threadIdx.x;
+    const int dc = (t & 15) * 8, kg = (t >> 4) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *(bf16x8*)(dst + (kg + i) * KS + dc) = x[i];
+}
+
+__device__ __forceinline__ void store_transposed(const bf16x8 (&x)[4], bf16* dst) {
+    const int t = threadIdx.x;
+    const int dc = (t & 15) * 8, kg = (t >> 4) * 4;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         bf16x4 w;
@@ -84,12 +99,11 @@ __device__ __forceinline__ void load_keys_transposed(const AttnDev& a, int kt, i
     }
 }
 
-__device__ __forceinline__ void load_key_bounds(const AttnDev& a, int kt, int* s_lo, int* s_hi) {
+__device__ __forceinline__ void store_bounds(const TileRegs& r, int* s_lo, int* s_hi) {
     const int t = threadIdx.x;
     if (t < TT_BK) {
-        const int kk = kt * TT_BK + t;
-        s_lo[t] = kk < a.n_keys ? a.key_lo[kk] : 0;
-        s_hi[t] = kk < a.n_keys ? a.key_hi[kk] : 0;
+        s_lo[t] = r.lo;
+        s_hi[t] = r.hi;
     }
 }
 
@@ -111,16 +125,37 @@ __device__ __forceinline__ void mask_scores(f32x16 (&s)[2], const int* s_lo, con
     }
 }
 
+// blockIdx.x -> (query block, q head). Workgroups are dispatched round-robin
+// over the 8 XCDs; each XCD gets the q heads of whole kv-head groups so their
+// K/V stay in its L2, and the heaviest query blocks go first.
+__device__ __forceinline__ void decode_qblock(const AttnDev& a, int& qb, int& h) {
+    const int bid = blockIdx.x;
+    if ((a.hq & 7) == 0) {
+        const int hpx = a.hq >> 3, xcd = bid & 7, slot = bid >> 3;
+        h = xcd * hpx + slot % hpx;
+        qb = a.row_order[slot / hpx];
+    } else {
+        h = bid % a.hq;
+        qb = a.row_order[bid / a.hq];
+    }
+}
+
 // ----------------------------------------------------------------------------
 // forward
 // ----------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void fwd_bf16_kernel(AttnDev a, bf16* __restrict__ out, float* __restrict__ lse) {
-    __shared__ __attribute__((aligned(16))) bf16 Ks[TT_BK * KS];
-    __shared__ __attribute__((aligned(16))) bf16 Vt[D * VS];
-    __shared__ __attribute__((aligned(16))) int s_lo[TT_BK];
-    __shared__ __attribute__((aligned(16))) int s_hi[TT_BK];
+struct FwdStage {
+    bf16 K[TT_BK * KS];
+    bf16 Vt[D * VS];
+    int lo[TT_BK];
+    int hi[TT_BK];
+};
 
-    const int qb = blockIdx.x, h = blockIdx.y, g = h / a.rep;
+__global__ __launch_bounds__(256) void fwd_bf16_kernel(AttnDev a, bf16* __restrict__ out, float* __restrict__ lse) {
+    __shared__ __attribute__((aligned(16))) FwdStage st[2];
+
+    int qb, h;
+    decode_qblock(a, qb, h);
+    const int g = h / a.rep;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int col = lane & 31, half = lane >> 5;
     const int qi = qb * TT_BQ + wave * 32 + col;
@@ -143,25 +178,26 @@ __global__ __launch_bounds__(256) void fwd_bf16_kernel(AttnDev a, bf16* __restri
 
     const int cnt = a.row_cnt[qb];
     const int* list = a.row_list + (size_t)qb * a.n_kt;
+    TileRegs nx;
+    if (cnt > 0) fetch_tile(a, list[0] >> 1, g, nx);
     for (int it = 0; it < cnt; ++it) {
-        const int ent = list[it];
-        const int kt = ent >> 1;
-        const bool full = ent & 1;
+        FwdStage& S = st[it & 1];
+        const bool full = list[it] & 1;
+        store_natural(nx.k, S.K);
+        store_transposed(nx.v, S.Vt);
+        store_bounds(nx, S.lo, S.hi);
         __syncthreads();
-        load_keys_natural(a, kt, g, false, Ks);
-        load_keys_transposed(a, kt, g, true, Vt);
-        load_key_bounds(a, kt, s_lo, s_hi);
-        __syncthreads();
+        if (it + 1 < cnt) fetch_tile(a, list[it + 1] >> 1, g, nx);
 
         f32x16 s[2];
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             s[b] = (f32x16){};
-            const bf16* kr = Ks + (32 * b + col) * KS + 8 * half;
+            const bf16* kr = S.K + (32 * b + col) * KS + 8 * half;
 #pragma unroll
             for (int t = 0; t < 8; ++t) s[b] = mfma32(*(const bf16x8*)(kr + 16 * t), qa[t], s[b]);
         }
-        if (!full) mask_scores(s, s_lo, s_hi, qi, half);
+        if (!full) mask_scores(s, S.lo, S.hi, qi, half);
 
         float mx = -INFINITY;
 #pragma unroll
@@ -189,14 +225,14 @@ __global__ __launch_bounds__(256) void fwd_bf16_kernel(AttnDev a, bf16* __restri
         }
 
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            const f32x16& pb = s[st >> 1];
-            const int r0 = 8 * (st & 1);
+        for (int stp = 0; stp < 4; ++stp) {
+            const f32x16& pb = s[stp >> 1];
+            const int r0 = 8 * (stp & 1);
             const bf16x8 pk = pack8(pb[r0 + 0], pb[r0 + 1], pb[r0 + 2], pb[r0 + 3], pb[r0 + 4], pb[r0 + 5],
                                     pb[r0 + 6], pb[r0 + 7]);
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
-                const bf16* vr = Vt + (32 * db + col) * VS + 16 * st + 4 * half;
+                const bf16* vr = S.Vt + (32 * db + col) * VS + 16 * stp + 4 * half;
                 const bf16x8 va = cat44(*(const bf16x4*)vr, *(const bf16x4*)(vr + 8));
                 o[db] = mfma32(va, pk, o[db]);
             }
@@ -246,16 +282,22 @@ __global__ __launch_bounds__(256) void bwd_delta_bf16_kernel(AttnDev a, BwdDev b
 }
 
 // ----------------------------------------------------------------------------
-// backward: dQ (query-major, same tiling as the forward)
+// backward: dQ (query-major, same tiling and pipeline as the forward)
 // ----------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void bwd_dq_bf16_kernel(AttnDev a, BwdDev bw) {
-    __shared__ __attribute__((aligned(16))) bf16 Ks[TT_BK * KS];
-    __shared__ __attribute__((aligned(16))) bf16 Vs[TT_BK * KS];
-    __shared__ __attribute__((aligned(16))) bf16 Kt[D * VS];
-    __shared__ __attribute__((aligned(16))) int s_lo[TT_BK];
-    __shared__ __attribute__((aligned(16))) int s_hi[TT_BK];
+struct DqStage {
+    bf16 K[TT_BK * KS];
+    bf16 V[TT_BK * KS];
+    bf16 Kt[D * VS];
+    int lo[TT_BK];
+    int hi[TT_BK];
+};
 
-    const int qb = blockIdx.x, h = blockIdx.y, g = h / a.rep;
+__global__ __launch_bounds__(256) void bwd_dq_bf16_kernel(AttnDev a, BwdDev bw) {
+    __shared__ __attribute__((aligned(16))) DqStage st[2];
+
+    int qb, h;
+    decode_qblock(a, qb, h);
+    const int g = h / a.rep;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int col = lane & 31, half = lane >> 5;
     const int qi = qb * TT_BQ + wave * 32 + col;
@@ -284,31 +326,32 @@ __global__ __launch_bounds__(256) void bwd_dq_bf16_kernel(AttnDev a, BwdDev bw) 
 
     const int cnt = a.row_cnt[qb];
     const int* list = a.row_list + (size_t)qb * a.n_kt;
+    TileRegs nx;
+    if (cnt > 0) fetch_tile(a, list[0] >> 1, g, nx);
     for (int it = 0; it < cnt; ++it) {
-        const int ent = list[it];
-        const int kt = ent >> 1;
-        const bool full = ent & 1;
+        DqStage& S = st[it & 1];
+        const bool full = list[it] & 1;
+        store_natural(nx.k, S.K);
+        store_natural(nx.v, S.V);
+        store_transposed(nx.k, S.Kt);
+        store_bounds(nx, S.lo, S.hi);
         __syncthreads();
-        load_keys_natural(a, kt, g, false, Ks);
-        load_keys_natural(a, kt, g, true, Vs);
-        load_keys_transposed(a, kt, g, false, Kt);
-        load_key_bounds(a, kt, s_lo, s_hi);
-        __syncthreads();
+        if (it + 1 < cnt) fetch_tile(a, list[it + 1] >> 1, g, nx);
 
         f32x16 s[2], dp[2];
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             s[b] = (f32x16){};
             dp[b] = (f32x16){};
-            const bf16* kr = Ks + (32 * b + col) * KS + 8 * half;
-            const bf16* vr = Vs + (32 * b + col) * KS + 8 * half;
+            const bf16* kr = S.K + (32 * b + col) * KS + 8 * half;
+            const bf16* vr = S.V + (32 * b + col) * KS + 8 * half;
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
                 s[b] = mfma32(*(const bf16x8*)(kr + 16 * t), qa[t], s[b]);
                 dp[b] = mfma32(*(const bf16x8*)(vr + 16 * t), da[t], dp[b]);
             }
         }
-        if (!full) mask_scores(s, s_lo, s_hi, qi, half);
+        if (!full) mask_scores(s, S.lo, S.hi, qi, half);
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -317,14 +360,14 @@ __global__ __launch_bounds__(256) void bwd_dq_bf16_kernel(AttnDev a, BwdDev bw) 
                 s[b][r] = p * (dp[b][r] - dlt);   // dS^T
             }
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            const f32x16& sb = s[st >> 1];
-            const int r0 = 8 * (st & 1);
+        for (int stp = 0; stp < 4; ++stp) {
+            const f32x16& sb = s[stp >> 1];
+            const int r0 = 8 * (stp & 1);
             const bf16x8 pk = pack8(sb[r0 + 0], sb[r0 + 1], sb[r0 + 2], sb[r0 + 3], sb[r0 + 4], sb[r0 + 5],
                                     sb[r0 + 6], sb[r0 + 7]);
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
-                const bf16* kr = Kt + (32 * db + col) * VS + 16 * st + 4 * half;
+                const bf16* kr = S.Kt + (32 * db + col) * VS + 16 * stp + 4 * half;
                 const bf16x8 ka = cat44(*(const bf16x4*)kr, *(const bf16x4*)(kr + 8));
                 dq[db] = mfma32(ka, pk, dq[db]);
             }
@@ -346,133 +389,173 @@ __global__ __launch_bounds__(256) void bwd_dq_bf16_kernel(AttnDev a, BwdDev bw) 
 }
 
 // ----------------------------------------------------------------------------
-// backward: dK, dV (key-major)
+// backward: dK, dV (key-major, persistent over work items)
 // ----------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void bwd_dkdv_bf16_kernel(AttnDev a, BwdDev bw) {
-    __shared__ __attribute__((aligned(16))) bf16 Qs[TT_BQB * KS];
-    __shared__ __attribute__((aligned(16))) bf16 Ds[TT_BQB * KS];
-    __shared__ __attribute__((aligned(16))) bf16 Qt[D * TS];
-    __shared__ __attribute__((aligned(16))) bf16 Dt[D * TS];
-    __shared__ __attribute__((aligned(16))) float s_lse[TT_BQB];
-    __shared__ __attribute__((aligned(16))) float s_dlt[TT_BQB];
-    __shared__ int s_rng[2];
+__device__ __forceinline__ int kb_chunks_dev(int qlo, int qhi) {
+    return qhi > qlo ? tt_cdiv(qhi - (qlo / TT_BQB) * TT_BQB, TT_QCH) : 1;
+}
 
-    const int kb = blockIdx.x, g = blockIdx.y;
+struct KvStage {
+    bf16 Q[TT_BQB * KS];
+    bf16 Dn[TT_BQB * KS];
+    bf16 Qt[D * TS];
+    bf16 Dt[D * TS];
+    float lse[TT_BQB];
+    float dlt[TT_BQB];
+};
+
+// Thread slice of a 32-query block: threads 0..127 stage Q, 128..255 stage
+// dO; each holds rows rg..rg+3 (rg = 4*((t%128)/16)) at dims dc..dc+7.
+struct QRegs {
+    bf16x8 x[4];
+    float s;      // lse (log2 units) or delta of one query, threads 0..31 / 64..95
+};
+
+__device__ __forceinline__ void fetch_qblock(const AttnDev& a, const BwdDev& bw, int q0, int h, QRegs& r) {
+    const int t = threadIdx.x & 127;
+    const bool isd = threadIdx.x >= 128;
+    const int dc = (t & 15) * 8, rg = (t >> 4) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int qq = q0 + rg + i;
+        if (qq < a.n_q) {
+            const bf16* src = isd ? (const bf16*)bw.dout + qq * bw.do_st + h * bw.do_sh
+                                  : (const bf16*)a.q + qq * a.q_st + h * a.q_sh;
+            r.x[i] = *(const bf16x8*)(src + dc);
+        } else {
+            r.x[i] = zero8();
+        }
+    }
+    if (threadIdx.x < TT_BQB) {
+        const int qq = q0 + threadIdx.x;
+        r.s = qq < a.n_q ? bw.lse[(size_t)h * a.n_q + qq] * TT_LOG2E : INFINITY;
+    } else if (threadIdx.x >= 64 && threadIdx.x < 64 + TT_BQB) {
+        const int qq = q0 + threadIdx.x - 64;
+        r.s = qq < a.n_q ? bw.delta[(size_t)h * a.n_q + qq] : 0.0f;
+    }
+}
+
+__device__ __forceinline__ void store_qblock(const QRegs& r, KvStage& S) {
+    const int t = threadIdx.x & 127;
+    const bool isd = threadIdx.x >= 128;
+    const int dc = (t & 15) * 8, rg = (t >> 4) * 4;
+    bf16* nat = isd ? S.Dn : S.Q;
+    bf16* tr = isd ? S.Dt : S.Qt;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *(bf16x8*)(nat + (rg + i) * KS + dc) = r.x[i];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        bf16x4 w;
+        w[0] = r.x[0][e]; w[1] = r.x[1][e]; w[2] = r.x[2][e]; w[3] = r.x[3][e];
+        *(bf16x4*)(tr + (dc + e) * TS + rg) = w;
+    }
+    if (threadIdx.x < TT_BQB) S.lse[threadIdx.x] = r.s;
+    else if (threadIdx.x >= 64 && threadIdx.x < 64 + TT_BQB) S.dlt[threadIdx.x - 64] = r.s;
+}
+
+__global__ __launch_bounds__(256) void bwd_dkdv_bf16_kernel(AttnDev a, BwdDev bw) {
+    __shared__ __attribute__((aligned(16))) KvStage st[2];
+
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int col = lane & 31, half = lane >> 5;
-    const int kk = kb * TT_BKB + wave * 32 + col;   // this lane's key (MFMA column)
     const float c = a.scale * TT_LOG2E;
+    const int n_work = (*a.n_items) * a.hkv;
 
-    int lo = 0, hi = 0;
-    bf16x8 kbv[8], vbv[8];
-    if (kk < a.n_keys) {
-        lo = max(a.key_lo[kk], 0);
-        hi = min(a.key_hi[kk], a.n_q);
-        const bf16* kp = key_row(a, kk, g, false) + 8 * half;
-        const bf16* vp = key_row(a, kk, g, true) + 8 * half;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            kbv[t] = *(const bf16x8*)(kp + 16 * t);
-            vbv[t] = *(const bf16x8*)(vp + 16 * t);
+    for (int w_id = blockIdx.x; w_id < n_work; w_id += gridDim.x) {
+        const int g = w_id % a.hkv;
+        const int item = w_id / a.hkv;
+        int lo_r = 0, hi_r = a.n_kb - 1;        // last tile rank whose first item <= item
+        while (lo_r < hi_r) {
+            const int mid = (lo_r + hi_r + 1) >> 1;
+            if (a.kb_base[mid] <= item) lo_r = mid; else hi_r = mid - 1;
         }
-    } else {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) { kbv[t] = zero8(); vbv[t] = zero8(); }
-    }
-    if (lo >= hi) { lo = a.n_q; hi = 0; }      // invisible key: neutral for min/max
-    const int w_lo = wave_min_i(lo), w_hi = wave_max_i(hi);
-    const int w_maxlo = wave_max_i(lo < hi ? lo : -1), w_minhi = wave_min_i(lo < hi ? hi : -1);
-    const bool w_all_vis = wave_min_i((kk < a.n_keys && lo < hi) ? 1 : 0) == 1;
+        const int kb = a.kb_order[lo_r];
+        const int chunk = item - a.kb_base[lo_r];
+        const int qlo = a.kb_qlo[kb], qhi = a.kb_qhi[kb];
+        const bool split = kb_chunks_dev(qlo, qhi) > 1;
+        int q_start = 0, q_stop = 0;
+        if (qhi > qlo) {
+            q_start = (qlo / TT_BQB) * TT_BQB + chunk * TT_QCH;
+            q_stop = min(q_start + TT_QCH, qhi);
+        }
 
-    if (threadIdx.x == 0) { s_rng[0] = a.n_q; s_rng[1] = 0; }
-    __syncthreads();
-    if (lane == 0) { atomicMin(&s_rng[0], w_lo); atomicMax(&s_rng[1], w_hi); }
-    __syncthreads();
-    const int q_begin = (s_rng[0] / TT_BQB) * TT_BQB, q_end = s_rng[1];
-
-    f32x16 dk[4], dv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { dk[i] = (f32x16){}; dv[i] = (f32x16){}; }
-
-    for (int q0 = q_begin; q0 < q_end; q0 += TT_BQB) {
-        const int q1 = min(q0 + TT_BQB, a.n_q);
-        const bool active = (q0 < w_hi) && (q1 > w_lo);
-        const bool full = w_all_vis && (w_maxlo <= q0) && (w_minhi >= q1);
-        for (int hh = 0; hh < a.rep; ++hh) {
-            const int h = g * a.rep + hh;
-            __syncthreads();
-            {   // stage Q (threads 0..127) and dO (128..255), natural and transposed
-                const int t = threadIdx.x & 127;
-                const bool isd = threadIdx.x >= 128;
-                const int dc = (t & 15) * 8, rg = (t >> 4) * 4;
-                bf16x8 x[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int qq = q0 + rg + i;
-                    if (qq < a.n_q) {
-                        const bf16* src = isd ? (const bf16*)bw.dout + qq * bw.do_st + h * bw.do_sh
-                                              : (const bf16*)a.q + qq * a.q_st + h * a.q_sh;
-                        x[i] = *(const bf16x8*)(src + dc);
-                    } else {
-                        x[i] = zero8();
-                    }
-                }
-                bf16* nat = isd ? Ds : Qs;
-                bf16* tr = isd ? Dt : Qt;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) *(bf16x8*)(nat + (rg + i) * KS + dc) = x[i];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    bf16x4 w;
-                    w[0] = x[0][e]; w[1] = x[1][e]; w[2] = x[2][e]; w[3] = x[3][e];
-                    *(bf16x4*)(tr + (dc + e) * TS + rg) = w;
-                }
-                if (threadIdx.x < TT_BQB) {
-                    const int qq = q0 + threadIdx.x;
-                    s_lse[threadIdx.x] = qq < a.n_q ? bw.lse[(size_t)h * a.n_q + qq] * TT_LOG2E : INFINITY;
-                } else if (threadIdx.x >= 64 && threadIdx.x < 64 + TT_BQB) {
-                    const int qq = q0 + threadIdx.x - 64;
-                    s_dlt[threadIdx.x - 64] = qq < a.n_q ? bw.delta[(size_t)h * a.n_q + qq] : 0.0f;
-                }
-            }
-            __syncthreads();
-            if (!active) continue;
-
-            // S = Q K^T and dP = dO V^T: rows = queries, lane = key column.
-            f32x16 s = (f32x16){}, dp = (f32x16){};
-            const bf16* qr = Qs + col * KS + 8 * half;
-            const bf16* dr = Ds + col * KS + 8 * half;
+        const int kk = kb * TT_BKB + wave * 32 + col;   // this lane's key (MFMA column)
+        int lo = 0, hi = 0;
+        bf16x8 kbv[8], vbv[8];
+        if (kk < a.n_keys) {
+            lo = max(a.key_lo[kk], 0);
+            hi = min(a.key_hi[kk], a.n_q);
+            const bf16* kp = key_row(a, kk, g, false) + 8 * half;
+            const bf16* vp = key_row(a, kk, g, true) + 8 * half;
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-                s = mfma32(*(const bf16x8*)(qr + 16 * t), kbv[t], s);
+                kbv[t] = *(const bf16x8*)(kp + 16 * t);
+                vbv[t] = *(const bf16x8*)(vp + 16 * t);
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) { kbv[t] = zero8(); vbv[t] = zero8(); }
+        }
+        if (lo >= hi) { lo = a.n_q; hi = 0; }          // invisible key: neutral for min/max
+        const int w_lo = wave_min_i(lo), w_hi = wave_max_i(hi);
+        const int w_maxlo = wave_max_i(lo < hi ? lo : -1), w_minhi = wave_min_i(lo < hi ? hi : -1);
+        const bool w_all_vis = wave_min_i((kk < a.n_keys && lo < hi) ? 1 : 0) == 1;
+
+        f32x16 dk[4], dv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { dk[i] = (f32x16){}; dv[i] = (f32x16){}; }
+
+        const int n_steps = (q_stop > q_start) ? tt_cdiv(q_stop - q_start, TT_BQB) * a.rep : 0;
+        QRegs nx;
+        if (n_steps > 0) fetch_qblock(a, bw, q_start, g * a.rep, nx);
+        for (int s = 0; s < n_steps; ++s) {
+            KvStage& S = st[s & 1];
+            const int q0 = q_start + (s / a.rep) * TT_BQB;
+            store_qblock(nx, S);
+            __syncthreads();
+            if (s + 1 < n_steps) {
+                const int s1 = s + 1;
+                fetch_qblock(a, bw, q_start + (s1 / a.rep) * TT_BQB, g * a.rep + s1 % a.rep, nx);
+            }
+            const int q1 = min(q0 + TT_BQB, a.n_q);
+            if (!((q0 < w_hi) && (q1 > w_lo))) continue;   // no key of this wave is seen here
+            const bool full = w_all_vis && (w_maxlo <= q0) && (w_minhi >= q1);
+
+            // S = Q K^T and dP = dO V^T: rows = queries, lane = key column.
+            f32x16 sc = (f32x16){}, dp = (f32x16){};
+            const bf16* qr = S.Q + col * KS + 8 * half;
+            const bf16* dr = S.Dn + col * KS + 8 * half;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                sc = mfma32(*(const bf16x8*)(qr + 16 * t), kbv[t], sc);
                 dp = mfma32(*(const bf16x8*)(dr + 16 * t), vbv[t], dp);
             }
 #pragma unroll
             for (int grp = 0; grp < 4; ++grp) {
                 const int r0 = 8 * grp + 4 * half;
-                const f32x4 l2 = *(const f32x4*)(s_lse + r0);
-                const f32x4 dl = *(const f32x4*)(s_dlt + r0);
+                const f32x4 l2 = *(const f32x4*)(S.lse + r0);
+                const f32x4 dl = *(const f32x4*)(S.dlt + r0);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int qq = q0 + r0 + e;
-                    float p = fast_exp2(fmaf(s[4 * grp + e], c, -l2[e]));
+                    float p = fast_exp2(fmaf(sc[4 * grp + e], c, -l2[e]));
                     if (!full) p = (lo <= qq && qq < hi) ? p : 0.0f;
-                    s[4 * grp + e] = p;                         // P
+                    sc[4 * grp + e] = p;                              // P
                     dp[4 * grp + e] = p * (dp[4 * grp + e] - dl[e]);  // dS
                 }
             }
             // dV += P^T dO, dK += dS^T Q: contraction over the 32 queries.
 #pragma unroll
-            for (int st = 0; st < 2; ++st) {
-                const int r0 = 8 * st;
-                const bf16x8 pa = pack8(s[r0 + 0], s[r0 + 1], s[r0 + 2], s[r0 + 3], s[r0 + 4], s[r0 + 5],
-                                        s[r0 + 6], s[r0 + 7]);
+            for (int stp = 0; stp < 2; ++stp) {
+                const int r0 = 8 * stp;
+                const bf16x8 pa = pack8(sc[r0 + 0], sc[r0 + 1], sc[r0 + 2], sc[r0 + 3], sc[r0 + 4], sc[r0 + 5],
+                                        sc[r0 + 6], sc[r0 + 7]);
                 const bf16x8 sa = pack8(dp[r0 + 0], dp[r0 + 1], dp[r0 + 2], dp[r0 + 3], dp[r0 + 4],
                                         dp[r0 + 5], dp[r0 + 6], dp[r0 + 7]);
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
-                    const bf16* dtr = Dt + (32 * db + col) * TS + 16 * st + 4 * half;
-                    const bf16* qtr = Qt + (32 * db + col) * TS + 16 * st + 4 * half;
+                    const bf16* dtr = S.Dt + (32 * db + col) * TS + 16 * stp + 4 * half;
+                    const bf16* qtr = S.Qt + (32 * db + col) * TS + 16 * stp + 4 * half;
                     const bf16x8 dob = cat44(*(const bf16x4*)dtr, *(const bf16x4*)(dtr + 8));
                     const bf16x8 qbb = cat44(*(const bf16x4*)qtr, *(const bf16x4*)(qtr + 8));
                     dv[db] = mfma32(pa, dob, dv[db]);
@@ -480,29 +563,69 @@ __global__ __launch_bounds__(256) void bwd_dkdv_bf16_kernel(AttnDev a, BwdDev bw
                 }
             }
         }
-    }
 
-    // Epilogue: rows of dk/dv = this wave's keys, columns = d.
-    const int kbase = kb * TT_BKB + wave * 32;
+        // Epilogue: rows of dk/dv = this wave's keys, columns = d.
+        const int kbase = kb * TT_BKB + wave * 32;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int key = kbase + acc_row(r, half);
-        if (key >= a.n_keys) continue;
+        for (int r = 0; r < 16; ++r) {
+            const int key = kbase + acc_row(r, half);
+            if (key >= a.n_keys) continue;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
-            const int d = 32 * db + col;
-            const float gk = dk[db][r] * a.scale, gv = dv[db][r];
-            if (key < a.n_past) {
-                if (bw.dk_acc) {
-                    const size_t idx = ((size_t)key * a.hkv + g) * D + d;
-                    bw.dk_acc[idx] += gk;
-                    bw.dv_acc[idx] += gv;
+            for (int db = 0; db < 4; ++db) {
+                const int d = 32 * db + col;
+                const float gk = dk[db][r] * a.scale, gv = dv[db][r];
+                const size_t widx = ((size_t)key * a.hkv + g) * D + d;
+                if (split) {
+                    atomicAdd(bw.dk_ws + widx, gk);
+                    atomicAdd(bw.dv_ws + widx, gv);
+                } else if (key < a.n_past) {
+                    if (bw.dk_acc) {
+                        bw.dk_acc[widx] += gk;
+                        bw.dv_acc[widx] += gv;
+                    }
+                } else {
+                    const size_t idx = ((size_t)(key - a.n_past) * a.hkv + g) * D + d;
+                    ((bf16*)bw.dk)[idx] = (bf16)gk;
+                    ((bf16*)bw.dv)[idx] = (bf16)gv;
                 }
-            } else {
-                const size_t idx = ((size_t)(key - a.n_past) * a.hkv + g) * D + d;
-                ((bf16*)bw.dk)[idx] = (bf16)gk;
-                ((bf16*)bw.dv)[idx] = (bf16)gv;
             }
+        }
+        __syncthreads();   // LDS stages are reused by the next item
+    }
+}
+
+// Split key tiles: zero their fp32 sums before the dK/dV pass ...
+__global__ __launch_bounds__(256) void bwd_split_zero_kernel(AttnDev a, BwdDev bw) {
+    const int kb = blockIdx.x, g = blockIdx.y;
+    if (kb_chunks_dev(a.kb_qlo[kb], a.kb_qhi[kb]) <= 1) return;
+    for (int e = threadIdx.x; e < TT_BKB * D; e += 256) {
+        const int key = kb * TT_BKB + e / D;
+        if (key >= a.n_keys) break;
+        const size_t idx = ((size_t)key * a.hkv + g) * D + (e % D);
+        bw.dk_ws[idx] = 0.0f;
+        bw.dv_ws[idx] = 0.0f;
+    }
+}
+
+// ... and convert them after it (own keys -> dk/dv, gateway keys -> fp32 accumulators).
+__global__ __launch_bounds__(256) void bwd_split_finalize_kernel(AttnDev a, BwdDev bw) {
+    const int kb = blockIdx.x, g = blockIdx.y;
+    if (kb_chunks_dev(a.kb_qlo[kb], a.kb_qhi[kb]) <= 1) return;
+    for (int e = threadIdx.x; e < TT_BKB * D; e += 256) {
+        const int key = kb * TT_BKB + e / D;
+        if (key >= a.n_keys) break;
+        const int d = e % D;
+        const size_t widx = ((size_t)key * a.hkv + g) * D + d;
+        const float gk = bw.dk_ws[widx], gv = bw.dv_ws[widx];
+        if (key < a.n_past) {
+            if (bw.dk_acc) {
+                bw.dk_acc[widx] += gk;
+                bw.dv_acc[widx] += gv;
+            }
+        } else {
+            const size_t idx = ((size_t)(key - a.n_past) * a.hkv + g) * D + d;
+            ((bf16*)bw.dk)[idx] = (bf16)gk;
+            ((bf16*)bw.dv)[idx] = (bf16)gv;
         }
     }
 }
@@ -531,8 +654,16 @@ int tt_selftest_mfma_launch(const void* a, const void* b, float* d, hipStream_t 
 }
 
 int tt_fwd_bf16_launch(const AttnDev& a, void* o, float* lse, hipStream_t s) {
-    hipLaunchKernelGGL(fwd_bf16_kernel, dim3(a.n_qb, a.hq), dim3(256), 0, s, a, (bf16*)o, lse);
+    hipLaunchKernelGGL(fwd_bf16_kernel, dim3(a.n_qb * a.hq), dim3(256), 0, s, a, (bf16*)o, lse);
     return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
+}
+
+// Persistent grid for the dK/dV pass: a multiple of Hkv so every workgroup
+// keeps one kv head (and, with Hkv = 8, one XCD).
+static int dkdv_grid(const AttnDev& a) {
+    const int target = 256 * 4;
+    const int gsz = (target / a.hkv) * a.hkv;
+    return gsz > 0 ? gsz : a.hkv;
 }
 
 int tt_bwd_bf16_launch(const AttnDev& a, const BwdDev& b, hipStream_t s) {
@@ -542,11 +673,13 @@ int tt_bwd_bf16_launch(const AttnDev& a, const BwdDev& b, hipStream_t s) {
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     if (b.parts & TT_BWD_DQ) {
-        hipLaunchKernelGGL(bwd_dq_bf16_kernel, dim3(a.n_qb, a.hq), dim3(256), 0, s, a, b);
+        hipLaunchKernelGGL(bwd_dq_bf16_kernel, dim3(a.n_qb * a.hq), dim3(256), 0, s, a, b);
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     if (b.parts & TT_BWD_DKDV) {
-        hipLaunchKernelGGL(bwd_dkdv_bf16_kernel, dim3(tt_cdiv(a.n_keys, TT_BKB), a.hkv), dim3(256), 0, s, a, b);
+        hipLaunchKernelGGL(bwd_split_zero_kernel, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
+        hipLaunchKernelGGL(bwd_dkdv_bf16_kernel, dim3(dkdv_grid(a)), dim3(256), 0, s, a, b);
+        hipLaunchKernelGGL(bwd_split_finalize_kernel, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     return TT_OK;

@@ -21,20 +21,46 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 //   forward / dQ pass: a workgroup owns TT_BQ queries of one q head, its four
 //   waves own 32 queries each; key tiles hold TT_BK keys.
 //   dK/dV pass: a workgroup owns TT_BKB keys of one kv head (32 per wave) and
-//   walks its visible query range in blocks of TT_BQB.
+//   walks at most TT_QCH queries of their visible range (one work item), in
+//   blocks of TT_BQB; longer ranges are split into several items.
 #define TT_BQ 128
 #define TT_BK 64
 #define TT_BKB 128
 #define TT_BQB 32
-
-// Plan buffer layout (bytes):
-//   [0,8)   uint64 visible pairs per head
-//   [8,12)  int32 n_qb, [12,16) int32 n_kt
-//   [64, 64 + 4*n_qb)            row_cnt
-//   [.., + 4*n_qb*n_kt)          row_list: (kt << 1) | full, ascending kt
-#define TT_PLAN_HDR 64
+#define TT_QCH 2048
 
 __host__ __device__ inline int tt_cdiv(int a, int b) { return (a + b - 1) / b; }
+
+// Plan buffer layout. Header (bytes): [0,8) uint64 visible pairs per head;
+// int32 at 8: n_qb, 12: n_kt, 16: n_kb, 20: n_items (dK/dV work items).
+// Then int32 arrays:
+//   row_cnt[n_qb]           non-empty key tiles per query block
+//   row_order[n_qb]         query blocks by decreasing tile count
+//   row_list[n_qb * n_kt]   (kt << 1) | full, ascending kt
+//   kb_qlo[n_kb], kb_qhi[n_kb]  visible query range of each 128-key tile
+//   kb_order[n_kb]          key tiles by decreasing range
+//   kb_base[n_kb + 1]       first work item of each key tile, in kb_order order
+// and a byte array cls[n_qb * n_kt] (tile classes, build scratch).
+#define TT_PLAN_HDR 64
+struct PlanLayout {
+    int n_qb, n_kt, n_kb;
+    size_t row_cnt, row_order, row_list, kb_qlo, kb_qhi, kb_order, kb_base, cls, total;
+    __host__ __device__ PlanLayout(int n_q, int n_keys) {
+        n_qb = tt_cdiv(n_q, TT_BQ);
+        n_kt = tt_cdiv(n_keys, TT_BK);
+        n_kb = tt_cdiv(n_keys, TT_BKB);
+        size_t o = TT_PLAN_HDR;
+        row_cnt = o;   o += 4 * (size_t)n_qb;
+        row_order = o; o += 4 * (size_t)n_qb;
+        row_list = o;  o += 4 * (size_t)n_qb * n_kt;
+        kb_qlo = o;    o += 4 * (size_t)n_kb;
+        kb_qhi = o;    o += 4 * (size_t)n_kb;
+        kb_order = o;  o += 4 * (size_t)n_kb;
+        kb_base = o;   o += 4 * ((size_t)n_kb + 1);
+        cls = o;       o += (size_t)n_qb * n_kt;
+        total = (o + 255) & ~(size_t)255;
+    }
+};
 
 // v_mfma_f32_32x32x16_bf16: D[32x32] += A[32x16] * B[16x32].
 // Lane l supplies row (l & 31) of A and column (l & 31) of B, 8 k-values

@@ -16,8 +16,14 @@ struct AttnDev {
     const int32_t* key_lo;
     const int32_t* key_hi;
     const int32_t* row_cnt;   // plan: per query block, number of key tiles
+    const int32_t* row_order; // plan: query blocks, heaviest first
     const int32_t* row_list;  // plan: per query block, (kt << 1) | full
-    int n_q, n_past, n_keys, hq, hkv, rep, n_qb, n_kt;
+    const int32_t* kb_qlo;    // plan: visible query range per 128-key tile
+    const int32_t* kb_qhi;
+    const int32_t* kb_order;  // plan: key tiles, widest range first
+    const int32_t* kb_base;   // plan: first dK/dV work item per key tile (kb_order order)
+    const int32_t* n_items;   // plan: number of dK/dV work items
+    int n_q, n_past, n_keys, hq, hkv, rep, n_qb, n_kt, n_kb;
     float scale;
 };
 
@@ -31,6 +37,8 @@ struct BwdDev {
     float* dk_acc;            // [n_past, hkv, 128] fp32 (+=), may be null
     float* dv_acc;
     float* delta;             // workspace [hq, n_q]: rowsum(dO * O)
+    float* dk_ws;             // workspace [n_keys, hkv, 128] fp32: split key tiles' dK
+    float* dv_ws;             // workspace [n_keys, hkv, 128] fp32: split key tiles' dV
     int parts;                // OR of TT_BWD_* (never 0 here)
 };
 

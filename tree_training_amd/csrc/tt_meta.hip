@@ -90,6 +90,7 @@ __global__ __launch_bounds__(kNodeThreads) void meta_nodes_kernel(
                 a_nxt[i] = -1;
             }
         }
+        __syncthreads();                // global-memory writes of this round visible
         any = __syncthreads_or(any);
         int32_t* t;
         t = a_cur; a_cur = a_nxt; a_nxt = t;
@@ -169,11 +170,13 @@ __global__ void dense_mask_kernel(const int32_t* __restrict__ key_lo, const int3
     mask[(size_t)i * n_keys + j] = (key_lo[j] <= i && i < key_hi[j]) ? 1 : 0;
 }
 
-__global__ void plan_header_kernel(uint8_t* plan, int n_qb, int n_kt) {
+__global__ void plan_header_kernel(uint8_t* plan, int n_qb, int n_kt, int n_kb) {
     if (threadIdx.x == 0) {
         *reinterpret_cast<unsigned long long*>(plan) = 0ull;
         reinterpret_cast<int32_t*>(plan)[2] = n_qb;
         reinterpret_cast<int32_t*>(plan)[3] = n_kt;
+        reinterpret_cast<int32_t*>(plan)[4] = n_kb;
+        reinterpret_cast<int32_t*>(plan)[5] = 0;
     }
 }
 
@@ -227,6 +230,97 @@ __global__ void plan_compact_kernel(const uint8_t* __restrict__ cls, int n_qb, i
     if (lane == 0) row_cnt[row] = cnt;
 }
 
+// Query blocks ranked by decreasing tile count (ties by index): heavy blocks
+// are dispatched first.
+__global__ void plan_row_order_kernel(const int32_t* __restrict__ row_cnt, int n_qb, int32_t* __restrict__ row_order) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_qb) return;
+    const int c = row_cnt[i];
+    int rank = 0;
+    for (int j = 0; j < n_qb; ++j) {
+        const int cj = row_cnt[j];
+        rank += (cj > c) || (cj == c && j < i);
+    }
+    row_order[rank] = i;
+}
+
+// One wave per 128-key tile: the union of its keys' visible query intervals,
+// which is a single range (consecutive lower bounds, non-empty intervals).
+__global__ void plan_kv_range_kernel(const int32_t* __restrict__ key_lo, const int32_t* __restrict__ key_hi,
+                                     int n_keys, int n_q, int n_kb, int32_t* __restrict__ kb_qlo,
+                                     int32_t* __restrict__ kb_qhi) {
+    const int kb = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+    const int lane = threadIdx.x & 63;
+    if (kb >= n_kb) return;
+    int lo = n_q, hi = 0;
+    for (int t = lane; t < TT_BKB; t += 64) {
+        const int j = kb * TT_BKB + t;
+        if (j < n_keys) {
+            const int a = max(key_lo[j], 0), b = min(key_hi[j], n_q);
+            if (a < b) { lo = min(lo, a); hi = max(hi, b); }
+        }
+    }
+    lo = wave_min_i(lo);
+    hi = wave_max_i(hi);
+    if (lane == 0) {
+        kb_qlo[kb] = lo < hi ? lo : 0;
+        kb_qhi[kb] = lo < hi ? hi : 0;
+    }
+}
+
+__global__ void plan_kb_order_kernel(const int32_t* __restrict__ kb_qlo, const int32_t* __restrict__ kb_qhi, int n_kb,
+                                     int32_t* __restrict__ kb_order) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_kb) return;
+    const int c = kb_qhi[i] - kb_qlo[i];
+    int rank = 0;
+    for (int j = 0; j < n_kb; ++j) {
+        const int cj = kb_qhi[j] - kb_qlo[j];
+        rank += (cj > c) || (cj == c && j < i);
+    }
+    kb_order[rank] = i;
+}
+
+__device__ __forceinline__ int kb_chunks(int qlo, int qhi) {
+    return qhi > qlo ? tt_cdiv(qhi - (qlo / TT_BQB) * TT_BQB, TT_QCH) : 1;
+}
+
+// Exclusive prefix sum of work items per key tile, in kb_order order (one workgroup).
+__global__ __launch_bounds__(1024) void plan_kb_base_kernel(const int32_t* __restrict__ kb_qlo,
+                                                            const int32_t* __restrict__ kb_qhi,
+                                                            const int32_t* __restrict__ kb_order, int n_kb,
+                                                            int32_t* __restrict__ kb_base, int32_t* __restrict__ n_items) {
+    __shared__ int s_scan[1024];
+    __shared__ int s_carry;
+    const int tid = threadIdx.x;
+    if (tid == 0) s_carry = 0;
+    __syncthreads();
+    for (int base = 0; base < n_kb; base += 1024) {
+        const int r = base + tid;
+        int v = 0;
+        if (r < n_kb) {
+            const int kb = kb_order[r];
+            v = kb_chunks(kb_qlo[kb], kb_qhi[kb]);
+        }
+        s_scan[tid] = v;
+        __syncthreads();
+        for (int o = 1; o < 1024; o <<= 1) {
+            const int t = tid >= o ? s_scan[tid - o] : 0;
+            __syncthreads();
+            s_scan[tid] += t;
+            __syncthreads();
+        }
+        if (r < n_kb) kb_base[r] = s_carry + s_scan[tid] - v;
+        __syncthreads();
+        if (tid == 1023) s_carry += s_scan[tid];
+        __syncthreads();
+    }
+    if (tid == 0) {
+        kb_base[n_kb] = s_carry;
+        *n_items = s_carry;
+    }
+}
+
 }  // namespace
 
 size_t tt_meta_ws_bytes_impl(int n) {
@@ -260,25 +354,35 @@ int tt_dense_mask_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys,
     return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
 }
 
-size_t tt_plan_bytes_impl(int n_q, int n_keys) {
-    const size_t n_qb = (size_t)tt_cdiv(n_q, TT_BQ), n_kt = (size_t)tt_cdiv(n_keys, TT_BK);
-    size_t b = TT_PLAN_HDR + 4 * n_qb + 4 * n_qb * n_kt + n_qb * n_kt;
-    return (b + 255) & ~(size_t)255;
-}
+size_t tt_plan_bytes_impl(int n_q, int n_keys) { return PlanLayout(n_q, n_keys).total; }
 
 int tt_plan_build_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys, int n_q, void* plan,
                        hipStream_t s) {
-    const int n_qb = tt_cdiv(n_q, TT_BQ), n_kt = tt_cdiv(n_keys, TT_BK);
+    const PlanLayout L(n_q, n_keys);
     uint8_t* base = reinterpret_cast<uint8_t*>(plan);
-    int32_t* row_cnt = reinterpret_cast<int32_t*>(base + TT_PLAN_HDR);
-    int32_t* row_list = row_cnt + n_qb;
-    uint8_t* cls = reinterpret_cast<uint8_t*>(row_list + (size_t)n_qb * n_kt);
-    hipLaunchKernelGGL(plan_header_kernel, dim3(1), dim3(64), 0, s, base, n_qb, n_kt);
+    int32_t* hdr = reinterpret_cast<int32_t*>(base);
+    int32_t* row_cnt = reinterpret_cast<int32_t*>(base + L.row_cnt);
+    int32_t* row_order = reinterpret_cast<int32_t*>(base + L.row_order);
+    int32_t* row_list = reinterpret_cast<int32_t*>(base + L.row_list);
+    int32_t* kb_qlo = reinterpret_cast<int32_t*>(base + L.kb_qlo);
+    int32_t* kb_qhi = reinterpret_cast<int32_t*>(base + L.kb_qhi);
+    int32_t* kb_order = reinterpret_cast<int32_t*>(base + L.kb_order);
+    int32_t* kb_base = reinterpret_cast<int32_t*>(base + L.kb_base);
+    uint8_t* cls = base + L.cls;
+    hipLaunchKernelGGL(plan_header_kernel, dim3(1), dim3(64), 0, s, base, L.n_qb, L.n_kt, L.n_kb);
     hipLaunchKernelGGL(plan_pairs_kernel, dim3(tt_cdiv(n_keys, 256)), dim3(256), 0, s, key_lo, key_hi, n_keys,
                        n_q, reinterpret_cast<unsigned long long*>(base));
-    hipLaunchKernelGGL(plan_classify_kernel, dim3(tt_cdiv(n_qb * n_kt, 256)), dim3(256), 0, s, key_lo, key_hi,
-                       n_keys, n_q, n_qb, n_kt, cls);
-    hipLaunchKernelGGL(plan_compact_kernel, dim3(tt_cdiv(n_qb, 4)), dim3(256), 0, s, cls, n_qb, n_kt, row_cnt,
-                       row_list);
+    hipLaunchKernelGGL(plan_classify_kernel, dim3(tt_cdiv(L.n_qb * L.n_kt, 256)), dim3(256), 0, s, key_lo, key_hi,
+                       n_keys, n_q, L.n_qb, L.n_kt, cls);
+    hipLaunchKernelGGL(plan_compact_kernel, dim3(tt_cdiv(L.n_qb, 4)), dim3(256), 0, s, cls, L.n_qb, L.n_kt,
+                       row_cnt, row_list);
+    hipLaunchKernelGGL(plan_row_order_kernel, dim3(tt_cdiv(L.n_qb, 256)), dim3(256), 0, s, row_cnt, L.n_qb,
+                       row_order);
+    hipLaunchKernelGGL(plan_kv_range_kernel, dim3(tt_cdiv(L.n_kb, 4)), dim3(256), 0, s, key_lo, key_hi, n_keys,
+                       n_q, L.n_kb, kb_qlo, kb_qhi);
+    hipLaunchKernelGGL(plan_kb_order_kernel, dim3(tt_cdiv(L.n_kb, 256)), dim3(256), 0, s, kb_qlo, kb_qhi, L.n_kb,
+                       kb_order);
+    hipLaunchKernelGGL(plan_kb_base_kernel, dim3(1), dim3(1024), 0, s, kb_qlo, kb_qhi, kb_order, L.n_kb, kb_base,
+                       hdr + 5);
     return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
 }
