@@ -40,6 +40,9 @@ def parse():
     ap.add_argument("--workload", default="agent16k", choices=["agent16k", "gateway16k", "rollout48k"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=3)
+    ap.add_argument("--calibrate-copy-mb", type=int, default=0,
+                    help="before timing, run a plain device copy of this many MB (a known-size kernel for "
+                         "scaling HBM byte counters)")
     return ap.parse_args()
 
 
@@ -153,6 +156,14 @@ def main():
             run_problem(seg["node_len"], seg["parent"], seg["q"], seg["k"], seg["v"], seg["do"],
                         seg.get("kp"), seg.get("vp"), seg.get("bias_dev"), seg.get("acc"),
                         ev=None, pos_off=seg["pos_offset"])
+
+    if args.calibrate_copy_mb:
+        src = torch.empty(args.calibrate_copy_mb << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     for _ in range(args.warmup):
         step()

@@ -10,7 +10,8 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "lib", "libtree_attn.so")
+# TREE_ATTN_LIB selects an alternate build of the same library (A/B timing).
+LIB_PATH = os.environ.get("TREE_ATTN_LIB") or os.path.join(_HERE, "lib", "libtree_attn.so")
 
 TT_OK = 0
 TT_E_ARG = -1

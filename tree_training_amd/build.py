@@ -42,26 +42,31 @@ def _compile(src: str, obj: str, extra):
     return r.stderr
 
 
-def build(verbose: bool = False, extra=()) -> str:
+def build(verbose: bool = False, extra=(), out: str = LIB) -> str:
     """Compiles every HIP source and links the shared library; returns its path."""
-    objdir = os.path.join(PKG, "_build")
+    objdir = os.path.join(PKG, "_build" if out == LIB else "_build_alt")
     os.makedirs(objdir, exist_ok=True)
-    os.makedirs(LIBDIR, exist_ok=True)
+    os.makedirs(os.path.dirname(out), exist_ok=True)
     objs = [os.path.join(objdir, s.replace(".hip", ".o")) for s in SOURCES]
     with ThreadPoolExecutor(max_workers=min(4, len(SOURCES))) as ex:
         logs = list(ex.map(lambda so: _compile(so[0], so[1], list(extra)), zip(SOURCES, objs)))
     if verbose:
         for s, log in zip(SOURCES, logs):
             print(f"[{s}]\n{log}")
-    tmp = LIB + ".tmp"
+    tmp = out + ".tmp"
     cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
-    extra = sys.argv[1:]
-    print(build(verbose=True, extra=extra))
+    args = sys.argv[1:]
+    out = LIB
+    if "--out" in args:
+        i = args.index("--out")
+        out = os.path.abspath(args[i + 1])
+        args = args[:i] + args[i + 2:]
+    print(build(verbose=True, extra=args, out=out))

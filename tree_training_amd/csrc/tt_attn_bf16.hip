@@ -5,9 +5,10 @@
 // the non-empty key tiles of the plan. Scores are computed transposed,
 // S^T = K Q^T with v_mfma_f32_32x32x16_bf16, so a lane owns one query column:
 // the online-softmax row max needs a single cross-half exchange and the
-// probabilities feed O^T = V^T P^T straight from the accumulators. V (and K
-// for dQ) is staged in LDS transposed ([d][key]) so every MFMA operand is a
-// pair of 8-byte LDS reads. Tiles are software-pipelined: the next tile's
+// probabilities feed O^T = V^T P^T straight from the accumulators. K and V
+// tiles sit in LDS in their natural [key][d] layout; the V^T (and, for dQ,
+// K^T) operands come out of them through gfx950's transposing LDS read
+// (ds_read_b64_tr_b16). Tiles are software-pipelined: the next tile's
 // global loads are in flight (in registers) while the current tile computes
 // out of the other LDS stage; one barrier per tile.
 //
@@ -15,8 +16,9 @@
 // each wave keeps K and V of 32 keys as MFMA operands and dK, dV of those
 // keys in fp32 accumulators, and walks a range of queries that can see them
 // (for a DFS-packed tree the range is contiguous: [first key, subtree end))
-// for the Hq/Hkv q heads of the group, with Q and dO blocks staged natural and
-// transposed, double-buffered. Ranges longer than TT_QCH queries are split
+// for the Hq/Hkv q heads of the group, with Q and dO blocks staged in LDS
+// (double-buffered) and read both row-wise and transposed. Ranges longer than
+// TT_QCH queries are split
 // into several work items; a persistent grid walks the items widest-first.
 // Unsplit tiles write dK/dV directly; split tiles add fp32 partial sums into a
 // workspace that a finalize pass converts.
@@ -32,15 +34,98 @@ namespace {
 typedef __bf16 bf16;
 
 constexpr int D = 128;
-constexpr int KS = D + 8;          // natural [key][d] row stride (elements): 272 B
-constexpr int VS = TT_BK + 8;      // transposed [d][key] row stride: 144 B
-constexpr int TS = TT_BQB + 8;     // transposed [d][query] row stride: 80 B
+
+// LDS tiles hold tokens in their natural [token][d] order. Two stagings:
+//  * TT_LDS_DMA = 0 (default): rows padded to 288 bytes; each thread loads
+//    its slice of the next tile into registers while the current one
+//    computes, then stores it. The padding puts consecutive rows 8 banks
+//    apart, so 16-byte row reads, transposed reads and the stores all run at
+//    the minimum number of LDS passes.
+//  * TT_LDS_DMA = 1: unpadded 256-byte rows written by global_load_lds
+//    (no registers, no store instructions); 16-byte chunks are XOR-swizzled
+//    (chunk c of row r at c ^ swz(r)) for the same bank behaviour.
+#ifndef TT_LDS_DMA
+#define TT_LDS_DMA 0
+#endif
+#if TT_LDS_DMA
+constexpr int ROW = D;
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+__device__ __forceinline__ int tile_off(int r, int d) { return r * ROW + (((d >> 3) ^ swz(r)) << 3) + (d & 7); }
+#else
+constexpr int ROW = D + 16;
+__device__ __forceinline__ int tile_off(int r, int d) { return r * ROW + d; }
+#endif
 
 __device__ __forceinline__ bf16x8 zero8() {
     bf16x8 z;
 #pragma unroll
     for (int i = 0; i < 8; ++i) z[i] = (bf16)0.0f;
     return z;
+}
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) const void glb_void;
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
+// (i & 3) of the 8-byte chunks read by lanes 4k + (i >> 2), k = 0..3.
+__device__ __forceinline__ bf16x4 ds_read_tr(const bf16* p) {
+    const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p));
+    return __builtin_bit_cast(bf16x4, r);
+}
+
+// MFMA operand "column = head dim, k = 16 tokens" from a tile X: lane l gets
+// X[r0 + kappa(e)][dbase + (l & 31)], kappa(e) = 8*(e/4) + 4*(l>>5) + (e%4) —
+// the accumulator row order, so it pairs with probabilities taken straight
+// from a score accumulator.
+__device__ __forceinline__ bf16x8 read_tr_operand(const bf16* X, int r0, int dbase, int lane) {
+    const int j = lane & 15, grp = lane >> 4;
+    const int d = dbase + 16 * (grp & 1) + 4 * (j & 3);
+    const int r = r0 + 4 * (grp >> 1) + (j >> 2);
+    return cat44(ds_read_tr(X + tile_off(r, d)), ds_read_tr(X + tile_off(r + 8, d)));
+}
+
+// MFMA operand "row = token, k = 16 head dims": X[r][d0 .. d0+7], d0 % 8 == 0.
+__device__ __forceinline__ bf16x8 read_row_operand(const bf16* X, int r, int d0) {
+    return *(const bf16x8*)(X + tile_off(r, d0));
+}
+
+#if TT_LDS_DMA
+// Direct global -> LDS copy of rows [row0, row0 + n_rows) of a tile: each wave
+// instruction moves 4 rows (1024 bytes, 16 per lane) into swizzled LDS order.
+template <typename RowPtr>
+__device__ __forceinline__ void dma_rows(bf16* X, int row0, int n_rows, RowPtr row_ptr) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int rb = row0 + 4 * wave; rb < row0 + n_rows; rb += 16) {
+        const int r = rb + (lane >> 4);
+        const int c = (lane & 15) ^ swz(r);
+        __builtin_amdgcn_global_load_lds((glb_void*)(row_ptr(r) + 8 * c), (lds_void*)(X + rb * ROW), 16, 0, 0);
+    }
+}
+
+__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+#endif
+
+// Register staging: thread t holds rows 4*(t/16)+i (i < 4, up to n_rows) at
+// head dims 8*(t%16) .. +7 of a tile; 16 lanes cover one 256-byte row.
+template <int NROWS>
+struct RowRegs {
+    bf16x8 x[NROWS / 16];
+};
+
+template <int NROWS, typename RowPtr>
+__device__ __forceinline__ void fetch_rows(RowRegs<NROWS>& r, int tid, RowPtr row_ptr) {
+    const int dc = (tid & 15) * 8, rg = (tid >> 4) * (NROWS / 16);
+#pragma unroll
+    for (int i = 0; i < NROWS / 16; ++i) r.x[i] = *(const bf16x8*)(row_ptr(rg + i) + dc);
+}
+
+template <int NROWS>
+__device__ __forceinline__ void store_rows(const RowRegs<NROWS>& r, int tid, bf16* X) {
+    const int dc = (tid & 15) * 8, rg = (tid >> 4) * (NROWS / 16);
+#pragma unroll
+    for (int i = 0; i < NROWS / 16; ++i) *(bf16x8*)(X + tile_off(rg + i, dc)) = r.x[i];
 }
 
 __device__ __forceinline__ const bf16* key_row(const AttnDev& a, int kk, int g, bool isv) {
@@ -52,28 +137,12 @@ __device__ __forceinline__ const bf16* key_row(const AttnDev& a, int kk, int g, 
     return isv ? (const bf16*)a.v + t * a.v_st + g * a.v_sh : (const bf16*)a.k + t * a.k_st + g * a.k_sh;
 }
 
-// Per-thread slice of a 64-key tile: keys kg..kg+3 (kg = 4*(t/16)) at head
-// dims dc..dc+7 (dc = 8*(t%16)); 16 lanes cover one 256-byte key row.
-struct TileRegs {
-    bf16x8 k[4];
-    bf16x8 v[4];
+struct Bounds {
     int lo, hi;
 };
 
-__device__ __forceinline__ void fetch_tile(const AttnDev& a, int kt, int g, TileRegs& r) {
+__device__ __forceinline__ void fetch_bounds(const AttnDev& a, int kt, Bounds& r) {
     const int t = threadIdx.x;
-    const int dc = (t & 15) * 8, kg = (t >> 4) * 4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int kk = kt * TT_BK + kg + i;
-        if (kk < a.n_keys) {
-            r.k[i] = *(const bf16x8*)(key_row(a, kk, g, false) + dc);
-            r.v[i] = *(const bf16x8*)(key_row(a, kk, g, true) + dc);
-        } else {
-            r.k[i] = zero8();
-            r.v[i] = zero8();
-        }
-    }
     if (t < TT_BK) {
         const int kk = kt * TT_BK + t;
         r.lo = kk < a.n_keys ? a.key_lo[kk] : 0;
@@ -81,25 +150,35 @@ __device__ __forceinline__ void fetch_tile(const AttnDev& a, int kt, int g, Tile
     }
 }
 
-__device__ __forceinline__ void store_natural(const bf16x8 (&x)[4], bf16* dst) {
-    const int t = threadIdx.x;
-    const int dc = (t & 15) * 8, kg = (t >> 4) * 4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *(bf16x8*)(dst + (kg + i) * KS + dc) = x[i];
-}
-
-__device__ __forceinline__ void store_transposed(const bf16x8 (&x)[4], bf16* dst) {
-    const int t = threadIdx.x;
-    const int dc = (t & 15) * 8, kg = (t >> 4) * 4;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        bf16x4 w;
-        w[0] = x[0][e]; w[1] = x[1][e]; w[2] = x[2][e]; w[3] = x[3][e];
-        *(bf16x4*)(dst + (dc + e) * VS + kg) = w;
+// Staging of the K and V rows of key tile kt (out-of-range rows alias the
+// last key; their empty bounds mask them). begin() starts the loads for a
+// stage; commit() makes them resident in that stage (before the barrier).
+struct KvTileStager {
+#if !TT_LDS_DMA
+    RowRegs<TT_BK> k, v;
+#endif
+    __device__ __forceinline__ void begin(const AttnDev& a, int kt, int g, bf16* K, bf16* V) {
+        auto krow = [&](int r) { return key_row(a, min(kt * TT_BK + r, a.n_keys - 1), g, false); };
+        auto vrow = [&](int r) { return key_row(a, min(kt * TT_BK + r, a.n_keys - 1), g, true); };
+#if TT_LDS_DMA
+        dma_rows(K, 0, TT_BK, krow);
+        dma_rows(V, 0, TT_BK, vrow);
+#else
+        fetch_rows(k, threadIdx.x, krow);
+        fetch_rows(v, threadIdx.x, vrow);
+#endif
     }
-}
+    __device__ __forceinline__ void commit(bf16* K, bf16* V) {
+#if TT_LDS_DMA
+        dma_wait();
+#else
+        store_rows(k, threadIdx.x, K);
+        store_rows(v, threadIdx.x, V);
+#endif
+    }
+};
 
-__device__ __forceinline__ void store_bounds(const TileRegs& r, int* s_lo, int* s_hi) {
+__device__ __forceinline__ void store_bounds(const Bounds& r, int* s_lo, int* s_hi) {
     const int t = threadIdx.x;
     if (t < TT_BK) {
         s_lo[t] = r.lo;
@@ -144,13 +223,13 @@ __device__ __forceinline__ void decode_qblock(const AttnDev& a, int& qb, int& h)
 // forward
 // ----------------------------------------------------------------------------
 struct FwdStage {
-    bf16 K[TT_BK * KS];
-    bf16 Vt[D * VS];
+    bf16 K[TT_BK * ROW];
+    bf16 V[TT_BK * ROW];
     int lo[TT_BK];
     int hi[TT_BK];
 };
 
-__global__ __launch_bounds__(256) void fwd_bf16_kernel(AttnDev a, bf16* __restrict__ out, float* __restrict__ lse) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_bf16_kernel(AttnDev a, bf16* __restrict__ out, float* __restrict__ lse) {
     __shared__ __attribute__((aligned(16))) FwdStage st[2];
 
     int qb, h;
@@ -178,24 +257,30 @@ __global__ __launch_bounds__(256) void fwd_bf16_kernel(AttnDev a, bf16* __restri
 
     const int cnt = a.row_cnt[qb];
     const int* list = a.row_list + (size_t)qb * a.n_kt;
-    TileRegs nx;
-    if (cnt > 0) fetch_tile(a, list[0] >> 1, g, nx);
+    KvTileStager stg;
+    Bounds nb;
+    if (cnt > 0) {
+        stg.begin(a, list[0] >> 1, g, st[0].K, st[0].V);
+        fetch_bounds(a, list[0] >> 1, nb);
+    }
     for (int it = 0; it < cnt; ++it) {
         FwdStage& S = st[it & 1];
         const bool full = list[it] & 1;
-        store_natural(nx.k, S.K);
-        store_transposed(nx.v, S.Vt);
-        store_bounds(nx, S.lo, S.hi);
+        stg.commit(S.K, S.V);
+        store_bounds(nb, S.lo, S.hi);
         __syncthreads();
-        if (it + 1 < cnt) fetch_tile(a, list[it + 1] >> 1, g, nx);
+        if (it + 1 < cnt) {
+            const int kt1 = list[it + 1] >> 1;
+            stg.begin(a, kt1, g, st[(it + 1) & 1].K, st[(it + 1) & 1].V);
+            fetch_bounds(a, kt1, nb);
+        }
 
         f32x16 s[2];
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             s[b] = (f32x16){};
-            const bf16* kr = S.K + (32 * b + col) * KS + 8 * half;
 #pragma unroll
-            for (int t = 0; t < 8; ++t) s[b] = mfma32(*(const bf16x8*)(kr + 16 * t), qa[t], s[b]);
+            for (int t = 0; t < 8; ++t) s[b] = mfma32(read_row_operand(S.K, 32 * b + col, 16 * t + 8 * half), qa[t], s[b]);
         }
         if (!full) mask_scores(s, S.lo, S.hi, qi, half);
 
@@ -231,11 +316,8 @@ __global__ __launch_bounds__(256) void fwd_bf16_kernel(AttnDev a, bf16* __restri
             const bf16x8 pk = pack8(pb[r0 + 0], pb[r0 + 1], pb[r0 + 2], pb[r0 + 3], pb[r0 + 4], pb[r0 + 5],
                                     pb[r0 + 6], pb[r0 + 7]);
 #pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const bf16* vr = S.Vt + (32 * db + col) * VS + 16 * stp + 4 * half;
-                const bf16x8 va = cat44(*(const bf16x4*)vr, *(const bf16x4*)(vr + 8));
-                o[db] = mfma32(va, pk, o[db]);
-            }
+            for (int db = 0; db < 4; ++db)
+                o[db] = mfma32(read_tr_operand(S.V, 16 * stp, 32 * db, lane), pk, o[db]);
         }
     }
 
@@ -285,14 +367,13 @@ __global__ __launch_bounds__(256) void bwd_delta_bf16_kernel(AttnDev a, BwdDev b
 // backward: dQ (query-major, same tiling and pipeline as the forward)
 // ----------------------------------------------------------------------------
 struct DqStage {
-    bf16 K[TT_BK * KS];
-    bf16 V[TT_BK * KS];
-    bf16 Kt[D * VS];
+    bf16 K[TT_BK * ROW];
+    bf16 V[TT_BK * ROW];
     int lo[TT_BK];
     int hi[TT_BK];
 };
 
-__global__ __launch_bounds__(256) void bwd_dq_bf16_kernel(AttnDev a, BwdDev bw) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_dq_bf16_kernel(AttnDev a, BwdDev bw) {
     __shared__ __attribute__((aligned(16))) DqStage st[2];
 
     int qb, h;
@@ -326,29 +407,33 @@ __global__ __launch_bounds__(256) void bwd_dq_bf16_kernel(AttnDev a, BwdDev bw) 
 
     const int cnt = a.row_cnt[qb];
     const int* list = a.row_list + (size_t)qb * a.n_kt;
-    TileRegs nx;
-    if (cnt > 0) fetch_tile(a, list[0] >> 1, g, nx);
+    KvTileStager stg;
+    Bounds nb;
+    if (cnt > 0) {
+        stg.begin(a, list[0] >> 1, g, st[0].K, st[0].V);
+        fetch_bounds(a, list[0] >> 1, nb);
+    }
     for (int it = 0; it < cnt; ++it) {
         DqStage& S = st[it & 1];
         const bool full = list[it] & 1;
-        store_natural(nx.k, S.K);
-        store_natural(nx.v, S.V);
-        store_transposed(nx.k, S.Kt);
-        store_bounds(nx, S.lo, S.hi);
+        stg.commit(S.K, S.V);
+        store_bounds(nb, S.lo, S.hi);
         __syncthreads();
-        if (it + 1 < cnt) fetch_tile(a, list[it + 1] >> 1, g, nx);
+        if (it + 1 < cnt) {
+            const int kt1 = list[it + 1] >> 1;
+            stg.begin(a, kt1, g, st[(it + 1) & 1].K, st[(it + 1) & 1].V);
+            fetch_bounds(a, kt1, nb);
+        }
 
         f32x16 s[2], dp[2];
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             s[b] = (f32x16){};
             dp[b] = (f32x16){};
-            const bf16* kr = S.K + (32 * b + col) * KS + 8 * half;
-            const bf16* vr = S.V + (32 * b + col) * KS + 8 * half;
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-                s[b] = mfma32(*(const bf16x8*)(kr + 16 * t), qa[t], s[b]);
-                dp[b] = mfma32(*(const bf16x8*)(vr + 16 * t), da[t], dp[b]);
+                s[b] = mfma32(read_row_operand(S.K, 32 * b + col, 16 * t + 8 * half), qa[t], s[b]);
+                dp[b] = mfma32(read_row_operand(S.V, 32 * b + col, 16 * t + 8 * half), da[t], dp[b]);
             }
         }
         if (!full) mask_scores(s, S.lo, S.hi, qi, half);
@@ -366,11 +451,8 @@ __global__ __launch_bounds__(256) void bwd_dq_bf16_kernel(AttnDev a, BwdDev bw) 
             const bf16x8 pk = pack8(sb[r0 + 0], sb[r0 + 1], sb[r0 + 2], sb[r0 + 3], sb[r0 + 4], sb[r0 + 5],
                                     sb[r0 + 6], sb[r0 + 7]);
 #pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const bf16* kr = S.Kt + (32 * db + col) * VS + 16 * stp + 4 * half;
-                const bf16x8 ka = cat44(*(const bf16x4*)kr, *(const bf16x4*)(kr + 8));
-                dq[db] = mfma32(ka, pk, dq[db]);
-            }
+            for (int db = 0; db < 4; ++db)
+                dq[db] = mfma32(read_tr_operand(S.K, 16 * stp, 32 * db, lane), pk, dq[db]);
         }
     }
 
@@ -396,64 +478,56 @@ __device__ __forceinline__ int kb_chunks_dev(int qlo, int qhi) {
 }
 
 struct KvStage {
-    bf16 Q[TT_BQB * KS];
-    bf16 Dn[TT_BQB * KS];
-    bf16 Qt[D * TS];
-    bf16 Dt[D * TS];
+    bf16 Q[TT_BQB * ROW];
+    bf16 Dn[TT_BQB * ROW];
     float lse[TT_BQB];
     float dlt[TT_BQB];
 };
 
-// Thread slice of a 32-query block: threads 0..127 stage Q, 128..255 stage
-// dO; each holds rows rg..rg+3 (rg = 4*((t%128)/16)) at dims dc..dc+7.
-struct QRegs {
-    bf16x8 x[4];
-    float s;      // lse (log2 units) or delta of one query, threads 0..31 / 64..95
-};
-
-__device__ __forceinline__ void fetch_qblock(const AttnDev& a, const BwdDev& bw, int q0, int h, QRegs& r) {
-    const int t = threadIdx.x & 127;
-    const bool isd = threadIdx.x >= 128;
-    const int dc = (t & 15) * 8, rg = (t >> 4) * 4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int qq = q0 + rg + i;
-        if (qq < a.n_q) {
-            const bf16* src = isd ? (const bf16*)bw.dout + qq * bw.do_st + h * bw.do_sh
-                                  : (const bf16*)a.q + qq * a.q_st + h * a.q_sh;
-            r.x[i] = *(const bf16x8*)(src + dc);
-        } else {
-            r.x[i] = zero8();
+// Staging of the Q and dO rows of a 32-query block of head h (rows past n_q
+// alias the last query; their lse is +inf so they contribute nothing), plus
+// one lse (log2 units) or delta value per thread for threads 0..31 / 64..95.
+struct QBlockStager {
+#if !TT_LDS_DMA
+    RowRegs<TT_BQB> q, d;
+#endif
+    float sv;
+    __device__ __forceinline__ void begin(const AttnDev& a, const BwdDev& bw, int q0, int h, KvStage& S) {
+        auto qrow = [&](int r) { return (const bf16*)a.q + (int64_t)min(q0 + r, a.n_q - 1) * a.q_st + h * a.q_sh; };
+        auto drow = [&](int r) {
+            return (const bf16*)bw.dout + (int64_t)min(q0 + r, a.n_q - 1) * bw.do_st + h * bw.do_sh;
+        };
+#if TT_LDS_DMA
+        dma_rows(S.Q, 0, TT_BQB, qrow);
+        dma_rows(S.Dn, 0, TT_BQB, drow);
+#else
+        fetch_rows(q, threadIdx.x, qrow);
+        fetch_rows(d, threadIdx.x, drow);
+#endif
+        if (threadIdx.x < TT_BQB) {
+            const int qq = q0 + threadIdx.x;
+            sv = qq < a.n_q ? bw.lse[(size_t)h * a.n_q + qq] * TT_LOG2E : INFINITY;
+        } else if (threadIdx.x >= 64 && threadIdx.x < 64 + TT_BQB) {
+            const int qq = q0 + threadIdx.x - 64;
+            sv = qq < a.n_q ? bw.delta[(size_t)h * a.n_q + qq] : 0.0f;
         }
     }
-    if (threadIdx.x < TT_BQB) {
-        const int qq = q0 + threadIdx.x;
-        r.s = qq < a.n_q ? bw.lse[(size_t)h * a.n_q + qq] * TT_LOG2E : INFINITY;
-    } else if (threadIdx.x >= 64 && threadIdx.x < 64 + TT_BQB) {
-        const int qq = q0 + threadIdx.x - 64;
-        r.s = qq < a.n_q ? bw.delta[(size_t)h * a.n_q + qq] : 0.0f;
+    __device__ __forceinline__ void commit(KvStage& S) {
+#if TT_LDS_DMA
+        dma_wait();
+#else
+        store_rows(q, threadIdx.x, S.Q);
+        store_rows(d, threadIdx.x, S.Dn);
+#endif
+        if (threadIdx.x < TT_BQB) S.lse[threadIdx.x] = sv;
+        else if (threadIdx.x >= 64 && threadIdx.x < 64 + TT_BQB) S.dlt[threadIdx.x - 64] = sv;
     }
-}
+};
 
-__device__ __forceinline__ void store_qblock(const QRegs& r, KvStage& S) {
-    const int t = threadIdx.x & 127;
-    const bool isd = threadIdx.x >= 128;
-    const int dc = (t & 15) * 8, rg = (t >> 4) * 4;
-    bf16* nat = isd ? S.Dn : S.Q;
-    bf16* tr = isd ? S.Dt : S.Qt;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *(bf16x8*)(nat + (rg + i) * KS + dc) = r.x[i];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        bf16x4 w;
-        w[0] = r.x[0][e]; w[1] = r.x[1][e]; w[2] = r.x[2][e]; w[3] = r.x[3][e];
-        *(bf16x4*)(tr + (dc + e) * TS + rg) = w;
-    }
-    if (threadIdx.x < TT_BQB) S.lse[threadIdx.x] = r.s;
-    else if (threadIdx.x >= 64 && threadIdx.x < 64 + TT_BQB) S.dlt[threadIdx.x - 64] = r.s;
-}
-
-__global__ __launch_bounds__(256) void bwd_dkdv_bf16_kernel(AttnDev a, BwdDev bw) {
+#ifndef TT_DKDV_WAVES_PER_EU
+#define TT_DKDV_WAVES_PER_EU 2
+#endif
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAVES_PER_EU, TT_DKDV_WAVES_PER_EU))) void bwd_dkdv_bf16_kernel(AttnDev a, BwdDev bw) {
     __shared__ __attribute__((aligned(16))) KvStage st[2];
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -506,16 +580,16 @@ __global__ __launch_bounds__(256) void bwd_dkdv_bf16_kernel(AttnDev a, BwdDev bw
         for (int i = 0; i < 4; ++i) { dk[i] = (f32x16){}; dv[i] = (f32x16){}; }
 
         const int n_steps = (q_stop > q_start) ? tt_cdiv(q_stop - q_start, TT_BQB) * a.rep : 0;
-        QRegs nx;
-        if (n_steps > 0) fetch_qblock(a, bw, q_start, g * a.rep, nx);
+        QBlockStager stg;
+        if (n_steps > 0) stg.begin(a, bw, q_start, g * a.rep, st[0]);
         for (int s = 0; s < n_steps; ++s) {
             KvStage& S = st[s & 1];
             const int q0 = q_start + (s / a.rep) * TT_BQB;
-            store_qblock(nx, S);
+            stg.commit(S);
             __syncthreads();
             if (s + 1 < n_steps) {
                 const int s1 = s + 1;
-                fetch_qblock(a, bw, q_start + (s1 / a.rep) * TT_BQB, g * a.rep + s1 % a.rep, nx);
+                stg.begin(a, bw, q_start + (s1 / a.rep) * TT_BQB, g * a.rep + s1 % a.rep, st[s1 & 1]);
             }
             const int q1 = min(q0 + TT_BQB, a.n_q);
             if (!((q0 < w_hi) && (q1 > w_lo))) continue;   // no key of this wave is seen here
@@ -523,12 +597,10 @@ __global__ __launch_bounds__(256) void bwd_dkdv_bf16_kernel(AttnDev a, BwdDev bw
 
             // S = Q K^T and dP = dO V^T: rows = queries, lane = key column.
             f32x16 sc = (f32x16){}, dp = (f32x16){};
-            const bf16* qr = S.Q + col * KS + 8 * half;
-            const bf16* dr = S.Dn + col * KS + 8 * half;
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-                sc = mfma32(*(const bf16x8*)(qr + 16 * t), kbv[t], sc);
-                dp = mfma32(*(const bf16x8*)(dr + 16 * t), vbv[t], dp);
+                sc = mfma32(read_row_operand(S.Q, col, 16 * t + 8 * half), kbv[t], sc);
+                dp = mfma32(read_row_operand(S.Dn, col, 16 * t + 8 * half), vbv[t], dp);
             }
 #pragma unroll
             for (int grp = 0; grp < 4; ++grp) {
@@ -554,12 +626,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_bf16_kernel(AttnDev a, BwdDev bw
                                         dp[r0 + 5], dp[r0 + 6], dp[r0 + 7]);
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
-                    const bf16* dtr = S.Dt + (32 * db + col) * TS + 16 * stp + 4 * half;
-                    const bf16* qtr = S.Qt + (32 * db + col) * TS + 16 * stp + 4 * half;
-                    const bf16x8 dob = cat44(*(const bf16x4*)dtr, *(const bf16x4*)(dtr + 8));
-                    const bf16x8 qbb = cat44(*(const bf16x4*)qtr, *(const bf16x4*)(qtr + 8));
-                    dv[db] = mfma32(pa, dob, dv[db]);
-                    dk[db] = mfma32(sa, qbb, dk[db]);
+                    dv[db] = mfma32(pa, read_tr_operand(S.Dn, 16 * stp, 32 * db, lane), dv[db]);
+                    dk[db] = mfma32(sa, read_tr_operand(S.Q, 16 * stp, 32 * db, lane), dk[db]);
                 }
             }
         }
