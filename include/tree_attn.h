@@ -105,8 +105,8 @@ int tt_plan_build(const int32_t* key_lo, const int32_t* key_hi, int32_t n_keys, 
  * the `k_past/v_past` segment, read in place. */
 typedef struct tt_tensor {
     const void* ptr;        /* element [t][h][d] at ptr + t*stride_tok + h*stride_head + d */
-    int64_t stride_tok;     /* in elements */
-    int64_t stride_head;    /* in elements */
+    int64_t stride_tok;     /* in elements; >= 128, and < 2^23 for bf16 */
+    int64_t stride_head;    /* in elements; >= 128 */
 } tt_tensor;
 
 typedef struct tt_attn_problem {

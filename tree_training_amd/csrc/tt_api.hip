@@ -7,6 +7,7 @@
 namespace {
 
 constexpr int kAbiVersion = 1;
+constexpr int64_t kMaxTokStride = int64_t(1) << 23;   // elements
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
@@ -33,6 +34,8 @@ int make_dev(const tt_attn_problem* p, AttnDev* a) {
         const tt_tensor* t = ts[i];
         if (t->stride_tok < 128 || t->stride_head < 128 || (t->stride_tok % gran) || (t->stride_head % gran))
             return TT_E_ARG;
+        // bf16 kernels address a tile of up to 128 rows with 32-bit byte offsets
+        if (p->dtype == TT_DTYPE_BF16 && t->stride_tok >= kMaxTokStride) return TT_E_ARG;
         if (!aligned(t->ptr, ealign)) return TT_E_ARG;
     }
     a->q = p->q.ptr; a->q_st = p->q.stride_tok; a->q_sh = p->q.stride_head;
@@ -164,6 +167,7 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
     const size_t ealign = p->dtype == TT_DTYPE_BF16 ? 16 : 4;
     if (d_o.stride_tok < 128 || d_o.stride_head < 128 || (d_o.stride_tok % gran) || (d_o.stride_head % gran))
         return TT_E_ARG;
+    if (p->dtype == TT_DTYPE_BF16 && d_o.stride_tok >= kMaxTokStride) return TT_E_ARG;
     if (!aligned(d_o.ptr, ealign) || !aligned(o, ealign) || !aligned(dq, ealign) || !aligned(dk, ealign) ||
         !aligned(dv, ealign) || !aligned(ws, 4))
         return TT_E_ARG;

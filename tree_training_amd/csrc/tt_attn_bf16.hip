@@ -35,26 +35,13 @@ typedef __bf16 bf16;
 
 constexpr int D = 128;
 
-// LDS tiles hold tokens in their natural [token][d] order. Two stagings:
-//  * TT_LDS_DMA = 0 (default): rows padded to 288 bytes; each thread loads
-//    its slice of the next tile into registers while the current one
-//    computes, then stores it. The padding puts consecutive rows 8 banks
-//    apart, so 16-byte row reads, transposed reads and the stores all run at
-//    the minimum number of LDS passes.
-//  * TT_LDS_DMA = 1: unpadded 256-byte rows written by global_load_lds
-//    (no registers, no store instructions); 16-byte chunks are XOR-swizzled
-//    (chunk c of row r at c ^ swz(r)) for the same bank behaviour.
-#ifndef TT_LDS_DMA
-#define TT_LDS_DMA 0
-#endif
-#if TT_LDS_DMA
-constexpr int ROW = D;
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
-__device__ __forceinline__ int tile_off(int r, int d) { return r * ROW + (((d >> 3) ^ swz(r)) << 3) + (d & 7); }
-#else
+// LDS tiles hold tokens in their natural [token][d] order, rows padded to 288
+// bytes. Each thread loads its slice of the next tile into registers while
+// the current one computes, then stores it. The padding puts consecutive rows
+// 8 banks apart, so 16-byte row reads, transposed reads and the stores all run
+// in at most two LDS passes.
 constexpr int ROW = D + 16;
 __device__ __forceinline__ int tile_off(int r, int d) { return r * ROW + d; }
-#endif
 
 __device__ __forceinline__ bf16x8 zero8() {
     bf16x8 z;
@@ -91,24 +78,10 @@ __device__ __forceinline__ bf16x8 read_row_operand(const bf16* X, int r, int d0)
     return *(const bf16x8*)(X + tile_off(r, d0));
 }
 
-#if TT_LDS_DMA
-// Direct global -> LDS copy of rows [row0, row0 + n_rows) of a tile: each wave
-// instruction moves 4 rows (1024 bytes, 16 per lane) into swizzled LDS order.
-template <typename RowPtr>
-__device__ __forceinline__ void dma_rows(bf16* X, int row0, int n_rows, RowPtr row_ptr) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int rb = row0 + 4 * wave; rb < row0 + n_rows; rb += 16) {
-        const int r = rb + (lane >> 4);
-        const int c = (lane & 15) ^ swz(r);
-        __builtin_amdgcn_global_load_lds((glb_void*)(row_ptr(r) + 8 * c), (lds_void*)(X + rb * ROW), 16, 0, 0);
-    }
-}
 
-__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-#endif
-
-// Register staging: thread t holds rows 4*(t/16)+i (i < 4, up to n_rows) at
-// head dims 8*(t%16) .. +7 of a tile; 16 lanes cover one 256-byte row.
+// Register staging: thread t holds rows (t/16) + 16*i (i < NROWS/16) at head
+// dims 8*(t%16) .. +7 of a tile; 16 lanes cover one 256-byte row, and a wave
+// instruction moves four whole rows.
 template <int NROWS>
 struct RowRegs {
     bf16x8 x[NROWS / 16];
@@ -116,16 +89,30 @@ struct RowRegs {
 
 template <int NROWS, typename RowPtr>
 __device__ __forceinline__ void fetch_rows(RowRegs<NROWS>& r, int tid, RowPtr row_ptr) {
-    const int dc = (tid & 15) * 8, rg = (tid >> 4) * (NROWS / 16);
+    const int dc = (tid & 15) * 8, r0 = tid >> 4;
 #pragma unroll
-    for (int i = 0; i < NROWS / 16; ++i) r.x[i] = *(const bf16x8*)(row_ptr(rg + i) + dc);
+    for (int i = 0; i < NROWS / 16; ++i) r.x[i] = *(const bf16x8*)(row_ptr(r0 + 16 * i) + dc);
+}
+
+// Same, for NROWS rows of one tensor that all exist: row 0 at `base` (a
+// uniform pointer), rows `stb` bytes apart. The loads go through a buffer
+// resource: base and row steps in scalar registers, one 32-bit lane offset.
+template <int NROWS>
+__device__ __forceinline__ void fetch_rows_buf(RowRegs<NROWS>& r, int tid, const void* base, uint32_t stb) {
+    const uint32_t bytes = (NROWS - 1) * stb + 2 * D;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+    const uint32_t vo = (tid >> 4) * stb + 16 * (tid & 15);
+#pragma unroll
+    for (int i = 0; i < NROWS / 16; ++i)
+        r.x[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vo, (int)(16 * i * stb), 0));
 }
 
 template <int NROWS>
 __device__ __forceinline__ void store_rows(const RowRegs<NROWS>& r, int tid, bf16* X) {
-    const int dc = (tid & 15) * 8, rg = (tid >> 4) * (NROWS / 16);
+    const int dc = (tid & 15) * 8, r0 = tid >> 4;
 #pragma unroll
-    for (int i = 0; i < NROWS / 16; ++i) *(bf16x8*)(X + tile_off(rg + i, dc)) = r.x[i];
+    for (int i = 0; i < NROWS / 16; ++i) *(bf16x8*)(X + tile_off(r0 + 16 * i, dc)) = r.x[i];
 }
 
 __device__ __forceinline__ const bf16* key_row(const AttnDev& a, int kk, int g, bool isv) {
@@ -150,31 +137,41 @@ __device__ __forceinline__ void fetch_bounds(const AttnDev& a, int kt, Bounds& r
     }
 }
 
-// Staging of the K and V rows of key tile kt (out-of-range rows alias the
-// last key; their empty bounds mask them). begin() starts the loads for a
+// Staging of the K and V rows of key tile kt (rows past the last key alias
+// it; their empty bounds mask them). begin() starts the loads for a
 // stage; commit() makes them resident in that stage (before the barrier).
 struct KvTileStager {
-#if !TT_LDS_DMA
     RowRegs<TT_BK> k, v;
-#endif
-    __device__ __forceinline__ void begin(const AttnDev& a, int kt, int g, bf16* K, bf16* V) {
-        auto krow = [&](int r) { return key_row(a, min(kt * TT_BK + r, a.n_keys - 1), g, false); };
-        auto vrow = [&](int r) { return key_row(a, min(kt * TT_BK + r, a.n_keys - 1), g, true); };
-#if TT_LDS_DMA
-        dma_rows(K, 0, TT_BK, krow);
-        dma_rows(V, 0, TT_BK, vrow);
-#else
-        fetch_rows(k, threadIdx.x, krow);
-        fetch_rows(v, threadIdx.x, vrow);
-#endif
+    int k0;
+    bool direct;   // straddles gateway and own keys, or runs past the last key: loaded in commit()
+    __device__ __forceinline__ void begin(const AttnDev& a, int kt, int g) {
+        k0 = kt * TT_BK;
+        direct = false;
+        if (k0 + TT_BK <= a.n_past) {            // all gateway keys (uniform branch)
+            fetch_rows_buf(k, threadIdx.x, (const bf16*)a.kp + k0 * a.kp_st + g * a.kp_sh, 2 * a.kp_st);
+            fetch_rows_buf(v, threadIdx.x, (const bf16*)a.vp + k0 * a.vp_st + g * a.vp_sh, 2 * a.vp_st);
+        } else if (k0 >= a.n_past && k0 + TT_BK <= a.n_keys) {   // all own keys
+            const int64_t t0 = k0 - a.n_past;
+            fetch_rows_buf(k, threadIdx.x, (const bf16*)a.k + t0 * a.k_st + g * a.k_sh, 2 * a.k_st);
+            fetch_rows_buf(v, threadIdx.x, (const bf16*)a.v + t0 * a.v_st + g * a.v_sh, 2 * a.v_st);
+        } else {
+            direct = true;
+        }
     }
-    __device__ __forceinline__ void commit(bf16* K, bf16* V) {
-#if TT_LDS_DMA
-        dma_wait();
-#else
-        store_rows(k, threadIdx.x, K);
-        store_rows(v, threadIdx.x, V);
-#endif
+    __device__ __forceinline__ void commit(const AttnDev& a, int g, bf16* K, bf16* V) {
+        if (!direct) {
+            store_rows(k, threadIdx.x, K);
+            store_rows(v, threadIdx.x, V);
+            return;
+        }
+        // At most two tiles per launch take this path: copied row by row,
+        // without prefetch (short register live ranges).
+        const int dc = (threadIdx.x & 15) * 8, r0 = threadIdx.x >> 4;
+        for (int i = 0; i < TT_BK / 16; ++i) {
+            const int r = r0 + 16 * i, kk = min(k0 + r, a.n_keys - 1);
+            *(bf16x8*)(K + tile_off(r, dc)) = *(const bf16x8*)(key_row(a, kk, g, false) + dc);
+            *(bf16x8*)(V + tile_off(r, dc)) = *(const bf16x8*)(key_row(a, kk, g, true) + dc);
+        }
     }
 };
 
@@ -260,18 +257,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     KvTileStager stg;
     Bounds nb;
     if (cnt > 0) {
-        stg.begin(a, list[0] >> 1, g, st[0].K, st[0].V);
+        stg.begin(a, list[0] >> 1, g);
         fetch_bounds(a, list[0] >> 1, nb);
     }
     for (int it = 0; it < cnt; ++it) {
         FwdStage& S = st[it & 1];
         const bool full = list[it] & 1;
-        stg.commit(S.K, S.V);
+        stg.commit(a, g, S.K, S.V);
         store_bounds(nb, S.lo, S.hi);
         __syncthreads();
         if (it + 1 < cnt) {
             const int kt1 = list[it + 1] >> 1;
-            stg.begin(a, kt1, g, st[(it + 1) & 1].K, st[(it + 1) & 1].V);
+            stg.begin(a, kt1, g);
             fetch_bounds(a, kt1, nb);
         }
 
@@ -410,18 +407,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     KvTileStager stg;
     Bounds nb;
     if (cnt > 0) {
-        stg.begin(a, list[0] >> 1, g, st[0].K, st[0].V);
+        stg.begin(a, list[0] >> 1, g);
         fetch_bounds(a, list[0] >> 1, nb);
     }
     for (int it = 0; it < cnt; ++it) {
         DqStage& S = st[it & 1];
         const bool full = list[it] & 1;
-        stg.commit(S.K, S.V);
+        stg.commit(a, g, S.K, S.V);
         store_bounds(nb, S.lo, S.hi);
         __syncthreads();
         if (it + 1 < cnt) {
             const int kt1 = list[it + 1] >> 1;
-            stg.begin(a, kt1, g, st[(it + 1) & 1].K, st[(it + 1) & 1].V);
+            stg.begin(a, kt1, g);
             fetch_bounds(a, kt1, nb);
         }
 
@@ -473,10 +470,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // ----------------------------------------------------------------------------
 // backward: dK, dV (key-major, persistent over work items)
 // ----------------------------------------------------------------------------
-__device__ __forceinline__ int kb_chunks_dev(int qlo, int qhi) {
-    return qhi > qlo ? tt_cdiv(qhi - (qlo / TT_BQB) * TT_BQB, TT_QCH) : 1;
-}
-
 struct KvStage {
     bf16 Q[TT_BQB * ROW];
     bf16 Dn[TT_BQB * ROW];
@@ -484,43 +477,49 @@ struct KvStage {
     float dlt[TT_BQB];
 };
 
-// Staging of the Q and dO rows of a 32-query block of head h (rows past n_q
-// alias the last query; their lse is +inf so they contribute nothing), plus
-// one lse (log2 units) or delta value per thread for threads 0..31 / 64..95.
+// Staging of the Q and dO rows of a 32-query block of head h, plus the
+// block's lse (log2 units, loaded by wave 0) and delta (wave 1). Loads are
+// unconditional within a wave, so nothing waits on the prefetch before
+// commit(). The last block of the queries (rows past n_q alias the last
+// query; their lse is +inf so they contribute nothing) is copied in commit().
 struct QBlockStager {
-#if !TT_LDS_DMA
     RowRegs<TT_BQB> q, d;
-#endif
     float sv;
-    __device__ __forceinline__ void begin(const AttnDev& a, const BwdDev& bw, int q0, int h, KvStage& S) {
-        auto qrow = [&](int r) { return (const bf16*)a.q + (int64_t)min(q0 + r, a.n_q - 1) * a.q_st + h * a.q_sh; };
-        auto drow = [&](int r) {
-            return (const bf16*)bw.dout + (int64_t)min(q0 + r, a.n_q - 1) * bw.do_st + h * bw.do_sh;
-        };
-#if TT_LDS_DMA
-        dma_rows(S.Q, 0, TT_BQB, qrow);
-        dma_rows(S.Dn, 0, TT_BQB, drow);
-#else
-        fetch_rows(q, threadIdx.x, qrow);
-        fetch_rows(d, threadIdx.x, drow);
-#endif
-        if (threadIdx.x < TT_BQB) {
-            const int qq = q0 + threadIdx.x;
-            sv = qq < a.n_q ? bw.lse[(size_t)h * a.n_q + qq] * TT_LOG2E : INFINITY;
-        } else if (threadIdx.x >= 64 && threadIdx.x < 64 + TT_BQB) {
-            const int qq = q0 + threadIdx.x - 64;
-            sv = qq < a.n_q ? bw.delta[(size_t)h * a.n_q + qq] : 0.0f;
+    int q0, h;
+    __device__ __forceinline__ void begin(const AttnDev& a, const BwdDev& bw, int q0_, int h_) {
+        q0 = q0_;
+        h = h_;
+        if (q0 + TT_BQB <= a.n_q) {              // uniform branch
+            fetch_rows_buf(q, threadIdx.x, (const bf16*)a.q + (int64_t)q0 * a.q_st + h * a.q_sh, 2 * a.q_st);
+            fetch_rows_buf(d, threadIdx.x, (const bf16*)bw.dout + (int64_t)q0 * bw.do_st + h * bw.do_sh,
+                          2 * bw.do_st);
+        }
+        const int wave = threadIdx.x >> 6;
+        if (wave < 2) {
+            const float* src = (wave == 0 ? bw.lse : bw.delta) + (size_t)h * a.n_q;
+            sv = src[min(q0 + (int)(threadIdx.x & 31), a.n_q - 1)];
         }
     }
-    __device__ __forceinline__ void commit(KvStage& S) {
-#if TT_LDS_DMA
-        dma_wait();
-#else
-        store_rows(q, threadIdx.x, S.Q);
-        store_rows(d, threadIdx.x, S.Dn);
-#endif
-        if (threadIdx.x < TT_BQB) S.lse[threadIdx.x] = sv;
-        else if (threadIdx.x >= 64 && threadIdx.x < 64 + TT_BQB) S.dlt[threadIdx.x - 64] = sv;
+    __device__ __forceinline__ void commit(const AttnDev& a, const BwdDev& bw, KvStage& S) {
+        if (q0 + TT_BQB <= a.n_q) {
+            store_rows(q, threadIdx.x, S.Q);
+            store_rows(d, threadIdx.x, S.Dn);
+        } else {
+            const int dc = (threadIdx.x & 15) * 8, r0 = threadIdx.x >> 4;
+            for (int i = 0; i < TT_BQB / 16; ++i) {
+                const int r = r0 + 16 * i;
+                const int64_t qq = min(q0 + r, a.n_q - 1);
+                *(bf16x8*)(S.Q + tile_off(r, dc)) = *(const bf16x8*)((const bf16*)a.q + qq * a.q_st + h * a.q_sh + dc);
+                *(bf16x8*)(S.Dn + tile_off(r, dc)) =
+                    *(const bf16x8*)((const bf16*)bw.dout + qq * bw.do_st + h * bw.do_sh + dc);
+            }
+        }
+        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+        if (wave < 2 && lane < TT_BQB) {
+            const bool in = q0 + lane < a.n_q;
+            if (wave == 0) S.lse[lane] = in ? sv * TT_LOG2E : INFINITY;
+            else S.dlt[lane] = in ? sv : 0.0f;
+        }
     }
 };
 
@@ -529,6 +528,7 @@ struct QBlockStager {
 #endif
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAVES_PER_EU, TT_DKDV_WAVES_PER_EU))) void bwd_dkdv_bf16_kernel(AttnDev a, BwdDev bw) {
     __shared__ __attribute__((aligned(16))) KvStage st[2];
+    __shared__ __attribute__((aligned(16))) bf16 Vs[TT_BKB * ROW];   // V rows of the item's keys
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int col = lane & 31, half = lane >> 5;
@@ -546,31 +546,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
         const int kb = a.kb_order[lo_r];
         const int chunk = item - a.kb_base[lo_r];
         const int qlo = a.kb_qlo[kb], qhi = a.kb_qhi[kb];
-        const bool split = kb_chunks_dev(qlo, qhi) > 1;
-        int q_start = 0, q_stop = 0;
-        if (qhi > qlo) {
-            q_start = (qlo / TT_BQB) * TT_BQB + chunk * TT_QCH;
-            q_stop = min(q_start + TT_QCH, qhi);
-        }
+        const bool split = tt_kb_items(qlo, qhi) > 1;
+        int q_start, q_stop;
+        tt_kb_item_range(qlo, qhi, chunk, q_start, q_stop);
 
+        // V rows of the tile's 128 keys go to LDS (read as MFMA operands every
+        // step); K of the lane's key stays in registers. Keys past the end alias
+        // the last key and are never visible.
+        {
+            const int k0 = kb * TT_BKB;
+            RowRegs<TT_BKB> vr;
+            if (k0 + TT_BKB <= a.n_past) {
+                fetch_rows_buf(vr, threadIdx.x, (const bf16*)a.vp + k0 * a.vp_st + g * a.vp_sh, 2 * a.vp_st);
+            } else if (k0 >= a.n_past && k0 + TT_BKB <= a.n_keys) {
+                fetch_rows_buf(vr, threadIdx.x, (const bf16*)a.v + (int64_t)(k0 - a.n_past) * a.v_st + g * a.v_sh,
+                               2 * a.v_st);
+            } else {
+                auto vrow = [&](int r) { return key_row(a, min(k0 + r, a.n_keys - 1), g, true); };
+                fetch_rows(vr, threadIdx.x, vrow);
+            }
+            store_rows(vr, threadIdx.x, Vs);
+        }
         const int kk = kb * TT_BKB + wave * 32 + col;   // this lane's key (MFMA column)
         int lo = 0, hi = 0;
-        bf16x8 kbv[8], vbv[8];
+        bf16x8 kbv[8];
         if (kk < a.n_keys) {
             lo = max(a.key_lo[kk], 0);
             hi = min(a.key_hi[kk], a.n_q);
             const bf16* kp = key_row(a, kk, g, false) + 8 * half;
-            const bf16* vp = key_row(a, kk, g, true) + 8 * half;
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                kbv[t] = *(const bf16x8*)(kp + 16 * t);
-                vbv[t] = *(const bf16x8*)(vp + 16 * t);
-            }
+            for (int t = 0; t < 8; ++t) kbv[t] = *(const bf16x8*)(kp + 16 * t);
         } else {
 #pragma unroll
-            for (int t = 0; t < 8; ++t) { kbv[t] = zero8(); vbv[t] = zero8(); }
+            for (int t = 0; t < 8; ++t) kbv[t] = zero8();
         }
         if (lo >= hi) { lo = a.n_q; hi = 0; }          // invisible key: neutral for min/max
+        const unsigned vis_w = (unsigned)(hi - lo);     // query q sees the key iff q - lo < vis_w (unsigned)
         const int w_lo = wave_min_i(lo), w_hi = wave_max_i(hi);
         const int w_maxlo = wave_max_i(lo < hi ? lo : -1), w_minhi = wave_min_i(lo < hi ? hi : -1);
         const bool w_all_vis = wave_min_i((kk < a.n_keys && lo < hi) ? 1 : 0) == 1;
@@ -579,17 +590,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
 #pragma unroll
         for (int i = 0; i < 4; ++i) { dk[i] = (f32x16){}; dv[i] = (f32x16){}; }
 
-        const int n_steps = (q_stop > q_start) ? tt_cdiv(q_stop - q_start, TT_BQB) * a.rep : 0;
+        // Query blocks are walked from the top of the range down, so items whose
+        // ranges end at the same subtree end read the same rows at the same time.
+        const int q_top = (q_stop > q_start) ? ((q_stop - 1) / TT_BQB) * TT_BQB : 0;
+        const int n_steps = (q_stop > q_start) ? ((q_top - q_start) / TT_BQB + 1) * a.rep : 0;
         QBlockStager stg;
-        if (n_steps > 0) stg.begin(a, bw, q_start, g * a.rep, st[0]);
+        if (n_steps > 0) stg.begin(a, bw, q_top, g * a.rep);
         for (int s = 0; s < n_steps; ++s) {
             KvStage& S = st[s & 1];
-            const int q0 = q_start + (s / a.rep) * TT_BQB;
-            stg.commit(S);
+            const int q0 = q_top - (s / a.rep) * TT_BQB;
+            stg.commit(a, bw, S);
             __syncthreads();
             if (s + 1 < n_steps) {
                 const int s1 = s + 1;
-                stg.begin(a, bw, q_start + (s1 / a.rep) * TT_BQB, g * a.rep + s1 % a.rep, st[s1 & 1]);
+                stg.begin(a, bw, q_top - (s1 / a.rep) * TT_BQB, g * a.rep + s1 % a.rep);
             }
             const int q1 = min(q0 + TT_BQB, a.n_q);
             if (!((q0 < w_hi) && (q1 > w_lo))) continue;   // no key of this wave is seen here
@@ -600,7 +614,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
                 sc = mfma32(read_row_operand(S.Q, col, 16 * t + 8 * half), kbv[t], sc);
-                dp = mfma32(read_row_operand(S.Dn, col, 16 * t + 8 * half), vbv[t], dp);
+                dp = mfma32(read_row_operand(S.Dn, col, 16 * t + 8 * half),
+                            read_row_operand(Vs, wave * 32 + col, 16 * t + 8 * half), dp);
             }
 #pragma unroll
             for (int grp = 0; grp < 4; ++grp) {
@@ -609,9 +624,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
                 const f32x4 dl = *(const f32x4*)(S.dlt + r0);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int qq = q0 + r0 + e;
                     float p = fast_exp2(fmaf(sc[4 * grp + e], c, -l2[e]));
-                    if (!full) p = (lo <= qq && qq < hi) ? p : 0.0f;
+                    if (!full) p = ((unsigned)(q0 + r0 + e - lo) < vis_w) ? p : 0.0f;
                     sc[4 * grp + e] = p;                              // P
                     dp[4 * grp + e] = p * (dp[4 * grp + e] - dl[e]);  // dS
                 }
@@ -665,7 +679,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
 // Split key tiles: zero their fp32 sums before the dK/dV pass ...
 __global__ __launch_bounds__(256) void bwd_split_zero_kernel(AttnDev a, BwdDev bw) {
     const int kb = blockIdx.x, g = blockIdx.y;
-    if (kb_chunks_dev(a.kb_qlo[kb], a.kb_qhi[kb]) <= 1) return;
+    if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb]) <= 1) return;
     for (int e = threadIdx.x; e < TT_BKB * D; e += 256) {
         const int key = kb * TT_BKB + e / D;
         if (key >= a.n_keys) break;
@@ -678,7 +692,7 @@ __global__ __launch_bounds__(256) void bwd_split_zero_kernel(AttnDev a, BwdDev b
 // ... and convert them after it (own keys -> dk/dv, gateway keys -> fp32 accumulators).
 __global__ __launch_bounds__(256) void bwd_split_finalize_kernel(AttnDev a, BwdDev bw) {
     const int kb = blockIdx.x, g = blockIdx.y;
-    if (kb_chunks_dev(a.kb_qlo[kb], a.kb_qhi[kb]) <= 1) return;
+    if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb]) <= 1) return;
     for (int e = threadIdx.x; e < TT_BKB * D; e += 256) {
         const int key = kb * TT_BKB + e / D;
         if (key >= a.n_keys) break;

@@ -31,6 +31,29 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __host__ __device__ inline int tt_cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// dK/dV work items of a key tile whose visible queries are [qlo, qhi). A range
+// of at most TT_QCH queries is one item; a longer one is cut at multiples of
+// TT_QCH in absolute query index, so workgroups busy with different key tiles
+// at the same time walk the same query windows (and share them in L2).
+__host__ __device__ inline int tt_kb_items(int qlo, int qhi) {
+    if (qhi - qlo <= TT_QCH) return 1;
+    return (qhi - 1) / TT_QCH - qlo / TT_QCH + 1;
+}
+// Query range [q_start, q_stop) of item `item`; q_start is a multiple of TT_BQB.
+__host__ __device__ inline void tt_kb_item_range(int qlo, int qhi, int item, int& q_start, int& q_stop) {
+    q_start = q_stop = 0;
+    if (qhi <= qlo) return;
+    const int a = (qlo / TT_BQB) * TT_BQB;
+    if (qhi - qlo <= TT_QCH) {
+        q_start = a;
+        q_stop = qhi;
+        return;
+    }
+    const int w = qlo / TT_QCH + item;
+    q_start = a > w * TT_QCH ? a : w * TT_QCH;
+    q_stop = qhi < (w + 1) * TT_QCH ? qhi : (w + 1) * TT_QCH;
+}
+
 // Plan buffer layout. Header (bytes): [0,8) uint64 visible pairs per head;
 // int32 at 8: n_qb, 12: n_kt, 16: n_kb, 20: n_items (dK/dV work items).
 // Then int32 arrays:

@@ -281,10 +281,6 @@ __global__ void plan_kb_order_kernel(const int32_t* __restrict__ kb_qlo, const i
     kb_order[rank] = i;
 }
 
-__device__ __forceinline__ int kb_chunks(int qlo, int qhi) {
-    return qhi > qlo ? tt_cdiv(qhi - (qlo / TT_BQB) * TT_BQB, TT_QCH) : 1;
-}
-
 // Exclusive prefix sum of work items per key tile, in kb_order order (one workgroup).
 __global__ __launch_bounds__(1024) void plan_kb_base_kernel(const int32_t* __restrict__ kb_qlo,
                                                             const int32_t* __restrict__ kb_qhi,
@@ -300,7 +296,7 @@ __global__ __launch_bounds__(1024) void plan_kb_base_kernel(const int32_t* __res
         int v = 0;
         if (r < n_kb) {
             const int kb = kb_order[r];
-            v = kb_chunks(kb_qlo[kb], kb_qhi[kb]);
+            v = tt_kb_items(kb_qlo[kb], kb_qhi[kb]);
         }
         s_scan[tid] = v;
         __syncthreads();
