@@ -17,7 +17,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 LIBDIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIBDIR, "libtree_attn.so")
-SOURCES = ["tt_meta.hip", "tt_attn_bf16.hip", "tt_attn_f32.hip", "tt_api.hip"]
+SOURCES = ["tt_meta.hip", "tt_attn_fwd_bf16.hip", "tt_attn_bwd_bf16.hip", "tt_attn_f32.hip", "tt_api.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17",
@@ -34,8 +34,15 @@ def hipcc() -> str:
     return cand if os.path.exists(cand) else (shutil.which("hipcc") or cand)
 
 
+# Per-source flags. The bf16 forward never produces or consumes NaN (masked
+# scores are -inf and every exp2/max/sum on them is guarded), so it is built
+# without NaN semantics and with IEEE mode off: its row max then needs no
+# operand canonicalisation (v_max3_f32 straight on MFMA results).
+SOURCE_FLAGS = {"tt_attn_fwd_bf16.hip": ["-fno-honor-nans", "-mno-amdgpu-ieee"]}
+
+
 def _compile(src: str, obj: str, extra):
-    cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, []), *extra, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
@@ -48,7 +55,7 @@ def build(verbose: bool = False, extra=(), out: str = LIB) -> str:
     os.makedirs(objdir, exist_ok=True)
     os.makedirs(os.path.dirname(out), exist_ok=True)
     objs = [os.path.join(objdir, s.replace(".hip", ".o")) for s in SOURCES]
-    with ThreadPoolExecutor(max_workers=min(4, len(SOURCES))) as ex:
+    with ThreadPoolExecutor(max_workers=min(5, len(SOURCES))) as ex:
         logs = list(ex.map(lambda so: _compile(so[0], so[1], list(extra)), zip(SOURCES, objs)))
     if verbose:
         for s, log in zip(SOURCES, logs):

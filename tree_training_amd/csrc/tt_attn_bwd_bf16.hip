@@ -1,342 +1,9 @@
-// Tree-masked GQA flash attention for gfx950, bf16 in / fp32 accumulate.
-//
-// Forward and dQ pass (query-major): a workgroup owns TT_BQ = 128 queries of
-// one q head; each of its four waves keeps 32 queries in registers and walks
-// the non-empty key tiles of the plan. Scores are computed transposed,
-// S^T = K Q^T with v_mfma_f32_32x32x16_bf16, so a lane owns one query column:
-// the online-softmax row max needs a single cross-half exchange and the
-// probabilities feed O^T = V^T P^T straight from the accumulators. K and V
-// tiles sit in LDS in their natural [key][d] layout; the V^T (and, for dQ,
-// K^T) operands come out of them through gfx950's transposing LDS read
-// (ds_read_b64_tr_b16). Tiles are software-pipelined: the next tile's
-// global loads are in flight (in registers) while the current tile computes
-// out of the other LDS stage; one barrier per tile.
-//
-// dK/dV pass (key-major): a workgroup owns TT_BKB = 128 keys of one kv head;
-// each wave keeps K and V of 32 keys as MFMA operands and dK, dV of those
-// keys in fp32 accumulators, and walks a range of queries that can see them
-// (for a DFS-packed tree the range is contiguous: [first key, subtree end))
-// for the Hq/Hkv q heads of the group, with Q and dO blocks staged in LDS
-// (double-buffered) and read both row-wise and transposed. Ranges longer than
-// TT_QCH queries are split
-// into several work items; a persistent grid walks the items widest-first.
-// Unsplit tiles write dK/dV directly; split tiles add fp32 partial sums into a
-// workspace that a finalize pass converts.
-//
-// Visibility: key j is seen by query i iff key_lo[j] <= i < key_hi[j]; the
-// plan marks each (query block, key tile) empty (skipped), full (no mask) or
-// partial (interval test per element).
-#include "tt_common.h"
-#include "tt_internal.h"
+// Tree-masked GQA flash attention backward for gfx950 (bf16 in, fp32
+// accumulate): delta, dQ (query-major) and dK/dV (key-major); the tiling is
+// described in tt_bf16_tiles.h.
+#include "tt_bf16_tiles.h"
 
 namespace {
-
-typedef __bf16 bf16;
-
-constexpr int D = 128;
-
-// LDS tiles hold tokens in their natural [token][d] order, rows padded to 288
-// bytes. Each thread loads its slice of the next tile into registers while
-// the current one computes, then stores it. The padding puts consecutive rows
-// 8 banks apart, so 16-byte row reads, transposed reads and the stores all run
-// in at most two LDS passes.
-constexpr int ROW = D + 16;
-__device__ __forceinline__ int tile_off(int r, int d) { return r * ROW + d; }
-
-__device__ __forceinline__ bf16x8 zero8() {
-    bf16x8 z;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) z[i] = (bf16)0.0f;
-    return z;
-}
-
-typedef short v4i16 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(1))) const void glb_void;
-
-// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
-// (i & 3) of the 8-byte chunks read by lanes 4k + (i >> 2), k = 0..3.
-__device__ __forceinline__ bf16x4 ds_read_tr(const bf16* p) {
-    const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p));
-    return __builtin_bit_cast(bf16x4, r);
-}
-
-// MFMA operand "column = head dim, k = 16 tokens" from a tile X: lane l gets
-// X[r0 + kappa(e)][dbase + (l & 31)], kappa(e) = 8*(e/4) + 4*(l>>5) + (e%4) —
-// the accumulator row order, so it pairs with probabilities taken straight
-// from a score accumulator.
-__device__ __forceinline__ bf16x8 read_tr_operand(const bf16* X, int r0, int dbase, int lane) {
-    const int j = lane & 15, grp = lane >> 4;
-    const int d = dbase + 16 * (grp & 1) + 4 * (j & 3);
-    const int r = r0 + 4 * (grp >> 1) + (j >> 2);
-    return cat44(ds_read_tr(X + tile_off(r, d)), ds_read_tr(X + tile_off(r + 8, d)));
-}
-
-// MFMA operand "row = token, k = 16 head dims": X[r][d0 .. d0+7], d0 % 8 == 0.
-__device__ __forceinline__ bf16x8 read_row_operand(const bf16* X, int r, int d0) {
-    return *(const bf16x8*)(X + tile_off(r, d0));
-}
-
-
-// Register staging: thread t holds rows (t/16) + 16*i (i < NROWS/16) at head
-// dims 8*(t%16) .. +7 of a tile; 16 lanes cover one 256-byte row, and a wave
-// instruction moves four whole rows.
-template <int NROWS>
-struct RowRegs {
-    bf16x8 x[NROWS / 16];
-};
-
-template <int NROWS, typename RowPtr>
-__device__ __forceinline__ void fetch_rows(RowRegs<NROWS>& r, int tid, RowPtr row_ptr) {
-    const int dc = (tid & 15) * 8, r0 = tid >> 4;
-#pragma unroll
-    for (int i = 0; i < NROWS / 16; ++i) r.x[i] = *(const bf16x8*)(row_ptr(r0 + 16 * i) + dc);
-}
-
-// Same, for NROWS rows of one tensor that all exist: row 0 at `base` (a
-// uniform pointer), rows `stb` bytes apart. The loads go through a buffer
-// resource: base and row steps in scalar registers, one 32-bit lane offset.
-template <int NROWS>
-__device__ __forceinline__ void fetch_rows_buf(RowRegs<NROWS>& r, int tid, const void* base, uint32_t stb) {
-    const uint32_t bytes = (NROWS - 1) * stb + 2 * D;
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-    const uint32_t vo = (tid >> 4) * stb + 16 * (tid & 15);
-#pragma unroll
-    for (int i = 0; i < NROWS / 16; ++i)
-        r.x[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vo, (int)(16 * i * stb), 0));
-}
-
-template <int NROWS>
-__device__ __forceinline__ void store_rows(const RowRegs<NROWS>& r, int tid, bf16* X) {
-    const int dc = (tid & 15) * 8, r0 = tid >> 4;
-#pragma unroll
-    for (int i = 0; i < NROWS / 16; ++i) *(bf16x8*)(X + tile_off(r0 + 16 * i, dc)) = r.x[i];
-}
-
-__device__ __forceinline__ const bf16* key_row(const AttnDev& a, int kk, int g, bool isv) {
-    if (kk < a.n_past) {
-        return isv ? (const bf16*)a.vp + kk * a.vp_st + g * a.vp_sh
-                   : (const bf16*)a.kp + kk * a.kp_st + g * a.kp_sh;
-    }
-    const int64_t t = kk - a.n_past;
-    return isv ? (const bf16*)a.v + t * a.v_st + g * a.v_sh : (const bf16*)a.k + t * a.k_st + g * a.k_sh;
-}
-
-struct Bounds {
-    int lo, hi;
-};
-
-__device__ __forceinline__ void fetch_bounds(const AttnDev& a, int kt, Bounds& r) {
-    const int t = threadIdx.x;
-    if (t < TT_BK) {
-        const int kk = kt * TT_BK + t;
-        r.lo = kk < a.n_keys ? a.key_lo[kk] : 0;
-        r.hi = kk < a.n_keys ? a.key_hi[kk] : 0;
-    }
-}
-
-// Staging of the K and V rows of key tile kt (rows past the last key alias
-// it; their empty bounds mask them). begin() starts the loads for a
-// stage; commit() makes them resident in that stage (before the barrier).
-struct KvTileStager {
-    RowRegs<TT_BK> k, v;
-    int k0;
-    bool direct;   // straddles gateway and own keys, or runs past the last key: loaded in commit()
-    __device__ __forceinline__ void begin(const AttnDev& a, int kt, int g) {
-        k0 = kt * TT_BK;
-        direct = false;
-        if (k0 + TT_BK <= a.n_past) {            // all gateway keys (uniform branch)
-            fetch_rows_buf(k, threadIdx.x, (const bf16*)a.kp + k0 * a.kp_st + g * a.kp_sh, 2 * a.kp_st);
-            fetch_rows_buf(v, threadIdx.x, (const bf16*)a.vp + k0 * a.vp_st + g * a.vp_sh, 2 * a.vp_st);
-        } else if (k0 >= a.n_past && k0 + TT_BK <= a.n_keys) {   // all own keys
-            const int64_t t0 = k0 - a.n_past;
-            fetch_rows_buf(k, threadIdx.x, (const bf16*)a.k + t0 * a.k_st + g * a.k_sh, 2 * a.k_st);
-            fetch_rows_buf(v, threadIdx.x, (const bf16*)a.v + t0 * a.v_st + g * a.v_sh, 2 * a.v_st);
-        } else {
-            direct = true;
-        }
-    }
-    __device__ __forceinline__ void commit(const AttnDev& a, int g, bf16* K, bf16* V) {
-        if (!direct) {
-            store_rows(k, threadIdx.x, K);
-            store_rows(v, threadIdx.x, V);
-            return;
-        }
-        // At most two tiles per launch take this path: copied row by row,
-        // without prefetch (short register live ranges).
-        const int dc = (threadIdx.x & 15) * 8, r0 = threadIdx.x >> 4;
-        for (int i = 0; i < TT_BK / 16; ++i) {
-            const int r = r0 + 16 * i, kk = min(k0 + r, a.n_keys - 1);
-            *(bf16x8*)(K + tile_off(r, dc)) = *(const bf16x8*)(key_row(a, kk, g, false) + dc);
-            *(bf16x8*)(V + tile_off(r, dc)) = *(const bf16x8*)(key_row(a, kk, g, true) + dc);
-        }
-    }
-};
-
-__device__ __forceinline__ void store_bounds(const Bounds& r, int* s_lo, int* s_hi) {
-    const int t = threadIdx.x;
-    if (t < TT_BK) {
-        s_lo[t] = r.lo;
-        s_hi[t] = r.hi;
-    }
-}
-
-// Lane's 32 query-column scores -> -inf where the key is invisible.
-__device__ __forceinline__ void mask_scores(f32x16 (&s)[2], const int* s_lo, const int* s_hi, int qi, int half) {
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-#pragma unroll
-        for (int grp = 0; grp < 4; ++grp) {
-            const int k0 = 32 * b + 8 * grp + 4 * half;
-            const i32x4 lo = *(const i32x4*)(s_lo + k0);
-            const i32x4 hi = *(const i32x4*)(s_hi + k0);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const bool vis = lo[e] <= qi && qi < hi[e];
-                s[b][4 * grp + e] = vis ? s[b][4 * grp + e] : -INFINITY;
-            }
-        }
-    }
-}
-
-// blockIdx.x -> (query block, q head). Workgroups are dispatched round-robin
-// over the 8 XCDs; each XCD gets the q heads of whole kv-head groups so their
-// K/V stay in its L2, and the heaviest query blocks go first.
-__device__ __forceinline__ void decode_qblock(const AttnDev& a, int& qb, int& h) {
-    const int bid = blockIdx.x;
-    if ((a.hq & 7) == 0) {
-        const int hpx = a.hq >> 3, xcd = bid & 7, slot = bid >> 3;
-        h = xcd * hpx + slot % hpx;
-        qb = a.row_order[slot / hpx];
-    } else {
-        h = bid % a.hq;
-        qb = a.row_order[bid / a.hq];
-    }
-}
-
-// ----------------------------------------------------------------------------
-// forward
-// ----------------------------------------------------------------------------
-struct FwdStage {
-    bf16 K[TT_BK * ROW];
-    bf16 V[TT_BK * ROW];
-    int lo[TT_BK];
-    int hi[TT_BK];
-};
-
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_bf16_kernel(AttnDev a, bf16* __restrict__ out, float* __restrict__ lse) {
-    __shared__ __attribute__((aligned(16))) FwdStage st[2];
-
-    int qb, h;
-    decode_qblock(a, qb, h);
-    const int g = h / a.rep;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int col = lane & 31, half = lane >> 5;
-    const int qi = qb * TT_BQ + wave * 32 + col;
-    const float c = a.scale * TT_LOG2E;
-
-    bf16x8 qa[8];
-    if (qi < a.n_q) {
-        const bf16* qp = (const bf16*)a.q + qi * a.q_st + h * a.q_sh + 8 * half;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) qa[t] = *(const bf16x8*)(qp + 16 * t);
-    } else {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) qa[t] = zero8();
-    }
-
-    f32x16 o[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = (f32x16){};
-    float m_run = -INFINITY, l_run = 0.0f;
-
-    const int cnt = a.row_cnt[qb];
-    const int* list = a.row_list + (size_t)qb * a.n_kt;
-    KvTileStager stg;
-    Bounds nb;
-    if (cnt > 0) {
-        stg.begin(a, list[0] >> 1, g);
-        fetch_bounds(a, list[0] >> 1, nb);
-    }
-    for (int it = 0; it < cnt; ++it) {
-        FwdStage& S = st[it & 1];
-        const bool full = list[it] & 1;
-        stg.commit(a, g, S.K, S.V);
-        store_bounds(nb, S.lo, S.hi);
-        __syncthreads();
-        if (it + 1 < cnt) {
-            const int kt1 = list[it + 1] >> 1;
-            stg.begin(a, kt1, g);
-            fetch_bounds(a, kt1, nb);
-        }
-
-        f32x16 s[2];
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            s[b] = (f32x16){};
-#pragma unroll
-            for (int t = 0; t < 8; ++t) s[b] = mfma32(read_row_operand(S.K, 32 * b + col, 16 * t + 8 * half), qa[t], s[b]);
-        }
-        if (!full) mask_scores(s, S.lo, S.hi, qi, half);
-
-        float mx = -INFINITY;
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx * c);
-        const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-        const float alpha = fast_exp2(m_run - m_use);
-        float psum = 0.0f;
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float p = fast_exp2(fmaf(s[b][r], c, -m_use));
-                s[b][r] = p;
-                psum += p;
-            }
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-        if (__ballot(alpha != 1.0f)) {
-#pragma unroll
-            for (int db = 0; db < 4; ++db) o[db] *= alpha;
-        }
-
-#pragma unroll
-        for (int stp = 0; stp < 4; ++stp) {
-            const f32x16& pb = s[stp >> 1];
-            const int r0 = 8 * (stp & 1);
-            const bf16x8 pk = pack8(pb[r0 + 0], pb[r0 + 1], pb[r0 + 2], pb[r0 + 3], pb[r0 + 4], pb[r0 + 5],
-                                    pb[r0 + 6], pb[r0 + 7]);
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-                o[db] = mfma32(read_tr_operand(S.V, 16 * stp, 32 * db, lane), pk, o[db]);
-        }
-    }
-
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
-    if (qi < a.n_q) {
-        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-        bf16* op = out + ((size_t)qi * a.hq + h) * D;
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int grp = 0; grp < 4; ++grp) {
-                bf16x4 w;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) w[e] = (bf16)(o[db][4 * grp + e] * inv);
-                *(bf16x4*)(op + 32 * db + 8 * grp + 4 * half) = w;
-            }
-        if (half == 0) {
-            const float m_fin = (m_run == -INFINITY) ? 0.0f : m_run;
-            lse[(size_t)h * a.n_q + qi] = l_tot > 0.0f ? (m_fin + __log2f(l_tot)) * TT_LN2 : -INFINITY;
-        }
-    }
-}
 
 // ----------------------------------------------------------------------------
 // backward: delta = rowsum(dO * O)
@@ -473,8 +140,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 struct KvStage {
     bf16 Q[TT_BQB * ROW];
     bf16 Dn[TT_BQB * ROW];
-    float lse[TT_BQB];
-    float dlt[TT_BQB];
+    float lse[TT_BQB];     // log2 units
+    float ndlt[TT_BQB];    // -delta
 };
 
 // Staging of the Q and dO rows of a 32-query block of head h, plus the
@@ -518,7 +185,7 @@ struct QBlockStager {
         if (wave < 2 && lane < TT_BQB) {
             const bool in = q0 + lane < a.n_q;
             if (wave == 0) S.lse[lane] = in ? sv * TT_LOG2E : INFINITY;
-            else S.dlt[lane] = in ? sv : 0.0f;
+            else S.ndlt[lane] = in ? -sv : 0.0f;
         }
     }
 };
@@ -595,19 +262,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
         const int q_top = (q_stop > q_start) ? ((q_stop - 1) / TT_BQB) * TT_BQB : 0;
         const int n_steps = (q_stop > q_start) ? ((q_top - q_start) / TT_BQB + 1) * a.rep : 0;
         QBlockStager stg;
-        if (n_steps > 0) stg.begin(a, bw, q_top, g * a.rep);
+        // step s covers query block q0 of q head g*rep + hh; (q0, hh) of the next
+        // step are kept incrementally
+        int q0 = q_top, hh = 0;
+        if (n_steps > 0) stg.begin(a, bw, q0, g * a.rep);
         for (int s = 0; s < n_steps; ++s) {
             KvStage& S = st[s & 1];
-            const int q0 = q_top - (s / a.rep) * TT_BQB;
             stg.commit(a, bw, S);
             __syncthreads();
-            if (s + 1 < n_steps) {
-                const int s1 = s + 1;
-                stg.begin(a, bw, q_top - (s1 / a.rep) * TT_BQB, g * a.rep + s1 % a.rep);
+            const int q0_cur = q0;
+            if (++hh == a.rep) {
+                hh = 0;
+                q0 -= TT_BQB;
             }
-            const int q1 = min(q0 + TT_BQB, a.n_q);
-            if (!((q0 < w_hi) && (q1 > w_lo))) continue;   // no key of this wave is seen here
-            const bool full = w_all_vis && (w_maxlo <= q0) && (w_minhi >= q1);
+            if (s + 1 < n_steps) stg.begin(a, bw, q0, g * a.rep + hh);
+            const int q1 = min(q0_cur + TT_BQB, a.n_q);
+            if (!((q0_cur < w_hi) && (q1 > w_lo))) continue;   // no key of this wave is seen here
+            const bool full = w_all_vis && (w_maxlo <= q0_cur) && (w_minhi >= q1);
 
             // S = Q K^T and dP = dO V^T: rows = queries, lane = key column.
             f32x16 sc = (f32x16){}, dp = (f32x16){};
@@ -617,17 +288,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
                 dp = mfma32(read_row_operand(S.Dn, col, 16 * t + 8 * half),
                             read_row_operand(Vs, wave * 32 + col, 16 * t + 8 * half), dp);
             }
+            // P = exp(S*scale - lse) (zero where the key is invisible), dS = P (dP - delta).
 #pragma unroll
             for (int grp = 0; grp < 4; ++grp) {
                 const int r0 = 8 * grp + 4 * half;
                 const f32x4 l2 = *(const f32x4*)(S.lse + r0);
-                const f32x4 dl = *(const f32x4*)(S.dlt + r0);
+                const f32x4 nd = *(const f32x4*)(S.ndlt + r0);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     float p = fast_exp2(fmaf(sc[4 * grp + e], c, -l2[e]));
-                    if (!full) p = ((unsigned)(q0 + r0 + e - lo) < vis_w) ? p : 0.0f;
-                    sc[4 * grp + e] = p;                              // P
-                    dp[4 * grp + e] = p * (dp[4 * grp + e] - dl[e]);  // dS
+                    if (!full) p = ((unsigned)(q0_cur + r0 + e - lo) < vis_w) ? p : 0.0f;
+                    sc[4 * grp + e] = p;
+                    dp[4 * grp + e] = p * (dp[4 * grp + e] + nd[e]);
                 }
             }
             // dV += P^T dO, dK += dS^T Q: contraction over the 32 queries.
@@ -735,11 +407,6 @@ int tt_selftest_mfma_launch(const void* a, const void* b, float* d, hipStream_t 
     return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
 }
 
-int tt_fwd_bf16_launch(const AttnDev& a, void* o, float* lse, hipStream_t s) {
-    hipLaunchKernelGGL(fwd_bf16_kernel, dim3(a.n_qb * a.hq), dim3(256), 0, s, a, (bf16*)o, lse);
-    return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
-}
-
 // Persistent grid for the dK/dV pass: a multiple of Hkv so every workgroup
 // keeps one kv head (and, with Hkv = 8, one XCD).
 static int dkdv_grid(const AttnDev& a) {
@@ -766,3 +433,4 @@ int tt_bwd_bf16_launch(const AttnDev& a, const BwdDev& b, hipStream_t s) {
     }
     return TT_OK;
 }
+

@@ -1,0 +1,143 @@
+// Tree-masked GQA flash attention forward for gfx950 (bf16 in, fp32
+// accumulate); the tiling is described in tt_bf16_tiles.h.
+//
+// Built without NaN semantics and with IEEE mode off (see build.py): masked
+// scores are -inf, never NaN, and every exp2/max/sum on them is guarded, so the
+// row max runs as v_max3_f32 straight on MFMA results.
+#include "tt_bf16_tiles.h"
+
+namespace {
+
+// ----------------------------------------------------------------------------
+// forward
+// ----------------------------------------------------------------------------
+struct FwdStage {
+    bf16 K[TT_BK * ROW];
+    bf16 V[TT_BK * ROW];
+    int lo[TT_BK];
+    int hi[TT_BK];
+};
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_bf16_kernel(AttnDev a, bf16* __restrict__ out, float* __restrict__ lse) {
+    __shared__ __attribute__((aligned(16))) FwdStage st[2];
+
+    int qb, h;
+    decode_qblock(a, qb, h);
+    const int g = h / a.rep;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int col = lane & 31, half = lane >> 5;
+    const int qi = qb * TT_BQ + wave * 32 + col;
+    const float c = a.scale * TT_LOG2E;
+
+    bf16x8 qa[8];
+    if (qi < a.n_q) {
+        const bf16* qp = (const bf16*)a.q + qi * a.q_st + h * a.q_sh + 8 * half;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) qa[t] = *(const bf16x8*)(qp + 16 * t);
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) qa[t] = zero8();
+    }
+
+    f32x16 o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = (f32x16){};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    const int cnt = a.row_cnt[qb];
+    const int* list = a.row_list + (size_t)qb * a.n_kt;
+    KvTileStager stg;
+    Bounds nb;
+    if (cnt > 0) {
+        stg.begin(a, list[0] >> 1, g);
+        fetch_bounds(a, list[0] >> 1, nb);
+    }
+    for (int it = 0; it < cnt; ++it) {
+        FwdStage& S = st[it & 1];
+        const bool full = list[it] & 1;
+        stg.commit(a, g, S.K, S.V);
+        store_bounds(nb, S.lo, S.hi);
+        __syncthreads();
+        if (it + 1 < cnt) {
+            const int kt1 = list[it + 1] >> 1;
+            stg.begin(a, kt1, g);
+            fetch_bounds(a, kt1, nb);
+        }
+
+        f32x16 s[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            s[b] = (f32x16){};
+#pragma unroll
+            for (int t = 0; t < 8; ++t) s[b] = mfma32(read_row_operand(S.K, 32 * b + col, 16 * t + 8 * half), qa[t], s[b]);
+        }
+        if (!full) mask_scores(s, S.lo, S.hi, qi, half);
+
+        // Tile row max (both lane halves hold the same query after the exchange).
+        float mx0 = -INFINITY, mx1 = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+            mx0 = fmaxf(mx0, fmaxf(s[0][r], s[0][r + 1]));
+            mx1 = fmaxf(mx1, fmaxf(s[1][r], s[1][r + 1]));
+        }
+        const float mx = halves_max(fmaxf(mx0, mx1));
+        // Lazy rescaling: the running max moves only when the tile's max exceeds
+        // it by more than TT_RESCALE_LOG2; otherwise probabilities are taken
+        // against the stale max, so they stay below 2^TT_RESCALE_LOG2.
+        const float mxc = mx * c;
+        const bool grow = mxc > m_run + TT_RESCALE_LOG2;
+        if (__ballot(grow)) {
+            const float alpha = grow ? fast_exp2(m_run - mxc) : 1.0f;
+            m_run = grow ? mxc : m_run;
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) o[db] *= alpha;
+        }
+        const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
+
+        // P^T (bf16) feeds O^T += V^T P^T; the row sum is taken from the same
+        // rounded values.
+        float ps0 = 0.0f, ps1 = 0.0f;
+#pragma unroll
+        for (int stp = 0; stp < 4; ++stp) {
+            const f32x16& sb = s[stp >> 1];
+            const int r0 = 8 * (stp & 1);
+            float p[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) p[e] = fast_exp2(fmaf(sb[r0 + e], c, -m_use));
+            const bf16x8 pk = pack8(p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]);
+            ps0 = sum4_bf16(pk, 0, ps0);
+            ps1 = sum4_bf16(pk, 4, ps1);
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+                o[db] = mfma32(read_tr_operand(S.V, 16 * stp, 32 * db, lane), pk, o[db]);
+        }
+        l_run += ps0 + ps1;
+    }
+
+    const float l_tot = halves_sum(l_run);
+    if (qi < a.n_q) {
+        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        bf16* op = out + ((size_t)qi * a.hq + h) * D;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int grp = 0; grp < 4; ++grp) {
+                bf16x4 w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[e] = (bf16)(o[db][4 * grp + e] * inv);
+                *(bf16x4*)(op + 32 * db + 8 * grp + 4 * half) = w;
+            }
+        if (half == 0) {
+            const float m_fin = (m_run == -INFINITY) ? 0.0f : m_run;
+            lse[(size_t)h * a.n_q + qi] = l_tot > 0.0f ? (m_fin + __log2f(l_tot)) * TT_LN2 : -INFINITY;
+        }
+    }
+}
+
+}  // namespace
+
+int tt_fwd_bf16_launch(const AttnDev& a, void* o, float* lse, hipStream_t s) {
+    hipLaunchKernelGGL(fwd_bf16_kernel, dim3(a.n_qb * a.hq), dim3(256), 0, s, a, (bf16*)o, lse);
+    return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
+}

@@ -1,0 +1,245 @@
+// Device code shared by the bf16 tree-attention kernels (forward in
+// tt_attn_fwd_bf16.hip, backward in tt_attn_bwd_bf16.hip): LDS tile layout,
+// MFMA operand reads, global -> register -> LDS staging, visibility masks and
+// the workgroup -> tile mapping.
+//
+// Tree-masked GQA flash attention for gfx950, bf16 in / fp32 accumulate.
+//
+// Forward and dQ pass (query-major): a workgroup owns TT_BQ = 128 queries of
+// one q head; each of its four waves keeps 32 queries in registers and walks
+// the non-empty key tiles of the plan. Scores are computed transposed,
+// S^T = K Q^T with v_mfma_f32_32x32x16_bf16, so a lane owns one query column:
+// the online-softmax row max needs a single cross-half exchange and the
+// probabilities feed O^T = V^T P^T straight from the accumulators. K and V
+// tiles sit in LDS in their natural [key][d] layout; the V^T (and, for dQ,
+// K^T) operands come out of them through gfx950's transposing LDS read
+// (ds_read_b64_tr_b16). Tiles are software-pipelined: the next tile's
+// global loads are in flight (in registers) while the current tile computes
+// out of the other LDS stage; one barrier per tile.
+//
+// dK/dV pass (key-major): a workgroup owns TT_BKB = 128 keys of one kv head;
+// each wave keeps K and V of 32 keys as MFMA operands and dK, dV of those
+// keys in fp32 accumulators, and walks a range of queries that can see them
+// (for a DFS-packed tree the range is contiguous: [first key, subtree end))
+// for the Hq/Hkv q heads of the group, with Q and dO blocks staged in LDS
+// (double-buffered) and read both row-wise and transposed. Ranges longer than
+// TT_QCH queries are split
+// into several work items; a persistent grid walks the items widest-first.
+// Unsplit tiles write dK/dV directly; split tiles add fp32 partial sums into a
+// workspace that a finalize pass converts.
+//
+// Visibility: key j is seen by query i iff key_lo[j] <= i < key_hi[j]; the
+// plan marks each (query block, key tile) empty (skipped), full (no mask) or
+// partial (interval test per element).
+#pragma once
+
+#include "tt_common.h"
+#include "tt_internal.h"
+
+namespace {
+
+typedef __bf16 bf16;
+
+constexpr int D = 128;
+
+// LDS tiles hold tokens in their natural [token][d] order, rows padded to 288
+// bytes. Each thread loads its slice of the next tile into registers while
+// the current one computes, then stores it. The padding puts consecutive rows
+// 8 banks apart, so 16-byte row reads, transposed reads and the stores all run
+// in at most two LDS passes.
+constexpr int ROW = D + 16;
+__device__ __forceinline__ int tile_off(int r, int d) { return r * ROW + d; }
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// acc + v[i0] + v[i0+1] + v[i0+2] + v[i0+3] (fp32 accumulation, v_dot2c_f32_bf16).
+__device__ __forceinline__ float sum4_bf16(const bf16x8& v, int i0, float acc) {
+    const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
+    acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{v[i0], v[i0 + 1]}, one, acc, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(bf16x2{v[i0 + 2], v[i0 + 3]}, one, acc, false);
+}
+
+// Forward online softmax: the running row max is moved only when a tile's max
+// exceeds it by more than this many log2 units.
+#define TT_RESCALE_LOG2 8.0f
+
+template <int I>
+struct IntC {
+    static constexpr int value = I;
+};
+
+__device__ __forceinline__ bf16x8 zero8() {
+    bf16x8 z;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) z[i] = (bf16)0.0f;
+    return z;
+}
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) const void glb_void;
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
+// (i & 3) of the 8-byte chunks read by lanes 4k + (i >> 2), k = 0..3.
+__device__ __forceinline__ bf16x4 ds_read_tr(const bf16* p) {
+    const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p));
+    return __builtin_bit_cast(bf16x4, r);
+}
+
+// MFMA operand "column = head dim, k = 16 tokens" from a tile X: lane l gets
+// X[r0 + kappa(e)][dbase + (l & 31)], kappa(e) = 8*(e/4) + 4*(l>>5) + (e%4) —
+// the accumulator row order, so it pairs with probabilities taken straight
+// from a score accumulator.
+__device__ __forceinline__ bf16x8 read_tr_operand(const bf16* X, int r0, int dbase, int lane) {
+    const int j = lane & 15, grp = lane >> 4;
+    const int d = dbase + 16 * (grp & 1) + 4 * (j & 3);
+    const int r = r0 + 4 * (grp >> 1) + (j >> 2);
+    return cat44(ds_read_tr(X + tile_off(r, d)), ds_read_tr(X + tile_off(r + 8, d)));
+}
+
+// MFMA operand "row = token, k = 16 head dims": X[r][d0 .. d0+7], d0 % 8 == 0.
+__device__ __forceinline__ bf16x8 read_row_operand(const bf16* X, int r, int d0) {
+    return *(const bf16x8*)(X + tile_off(r, d0));
+}
+
+
+// Register staging: thread t holds rows (t/16) + 16*i (i < NROWS/16) at head
+// dims 8*(t%16) .. +7 of a tile; 16 lanes cover one 256-byte row, and a wave
+// instruction moves four whole rows.
+template <int NROWS>
+struct RowRegs {
+    bf16x8 x[NROWS / 16];
+};
+
+template <int NROWS, typename RowPtr>
+__device__ __forceinline__ void fetch_rows(RowRegs<NROWS>& r, int tid, RowPtr row_ptr) {
+    const int dc = (tid & 15) * 8, r0 = tid >> 4;
+#pragma unroll
+    for (int i = 0; i < NROWS / 16; ++i) r.x[i] = *(const bf16x8*)(row_ptr(r0 + 16 * i) + dc);
+}
+
+// Same, for NROWS rows of one tensor that all exist: row 0 at `base` (a
+// uniform pointer), rows `stb` bytes apart. The loads go through a buffer
+// resource: base and row steps in scalar registers, one 32-bit lane offset.
+template <int NROWS>
+__device__ __forceinline__ void fetch_rows_buf(RowRegs<NROWS>& r, int tid, const void* base, uint32_t stb) {
+    const uint32_t bytes = (NROWS - 1) * stb + 2 * D;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+    const uint32_t vo = (tid >> 4) * stb + 16 * (tid & 15);
+#pragma unroll
+    for (int i = 0; i < NROWS / 16; ++i)
+        r.x[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vo, (int)(16 * i * stb), 0));
+}
+
+template <int NROWS>
+__device__ __forceinline__ void store_rows(const RowRegs<NROWS>& r, int tid, bf16* X) {
+    const int dc = (tid & 15) * 8, r0 = tid >> 4;
+#pragma unroll
+    for (int i = 0; i < NROWS / 16; ++i) *(bf16x8*)(X + tile_off(r0 + 16 * i, dc)) = r.x[i];
+}
+
+__device__ __forceinline__ const bf16* key_row(const AttnDev& a, int kk, int g, bool isv) {
+    if (kk < a.n_past) {
+        return isv ? (const bf16*)a.vp + kk * a.vp_st + g * a.vp_sh
+                   : (const bf16*)a.kp + kk * a.kp_st + g * a.kp_sh;
+    }
+    const int64_t t = kk - a.n_past;
+    return isv ? (const bf16*)a.v + t * a.v_st + g * a.v_sh : (const bf16*)a.k + t * a.k_st + g * a.k_sh;
+}
+
+struct Bounds {
+    int lo, hi;
+};
+
+__device__ __forceinline__ void fetch_bounds(const AttnDev& a, int kt, Bounds& r) {
+    const int t = threadIdx.x;
+    if (t < TT_BK) {
+        const int kk = kt * TT_BK + t;
+        r.lo = kk < a.n_keys ? a.key_lo[kk] : 0;
+        r.hi = kk < a.n_keys ? a.key_hi[kk] : 0;
+    }
+}
+
+// Staging of the K and V rows of key tile kt (rows past the last key alias
+// it; their empty bounds mask them). begin() starts the loads for a
+// stage; commit() makes them resident in that stage (before the barrier).
+struct KvTileStager {
+    RowRegs<TT_BK> k, v;
+    int k0;
+    bool direct;   // straddles gateway and own keys, or runs past the last key: loaded in commit()
+    __device__ __forceinline__ void begin(const AttnDev& a, int kt, int g) {
+        k0 = kt * TT_BK;
+        direct = false;
+        if (k0 + TT_BK <= a.n_past) {            // all gateway keys (uniform branch)
+            fetch_rows_buf(k, threadIdx.x, (const bf16*)a.kp + k0 * a.kp_st + g * a.kp_sh, 2 * a.kp_st);
+            fetch_rows_buf(v, threadIdx.x, (const bf16*)a.vp + k0 * a.vp_st + g * a.vp_sh, 2 * a.vp_st);
+        } else if (k0 >= a.n_past && k0 + TT_BK <= a.n_keys) {   // all own keys
+            const int64_t t0 = k0 - a.n_past;
+            fetch_rows_buf(k, threadIdx.x, (const bf16*)a.k + t0 * a.k_st + g * a.k_sh, 2 * a.k_st);
+            fetch_rows_buf(v, threadIdx.x, (const bf16*)a.v + t0 * a.v_st + g * a.v_sh, 2 * a.v_st);
+        } else {
+            direct = true;
+        }
+    }
+    __device__ __forceinline__ void commit(const AttnDev& a, int g, bf16* K, bf16* V) {
+        if (!direct) {
+            store_rows(k, threadIdx.x, K);
+            store_rows(v, threadIdx.x, V);
+            return;
+        }
+        // At most two tiles per launch take this path: copied row by row,
+        // without prefetch (short register live ranges).
+        const int dc = (threadIdx.x & 15) * 8, r0 = threadIdx.x >> 4;
+        for (int i = 0; i < TT_BK / 16; ++i) {
+            const int r = r0 + 16 * i, kk = min(k0 + r, a.n_keys - 1);
+            *(bf16x8*)(K + tile_off(r, dc)) = *(const bf16x8*)(key_row(a, kk, g, false) + dc);
+            *(bf16x8*)(V + tile_off(r, dc)) = *(const bf16x8*)(key_row(a, kk, g, true) + dc);
+        }
+    }
+};
+
+__device__ __forceinline__ void store_bounds(const Bounds& r, int* s_lo, int* s_hi) {
+    const int t = threadIdx.x;
+    if (t < TT_BK) {
+        s_lo[t] = r.lo;
+        s_hi[t] = r.hi;
+    }
+}
+
+// Lane's 32 query-column scores -> -inf where the key is invisible.
+__device__ __forceinline__ void mask_scores(f32x16 (&s)[2], const int* s_lo, const int* s_hi, int qi, int half) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+        for (int grp = 0; grp < 4; ++grp) {
+            const int k0 = 32 * b + 8 * grp + 4 * half;
+            const i32x4 lo = *(const i32x4*)(s_lo + k0);
+            const i32x4 hi = *(const i32x4*)(s_hi + k0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const bool vis = lo[e] <= qi && qi < hi[e];
+                s[b][4 * grp + e] = vis ? s[b][4 * grp + e] : -INFINITY;
+            }
+        }
+    }
+}
+
+// blockIdx.x -> (query block, q head). Workgroups are dispatched round-robin
+// over the 8 XCDs; each XCD gets the q heads of whole kv-head groups so their
+// K/V stay in its L2, and the heaviest query blocks go first.
+__device__ __forceinline__ void decode_qblock(const AttnDev& a, int& qb, int& h) {
+    const int bid = blockIdx.x;
+    if ((a.hq & 7) == 0) {
+        const int hpx = a.hq >> 3, xcd = bid & 7, slot = bid >> 3;
+        h = xcd * hpx + slot % hpx;
+        qb = a.row_order[slot / hpx];
+    } else {
+        h = bid % a.hq;
+        qb = a.row_order[bid / a.hq];
+    }
+}
+
+
+}  // namespace

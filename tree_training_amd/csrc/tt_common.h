@@ -118,6 +118,18 @@ __device__ __forceinline__ int wave_max_i(int x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Max / sum of x over lanes l and l ^ 32 (the two halves of a wave), with
+// gfx950's v_permlane32_swap: of the returned pair, one element is the lane's
+// own x and the other its partner's, in either order.
+__device__ __forceinline__ float halves_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Pack 8 floats (round-to-nearest-even) into a bf16x8 MFMA operand.
 __device__ __forceinline__ bf16x8 pack8(float a0, float a1, float a2, float a3, float a4, float a5,
                                         float a6, float a7) {
