@@ -30,6 +30,26 @@ import time
 HQ, HKV, D = 32, 8, 128
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "tree_attn_agent16k_hbm_traffic.md")
+
+
+def profiled_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel`, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (copy-calibrated), for the agent16k
+    workload it was measured on; None otherwise."""
+    if workload != "agent16k":
+        return None
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            lines = f.read().splitlines()
+    except OSError:
+        return None
+    for ln in lines:
+        cells = [c.strip() for c in ln.strip().strip("|").split("|")]
+        if len(cells) >= 4 and cells[0] == kernel and cells[3].isdigit():
+            return int(cells[3])
+    return None
 
 
 def parse():
@@ -195,8 +215,11 @@ def main():
         dom = max((n for n in names if kernels[n]["useful_tflops"]), key=lambda n: kernels[n]["ms"])
         ach = kernels[dom]["useful_tflops"]
         roofline = {"bound": "mfma", "kernel": dom, "achieved": ach, "peak": PEAK_BF16_TFLOPS,
-                    "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                    "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4),
+                    "traffic": profiled_traffic(dom, args.workload),
                     "flops_per_launch": useful[names.index(dom)]}
+        if dom == "bwd_dkdv_bf16_kernel":
+            roofline["timed"] = "dK/dV pass: split-sum zero + bwd_dkdv_bf16_kernel + split-sum finalize"
 
     cpu = None
     if not args.no_cpu_baseline:

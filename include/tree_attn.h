@@ -133,9 +133,13 @@ int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* stream);
 /* Backward for upstream gradient d_o (n_q x Hq, strides given). Writes
  * dq [n_q,Hq,D], dk/dv [n_q,Hkv,D] (contiguous, problem dtype, overwritten).
  * Gateway gradients are ADDED in float32 to dk_past_acc/dv_past_acc
- * [n_past, Hkv, D] contiguous (the fp32 hook accumulation of
+ * [n_past, Hkv, D] contiguous, 16-byte aligned (the fp32 hook accumulation of
  * tree_grad_hybrid.py:220-225, kept on the device); pass NULL to drop them.
- * Deterministic: no atomics, every output element has one writer. */
+ * ws must be 16-byte aligned. float32 problems are deterministic (one writer
+ * per output element). bf16 problems are too, except that keys whose visible
+ * query range spans more than 2048 queries (split into several work items)
+ * sum their dK/dV partials with fp32 atomics, so their rounding can vary
+ * from run to run. */
 size_t tt_attn_bwd_workspace_bytes(const tt_attn_problem* p);
 int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_tensor d_o,
                 void* dq, void* dk, void* dv, float* dk_past_acc, float* dv_past_acc,

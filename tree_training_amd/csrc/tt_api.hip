@@ -169,7 +169,7 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
         return TT_E_ARG;
     if (p->dtype == TT_DTYPE_BF16 && d_o.stride_tok >= kMaxTokStride) return TT_E_ARG;
     if (!aligned(d_o.ptr, ealign) || !aligned(o, ealign) || !aligned(dq, ealign) || !aligned(dk, ealign) ||
-        !aligned(dv, ealign) || !aligned(ws, 4))
+        !aligned(dv, ealign) || !aligned(ws, 16) || !aligned(dk_past_acc, 16) || !aligned(dv_past_acc, 16))
         return TT_E_ARG;
     BwdDev b;
     b.o = o;

@@ -348,16 +348,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
     }
 }
 
-// Split key tiles: zero their fp32 sums before the dK/dV pass ...
+// Split key tiles: zero their fp32 sums before the dK/dV pass ... (16-byte
+// vectors: the workspace and the gateway accumulators are 16-byte aligned and
+// rows are 128 floats)
 __global__ __launch_bounds__(256) void bwd_split_zero_kernel(AttnDev a, BwdDev bw) {
     const int kb = blockIdx.x, g = blockIdx.y;
     if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb]) <= 1) return;
-    for (int e = threadIdx.x; e < TT_BKB * D; e += 256) {
-        const int key = kb * TT_BKB + e / D;
-        if (key >= a.n_keys) break;
-        const size_t idx = ((size_t)key * a.hkv + g) * D + (e % D);
-        bw.dk_ws[idx] = 0.0f;
-        bw.dv_ws[idx] = 0.0f;
+    const int nk = min(TT_BKB, a.n_keys - kb * TT_BKB);
+    for (int e = threadIdx.x; e < nk * (D / 4); e += 256) {
+        const int key = kb * TT_BKB + e / (D / 4);
+        const size_t idx = ((size_t)key * a.hkv + g) * D + 4 * (e % (D / 4));
+        *(f32x4*)(bw.dk_ws + idx) = (f32x4){};
+        *(f32x4*)(bw.dv_ws + idx) = (f32x4){};
     }
 }
 
@@ -365,21 +367,26 @@ __global__ __launch_bounds__(256) void bwd_split_zero_kernel(AttnDev a, BwdDev b
 __global__ __launch_bounds__(256) void bwd_split_finalize_kernel(AttnDev a, BwdDev bw) {
     const int kb = blockIdx.x, g = blockIdx.y;
     if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb]) <= 1) return;
-    for (int e = threadIdx.x; e < TT_BKB * D; e += 256) {
-        const int key = kb * TT_BKB + e / D;
-        if (key >= a.n_keys) break;
-        const int d = e % D;
+    const int nk = min(TT_BKB, a.n_keys - kb * TT_BKB);
+    for (int e = threadIdx.x; e < nk * (D / 4); e += 256) {
+        const int key = kb * TT_BKB + e / (D / 4), d = 4 * (e % (D / 4));
         const size_t widx = ((size_t)key * a.hkv + g) * D + d;
-        const float gk = bw.dk_ws[widx], gv = bw.dv_ws[widx];
+        const f32x4 gk = *(const f32x4*)(bw.dk_ws + widx), gv = *(const f32x4*)(bw.dv_ws + widx);
         if (key < a.n_past) {
             if (bw.dk_acc) {
-                bw.dk_acc[widx] += gk;
-                bw.dv_acc[widx] += gv;
+                *(f32x4*)(bw.dk_acc + widx) += gk;
+                *(f32x4*)(bw.dv_acc + widx) += gv;
             }
         } else {
             const size_t idx = ((size_t)(key - a.n_past) * a.hkv + g) * D + d;
-            ((bf16*)bw.dk)[idx] = (bf16)gk;
-            ((bf16*)bw.dv)[idx] = (bf16)gv;
+            bf16x4 wk, wv;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                wk[i] = (bf16)gk[i];
+                wv[i] = (bf16)gv[i];
+            }
+            *(bf16x4*)((bf16*)bw.dk + idx) = wk;
+            *(bf16x4*)((bf16*)bw.dv + idx) = wv;
         }
     }
 }
