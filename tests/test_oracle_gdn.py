@@ -1,0 +1,149 @@
+"""Pins for the tree gated-delta-rule oracle (oracle/gdn.py), CPU only.
+
+Each oracle function is checked against something its own formula does not
+contain: transformers' recurrent and chunked gated-delta-rule routines
+(library), torch's conv1d (library), per-path equivalence of the tree outputs,
+chunk-size independence, and the R^3 identity that separates the reference's
+truncated correction from the exact one.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import gdn
+from tree_training_amd.workloads import random_forest
+
+hf = pytest.importorskip("transformers.models.qwen3_5_moe.modeling_qwen3_5_moe")
+
+
+def _inputs(T, Hk, Hv, Dk, Dv, seed, g_scale=0.3):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((T, Hk, Dk))
+    k = rng.standard_normal((T, Hk, Dk))
+    v = rng.standard_normal((T, Hv, Dv))
+    g = -np.abs(rng.standard_normal((T, Hv))) * g_scale
+    beta = 1.0 / (1.0 + np.exp(-rng.standard_normal((T, Hv))))
+    return q, k, v, g, beta
+
+
+def _paths(parent):
+    """Root-to-leaf node paths of a DFS-ordered forest."""
+    children = {i: [] for i in range(len(parent))}
+    for i, p in enumerate(parent):
+        if p >= 0:
+            children[p].append(i)
+    out = []
+    for i in range(len(parent)):
+        if not children[i]:
+            path, j = [], i
+            while j >= 0:
+                path.append(j)
+                j = parent[j]
+            out.append(path[::-1])
+    return out
+
+
+def _hf_recurrent(q, k, v, g, beta):
+    """transformers' recurrence on one sequence [L, H, D] (float64 in, fp32 inside)."""
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x))[None]
+    o, _ = hf.torch_recurrent_gated_delta_rule(t(q), t(k), t(v), t(g), t(beta), None, False,
+                                               use_qk_l2norm_in_kernel=True)
+    return o[0].numpy()
+
+
+def _rel(a, b):
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def test_recurrent_matches_transformers():
+    q, k, v, g, beta = _inputs(37, 2, 2, 16, 12, 0)
+    o_hf = _hf_recurrent(q, k, v, g, beta)
+    o, _ = gdn.gdn_tree(q, k, v, g, beta, [37], [-1], mode="exact")
+    assert _rel(o, o_hf) < 1e-5
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_tree_exact_is_per_path(seed):
+    lens, par = random_forest(seed, node_len=(1, 12))
+    T = sum(lens)
+    q, k, v, g, beta = _inputs(T, 2, 4, 16, 8, seed)
+    o, _ = gdn.gdn_tree(q, k, v, g, beta, lens, par, mode="exact")
+    starts = gdn.node_starts(lens)
+    for path in _paths(par):
+        idx = np.concatenate([np.arange(starts[i], starts[i] + lens[i]) for i in path])
+        # the reference's repeat_interleave of q/k heads
+        rq, rk = np.repeat(q[idx], 2, axis=1), np.repeat(k[idx], 2, axis=1)
+        o_path = _hf_recurrent(rq, rk, v[idx], g[idx], beta[idx])
+        assert _rel(o[idx], o_path) < 1e-5
+
+
+@pytest.mark.parametrize("chunk", [1, 4, 7, 64])
+def test_chunked_equals_exact(chunk):
+    lens, par = random_forest(11, node_len=(1, 30))
+    T = sum(lens)
+    q, k, v, g, beta = _inputs(T, 1, 2, 16, 8, 5)
+    o_e, s_e = gdn.gdn_tree(q, k, v, g, beta, lens, par, mode="exact")
+    o_c, s_c = gdn.gdn_tree(q, k, v, g, beta, lens, par, mode="chunked", chunk=chunk)
+    assert _rel(o_c, o_e) < 1e-10
+    assert _rel(s_c, s_e) < 1e-10
+
+
+def test_transformers_chunked_matches_exact():
+    q, k, v, g, beta = _inputs(150, 2, 2, 32, 16, 7)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x))[None]
+    o_hf, _ = hf.torch_chunk_gated_delta_rule(t(q), t(k), t(v), t(g), t(beta), chunk_size=64,
+                                              use_qk_l2norm_in_kernel=True)
+    o, _ = gdn.gdn_tree(q, k, v, g, beta, [150], [-1], mode="exact")
+    assert _rel(o, o_hf[0].numpy()) < 1e-5
+
+
+def test_reference_equals_exact_for_nodes_up_to_three_tokens():
+    lens, par = random_forest(4, node_len=(1, 3))
+    T = sum(lens)
+    q, k, v, g, beta = _inputs(T, 2, 2, 16, 8, 9)
+    o_r, _ = gdn.gdn_tree(q, k, v, g, beta, lens, par, mode="reference")
+    o_e, _ = gdn.gdn_tree(q, k, v, g, beta, lens, par, mode="exact")
+    assert _rel(o_r, o_e) < 1e-10
+
+
+def test_reference_deviation_is_the_r_cubed_term():
+    rng = np.random.default_rng(3)
+    for L in (4, 9, 33):
+        N = np.tril(rng.standard_normal((L, L)) * 0.3, -1)
+        ex, tr = gdn.exact_correction(N), gdn.truncated_correction(N)
+        assert np.abs((ex - tr) - np.linalg.matrix_power(N, 3) @ ex).max() < 1e-10
+    # and on real inputs the modes differ once a node has more than 3 tokens
+    q, k, v, g, beta = _inputs(40, 1, 1, 16, 8, 2, g_scale=0.05)
+    o_r, _ = gdn.gdn_tree(q, k, v, g, beta, [40], [-1], mode="reference")
+    o_e, _ = gdn.gdn_tree(q, k, v, g, beta, [40], [-1], mode="exact")
+    assert _rel(o_r, o_e) > 1e-6
+
+
+@pytest.mark.parametrize("seed", [0, 6])
+def test_tree_conv_is_per_path_causal_conv(seed):
+    lens, par = random_forest(seed, node_len=(1, 9))
+    T, C, K = sum(lens), 6, 4
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((T, C))
+    w = rng.standard_normal((C, K))
+    b = rng.standard_normal(C)
+    out = gdn.tree_conv(x, w, b, lens, par)
+    starts = gdn.node_starts(lens)
+    for path in _paths(par):
+        idx = np.concatenate([np.arange(starts[i], starts[i] + lens[i]) for i in path])
+        xp = torch.from_numpy(x[idx].T.copy())[None]
+        y = F.conv1d(xp, torch.from_numpy(w)[:, None, :], torch.from_numpy(b), padding=K - 1, groups=C)
+        y = F.silu(y[..., :len(idx)])[0].T.numpy()
+        assert np.abs(out[idx] - y).max() < 1e-12
+
+
+def test_gates_match_torch():
+    rng = np.random.default_rng(0)
+    a, b = rng.standard_normal((9, 4)), rng.standard_normal((9, 4))
+    A_log, dt = np.log(rng.uniform(0.5, 16, 4)), np.ones(4)
+    g, beta = gdn.gdn_gates(a, b, A_log, dt)
+    ta = torch.from_numpy(a)
+    g_t = -torch.from_numpy(A_log).exp() * F.softplus(ta + torch.from_numpy(dt))
+    assert np.abs(g - g_t.numpy()).max() < 1e-12
+    assert np.abs(beta - torch.from_numpy(b).sigmoid().numpy()).max() < 1e-12
