@@ -145,6 +145,49 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
                 void* dq, void* dk, void* dv, float* dk_past_acc, float* dv_past_acc,
                 void* ws, size_t ws_bytes, void* stream);
 
+/* ---- tree gated delta rule (linear-attention layers) ----------------------
+ * Replaces torch_chunk_gated_delta_rule_tree_varlen (tree_dfs_ssm.py:38-156;
+ * twin dfs_tree_forward.py:253-353) as called from the patched GDN layer
+ * (tree_dfs_ssm.py:399-414): q/k/v of the packed tree, per-node parent-state
+ * routing (chunk_parent_map, :131-132). Semantics: the exact gated delta rule
+ * along every root-to-leaf path (the function's stated contract, :49-52),
+ * evaluated in 32-token chunks; the reference's own evaluation truncates the
+ * within-node correction to I + R + R^2 (:114-121) and differs for nodes of
+ * more than 3 tokens.
+ *
+ * Nodes are in DFS pre-order (parent[i] < i, -1 for a root); node i owns
+ * tokens [node_start[i], node_start[i] + node_len[i]). level_nodes lists
+ * every node once, grouped by depth (roots first); level_offsets (HOST
+ * memory, n_levels + 1 entries, level_offsets[n_levels] = n_nodes) delimits
+ * the groups. A node whose parent is not in an earlier group reads an
+ * undefined state. */
+typedef struct tt_gdn_problem {
+    int32_t dtype;          /* TT_DTYPE_BF16 or TT_DTYPE_F32 for q, k, v and o */
+    int32_t n_tokens;
+    int32_t n_nodes;
+    int32_t n_heads_k;      /* q/k heads */
+    int32_t n_heads_v;      /* v heads, a multiple of n_heads_k; v head h reads q/k head h / (Hv/Hk) */
+    int32_t head_dim;       /* 128 (key and value) */
+    int32_t l2norm;         /* 1: q and k are l2-normalised (eps 1e-6) before use */
+    float scale;            /* q multiplier after normalisation, usually head_dim^-1/2 */
+    tt_tensor q, k, v;      /* [T, H, 128], 16-byte aligned rows */
+    const float* g;         /* [T, Hv] log decay (<= 0), element [t][h] at g + t*g_stride_tok + h */
+    int64_t g_stride_tok;
+    const float* beta;      /* [T, Hv] write strength */
+    int64_t beta_stride_tok;
+    const int32_t* node_start;   /* device, [n_nodes] */
+    const int32_t* node_len;     /* device, [n_nodes] */
+    const int32_t* node_parent;  /* device, [n_nodes] */
+    const int32_t* level_nodes;  /* device, [n_nodes] */
+    const int32_t* level_offsets;/* HOST, [n_levels + 1] */
+    int32_t n_levels;
+} tt_gdn_problem;
+
+/* o: [T, Hv, 128] contiguous, problem dtype. node_states: [n_nodes, Hv, 128,
+ * 128] float32, the state after each node (its children's initial state;
+ * kept for the backward). One launch per tree level. */
+int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* stream);
+
 /* ---- device self-test ----------------------------------------------------
  * No counterpart in the reference. Runs one v_mfma_f32_32x32x16_bf16 with the
  * operand and accumulator lane layout the bf16 kernels assume:

@@ -97,3 +97,44 @@ def test_meta_and_plan_validation():
     assert lib.tt_plan_bytes(0, 5) == 0
     assert lib.tt_meta_workspace_bytes(0) == 0
     assert lib.tt_meta_dense_mask(V, V, 4, 70000, V, None) == _lib.TT_E_UNSUPPORTED
+
+
+def _gdn_problem(offsets=(0, 1, 3), **kw):
+    arr = (ctypes.c_int32 * len(offsets))(*offsets)
+    p = _lib.TTGdnProblem(dtype=_lib.TT_DTYPE_BF16, n_tokens=100, n_nodes=3, n_heads_k=16, n_heads_v=32,
+                          head_dim=128, l2norm=1, scale=128 ** -0.5,
+                          q=_lib.TTTensor(16, 16 * 128, 128), k=_lib.TTTensor(16, 16 * 128, 128),
+                          v=_lib.TTTensor(16, 32 * 128, 128), g=16, g_stride_tok=32, beta=16,
+                          beta_stride_tok=32, node_start=16, node_len=16, node_parent=16, level_nodes=16,
+                          level_offsets=arr, n_levels=len(offsets) - 1)
+    p._keep = arr
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("head_dim", 64, _lib.TT_E_UNSUPPORTED),
+    ("dtype", 7, _lib.TT_E_UNSUPPORTED),
+    ("n_heads_v", 24, _lib.TT_E_UNSUPPORTED),     # not a multiple of n_heads_k
+    ("n_tokens", 0, _lib.TT_E_ARG),
+    ("n_nodes", 101, _lib.TT_E_ARG),             # more nodes than tokens
+    ("scale", float("nan"), _lib.TT_E_ARG),
+    ("g_stride_tok", 8, _lib.TT_E_ARG),           # rows of g overlap
+    ("node_parent", None, _lib.TT_E_ARG),
+    ("q", _lib.TTTensor(18, 16 * 128, 128), _lib.TT_E_ARG),   # misaligned
+])
+def test_gdn_validation(field, value, code):
+    lib = _lib.lib()
+    p = _gdn_problem(**{field: value})
+    assert lib.tt_gdn_tree_fwd(ctypes.byref(p), ctypes.c_void_p(16), ctypes.c_void_p(16), None) == code
+
+
+def test_gdn_level_offsets_validation():
+    lib = _lib.lib()
+    V = ctypes.c_void_p(16)
+    for offs in ((0, 2), (1, 3), (0, 2, 1, 3)):        # wrong total, wrong start, not monotone
+        p = _gdn_problem(offsets=offs)
+        assert lib.tt_gdn_tree_fwd(ctypes.byref(p), V, V, None) == _lib.TT_E_ARG
+    p = _gdn_problem()
+    assert lib.tt_gdn_tree_fwd(ctypes.byref(p), None, V, None) == _lib.TT_E_ARG

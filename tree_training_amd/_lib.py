@@ -34,7 +34,7 @@ ABI_VERSION = 1
 EXPORTS = (
     "tt_abi_version", "tt_strerror", "tt_meta_workspace_bytes", "tt_meta_build", "tt_keys_build",
     "tt_meta_dense_mask", "tt_plan_bytes", "tt_plan_build", "tt_attn_fwd",
-    "tt_attn_bwd_workspace_bytes", "tt_attn_bwd", "tt_selftest_mfma32",
+    "tt_attn_bwd_workspace_bytes", "tt_attn_bwd", "tt_gdn_tree_fwd", "tt_selftest_mfma32",
 )
 
 
@@ -50,6 +50,20 @@ class TTAttnProblem(ctypes.Structure):
         ("q", TTTensor), ("k", TTTensor), ("v", TTTensor), ("k_past", TTTensor), ("v_past", TTTensor),
         ("key_lo", ctypes.c_void_p), ("key_hi", ctypes.c_void_p), ("plan", ctypes.c_void_p),
         ("plan_bytes", ctypes.c_size_t),
+    ]
+
+
+class TTGdnProblem(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("n_tokens", ctypes.c_int32), ("n_nodes", ctypes.c_int32),
+        ("n_heads_k", ctypes.c_int32), ("n_heads_v", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("l2norm", ctypes.c_int32), ("scale", ctypes.c_float),
+        ("q", TTTensor), ("k", TTTensor), ("v", TTTensor),
+        ("g", ctypes.c_void_p), ("g_stride_tok", ctypes.c_int64),
+        ("beta", ctypes.c_void_p), ("beta_stride_tok", ctypes.c_int64),
+        ("node_start", ctypes.c_void_p), ("node_len", ctypes.c_void_p), ("node_parent", ctypes.c_void_p),
+        ("level_nodes", ctypes.c_void_p), ("level_offsets", ctypes.POINTER(ctypes.c_int32)),
+        ("n_levels", ctypes.c_int32),
     ]
 
 
@@ -75,6 +89,7 @@ def _declare(lib):
         "tt_attn_bwd_workspace_bytes": (SZ, [ctypes.POINTER(TTAttnProblem)]),
         "tt_attn_bwd": (ctypes.c_int, [ctypes.POINTER(TTAttnProblem), P, P, TTTensor, P, P, P, P, P, P, SZ,
                                        VP]),
+        "tt_gdn_tree_fwd": (ctypes.c_int, [ctypes.POINTER(TTGdnProblem), P, P, VP]),
         "tt_selftest_mfma32": (ctypes.c_int, [P, P, P, VP]),
     }
     for name, (res, args) in sig.items():

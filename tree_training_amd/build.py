@@ -17,7 +17,8 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 LIBDIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIBDIR, "libtree_attn.so")
-SOURCES = ["tt_meta.hip", "tt_attn_fwd_bf16.hip", "tt_attn_bwd_bf16.hip", "tt_attn_f32.hip", "tt_api.hip"]
+SOURCES = ["tt_meta.hip", "tt_attn_fwd_bf16.hip", "tt_attn_bwd_bf16.hip", "tt_attn_f32.hip", "tt_gdn.hip",
+           "tt_api.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17",
@@ -55,7 +56,7 @@ def build(verbose: bool = False, extra=(), out: str = LIB) -> str:
     os.makedirs(objdir, exist_ok=True)
     os.makedirs(os.path.dirname(out), exist_ok=True)
     objs = [os.path.join(objdir, s.replace(".hip", ".o")) for s in SOURCES]
-    with ThreadPoolExecutor(max_workers=min(5, len(SOURCES))) as ex:
+    with ThreadPoolExecutor(max_workers=min(6, len(SOURCES))) as ex:
         logs = list(ex.map(lambda so: _compile(so[0], so[1], list(extra)), zip(SOURCES, objs)))
     if verbose:
         for s, log in zip(SOURCES, logs):

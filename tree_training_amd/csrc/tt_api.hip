@@ -194,6 +194,51 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
     return tt_bwd_f32_launch(a, b, (hipStream_t)stream);
 }
 
+int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* stream) {
+    if (!p || !o || !node_states) return TT_E_ARG;
+    if (p->dtype != TT_DTYPE_BF16 && p->dtype != TT_DTYPE_F32) return TT_E_UNSUPPORTED;
+    if (p->head_dim != 128) return TT_E_UNSUPPORTED;
+    if (p->n_tokens < 1 || p->n_nodes < 1 || p->n_nodes > p->n_tokens || p->n_heads_k < 1 || p->n_heads_v < 1)
+        return TT_E_ARG;
+    if (p->n_heads_v % p->n_heads_k != 0) return TT_E_UNSUPPORTED;
+    if (p->n_heads_v > 65535 || !(p->scale > 0.0f) || !isfinite(p->scale)) return TT_E_ARG;
+    if (!p->q.ptr || !p->k.ptr || !p->v.ptr || !p->g || !p->beta || !p->node_start || !p->node_len ||
+        !p->node_parent || !p->level_nodes || !p->level_offsets || p->n_levels < 1)
+        return TT_E_ARG;
+    const int64_t gran = p->dtype == TT_DTYPE_BF16 ? 8 : 4;
+    const tt_tensor* ts[3] = {&p->q, &p->k, &p->v};
+    for (int i = 0; i < 3; ++i) {
+        const tt_tensor* t = ts[i];
+        if (t->stride_tok < 128 || t->stride_head < 128 || (t->stride_tok % gran) || (t->stride_head % gran) ||
+            !aligned(t->ptr, 16))
+            return TT_E_ARG;
+    }
+    if (p->g_stride_tok < p->n_heads_v || p->beta_stride_tok < p->n_heads_v) return TT_E_ARG;
+    if (!aligned(o, 16) || !aligned(node_states, 16)) return TT_E_ARG;
+    if (p->level_offsets[0] != 0 || p->level_offsets[p->n_levels] != p->n_nodes) return TT_E_ARG;
+    for (int l = 0; l < p->n_levels; ++l)
+        if (p->level_offsets[l + 1] < p->level_offsets[l]) return TT_E_ARG;
+    GdnDev d;
+    d.q = p->q.ptr; d.q_st = p->q.stride_tok; d.q_sh = p->q.stride_head;
+    d.k = p->k.ptr; d.k_st = p->k.stride_tok; d.k_sh = p->k.stride_head;
+    d.v = p->v.ptr; d.v_st = p->v.stride_tok; d.v_sh = p->v.stride_head;
+    d.g = p->g; d.g_st = p->g_stride_tok;
+    d.beta = p->beta; d.b_st = p->beta_stride_tok;
+    d.node_start = p->node_start;
+    d.node_len = p->node_len;
+    d.parent = p->node_parent;
+    d.level_nodes = p->level_nodes;
+    d.dtype = p->dtype;
+    d.n_tokens = p->n_tokens;
+    d.n_nodes = p->n_nodes;
+    d.hk = p->n_heads_k;
+    d.hv = p->n_heads_v;
+    d.rep = p->n_heads_v / p->n_heads_k;
+    d.l2 = p->l2norm ? 1 : 0;
+    d.scale = p->scale;
+    return tt_gdn_fwd_launch(d, p->level_offsets, p->n_levels, o, node_states, (hipStream_t)stream);
+}
+
 int tt_selftest_mfma32(const void* a, const void* b, float* d, void* stream) {
     if (!a || !b || !d || !aligned(a, 2) || !aligned(b, 2) || !aligned(d, 4)) return TT_E_ARG;
     return tt_selftest_mfma_launch(a, b, d, (hipStream_t)stream);

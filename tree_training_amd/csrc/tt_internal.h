@@ -42,6 +42,24 @@ struct BwdDev {
     int parts;                // OR of TT_BWD_* (never 0 here)
 };
 
+// Device-side view of a tt_gdn_problem.
+struct GdnDev {
+    const void* q; int64_t q_st, q_sh;
+    const void* k; int64_t k_st, k_sh;
+    const void* v; int64_t v_st, v_sh;
+    const float* g; int64_t g_st;          // [T, Hv] (token stride, heads contiguous)
+    const float* beta; int64_t b_st;
+    const int32_t* node_start;
+    const int32_t* node_len;
+    const int32_t* parent;
+    const int32_t* level_nodes;            // nodes grouped by tree depth
+    int dtype, n_tokens, n_nodes, hk, hv, rep, l2;
+    float scale;
+};
+
+int tt_gdn_fwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, void* out, float* states,
+                      hipStream_t s);
+
 size_t tt_meta_ws_bytes_impl(int n);
 int tt_meta_build_impl(const int32_t* len, const int32_t* par, int n, int T, int pos_offset, int32_t* start,
                        int32_t* off, int32_t* hend, int32_t* pos, int32_t* node_of, int32_t* horizon,

@@ -1,0 +1,149 @@
+"""Tree gated delta rule (linear-attention layers) on the GPU.
+
+Drop-in for ``torch_chunk_gated_delta_rule_tree_varlen`` (tree_dfs_ssm.py:38-156,
+twin ``_tree_gated_delta_net_varlen`` in dfs_tree_forward.py:253-353): the same
+inputs — q, k ``[B=1, T, Hk, D]``, v ``[1, T, Hv, D]``, g, beta ``[1, T, Hv]``,
+``chunk_boundaries`` (one (start, end) per tree node, DFS order) and
+``chunk_parent_map`` (parent node index, -1 for a root) — computed by one HIP
+scan launch per tree level through ``tt_gdn_tree_fwd``.
+
+Semantics: the exact gated delta rule along every root-to-leaf path (what the
+reference function states it computes, tree_dfs_ssm.py:49-52). The reference's
+own evaluation truncates the within-node correction to I + R + R^2
+(tree_dfs_ssm.py:114-121), which agrees with this for nodes of at most three
+tokens and deviates for longer ones.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+from .meta import _ptr, _stream, require_device
+
+HEAD_DIM = 128
+
+
+class GdnTree:
+    """Node ranges, parents and per-depth node groups of a DFS-packed forest,
+    resident on the device (level offsets stay on the host: one launch per
+    level)."""
+
+    def __init__(self, node_len: Sequence[int], parent: Sequence[int], device):
+        n = len(node_len)
+        if n < 1 or len(parent) != n:
+            raise ValueError("node_len and parent must be non-empty and of equal length")
+        start, s = [], 0
+        depth = []
+        for i, (L, p) in enumerate(zip(node_len, parent)):
+            if L < 1:
+                raise ValueError(f"node {i} is empty")
+            if not (-1 <= p < i):
+                raise ValueError(f"node {i}: parent {p} does not precede it (DFS pre-order expected)")
+            start.append(s)
+            s += int(L)
+            depth.append(0 if p < 0 else depth[p] + 1)
+        self.n_nodes = n
+        self.n_tokens = s
+        self.node_len = [int(x) for x in node_len]
+        self.parent = [int(x) for x in parent]
+        self.node_start = start
+        levels: List[List[int]] = [[] for _ in range(max(depth) + 1)]
+        for i, d in enumerate(depth):
+            levels[d].append(i)
+        order = [i for lv in levels for i in lv]
+        offs = [0]
+        for lv in levels:
+            offs.append(offs[-1] + len(lv))
+        self.n_levels = len(levels)
+        self.level_offsets = (ctypes.c_int32 * len(offs))(*offs)
+        dev = require_device(device)
+        i32 = dict(dtype=torch.int32, device=dev)
+        self.d_start = torch.tensor(start, **i32)
+        self.d_len = torch.tensor(self.node_len, **i32)
+        self.d_parent = torch.tensor(self.parent, **i32)
+        self.d_levels = torch.tensor(order, **i32)
+        self.device = dev
+
+    @classmethod
+    def from_boundaries(cls, chunk_boundaries: Sequence[Tuple[int, int]], chunk_parent_map: Sequence[int],
+                        device) -> "GdnTree":
+        """From the reference's ``chunk_boundaries`` / ``chunk_parent_map``."""
+        s = 0
+        for a, b in chunk_boundaries:
+            if a != s or b <= a:
+                raise ValueError("chunk_boundaries must tile [0, T) in order with non-empty chunks")
+            s = b
+        return cls([b - a for a, b in chunk_boundaries], list(chunk_parent_map), device)
+
+
+def _tok_heads(x: torch.Tensor, name: str) -> torch.Tensor:
+    if x.dim() == 4:
+        if x.shape[0] != 1:
+            raise ValueError(f"{name}: batch size must be 1 (one packed tree)")
+        x = x[0]
+    if x.dim() != 3 or x.shape[-1] != HEAD_DIM:
+        raise ValueError(f"{name}: expected [T, H, {HEAD_DIM}], got {tuple(x.shape)}")
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    return x
+
+
+def _tok_vec(x: torch.Tensor, name: str) -> torch.Tensor:
+    if x.dim() == 3:
+        if x.shape[0] != 1:
+            raise ValueError(f"{name}: batch size must be 1")
+        x = x[0]
+    if x.dim() != 2:
+        raise ValueError(f"{name}: expected [T, H], got {tuple(x.shape)}")
+    x = x.float()
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    return x
+
+
+def gdn_tree_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
+                     tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True):
+    """o [T, Hv, 128] (dtype of v) and node_states [n_nodes, Hv, 128, 128]
+    (float32; the state after each node)."""
+    q, k, v = _tok_heads(q, "q"), _tok_heads(k, "k"), _tok_heads(v, "v")
+    g, beta = _tok_vec(g, "g"), _tok_vec(beta, "beta")
+    T, Hk, _ = q.shape
+    Hv = v.shape[1]
+    if k.shape != q.shape or v.shape[0] != T or g.shape != (T, Hv) or beta.shape != (T, Hv):
+        raise ValueError("q/k/v/g/beta shapes disagree")
+    if T != tree.n_tokens:
+        raise ValueError(f"{T} tokens but the tree holds {tree.n_tokens}")
+    if v.dtype not in (torch.bfloat16, torch.float32) or q.dtype != v.dtype or k.dtype != v.dtype:
+        raise ValueError("q, k, v must share dtype bfloat16 or float32")
+    dev = require_device(q.device)
+    o = torch.empty((T, Hv, HEAD_DIM), dtype=v.dtype, device=dev)
+    states = torch.empty((tree.n_nodes, Hv, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=dev)
+    p = _lib.TTGdnProblem(
+        dtype=_lib.TT_DTYPE_BF16 if v.dtype == torch.bfloat16 else _lib.TT_DTYPE_F32,
+        n_tokens=T, n_nodes=tree.n_nodes, n_heads_k=Hk, n_heads_v=Hv, head_dim=HEAD_DIM,
+        l2norm=1 if l2norm else 0, scale=float(scale if scale is not None else HEAD_DIM ** -0.5),
+        q=_lib.TTTensor(q.data_ptr(), q.stride(0), q.stride(1)),
+        k=_lib.TTTensor(k.data_ptr(), k.stride(0), k.stride(1)),
+        v=_lib.TTTensor(v.data_ptr(), v.stride(0), v.stride(1)),
+        g=g.data_ptr(), g_stride_tok=g.stride(0), beta=beta.data_ptr(), beta_stride_tok=beta.stride(0),
+        node_start=_ptr(tree.d_start), node_len=_ptr(tree.d_len), node_parent=_ptr(tree.d_parent),
+        level_nodes=_ptr(tree.d_levels), level_offsets=tree.level_offsets, n_levels=tree.n_levels)
+    _lib.check(_lib.lib().tt_gdn_tree_fwd(ctypes.byref(p), _ptr(o), _ptr(states), _stream(dev)),
+               "tt_gdn_tree_fwd")
+    return o, states
+
+
+def torch_chunk_gated_delta_rule_tree_varlen(query, key, value, g, beta, chunk_boundaries, chunk_parent_map,
+                                             initial_state=None, output_final_state=False,
+                                             use_qk_l2norm_in_kernel=False):
+    """Signature of tree_dfs_ssm.py:38-46 (no initial state; forward only).
+    Returns (core_out [1, T, Hv, 128], None or the last node's state)."""
+    if initial_state is not None:
+        raise NotImplementedError("initial_state is not supported (the reference drivers pass None)")
+    tree = GdnTree.from_boundaries(chunk_boundaries, chunk_parent_map, query.device)
+    o, states = gdn_tree_forward(query, key, value, g, beta, tree, l2norm=use_qk_l2norm_in_kernel)
+    last = states[-1][None] if output_final_state else None
+    return o[None], last
