@@ -156,11 +156,14 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
  * more than 3 tokens.
  *
  * Nodes are in DFS pre-order (parent[i] < i, -1 for a root); node i owns
- * tokens [node_start[i], node_start[i] + node_len[i]). level_nodes lists
- * every node once, grouped by depth (roots first); level_offsets (HOST
- * memory, n_levels + 1 entries, level_offsets[n_levels] = n_nodes) delimits
- * the groups. A node whose parent is not in an earlier group reads an
- * undefined state. */
+ * tokens [node_start[i], node_start[i] + node_len[i]) and is cut into
+ * ceil(node_len[i] / TT_GDN_CHUNK) consecutive chunks, numbered globally in
+ * node order: node_chunk0[i] is node i's first chunk and chunk_node[c] the
+ * node of chunk c (n_chunks in all). level_nodes lists every node once,
+ * grouped by depth (roots first); level_offsets (HOST memory, n_levels + 1
+ * entries, level_offsets[n_levels] = n_nodes) delimits the groups. A node
+ * whose parent is not in an earlier group reads an undefined state. */
+#define TT_GDN_CHUNK 32
 typedef struct tt_gdn_problem {
     int32_t dtype;          /* TT_DTYPE_BF16 or TT_DTYPE_F32 for q, k, v and o */
     int32_t n_tokens;
@@ -181,12 +184,20 @@ typedef struct tt_gdn_problem {
     const int32_t* level_nodes;  /* device, [n_nodes] */
     const int32_t* level_offsets;/* HOST, [n_levels + 1] */
     int32_t n_levels;
+    int32_t n_chunks;
+    const int32_t* node_chunk0;  /* device, [n_nodes] */
+    const int32_t* chunk_node;   /* device, [n_chunks] */
 } tt_gdn_problem;
 
+/* Workspace of tt_gdn_tree_fwd: per (chunk, v head) the state-independent
+ * chunk terms (U, W, A, G) in float32. */
+size_t tt_gdn_workspace_bytes(const tt_gdn_problem* p);
 /* o: [T, Hv, 128] contiguous, problem dtype. node_states: [n_nodes, Hv, 128,
  * 128] float32, the state after each node (its children's initial state;
- * kept for the backward). One launch per tree level. */
-int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* stream);
+ * kept for the backward). One parallel launch over all chunks, then one
+ * launch per tree level. */
+int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* ws, size_t ws_bytes,
+                    void* stream);
 
 /* ---- device self-test ----------------------------------------------------
  * No counterpart in the reference. Runs one v_mfma_f32_32x32x16_bf16 with the

@@ -106,7 +106,8 @@ def _gdn_problem(offsets=(0, 1, 3), **kw):
                           q=_lib.TTTensor(16, 16 * 128, 128), k=_lib.TTTensor(16, 16 * 128, 128),
                           v=_lib.TTTensor(16, 32 * 128, 128), g=16, g_stride_tok=32, beta=16,
                           beta_stride_tok=32, node_start=16, node_len=16, node_parent=16, level_nodes=16,
-                          level_offsets=arr, n_levels=len(offsets) - 1)
+                          level_offsets=arr, n_levels=len(offsets) - 1, n_chunks=5, node_chunk0=16,
+                          chunk_node=16)
     p._keep = arr
     for k, v in kw.items():
         setattr(p, k, v)
@@ -127,7 +128,8 @@ def _gdn_problem(offsets=(0, 1, 3), **kw):
 def test_gdn_validation(field, value, code):
     lib = _lib.lib()
     p = _gdn_problem(**{field: value})
-    assert lib.tt_gdn_tree_fwd(ctypes.byref(p), ctypes.c_void_p(16), ctypes.c_void_p(16), None) == code
+    V = ctypes.c_void_p(16)
+    assert lib.tt_gdn_tree_fwd(ctypes.byref(p), V, V, V, 1 << 30, None) == code
 
 
 def test_gdn_level_offsets_validation():
@@ -135,6 +137,10 @@ def test_gdn_level_offsets_validation():
     V = ctypes.c_void_p(16)
     for offs in ((0, 2), (1, 3), (0, 2, 1, 3)):        # wrong total, wrong start, not monotone
         p = _gdn_problem(offsets=offs)
-        assert lib.tt_gdn_tree_fwd(ctypes.byref(p), V, V, None) == _lib.TT_E_ARG
+        assert lib.tt_gdn_tree_fwd(ctypes.byref(p), V, V, V, 1 << 30, None) == _lib.TT_E_ARG
     p = _gdn_problem()
-    assert lib.tt_gdn_tree_fwd(ctypes.byref(p), None, V, None) == _lib.TT_E_ARG
+    assert lib.tt_gdn_tree_fwd(ctypes.byref(p), None, V, V, 1 << 30, None) == _lib.TT_E_ARG
+    assert lib.tt_gdn_tree_fwd(ctypes.byref(p), V, V, V, 64, None) == _lib.TT_E_WORKSPACE
+    p = _gdn_problem(n_chunks=2)                      # fewer chunks than nodes
+    assert lib.tt_gdn_tree_fwd(ctypes.byref(p), V, V, V, 1 << 30, None) == _lib.TT_E_ARG
+    assert lib.tt_gdn_workspace_bytes(ctypes.byref(_gdn_problem())) == 5 * 32 * (2 * 32 * 128 + 32 * 32 + 32) * 4

@@ -34,7 +34,8 @@ ABI_VERSION = 1
 EXPORTS = (
     "tt_abi_version", "tt_strerror", "tt_meta_workspace_bytes", "tt_meta_build", "tt_keys_build",
     "tt_meta_dense_mask", "tt_plan_bytes", "tt_plan_build", "tt_attn_fwd",
-    "tt_attn_bwd_workspace_bytes", "tt_attn_bwd", "tt_gdn_tree_fwd", "tt_selftest_mfma32",
+    "tt_attn_bwd_workspace_bytes", "tt_attn_bwd", "tt_gdn_workspace_bytes", "tt_gdn_tree_fwd",
+    "tt_selftest_mfma32",
 )
 
 
@@ -63,7 +64,8 @@ class TTGdnProblem(ctypes.Structure):
         ("beta", ctypes.c_void_p), ("beta_stride_tok", ctypes.c_int64),
         ("node_start", ctypes.c_void_p), ("node_len", ctypes.c_void_p), ("node_parent", ctypes.c_void_p),
         ("level_nodes", ctypes.c_void_p), ("level_offsets", ctypes.POINTER(ctypes.c_int32)),
-        ("n_levels", ctypes.c_int32),
+        ("n_levels", ctypes.c_int32), ("n_chunks", ctypes.c_int32),
+        ("node_chunk0", ctypes.c_void_p), ("chunk_node", ctypes.c_void_p),
     ]
 
 
@@ -89,7 +91,8 @@ def _declare(lib):
         "tt_attn_bwd_workspace_bytes": (SZ, [ctypes.POINTER(TTAttnProblem)]),
         "tt_attn_bwd": (ctypes.c_int, [ctypes.POINTER(TTAttnProblem), P, P, TTTensor, P, P, P, P, P, P, SZ,
                                        VP]),
-        "tt_gdn_tree_fwd": (ctypes.c_int, [ctypes.POINTER(TTGdnProblem), P, P, VP]),
+        "tt_gdn_workspace_bytes": (SZ, [ctypes.POINTER(TTGdnProblem)]),
+        "tt_gdn_tree_fwd": (ctypes.c_int, [ctypes.POINTER(TTGdnProblem), P, P, P, SZ, VP]),
         "tt_selftest_mfma32": (ctypes.c_int, [P, P, P, VP]),
     }
     for name, (res, args) in sig.items():

@@ -194,8 +194,14 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
     return tt_bwd_f32_launch(a, b, (hipStream_t)stream);
 }
 
-int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* stream) {
-    if (!p || !o || !node_states) return TT_E_ARG;
+size_t tt_gdn_workspace_bytes(const tt_gdn_problem* p) {
+    if (!p || p->n_chunks < 1 || p->n_heads_v < 1) return 0;
+    return tt_gdn_ws_bytes_impl(p->n_chunks, p->n_heads_v);
+}
+
+int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* ws, size_t ws_bytes,
+                    void* stream) {
+    if (!p || !o || !node_states || !ws) return TT_E_ARG;
     if (p->dtype != TT_DTYPE_BF16 && p->dtype != TT_DTYPE_F32) return TT_E_UNSUPPORTED;
     if (p->head_dim != 128) return TT_E_UNSUPPORTED;
     if (p->n_tokens < 1 || p->n_nodes < 1 || p->n_nodes > p->n_tokens || p->n_heads_k < 1 || p->n_heads_v < 1)
@@ -203,8 +209,11 @@ int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* 
     if (p->n_heads_v % p->n_heads_k != 0) return TT_E_UNSUPPORTED;
     if (p->n_heads_v > 65535 || !(p->scale > 0.0f) || !isfinite(p->scale)) return TT_E_ARG;
     if (!p->q.ptr || !p->k.ptr || !p->v.ptr || !p->g || !p->beta || !p->node_start || !p->node_len ||
-        !p->node_parent || !p->level_nodes || !p->level_offsets || p->n_levels < 1)
+        !p->node_parent || !p->level_nodes || !p->level_offsets || p->n_levels < 1 || !p->node_chunk0 ||
+        !p->chunk_node)
         return TT_E_ARG;
+    if (p->n_chunks < p->n_nodes || p->n_chunks > p->n_tokens) return TT_E_ARG;
+    if (ws_bytes < tt_gdn_ws_bytes_impl(p->n_chunks, p->n_heads_v)) return TT_E_WORKSPACE;
     const int64_t gran = p->dtype == TT_DTYPE_BF16 ? 8 : 4;
     const tt_tensor* ts[3] = {&p->q, &p->k, &p->v};
     for (int i = 0; i < 3; ++i) {
@@ -214,7 +223,7 @@ int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* 
             return TT_E_ARG;
     }
     if (p->g_stride_tok < p->n_heads_v || p->beta_stride_tok < p->n_heads_v) return TT_E_ARG;
-    if (!aligned(o, 16) || !aligned(node_states, 16)) return TT_E_ARG;
+    if (!aligned(o, 16) || !aligned(node_states, 16) || !aligned(ws, 16)) return TT_E_ARG;
     if (p->level_offsets[0] != 0 || p->level_offsets[p->n_levels] != p->n_nodes) return TT_E_ARG;
     for (int l = 0; l < p->n_levels; ++l)
         if (p->level_offsets[l + 1] < p->level_offsets[l]) return TT_E_ARG;
@@ -228,6 +237,9 @@ int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* 
     d.node_len = p->node_len;
     d.parent = p->node_parent;
     d.level_nodes = p->level_nodes;
+    d.node_chunk0 = p->node_chunk0;
+    d.chunk_node = p->chunk_node;
+    d.n_chunks = p->n_chunks;
     d.dtype = p->dtype;
     d.n_tokens = p->n_tokens;
     d.n_nodes = p->n_nodes;
@@ -236,7 +248,7 @@ int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* 
     d.rep = p->n_heads_v / p->n_heads_k;
     d.l2 = p->l2norm ? 1 : 0;
     d.scale = p->scale;
-    return tt_gdn_fwd_launch(d, p->level_offsets, p->n_levels, o, node_states, (hipStream_t)stream);
+    return tt_gdn_fwd_launch(d, p->level_offsets, p->n_levels, o, node_states, (float*)ws, (hipStream_t)stream);
 }
 
 int tt_selftest_mfma32(const void* a, const void* b, float* d, void* stream) {

@@ -28,6 +28,7 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 #define TT_BKB 128
 #define TT_BQB 32
 #define TT_QCH 2048
+#define TT_GDN_CHUNK 32
 
 __host__ __device__ inline int tt_cdiv(int a, int b) { return (a + b - 1) / b; }
 

@@ -53,12 +53,15 @@ struct GdnDev {
     const int32_t* node_len;
     const int32_t* parent;
     const int32_t* level_nodes;            // nodes grouped by tree depth
-    int dtype, n_tokens, n_nodes, hk, hv, rep, l2;
+    const int32_t* node_chunk0;            // first chunk of each node
+    const int32_t* chunk_node;             // node of each chunk
+    int dtype, n_tokens, n_nodes, n_chunks, hk, hv, rep, l2;
     float scale;
 };
 
+size_t tt_gdn_ws_bytes_impl(int n_chunks, int n_heads_v);
 int tt_gdn_fwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, void* out, float* states,
-                      hipStream_t s);
+                      float* ws, hipStream_t s);
 
 size_t tt_meta_ws_bytes_impl(int n);
 int tt_meta_build_impl(const int32_t* len, const int32_t* par, int n, int T, int pos_offset, int32_t* start,

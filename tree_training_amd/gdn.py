@@ -4,8 +4,9 @@ Drop-in for ``torch_chunk_gated_delta_rule_tree_varlen`` (tree_dfs_ssm.py:38-156
 twin ``_tree_gated_delta_net_varlen`` in dfs_tree_forward.py:253-353): the same
 inputs — q, k ``[B=1, T, Hk, D]``, v ``[1, T, Hv, D]``, g, beta ``[1, T, Hv]``,
 ``chunk_boundaries`` (one (start, end) per tree node, DFS order) and
-``chunk_parent_map`` (parent node index, -1 for a root) — computed by one HIP
-scan launch per tree level through ``tt_gdn_tree_fwd``.
+``chunk_parent_map`` (parent node index, -1 for a root) — computed through
+``tt_gdn_tree_fwd``: one parallel HIP launch over all 32-token chunks for the
+state-independent terms, then one scan launch per tree level.
 
 Semantics: the exact gated delta rule along every root-to-leaf path (what the
 reference function states it computes, tree_dfs_ssm.py:49-52). The reference's
@@ -24,6 +25,7 @@ from . import _lib
 from .meta import _ptr, _stream, require_device
 
 HEAD_DIM = 128
+CHUNK = 32        # TT_GDN_CHUNK
 
 
 class GdnTree:
@@ -59,12 +61,19 @@ class GdnTree:
             offs.append(offs[-1] + len(lv))
         self.n_levels = len(levels)
         self.level_offsets = (ctypes.c_int32 * len(offs))(*offs)
+        chunk0, chunk_node = [], []
+        for i, L in enumerate(self.node_len):
+            chunk0.append(len(chunk_node))
+            chunk_node.extend([i] * ((L + CHUNK - 1) // CHUNK))
+        self.n_chunks = len(chunk_node)
         dev = require_device(device)
         i32 = dict(dtype=torch.int32, device=dev)
         self.d_start = torch.tensor(start, **i32)
         self.d_len = torch.tensor(self.node_len, **i32)
         self.d_parent = torch.tensor(self.parent, **i32)
         self.d_levels = torch.tensor(order, **i32)
+        self.d_chunk0 = torch.tensor(chunk0, **i32)
+        self.d_chunk_node = torch.tensor(chunk_node, **i32)
         self.device = dev
 
     @classmethod
@@ -130,8 +139,12 @@ def gdn_tree_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch
         v=_lib.TTTensor(v.data_ptr(), v.stride(0), v.stride(1)),
         g=g.data_ptr(), g_stride_tok=g.stride(0), beta=beta.data_ptr(), beta_stride_tok=beta.stride(0),
         node_start=_ptr(tree.d_start), node_len=_ptr(tree.d_len), node_parent=_ptr(tree.d_parent),
-        level_nodes=_ptr(tree.d_levels), level_offsets=tree.level_offsets, n_levels=tree.n_levels)
-    _lib.check(_lib.lib().tt_gdn_tree_fwd(ctypes.byref(p), _ptr(o), _ptr(states), _stream(dev)),
+        level_nodes=_ptr(tree.d_levels), level_offsets=tree.level_offsets, n_levels=tree.n_levels,
+        n_chunks=tree.n_chunks, node_chunk0=_ptr(tree.d_chunk0), chunk_node=_ptr(tree.d_chunk_node))
+    lib = _lib.lib()
+    ws_bytes = lib.tt_gdn_workspace_bytes(ctypes.byref(p))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    _lib.check(lib.tt_gdn_tree_fwd(ctypes.byref(p), _ptr(o), _ptr(states), _ptr(ws), ws_bytes, _stream(dev)),
                "tt_gdn_tree_fwd")
     return o, states
 
