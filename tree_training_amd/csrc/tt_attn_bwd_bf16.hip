@@ -288,7 +288,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
                 dp = mfma32(read_row_operand(S.Dn, col, 16 * t + 8 * half),
                             read_row_operand(Vs, wave * 32 + col, 16 * t + 8 * half), dp);
             }
-            // P = exp(S*scale - lse) (zero where the key is invisible), dS = P (dP - delta).
+            // P = exp(S*scale - lse), dS = P (dP - delta); on the few steps where
+            // some key of the wave is invisible to some query, those entries are
+            // then zeroed (selects, so an overflowing exp of an invisible score
+            // never propagates).
 #pragma unroll
             for (int grp = 0; grp < 4; ++grp) {
                 const int r0 = 8 * grp + 4 * half;
@@ -296,11 +299,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
                 const f32x4 nd = *(const f32x4*)(S.ndlt + r0);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    float p = fast_exp2(fmaf(sc[4 * grp + e], c, -l2[e]));
-                    if (!full) p = ((unsigned)(q0_cur + r0 + e - lo) < vis_w) ? p : 0.0f;
+                    const float p = fast_exp2(fmaf(sc[4 * grp + e], c, -l2[e]));
                     sc[4 * grp + e] = p;
                     dp[4 * grp + e] = p * (dp[4 * grp + e] + nd[e]);
                 }
+            }
+            if (!full) {
+#pragma unroll
+                for (int grp = 0; grp < 4; ++grp)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const bool vis = (unsigned)(q0_cur + 8 * grp + 4 * half + e - lo) < vis_w;
+                        sc[4 * grp + e] = vis ? sc[4 * grp + e] : 0.0f;
+                        dp[4 * grp + e] = vis ? dp[4 * grp + e] : 0.0f;
+                    }
             }
             // dV += P^T dO, dK += dS^T Q: contraction over the 32 queries.
 #pragma unroll
