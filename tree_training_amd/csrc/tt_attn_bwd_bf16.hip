@@ -138,8 +138,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // backward: dK, dV (key-major, persistent over work items)
 // ----------------------------------------------------------------------------
 struct KvStage {
-    bf16 Q[TT_BQB * ROW];
-    bf16 Dn[TT_BQB * ROW];
+    bf16 Q[TT_BQB * ROWX];     // swizzled: read row-wise and transposed
+    bf16 Dn[TT_BQB * ROWX];
     float lse[TT_BQB];     // log2 units
     float ndlt[TT_BQB];    // -delta
 };
@@ -169,15 +169,15 @@ struct QBlockStager {
     }
     __device__ __forceinline__ void commit(const AttnDev& a, const BwdDev& bw, KvStage& S) {
         if (q0 + TT_BQB <= a.n_q) {
-            store_rows(q, threadIdx.x, S.Q);
-            store_rows(d, threadIdx.x, S.Dn);
+            store_rows<TT_BQB, true>(q, threadIdx.x, S.Q);
+            store_rows<TT_BQB, true>(d, threadIdx.x, S.Dn);
         } else {
             const int dc = (threadIdx.x & 15) * 8, r0 = threadIdx.x >> 4;
             for (int i = 0; i < TT_BQB / 16; ++i) {
                 const int r = r0 + 16 * i;
                 const int64_t qq = min(q0 + r, a.n_q - 1);
-                *(bf16x8*)(S.Q + tile_off(r, dc)) = *(const bf16x8*)((const bf16*)a.q + qq * a.q_st + h * a.q_sh + dc);
-                *(bf16x8*)(S.Dn + tile_off(r, dc)) =
+                *(bf16x8*)(S.Q + tile_offx(r, dc)) = *(const bf16x8*)((const bf16*)a.q + qq * a.q_st + h * a.q_sh + dc);
+                *(bf16x8*)(S.Dn + tile_offx(r, dc)) =
                     *(const bf16x8*)((const bf16*)bw.dout + qq * bw.do_st + h * bw.do_sh + dc);
             }
         }
@@ -201,6 +201,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
     const int col = lane & 31, half = lane >> 5;
     const float c = a.scale * TT_LOG2E;
     const int n_work = (*a.n_items) * a.hkv;
+    const RowOffsX qro = row_offsx(col, half);   // this lane's query row in the Q / dO blocks
+    const TrOffsX tro = tr_offsx(lane);
 
     for (int w_id = blockIdx.x; w_id < n_work; w_id += gridDim.x) {
         const int g = w_id % a.hkv;
@@ -282,12 +284,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
 
             // S = Q K^T and dP = dO V^T: rows = queries, lane = key column.
             f32x16 sc = (f32x16){}, dp = (f32x16){};
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                sc = mfma32(read_row_operand(S.Q, col, 16 * t + 8 * half), kbv[t], sc);
-                dp = mfma32(read_row_operand(S.Dn, col, 16 * t + 8 * half),
-                            read_row_operand(Vs, wave * 32 + col, 16 * t + 8 * half), dp);
-            }
+            static_for<8>([&](auto tt) {
+                constexpr int t = decltype(tt)::value;
+                sc = mfma32(read_rowx<t>(S.Q, qro), kbv[t], sc);
+                dp = mfma32(read_rowx<t>(S.Dn, qro), read_row_operand(Vs, wave * 32 + col, 16 * t + 8 * half), dp);
+            });
             // P = exp(S*scale - lse), dS = P (dP - delta); on the few steps where
             // some key of the wave is invisible to some query, those entries are
             // then zeroed (selects, so an overflowing exp of an invisible score
@@ -324,8 +325,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
                                         dp[r0 + 5], dp[r0 + 6], dp[r0 + 7]);
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
-                    dv[db] = mfma32(pa, read_tr_operand(S.Dn, 16 * stp, 32 * db, lane), dv[db]);
-                    dk[db] = mfma32(sa, read_tr_operand(S.Q, 16 * stp, 32 * db, lane), dk[db]);
+                    dv[db] = mfma32(pa, read_trx(S.Dn, tro, 16 * stp, 32 * db), dv[db]);
+                    dk[db] = mfma32(sa, read_trx(S.Q, tro, 16 * stp, 32 * db), dk[db]);
                 }
             }
         }

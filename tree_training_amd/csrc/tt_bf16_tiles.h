@@ -103,6 +103,57 @@ __device__ __forceinline__ bf16x8 read_row_operand(const bf16* X, int r, int d0)
     return *(const bf16x8*)(X + tile_off(r, d0));
 }
 
+// Swizzled layout for tiles read both row-wise and transposed many times
+// (the dK/dV pass's Q and dO blocks): 320-byte rows, 16-byte chunk c of row r
+// stored at chunk c ^ ((r >> 2) & 3). Both read patterns then reach every
+// bank once per LDS pass (64 banks x 4 bytes; 16-byte reads serve 16 lanes
+// per pass, transposed 8-byte reads 32).
+constexpr int ROWX = D + 32;
+__device__ __forceinline__ int tile_offx(int r, int d) {
+    return r * ROWX + ((((d >> 3) ^ ((r >> 2) & 3))) << 3) + (d & 7);
+}
+
+// Lane offsets into a swizzled tile (every access is a lane base plus a
+// compile-time offset). Row operand for head dims 16t + 8*half .. +7 of row
+// r: at (t odd ? o : e) + 32*(t/2).
+struct RowOffsX {
+    int e, o;
+};
+__device__ __forceinline__ RowOffsX row_offsx(int r, int half) {
+    const int f = (r >> 2) & 3, b = r * ROWX, x = half ^ (f & 1);
+    return {b + 8 * (2 * (f >> 1) + x), b + 8 * (2 * (1 ^ (f >> 1)) + x)};
+}
+template <int T>
+__device__ __forceinline__ bf16x8 read_rowx(const bf16* X, const RowOffsX& ro) {
+    return *(const bf16x8*)(X + ((T & 1) ? ro.o : ro.e) + 32 * (T >> 1));
+}
+// Transposed operand (as read_tr_operand) from a swizzled tile: lane l gets
+// X[r0 + kappa(e)][dbase + (l & 31)], r0 % 16 == 0, dbase % 32 == 0.
+struct TrOffsX {
+    int a, b;   // rows +0..7 and +8..15 of the 16-row group
+};
+__device__ __forceinline__ TrOffsX tr_offsx(int lane) {
+    const int j = lane & 15, grp = lane >> 4, h = grp >> 1;
+    const int rl = 4 * h + (j >> 2);
+    const int c = 2 * (grp & 1) + ((j & 3) >> 1), p = 4 * (j & 1);
+    return {rl * ROWX + ((c ^ h) << 3) + p, (rl + 8) * ROWX + ((c ^ (h ^ 2)) << 3) + p};
+}
+__device__ __forceinline__ bf16x8 read_trx(const bf16* X, const TrOffsX& to, int r0, int dbase) {
+    return cat44(ds_read_tr(X + to.a + r0 * ROWX + dbase), ds_read_tr(X + to.b + r0 * ROWX + dbase));
+}
+
+template <int I>
+struct IntT {
+    static constexpr int value = I;
+};
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(IntT<I>{});
+        static_for<N, I + 1>(f);
+    }
+}
+
 
 // Register staging: thread t holds rows (t/16) + 16*i (i < NROWS/16) at head
 // dims 8*(t%16) .. +7 of a tile; 16 lanes cover one 256-byte row, and a wave
@@ -133,11 +184,12 @@ __device__ __forceinline__ void fetch_rows_buf(RowRegs<NROWS>& r, int tid, const
         r.x[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vo, (int)(16 * i * stb), 0));
 }
 
-template <int NROWS>
+template <int NROWS, bool SWZ = false>
 __device__ __forceinline__ void store_rows(const RowRegs<NROWS>& r, int tid, bf16* X) {
     const int dc = (tid & 15) * 8, r0 = tid >> 4;
 #pragma unroll
-    for (int i = 0; i < NROWS / 16; ++i) *(bf16x8*)(X + tile_off(r0 + 16 * i, dc)) = r.x[i];
+    for (int i = 0; i < NROWS / 16; ++i)
+        *(bf16x8*)(X + (SWZ ? tile_offx(r0 + 16 * i, dc) : tile_off(r0 + 16 * i, dc))) = r.x[i];
 }
 
 __device__ __forceinline__ const bf16* key_row(const AttnDev& a, int kk, int g, bool isv) {
