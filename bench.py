@@ -15,7 +15,11 @@ with HIP events on the launch stream; the CPU baseline times the dense-mask
 restatement of the reference path (additive mask + repeat_kv + SDPA + autograd)
 on a bounded sample on the host cores.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload agent16k|gateway16k|rollout48k]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload agent16k|gateway16k|rollout48k|gdn16k]
+
+``gdn16k`` times the tree gated-delta-rule forward instead (the same 16K tree,
+16 q/k heads, 32 v heads, head_dim 128, bf16 q/k/v, fp32 gates and state) and
+reports packed tokens/s with the HBM roofline of the scan.
 """
 from __future__ import annotations
 
@@ -57,7 +61,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="agent16k", choices=["agent16k", "gateway16k", "rollout48k"])
+    ap.add_argument("--workload", default="agent16k",
+                    choices=["agent16k", "gateway16k", "rollout48k", "gdn16k"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=3)
     ap.add_argument("--calibrate-copy-mb", type=int, default=0,
@@ -89,6 +94,8 @@ def main():
         print("bench.py measures one GPU: the tree-attention path has no multi-GPU mode in this build "
               "(see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "gdn16k":
+        return run_gdn(args)
     import torch
     from tree_training_amd import _lib
     from tree_training_amd.attention import _Problem, attn_forward
@@ -249,6 +256,93 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def run_gdn(args):
+    """Tree gated-delta-rule forward on the 16K agent tree (one GDN layer)."""
+    import torch
+    from tree_training_amd.gdn import GdnTree, gdn_tree_forward
+    from tree_training_amd.workloads import agent_tree
+    HK, HV = 16, 32
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    lens, par = agent_tree(0)
+    T = sum(lens)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    bf = torch.bfloat16
+    q = torch.randn(T, HK, D, device=dev, generator=gen, dtype=bf)
+    k = torch.randn(T, HK, D, device=dev, generator=gen, dtype=bf)
+    v = torch.randn(T, HV, D, device=dev, generator=gen, dtype=bf)
+    a = torch.randn(T, HV, device=dev, generator=gen)
+    b = torch.randn(T, HV, device=dev, generator=gen)
+    A_log = torch.log(torch.rand(HV, device=dev, generator=gen) * 16.0 + 1e-3)
+    g = -A_log.exp() * torch.nn.functional.softplus(a + 1.0)   # dt_bias = 1
+    beta = b.sigmoid()
+    tree = GdnTree(lens, par, dev)
+    for _ in range(args.warmup):
+        gdn_tree_forward(q, k, v, g, beta, tree)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        gdn_tree_forward(q, k, v, g, beta, tree)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+    n_internal = len(set(p for p in par if p >= 0))
+    # bytes the scan must move at least once: q, k, v (bf16), g, beta (fp32), o (bf16),
+    # parent-state reads and node-state writes of internal nodes (fp32)
+    alg = (T * (2 * HK * D + HV * D) * 2 + T * HV * 2 * 4 + T * HV * D * 2
+           + n_internal * HV * D * D * 4 * 2)
+    gbs = alg / (ms * 1e-3) / 1e9
+    cpu = None if args.no_cpu_baseline else gdn_cpu_baseline(lens, par, args.cpu_runs)
+    line = {
+        "metric": "tree GDN scan fwd packed tokens/s (16K-token DFS tree)",
+        "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 in/out, f32 state",
+        "data": "synthetic (seeded topology; q/k/v N(0,1); gates from N(0,1) logits, A_log = log U(0,16), "
+                "dt_bias = 1)",
+        "config": {"workload": "gdn16k", "packed_tokens": T, "n_nodes": len(lens), "tree_levels": tree.n_levels,
+                   "heads_qk": HK, "heads_v": HV, "head_dim": D, "chunk": 32, "layer": "one GDN core scan",
+                   "parallelism": "single GPU"},
+        "wall_s_timed": round(wall, 3),
+        "roofline": {"bound": "hbm", "kernel": "gdn prep + per-level scan", "achieved": round(gbs, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 5), "traffic": None,
+                     "bytes_per_launch": alg},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def gdn_cpu_baseline(lens, par, runs):
+    """The oracle's chunked exact scan (float64 numpy) on one v head of the
+    same tree, scaled to all 32 heads; median of ``runs`` after a warm-up."""
+    import numpy as np
+    from oracle.gdn import gdn_tree
+    rng = np.random.default_rng(0)
+    T = sum(lens)
+    q = rng.standard_normal((T, 1, D))
+    k = rng.standard_normal((T, 1, D))
+    v = rng.standard_normal((T, 1, D))
+    g = -np.abs(rng.standard_normal((T, 1))) * 0.5
+    beta = rng.uniform(0, 1, (T, 1))
+    from threadpoolctl import threadpool_limits
+    times = []
+    with threadpool_limits(limits=1):          # one host core, stated below
+        for i in range(runs + 1):
+            t0 = time.perf_counter()
+            gdn_tree(q, k, v, g, beta, lens, par, mode="chunked", chunk=64)
+            if i:
+                times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": round(T / (t * 32), 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"1 of 32 v heads of the full {T}-token tree, oracle chunked scan (numpy float64, "
+                      f"chunk 64), median of {runs} after 1 warm-up, scaled by 1/32",
+            "seconds_per_sample": round(t, 3)}
 
 
 def cpu_baseline(topo, runs):
