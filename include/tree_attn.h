@@ -187,6 +187,11 @@ typedef struct tt_gdn_problem {
     int32_t n_chunks;
     const int32_t* node_chunk0;  /* device, [n_nodes] */
     const int32_t* chunk_node;   /* device, [n_chunks] */
+    /* Children of node i (any order): node_child[node_child_off[i] ..
+     * node_child_off[i + 1]). Device, [n_nodes + 1] and [n_nodes]; read by
+     * tt_gdn_tree_bwd only (may be NULL for the forward). */
+    const int32_t* node_child_off;
+    const int32_t* node_child;
 } tt_gdn_problem;
 
 /* Workspace of tt_gdn_tree_fwd: per (chunk, v head) the state-independent
@@ -198,6 +203,19 @@ size_t tt_gdn_workspace_bytes(const tt_gdn_problem* p);
  * launch per tree level. */
 int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* ws, size_t ws_bytes,
                     void* stream);
+
+/* Backward of tt_gdn_tree_fwd's o (what autograd computes through the
+ * reference's torch function, tree_dfs_ssm.py:38-156, for the exact rule):
+ * given d_o [T, Hv, 128] (problem dtype, strided like q), writes dq, dk [T, Hk,
+ * 128] and dv [T, Hv, 128] contiguous in the problem dtype, and dg, dbeta
+ * [T, Hv] contiguous float32. The node states carry no incoming gradient. It
+ * recomputes the forward (keeping every chunk's initial state), runs one
+ * reverse launch per tree level (deepest first) for the state gradient, then
+ * two launches over all chunks. Workspace: tt_gdn_bwd_workspace_bytes (per
+ * (chunk, v head) about 240 KiB; per (node, v head) 128 KiB). */
+size_t tt_gdn_bwd_workspace_bytes(const tt_gdn_problem* p);
+int tt_gdn_tree_bwd(const tt_gdn_problem* p, tt_tensor d_o, void* dq, void* dk, void* dv, float* dg, float* dbeta,
+                    void* ws, size_t ws_bytes, void* stream);
 
 /* ---- device self-test ----------------------------------------------------
  * No counterpart in the reference. Runs one v_mfma_f32_32x32x16_bf16 with the

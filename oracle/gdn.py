@@ -200,3 +200,31 @@ def gdn_gates(a, b, A_log, dt_bias):
     sp = np.where(z > 20.0, z, np.log1p(np.exp(np.minimum(z, 20.0))))
     g = -np.exp(np.asarray(A_log, np.float64)) * sp
     return g, beta
+
+
+def gdn_tree_torch(q, k, v, g, beta, node_len, parent, l2=True, eps=1e-6):
+    """The exact tree gated delta rule (token recurrence, as ``gdn_tree``
+    mode="exact") in torch, differentiable: the backward oracle (autograd on
+    float64). q, k [T, Hk, Dk]; v [T, Hv, Dv]; g, beta [T, Hv]. Returns o."""
+    import torch
+    T, Hk, Dk = q.shape
+    Hv, Dv = v.shape[1], v.shape[2]
+    rep = Hv // Hk
+    if l2:
+        q = q * torch.rsqrt((q * q).sum(-1, keepdim=True) + eps)
+        k = k * torch.rsqrt((k * k).sum(-1, keepdim=True) + eps)
+    q = q * Dk ** -0.5
+    q = q.repeat_interleave(rep, dim=1)
+    k = k.repeat_interleave(rep, dim=1)
+    starts = node_starts(node_len)
+    finals = [None] * len(node_len)
+    outs = []
+    for i in range(len(node_len)):
+        S = finals[parent[i]] if parent[i] >= 0 else torch.zeros(Hv, Dk, Dv, dtype=q.dtype)
+        for t in range(int(starts[i]), int(starts[i] + node_len[i])):
+            S = S * torch.exp(g[t])[:, None, None]
+            delta = (v[t] - torch.einsum("hk,hkv->hv", k[t], S)) * beta[t][:, None]
+            S = S + k[t][:, :, None] * delta[:, None, :]
+            outs.append(torch.einsum("hk,hkv->hv", q[t], S))
+        finals[i] = S
+    return torch.stack(outs, 0)

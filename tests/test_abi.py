@@ -143,4 +143,23 @@ def test_gdn_level_offsets_validation():
     assert lib.tt_gdn_tree_fwd(ctypes.byref(p), V, V, V, 64, None) == _lib.TT_E_WORKSPACE
     p = _gdn_problem(n_chunks=2)                      # fewer chunks than nodes
     assert lib.tt_gdn_tree_fwd(ctypes.byref(p), V, V, V, 1 << 30, None) == _lib.TT_E_ARG
-    assert lib.tt_gdn_workspace_bytes(ctypes.byref(_gdn_problem())) == 5 * 32 * (2 * 32 * 128 + 32 * 32 + 32) * 4
+    # per (chunk, v head): W, U [32 x 128], A, T [32 x 32], G [32] floats
+    assert lib.tt_gdn_workspace_bytes(ctypes.byref(_gdn_problem())) == 5 * 32 * (2 * 32 * 128 + 2 * 32 * 32 + 32) * 4
+
+
+def test_gdn_bwd_validation():
+    lib = _lib.lib()
+    V = ctypes.c_void_p(16)
+    DO = _lib.TTTensor(16, 32 * 128, 128)
+    p = _gdn_problem(node_child_off=16, node_child=16)
+    per_chunk = (2 * 32 * 128 + 2 * 32 * 32 + 32) + 2 * 128 * 128 + 5 * 32 * 128 + 1
+    want = (5 * 32 * per_chunk + 3 * 32 * 2 * 128 * 128) * 4
+    assert lib.tt_gdn_bwd_workspace_bytes(ctypes.byref(p)) == want
+    args = lambda ws_bytes: (V, V, V, V, V, V, ws_bytes, None)
+    assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, *args(want - 4)) == _lib.TT_E_WORKSPACE
+    assert lib.tt_gdn_tree_bwd(ctypes.byref(_gdn_problem()), DO, *args(want)) == _lib.TT_E_ARG   # no children CSR
+    assert lib.tt_gdn_tree_bwd(ctypes.byref(p), _lib.TTTensor(18, 32 * 128, 128), *args(want)) == _lib.TT_E_ARG
+    assert lib.tt_gdn_tree_bwd(ctypes.byref(p), _lib.TTTensor(16, 64, 128), *args(want)) == _lib.TT_E_ARG
+    assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, V, V, V, ctypes.c_void_p(18), V, V, want, None) == _lib.TT_E_ARG
+    assert lib.tt_gdn_tree_bwd(ctypes.byref(_gdn_problem(head_dim=64, node_child_off=16, node_child=16)), DO,
+                               *args(want)) == _lib.TT_E_UNSUPPORTED

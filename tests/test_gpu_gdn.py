@@ -1,17 +1,21 @@
-"""GPU parity of the tree gated-delta-rule scan (tt_gdn_tree_fwd) against the
-float64 oracle (oracle/gdn.py, exact mode), through the C ABI.
+"""GPU parity of the tree gated-delta-rule scan (tt_gdn_tree_fwd,
+tt_gdn_tree_bwd) against the float64 oracle (oracle/gdn.py: exact mode for the
+forward, autograd through the token recurrence for the backward), through the
+C ABI.
 
-Bars: float32 outputs and node states max_rel < 1e-5; bf16 outputs < 2e-2
-(max |error| over max |reference|). At the 16K-tree size the oracle is too
-slow, so the check there is per-path equivalence: every root-to-leaf path run
-as a plain chain of the same nodes gives bitwise the same outputs.
+Bars: float32 outputs, node states and gradients (each of dq, dk, dv, dg,
+dbeta) max_rel < 1e-5; bf16 outputs and gradients < 2e-2 (max |error| over
+max |reference|). At the 16K-tree size the oracle is too slow, so the checks
+there are per-path: every root-to-leaf path run as a plain chain of the same
+nodes gives bitwise the same outputs, and with d_o supported on one path the
+gradients equal that chain's, bitwise, and vanish off the path.
 """
 import numpy as np
 import pytest
 import torch
 
 from oracle import gdn as ogdn
-from tree_training_amd.gdn import GdnTree, gdn_tree_forward
+from tree_training_amd.gdn import GdnTree, gdn_tree_backward, gdn_tree_forward
 from tree_training_amd.workloads import agent_tree, random_forest
 
 pytestmark = pytest.mark.gpu
@@ -103,3 +107,81 @@ def test_gdn_16k_tree_per_path_equivalence():
         o_p, st_p = _run(q[idx], k[idx], v[idx], g[idx], beta[idx], plens, ppar, torch.bfloat16)
         assert np.array_equal(o_p, o[idx])
         assert np.array_equal(st_p[-1], st[leaf])
+
+
+def _run_bwd(q, k, v, g, beta, d_o, lens, par, dtype):
+    dev = torch.device("cuda", 0)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    tree = GdnTree(lens, par, dev)
+    outs = gdn_tree_backward(t(q).to(dtype), t(k).to(dtype), t(v).to(dtype), t(g), t(beta), t(d_o).to(dtype), tree)
+    torch.cuda.synchronize()
+    return [x.float().cpu().numpy() for x in outs]
+
+
+def _oracle_grads(q, k, v, g, beta, d_o, lens, par):
+    tt = [torch.from_numpy(np.asarray(x, np.float64)).requires_grad_(True) for x in (q, k, v, g, beta)]
+    o = ogdn.gdn_tree_torch(*tt, lens, par)
+    return [x.numpy() for x in torch.autograd.grad((o * torch.from_numpy(np.asarray(d_o, np.float64))).sum(), tt)]
+
+
+BWD_NAMES = ("dq", "dk", "dv", "dg", "dbeta")
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_gdn_bwd_fp32_matches_autograd_oracle(case):
+    c = CASES[case]
+    lens, par = c["topo"]()
+    T = sum(lens)
+    q, k, v, g, beta = _inputs(T, c["Hk"], c["Hv"], 3 + sum(map(ord, case)))
+    d_o = np.random.default_rng(11).standard_normal((T, c["Hv"], D)).astype(np.float32)
+    print(f"gdn bwd fp32 {case}: T={T} nodes={len(lens)}", flush=True)
+    got = _run_bwd(q, k, v, g, beta, d_o, lens, par, torch.float32)
+    ref = _oracle_grads(q, k, v, g, beta, d_o, lens, par)
+    for name, a, b in zip(BWD_NAMES, got, ref):
+        assert _rel(a, b) < 1e-5, (case, name, _rel(a, b))
+
+
+@pytest.mark.parametrize("case", ["forest_multi_chunk", "c1_heads"])
+def test_gdn_bwd_bf16_matches_autograd_oracle(case):
+    c = CASES[case]
+    lens, par = c["topo"]()
+    T = sum(lens)
+    q, k, v, g, beta = _inputs(T, c["Hk"], c["Hv"], 5 + sum(map(ord, case)), realistic_gates=True)
+    rb = lambda x: torch.from_numpy(x).bfloat16().float().numpy()
+    d_o = rb(np.random.default_rng(12).standard_normal((T, c["Hv"], D)).astype(np.float32))
+    q, k, v = rb(q), rb(k), rb(v)
+    print(f"gdn bwd bf16 {case}: T={T} nodes={len(lens)}", flush=True)
+    got = _run_bwd(q, k, v, g, beta, d_o, lens, par, torch.bfloat16)
+    ref = _oracle_grads(q, k, v, g, beta, d_o, lens, par)
+    for name, a, b in zip(BWD_NAMES, got, ref):
+        assert _rel(a, b) < 2e-2, (case, name, _rel(a, b))
+
+
+def test_gdn_bwd_16k_tree_path_support():
+    """Full size (agent tree, 16,318 tokens, 16/32 heads, bf16): with d_o
+    non-zero only on one root-to-leaf path, the tree's gradients on that path
+    equal the path run alone as a chain, bit for bit, and are exactly zero on
+    every other token."""
+    lens, par = agent_tree(0)
+    T = sum(lens)
+    q, k, v, g, beta = _inputs(T, 16, 32, 9, realistic_gates=True)
+    starts = np.concatenate([[0], np.cumsum(lens)[:-1]])
+    leaves = [i for i in range(len(lens)) if i not in set(par)]
+    leaf = leaves[len(leaves) // 2]
+    path, j = [], leaf
+    while j >= 0:
+        path.append(j)
+        j = par[j]
+    path = path[::-1]
+    idx = np.concatenate([np.arange(starts[i], starts[i] + lens[i]) for i in path])
+    d_o = np.zeros((T, 32, D), np.float32)
+    d_o[idx] = np.random.default_rng(4).standard_normal((len(idx), 32, D))
+    print(f"gdn bwd 16k path support: leaf={leaf} path_tokens={len(idx)}", flush=True)
+    full = _run_bwd(q, k, v, g, beta, d_o, lens, par, torch.bfloat16)
+    chain = _run_bwd(q[idx], k[idx], v[idx], g[idx], beta[idx], d_o[idx], [lens[i] for i in path],
+                     list(range(-1, len(path) - 1)), torch.bfloat16)
+    off = np.setdiff1d(np.arange(T), idx)
+    for name, a, b in zip(BWD_NAMES, full, chain):
+        assert np.isfinite(a).all(), name
+        assert np.array_equal(a[idx], b), name
+        assert not np.any(a[off]), name

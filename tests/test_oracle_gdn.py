@@ -147,3 +147,29 @@ def test_gates_match_torch():
     g_t = -torch.from_numpy(A_log).exp() * F.softplus(ta + torch.from_numpy(dt))
     assert np.abs(g - g_t.numpy()).max() < 1e-12
     assert np.abs(beta - torch.from_numpy(b).sigmoid().numpy()).max() < 1e-12
+
+
+def test_torch_oracle_forward_matches_numpy_and_grads_match_finite_differences():
+    lens, par = [3, 2, 4], [-1, 0, 0]
+    T = sum(lens)
+    q, k, v, g, beta = _inputs(T, 1, 2, 6, 5, 12)
+    tt = [torch.from_numpy(x).requires_grad_(True) for x in (q, k, v, g, beta)]
+    o = gdn.gdn_tree_torch(*tt, lens, par)
+    o_np, _ = gdn.gdn_tree(q, k, v, g, beta, lens, par, mode="exact")
+    assert _rel(o.detach().numpy(), o_np) < 1e-12
+    w = torch.from_numpy(np.random.default_rng(1).standard_normal(o.shape))
+    grads = torch.autograd.grad((o * w).sum(), tt)
+    rng = np.random.default_rng(2)
+    for x, gr in zip((q, k, v, g, beta), grads):
+        for _ in range(3):
+            idx = tuple(int(rng.integers(0, s)) for s in x.shape)
+            h = 1e-6
+            xp, xm = x.copy(), x.copy()
+            xp[idx] += h
+            xm[idx] -= h
+            args_p = [xp if a is x else a for a in (q, k, v, g, beta)]
+            args_m = [xm if a is x else a for a in (q, k, v, g, beta)]
+            fp = (gdn.gdn_tree(*args_p, lens, par, mode="exact")[0] * w.numpy()).sum()
+            fm = (gdn.gdn_tree(*args_m, lens, par, mode="exact")[0] * w.numpy()).sum()
+            fd = (fp - fm) / (2 * h)
+            assert abs(fd - float(gr[idx])) < 1e-6 * max(1.0, abs(fd))

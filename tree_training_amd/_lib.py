@@ -35,6 +35,7 @@ EXPORTS = (
     "tt_abi_version", "tt_strerror", "tt_meta_workspace_bytes", "tt_meta_build", "tt_keys_build",
     "tt_meta_dense_mask", "tt_plan_bytes", "tt_plan_build", "tt_attn_fwd",
     "tt_attn_bwd_workspace_bytes", "tt_attn_bwd", "tt_gdn_workspace_bytes", "tt_gdn_tree_fwd",
+    "tt_gdn_bwd_workspace_bytes", "tt_gdn_tree_bwd",
     "tt_selftest_mfma32",
 )
 
@@ -66,6 +67,7 @@ class TTGdnProblem(ctypes.Structure):
         ("level_nodes", ctypes.c_void_p), ("level_offsets", ctypes.POINTER(ctypes.c_int32)),
         ("n_levels", ctypes.c_int32), ("n_chunks", ctypes.c_int32),
         ("node_chunk0", ctypes.c_void_p), ("chunk_node", ctypes.c_void_p),
+        ("node_child_off", ctypes.c_void_p), ("node_child", ctypes.c_void_p),
     ]
 
 
@@ -93,6 +95,8 @@ def _declare(lib):
                                        VP]),
         "tt_gdn_workspace_bytes": (SZ, [ctypes.POINTER(TTGdnProblem)]),
         "tt_gdn_tree_fwd": (ctypes.c_int, [ctypes.POINTER(TTGdnProblem), P, P, P, SZ, VP]),
+        "tt_gdn_bwd_workspace_bytes": (SZ, [ctypes.POINTER(TTGdnProblem)]),
+        "tt_gdn_tree_bwd": (ctypes.c_int, [ctypes.POINTER(TTGdnProblem), TTTensor, P, P, P, P, P, P, SZ, VP]),
         "tt_selftest_mfma32": (ctypes.c_int, [P, P, P, VP]),
     }
     for name, (res, args) in sig.items():

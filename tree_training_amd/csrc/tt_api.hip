@@ -199,9 +199,11 @@ size_t tt_gdn_workspace_bytes(const tt_gdn_problem* p) {
     return tt_gdn_ws_bytes_impl(p->n_chunks, p->n_heads_v);
 }
 
-int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* ws, size_t ws_bytes,
-                    void* stream) {
-    if (!p || !o || !node_states || !ws) return TT_E_ARG;
+}  // extern "C"
+
+// Checks a tt_gdn_problem and fills the device view; TT_OK or a TT_E_* code.
+static int gdn_problem(const tt_gdn_problem* p, GdnDev& d) {
+    if (!p) return TT_E_ARG;
     if (p->dtype != TT_DTYPE_BF16 && p->dtype != TT_DTYPE_F32) return TT_E_UNSUPPORTED;
     if (p->head_dim != 128) return TT_E_UNSUPPORTED;
     if (p->n_tokens < 1 || p->n_nodes < 1 || p->n_nodes > p->n_tokens || p->n_heads_k < 1 || p->n_heads_v < 1)
@@ -213,7 +215,6 @@ int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* 
         !p->chunk_node)
         return TT_E_ARG;
     if (p->n_chunks < p->n_nodes || p->n_chunks > p->n_tokens) return TT_E_ARG;
-    if (ws_bytes < tt_gdn_ws_bytes_impl(p->n_chunks, p->n_heads_v)) return TT_E_WORKSPACE;
     const int64_t gran = p->dtype == TT_DTYPE_BF16 ? 8 : 4;
     const tt_tensor* ts[3] = {&p->q, &p->k, &p->v};
     for (int i = 0; i < 3; ++i) {
@@ -223,11 +224,9 @@ int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* 
             return TT_E_ARG;
     }
     if (p->g_stride_tok < p->n_heads_v || p->beta_stride_tok < p->n_heads_v) return TT_E_ARG;
-    if (!aligned(o, 16) || !aligned(node_states, 16) || !aligned(ws, 16)) return TT_E_ARG;
     if (p->level_offsets[0] != 0 || p->level_offsets[p->n_levels] != p->n_nodes) return TT_E_ARG;
     for (int l = 0; l < p->n_levels; ++l)
         if (p->level_offsets[l + 1] < p->level_offsets[l]) return TT_E_ARG;
-    GdnDev d;
     d.q = p->q.ptr; d.q_st = p->q.stride_tok; d.q_sh = p->q.stride_head;
     d.k = p->k.ptr; d.k_st = p->k.stride_tok; d.k_sh = p->k.stride_head;
     d.v = p->v.ptr; d.v_st = p->v.stride_tok; d.v_sh = p->v.stride_head;
@@ -239,6 +238,8 @@ int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* 
     d.level_nodes = p->level_nodes;
     d.node_chunk0 = p->node_chunk0;
     d.chunk_node = p->chunk_node;
+    d.child_off = p->node_child_off;
+    d.child = p->node_child;
     d.n_chunks = p->n_chunks;
     d.dtype = p->dtype;
     d.n_tokens = p->n_tokens;
@@ -248,7 +249,44 @@ int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* 
     d.rep = p->n_heads_v / p->n_heads_k;
     d.l2 = p->l2norm ? 1 : 0;
     d.scale = p->scale;
+    return TT_OK;
+}
+
+extern "C" {
+
+int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* ws, size_t ws_bytes,
+                    void* stream) {
+    GdnDev d;
+    const int rc = gdn_problem(p, d);
+    if (rc != TT_OK) return rc;
+    if (!o || !node_states || !ws) return TT_E_ARG;
+    if (ws_bytes < tt_gdn_ws_bytes_impl(p->n_chunks, p->n_heads_v)) return TT_E_WORKSPACE;
+    if (!aligned(o, 16) || !aligned(node_states, 16) || !aligned(ws, 16)) return TT_E_ARG;
     return tt_gdn_fwd_launch(d, p->level_offsets, p->n_levels, o, node_states, (float*)ws, (hipStream_t)stream);
+}
+
+size_t tt_gdn_bwd_workspace_bytes(const tt_gdn_problem* p) {
+    if (!p || p->n_chunks < 1 || p->n_nodes < 1 || p->n_heads_v < 1) return 0;
+    return tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v);
+}
+
+int tt_gdn_tree_bwd(const tt_gdn_problem* p, tt_tensor d_o, void* dq, void* dk, void* dv, float* dg, float* dbeta,
+                    void* ws, size_t ws_bytes, void* stream) {
+    GdnDev d;
+    const int rc = gdn_problem(p, d);
+    if (rc != TT_OK) return rc;
+    if (!p->node_child_off || !p->node_child) return TT_E_ARG;
+    if (!d_o.ptr || !dq || !dk || !dv || !dg || !dbeta || !ws) return TT_E_ARG;
+    const int64_t gran = p->dtype == TT_DTYPE_BF16 ? 8 : 4;
+    if (d_o.stride_tok < 128 || d_o.stride_head < 128 || (d_o.stride_tok % gran) || (d_o.stride_head % gran) ||
+        !aligned(d_o.ptr, 16))
+        return TT_E_ARG;
+    if (ws_bytes < tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v)) return TT_E_WORKSPACE;
+    if (!aligned(dq, 16) || !aligned(dk, 16) || !aligned(dv, 16) || !aligned(ws, 16) || !aligned(dg, 4) ||
+        !aligned(dbeta, 4))
+        return TT_E_ARG;
+    return tt_gdn_bwd_launch(d, p->level_offsets, p->n_levels, d_o.ptr, d_o.stride_tok, d_o.stride_head, dq, dk,
+                             dv, dg, dbeta, (float*)ws, (hipStream_t)stream);
 }
 
 int tt_selftest_mfma32(const void* a, const void* b, float* d, void* stream) {

@@ -36,8 +36,9 @@ constexpr int NSL = 4;            // value-column slices in the scan
 constexpr int VS = GD / NSL;      // columns per slice
 constexpr int VP = VS + 4;        // row stride of [* x VS] tiles
 
-// Workspace per (chunk, v head), floats: W [GC][GD], U [GC][GD], A [GC][GC], G [GC].
-constexpr size_t kWsW = 0, kWsU = GC * GD, kWsA = 2 * GC * GD, kWsG = 2 * GC * GD + GC * GC;
+// Workspace per (chunk, v head), floats: W [GC][GD], U [GC][GD], A [GC][GC],
+// T [GC][GC] (the inverse, for the backward), G [GC].
+constexpr size_t kWsW = 0, kWsU = GC * GD, kWsA = 2 * GC * GD, kWsT = kWsA + GC * GC, kWsG = kWsT + GC * GC;
 constexpr size_t kWsChunk = kWsG + GC;
 
 template <typename T>
@@ -223,6 +224,7 @@ __global__ __launch_bounds__(GT) void gdn_prep_kernel(GdnDev p, float* __restric
             *(f32x4*)&L.Tm[ti * MS + tc] += tp;
             __syncthreads();
         }
+        *(f32x4*)(out + kWsT + ti * GC + tc) = *(const f32x4*)&L.Tm[ti * MS + tc];
     }
 
     // U = T (beta v), W = T (beta e^G k^): thread t owns rows oi0..+3, columns oc0..+3.
@@ -272,9 +274,13 @@ struct ScanLds {
     float G[GC];
 };
 
+// out may be null (the backward's recompute); chunk_sin / chunk_vp, when
+// given, receive each chunk's initial state and V' ([n_chunks, Hv, 128, 128]
+// and [n_chunks, Hv, 32, 128] floats).
 template <typename TIn>
 __global__ __launch_bounds__(GT) void gdn_scan_kernel(GdnDev p, int lvl_begin, const float* __restrict__ ws,
-                                                      TIn* __restrict__ out, float* __restrict__ states) {
+                                                      TIn* __restrict__ out, float* __restrict__ states,
+                                                      float* __restrict__ chunk_sin, float* __restrict__ chunk_vp) {
     __shared__ __attribute__((aligned(16))) ScanLds L;
     const int node = p.level_nodes[lvl_begin + blockIdx.x];
     if (node < 0 || node >= p.n_nodes) return;
@@ -302,7 +308,14 @@ __global__ __launch_bounds__(GT) void gdn_scan_kernel(GdnDev p, int lvl_begin, c
 
     for (int c0 = 0; c0 < len; c0 += GC) {
         const int Lc = min(GC, len - c0);
-        const float* cw = ws + ((size_t)(chunk0 + c0 / GC) * p.hv + h) * kWsChunk;
+        const size_t ch = (size_t)(chunk0 + c0 / GC) * p.hv + h;
+        const float* cw = ws + ch * kWsChunk;
+        if (chunk_sin) {   // this thread's own state elements (written by it)
+            float* dst = chunk_sin + ch * GD * GD;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                *(f32x4*)(dst + (sr0 + r) * GD + col0 + sc) = *(const f32x4*)&L.S[(sr0 + r) * VP + sc];
+        }
         __syncthreads();   // readers of the previous chunk's tiles are done
         load_chunk_rows<TIn>(p, start + c0, Lc, h, L.Q, L.K, nullptr);
         {
@@ -337,6 +350,7 @@ __global__ __launch_bounds__(GT) void gdn_scan_kernel(GdnDev p, int lvl_begin, c
             }
         }
         *(f32x4*)&L.Vp[oi * VP + oc] = vp;
+        if (chunk_vp) *(f32x4*)(chunk_vp + ch * GC * GD + oi * GD + col0 + oc) = vp;
         __syncthreads();   // V' complete; every reader of S for this chunk is done
 
         // O = e^G (q^ S) + A V'.
@@ -352,7 +366,7 @@ __global__ __launch_bounds__(GT) void gdn_scan_kernel(GdnDev p, int lvl_begin, c
                     for (int b = 0; b < 4; ++b) o[b] = fmaf(ar[jj], v[b], o[b]);
                 }
             }
-            if (oi < Lc) store4(out + ((int64_t)(start + c0 + oi) * p.hv + h) * GD + col0 + oc, o);
+            if (out && oi < Lc) store4(out + ((int64_t)(start + c0 + oi) * p.hv + h) * GD + col0 + oc, o);
         }
         // S <- e^{G_last} S + (k^ e^{G_last - G})^T V'.
         {
@@ -383,6 +397,594 @@ __global__ __launch_bounds__(GT) void gdn_scan_kernel(GdnDev p, int lvl_begin, c
         *(f32x4*)(dst + (sr0 + r) * GD + col0 + sc) = *(const f32x4*)&L.S[(sr0 + r) * VP + sc];
 }
 
+
+// ----------------------------------------------------------------------------
+// backward
+// ----------------------------------------------------------------------------
+// The backward recomputes the forward (prep + level scans, keeping each
+// chunk's initial state S and V'), then:
+//  * gdn_rscan_kernel — reverse level scan (deepest level first) of dS, the
+//    gradient of the state after a chunk, per (node, v head, value slice):
+//      dV' = A^T dO + (e^{G_L - G} k^) dS,
+//      dS <- e^{G_L} dS + (e^G q^)^T dO - W^T dV'.
+//    A node's last chunk starts from the sum of its children's dS at entry
+//    (zero for a leaf, whose final state is not an output that carries a
+//    gradient).
+//  * gdn_bwd_state_kernel — per (chunk, v head), the products with the
+//    128 x 128 states: X = dO S^T, dW = -dV' S^T, dK~ = V' dS^T, <S, dS>.
+//  * gdn_bwd_chunk_kernel — per (chunk, q/k head, looping over its v heads),
+//    everything else: the chunk's 32 x 32 algebra (A, T = (I - N)^-1, N),
+//    dv, dbeta, dg (reverse cumulative sum of dG within the chunk), and
+//    dq, dk summed over the v heads of the group, then through the l2 norm.
+
+template <typename T>
+__device__ __forceinline__ f32x4 load4(const T* p) {
+    if constexpr (sizeof(T) == 2) {
+        const bf16x4 a = *(const bf16x4*)p;
+        return (f32x4){(float)a[0], (float)a[1], (float)a[2], (float)a[3]};
+    } else {
+        return *(const f32x4*)p;
+    }
+}
+
+__device__ __forceinline__ float dot4(const f32x4& a, const f32x4& b) {
+    return fmaf(a[0], b[0], fmaf(a[1], b[1], fmaf(a[2], b[2], a[3] * b[3])));
+}
+
+// Rows of a [GC x GD] tile into LDS (stride RS): thread t copies row t/8,
+// dims 16*(t%8)..+15; rows at or past `len` are zero.
+template <typename T>
+__device__ __forceinline__ void tile_in(const T* base, int64_t row_stride, int len, float* dst) {
+    const int i = threadIdx.x >> 3, d0 = 16 * (threadIdx.x & 7);
+    float x[16];
+    if (i < len) {
+        load16(base + i * row_stride + d0, x);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) x[e] = 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < 16; e += 4) *(f32x4*)&dst[i * RS + d0 + e] = (f32x4){x[e], x[e + 1], x[e + 2], x[e + 3]};
+}
+
+struct RscanLds {
+    float S[GD * VP];     // dS slice [Dk][VS]
+    float Q[GC * RS];     // e^G q^ * scale
+    float K[GC * RS];     // e^{G_L - G} k^
+    float W[GC * RS];
+    float dO[GC * VP];    // dO slice
+    float dV[GC * VP];    // dV' slice
+    float A[GC * MS];
+    float G[GC];
+};
+
+template <typename TIn>
+__global__ __launch_bounds__(GT) void gdn_rscan_kernel(GdnDev p, int lvl_begin, const float* __restrict__ ws,
+                                                       const TIn* __restrict__ d_o, int64_t do_st, int64_t do_sh,
+                                                       float* __restrict__ chunk_dso, float* __restrict__ chunk_dvp,
+                                                       float* __restrict__ node_dsin) {
+    __shared__ __attribute__((aligned(16))) RscanLds L;
+    const int node = p.level_nodes[lvl_begin + blockIdx.x];
+    if (node < 0 || node >= p.n_nodes) return;
+    const int h = blockIdx.y, col0 = VS * blockIdx.z;
+    const int t = threadIdx.x;
+    const int start = p.node_start[node], len = p.node_len[node], chunk0 = p.node_chunk0[node];
+    if (start < 0 || len < 1 || start > p.n_tokens - len) return;        // malformed node: skipped
+    if (chunk0 < 0 || chunk0 > p.n_chunks - tt_cdiv(len, GC)) return;
+
+    // dS slice: thread t owns rows sr0..sr0+3, columns sc..sc+3 (of the slice).
+    const int sr0 = 4 * (t >> 3), sc = 4 * (t & 7);
+    {
+        f32x4 acc[4] = {};
+        const int c_lo = max(p.child_off[node], 0), c_hi = min(p.child_off[node + 1], p.n_nodes);
+        for (int ci = c_lo; ci < c_hi; ++ci) {
+            const int child = p.child[ci];
+            if (child <= node || child >= p.n_nodes) continue;          // children follow their parent
+            const float* src = node_dsin + ((size_t)child * p.hv + h) * GD * GD;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] += *(const f32x4*)(src + (sr0 + r) * GD + col0 + sc);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) *(f32x4*)&L.S[(sr0 + r) * VP + sc] = acc[r];
+    }
+    const int oi = t >> 3, oc = 4 * (t & 7);
+
+    for (int ci = tt_cdiv(len, GC) - 1; ci >= 0; --ci) {
+        const int c0 = GC * ci, Lc = min(GC, len - c0);
+        const size_t chn = (size_t)(chunk0 + ci) * p.hv + h;
+        const float* cw = ws + chn * kWsChunk;
+        {   // the gradient of this chunk's output state (own elements)
+            float* dst = chunk_dso + chn * GD * GD;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                *(f32x4*)(dst + (sr0 + r) * GD + col0 + sc) = *(const f32x4*)&L.S[(sr0 + r) * VP + sc];
+        }
+        __syncthreads();   // readers of the previous chunk's tiles are done
+        load_chunk_rows<TIn>(p, start + c0, Lc, h, L.Q, L.K, nullptr);
+        {
+            const int i = t >> 3, d0 = 16 * (t & 7);
+            const float gi = cw[kWsG + i], gl = cw[kWsG + GC - 1];
+            const float eq = expf(gi), ek = expf(gl - gi);
+#pragma unroll
+            for (int e = 0; e < 16; e += 4) {   // rows written by this thread just above
+                *(f32x4*)&L.Q[i * RS + d0 + e] *= eq;
+                *(f32x4*)&L.K[i * RS + d0 + e] *= ek;
+                *(f32x4*)&L.W[i * RS + d0 + e] = *(const f32x4*)(cw + kWsW + i * GD + d0 + e);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int pi = t + GT * e;
+                L.A[(pi >> 5) * MS + (pi & 31)] = cw[kWsA + pi];
+            }
+            if (t < GC) L.G[t] = cw[kWsG + t];
+            f32x4 dov = {};
+            if (oi < Lc) dov = load4(d_o + (int64_t)(start + c0 + oi) * do_st + (int64_t)h * do_sh + col0 + oc);
+            *(f32x4*)&L.dO[oi * VP + oc] = dov;
+        }
+        __syncthreads();
+
+        // dV'[oi] = sum_j A[j][oi] dO[j] + sum_r K[oi][r] dS[r]
+        f32x4 dv = {};
+#pragma unroll 4
+        for (int j = 0; j < GC; ++j) dv += L.A[j * MS + oi] * *(const f32x4*)&L.dO[j * VP + oc];
+#pragma unroll 2
+        for (int r0 = 0; r0 < GD; r0 += 4) {
+            const f32x4 kr = *(const f32x4*)&L.K[oi * RS + r0];
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const f32x4 sv = *(const f32x4*)&L.S[(r0 + rr) * VP + oc];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) dv[b] = fmaf(kr[rr], sv[b], dv[b]);
+            }
+        }
+        *(f32x4*)&L.dV[oi * VP + oc] = dv;
+        *(f32x4*)(chunk_dvp + chn * GC * GD + oi * GD + col0 + oc) = dv;
+        __syncthreads();   // dV' complete; every reader of dS for this chunk is done
+
+        // dS <- e^{G_L} dS + sum_i (Q[i][r] dO[i] - W[i][r] dV'[i])
+        {
+            const float el = expf(L.G[GC - 1]);
+            f32x4 sv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sv[r] = *(const f32x4*)&L.S[(sr0 + r) * VP + sc] * el;
+#pragma unroll 4
+            for (int i = 0; i < GC; ++i) {
+                const f32x4 qr = *(const f32x4*)&L.Q[i * RS + sr0];
+                const f32x4 wr = *(const f32x4*)&L.W[i * RS + sr0];
+                const f32x4 o = *(const f32x4*)&L.dO[i * VP + sc];
+                const f32x4 v = *(const f32x4*)&L.dV[i * VP + sc];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) sv[r][b] = fmaf(qr[r], o[b], fmaf(-wr[r], v[b], sv[r][b]));
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) *(f32x4*)&L.S[(sr0 + r) * VP + sc] = sv[r];
+        }
+    }
+    // dS at the node's entry, summed into its parent by the next (shallower) level.
+    float* dst = node_dsin + ((size_t)node * p.hv + h) * GD * GD;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        *(f32x4*)(dst + (sr0 + r) * GD + col0 + sc) = *(const f32x4*)&L.S[(sr0 + r) * VP + sc];
+}
+
+struct StateGradLds {
+    float dO[GC * RS];
+    float dV[GC * RS];
+    float Vp[GC * RS];
+    float Sl[GC * RS];    // 32-row slab of S or dS
+    float red[GT / 64];
+};
+
+// X = dO S^T, dW = -dV' S^T, dK~ = V' dS^T ([GC x GD] each) and <S, dS>.
+template <typename TIn>
+__global__ __launch_bounds__(GT) void gdn_bwd_state_kernel(GdnDev p, const TIn* __restrict__ d_o, int64_t do_st,
+                                                           int64_t do_sh, const float* __restrict__ chunk_sin,
+                                                           const float* __restrict__ chunk_dso,
+                                                           const float* __restrict__ chunk_vp,
+                                                           const float* __restrict__ chunk_dvp,
+                                                           float* __restrict__ xo, float* __restrict__ dwo,
+                                                           float* __restrict__ dkto, float* __restrict__ sdot) {
+    __shared__ __attribute__((aligned(16))) StateGradLds L;
+    const int c = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
+    int start, len;
+    if (!chunk_span(p, c, start, len)) return;
+    const size_t chn = (size_t)c * p.hv + h;
+    const int i = t >> 3, s = t & 7, d0 = 16 * s;
+    tile_in(d_o + (int64_t)start * do_st + (int64_t)h * do_sh, do_st, len, L.dO);
+    tile_in(chunk_dvp + chn * GC * GD, GD, GC, L.dV);
+    tile_in(chunk_vp + chn * GC * GD, GD, GC, L.Vp);
+    const float* Sin = chunk_sin + chn * GD * GD;
+    const float* dSo = chunk_dso + chn * GD * GD;
+    float* xr = xo + chn * GC * GD + i * GD;
+    float* wr = dwo + chn * GC * GD + i * GD;
+    float* kr = dkto + chn * GC * GD + i * GD;
+    float sd = 0.0f;
+    // Slab rows this thread contracts against: s, s + 8, s + 16, s + 24.
+#pragma unroll 1
+    for (int sb = 0; sb < GD / GC; ++sb) {
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < 16; e += 4)
+            *(f32x4*)&L.Sl[i * RS + d0 + e] = *(const f32x4*)(Sin + (GC * sb + i) * GD + d0 + e);
+        __syncthreads();
+        float x[4] = {}, w[4] = {};
+#pragma unroll 4
+        for (int v = 0; v < GD; v += 4) {
+            const f32x4 a = *(const f32x4*)&L.dO[i * RS + v];
+            const f32x4 b = *(const f32x4*)&L.dV[i * RS + v];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const f32x4 sv = *(const f32x4*)&L.Sl[(s + 8 * e) * RS + v];
+                x[e] += dot4(a, sv);
+                w[e] += dot4(b, sv);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            xr[GC * sb + s + 8 * e] = x[e];
+            wr[GC * sb + s + 8 * e] = -w[e];
+        }
+    }
+#pragma unroll 1
+    for (int sb = 0; sb < GD / GC; ++sb) {
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < 16; e += 4) {
+            const size_t off = (size_t)(GC * sb + i) * GD + d0 + e;
+            const f32x4 a = *(const f32x4*)(dSo + off);
+            sd += dot4(a, *(const f32x4*)(Sin + off));
+            *(f32x4*)&L.Sl[i * RS + d0 + e] = a;
+        }
+        __syncthreads();
+        float k[4] = {};
+#pragma unroll 4
+        for (int v = 0; v < GD; v += 4) {
+            const f32x4 a = *(const f32x4*)&L.Vp[i * RS + v];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) k[e] += dot4(a, *(const f32x4*)&L.Sl[(s + 8 * e) * RS + v]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kr[GC * sb + s + 8 * e] = k[e];
+    }
+    sd = wave_sum(sd);
+    if ((t & 63) == 0) L.red[t >> 6] = sd;
+    __syncthreads();
+    if (t == 0) {
+        float tot = 0.0f;
+#pragma unroll
+        for (int w2 = 0; w2 < GT / 64; ++w2) tot += L.red[w2];
+        sdot[chn] = tot;
+    }
+}
+
+struct ChunkGradLds {
+    float Qs[GC * RS];    // q^ * scale
+    float Ks[GC * RS];    // k^
+    float P1[GC * RS];
+    float P2[GC * RS];
+    float P3[GC * RS];    // v; later Y = T^T dT (stride MS)
+    float KK[GC * MS];    // k^ k^T
+    float M1[GC * MS];    // A -> dA * D -> dT -> E
+    float M2[GC * MS];    // T
+    float M3[GC * MS];    // dA * A + dN * N (for the column sums of dG)
+    float G[GC];
+    float B[GC];
+    float Grow[GC];
+    float Crow[GC];
+};
+
+// Thread t owns row i = t/8 of every [GC x *] result; in [GC x GD] results the
+// columns 32m + 4s + e (s = t%8, m, e < 4), in [GC x GC] results s + 8e.
+template <typename TIn>
+__global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* __restrict__ d_o, int64_t do_st,
+                                                           int64_t do_sh, const float* __restrict__ ws,
+                                                           const float* __restrict__ chunk_vp,
+                                                           const float* __restrict__ chunk_dvp,
+                                                           const float* __restrict__ xo, const float* __restrict__ dwo,
+                                                           const float* __restrict__ dkto,
+                                                           const float* __restrict__ sdot, TIn* __restrict__ dq,
+                                                           TIn* __restrict__ dk, TIn* __restrict__ dv,
+                                                           float* __restrict__ dg, float* __restrict__ dbeta) {
+    __shared__ __attribute__((aligned(16))) ChunkGradLds L;
+    const int c = blockIdx.x, hk = blockIdx.y, t = threadIdx.x;
+    int start, len;
+    if (!chunk_span(p, c, start, len)) return;
+    const int i = t >> 3, s = t & 7;
+    const bool valid = i < len;
+    const int64_t tok = start + i;
+
+    load_chunk_rows<TIn>(p, start, len, hk * p.rep, L.Qs, L.Ks, nullptr);
+    __syncthreads();
+    {
+        float kk[4] = {};
+#pragma unroll 4
+        for (int d = 0; d < GD; d += 4) {
+            const f32x4 a = *(const f32x4*)&L.Ks[i * RS + d];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) kk[e] += dot4(a, *(const f32x4*)&L.Ks[(s + 8 * e) * RS + d]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) L.KK[i * MS + s + 8 * e] = kk[e];
+    }
+    float dqa[16], dka[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dqa[e] = dka[e] = 0.0f;
+
+#pragma unroll 1
+    for (int hh = 0; hh < p.rep; ++hh) {
+        const int h = hk * p.rep + hh;
+        const size_t chn = (size_t)c * p.hv + h;
+        const float* cw = ws + chn * kWsChunk;
+        __syncthreads();   // the previous head's readers are done
+        if (t < GC) {
+            L.G[t] = cw[kWsG + t];
+            L.B[t] = t < len ? p.beta[(int64_t)(start + t) * p.b_st + h] : 0.0f;
+        }
+        tile_in(d_o + (int64_t)start * do_st + (int64_t)h * do_sh, do_st, len, L.P1);
+        tile_in(chunk_vp + chn * GC * GD, GD, GC, L.P2);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int j = s + 8 * e;
+            L.M1[i * MS + j] = cw[kWsA + i * GC + j];
+            L.M2[i * MS + j] = cw[kWsT + i * GC + j];
+        }
+        __syncthreads();
+        const float gi = L.G[i], gl = L.G[GC - 1], egi = expf(gi), bi = L.B[i];
+        float dgp = 0.0f, dbp = 0.0f, cp = 0.0f;   // this thread's share of row i's dG, dbeta, c
+
+        // dA = dO V'^T (j <= i): dG from A = (q^ k^T) * D, then dP = dA * D.
+        {
+            float da[4] = {};
+#pragma unroll 4
+            for (int d = 0; d < GD; d += 4) {
+                const f32x4 a = *(const f32x4*)&L.P1[i * RS + d];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) da[e] += dot4(a, *(const f32x4*)&L.P2[(s + 8 * e) * RS + d]);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = s + 8 * e;
+                const float dae = j <= i ? da[e] : 0.0f;
+                const float pa = dae * L.M1[i * MS + j];
+                dgp += pa;
+                L.M3[i * MS + j] = pa;
+                L.M1[i * MS + j] = j <= i ? dae * expf(gi - L.G[j]) : 0.0f;
+            }
+        }
+        // O's state term e^G q^ S: dq^ += e^G X, dG += e^G q^ . X.
+        {
+            const float* xr = xo + chn * GC * GD + i * GD;
+            float xq = 0.0f;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const f32x4 x = *(const f32x4*)(xr + 32 * m + 4 * s);
+                const f32x4 q = *(const f32x4*)&L.Qs[i * RS + 32 * m + 4 * s];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) dqa[4 * m + e] = fmaf(egi, x[e], dqa[4 * m + e]);
+                xq += dot4(q, x);
+            }
+            dgp = fmaf(egi, xq, dgp);
+        }
+        __syncthreads();   // dP complete
+        // dq^ += dP k^, dk^ += dP^T q^.
+#pragma unroll 2
+        for (int j = 0; j < GC; ++j) {
+            const float pij = L.M1[i * MS + j], pji = L.M1[j * MS + i];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const f32x4 kj = *(const f32x4*)&L.Ks[j * RS + 32 * m + 4 * s];
+                const f32x4 qj = *(const f32x4*)&L.Qs[j * RS + 32 * m + 4 * s];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    dqa[4 * m + e] = fmaf(pij, kj[e], dqa[4 * m + e]);
+                    dka[4 * m + e] = fmaf(pji, qj[e], dka[4 * m + e]);
+                }
+            }
+        }
+        __syncthreads();   // P1, P2, M1 free
+        tile_in(chunk_dvp + chn * GC * GD, GD, GC, L.P1);
+        tile_in(dwo + chn * GC * GD, GD, GC, L.P2);
+        tile_in((const TIn*)p.v + (int64_t)start * p.v_st + (int64_t)h * p.v_sh, p.v_st, len, L.P3);
+        __syncthreads();
+
+        // dBv = T^T dV', dBk = T^T dW; dv = beta dBv; dbeta, dk^, dG from
+        // U = T (beta v) and W = T (beta e^G k^).
+        {
+            float dbv[16], dbk[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) dbv[e] = dbk[e] = 0.0f;
+#pragma unroll 2
+            for (int j = 0; j < GC; ++j) {
+                const float tji = L.M2[j * MS + i];
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const f32x4 a = *(const f32x4*)&L.P1[j * RS + 32 * m + 4 * s];
+                    const f32x4 b = *(const f32x4*)&L.P2[j * RS + 32 * m + 4 * s];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        dbv[4 * m + e] = fmaf(tji, a[e], dbv[4 * m + e]);
+                        dbk[4 * m + e] = fmaf(tji, b[e], dbk[4 * m + e]);
+                    }
+                }
+            }
+            float vb = 0.0f, kb = 0.0f;
+            const float bge = bi * egi;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const f32x4 vv = *(const f32x4*)&L.P3[i * RS + 32 * m + 4 * s];
+                const f32x4 kv = *(const f32x4*)&L.Ks[i * RS + 32 * m + 4 * s];
+                f32x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    vb = fmaf(vv[e], dbv[4 * m + e], vb);
+                    kb = fmaf(kv[e], dbk[4 * m + e], kb);
+                    dka[4 * m + e] = fmaf(bge, dbk[4 * m + e], dka[4 * m + e]);
+                    o[e] = bi * dbv[4 * m + e];
+                }
+                if (valid) store4(dv + (tok * p.hv + h) * GD + 32 * m + 4 * s, o);
+            }
+            dbp += vb + egi * kb;
+            dgp = fmaf(bge, kb, dgp);
+        }
+        // dT = dV' (beta v)^T + dW (beta e^G k^)^T
+        {
+            float t1[4] = {}, t2[4] = {};
+#pragma unroll 4
+            for (int d = 0; d < GD; d += 4) {
+                const f32x4 a = *(const f32x4*)&L.P1[i * RS + d];
+                const f32x4 b = *(const f32x4*)&L.P2[i * RS + d];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    t1[e] += dot4(a, *(const f32x4*)&L.P3[(s + 8 * e) * RS + d]);
+                    t2[e] += dot4(b, *(const f32x4*)&L.Ks[(s + 8 * e) * RS + d]);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = s + 8 * e;
+                const float bj = L.B[j];
+                L.M1[i * MS + j] = bj * t1[e] + bj * expf(L.G[j]) * t2[e];
+            }
+        }
+        __syncthreads();   // dT complete; P1..P3 free
+        // Y = T^T dT into P3 (stride MS)
+        {
+            float y[4] = {};
+#pragma unroll 4
+            for (int m = 0; m < GC; ++m) {
+                const float tmi = L.M2[m * MS + i];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) y[e] = fmaf(tmi, L.M1[m * MS + s + 8 * e], y[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) L.P3[i * MS + s + 8 * e] = y[e];
+        }
+        __syncthreads();
+        // dN = Y T^T (strictly lower): dbeta, dG and E = dL/d(k^ k^T) from
+        // N = -beta (k^ k^T) * D.
+        {
+            float ev[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = s + 8 * e;
+                float dn = 0.0f;
+#pragma unroll 4
+                for (int m = 0; m < GC; ++m) dn = fmaf(L.P3[i * MS + m], L.M2[j * MS + m], dn);
+                ev[e] = 0.0f;
+                if (j < i) {
+                    const float dd = expf(gi - L.G[j]), kk = L.KK[i * MS + j];
+                    const float pa = dn * (-bi * kk * dd);
+                    dbp = fmaf(dn, -kk * dd, dbp);
+                    ev[e] = -dn * bi * dd;
+                    dgp += pa;
+                    L.M3[i * MS + j] += pa;
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) L.M1[i * MS + s + 8 * e] = ev[e];   // dT's readers passed the last barrier
+        }
+        __syncthreads();
+        // dk^ += (E + E^T) k^
+#pragma unroll 2
+        for (int j = 0; j < GC; ++j) {
+            const float ej = L.M1[i * MS + j] + L.M1[j * MS + i];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const f32x4 kj = *(const f32x4*)&L.Ks[j * RS + 32 * m + 4 * s];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) dka[4 * m + e] = fmaf(ej, kj[e], dka[4 * m + e]);
+            }
+        }
+        // The output state S_out = e^{G_L} S + (e^{G_L - G} k^)^T V': dk^ and dG.
+        {
+            const float* kr = dkto + chn * GC * GD + i * GD;
+            const float ed = expf(gl - gi);
+            float kt = 0.0f;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const f32x4 x = *(const f32x4*)(kr + 32 * m + 4 * s);
+                const f32x4 kv = *(const f32x4*)&L.Ks[i * RS + 32 * m + 4 * s];
+                kt += dot4(kv, x);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) dka[4 * m + e] = fmaf(ed, x[e], dka[4 * m + e]);
+            }
+            cp = ed * kt;
+            dgp -= cp;
+        }
+        dgp = row8_sum(dgp);
+        dbp = row8_sum(dbp);
+        cp = row8_sum(cp);
+        if (s == 0) {
+            L.Grow[i] = dgp;
+            L.Crow[i] = cp;
+            if (valid) dbeta[tok * p.hv + h] = dbp;
+        }
+        __syncthreads();
+        if (t < GC) {
+            float col = 0.0f, ctot = 0.0f;
+#pragma unroll 4
+            for (int r = 0; r < GC; ++r) {
+                col += L.M3[r * MS + t];
+                ctot += L.Crow[r];
+            }
+            float dG = L.Grow[t] - col;
+            if (t == GC - 1) dG += expf(gl) * sdot[chn] + ctot;
+            // dg_t = sum of dG_u over u >= t within the chunk (G is its cumulative sum)
+#pragma unroll
+            for (int o = 1; o < GC; o <<= 1) {
+                const float up = __shfl_down(dG, o, GC);
+                if (t + o < GC) dG += up;
+            }
+            if (t < len) dg[(int64_t)(start + t) * p.hv + h] = dG;
+        }
+    }
+
+    // Through q^ = scale q / sqrt(|q|^2 + eps) and k^ = k / sqrt(|k|^2 + eps).
+    if (valid) {
+        const TIn* qr = (const TIn*)p.q + tok * p.q_st + (int64_t)hk * p.q_sh;
+        const TIn* kr = (const TIn*)p.k + tok * p.k_st + (int64_t)hk * p.k_sh;
+        f32x4 qv[4], kv[4];
+        float sq = 0.0f, sk = 0.0f, dq_dot = 0.0f, dk_dot = 0.0f;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            qv[m] = load4(qr + 32 * m + 4 * s);
+            kv[m] = load4(kr + 32 * m + 4 * s);
+            sq += dot4(qv[m], qv[m]);
+            sk += dot4(kv[m], kv[m]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                dq_dot = fmaf(qv[m][e], dqa[4 * m + e], dq_dot);
+                dk_dot = fmaf(kv[m][e], dka[4 * m + e], dk_dot);
+            }
+        }
+        sq = row8_sum(sq);
+        sk = row8_sum(sk);
+        dq_dot = row8_sum(dq_dot);
+        dk_dot = row8_sum(dk_dot);
+        float aq = p.scale, bq = 0.0f, ak = 1.0f, bk = 0.0f;
+        if (p.l2) {
+            const float rq = 1.0f / sqrtf(sq + 1e-6f), rk = 1.0f / sqrtf(sk + 1e-6f);
+            aq = p.scale * rq;
+            bq = -p.scale * rq * rq * rq * dq_dot;
+            ak = rk;
+            bk = -rk * rk * rk * dk_dot;
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            f32x4 oq, ok;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                oq[e] = fmaf(aq, dqa[4 * m + e], bq * qv[m][e]);
+                ok[e] = fmaf(ak, dka[4 * m + e], bk * kv[m][e]);
+            }
+            store4(dq + (tok * p.hk + hk) * GD + 32 * m + 4 * s, oq);
+            store4(dk + (tok * p.hk + hk) * GD + 32 * m + 4 * s, ok);
+        }
+    }
+}
+
 }  // namespace
 
 size_t tt_gdn_ws_bytes_impl(int n_chunks, int n_heads_v) {
@@ -401,11 +1003,82 @@ int tt_gdn_fwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_level
         if (n <= 0) continue;
         if (d.dtype == TT_DTYPE_BF16)
             hipLaunchKernelGGL(gdn_scan_kernel<__bf16>, dim3(n, d.hv, NSL), dim3(GT), 0, s, d, b, ws,
-                               (__bf16*)out, states);
+                               (__bf16*)out, states, nullptr, nullptr);
         else
             hipLaunchKernelGGL(gdn_scan_kernel<float>, dim3(n, d.hv, NSL), dim3(GT), 0, s, d, b, ws,
-                               (float*)out, states);
+                               (float*)out, states, nullptr, nullptr);
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     return TT_OK;
+}
+
+// Backward workspace, floats, in order: prep terms [n_chunks, Hv][kWsChunk];
+// per (chunk, v head) S and dS [128 x 128], V', dV', X, dW, dK~ [32 x 128];
+// per (node, v head) the node's final state and its dS at entry [128 x 128];
+// <S, dS> per (chunk, v head).
+namespace {
+struct GdnBwdWs {
+    float *prep, *sin, *dso, *vp, *dvp, *x, *dw, *dkt, *nstate, *dsn, *sdot;
+};
+GdnBwdWs gdn_bwd_carve(float* base, size_t n_chunks, size_t n_nodes, size_t hv) {
+    const size_t ch = n_chunks * hv, nd = n_nodes * hv;
+    GdnBwdWs w;
+    float* q = base;
+    w.prep = q; q += ch * kWsChunk;
+    w.sin = q; q += ch * GD * GD;
+    w.dso = q; q += ch * GD * GD;
+    w.vp = q; q += ch * GC * GD;
+    w.dvp = q; q += ch * GC * GD;
+    w.x = q; q += ch * GC * GD;
+    w.dw = q; q += ch * GC * GD;
+    w.dkt = q; q += ch * GC * GD;
+    w.nstate = q; q += nd * GD * GD;
+    w.dsn = q; q += nd * GD * GD;
+    w.sdot = q; q += ch;
+    return w;
+}
+}  // namespace
+
+size_t tt_gdn_bwd_ws_bytes_impl(int n_chunks, int n_nodes, int n_heads_v) {
+    const size_t ch = (size_t)n_chunks * n_heads_v, nd = (size_t)n_nodes * n_heads_v;
+    return (ch * (kWsChunk + 2 * GD * GD + 5 * GC * GD + 1) + nd * 2 * GD * GD) * sizeof(float);
+}
+
+template <typename TIn>
+static int gdn_bwd_run(const GdnDev& d, const int32_t* level_offsets, int n_levels, const TIn* d_o, int64_t do_st,
+                       int64_t do_sh, TIn* dq, TIn* dk, TIn* dv, float* dg, float* dbeta, float* ws, hipStream_t s) {
+    const GdnBwdWs w = gdn_bwd_carve(ws, d.n_chunks, d.n_nodes, d.hv);
+    hipLaunchKernelGGL(gdn_prep_kernel<TIn>, dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, w.prep);
+    if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+    for (int l = 0; l < n_levels; ++l) {
+        const int b = level_offsets[l], n = level_offsets[l + 1] - b;
+        if (n <= 0) continue;
+        hipLaunchKernelGGL(gdn_scan_kernel<TIn>, dim3(n, d.hv, NSL), dim3(GT), 0, s, d, b, w.prep, (TIn*)nullptr,
+                           w.nstate, w.sin, w.vp);
+        if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+    }
+    for (int l = n_levels - 1; l >= 0; --l) {
+        const int b = level_offsets[l], n = level_offsets[l + 1] - b;
+        if (n <= 0) continue;
+        hipLaunchKernelGGL(gdn_rscan_kernel<TIn>, dim3(n, d.hv, NSL), dim3(GT), 0, s, d, b, w.prep, d_o, do_st,
+                           do_sh, w.dso, w.dvp, w.dsn);
+        if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+    }
+    hipLaunchKernelGGL(gdn_bwd_state_kernel<TIn>, dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, d_o, do_st, do_sh,
+                       w.sin, w.dso, w.vp, w.dvp, w.x, w.dw, w.dkt, w.sdot);
+    if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+    hipLaunchKernelGGL(gdn_bwd_chunk_kernel<TIn>, dim3(d.n_chunks, d.hk), dim3(GT), 0, s, d, d_o, do_st, do_sh,
+                       w.prep, w.vp, w.dvp, w.x, w.dw, w.dkt, w.sdot, dq, dk, dv, dg, dbeta);
+    if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+    return TT_OK;
+}
+
+int tt_gdn_bwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, const void* d_o, int64_t do_st,
+                      int64_t do_sh, void* dq, void* dk, void* dv, float* dg, float* dbeta, float* ws,
+                      hipStream_t s) {
+    if (d.dtype == TT_DTYPE_BF16)
+        return gdn_bwd_run<__bf16>(d, level_offsets, n_levels, (const __bf16*)d_o, do_st, do_sh, (__bf16*)dq,
+                                   (__bf16*)dk, (__bf16*)dv, dg, dbeta, ws, s);
+    return gdn_bwd_run<float>(d, level_offsets, n_levels, (const float*)d_o, do_st, do_sh, (float*)dq, (float*)dk,
+                              (float*)dv, dg, dbeta, ws, s);
 }

@@ -55,6 +55,8 @@ struct GdnDev {
     const int32_t* level_nodes;            // nodes grouped by tree depth
     const int32_t* node_chunk0;            // first chunk of each node
     const int32_t* chunk_node;             // node of each chunk
+    const int32_t* child_off;              // children of node i: child[child_off[i] .. child_off[i+1]) (backward)
+    const int32_t* child;
     int dtype, n_tokens, n_nodes, n_chunks, hk, hv, rep, l2;
     float scale;
 };
@@ -62,6 +64,10 @@ struct GdnDev {
 size_t tt_gdn_ws_bytes_impl(int n_chunks, int n_heads_v);
 int tt_gdn_fwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, void* out, float* states,
                       float* ws, hipStream_t s);
+size_t tt_gdn_bwd_ws_bytes_impl(int n_chunks, int n_nodes, int n_heads_v);
+int tt_gdn_bwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, const void* d_o, int64_t do_st,
+                      int64_t do_sh, void* dq, void* dk, void* dv, float* dg, float* dbeta, float* ws,
+                      hipStream_t s);
 
 size_t tt_meta_ws_bytes_impl(int n);
 int tt_meta_build_impl(const int32_t* len, const int32_t* par, int n, int T, int pos_offset, int32_t* start,

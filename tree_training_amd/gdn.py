@@ -61,6 +61,14 @@ class GdnTree:
             offs.append(offs[-1] + len(lv))
         self.n_levels = len(levels)
         self.level_offsets = (ctypes.c_int32 * len(offs))(*offs)
+        kids: List[List[int]] = [[] for _ in range(n)]
+        for i, par in enumerate(self.parent):
+            if par >= 0:
+                kids[par].append(i)
+        child_off = [0]
+        for ks in kids:
+            child_off.append(child_off[-1] + len(ks))
+        child = [c for ks in kids for c in ks] or [0]
         chunk0, chunk_node = [], []
         for i, L in enumerate(self.node_len):
             chunk0.append(len(chunk_node))
@@ -74,6 +82,8 @@ class GdnTree:
         self.d_levels = torch.tensor(order, **i32)
         self.d_chunk0 = torch.tensor(chunk0, **i32)
         self.d_chunk_node = torch.tensor(chunk_node, **i32)
+        self.d_child_off = torch.tensor(child_off, **i32)
+        self.d_child = torch.tensor(child, **i32)
         self.device = dev
 
     @classmethod
@@ -113,10 +123,7 @@ def _tok_vec(x: torch.Tensor, name: str) -> torch.Tensor:
     return x
 
 
-def gdn_tree_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
-                     tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True):
-    """o [T, Hv, 128] (dtype of v) and node_states [n_nodes, Hv, 128, 128]
-    (float32; the state after each node)."""
+def _problem(q, k, v, g, beta, tree: GdnTree, scale, l2norm):
     q, k, v = _tok_heads(q, "q"), _tok_heads(k, "k"), _tok_heads(v, "v")
     g, beta = _tok_vec(g, "g"), _tok_vec(beta, "beta")
     T, Hk, _ = q.shape
@@ -127,9 +134,6 @@ def gdn_tree_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch
         raise ValueError(f"{T} tokens but the tree holds {tree.n_tokens}")
     if v.dtype not in (torch.bfloat16, torch.float32) or q.dtype != v.dtype or k.dtype != v.dtype:
         raise ValueError("q, k, v must share dtype bfloat16 or float32")
-    dev = require_device(q.device)
-    o = torch.empty((T, Hv, HEAD_DIM), dtype=v.dtype, device=dev)
-    states = torch.empty((tree.n_nodes, Hv, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=dev)
     p = _lib.TTGdnProblem(
         dtype=_lib.TT_DTYPE_BF16 if v.dtype == torch.bfloat16 else _lib.TT_DTYPE_F32,
         n_tokens=T, n_nodes=tree.n_nodes, n_heads_k=Hk, n_heads_v=Hv, head_dim=HEAD_DIM,
@@ -140,7 +144,20 @@ def gdn_tree_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch
         g=g.data_ptr(), g_stride_tok=g.stride(0), beta=beta.data_ptr(), beta_stride_tok=beta.stride(0),
         node_start=_ptr(tree.d_start), node_len=_ptr(tree.d_len), node_parent=_ptr(tree.d_parent),
         level_nodes=_ptr(tree.d_levels), level_offsets=tree.level_offsets, n_levels=tree.n_levels,
-        n_chunks=tree.n_chunks, node_chunk0=_ptr(tree.d_chunk0), chunk_node=_ptr(tree.d_chunk_node))
+        n_chunks=tree.n_chunks, node_chunk0=_ptr(tree.d_chunk0), chunk_node=_ptr(tree.d_chunk_node),
+        node_child_off=_ptr(tree.d_child_off), node_child=_ptr(tree.d_child))
+    return p, (q, k, v, g, beta)
+
+
+def gdn_tree_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
+                     tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True):
+    """o [T, Hv, 128] (dtype of v) and node_states [n_nodes, Hv, 128, 128]
+    (float32; the state after each node)."""
+    p, (q, k, v, g, beta) = _problem(q, k, v, g, beta, tree, scale, l2norm)
+    T, Hv = v.shape[0], v.shape[1]
+    dev = require_device(q.device)
+    o = torch.empty((T, Hv, HEAD_DIM), dtype=v.dtype, device=dev)
+    states = torch.empty((tree.n_nodes, Hv, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=dev)
     lib = _lib.lib()
     ws_bytes = lib.tt_gdn_workspace_bytes(ctypes.byref(p))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
@@ -149,14 +166,65 @@ def gdn_tree_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch
     return o, states
 
 
+def gdn_tree_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
+                      d_o: torch.Tensor, tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True):
+    """Gradients of sum(o * d_o) for ``gdn_tree_forward``'s o: dq, dk [T, Hk,
+    128] and dv [T, Hv, 128] in the dtype of v, dg and dbeta [T, Hv] float32.
+    Recomputes the forward internally (tt_gdn_tree_bwd)."""
+    p, (q, k, v, g, beta) = _problem(q, k, v, g, beta, tree, scale, l2norm)
+    d_o = _tok_heads(d_o, "d_o").to(v.dtype)
+    T, Hk, Hv = q.shape[0], q.shape[1], v.shape[1]
+    if d_o.shape != v.shape:
+        raise ValueError(f"d_o: expected {tuple(v.shape)}, got {tuple(d_o.shape)}")
+    dev = require_device(q.device)
+    dq = torch.empty((T, Hk, HEAD_DIM), dtype=v.dtype, device=dev)
+    dk = torch.empty_like(dq)
+    dv = torch.empty((T, Hv, HEAD_DIM), dtype=v.dtype, device=dev)
+    dg = torch.empty((T, Hv), dtype=torch.float32, device=dev)
+    dbeta = torch.empty_like(dg)
+    lib = _lib.lib()
+    ws_bytes = lib.tt_gdn_bwd_workspace_bytes(ctypes.byref(p))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    _lib.check(lib.tt_gdn_tree_bwd(ctypes.byref(p), _lib.TTTensor(d_o.data_ptr(), d_o.stride(0), d_o.stride(1)),
+                                   _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(dbeta), _ptr(ws), ws_bytes,
+                                   _stream(dev)), "tt_gdn_tree_bwd")
+    return dq, dk, dv, dg, dbeta
+
+
+class GdnTreeFunction(torch.autograd.Function):
+    """Differentiable tree GDN: forward ``tt_gdn_tree_fwd``, backward
+    ``tt_gdn_tree_bwd`` (the node states are returned without a gradient)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, tree, scale, l2norm):
+        o, states = gdn_tree_forward(q, k, v, g, beta, tree, scale, l2norm)
+        ctx.save_for_backward(q, k, v, g, beta)
+        ctx.tree, ctx.scale, ctx.l2norm = tree, scale, l2norm
+        ctx.mark_non_differentiable(states)
+        return o, states
+
+    @staticmethod
+    def backward(ctx, d_o, _d_states):
+        q, k, v, g, beta = ctx.saved_tensors
+        dq, dk, dv, dg, dbeta = gdn_tree_backward(q, k, v, g, beta, d_o, ctx.tree, ctx.scale, ctx.l2norm)
+        return (dq.reshape(q.shape).to(q.dtype), dk.reshape(k.shape).to(k.dtype), dv.reshape(v.shape).to(v.dtype),
+                dg.reshape(g.shape).to(g.dtype), dbeta.reshape(beta.shape).to(beta.dtype), None, None, None)
+
+
+def gdn_tree(q, k, v, g, beta, tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True):
+    """Autograd-aware ``gdn_tree_forward``: (o, node_states)."""
+    return GdnTreeFunction.apply(q, k, v, g, beta, tree, scale, l2norm)
+
+
 def torch_chunk_gated_delta_rule_tree_varlen(query, key, value, g, beta, chunk_boundaries, chunk_parent_map,
                                              initial_state=None, output_final_state=False,
                                              use_qk_l2norm_in_kernel=False):
-    """Signature of tree_dfs_ssm.py:38-46 (no initial state; forward only).
-    Returns (core_out [1, T, Hv, 128], None or the last node's state)."""
+    """Signature of tree_dfs_ssm.py:38-46 (no initial state), differentiable in
+    q, k, v, g and beta. Returns (core_out [1, T, Hv, 128], None or the last
+    node's state)."""
     if initial_state is not None:
         raise NotImplementedError("initial_state is not supported (the reference drivers pass None)")
     tree = GdnTree.from_boundaries(chunk_boundaries, chunk_parent_map, query.device)
-    o, states = gdn_tree_forward(query, key, value, g, beta, tree, l2norm=use_qk_l2norm_in_kernel)
+    o, states = gdn_tree(query, key, value, g, beta, tree, l2norm=use_qk_l2norm_in_kernel)
     last = states[-1][None] if output_final_state else None
     return o[None], last
