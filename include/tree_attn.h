@@ -217,6 +217,40 @@ size_t tt_gdn_bwd_workspace_bytes(const tt_gdn_problem* p);
 int tt_gdn_tree_bwd(const tt_gdn_problem* p, tt_tensor d_o, void* dq, void* dk, void* dv, float* dg, float* dbeta,
                     void* ws, size_t ws_bytes, void* stream);
 
+/* ---- tree-correct short convolution --------------------------------------
+ * Replaces _tree_correct_conv_varlen (tree_dfs_ssm.py:284-346; twin
+ * dfs_tree_forward.py:191-246): depthwise causal conv of kernel size K + SiLU
+ * over the packed tree, where each node's window reaches into its ancestors'
+ * last K-1 inputs (zeros before a root) instead of the DFS neighbours:
+ *   y[t][c] = silu(bias[c] + sum_i weight[c][i] * x[prev^(K-1-i)(t)][c]),
+ * with tok_prev[t] = t - 1 inside a node, the parent's last token for a node's
+ * first token, -1 for a root's first token. The reference's conv reads the
+ * channel-major [B, C, T] layout; here rows are tokens (channels contiguous),
+ * the layout the q/k/v split after it reads. */
+typedef struct tt_conv_problem {
+    int32_t dtype;          /* TT_DTYPE_BF16 or TT_DTYPE_F32: x, weight, bias, y, dy, dx */
+    int32_t n_tokens;
+    int32_t n_channels;     /* multiple of 4 */
+    int32_t kernel_size;    /* 1..4 */
+    const void* x;          /* [T, C], element [t][c] at x + t*x_stride_tok + c */
+    int64_t x_stride_tok;   /* multiple of 4, >= n_channels */
+    const void* weight;     /* [C, K] contiguous (conv1d.weight [C, 1, K]) */
+    const void* bias;       /* [C] or NULL */
+    const int32_t* tok_prev;      /* device, [T] */
+    const int32_t* tok_next_off;  /* device, [T + 1]: successors of t (tokens u with tok_prev[u] = t) are */
+    const int32_t* tok_next;      /* tok_next[tok_next_off[t] .. tok_next_off[t+1]); backward only */
+} tt_conv_problem;
+
+/* y: [T, C] rows y + t*y_stride_tok (multiple of 4, >= n_channels). */
+int tt_tree_conv_fwd(const tt_conv_problem* p, void* y, int64_t y_stride_tok, void* stream);
+/* Gradients for dy [T, C] (rows dy + t*dy_stride_tok): dx [T, C] contiguous
+ * (problem dtype), dweight [C, K] and dbias [C] float32 (dbias may be NULL).
+ * Deterministic: the weight gradient is summed in a fixed order, dx gathers
+ * over the successor lists. Workspace: tt_tree_conv_bwd_workspace_bytes. */
+size_t tt_tree_conv_bwd_workspace_bytes(const tt_conv_problem* p);
+int tt_tree_conv_bwd(const tt_conv_problem* p, const void* dy, int64_t dy_stride_tok, void* dx, float* dweight,
+                     float* dbias, void* ws, size_t ws_bytes, void* stream);
+
 /* ---- device self-test ----------------------------------------------------
  * No counterpart in the reference. Runs one v_mfma_f32_32x32x16_bf16 with the
  * operand and accumulator lane layout the bf16 kernels assume:

@@ -186,7 +186,10 @@ def tree_conv(x, weight, bias, node_len, parent):
         if bias is not None:
             y += np.asarray(bias, np.float64)
         out[s0:s0 + L] = y / (1.0 + np.exp(-y))
-        ctx[i] = ext[-(K - 1):]
+        # the last K-1 rows (the reference slices ext[-(K-1):], which for K = 1
+        # is the whole of ext: its kernel-size-1 case is not well formed, so the
+        # empty context is taken explicitly here)
+        ctx[i] = ext[len(ext) - (K - 1):]
     return out
 
 
@@ -228,3 +231,31 @@ def gdn_tree_torch(q, k, v, g, beta, node_len, parent, l2=True, eps=1e-6):
             outs.append(torch.einsum("hk,hkv->hv", q[t], S))
         finals[i] = S
     return torch.stack(outs, 0)
+
+
+def token_prev(node_len, parent):
+    """Path predecessor of every token: t - 1 inside a node, the parent's
+    last token for a node's first token, -1 before a root."""
+    starts = node_starts(node_len)
+    prev = np.arange(-1, int(sum(node_len)) - 1)
+    for i, p in enumerate(parent):
+        prev[starts[i]] = starts[p] + node_len[p] - 1 if p >= 0 else -1
+    return prev
+
+
+def tree_conv_torch(x, weight, bias, node_len, parent):
+    """``tree_conv`` written over token predecessor chains in torch,
+    differentiable (the backward oracle): y[t] = silu(b + sum_i w[:, i] *
+    x[prev^(K-1-i)(t)]). x [T, C], weight [C, K], bias [C] or None."""
+    import torch
+    T, C = x.shape
+    K = weight.shape[1]
+    prev = torch.from_numpy(token_prev(node_len, parent))
+    idx = torch.arange(T)
+    acc = bias.expand(T, C) if bias is not None else torch.zeros(T, C, dtype=x.dtype)
+    xz = torch.cat([x, torch.zeros(1, C, dtype=x.dtype)], 0)      # row T is the zero row
+    for m in range(K):
+        sel = torch.where(idx >= 0, idx, torch.full_like(idx, T))
+        acc = acc + weight[:, K - 1 - m] * xz[sel]
+        idx = torch.where(idx >= 0, prev[idx.clamp(min=0)], idx)
+    return acc * torch.sigmoid(acc)

@@ -163,3 +163,40 @@ def test_gdn_bwd_validation():
     assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, V, V, V, ctypes.c_void_p(18), V, V, want, None) == _lib.TT_E_ARG
     assert lib.tt_gdn_tree_bwd(ctypes.byref(_gdn_problem(head_dim=64, node_child_off=16, node_child=16)), DO,
                                *args(want)) == _lib.TT_E_UNSUPPORTED
+
+
+def _conv_problem(**kw):
+    p = _lib.TTConvProblem(dtype=_lib.TT_DTYPE_BF16, n_tokens=10, n_channels=8, kernel_size=4, x=16,
+                           x_stride_tok=8, weight=16, bias=None, tok_prev=16, tok_next_off=16, tok_next=16)
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("kernel_size", 5, _lib.TT_E_UNSUPPORTED),
+    ("kernel_size", 0, _lib.TT_E_UNSUPPORTED),
+    ("dtype", 9, _lib.TT_E_UNSUPPORTED),
+    ("n_channels", 6, _lib.TT_E_ARG),            # not a multiple of 4
+    ("x_stride_tok", 4, _lib.TT_E_ARG),          # rows overlap
+    ("x", 12, _lib.TT_E_ARG),                    # misaligned for bf16x4
+    ("tok_prev", None, _lib.TT_E_ARG),
+])
+def test_conv_validation(field, value, code):
+    lib = _lib.lib()
+    p = _conv_problem(**{field: value})
+    assert lib.tt_tree_conv_fwd(ctypes.byref(p), ctypes.c_void_p(16), 8, None) == code
+
+
+def test_conv_bwd_validation():
+    lib = _lib.lib()
+    V = ctypes.c_void_p(16)
+    p = _conv_problem()
+    # gp [T, C] + one partial block (K + 1 slots of C) in float32
+    want = (10 * 8 + 1 * 5 * 8) * 4
+    assert lib.tt_tree_conv_bwd_workspace_bytes(ctypes.byref(p)) == want
+    assert lib.tt_tree_conv_bwd(ctypes.byref(p), V, 8, V, V, None, V, want - 4, None) == _lib.TT_E_WORKSPACE
+    assert lib.tt_tree_conv_bwd(ctypes.byref(_conv_problem(tok_next=None)), V, 8, V, V, None, V, want,
+                                None) == _lib.TT_E_ARG
+    assert lib.tt_tree_conv_bwd(ctypes.byref(p), V, 4, V, V, None, V, want, None) == _lib.TT_E_ARG
+    assert lib.tt_tree_conv_fwd(ctypes.byref(p), ctypes.c_void_p(20), 8, None) == _lib.TT_E_ARG

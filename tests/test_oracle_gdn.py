@@ -173,3 +173,25 @@ def test_torch_oracle_forward_matches_numpy_and_grads_match_finite_differences()
             fm = (gdn.gdn_tree(*args_m, lens, par, mode="exact")[0] * w.numpy()).sum()
             fd = (fp - fm) / (2 * h)
             assert abs(fd - float(gr[idx])) < 1e-6 * max(1.0, abs(fd))
+
+
+@pytest.mark.parametrize("seed", [2, 5])
+def test_tree_conv_torch_matches_numpy_and_grads_match_finite_differences(seed):
+    lens, par = random_forest(seed, node_len=(1, 4))
+    T, C, K = sum(lens), 3, 4
+    rng = np.random.default_rng(seed)
+    x, w, b = rng.standard_normal((T, C)), rng.standard_normal((C, K)), rng.standard_normal(C)
+    tt = [torch.from_numpy(a).requires_grad_(True) for a in (x, w, b)]
+    y = gdn.tree_conv_torch(*tt, lens, par)
+    assert np.abs(y.detach().numpy() - gdn.tree_conv(x, w, b, lens, par)).max() < 1e-12
+    dy = rng.standard_normal((T, C))
+    grads = torch.autograd.grad((y * torch.from_numpy(dy)).sum(), tt)
+    for a, gr in zip((x, w, b), grads):
+        for _ in range(4):
+            i = tuple(int(rng.integers(0, s)) for s in a.shape)
+            ap, am = a.copy(), a.copy()
+            ap[i] += 1e-6
+            am[i] -= 1e-6
+            f = lambda arr: (gdn.tree_conv(*[arr if z is a else z for z in (x, w, b)], lens, par) * dy).sum()
+            fd = (f(ap) - f(am)) / 2e-6
+            assert abs(fd - float(gr[i])) < 1e-6 * max(1.0, abs(fd))

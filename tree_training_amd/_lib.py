@@ -35,7 +35,8 @@ EXPORTS = (
     "tt_abi_version", "tt_strerror", "tt_meta_workspace_bytes", "tt_meta_build", "tt_keys_build",
     "tt_meta_dense_mask", "tt_plan_bytes", "tt_plan_build", "tt_attn_fwd",
     "tt_attn_bwd_workspace_bytes", "tt_attn_bwd", "tt_gdn_workspace_bytes", "tt_gdn_tree_fwd",
-    "tt_gdn_bwd_workspace_bytes", "tt_gdn_tree_bwd",
+    "tt_gdn_bwd_workspace_bytes", "tt_gdn_tree_bwd", "tt_tree_conv_fwd", "tt_tree_conv_bwd_workspace_bytes",
+    "tt_tree_conv_bwd",
     "tt_selftest_mfma32",
 )
 
@@ -71,6 +72,15 @@ class TTGdnProblem(ctypes.Structure):
     ]
 
 
+class TTConvProblem(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("n_tokens", ctypes.c_int32), ("n_channels", ctypes.c_int32),
+        ("kernel_size", ctypes.c_int32), ("x", ctypes.c_void_p), ("x_stride_tok", ctypes.c_int64),
+        ("weight", ctypes.c_void_p), ("bias", ctypes.c_void_p), ("tok_prev", ctypes.c_void_p),
+        ("tok_next_off", ctypes.c_void_p), ("tok_next", ctypes.c_void_p),
+    ]
+
+
 class TreeAttnError(RuntimeError):
     pass
 
@@ -97,6 +107,10 @@ def _declare(lib):
         "tt_gdn_tree_fwd": (ctypes.c_int, [ctypes.POINTER(TTGdnProblem), P, P, P, SZ, VP]),
         "tt_gdn_bwd_workspace_bytes": (SZ, [ctypes.POINTER(TTGdnProblem)]),
         "tt_gdn_tree_bwd": (ctypes.c_int, [ctypes.POINTER(TTGdnProblem), TTTensor, P, P, P, P, P, P, SZ, VP]),
+        "tt_tree_conv_fwd": (ctypes.c_int, [ctypes.POINTER(TTConvProblem), P, ctypes.c_int64, VP]),
+        "tt_tree_conv_bwd_workspace_bytes": (SZ, [ctypes.POINTER(TTConvProblem)]),
+        "tt_tree_conv_bwd": (ctypes.c_int, [ctypes.POINTER(TTConvProblem), P, ctypes.c_int64, P, P, P, P, SZ,
+                                            VP]),
         "tt_selftest_mfma32": (ctypes.c_int, [P, P, P, VP]),
     }
     for name, (res, args) in sig.items():

@@ -289,6 +289,62 @@ int tt_gdn_tree_bwd(const tt_gdn_problem* p, tt_tensor d_o, void* dq, void* dk, 
                              dv, dg, dbeta, (float*)ws, (hipStream_t)stream);
 }
 
+}  // extern "C"
+
+static int conv_problem(const tt_conv_problem* p, ConvDev& d) {
+    if (!p) return TT_E_ARG;
+    if (p->dtype != TT_DTYPE_BF16 && p->dtype != TT_DTYPE_F32) return TT_E_UNSUPPORTED;
+    if (p->kernel_size < 1 || p->kernel_size > 4) return TT_E_UNSUPPORTED;
+    if (p->n_tokens < 1 || p->n_channels < 4 || (p->n_channels % 4)) return TT_E_ARG;
+    if (!p->x || !p->weight || !p->tok_prev) return TT_E_ARG;
+    if (p->x_stride_tok < p->n_channels || (p->x_stride_tok % 4)) return TT_E_ARG;
+    const size_t ea = p->dtype == TT_DTYPE_BF16 ? 8 : 16;
+    if (!aligned(p->x, ea) || !aligned(p->weight, p->dtype == TT_DTYPE_BF16 ? 2 : 4)) return TT_E_ARG;
+    if (p->bias && !aligned(p->bias, p->dtype == TT_DTYPE_BF16 ? 2 : 4)) return TT_E_ARG;
+    d.x = p->x; d.x_st = p->x_stride_tok;
+    d.weight = p->weight;
+    d.bias = p->bias;
+    d.prev = p->tok_prev;
+    d.next_off = p->tok_next_off;
+    d.next = p->tok_next;
+    d.dtype = p->dtype;
+    d.n_tokens = p->n_tokens;
+    d.n_ch = p->n_channels;
+    d.k = p->kernel_size;
+    return TT_OK;
+}
+
+extern "C" {
+
+int tt_tree_conv_fwd(const tt_conv_problem* p, void* y, int64_t y_stride_tok, void* stream) {
+    ConvDev d;
+    const int rc = conv_problem(p, d);
+    if (rc != TT_OK) return rc;
+    if (!y || y_stride_tok < p->n_channels || (y_stride_tok % 4) ||
+        !aligned(y, p->dtype == TT_DTYPE_BF16 ? 8 : 16))
+        return TT_E_ARG;
+    return tt_conv_fwd_launch(d, y, y_stride_tok, (hipStream_t)stream);
+}
+
+size_t tt_tree_conv_bwd_workspace_bytes(const tt_conv_problem* p) {
+    if (!p || p->n_tokens < 1 || p->n_channels < 1 || p->kernel_size < 1 || p->kernel_size > 4) return 0;
+    return tt_conv_bwd_ws_bytes_impl(p->n_tokens, p->n_channels, p->kernel_size);
+}
+
+int tt_tree_conv_bwd(const tt_conv_problem* p, const void* dy, int64_t dy_stride_tok, void* dx, float* dweight,
+                     float* dbias, void* ws, size_t ws_bytes, void* stream) {
+    ConvDev d;
+    const int rc = conv_problem(p, d);
+    if (rc != TT_OK) return rc;
+    if (!p->tok_next_off || !p->tok_next || !dy || !dx || !dweight || !ws) return TT_E_ARG;
+    const size_t ea = p->dtype == TT_DTYPE_BF16 ? 8 : 16;
+    if (dy_stride_tok < p->n_channels || (dy_stride_tok % 4) || !aligned(dy, ea) || !aligned(dx, ea) ||
+        !aligned(ws, 16) || !aligned(dweight, 4) || (dbias && !aligned(dbias, 4)))
+        return TT_E_ARG;
+    if (ws_bytes < tt_conv_bwd_ws_bytes_impl(p->n_tokens, p->n_channels, p->kernel_size)) return TT_E_WORKSPACE;
+    return tt_conv_bwd_launch(d, dy, dy_stride_tok, dx, dweight, dbias, (float*)ws, (hipStream_t)stream);
+}
+
 int tt_selftest_mfma32(const void* a, const void* b, float* d, void* stream) {
     if (!a || !b || !d || !aligned(a, 2) || !aligned(b, 2) || !aligned(d, 4)) return TT_E_ARG;
     return tt_selftest_mfma_launch(a, b, d, (hipStream_t)stream);

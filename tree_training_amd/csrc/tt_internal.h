@@ -61,6 +61,22 @@ struct GdnDev {
     float scale;
 };
 
+// Device-side view of a tt_conv_problem.
+struct ConvDev {
+    const void* x; int64_t x_st;           // [T, C] rows, channels contiguous
+    const void* weight;                    // [C, K]
+    const void* bias;                      // [C] or null
+    const int32_t* prev;                   // [T] path predecessor (-1: none)
+    const int32_t* next_off;               // [T + 1] successor lists (backward)
+    const int32_t* next;
+    int dtype, n_tokens, n_ch, k;
+};
+
+size_t tt_conv_bwd_ws_bytes_impl(int n_tokens, int n_ch, int k);
+int tt_conv_fwd_launch(const ConvDev& d, void* y, int64_t y_st, hipStream_t s);
+int tt_conv_bwd_launch(const ConvDev& d, const void* dy, int64_t dy_st, void* dx, float* dw, float* db, float* ws,
+                       hipStream_t s);
+
 size_t tt_gdn_ws_bytes_impl(int n_chunks, int n_heads_v);
 int tt_gdn_fwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, void* out, float* states,
                       float* ws, hipStream_t s);

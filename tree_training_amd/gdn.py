@@ -19,6 +19,7 @@ from __future__ import annotations
 import ctypes
 from typing import List, Optional, Sequence, Tuple
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -85,6 +86,25 @@ class GdnTree:
         self.d_child_off = torch.tensor(child_off, **i32)
         self.d_child = torch.tensor(child, **i32)
         self.device = dev
+
+    def token_links(self):
+        """Device (tok_prev [T], tok_next_off [T + 1], tok_next) of the tree's
+        tokens: the path predecessor of each token and the successor lists
+        (built once, on first use)."""
+        if getattr(self, "_links", None) is None:
+            T = self.n_tokens
+            prev = np.arange(-1, T - 1, dtype=np.int64)
+            for i, (st, par) in enumerate(zip(self.node_start, self.parent)):
+                prev[st] = self.node_start[par] + self.node_len[par] - 1 if par >= 0 else -1
+            has = prev >= 0
+            order = np.argsort(prev[has], kind="stable")
+            nxt = np.arange(T, dtype=np.int64)[has][order]
+            off = np.zeros(T + 1, dtype=np.int64)
+            np.cumsum(np.bincount(prev[has], minlength=T), out=off[1:])
+            i32 = dict(dtype=torch.int32, device=self.device)
+            self._links = (torch.tensor(prev, **i32), torch.tensor(off, **i32),
+                           torch.tensor(nxt if len(nxt) else np.zeros(1, np.int64), **i32))
+        return self._links
 
     @classmethod
     def from_boundaries(cls, chunk_boundaries: Sequence[Tuple[int, int]], chunk_parent_map: Sequence[int],
