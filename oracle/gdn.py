@@ -259,3 +259,35 @@ def tree_conv_torch(x, weight, bias, node_len, parent):
         acc = acc + weight[:, K - 1 - m] * xz[sel]
         idx = torch.where(idx >= 0, prev[idx.clamp(min=0)], idx)
     return acc * torch.sigmoid(acc)
+
+
+def gdn_layer_torch(ssm, hidden, node_len, parent):
+    """The tree-aware GatedDeltaNet layer in float64 torch, differentiable:
+    projections, ``tree_conv_torch``, gates, ``gdn_tree_torch`` (exact rule,
+    q/k heads shared by Hv/Hk v heads), gated RMSNorm and out_proj, with the
+    parameters of ``ssm`` (a transformers Qwen3_5MoeGatedDeltaNet, whose
+    attributes this reads: the layer of R/tree_dfs_ssm.py:355-423 and
+    R/dfs_tree_forward.py:360-435). hidden [T, d] float64; the module's
+    parameters are used in float64. Returns [T, d]."""
+    import torch
+    P = {n: p.double() for n, p in ssm.named_parameters()}
+    lin = lambda x, n: x @ P[n + ".weight"].T
+    mixed = lin(hidden, "in_proj_qkv")
+    z = lin(hidden, "in_proj_z")
+    b = lin(hidden, "in_proj_b")
+    a = lin(hidden, "in_proj_a")
+    cb = P.get("conv1d.bias")
+    mixed = tree_conv_torch(mixed, P["conv1d.weight"][:, 0, :], cb, node_len, parent)
+    T = hidden.shape[0]
+    q, k, v = torch.split(mixed, [ssm.key_dim, ssm.key_dim, ssm.value_dim], dim=-1)
+    q = q.reshape(T, -1, ssm.head_k_dim)
+    k = k.reshape(T, -1, ssm.head_k_dim)
+    v = v.reshape(T, -1, ssm.head_v_dim)
+    beta = torch.sigmoid(b)
+    g = -torch.exp(P["A_log"]) * torch.nn.functional.softplus(a + P["dt_bias"])
+    o = gdn_tree_torch(q, k, v, g, beta, node_len, parent)
+    o = o.reshape(-1, ssm.head_v_dim)
+    zz = z.reshape(-1, ssm.head_v_dim)
+    o = o * torch.rsqrt(o.pow(2).mean(-1, keepdim=True) + ssm.norm.variance_epsilon)
+    o = P["norm.weight"] * o * (zz * torch.sigmoid(zz))
+    return lin(o.reshape(T, -1), "out_proj")

@@ -1,0 +1,32 @@
+"""A small transformers Qwen3.5-MoE GatedDeltaNet layer (head dims 128, the
+size the kernels are built for) for the layer-patch tests."""
+import torch
+
+from transformers.models.qwen3_5_moe import configuration_qwen3_5_moe as qcfg
+from transformers.models.qwen3_5_moe import modeling_qwen3_5_moe as qmod
+
+
+def small_gdn_layer(seed=0, hidden=256, hv=4, hk=2, k=4):
+    cfg = qcfg.Qwen3_5MoeTextConfig(
+        hidden_size=hidden, linear_num_value_heads=hv, linear_num_key_heads=hk, linear_key_head_dim=128,
+        linear_value_head_dim=128, linear_conv_kernel_dim=k, num_hidden_layers=2,
+        layer_types=["linear_attention", "full_attention"], num_attention_heads=4, num_key_value_heads=2,
+        head_dim=128, vocab_size=64, num_experts=4, num_experts_per_tok=2, moe_intermediate_size=64,
+        shared_expert_intermediate_size=64)
+    torch.manual_seed(seed)
+    layer = qmod.Qwen3_5MoeGatedDeltaNet(cfg, 0)
+    with torch.no_grad():                      # non-trivial norm weight and decay
+        layer.norm.weight.uniform_(0.5, 1.5)
+        layer.dt_bias.uniform_(-1.0, 1.0)
+    return layer
+
+
+class FakeModel(torch.nn.Module):
+    """model.model.layers[i].linear_attn, the structure the patch walks."""
+
+    def __init__(self, ssm):
+        super().__init__()
+        layer = torch.nn.Module()
+        layer.linear_attn = ssm
+        self.model = torch.nn.Module()
+        self.model.layers = torch.nn.ModuleList([layer, torch.nn.Module()])

@@ -1,0 +1,58 @@
+"""GPU parity of the patched GatedDeltaNet layer (tree conv + tree scan
+kernels, torch projections and norm) against the float64 layer oracle
+(oracle/gdn.py ``gdn_layer_torch``, pinned to transformers' module per path
+in tests/test_gdn_layer.py): forward output and the gradients with respect to
+the input and every parameter.
+
+Bars: float32 max_rel < 1e-5 per tensor; bf16 < 2e-2.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gdn as ogdn
+from tree_training_amd import gdn_layer
+from tree_training_amd.workloads import random_forest
+
+pytestmark = pytest.mark.gpu
+pytest.importorskip("transformers.models.qwen3_5_moe.modeling_qwen3_5_moe")
+from tests.gdn_layer_util import small_gdn_layer  # noqa: E402
+
+DEV = torch.device("cuda", 0)
+
+
+def _rel(a, b):
+    return float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_patched_layer_matches_oracle(dtype, tol):
+    lens, par = random_forest(5, node_len=(1, 45))
+    T = sum(lens)
+    starts = np.concatenate([[0], np.cumsum(lens)[:-1]])
+    bounds = [(int(s), int(s + n)) for s, n in zip(starts, lens)]
+    ssm = small_gdn_layer(2)
+    ref_ssm = small_gdn_layer(2).double()
+    ssm = ssm.to(DEV, dtype)
+    h64 = torch.randn(T, 256, dtype=torch.float64, generator=torch.Generator().manual_seed(4))
+    if dtype == torch.bfloat16:      # the oracle sees the same rounded weights and input
+        with torch.no_grad():
+            for p_ref, p in zip(ref_ssm.parameters(), ssm.parameters()):
+                p_ref.copy_(p.double().cpu())
+        h64 = h64.bfloat16().double()
+    dy64 = torch.randn(T, 256, dtype=torch.float64, generator=torch.Generator().manual_seed(5))
+    print(f"gdn layer {dtype}: T={T} nodes={len(lens)}", flush=True)
+
+    fwd = gdn_layer._make_dfs_ssm_forward(ssm, bounds, par)
+    h = h64.to(DEV, dtype).requires_grad_(True)
+    y = fwd(h[None])[0]
+    y.backward(dy64.to(DEV, dtype))
+
+    hr = h64.clone().requires_grad_(True)
+    yr = ogdn.gdn_layer_torch(ref_ssm, hr, lens, par)
+    yr.backward(dy64)
+
+    assert _rel(y.detach().double().cpu(), yr.detach()) < tol
+    assert _rel(h.grad.double().cpu(), hr.grad) < tol, "d hidden"
+    for (name, p), p_ref in zip(ssm.named_parameters(), ref_ssm.parameters()):
+        assert _rel(p.grad.double().cpu(), p_ref.grad) < tol, name

@@ -4,7 +4,9 @@
 DFS-packed forest and returns per-leaf logit views (dfs_tree_forward.py:513-576).
 Instead of a dense [1,1,N,N] additive mask the model runs with the
 ``"tree_hip"`` attention implementation: positions come straight from the GPU
-metadata kernel and every layer shares one tile plan.
+metadata kernel and every layer shares one tile plan. Gated-delta-rule layers
+of hybrid models are patched for the duration of the forward (tree conv + tree
+scan, ``gdn_layer._patch_ssm``), as the reference does (dfs_tree_forward.py:553-562).
 """
 from __future__ import annotations
 
@@ -60,7 +62,13 @@ def dfs_tree_forward(model, roots: List[TreeNode], dtype: Optional[torch.dtype] 
     """
     dev = next(model.parameters()).device
     info = build_dfs_tree_info(roots)
-    out = run_tree_model(model, info, dev)
+    # gated-delta-rule layers (hybrid models) run the tree-aware conv + scan
+    from .gdn_layer import _patch_ssm, _unpatch_ssm
+    saved = _patch_ssm(model, info.chunk_boundaries, info.chunk_parent_map)
+    try:
+        out = run_tree_model(model, info, dev)
+    finally:
+        _unpatch_ssm(saved)       # always restored, even if the forward raises
     logits = out.logits
     leaf_logits = [logits[:, s:e, :] for s, e in (info.chunk_boundaries[c] for c in info.leaf_chunk_ids)]
     return DFSTreeResult(leaf_logits=leaf_logits, leaf_nodes=info.leaf_nodes, info=info)
