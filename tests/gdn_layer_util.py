@@ -30,3 +30,24 @@ class FakeModel(torch.nn.Module):
         layer.linear_attn = ssm
         self.model = torch.nn.Module()
         self.model.layers = torch.nn.ModuleList([layer, torch.nn.Module()])
+
+
+def small_hybrid_model(seed=0):
+    """A two-layer Qwen3.5-MoE text model: one gated-delta-rule layer, one
+    full-attention layer (head_dim 128, GQA 4/2), vocabulary 64."""
+    cfg = qcfg.Qwen3_5MoeTextConfig(
+        hidden_size=256, linear_num_value_heads=4, linear_num_key_heads=2, linear_key_head_dim=128,
+        linear_value_head_dim=128, linear_conv_kernel_dim=4, num_hidden_layers=2,
+        layer_types=["linear_attention", "full_attention"], num_attention_heads=4, num_key_value_heads=2,
+        head_dim=128, vocab_size=64, num_experts=4, num_experts_per_tok=2, moe_intermediate_size=64,
+        shared_expert_intermediate_size=64)
+    cfg._attn_implementation = "eager"
+    cfg._experts_implementation = "eager"      # plain per-expert matmuls (any dtype, float64 included)
+    torch.manual_seed(seed)
+    model = qmod.Qwen3_5MoeForCausalLM(cfg)
+    with torch.no_grad():
+        for m in model.modules():
+            if isinstance(m, qmod.Qwen3_5MoeGatedDeltaNet):
+                m.norm.weight.uniform_(0.5, 1.5)
+                m.dt_bias.uniform_(-1.0, 1.0)
+    return model.eval()

@@ -41,7 +41,7 @@ class DFSTreeResult:
 
 
 def run_tree_model(model, info: DFSTreeInfo, dev, pos_offset: int = 0, cache=None, accumulators=None,
-                   past_bias: Optional[torch.Tensor] = None):
+                   past_bias: Optional[torch.Tensor] = None, linear_attention_patched: bool = False):
     """One model forward over a DFS-packed forest (or partition) with tree
     attention. Returns the model output."""
     meta = info.device_meta(dev, pos_offset)
@@ -49,7 +49,7 @@ def run_tree_model(model, info: DFSTreeInfo, dev, pos_offset: int = 0, cache=Non
     ids_t = torch.tensor([info.dfs_token_ids], device=dev)
     pos_t = meta.pos.long().unsqueeze(0)
     ctx = TreeAttnContext(plan=plan, cache=cache, accumulators=accumulators)
-    with tree_attention_mode(model):
+    with tree_attention_mode(model, linear_attention_patched):
         return model(input_ids=ids_t, attention_mask=None, position_ids=pos_t,
                      past_key_values=cache, use_cache=cache is not None, tree_ctx=ctx)
 
@@ -66,7 +66,7 @@ def dfs_tree_forward(model, roots: List[TreeNode], dtype: Optional[torch.dtype] 
     from .gdn_layer import _patch_ssm, _unpatch_ssm
     saved = _patch_ssm(model, info.chunk_boundaries, info.chunk_parent_map)
     try:
-        out = run_tree_model(model, info, dev)
+        out = run_tree_model(model, info, dev, linear_attention_patched=True)
     finally:
         _unpatch_ssm(saved)       # always restored, even if the forward raises
     logits = out.logits

@@ -70,12 +70,15 @@ def _has_linear_attention(model) -> bool:
 
 
 @contextlib.contextmanager
-def tree_attention_mode(model):
+def tree_attention_mode(model, linear_attention_patched: bool = False):
     """Switches every attention layer of ``model`` to the tree kernels for the
-    duration of the block."""
+    duration of the block. Gated-delta-rule (linear_attn) layers must have been
+    patched with the tree-aware forward (``gdn_layer._patch_ssm``, done by
+    dfs_tree_forward); the partitioned drivers do not carry their recurrent
+    state across partitions and refuse such models."""
     register()
-    if _has_linear_attention(model):
-        raise NotImplementedError("models with gated-delta-rule (linear_attn) layers are not supported yet")
+    if not linear_attention_patched and _has_linear_attention(model):
+        raise NotImplementedError("gated-delta-rule (linear_attn) layers are supported by dfs_tree_forward only")
     cfg = model.config
     saved = cfg._attn_implementation
     cfg._attn_implementation = ATTN_IMPL
