@@ -33,6 +33,7 @@ import time
 
 HQ, HKV, D = 32, 8, 128
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_FP32_TFS = 157.3        # MI355X fp32 (dense) TFLOP/s
 PEAK_HBM_GBS = 8000.0
 TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                "tree_attn_agent16k_hbm_traffic.md")
@@ -258,90 +259,124 @@ def main():
     print(json.dumps(line), flush=True)
 
 
+def gdn_useful_flops(n_chunk_heads, C=32, Dh=128):
+    """fp32 FLOPs of the chunked tree gated delta rule, forward + backward,
+    counted once (the backward's forward recompute excluded), per (chunk, v
+    head) pair, as multiply-adds x 2:
+      forward   3 C D^2 (W S, q S, the state update) + 5 C^2 D (q k^T, k k^T,
+                T (beta v), T (beta k), A V') + C^3 / 3 (the triangular inverse)
+      backward  6 C D^2 (A^T dO and K~ dS aside, the products with the states:
+                K~ dS, (e^G q)^T dO, W^T dV', dO S^T, dV' S^T, V' dS^T)
+                + 11 C^2 D + 2 C^3 (the chunk's 32 x 32 algebra)."""
+    fwd = 3 * C * Dh * Dh + 5 * C * C * Dh + C ** 3 / 3
+    bwd = 6 * C * Dh * Dh + 11 * C * C * Dh + 2 * C ** 3
+    return 2.0 * (fwd + bwd) * n_chunk_heads
+
+
 def run_gdn(args):
-    """Tree gated-delta-rule forward on the 16K agent tree (one GDN layer)."""
+    """One tree-aware GDN layer core on the 16K agent tree, forward + backward:
+    tree conv (8192 channels, width 4) + tree gated-delta-rule scan, through
+    the autograd Functions (the projections and the norm stay torch GEMMs and
+    are not timed)."""
     import torch
-    from tree_training_amd.gdn import GdnTree, gdn_tree_forward
+    from tree_training_amd.conv import tree_conv
+    from tree_training_amd.gdn import GdnTree, gdn_tree
     from tree_training_amd.workloads import agent_tree
-    HK, HV = 16, 32
+    HK, HV, K = 16, 32, 4
+    C = 2 * HK * D + HV * D
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     lens, par = agent_tree(0)
     T = sum(lens)
     gen = torch.Generator(device=dev).manual_seed(0)
     bf = torch.bfloat16
-    q = torch.randn(T, HK, D, device=dev, generator=gen, dtype=bf)
-    k = torch.randn(T, HK, D, device=dev, generator=gen, dtype=bf)
-    v = torch.randn(T, HV, D, device=dev, generator=gen, dtype=bf)
+    x = torch.randn(T, C, device=dev, generator=gen, dtype=bf).requires_grad_(True)   # raw qkv projections
+    w = (torch.randn(C, K, device=dev, generator=gen) * 0.5).to(bf).requires_grad_(True)
     a = torch.randn(T, HV, device=dev, generator=gen)
     b = torch.randn(T, HV, device=dev, generator=gen)
     A_log = torch.log(torch.rand(HV, device=dev, generator=gen) * 16.0 + 1e-3)
-    g = -A_log.exp() * torch.nn.functional.softplus(a + 1.0)   # dt_bias = 1
-    beta = b.sigmoid()
+    g = (-A_log.exp() * torch.nn.functional.softplus(a + 1.0)).requires_grad_(True)   # dt_bias = 1
+    beta = b.sigmoid().requires_grad_(True)
+    d_o = torch.randn(T, HV, D, device=dev, generator=gen, dtype=bf)
     tree = GdnTree(lens, par, dev)
+
+    def step():
+        y = tree_conv(x, w, None, tree)
+        q, k, v = torch.split(y, [HK * D, HK * D, HV * D], dim=-1)
+        o, _ = gdn_tree(q.view(T, HK, D), k.view(T, HK, D), v.view(T, HV, D), g, beta, tree, None, True)
+        o.backward(d_o)
+
     for _ in range(args.warmup):
-        gdn_tree_forward(q, k, v, g, beta, tree)
+        step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record(stream)
     for _ in range(args.steps):
-        gdn_tree_forward(q, k, v, g, beta, tree)
+        step()
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / args.steps
-    n_internal = len(set(p for p in par if p >= 0))
-    # bytes the scan must move at least once: q, k, v (bf16), g, beta (fp32), o (bf16),
-    # parent-state reads and node-state writes of internal nodes (fp32)
-    alg = (T * (2 * HK * D + HV * D) * 2 + T * HV * 2 * 4 + T * HV * D * 2
-           + n_internal * HV * D * D * 4 * 2)
-    gbs = alg / (ms * 1e-3) / 1e9
+    flops = gdn_useful_flops(tree.n_chunks * HV)
+    tfs = flops / (ms * 1e-3) / 1e12
     cpu = None if args.no_cpu_baseline else gdn_cpu_baseline(lens, par, args.cpu_runs)
     line = {
-        "metric": "tree GDN scan fwd packed tokens/s (16K-token DFS tree)",
+        "metric": "tree GDN layer core (conv + scan) fwd+bwd packed tokens/s (16K-token DFS tree)",
         "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16 in/out, f32 state",
-        "data": "synthetic (seeded topology; q/k/v N(0,1); gates from N(0,1) logits, A_log = log U(0,16), "
-                "dt_bias = 1)",
+        "vs_baseline": None, "dtype": "bf16 in/out, f32 arithmetic and state",
+        "data": "synthetic (seeded topology; qkv rows and dO N(0,1); conv weight 0.5 N(0,1); gates from N(0,1) "
+                "logits, A_log = log U(0,16), dt_bias = 1)",
         "config": {"workload": "gdn16k", "packed_tokens": T, "n_nodes": len(lens), "tree_levels": tree.n_levels,
-                   "heads_qk": HK, "heads_v": HV, "head_dim": D, "chunk": 32, "layer": "one GDN core scan",
+                   "chunks": tree.n_chunks, "heads_qk": HK, "heads_v": HV, "head_dim": D, "conv_channels": C,
+                   "conv_width": K, "chunk": 32, "layer": "one GDN layer core (conv + scan), fwd+bwd",
                    "parallelism": "single GPU"},
         "wall_s_timed": round(wall, 3),
-        "roofline": {"bound": "hbm", "kernel": "gdn prep + per-level scan", "achieved": round(gbs, 1),
-                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 5), "traffic": None,
-                     "bytes_per_launch": alg},
+        "roofline": {"bound": "mfma", "kernel": "whole step (conv, prep, level scans, reverse scans, gradient "
+                                                 "kernels); fp32 products on the vector ALUs, ceiling = fp32 peak",
+                     "achieved": round(tfs, 2), "peak": PEAK_FP32_TFS, "unit": "TFLOP/s",
+                     "frac": round(tfs / PEAK_FP32_TFS, 5), "traffic": None, "flops_per_step": flops},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
 
 
 def gdn_cpu_baseline(lens, par, runs):
-    """The oracle's chunked exact scan (float64 numpy) on one v head of the
-    same tree, scaled to all 32 heads; median of ``runs`` after a warm-up."""
+    """The float64 torch oracle (token recurrence, autograd backward) on one
+    root-to-leaf path of the tree and one v head, forward + backward, one host
+    thread; median of ``runs`` after a warm-up, in tokens/s scaled to the 32
+    v heads of the workload."""
     import numpy as np
-    from oracle.gdn import gdn_tree
+    import torch
+    from oracle.gdn import gdn_tree_torch
+    torch.set_num_threads(1)
+    leaf = next(i for i in range(len(lens)) if i not in set(par))
+    path, j = [], leaf
+    while j >= 0:
+        path.append(j)
+        j = par[j]
+    plens = [lens[i] for i in path[::-1]]
+    T = sum(plens)
     rng = np.random.default_rng(0)
-    T = sum(lens)
-    q = rng.standard_normal((T, 1, D))
-    k = rng.standard_normal((T, 1, D))
-    v = rng.standard_normal((T, 1, D))
-    g = -np.abs(rng.standard_normal((T, 1))) * 0.5
-    beta = rng.uniform(0, 1, (T, 1))
-    from threadpoolctl import threadpool_limits
+    mk = lambda *s: torch.from_numpy(rng.standard_normal(s)).requires_grad_(True)
+    q, k, v = mk(T, 1, D), mk(T, 1, D), mk(T, 1, D)
+    g = torch.from_numpy(-np.abs(rng.standard_normal((T, 1))) * 0.5).requires_grad_(True)
+    beta = torch.from_numpy(rng.uniform(0, 1, (T, 1))).requires_grad_(True)
+    d_o = torch.from_numpy(rng.standard_normal((T, 1, D)))
     times = []
-    with threadpool_limits(limits=1):          # one host core, stated below
-        for i in range(runs + 1):
-            t0 = time.perf_counter()
-            gdn_tree(q, k, v, g, beta, lens, par, mode="chunked", chunk=64)
-            if i:
-                times.append(time.perf_counter() - t0)
+    for i in range(runs + 1):
+        t0 = time.perf_counter()
+        o = gdn_tree_torch(q, k, v, g, beta, plens, list(range(-1, len(plens) - 1)))
+        o.backward(d_o)
+        if i:
+            times.append(time.perf_counter() - t0)
     t = statistics.median(times)
     return {"value": round(T / (t * 32), 1), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"1 of 32 v heads of the full {T}-token tree, oracle chunked scan (numpy float64, "
-                      f"chunk 64), median of {runs} after 1 warm-up, scaled by 1/32",
+            "sample": f"one root-to-leaf path ({T} tokens, {len(plens)} nodes) of the tree, 1 of 32 v heads: "
+                      f"float64 token recurrence with autograd backward (oracle), median of {runs} after 1 "
+                      f"warm-up, scaled by 1/32",
             "seconds_per_sample": round(t, 3)}
 
 
