@@ -42,7 +42,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     int qb, h;
     decode_qblock(a, qb, h);
-    const int g = h / a.rep;
+    const int g = __builtin_amdgcn_readfirstlane(h / a.rep);   // the division runs on the VALU
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int col = lane & 31, half = lane >> 5;
     const int qi = qb * TT_BQ + wave * 32 + col;
@@ -205,16 +205,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
     const TrOffsX tro = tr_offsx(lane);
 
     for (int w_id = blockIdx.x; w_id < n_work; w_id += gridDim.x) {
-        const int g = w_id % a.hkv;
-        const int item = w_id / a.hkv;
+        // Workgroup-uniform values (the integer divisions run on the VALU):
+        // readfirstlane keeps them, and everything derived from them, scalar.
+        const int g = __builtin_amdgcn_readfirstlane(w_id % a.hkv);
+        const int item = __builtin_amdgcn_readfirstlane(w_id / a.hkv);
         int lo_r = 0, hi_r = a.n_kb - 1;        // last tile rank whose first item <= item
         while (lo_r < hi_r) {
             const int mid = (lo_r + hi_r + 1) >> 1;
             if (a.kb_base[mid] <= item) lo_r = mid; else hi_r = mid - 1;
         }
-        const int kb = a.kb_order[lo_r];
-        const int chunk = item - a.kb_base[lo_r];
-        const int qlo = a.kb_qlo[kb], qhi = a.kb_qhi[kb];
+        const int kb = __builtin_amdgcn_readfirstlane(a.kb_order[lo_r]);
+        const int chunk = __builtin_amdgcn_readfirstlane(item - a.kb_base[lo_r]);
+        const int qlo = __builtin_amdgcn_readfirstlane(a.kb_qlo[kb]);
+        const int qhi = __builtin_amdgcn_readfirstlane(a.kb_qhi[kb]);
         const bool split = tt_kb_items(qlo, qhi) > 1;
         int q_start, q_stop;
         tt_kb_item_range(qlo, qhi, chunk, q_start, q_stop);

@@ -23,7 +23,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     int qb, h;
     decode_qblock(a, qb, h);
-    const int g = h / a.rep;
+    const int g = __builtin_amdgcn_readfirstlane(h / a.rep);   // the division runs on the VALU
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int col = lane & 31, half = lane >> 5;
     const int qi = qb * TT_BQ + wave * 32 + col;
@@ -44,22 +44,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int i = 0; i < 4; ++i) o[i] = (f32x16){};
     float m_run = -INFINITY, l_run = 0.0f;
 
-    const int cnt = a.row_cnt[qb];
+    // The plan entries are wave-uniform; readfirstlane keeps everything derived
+    // from them (tile bases, buffer descriptors) in scalar registers.
+    const int cnt = __builtin_amdgcn_readfirstlane(a.row_cnt[qb]);
     const int* list = a.row_list + (size_t)qb * a.n_kt;
     KvTileStager stg;
     Bounds nb;
     if (cnt > 0) {
-        stg.begin(a, list[0] >> 1, g);
-        fetch_bounds(a, list[0] >> 1, nb);
+        const int kt0 = __builtin_amdgcn_readfirstlane(list[0] >> 1);
+        stg.begin(a, kt0, g);
+        fetch_bounds(a, kt0, nb);
     }
     for (int it = 0; it < cnt; ++it) {
         FwdStage& S = st[it & 1];
-        const bool full = list[it] & 1;
+        const bool full = __builtin_amdgcn_readfirstlane(list[it]) & 1;
         stg.commit(a, g, S.K, S.V);
         store_bounds(nb, S.lo, S.hi);
         __syncthreads();
         if (it + 1 < cnt) {
-            const int kt1 = list[it + 1] >> 1;
+            const int kt1 = __builtin_amdgcn_readfirstlane(list[it + 1] >> 1);
             stg.begin(a, kt1, g);
             fetch_bounds(a, kt1, nb);
         }

@@ -291,6 +291,10 @@ __device__ __forceinline__ void decode_qblock(const AttnDev& a, int& qb, int& h)
         h = bid % a.hq;
         qb = a.row_order[bid / a.hq];
     }
+    // Workgroup-uniform: keeps the tile bases and buffer descriptors derived
+    // from qb in scalar registers (no per-load uniformity loops).
+    qb = __builtin_amdgcn_readfirstlane(qb);
+    h = __builtin_amdgcn_readfirstlane(h);
 }
 
 
