@@ -63,7 +63,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="agent16k",
-                    choices=["agent16k", "gateway16k", "rollout48k", "gdn16k"])
+                    choices=["agent16k", "gateway16k", "rollout48k", "gdn16k", "prologue16k"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=3)
     ap.add_argument("--calibrate-copy-mb", type=int, default=0,
@@ -97,6 +97,8 @@ def main():
         sys.exit(2)
     if args.workload == "gdn16k":
         return run_gdn(args)
+    if args.workload == "prologue16k":
+        return run_prologue(args)
     import torch
     from tree_training_amd import _lib
     from tree_training_amd.attention import _Problem, attn_forward
@@ -257,6 +259,117 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def run_prologue(args):
+    """Fused attention prologue (q/k RMSNorm + rotary embedding) forward +
+    backward on the 16K agent tree at its depth positions, Qwen3-4B shapes (32
+    q / 8 kv heads, d 128), bf16, through the C ABI. Also times transformers'
+    own prologue (q_norm / k_norm + apply_rotary_pos_emb, forward + autograd
+    backward) on the same GPU for comparison."""
+    import torch
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm, apply_rotary_pos_emb
+    from tree_training_amd.meta import TreeMetaDevice
+    from tree_training_amd.prologue import qk_prologue_backward, qk_prologue_forward
+    from tree_training_amd.workloads import agent_tree
+    Hq, Hkv = HQ, HKV
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    lens, par = agent_tree(0)
+    T = sum(lens)
+    pos = TreeMetaDevice(lens, par, pos_offset=0, device=dev).pos       # depth positions (metadata kernel)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    bf = torch.bfloat16
+    pq = torch.randn(T, Hq * D, device=dev, generator=gen, dtype=bf)
+    pk = torch.randn(T, Hkv * D, device=dev, generator=gen, dtype=bf)
+    qw = (torch.rand(D, device=dev, generator=gen) + 0.5).to(bf)
+    kw = (torch.rand(D, device=dev, generator=gen) + 0.5).to(bf)
+    inv = 1.0 / (1e6 ** (torch.arange(0, D, 2, device=dev, dtype=torch.float32) / D))
+    emb = torch.cat([pos[:, None].float() * inv[None]] * 2, dim=-1)
+    cos, sin = emb.cos().to(bf), emb.sin().to(bf)
+    dq = torch.randn(T, Hq, D, device=dev, generator=gen, dtype=bf)
+    dk = torch.randn(T, Hkv, D, device=dev, generator=gen, dtype=bf)
+    q_raw, k_raw = pq.view(T, Hq, D), pk.view(T, Hkv, D)
+
+    def step():
+        qk_prologue_forward(q_raw, k_raw, qw, kw, 1e-6, 1e-6, cos, sin)
+        qk_prologue_backward(q_raw, k_raw, qw, kw, 1e-6, 1e-6, cos, sin, dq, dk)
+
+    qn, kn = Qwen3RMSNorm(D).to(dev, bf), Qwen3RMSNorm(D).to(dev, bf)
+    with torch.no_grad():
+        qn.weight.copy_(qw)
+        kn.weight.copy_(kw)
+    xq = q_raw.detach().requires_grad_(True)
+    xk = k_raw.detach().requires_grad_(True)
+
+    def torch_step():
+        a = qn(xq[None]).transpose(1, 2)
+        b = kn(xk[None]).transpose(1, 2)
+        qe, ke = apply_rotary_pos_emb(a, b, cos[None], sin[None])
+        torch.autograd.backward((qe, ke), (dq[None].transpose(1, 2), dk[None].transpose(1, 2)))
+
+    def timed(fn, steps):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st = torch.cuda.current_stream(dev)
+        t0 = time.perf_counter()
+        e0.record(st)
+        for _ in range(steps):
+            fn()
+        e1.record(st)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps, time.perf_counter() - t0
+
+    ms, wall = timed(step, args.steps)
+    ms_torch, _ = timed(torch_step, args.steps)
+    row = (Hq + Hkv) * D * 2
+    alg = T * (row + 2 * D * 2) + T * (3 * row + 2 * D * 2)     # fwd: x, cos/sin, out; bwd: x, dout, cos/sin, dx
+    gbs = alg / (ms * 1e-3) / 1e9
+    cpu = None if args.no_cpu_baseline else prologue_cpu_baseline(args.cpu_runs)
+    line = {
+        "metric": "attention prologue (q/k RMSNorm + RoPE) fwd+bwd packed tokens/s (16K-token DFS tree)",
+        "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 in/out, f32 arithmetic",
+        "data": "synthetic (seeded N(0,1) projections and gradients; rotary table at the tree's depth positions)",
+        "config": {"workload": "prologue16k", "packed_tokens": T, "heads_q": Hq, "heads_kv": Hkv, "head_dim": D,
+                   "rope_theta": 1e6, "parallelism": "single GPU"},
+        "wall_s_timed": round(wall, 3),
+        "torch_prologue_ms": round(ms_torch, 4),
+        "roofline": {"bound": "hbm", "kernel": "prologue_fwd_kernel + prologue_bwd_kernel (+ dw reduce)",
+                     "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 5), "traffic": None, "bytes_per_step": alg},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def prologue_cpu_baseline(runs):
+    """The float64 oracle (torch, autograd backward) on 512 tokens x 40 heads,
+    16 host threads, median of ``runs`` after a warm-up, in tokens/s."""
+    import torch
+    from oracle.prologue import qk_prologue
+    cores = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    n = 512
+    x = torch.randn(n, HQ + HKV, D, dtype=torch.float64, generator=g).requires_grad_(True)
+    w = torch.rand(D, dtype=torch.float64, generator=g).requires_grad_(True)
+    cos, sin = torch.rand(n, D, dtype=torch.float64), torch.rand(n, D, dtype=torch.float64)
+    dy = torch.randn(n, HQ + HKV, D, dtype=torch.float64, generator=g)
+    times = []
+    for i in range(runs + 1):
+        t0 = time.perf_counter()
+        out = qk_prologue(x, w, 1e-6, cos, sin)
+        torch.autograd.grad((out * dy).sum(), (x, w))
+        if i:
+            times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": round(n / t, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{n} tokens x 40 heads, float64 oracle forward + autograd backward (torch CPU), "
+                      f"median of {runs} after 1 warm-up", "seconds_per_sample": round(t, 4)}
 
 
 def gdn_useful_flops(n_chunk_heads, C=32, Dh=128):

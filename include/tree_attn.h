@@ -145,6 +145,41 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
                 void* dq, void* dk, void* dv, float* dk_past_acc, float* dv_past_acc,
                 void* ws, size_t ws_bytes, void* stream);
 
+/* ---- attention prologue: q/k RMSNorm + rotary embedding -------------------
+ * Replaces the per-head q_norm / k_norm and apply_rotary_pos_emb that
+ * Qwen3Attention runs between the projections and the attention call
+ * (HF/models/qwen3/modeling_qwen3.py:252-257; RMSNorm :59-64, rotate_half and
+ * apply_rotary_pos_emb :140-170), at the depth positions the reference passes
+ * as position_ids (dfs_tree_forward.py:543-560):
+ *   y = w * x / sqrt(mean(x^2) + eps),  out = y * cos + [-y[64:], y[:64]] * sin,
+ * fused into one pass that writes q and k in the [T, H, 128] layout of
+ * tt_attn_problem. cos/sin are the model's rotary table at each token's
+ * position (any rotary scaling variant). */
+typedef struct tt_prologue_problem {
+    int32_t dtype;          /* TT_DTYPE_BF16 or TT_DTYPE_F32 for every tensor here */
+    int32_t n_tokens;
+    int32_t n_heads_q;
+    int32_t n_heads_kv;
+    int32_t head_dim;       /* 128 */
+    float eps_q, eps_k;     /* the two norms' epsilons */
+    tt_tensor q, k;         /* projected q [T, Hq, 128], k [T, Hkv, 128]; 16-byte aligned rows */
+    const void* q_weight;   /* [128] */
+    const void* k_weight;   /* [128] */
+    const void* cos;        /* [T, 128], element [t][d] at cos + t*cs_stride_tok + d */
+    const void* sin;
+    int64_t cs_stride_tok;
+} tt_prologue_problem;
+
+/* q_out [T, Hq, 128] and k_out [T, Hkv, 128], contiguous. */
+int tt_qk_prologue_fwd(const tt_prologue_problem* p, void* q_out, void* k_out, void* stream);
+/* Gradients for dq_out / dk_out (strided like q / k): dq_raw, dk_raw
+ * contiguous [T, H, 128] in the problem dtype, dq_weight / dk_weight [128]
+ * float32 (summed in a fixed order: deterministic). Workspace:
+ * tt_qk_prologue_bwd_workspace_bytes (fixed, 1 MiB). */
+size_t tt_qk_prologue_bwd_workspace_bytes(const tt_prologue_problem* p);
+int tt_qk_prologue_bwd(const tt_prologue_problem* p, tt_tensor dq_out, tt_tensor dk_out, void* dq_raw, void* dk_raw,
+                       float* dq_weight, float* dk_weight, void* ws, size_t ws_bytes, void* stream);
+
 /* ---- tree gated delta rule (linear-attention layers) ----------------------
  * Replaces torch_chunk_gated_delta_rule_tree_varlen (tree_dfs_ssm.py:38-156;
  * twin dfs_tree_forward.py:253-353) as called from the patched GDN layer

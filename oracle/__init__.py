@@ -21,4 +21,8 @@ Pinning (what fixes each function independently of its own formula):
   * attention.attn_fwd / attn_bwd — torch.nn.functional.scaled_dot_product_attention
     and torch autograd (library routines), finite differences, and per-path
     equivalence (tree rows == plain causal attention over each root-to-leaf path).
+  * gdn — transformers' gated-delta-rule routines and module (library), conv1d
+    on every path, finite differences; see oracle/gdn.py.
+  * prologue.qk_prologue — transformers' Qwen3RMSNorm + apply_rotary_pos_emb and
+    their autograd gradients (library), in float64.
 """

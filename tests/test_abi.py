@@ -200,3 +200,43 @@ def test_conv_bwd_validation():
                                 None) == _lib.TT_E_ARG
     assert lib.tt_tree_conv_bwd(ctypes.byref(p), V, 4, V, V, None, V, want, None) == _lib.TT_E_ARG
     assert lib.tt_tree_conv_fwd(ctypes.byref(p), ctypes.c_void_p(20), 8, None) == _lib.TT_E_ARG
+
+
+def _prologue_problem(**kw):
+    p = _lib.TTPrologueProblem(dtype=_lib.TT_DTYPE_BF16, n_tokens=10, n_heads_q=32, n_heads_kv=8, head_dim=128,
+                               eps_q=1e-6, eps_k=1e-6, q=_lib.TTTensor(16, 32 * 128, 128),
+                               k=_lib.TTTensor(16, 8 * 128, 128), q_weight=16, k_weight=16, cos=16, sin=16,
+                               cs_stride_tok=128)
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("head_dim", 64, _lib.TT_E_UNSUPPORTED),
+    ("dtype", 3, _lib.TT_E_UNSUPPORTED),
+    ("n_tokens", 0, _lib.TT_E_ARG),
+    ("eps_q", float("nan"), _lib.TT_E_ARG),
+    ("q", _lib.TTTensor(24, 32 * 128, 128), _lib.TT_E_ARG),      # misaligned rows
+    ("k", _lib.TTTensor(16, 8 * 128, 100), _lib.TT_E_ARG),       # heads overlap
+    ("cos", None, _lib.TT_E_ARG),
+    ("cs_stride_tok", 64, _lib.TT_E_ARG),
+])
+def test_prologue_validation(field, value, code):
+    lib = _lib.lib()
+    p = _prologue_problem(**{field: value})
+    assert lib.tt_qk_prologue_fwd(ctypes.byref(p), ctypes.c_void_p(16), ctypes.c_void_p(16), None) == code
+
+
+def test_prologue_bwd_validation():
+    lib = _lib.lib()
+    V = ctypes.c_void_p(16)
+    p = _prologue_problem()
+    want = lib.tt_qk_prologue_bwd_workspace_bytes(ctypes.byref(p))
+    assert want == 1024 * 2 * 128 * 4
+    DQ, DK = _lib.TTTensor(16, 32 * 128, 128), _lib.TTTensor(16, 8 * 128, 128)
+    assert lib.tt_qk_prologue_bwd(ctypes.byref(p), DQ, DK, V, V, V, V, V, want - 1, None) == _lib.TT_E_WORKSPACE
+    assert lib.tt_qk_prologue_bwd(ctypes.byref(p), _lib.TTTensor(16, 64, 128), DK, V, V, V, V, V, want,
+                                  None) == _lib.TT_E_ARG
+    assert lib.tt_qk_prologue_bwd(ctypes.byref(p), DQ, DK, V, V, ctypes.c_void_p(18), V, V, want,
+                                  None) == _lib.TT_E_ARG

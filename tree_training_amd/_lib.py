@@ -36,7 +36,7 @@ EXPORTS = (
     "tt_meta_dense_mask", "tt_plan_bytes", "tt_plan_build", "tt_attn_fwd",
     "tt_attn_bwd_workspace_bytes", "tt_attn_bwd", "tt_gdn_workspace_bytes", "tt_gdn_tree_fwd",
     "tt_gdn_bwd_workspace_bytes", "tt_gdn_tree_bwd", "tt_tree_conv_fwd", "tt_tree_conv_bwd_workspace_bytes",
-    "tt_tree_conv_bwd",
+    "tt_tree_conv_bwd", "tt_qk_prologue_fwd", "tt_qk_prologue_bwd_workspace_bytes", "tt_qk_prologue_bwd",
     "tt_selftest_mfma32",
 )
 
@@ -81,6 +81,16 @@ class TTConvProblem(ctypes.Structure):
     ]
 
 
+class TTPrologueProblem(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32), ("n_tokens", ctypes.c_int32), ("n_heads_q", ctypes.c_int32),
+        ("n_heads_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("eps_q", ctypes.c_float),
+        ("eps_k", ctypes.c_float), ("q", TTTensor), ("k", TTTensor), ("q_weight", ctypes.c_void_p),
+        ("k_weight", ctypes.c_void_p), ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p),
+        ("cs_stride_tok", ctypes.c_int64),
+    ]
+
+
 class TreeAttnError(RuntimeError):
     pass
 
@@ -108,6 +118,10 @@ def _declare(lib):
         "tt_gdn_bwd_workspace_bytes": (SZ, [ctypes.POINTER(TTGdnProblem)]),
         "tt_gdn_tree_bwd": (ctypes.c_int, [ctypes.POINTER(TTGdnProblem), TTTensor, P, P, P, P, P, P, SZ, VP]),
         "tt_tree_conv_fwd": (ctypes.c_int, [ctypes.POINTER(TTConvProblem), P, ctypes.c_int64, VP]),
+        "tt_qk_prologue_fwd": (ctypes.c_int, [ctypes.POINTER(TTPrologueProblem), P, P, VP]),
+        "tt_qk_prologue_bwd_workspace_bytes": (SZ, [ctypes.POINTER(TTPrologueProblem)]),
+        "tt_qk_prologue_bwd": (ctypes.c_int, [ctypes.POINTER(TTPrologueProblem), TTTensor, TTTensor, P, P, P, P, P,
+                                              SZ, VP]),
         "tt_tree_conv_bwd_workspace_bytes": (SZ, [ctypes.POINTER(TTConvProblem)]),
         "tt_tree_conv_bwd": (ctypes.c_int, [ctypes.POINTER(TTConvProblem), P, ctypes.c_int64, P, P, P, P, SZ,
                                             VP]),

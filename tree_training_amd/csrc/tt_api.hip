@@ -345,6 +345,69 @@ int tt_tree_conv_bwd(const tt_conv_problem* p, const void* dy, int64_t dy_stride
     return tt_conv_bwd_launch(d, dy, dy_stride_tok, dx, dweight, dbias, (float*)ws, (hipStream_t)stream);
 }
 
+}  // extern "C"
+
+static bool prologue_tensor_ok(const tt_tensor& t, int64_t gran) {
+    return t.ptr && t.stride_tok >= 128 && t.stride_head >= 128 && !(t.stride_tok % gran) &&
+           !(t.stride_head % gran) && aligned(t.ptr, 16);
+}
+
+static int prologue_problem(const tt_prologue_problem* p, PrologueDev& d) {
+    if (!p) return TT_E_ARG;
+    if (p->dtype != TT_DTYPE_BF16 && p->dtype != TT_DTYPE_F32) return TT_E_UNSUPPORTED;
+    if (p->head_dim != 128) return TT_E_UNSUPPORTED;
+    if (p->n_tokens < 1 || p->n_heads_q < 1 || p->n_heads_kv < 1) return TT_E_ARG;
+    if ((int64_t)p->n_tokens * (p->n_heads_q + p->n_heads_kv) > INT32_MAX) return TT_E_ARG;
+    if (!(p->eps_q >= 0.0f) || !(p->eps_k >= 0.0f)) return TT_E_ARG;
+    const int64_t gran = p->dtype == TT_DTYPE_BF16 ? 8 : 4;
+    if (!prologue_tensor_ok(p->q, gran) || !prologue_tensor_ok(p->k, gran)) return TT_E_ARG;
+    if (!p->q_weight || !p->k_weight || !p->cos || !p->sin) return TT_E_ARG;
+    if (!aligned(p->q_weight, 16) || !aligned(p->k_weight, 16) || !aligned(p->cos, 16) || !aligned(p->sin, 16) ||
+        p->cs_stride_tok < 128 || (p->cs_stride_tok % gran))
+        return TT_E_ARG;
+    d.q = p->q.ptr; d.q_st = p->q.stride_tok; d.q_sh = p->q.stride_head;
+    d.k = p->k.ptr; d.k_st = p->k.stride_tok; d.k_sh = p->k.stride_head;
+    d.qw = p->q_weight; d.kw = p->k_weight;
+    d.cos = p->cos; d.sin = p->sin; d.cs_st = p->cs_stride_tok;
+    d.eps_q = p->eps_q; d.eps_k = p->eps_k;
+    d.dtype = p->dtype;
+    d.n_tokens = p->n_tokens;
+    d.hq = p->n_heads_q;
+    d.hkv = p->n_heads_kv;
+    d.n_rows = p->n_tokens * (p->n_heads_q + p->n_heads_kv);
+    return TT_OK;
+}
+
+extern "C" {
+
+int tt_qk_prologue_fwd(const tt_prologue_problem* p, void* q_out, void* k_out, void* stream) {
+    PrologueDev d;
+    const int rc = prologue_problem(p, d);
+    if (rc != TT_OK) return rc;
+    if (!q_out || !k_out || !aligned(q_out, 16) || !aligned(k_out, 16)) return TT_E_ARG;
+    return tt_prologue_fwd_launch(d, q_out, k_out, (hipStream_t)stream);
+}
+
+size_t tt_qk_prologue_bwd_workspace_bytes(const tt_prologue_problem* p) {
+    return p ? tt_prologue_bwd_ws_bytes_impl() : 0;
+}
+
+int tt_qk_prologue_bwd(const tt_prologue_problem* p, tt_tensor dq_out, tt_tensor dk_out, void* dq_raw, void* dk_raw,
+                       float* dq_weight, float* dk_weight, void* ws, size_t ws_bytes, void* stream) {
+    PrologueDev d;
+    const int rc = prologue_problem(p, d);
+    if (rc != TT_OK) return rc;
+    const int64_t gran = p->dtype == TT_DTYPE_BF16 ? 8 : 4;
+    if (!prologue_tensor_ok(dq_out, gran) || !prologue_tensor_ok(dk_out, gran)) return TT_E_ARG;
+    if (!dq_raw || !dk_raw || !dq_weight || !dk_weight || !ws || !aligned(dq_raw, 16) || !aligned(dk_raw, 16) ||
+        !aligned(ws, 16) || !aligned(dq_weight, 4) || !aligned(dk_weight, 4))
+        return TT_E_ARG;
+    if (ws_bytes < tt_prologue_bwd_ws_bytes_impl()) return TT_E_WORKSPACE;
+    return tt_prologue_bwd_launch(d, dq_out.ptr, dq_out.stride_tok, dq_out.stride_head, dk_out.ptr,
+                                  dk_out.stride_tok, dk_out.stride_head, dq_raw, dk_raw, dq_weight, dk_weight,
+                                  (float*)ws, (hipStream_t)stream);
+}
+
 int tt_selftest_mfma32(const void* a, const void* b, float* d, void* stream) {
     if (!a || !b || !d || !aligned(a, 2) || !aligned(b, 2) || !aligned(d, 4)) return TT_E_ARG;
     return tt_selftest_mfma_launch(a, b, d, (hipStream_t)stream);

@@ -77,6 +77,22 @@ int tt_conv_fwd_launch(const ConvDev& d, void* y, int64_t y_st, hipStream_t s);
 int tt_conv_bwd_launch(const ConvDev& d, const void* dy, int64_t dy_st, void* dx, float* dw, float* db, float* ws,
                        hipStream_t s);
 
+// Device-side view of a tt_prologue_problem.
+struct PrologueDev {
+    const void* q; int64_t q_st, q_sh;     // projected q [T, Hq, 128]
+    const void* k; int64_t k_st, k_sh;     // projected k [T, Hkv, 128]
+    const void* qw; const void* kw;        // norm weights [128]
+    const void* cos; const void* sin; int64_t cs_st;   // [T, 128]
+    float eps_q, eps_k;
+    int dtype, n_tokens, hq, hkv, n_rows;  // n_rows = T * (Hq + Hkv)
+};
+
+size_t tt_prologue_bwd_ws_bytes_impl();
+int tt_prologue_fwd_launch(const PrologueDev& p, void* q_out, void* k_out, hipStream_t s);
+int tt_prologue_bwd_launch(const PrologueDev& p, const void* dq_out, int64_t dq_st, int64_t dq_sh, const void* dk_out,
+                           int64_t dk_st, int64_t dk_sh, void* dq_raw, void* dk_raw, float* dqw, float* dkw,
+                           float* ws, hipStream_t s);
+
 size_t tt_gdn_ws_bytes_impl(int n_chunks, int n_heads_v);
 int tt_gdn_fwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, void* out, float* states,
                       float* ws, hipStream_t s);

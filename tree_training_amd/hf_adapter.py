@@ -70,19 +70,24 @@ def _has_linear_attention(model) -> bool:
 
 
 @contextlib.contextmanager
-def tree_attention_mode(model, linear_attention_patched: bool = False):
+def tree_attention_mode(model, linear_attention_patched: bool = False, fused_prologue: bool = True):
     """Switches every attention layer of ``model`` to the tree kernels for the
-    duration of the block. Gated-delta-rule (linear_attn) layers must have been
-    patched with the tree-aware forward (``gdn_layer._patch_ssm``, done by
-    dfs_tree_forward); the partitioned drivers do not carry their recurrent
-    state across partitions and refuse such models."""
+    duration of the block, and (``fused_prologue``) every Qwen3Attention to the
+    fused q/k RMSNorm + rotary prologue (``prologue.py``). Gated-delta-rule
+    (linear_attn) layers must have been patched with the tree-aware forward
+    (``gdn_layer._patch_ssm``, done by dfs_tree_forward); the partitioned
+    drivers do not carry their recurrent state across partitions and refuse
+    such models."""
+    from .prologue import patch_attention_prologue, unpatch_attention_prologue
     register()
     if not linear_attention_patched and _has_linear_attention(model):
         raise NotImplementedError("gated-delta-rule (linear_attn) layers are supported by dfs_tree_forward only")
     cfg = model.config
     saved = cfg._attn_implementation
     cfg._attn_implementation = ATTN_IMPL
+    patched = patch_attention_prologue(model) if fused_prologue else []
     try:
         yield
     finally:
+        unpatch_attention_prologue(patched)
         cfg._attn_implementation = saved
