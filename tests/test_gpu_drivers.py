@@ -111,6 +111,25 @@ def test_hybrid_grads_fp32(max_tokens):
     assert r < 1e-5, r
 
 
+@pytest.mark.parametrize("tree,max_tokens", [("c1", 20), ("c1", 10), ("q1", 6)])
+def test_hybrid_summed_backward_fp32(tree, max_tokens):
+    """One backward per partition (summed leaf losses + gateway chains) gives
+    the oracle's gradients, like the reference's per-leaf schedule."""
+    from tree_training_amd.hybrid import tree_grad_hybrid
+    say(f"hybrid summed backward fp32 {tree} max_tokens={max_tokens}")
+    base = make_qwen3("tiny", layers=2)
+    ref_model = copy.deepcopy(base).double()
+    model = base.to(DEV)
+    roots, leaves = _tree(tree)
+    labels = _labels(leaves)
+    ref = sequential_param_grads(ref_model, roots, labels, len(leaves))
+    new = _grads(model, lambda: tree_grad_hybrid(model, roots, _loss_fn(labels, len(leaves)), max_tokens,
+                                                 summed_backward=True))
+    r = _max_rel_params(ref, new)
+    say(f"  max_rel {r:.3e}")
+    assert r < 1e-5, r
+
+
 def test_hybrid_chain_inherited_bias_equals_whole_tree():
     """Two-level partition chain: with the inherited gateway bias the hybrid
     run equals the whole tree; the reference's literal bias does not."""

@@ -166,3 +166,15 @@ def test_transformers_passes_tree_ctx_to_attention():
     marker = object()
     m(input_ids=torch.tensor([[1, 2, 3]]), position_ids=torch.tensor([[0, 1, 1]]), tree_ctx=marker)
     assert seen["ctx"] is marker and seen["mask"] is None and seen["layers"] == 2
+
+
+def test_run_tree_model_rejects_token_ids_outside_the_vocabulary():
+    """The device embedding lookup does not check its indices; the driver
+    refuses out-of-range ids on the host before any launch."""
+    import types
+    from tree_training_amd.dfs_tree_forward import run_tree_model
+    from tree_training_amd.tree import TreeNode, build_dfs_tree_info
+    info = build_dfs_tree_info([TreeNode([1, 2, 1000])])
+    model = types.SimpleNamespace(config=types.SimpleNamespace(vocab_size=1000))
+    with pytest.raises(ValueError, match="vocabulary"):
+        run_tree_model(model, info, "cpu")

@@ -44,6 +44,12 @@ def run_tree_model(model, info: DFSTreeInfo, dev, pos_offset: int = 0, cache=Non
                    past_bias: Optional[torch.Tensor] = None, linear_attention_patched: bool = False):
     """One model forward over a DFS-packed forest (or partition) with tree
     attention. Returns the model output."""
+    vocab = getattr(getattr(model, "config", None), "vocab_size", None)
+    if vocab is not None and info.dfs_token_ids and not (0 <= min(info.dfs_token_ids) and
+                                                         max(info.dfs_token_ids) < vocab):
+        # the embedding lookup on the device does not check its indices
+        raise ValueError(f"token ids must lie in [0, {vocab}) (the model's vocabulary); got "
+                         f"[{min(info.dfs_token_ids)}, {max(info.dfs_token_ids)}]")
     meta = info.device_meta(dev, pos_offset)
     plan = info.key_plan(dev, past_bias, pos_offset)
     ids_t = torch.tensor([info.dfs_token_ids], device=dev)

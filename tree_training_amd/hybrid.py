@@ -231,12 +231,13 @@ def _make_child_gateways(own_kv, dfs_info, orig_id_to_start, orig_id_to_end, ori
     return gateways
 
 
-def _chain_gateway_grads(gw: SubtreeGateway, retain_graph: bool = False) -> None:
+def _chain_gateway_grads(gw: SubtreeGateway, retain_graph: bool = False, collect: Optional[list] = None) -> None:
     """Chain a gateway's fp32 gradients into the parent (tree_grad_hybrid.py:253-272).
 
     The own-token part goes through autograd into the parent partition's graph
     (autograd casts it to the K/V dtype, as in the reference); the inherited
-    part is added to the parent gateway's fp32 accumulators."""
+    part is added to the parent gateway's fp32 accumulators. With ``collect``
+    the (tensor, gradient) pairs are appended there instead of run."""
     raws, grads = [], []
     ppl = gw.parent_past_len
     for l, acc in enumerate(gw.fp32_acc):
@@ -249,7 +250,9 @@ def _chain_gateway_grads(gw: SubtreeGateway, retain_graph: bool = False) -> None
             pa.touched = True
         raws += [gw.raw_keys[l], gw.raw_vals[l]]
         grads += [acc.as_hf("k")[:, :, ppl:], acc.as_hf("v")[:, :, ppl:]]
-    if raws:
+    if collect is not None:
+        collect.extend(zip(raws, grads))
+    elif raws:
         torch.autograd.backward(raws, grads, retain_graph=retain_graph)
 
 
@@ -274,13 +277,19 @@ def _subtree_forward(model, partition: SubtreePartition, gateway: Optional[Subtr
 # 5. driver
 # ---------------------------------------------------------------------------
 def tree_grad_hybrid(model, roots: List[TreeNode], leaf_loss_fn: Callable[[torch.Tensor, TreeNode], torch.Tensor],
-                     max_tokens: int, legacy_gateway_bias: bool = False) -> None:
+                     max_tokens: int, legacy_gateway_bias: bool = False, summed_backward: bool = False) -> None:
     """Hybrid tree training (tree_grad_hybrid.py:434-539); grads accumulate in ``.grad``.
 
     model        : HF causal LM (Qwen3 family), train mode, zero_grad() already called
     roots        : forest roots
     leaf_loss_fn : loss = leaf_loss_fn(logits [1, L, V], node) -> scalar
     max_tokens   : max DFS token count per partition
+    summed_backward : False (default) keeps the reference's schedule, one
+                   ``retain_graph`` backward per leaf and per gateway chain
+                   (:526-539), each running the partition's whole backward
+                   graph; True runs ONE backward per partition over the sum of
+                   its leaf losses and its chain gradients (the same gradients
+                   up to summation order).
     """
     dev = next(model.parameters()).device
     dtype = next(model.parameters()).dtype
@@ -322,6 +331,17 @@ def tree_grad_hybrid(model, roots: List[TreeNode], leaf_loss_fn: Callable[[torch
             if cgw is not None and id(cgw) not in seen_gw:
                 seen_gw.add(id(cgw))
                 chains.append(cgw)
+        if summed_backward:
+            pairs = []
+            for cgw in chains:
+                _chain_gateway_grads(cgw, collect=pairs)
+            roots_, grads_ = [t for t, _ in pairs], [g for _, g in pairs]
+            if leaf_chunks:
+                roots_.append(sum(leaf_loss_fn(logits[:, s:e, :], leaf) for s, e, leaf in leaf_chunks))
+                grads_.append(None)
+            if roots_:
+                torch.autograd.backward(roots_, grads_)
+            continue
         remaining = [len(leaf_chunks) + len(chains)]
 
         def _retain():
