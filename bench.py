@@ -63,7 +63,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="agent16k",
-                    choices=["agent16k", "gateway16k", "rollout48k", "gdn16k", "prologue16k"])
+                    choices=["agent16k", "gateway16k", "rollout48k", "gdn16k", "prologue16k", "leafce16k"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=3)
     ap.add_argument("--calibrate-copy-mb", type=int, default=0,
@@ -99,6 +99,8 @@ def main():
         return run_gdn(args)
     if args.workload == "prologue16k":
         return run_prologue(args)
+    if args.workload == "leafce16k":
+        return run_leafce(args)
     import torch
     from tree_training_amd import _lib
     from tree_training_amd.attention import _Problem, attn_forward
@@ -259,6 +261,109 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def run_leafce(args):
+    """Leaf loss head on the 16K agent tree: lm_head (V = 151,936, hidden 2560,
+    bf16) + cross-entropy on every leaf's tokens, forward + backward, through
+    the fused chunked path (``loss.TreeCELoss.fused``: tt_ce_rows between
+    hipBLASLt GEMMs, no [T, V] logits). The reference's path (logits for every
+    token, then F.cross_entropy per leaf) is timed beside it on the same GPU,
+    with both paths' peak memory."""
+    import torch
+    import torch.nn.functional as F
+    from tree_training_amd.loss import TreeCELoss
+    from tree_training_amd.workloads import agent_tree
+    V, H = 151936, 2560
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    lens, par = agent_tree(0)
+    T = sum(lens)
+    starts = [0]
+    for L in lens[:-1]:
+        starts.append(starts[-1] + L)
+    kids = set(p for p in par if p >= 0)
+    spans = [(starts[i], starts[i] + lens[i]) for i in range(len(lens)) if i not in kids]
+    n_leaf_tok = sum(e - s for s, e in spans)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    bf = torch.bfloat16
+    hidden = torch.randn(T, H, device=dev, generator=gen, dtype=bf).requires_grad_(True)
+    weight = (torch.randn(V, H, device=dev, generator=gen, dtype=bf) * 0.02).requires_grad_(True)
+    nodes = [object() for _ in spans]
+    labels = [torch.randint(0, V, (e - s,), device=dev, generator=gen) for s, e in spans]
+    fn = TreeCELoss(labels, nodes, len(spans))
+
+    def fused_step():
+        fn.fused_spans(hidden, [(s, e, n) for (s, e), n in zip(spans, nodes)], weight).backward()
+
+    def torch_step():
+        logits = (hidden @ weight.t())[None]
+        loss = sum(fn(logits[:, s:e, :], n) for (s, e), n in zip(spans, nodes))
+        loss.backward()
+
+    def timed(step, steps):
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats(dev)
+        base = torch.cuda.memory_allocated(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st = torch.cuda.current_stream(dev)
+        t0 = time.perf_counter()
+        e0.record(st)
+        for _ in range(steps):
+            step()
+        e1.record(st)
+        torch.cuda.synchronize()
+        peak = torch.cuda.max_memory_allocated(dev) - base
+        return e0.elapsed_time(e1) / steps, time.perf_counter() - t0, peak
+
+    ms, wall, peak = timed(fused_step, args.steps)
+    ms_t, _, peak_t = timed(torch_step, max(2, args.steps // 4))
+    flops = 3 * 2.0 * n_leaf_tok * V * H          # logits, d_hidden, d_weight GEMMs (leaf tokens only)
+    tfs = flops / (ms * 1e-3) / 1e12
+    cpu = None if args.no_cpu_baseline else leafce_cpu_baseline(args.cpu_runs)
+    line = {
+        "metric": "leaf loss head (lm_head + CE) fwd+bwd leaf tokens/s (16K-token DFS tree, V=151936)",
+        "value": round(n_leaf_tok / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 GEMMs, f32 softmax",
+        "data": "synthetic (seeded N(0,1) hidden states, 0.02 N(0,1) lm_head, uniform labels)",
+        "config": {"workload": "leafce16k", "packed_tokens": T, "leaf_tokens": n_leaf_tok, "leaves": len(spans),
+                   "vocab": V, "hidden": H, "chunk": 4096, "parallelism": "single GPU"},
+        "wall_s_timed": round(wall, 3),
+        "peak_extra_bytes": int(peak),
+        "reference_path": {"ms_per_step": round(ms_t, 4), "peak_extra_bytes": int(peak_t),
+                           "what": "logits for every token (hidden @ W^T) + F.cross_entropy per leaf + autograd"},
+        "roofline": {"bound": "mfma", "kernel": "whole step (3 GEMMs per chunk + tt_ce_rows)", "achieved": round(tfs, 1),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tfs / PEAK_BF16_TFLOPS, 5),
+                     "traffic": None, "flops_per_step": flops},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def leafce_cpu_baseline(runs):
+    """torch cross-entropy (forward + autograd backward) on 64 rows of the
+    full vocabulary in float32 on the host, 16 threads, median of ``runs``,
+    in rows/s (the GEMMs are not included)."""
+    import torch
+    import torch.nn.functional as F
+    cores = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(64, 151936, generator=g).requires_grad_(True)
+    y = torch.randint(0, 151936, (64,), generator=g)
+    times = []
+    for i in range(runs + 1):
+        t0 = time.perf_counter()
+        F.cross_entropy(x, y).backward()
+        if i:
+            times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": round(64 / t, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"64 rows x 151936 classes, torch float32 cross-entropy forward + backward on the host "
+                      f"(the softmax part only), median of {runs} after 1 warm-up", "seconds_per_sample": round(t, 4)}
 
 
 def run_prologue(args):

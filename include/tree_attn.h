@@ -286,6 +286,20 @@ size_t tt_tree_conv_bwd_workspace_bytes(const tt_conv_problem* p);
 int tt_tree_conv_bwd(const tt_conv_problem* p, const void* dy, int64_t dy_stride_tok, void* dx, float* dweight,
                      float* dbias, void* ws, size_t ws_bytes, void* stream);
 
+/* ---- leaf loss: row-wise cross-entropy ------------------------------------
+ * The step after the tree forward: the reference scores each leaf with
+ * F.cross_entropy(logits, labels, ignore_index) / n_leaves
+ * (tree_grad_hybrid.py:546-558, tree_grad_ckpt.py:280-297) on logits of every
+ * token. Applied to one chunk of lm_head logits at a time (the caller's
+ * GEMMs), this gives each row's weighted loss and its logit gradient in one
+ * kernel, so the [T, V] logits never exist at once:
+ *   loss[r] = c_r (lse_r - x[r][y_r]),  grad[r][j] = c_r (softmax_r[j] - [j == y_r]);
+ * rows labelled ignore_index get loss 0 and a zero gradient; a label outside
+ * [0, vocab) gives a NaN loss. grad may be the logits buffer itself (ldg ==
+ * ld). Rows ld / ldg apart, 16-byte aligned. */
+int tt_ce_rows(int32_t dtype, const void* logits, int64_t ld, int32_t n_rows, int32_t vocab, const int32_t* labels,
+               const float* row_scale, int32_t ignore_index, float* loss, void* grad, int64_t ldg, void* stream);
+
 /* ---- device self-test ----------------------------------------------------
  * No counterpart in the reference. Runs one v_mfma_f32_32x32x16_bf16 with the
  * operand and accumulator lane layout the bf16 kernels assume:

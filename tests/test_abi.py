@@ -240,3 +240,15 @@ def test_prologue_bwd_validation():
                                   None) == _lib.TT_E_ARG
     assert lib.tt_qk_prologue_bwd(ctypes.byref(p), DQ, DK, V, V, ctypes.c_void_p(18), V, V, want,
                                   None) == _lib.TT_E_ARG
+
+
+def test_ce_rows_validation():
+    lib = _lib.lib()
+    V = ctypes.c_void_p(16)
+    args = lambda **kw: dict(dict(dtype=_lib.TT_DTYPE_BF16, ld=1000, n=4, vocab=1000, ldg=1000), **kw)
+    call = lambda a: lib.tt_ce_rows(a["dtype"], V, a["ld"], a["n"], a["vocab"], V, V, -100, V, V, a["ldg"], None)
+    assert call(args(dtype=5)) == _lib.TT_E_UNSUPPORTED
+    assert call(args(n=0)) == _lib.TT_E_ARG
+    assert call(args(ld=999)) == _lib.TT_E_ARG          # shorter than a row
+    assert call(args(ld=1004)) == _lib.TT_E_ARG         # rows not 16-byte aligned for bf16
+    assert call(args(ldg=500)) == _lib.TT_E_ARG

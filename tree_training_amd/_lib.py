@@ -36,7 +36,7 @@ EXPORTS = (
     "tt_meta_dense_mask", "tt_plan_bytes", "tt_plan_build", "tt_attn_fwd",
     "tt_attn_bwd_workspace_bytes", "tt_attn_bwd", "tt_gdn_workspace_bytes", "tt_gdn_tree_fwd",
     "tt_gdn_bwd_workspace_bytes", "tt_gdn_tree_bwd", "tt_tree_conv_fwd", "tt_tree_conv_bwd_workspace_bytes",
-    "tt_tree_conv_bwd", "tt_qk_prologue_fwd", "tt_qk_prologue_bwd_workspace_bytes", "tt_qk_prologue_bwd",
+    "tt_tree_conv_bwd", "tt_qk_prologue_fwd", "tt_qk_prologue_bwd_workspace_bytes", "tt_qk_prologue_bwd", "tt_ce_rows",
     "tt_selftest_mfma32",
 )
 
@@ -119,6 +119,7 @@ def _declare(lib):
         "tt_gdn_tree_bwd": (ctypes.c_int, [ctypes.POINTER(TTGdnProblem), TTTensor, P, P, P, P, P, P, SZ, VP]),
         "tt_tree_conv_fwd": (ctypes.c_int, [ctypes.POINTER(TTConvProblem), P, ctypes.c_int64, VP]),
         "tt_qk_prologue_fwd": (ctypes.c_int, [ctypes.POINTER(TTPrologueProblem), P, P, VP]),
+        "tt_ce_rows": (ctypes.c_int, [I32, P, ctypes.c_int64, I32, I32, P, P, I32, P, P, ctypes.c_int64, VP]),
         "tt_qk_prologue_bwd_workspace_bytes": (SZ, [ctypes.POINTER(TTPrologueProblem)]),
         "tt_qk_prologue_bwd": (ctypes.c_int, [ctypes.POINTER(TTPrologueProblem), TTTensor, TTTensor, P, P, P, P, P,
                                               SZ, VP]),

@@ -408,6 +408,18 @@ int tt_qk_prologue_bwd(const tt_prologue_problem* p, tt_tensor dq_out, tt_tensor
                                   (float*)ws, (hipStream_t)stream);
 }
 
+int tt_ce_rows(int32_t dtype, const void* logits, int64_t ld, int32_t n_rows, int32_t vocab, const int32_t* labels,
+               const float* row_scale, int32_t ignore_index, float* loss, void* grad, int64_t ldg, void* stream) {
+    if (dtype != TT_DTYPE_BF16 && dtype != TT_DTYPE_F32) return TT_E_UNSUPPORTED;
+    if (n_rows < 1 || vocab < 1 || !logits || !labels || !row_scale || !loss || !grad) return TT_E_ARG;
+    const int64_t gran = dtype == TT_DTYPE_BF16 ? 8 : 4;
+    if (ld < vocab || ldg < vocab || (ld % gran) || (ldg % gran) || !aligned(logits, 16) || !aligned(grad, 16) ||
+        !aligned(labels, 4) || !aligned(row_scale, 4) || !aligned(loss, 4))
+        return TT_E_ARG;
+    return tt_ce_rows_launch(dtype, logits, ld, n_rows, vocab, labels, row_scale, ignore_index, loss, grad, ldg,
+                             (hipStream_t)stream);
+}
+
 int tt_selftest_mfma32(const void* a, const void* b, float* d, void* stream) {
     if (!a || !b || !d || !aligned(a, 2) || !aligned(b, 2) || !aligned(d, 4)) return TT_E_ARG;
     return tt_selftest_mfma_launch(a, b, d, (hipStream_t)stream);

@@ -93,6 +93,10 @@ int tt_prologue_bwd_launch(const PrologueDev& p, const void* dq_out, int64_t dq_
                            int64_t dk_st, int64_t dk_sh, void* dq_raw, void* dk_raw, float* dqw, float* dkw,
                            float* ws, hipStream_t s);
 
+int tt_ce_rows_launch(int dtype, const void* logits, int64_t ld, int n_rows, int vocab, const int32_t* labels,
+                      const float* row_scale, int ignore_index, float* loss, void* grad, int64_t ldg,
+                      hipStream_t s);
+
 size_t tt_gdn_ws_bytes_impl(int n_chunks, int n_heads_v);
 int tt_gdn_fwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, void* out, float* states,
                       float* ws, hipStream_t s);

@@ -40,10 +40,23 @@ class DFSTreeResult:
                    for lg, lab in zip(self.leaf_logits, labels))
 
 
+def fused_ce_capable(model, leaf_loss_fn) -> bool:
+    """True when the leaf loss can be taken from the final hidden states with
+    the fused lm_head + cross-entropy (``loss.TreeCELoss`` on a causal LM whose
+    logits are plain ``lm_head(hidden)``)."""
+    from .loss import TreeCELoss
+    head = getattr(model, "lm_head", None)
+    return (isinstance(leaf_loss_fn, TreeCELoss) and hasattr(model, "model") and head is not None
+            and getattr(head, "bias", None) is None and hasattr(head, "weight")
+            and getattr(model.config, "final_logit_softcapping", None) is None)
+
+
 def run_tree_model(model, info: DFSTreeInfo, dev, pos_offset: int = 0, cache=None, accumulators=None,
-                   past_bias: Optional[torch.Tensor] = None, linear_attention_patched: bool = False):
+                   past_bias: Optional[torch.Tensor] = None, linear_attention_patched: bool = False,
+                   hidden_only: bool = False):
     """One model forward over a DFS-packed forest (or partition) with tree
-    attention. Returns the model output."""
+    attention. Returns the model output (the decoder's, with the final hidden
+    states and no logits, when ``hidden_only``)."""
     vocab = getattr(getattr(model, "config", None), "vocab_size", None)
     if vocab is not None and info.dfs_token_ids and not (0 <= min(info.dfs_token_ids) and
                                                          max(info.dfs_token_ids) < vocab):
@@ -56,8 +69,9 @@ def run_tree_model(model, info: DFSTreeInfo, dev, pos_offset: int = 0, cache=Non
     pos_t = meta.pos.long().unsqueeze(0)
     ctx = TreeAttnContext(plan=plan, cache=cache, accumulators=accumulators)
     with tree_attention_mode(model, linear_attention_patched):
-        return model(input_ids=ids_t, attention_mask=None, position_ids=pos_t,
-                     past_key_values=cache, use_cache=cache is not None, tree_ctx=ctx)
+        body = model.model if hidden_only else model
+        return body(input_ids=ids_t, attention_mask=None, position_ids=pos_t,
+                    past_key_values=cache, use_cache=cache is not None, tree_ctx=ctx)
 
 
 def dfs_tree_forward(model, roots: List[TreeNode], dtype: Optional[torch.dtype] = None) -> DFSTreeResult:

@@ -29,7 +29,8 @@ from typing import Callable, Dict, List, Optional, Tuple
 import torch
 import torch.nn.functional as F
 
-from .dfs_tree_forward import run_tree_model
+from .dfs_tree_forward import fused_ce_capable, run_tree_model
+from .loss import TreeCELoss
 from .gateway import GatewayAccumulator, GatewayCache
 from .tree import DFSTreeInfo, TreeNode, info_from_flat
 
@@ -259,25 +260,29 @@ def _chain_gateway_grads(gw: SubtreeGateway, retain_graph: bool = False, collect
 # ---------------------------------------------------------------------------
 # 4. one partition forward
 # ---------------------------------------------------------------------------
-def _subtree_forward(model, partition: SubtreePartition, gateway: Optional[SubtreeGateway], dev, dtype):
+def _subtree_forward(model, partition: SubtreePartition, gateway: Optional[SubtreeGateway], dev, dtype,
+                     hidden_only: bool = False):
     """Forward of one partition with its gateway (tree_grad_hybrid.py:279-427).
 
-    Returns (logits, dfs_info, own_kv, start, end, par, chunk_idx, copy_to_orig)."""
+    Returns (logits, or the final hidden states when ``hidden_only``, dfs_info,
+    own_kv, start, end, par, chunk_idx, copy_to_orig)."""
     info, start, end, par, cidx, c2o = _dfs_info_for_partition(partition)
     gate_kv = list(zip(gateway.key_gates, gateway.val_gates)) if gateway is not None else []
     cache = GatewayCache(gate_kv, segmented=True)
     out = run_tree_model(model, info, dev, pos_offset=partition.pos_offset, cache=cache,
                          accumulators=gateway.fp32_acc if gateway is not None else None,
-                         past_bias=gateway.attn_bias if gateway is not None else None)
+                         past_bias=gateway.attn_bias if gateway is not None else None, hidden_only=hidden_only)
     own_kv = [cache.own_kv(l) for l in sorted(cache._segments)]
-    return out.logits, info, own_kv, start, end, par, cidx, c2o
+    res = out.last_hidden_state if hidden_only else out.logits
+    return res, info, own_kv, start, end, par, cidx, c2o
 
 
 # ---------------------------------------------------------------------------
 # 5. driver
 # ---------------------------------------------------------------------------
 def tree_grad_hybrid(model, roots: List[TreeNode], leaf_loss_fn: Callable[[torch.Tensor, TreeNode], torch.Tensor],
-                     max_tokens: int, legacy_gateway_bias: bool = False, summed_backward: bool = False) -> None:
+                     max_tokens: int, legacy_gateway_bias: bool = False, summed_backward: bool = False,
+                     fused_leaf_ce: bool = True) -> None:
     """Hybrid tree training (tree_grad_hybrid.py:434-539); grads accumulate in ``.grad``.
 
     model        : HF causal LM (Qwen3 family), train mode, zero_grad() already called
@@ -290,9 +295,14 @@ def tree_grad_hybrid(model, roots: List[TreeNode], leaf_loss_fn: Callable[[torch
                    graph; True runs ONE backward per partition over the sum of
                    its leaf losses and its chain gradients (the same gradients
                    up to summation order).
+    fused_leaf_ce : with a ``make_tree_loss_fn`` loss, take the leaf losses from
+                   the final hidden states through the chunked lm_head + fused
+                   cross-entropy (no [T, V] logits), one backward per partition
+                   as with ``summed_backward``; other losses get logits.
     """
     dev = next(model.parameters()).device
     dtype = next(model.parameters()).dtype
+    fused = fused_leaf_ce and fused_ce_capable(model, leaf_loss_fn)
     partitions = partition_tree(roots, max_tokens)
     children_of: Dict[int, List[Tuple[TreeNode, SubtreePartition]]] = {id(p): [] for p in partitions}
     for p in partitions:
@@ -304,7 +314,8 @@ def tree_grad_hybrid(model, roots: List[TreeNode], leaf_loss_fn: Callable[[torch
     for p in partitions:                                   # top-down forward
         gw = gateways.get(id(p))
         p.pos_offset = gw.pos_offset if gw is not None else 0
-        logits, info, own_kv, s_map, e_map, par_map, ci_map, c2o = _subtree_forward(model, p, gw, dev, dtype)
+        logits, info, own_kv, s_map, e_map, par_map, ci_map, c2o = _subtree_forward(model, p, gw, dev, dtype,
+                                                                                     hidden_only=fused)
         fwd_cache[id(p)] = (logits, info, c2o)
         seen, cuts = set(), []
         for cn, _ in children_of[id(p)]:
@@ -331,12 +342,15 @@ def tree_grad_hybrid(model, roots: List[TreeNode], leaf_loss_fn: Callable[[torch
             if cgw is not None and id(cgw) not in seen_gw:
                 seen_gw.add(id(cgw))
                 chains.append(cgw)
-        if summed_backward:
+        if summed_backward or fused:
             pairs = []
             for cgw in chains:
                 _chain_gateway_grads(cgw, collect=pairs)
             roots_, grads_ = [t for t, _ in pairs], [g for _, g in pairs]
-            if leaf_chunks:
+            if leaf_chunks and fused:
+                roots_.append(leaf_loss_fn.fused_spans(logits[0], leaf_chunks, model.lm_head.weight))
+                grads_.append(None)
+            elif leaf_chunks:
                 roots_.append(sum(leaf_loss_fn(logits[:, s:e, :], leaf) for s, e, leaf in leaf_chunks))
                 grads_.append(None)
             if roots_:
@@ -355,15 +369,9 @@ def tree_grad_hybrid(model, roots: List[TreeNode], leaf_loss_fn: Callable[[torch
 
 
 def make_tree_loss_fn(leaf_labels: List[torch.Tensor], leaf_nodes: List[TreeNode], n_leaves: int,
-                      ignore_index: int = -100) -> Callable:
+                      ignore_index: int = -100) -> TreeCELoss:
     """CE(logits[0], labels, ignore_index) / n_leaves (tree_grad_hybrid.py:546-558)."""
-    label_map = {id(n): lab for n, lab in zip(leaf_nodes, leaf_labels)}
-
-    def _fn(logits: torch.Tensor, node: TreeNode) -> torch.Tensor:
-        labels = label_map[id(node)].to(logits.device)
-        return F.cross_entropy(logits[0], labels, ignore_index=ignore_index) / n_leaves
-
-    return _fn
+    return TreeCELoss(leaf_labels, leaf_nodes, n_leaves, ignore_index)
 
 
 # ---------------------------------------------------------------------------
