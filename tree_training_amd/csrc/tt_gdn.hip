@@ -41,6 +41,11 @@ constexpr int VP = VS + 4;        // row stride of [* x VS] tiles
 constexpr size_t kWsW = 0, kWsU = GC * GD, kWsA = 2 * GC * GD, kWsT = kWsA + GC * GC, kWsG = kWsT + GC * GC;
 constexpr size_t kWsChunk = kWsG + GC;
 
+template <int I>
+struct IntC4 {
+    static constexpr int value = I;
+};
+
 template <typename T>
 __device__ __forceinline__ void load16(const T* p, float (&x)[16]) {
     if constexpr (sizeof(T) == 2) {
@@ -262,67 +267,115 @@ __global__ __launch_bounds__(GT) void gdn_prep_kernel(GdnDev p, float* __restric
 }
 
 // ----------------------------------------------------------------------------
-// scan: per (node, v head, value slice), the node's chunks in order
+// scan: per (node, v head), the node's chunks in order, on fp32 MFMA
 // ----------------------------------------------------------------------------
+// v_mfma_f32_32x32x2_f32: D[32x32] += A[32x2] B[2x32]; lane l supplies
+// A[l & 31][l >> 5] and B[l >> 5][l & 31], and accumulator element r of lane l
+// is D[acc_row(r, l >> 5)][l & 31]. The contraction order is free, so step r
+// of a 32-deep contraction pairs k = acc_row(r, 0) (lanes 0-31) with
+// k = acc_row(r, 1) (lanes 32-63): a matrix held as accumulators (rows k,
+// columns j) is then directly the B operand, element r of each lane.
+__device__ __forceinline__ f32x16 mfma_f32(float a, float b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// Accumulator-layout access to a row-major fp32 matrix of GD-float rows:
+// element r of lane l is row ROW0 + acc_row(r, l >> 5), column `col`. One
+// buffer resource (scalar registers), four lane offsets (rows r % 4); the
+// uniform part of the row, ROW0 + 8 (r / 4), goes in the scalar offset.
+struct AccMat {
+    __amdgpu_buffer_rsrc_t rs;
+    int vo[4];
+};
+__device__ __forceinline__ AccMat acc_mat(const float* base, int rows, int half, int col) {
+    AccMat m;
+    m.rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, rows * GD * 4, 0x00020000);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) m.vo[k] = ((4 * half + k) * GD + col) * 4;
+    return m;
+}
+template <int ROW0>
+__device__ __forceinline__ f32x16 load_acc(const AccMat& m) {
+    f32x16 v;
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+        v[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(m.rs, m.vo[r & 3], (ROW0 + 8 * (r >> 2)) * GD * 4, 0));
+    return v;
+}
+template <int ROW0>
+__device__ __forceinline__ void store_acc(const AccMat& m, const f32x16& v) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[r]), m.rs, m.vo[r & 3], (ROW0 + 8 * (r >> 2)) * GD * 4, 0);
+}
+template <typename F>
+__device__ __forceinline__ void for_tiles(F&& f) {
+    f(IntC4<0>{});
+    f(IntC4<1>{});
+    f(IntC4<2>{});
+    f(IntC4<3>{});
+}
+
 struct ScanLds {
-    float S[GD * VP];     // state slice [Dk][VS]
+    float W[GC * RS];     // W [token][state row]
     float Q[GC * RS];     // q^ * scale
-    float K[GC * RS];     // k^
-    float W[GC * RS];
-    float Vp[GC * VP];    // V' slice
+    float K[GC * RS];     // k^ e^{G_L - G}
     float A[GC * MS];
     float G[GC];
 };
 
+// Wave w owns value columns 32w .. 32w+31 of one (node, v head): its 128 x 32
+// state slice lives in four accumulator tiles (rows 32 rb + acc_row(r, half))
+// for the whole node. Per chunk:
+//   V' = U - W S,  qS  (A = W / q^ rows from LDS, B = S from registers)
+//   O = e^G qS + A V'  (B = V' from registers)
+//   S <- e^{G_L} S + (k^ e^{G_L - G})^T V'  (A = k~ from LDS, B = V')
 // out may be null (the backward's recompute); chunk_sin / chunk_vp, when
 // given, receive each chunk's initial state and V' ([n_chunks, Hv, 128, 128]
 // and [n_chunks, Hv, 32, 128] floats).
 template <typename TIn>
-__global__ __launch_bounds__(GT) void gdn_scan_kernel(GdnDev p, int lvl_begin, const float* __restrict__ ws,
+__global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_scan_kernel(GdnDev p, int lvl_begin, const float* __restrict__ ws,
                                                       TIn* __restrict__ out, float* __restrict__ states,
                                                       float* __restrict__ chunk_sin, float* __restrict__ chunk_vp) {
     __shared__ __attribute__((aligned(16))) ScanLds L;
     const int node = p.level_nodes[lvl_begin + blockIdx.x];
     if (node < 0 || node >= p.n_nodes) return;
-    const int h = blockIdx.y, col0 = VS * blockIdx.z;
-    const int t = threadIdx.x;
+    const int h = blockIdx.y;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, col = lane & 31, half = lane >> 5;
+    const int j = 32 * wave + col;                                        // this lane's value column
     const int start = p.node_start[node], len = p.node_len[node], chunk0 = p.node_chunk0[node];
     int par = p.parent[node];
     if (start < 0 || len < 0 || start > p.n_tokens - len) return;        // malformed node: skipped
     if (chunk0 < 0 || chunk0 > p.n_chunks - tt_cdiv(len, GC)) return;
     if (par >= node || par < -1) par = -1;                               // parents precede children
 
-    // State slice: thread t owns rows sr0..sr0+3, columns sc..sc+3 (of the slice).
-    const int sr0 = 4 * (t >> 3), sc = 4 * (t & 7);
-    {
-        const float* src = par >= 0 ? states + ((size_t)par * p.hv + h) * GD * GD : nullptr;
+    f32x16 S[4];
+    if (par >= 0) {
+        const AccMat m = acc_mat(states + ((size_t)par * p.hv + h) * GD * GD, GD, half, j);
+        for_tiles([&](auto rb) { S[rb.value] = load_acc<32 * rb.value>(m); });
+    } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            f32x4 a = {};
-            if (src) a = *(const f32x4*)(src + (sr0 + r) * GD + col0 + sc);
-            *(f32x4*)&L.S[(sr0 + r) * VP + sc] = a;
-        }
+        for (int rb = 0; rb < 4; ++rb) S[rb] = (f32x16){};
     }
-    // [GC x VS] outputs: thread t owns row oi, columns oc..oc+3.
-    const int oi = t >> 3, oc = 4 * (t & 7);
 
     for (int c0 = 0; c0 < len; c0 += GC) {
         const int Lc = min(GC, len - c0);
         const size_t ch = (size_t)(chunk0 + c0 / GC) * p.hv + h;
         const float* cw = ws + ch * kWsChunk;
-        if (chunk_sin) {   // this thread's own state elements (written by it)
-            float* dst = chunk_sin + ch * GD * GD;
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                *(f32x4*)(dst + (sr0 + r) * GD + col0 + sc) = *(const f32x4*)&L.S[(sr0 + r) * VP + sc];
+        if (chunk_sin) {
+            const AccMat m = acc_mat(chunk_sin + ch * GD * GD, GD, half, j);
+            for_tiles([&](auto rb) { store_acc<32 * rb.value>(m, S[rb.value]); });
         }
         __syncthreads();   // readers of the previous chunk's tiles are done
         load_chunk_rows<TIn>(p, start + c0, Lc, h, L.Q, L.K, nullptr);
         {
             const int i = t >> 3, d0 = 16 * (t & 7);
+            const float ek = expf(cw[kWsG + GC - 1] - cw[kWsG + i]);
 #pragma unroll
-            for (int e = 0; e < 16; e += 4)
+            for (int e = 0; e < 16; e += 4) {   // rows written by this thread just above
+                *(f32x4*)&L.K[i * RS + d0 + e] *= ek;
                 *(f32x4*)&L.W[i * RS + d0 + e] = *(const f32x4*)(cw + kWsW + i * GD + d0 + e);
+            }
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int pi = t + GT * e;
@@ -330,73 +383,73 @@ __global__ __launch_bounds__(GT) void gdn_scan_kernel(GdnDev p, int lvl_begin, c
             }
             if (t < GC) L.G[t] = cw[kWsG + t];
         }
-        const f32x4 u = *(const f32x4*)(cw + kWsU + oi * GD + col0 + oc);
+        f32x16 vp = load_acc<0>(acc_mat(cw + kWsU, GC, half, j)), qs = {};
         __syncthreads();
 
-        // V' = U - W S and q^ S (both contract over the 128 state rows).
-        f32x4 vp = u, qs = {};
-#pragma unroll 2
-        for (int r0 = 0; r0 < GD; r0 += 4) {
-            const f32x4 wr = *(const f32x4*)&L.W[oi * RS + r0];
-            const f32x4 qr = *(const f32x4*)&L.Q[oi * RS + r0];
+        // V' = U - W S and q^ S: 4 row tiles of S x 16 steps.
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const f32x4 s = *(const f32x4*)&L.S[(r0 + rr) * VP + oc];
+        for (int rb = 0; rb < 4; ++rb) {
 #pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    vp[b] = fmaf(-wr[rr], s[b], vp[b]);
-                    qs[b] = fmaf(qr[rr], s[b], qs[b]);
+            for (int r4 = 0; r4 < 16; r4 += 4) {
+                const int k0 = 32 * rb + 8 * (r4 >> 2) + 4 * half;          // acc_row(r4 .. r4+3, half)
+                const f32x4 wv = *(const f32x4*)&L.W[col * RS + k0];
+                const f32x4 qv = *(const f32x4*)&L.Q[col * RS + k0];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    vp = mfma_f32(-wv[e], S[rb][r4 + e], vp);
+                    qs = mfma_f32(qv[e], S[rb][r4 + e], qs);
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);   // keep operand prefetch within one row tile (registers)
         }
-        *(f32x4*)&L.Vp[oi * VP + oc] = vp;
-        if (chunk_vp) *(f32x4*)(chunk_vp + ch * GC * GD + oi * GD + col0 + oc) = vp;
-        __syncthreads();   // V' complete; every reader of S for this chunk is done
-
+        if (chunk_vp) store_acc<0>(acc_mat(chunk_vp + ch * GC * GD, GC, half, j), vp);
         // O = e^G (q^ S) + A V'.
         {
-            f32x4 o = qs * expf(L.G[oi]);
-#pragma unroll 2
-            for (int j0 = 0; j0 < GC; j0 += 4) {
-                const f32x4 ar = *(const f32x4*)&L.A[oi * MS + j0];
+            f32x16 o;
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                    const f32x4 v = *(const f32x4*)&L.Vp[(j0 + jj) * VP + oc];
+            for (int r = 0; r < 16; ++r) o[r] = qs[r] * expf(L.G[acc_row(r, half)]);
 #pragma unroll
-                    for (int b = 0; b < 4; ++b) o[b] = fmaf(ar[jj], v[b], o[b]);
+            for (int r4 = 0; r4 < 16; r4 += 4) {
+                const f32x4 av = *(const f32x4*)&L.A[col * MS + 8 * (r4 >> 2) + 4 * half];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o = mfma_f32(av[e], vp[r4 + e], o);
+            }
+            if (out) {   // rows of the chunk; a buffer resource over them, lane offsets per row group
+                const int rs_b = p.hv * GD * (int)sizeof(TIn);
+                const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                    out + (int64_t)(start + c0) * p.hv * GD, (short)0, Lc * rs_b, 0x00020000);
+                int vo[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) vo[k] = (4 * half + k) * rs_b + (h * GD + j) * (int)sizeof(TIn);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    if (acc_row(r, half) >= Lc) continue;
+                    const int so = 8 * (r >> 2) * rs_b;
+                    if constexpr (sizeof(TIn) == 2)
+                        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (TIn)o[r]), rs,
+                                                              vo[r & 3], so, 0);
+                    else
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o[r]), rs, vo[r & 3], so, 0);
                 }
             }
-            if (out && oi < Lc) store4(out + ((int64_t)(start + c0 + oi) * p.hv + h) * GD + col0 + oc, o);
         }
-        // S <- e^{G_last} S + (k^ e^{G_last - G})^T V'.
+        // S <- e^{G_L} S + k~^T V': A[state row][token] = k~[token][state row].
         {
-            const float gl = L.G[GC - 1], el = expf(gl);
-            f32x4 s[4];
+            const float el = expf(L.G[GC - 1]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) s[r] = *(const f32x4*)&L.S[(sr0 + r) * VP + sc] * el;
-#pragma unroll 4
-            for (int i = 0; i < GC; ++i) {
-                const float kd = expf(gl - L.G[i]);
-                const f32x4 kr = *(const f32x4*)&L.K[i * RS + sr0] * kd;
-                const f32x4 v = *(const f32x4*)&L.Vp[i * VP + sc];
+            for (int rb = 0; rb < 4; ++rb) {
+                S[rb] *= el;
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) s[r][b] = fmaf(kr[r], v[b], s[r][b]);
+                for (int r = 0; r < 16; ++r) S[rb] = mfma_f32(L.K[acc_row(r, half) * RS + 32 * rb + col], vp[r], S[rb]);
+                __builtin_amdgcn_sched_barrier(0);
             }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) *(f32x4*)&L.S[(sr0 + r) * VP + sc] = s[r];
         }
     }
-    __syncthreads();
 
     // Final state of the node (the initial state of its children).
-    float* dst = states + ((size_t)node * p.hv + h) * GD * GD;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-        *(f32x4*)(dst + (sr0 + r) * GD + col0 + sc) = *(const f32x4*)&L.S[(sr0 + r) * VP + sc];
+    const AccMat m = acc_mat(states + ((size_t)node * p.hv + h) * GD * GD, GD, half, j);
+    for_tiles([&](auto rb) { store_acc<32 * rb.value>(m, S[rb.value]); });
 }
-
 
 // ----------------------------------------------------------------------------
 // backward
@@ -1002,11 +1055,11 @@ int tt_gdn_fwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_level
         const int b = level_offsets[l], n = level_offsets[l + 1] - b;
         if (n <= 0) continue;
         if (d.dtype == TT_DTYPE_BF16)
-            hipLaunchKernelGGL(gdn_scan_kernel<__bf16>, dim3(n, d.hv, NSL), dim3(GT), 0, s, d, b, ws,
-                               (__bf16*)out, states, nullptr, nullptr);
+            hipLaunchKernelGGL(gdn_scan_kernel<__bf16>, dim3(n, d.hv), dim3(GT), 0, s, d, b, ws, (__bf16*)out,
+                               states, nullptr, nullptr);
         else
-            hipLaunchKernelGGL(gdn_scan_kernel<float>, dim3(n, d.hv, NSL), dim3(GT), 0, s, d, b, ws,
-                               (float*)out, states, nullptr, nullptr);
+            hipLaunchKernelGGL(gdn_scan_kernel<float>, dim3(n, d.hv), dim3(GT), 0, s, d, b, ws, (float*)out,
+                               states, nullptr, nullptr);
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     return TT_OK;
@@ -1053,7 +1106,7 @@ static int gdn_bwd_run(const GdnDev& d, const int32_t* level_offsets, int n_leve
     for (int l = 0; l < n_levels; ++l) {
         const int b = level_offsets[l], n = level_offsets[l + 1] - b;
         if (n <= 0) continue;
-        hipLaunchKernelGGL(gdn_scan_kernel<TIn>, dim3(n, d.hv, NSL), dim3(GT), 0, s, d, b, w.prep, (TIn*)nullptr,
+        hipLaunchKernelGGL(gdn_scan_kernel<TIn>, dim3(n, d.hv), dim3(GT), 0, s, d, b, w.prep, (TIn*)nullptr,
                            w.nstate, w.sin, w.vp);
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
