@@ -501,56 +501,52 @@ __device__ __forceinline__ void tile_in(const T* base, int64_t row_stride, int l
 }
 
 struct RscanLds {
-    float S[GD * VP];     // dS slice [Dk][VS]
     float Q[GC * RS];     // e^G q^ * scale
     float K[GC * RS];     // e^{G_L - G} k^
     float W[GC * RS];
-    float dO[GC * VP];    // dO slice
-    float dV[GC * VP];    // dV' slice
     float A[GC * MS];
     float G[GC];
 };
 
+// Wave w owns value columns 32w .. 32w+31: its 128 x 32 slice of dS lives in
+// four accumulator tiles (as the forward's state), dO of the chunk is loaded
+// in accumulator layout (rows = tokens), and dV' is produced in it, so all
+// three are used straight from registers as MFMA B operands.
 template <typename TIn>
-__global__ __launch_bounds__(GT) void gdn_rscan_kernel(GdnDev p, int lvl_begin, const float* __restrict__ ws,
-                                                       const TIn* __restrict__ d_o, int64_t do_st, int64_t do_sh,
-                                                       float* __restrict__ chunk_dso, float* __restrict__ chunk_dvp,
-                                                       float* __restrict__ node_dsin) {
+__global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_rscan_kernel(
+        GdnDev p, int lvl_begin, const float* __restrict__ ws, const TIn* __restrict__ d_o, int64_t do_st,
+        int64_t do_sh, float* __restrict__ chunk_dso, float* __restrict__ chunk_dvp, float* __restrict__ node_dsin) {
     __shared__ __attribute__((aligned(16))) RscanLds L;
     const int node = p.level_nodes[lvl_begin + blockIdx.x];
     if (node < 0 || node >= p.n_nodes) return;
-    const int h = blockIdx.y, col0 = VS * blockIdx.z;
-    const int t = threadIdx.x;
+    const int h = blockIdx.y;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, col = lane & 31, half = lane >> 5;
+    const int j = 32 * wave + col;
     const int start = p.node_start[node], len = p.node_len[node], chunk0 = p.node_chunk0[node];
     if (start < 0 || len < 1 || start > p.n_tokens - len) return;        // malformed node: skipped
     if (chunk0 < 0 || chunk0 > p.n_chunks - tt_cdiv(len, GC)) return;
 
-    // dS slice: thread t owns rows sr0..sr0+3, columns sc..sc+3 (of the slice).
-    const int sr0 = 4 * (t >> 3), sc = 4 * (t & 7);
+    // dS after the node: the sum over its children of their dS at entry.
+    f32x16 dS[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) dS[rb] = (f32x16){};
     {
-        f32x4 acc[4] = {};
         const int c_lo = max(p.child_off[node], 0), c_hi = min(p.child_off[node + 1], p.n_nodes);
         for (int ci = c_lo; ci < c_hi; ++ci) {
             const int child = p.child[ci];
             if (child <= node || child >= p.n_nodes) continue;          // children follow their parent
-            const float* src = node_dsin + ((size_t)child * p.hv + h) * GD * GD;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] += *(const f32x4*)(src + (sr0 + r) * GD + col0 + sc);
+            const AccMat m = acc_mat(node_dsin + ((size_t)child * p.hv + h) * GD * GD, GD, half, j);
+            for_tiles([&](auto rb) { dS[rb.value] += load_acc<32 * rb.value>(m); });
         }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) *(f32x4*)&L.S[(sr0 + r) * VP + sc] = acc[r];
     }
-    const int oi = t >> 3, oc = 4 * (t & 7);
 
     for (int ci = tt_cdiv(len, GC) - 1; ci >= 0; --ci) {
         const int c0 = GC * ci, Lc = min(GC, len - c0);
         const size_t chn = (size_t)(chunk0 + ci) * p.hv + h;
         const float* cw = ws + chn * kWsChunk;
-        {   // the gradient of this chunk's output state (own elements)
-            float* dst = chunk_dso + chn * GD * GD;
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                *(f32x4*)(dst + (sr0 + r) * GD + col0 + sc) = *(const f32x4*)&L.S[(sr0 + r) * VP + sc];
+        {   // the gradient of this chunk's output state
+            const AccMat m = acc_mat(chunk_dso + chn * GD * GD, GD, half, j);
+            for_tiles([&](auto rb) { store_acc<32 * rb.value>(m, dS[rb.value]); });
         }
         __syncthreads();   // readers of the previous chunk's tiles are done
         load_chunk_rows<TIn>(p, start + c0, Lc, h, L.Q, L.K, nullptr);
@@ -570,56 +566,51 @@ __global__ __launch_bounds__(GT) void gdn_rscan_kernel(GdnDev p, int lvl_begin, 
                 L.A[(pi >> 5) * MS + (pi & 31)] = cw[kWsA + pi];
             }
             if (t < GC) L.G[t] = cw[kWsG + t];
-            f32x4 dov = {};
-            if (oi < Lc) dov = load4(d_o + (int64_t)(start + c0 + oi) * do_st + (int64_t)h * do_sh + col0 + oc);
-            *(f32x4*)&L.dO[oi * VP + oc] = dov;
+        }
+        f32x16 dov;   // dO[token acc_row(r, half)][j], zero past the chunk
+        {
+            const TIn* base = d_o + (int64_t)(start + c0) * do_st + (int64_t)h * do_sh + j;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int i = acc_row(r, half);
+                dov[r] = i < Lc ? (float)base[(int64_t)i * do_st] : 0.0f;
+            }
         }
         __syncthreads();
 
-        // dV'[oi] = sum_j A[j][oi] dO[j] + sum_r K[oi][r] dS[r]
-        f32x4 dv = {};
-#pragma unroll 4
-        for (int j = 0; j < GC; ++j) dv += L.A[j * MS + oi] * *(const f32x4*)&L.dO[j * VP + oc];
-#pragma unroll 2
-        for (int r0 = 0; r0 < GD; r0 += 4) {
-            const f32x4 kr = *(const f32x4*)&L.K[oi * RS + r0];
+        // dV' = A^T dO + k~ dS
+        f32x16 dv = {};
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const f32x4 sv = *(const f32x4*)&L.S[(r0 + rr) * VP + oc];
+        for (int r = 0; r < 16; ++r) dv = mfma_f32(L.A[acc_row(r, half) * MS + col], dov[r], dv);
 #pragma unroll
-                for (int b = 0; b < 4; ++b) dv[b] = fmaf(kr[rr], sv[b], dv[b]);
+        for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+            for (int r4 = 0; r4 < 16; r4 += 4) {
+                const f32x4 kv = *(const f32x4*)&L.K[col * RS + 32 * rb + 8 * (r4 >> 2) + 4 * half];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) dv = mfma_f32(kv[e], dS[rb][r4 + e], dv);
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        *(f32x4*)&L.dV[oi * VP + oc] = dv;
-        *(f32x4*)(chunk_dvp + chn * GC * GD + oi * GD + col0 + oc) = dv;
-        __syncthreads();   // dV' complete; every reader of dS for this chunk is done
+        store_acc<0>(acc_mat(chunk_dvp + chn * GC * GD, GC, half, j), dv);
 
-        // dS <- e^{G_L} dS + sum_i (Q[i][r] dO[i] - W[i][r] dV'[i])
-        {
-            const float el = expf(L.G[GC - 1]);
-            f32x4 sv[4];
+        // dS <- e^{G_L} dS + (e^G q^)^T dO - W^T dV'
+        const float el = expf(L.G[GC - 1]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) sv[r] = *(const f32x4*)&L.S[(sr0 + r) * VP + sc] * el;
-#pragma unroll 4
-            for (int i = 0; i < GC; ++i) {
-                const f32x4 qr = *(const f32x4*)&L.Q[i * RS + sr0];
-                const f32x4 wr = *(const f32x4*)&L.W[i * RS + sr0];
-                const f32x4 o = *(const f32x4*)&L.dO[i * VP + sc];
-                const f32x4 v = *(const f32x4*)&L.dV[i * VP + sc];
+        for (int rb = 0; rb < 4; ++rb) {
+            dS[rb] *= el;
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) sv[r][b] = fmaf(qr[r], o[b], fmaf(-wr[r], v[b], sv[r][b]));
+            for (int r = 0; r < 16; ++r) {
+                const int i = acc_row(r, half);
+                dS[rb] = mfma_f32(L.Q[i * RS + 32 * rb + col], dov[r], dS[rb]);
+                dS[rb] = mfma_f32(-L.W[i * RS + 32 * rb + col], dv[r], dS[rb]);
             }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) *(f32x4*)&L.S[(sr0 + r) * VP + sc] = sv[r];
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     // dS at the node's entry, summed into its parent by the next (shallower) level.
-    float* dst = node_dsin + ((size_t)node * p.hv + h) * GD * GD;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-        *(f32x4*)(dst + (sr0 + r) * GD + col0 + sc) = *(const f32x4*)&L.S[(sr0 + r) * VP + sc];
+    const AccMat m = acc_mat(node_dsin + ((size_t)node * p.hv + h) * GD * GD, GD, half, j);
+    for_tiles([&](auto rb) { store_acc<32 * rb.value>(m, dS[rb.value]); });
 }
 
 struct StateGradLds {
@@ -1113,8 +1104,8 @@ static int gdn_bwd_run(const GdnDev& d, const int32_t* level_offsets, int n_leve
     for (int l = n_levels - 1; l >= 0; --l) {
         const int b = level_offsets[l], n = level_offsets[l + 1] - b;
         if (n <= 0) continue;
-        hipLaunchKernelGGL(gdn_rscan_kernel<TIn>, dim3(n, d.hv, NSL), dim3(GT), 0, s, d, b, w.prep, d_o, do_st,
-                           do_sh, w.dso, w.dvp, w.dsn);
+        hipLaunchKernelGGL(gdn_rscan_kernel<TIn>, dim3(n, d.hv), dim3(GT), 0, s, d, b, w.prep, d_o, do_st, do_sh,
+                           w.dso, w.dvp, w.dsn);
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     hipLaunchKernelGGL(gdn_bwd_state_kernel<TIn>, dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, d_o, do_st, do_sh,
