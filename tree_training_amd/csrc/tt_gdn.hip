@@ -16,12 +16,13 @@
 //  * gdn_prep_kernel — one workgroup per (chunk, v head), all chunks at once:
 //    everything that does not depend on the state (A, T by a product of
 //    (I + N^(2^r)) factors, U, W, G) into the workspace.
-//  * gdn_scan_kernel — one workgroup per (node, v head, 32-column slice of
-//    the value dimension; the delta rule is independent per value column),
-//    one launch per tree level so a node's parent state (in the caller's
-//    node_states buffer) is complete when it starts; walks the node's chunks
-//    with its 128 x 32 state slice in LDS.
-// Every product is fp32 FMA on the vector ALUs (fp32 end to end).
+//  * gdn_scan_kernel — one workgroup per (node, v head), one launch per tree
+//    level so a node's parent state (in the caller's node_states buffer) is
+//    complete when it starts; each of its four waves holds a 128 x 32 value
+//    slice of the state in MFMA accumulators (the delta rule is independent
+//    per value column) and walks the node's chunks.
+// fp32 end to end: the prep on the vector ALUs, the scans on fp32 MFMA
+// (v_mfma_f32_32x32x2_f32).
 #include "tt_common.h"
 #include "tt_internal.h"
 
@@ -457,7 +458,7 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 // The backward recomputes the forward (prep + level scans, keeping each
 // chunk's initial state S and V'), then:
 //  * gdn_rscan_kernel — reverse level scan (deepest level first) of dS, the
-//    gradient of the state after a chunk, per (node, v head, value slice):
+//    gradient of the state after a chunk, per (node, v head), on fp32 MFMA:
 //      dV' = A^T dO + (e^{G_L - G} k^) dS,
 //      dS <- e^{G_L} dS + (e^G q^)^T dO - W^T dV'.
 //    A node's last chunk starts from the sum of its children's dS at entry
