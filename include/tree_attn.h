@@ -252,6 +252,23 @@ size_t tt_gdn_bwd_workspace_bytes(const tt_gdn_problem* p);
 int tt_gdn_tree_bwd(const tt_gdn_problem* p, tt_tensor d_o, void* dq, void* dk, void* dv, float* dg, float* dbeta,
                     void* ws, size_t ws_bytes, void* stream);
 
+/* The same forward and backward without the backward's recompute of the
+ * forward (what autograd keeps through the reference's torch function,
+ * tree_dfs_ssm.py:38-156, between its forward and backward):
+ * tt_gdn_tree_fwd_save computes o and node_states as tt_gdn_tree_fwd and also
+ * keeps, in `saved` (tt_gdn_saved_bytes: per (chunk, v head) the prep terms,
+ * the chunk's initial state and V', about 123 KiB), what the backward needs.
+ * tt_gdn_tree_bwd_saved then gives the gradients tt_gdn_tree_bwd gives, from
+ * `saved` (unchanged since, same problem and inputs) and a scratch workspace of
+ * tt_gdn_bwd_saved_workspace_bytes. */
+size_t tt_gdn_saved_bytes(const tt_gdn_problem* p);
+int tt_gdn_tree_fwd_save(const tt_gdn_problem* p, void* o, float* node_states, void* saved, size_t saved_bytes,
+                         void* stream);
+size_t tt_gdn_bwd_saved_workspace_bytes(const tt_gdn_problem* p);
+int tt_gdn_tree_bwd_saved(const tt_gdn_problem* p, tt_tensor d_o, void* dq, void* dk, void* dv, float* dg,
+                          float* dbeta, const void* saved, size_t saved_bytes, void* ws, size_t ws_bytes,
+                          void* stream);
+
 /* ---- tree-correct short convolution --------------------------------------
  * Replaces _tree_correct_conv_varlen (tree_dfs_ssm.py:284-346; twin
  * dfs_tree_forward.py:191-246): depthwise causal conv of kernel size K + SiLU

@@ -165,6 +165,32 @@ def test_gdn_bwd_validation():
                                *args(want)) == _lib.TT_E_UNSUPPORTED
 
 
+def test_gdn_saved_validation():
+    """Forward that keeps what the backward needs, and the backward from it."""
+    lib = _lib.lib()
+    V = ctypes.c_void_p(16)
+    DO = _lib.TTTensor(16, 32 * 128, 128)
+    p = _gdn_problem(node_child_off=16, node_child=16)
+    # per (chunk, v head): prep terms, initial state [128 x 128], V' [32 x 128]
+    saved = 5 * 32 * ((2 * 32 * 128 + 2 * 32 * 32 + 32) + 128 * 128 + 32 * 128) * 4
+    assert lib.tt_gdn_saved_bytes(ctypes.byref(p)) == saved
+    # scratch: dS [128 x 128], dV', X, dW, dK~ [32 x 128], <S, dS> per chunk; dS at entry per node
+    scratch = (5 * 32 * (128 * 128 + 4 * 32 * 128 + 1) + 3 * 32 * 128 * 128) * 4
+    assert lib.tt_gdn_bwd_saved_workspace_bytes(ctypes.byref(p)) == scratch
+    # the recomputing backward's workspace is the two plus the node states
+    assert lib.tt_gdn_bwd_workspace_bytes(ctypes.byref(p)) == saved + scratch + 3 * 32 * 128 * 128 * 4
+    assert lib.tt_gdn_tree_fwd_save(ctypes.byref(p), V, V, V, saved - 4, None) == _lib.TT_E_WORKSPACE
+    assert lib.tt_gdn_tree_fwd_save(ctypes.byref(p), V, V, None, saved, None) == _lib.TT_E_ARG
+    assert lib.tt_gdn_tree_fwd_save(ctypes.byref(p), V, V, ctypes.c_void_p(20), saved, None) == _lib.TT_E_ARG
+    args = lambda sv, sb, wb: (V, V, V, V, V, sv, sb, V, wb, None)
+    assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), DO, *args(V, saved - 4, scratch)) == _lib.TT_E_WORKSPACE
+    assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), DO, *args(V, saved, scratch - 4)) == _lib.TT_E_WORKSPACE
+    assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), DO, *args(None, saved, scratch)) == _lib.TT_E_ARG
+    assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(_gdn_problem()), DO, *args(V, saved, scratch)) == _lib.TT_E_ARG
+    assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), _lib.TTTensor(18, 32 * 128, 128),
+                                     *args(V, saved, scratch)) == _lib.TT_E_ARG
+
+
 def _conv_problem(**kw):
     p = _lib.TTConvProblem(dtype=_lib.TT_DTYPE_BF16, n_tokens=10, n_channels=8, kernel_size=4, x=16,
                            x_stride_tok=8, weight=16, bias=None, tok_prev=16, tok_next_off=16, tok_next=16)

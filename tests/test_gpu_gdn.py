@@ -185,3 +185,57 @@ def test_gdn_bwd_16k_tree_path_support():
         assert np.isfinite(a).all(), name
         assert np.array_equal(a[idx], b), name
         assert not np.any(a[off]), name
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("case", ["forest_multi_chunk", "c1_heads", "chain_ragged"])
+def test_gdn_saved_forward_equals_recompute(case, dtype):
+    """tt_gdn_tree_fwd_save + tt_gdn_tree_bwd_saved give bitwise the outputs,
+    node states and gradients of tt_gdn_tree_fwd + the recomputing
+    tt_gdn_tree_bwd (same kernels, same order of operations)."""
+    from tree_training_amd import gdn as tgdn
+    c = CASES[case]
+    lens, par = c["topo"]()
+    T = sum(lens)
+    q, k, v, g, beta = _inputs(T, c["Hk"], c["Hv"], 21 + sum(map(ord, case)), realistic_gates=True)
+    d_o = np.random.default_rng(13).standard_normal((T, c["Hv"], D)).astype(np.float32)
+    dev = torch.device("cuda", 0)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    tree = GdnTree(lens, par, dev)
+    args = (t(q).to(dtype), t(k).to(dtype), t(v).to(dtype), t(g), t(beta))
+    print(f"gdn saved vs recompute {case} {dtype}: T={T}", flush=True)
+    o0, st0 = gdn_tree_forward(*args, tree)
+    o1, st1, saved = tgdn._gdn_forward(*args, tree, None, True, True)
+    g0 = gdn_tree_backward(*args, t(d_o).to(dtype), tree)
+    g1 = gdn_tree_backward(*args, t(d_o).to(dtype), tree, saved=saved)
+    torch.cuda.synchronize()
+    assert torch.equal(o0, o1) and torch.equal(st0, st1)
+    for name, a, b in zip(BWD_NAMES, g0, g1):
+        assert torch.equal(a, b), name
+
+
+def test_gdn_autograd_keep_and_recompute_agree():
+    """The autograd Function with and without kept forward states: bitwise
+    the same gradients, and within the fp32 bar of the oracle."""
+    from tree_training_amd import gdn as tgdn
+    c = CASES["forest_multi_chunk"]
+    lens, par = c["topo"]()
+    T = sum(lens)
+    q, k, v, g, beta = _inputs(T, c["Hk"], c["Hv"], 77)
+    d_o = np.random.default_rng(14).standard_normal((T, c["Hv"], D)).astype(np.float32)
+    dev = torch.device("cuda", 0)
+    tree = GdnTree(lens, par, dev)
+    grads = []
+    for keep in (True, False):
+        tgdn.KEEP_FORWARD_STATES = keep
+        try:
+            tt = [torch.from_numpy(x).to(dev).requires_grad_(True) for x in (q, k, v, g, beta)]
+            o, _ = tgdn.gdn_tree(*tt, tree)
+            grads.append(torch.autograd.grad((o * torch.from_numpy(d_o).to(dev)).sum(), tt))
+        finally:
+            tgdn.KEEP_FORWARD_STATES = True
+    for name, a, b in zip(BWD_NAMES, *grads):
+        assert torch.equal(a, b), name
+    ref = _oracle_grads(q, k, v, g, beta, d_o, lens, par)
+    for name, a, b in zip(BWD_NAMES, grads[0], ref):
+        assert _rel(a.cpu().numpy(), b) < 1e-5, (name, _rel(a.cpu().numpy(), b))

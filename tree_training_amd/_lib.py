@@ -35,7 +35,8 @@ EXPORTS = (
     "tt_abi_version", "tt_strerror", "tt_meta_workspace_bytes", "tt_meta_build", "tt_keys_build",
     "tt_meta_dense_mask", "tt_plan_bytes", "tt_plan_build", "tt_attn_fwd",
     "tt_attn_bwd_workspace_bytes", "tt_attn_bwd", "tt_gdn_workspace_bytes", "tt_gdn_tree_fwd",
-    "tt_gdn_bwd_workspace_bytes", "tt_gdn_tree_bwd", "tt_tree_conv_fwd", "tt_tree_conv_bwd_workspace_bytes",
+    "tt_gdn_bwd_workspace_bytes", "tt_gdn_tree_bwd", "tt_gdn_saved_bytes", "tt_gdn_tree_fwd_save",
+    "tt_gdn_bwd_saved_workspace_bytes", "tt_gdn_tree_bwd_saved", "tt_tree_conv_fwd", "tt_tree_conv_bwd_workspace_bytes",
     "tt_tree_conv_bwd", "tt_qk_prologue_fwd", "tt_qk_prologue_bwd_workspace_bytes", "tt_qk_prologue_bwd", "tt_ce_rows",
     "tt_selftest_mfma32",
 )
@@ -117,6 +118,11 @@ def _declare(lib):
         "tt_gdn_tree_fwd": (ctypes.c_int, [ctypes.POINTER(TTGdnProblem), P, P, P, SZ, VP]),
         "tt_gdn_bwd_workspace_bytes": (SZ, [ctypes.POINTER(TTGdnProblem)]),
         "tt_gdn_tree_bwd": (ctypes.c_int, [ctypes.POINTER(TTGdnProblem), TTTensor, P, P, P, P, P, P, SZ, VP]),
+        "tt_gdn_saved_bytes": (SZ, [ctypes.POINTER(TTGdnProblem)]),
+        "tt_gdn_tree_fwd_save": (ctypes.c_int, [ctypes.POINTER(TTGdnProblem), P, P, P, SZ, VP]),
+        "tt_gdn_bwd_saved_workspace_bytes": (SZ, [ctypes.POINTER(TTGdnProblem)]),
+        "tt_gdn_tree_bwd_saved": (ctypes.c_int, [ctypes.POINTER(TTGdnProblem), TTTensor, P, P, P, P, P, P, SZ, P, SZ,
+                                                 VP]),
         "tt_tree_conv_fwd": (ctypes.c_int, [ctypes.POINTER(TTConvProblem), P, ctypes.c_int64, VP]),
         "tt_qk_prologue_fwd": (ctypes.c_int, [ctypes.POINTER(TTPrologueProblem), P, P, VP]),
         "tt_ce_rows": (ctypes.c_int, [I32, P, ctypes.c_int64, I32, I32, P, P, I32, P, P, ctypes.c_int64, VP]),

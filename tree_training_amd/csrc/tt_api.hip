@@ -267,26 +267,69 @@ int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* 
 
 size_t tt_gdn_bwd_workspace_bytes(const tt_gdn_problem* p) {
     if (!p || p->n_chunks < 1 || p->n_nodes < 1 || p->n_heads_v < 1) return 0;
-    return tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v);
+    return tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v, true);
 }
 
-int tt_gdn_tree_bwd(const tt_gdn_problem* p, tt_tensor d_o, void* dq, void* dk, void* dv, float* dg, float* dbeta,
-                    void* ws, size_t ws_bytes, void* stream) {
+size_t tt_gdn_saved_bytes(const tt_gdn_problem* p) {
+    if (!p || p->n_chunks < 1 || p->n_heads_v < 1) return 0;
+    return tt_gdn_saved_bytes_impl(p->n_chunks, p->n_heads_v);
+}
+
+int tt_gdn_tree_fwd_save(const tt_gdn_problem* p, void* o, float* node_states, void* saved, size_t saved_bytes,
+                         void* stream) {
     GdnDev d;
     const int rc = gdn_problem(p, d);
     if (rc != TT_OK) return rc;
+    if (!o || !node_states || !saved) return TT_E_ARG;
+    if (saved_bytes < tt_gdn_saved_bytes_impl(p->n_chunks, p->n_heads_v)) return TT_E_WORKSPACE;
+    if (!aligned(o, 16) || !aligned(node_states, 16) || !aligned(saved, 16)) return TT_E_ARG;
+    return tt_gdn_fwd_save_launch(d, p->level_offsets, p->n_levels, o, node_states, (float*)saved,
+                                  (hipStream_t)stream);
+}
+
+size_t tt_gdn_bwd_saved_workspace_bytes(const tt_gdn_problem* p) {
+    if (!p || p->n_chunks < 1 || p->n_nodes < 1 || p->n_heads_v < 1) return 0;
+    return tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v, false);
+}
+
+// Shared argument checks of the two backward entry points.
+static int gdn_bwd_args(const tt_gdn_problem* p, const tt_tensor& d_o, void* dq, void* dk, void* dv, float* dg,
+                        float* dbeta, void* ws) {
     if (!p->node_child_off || !p->node_child) return TT_E_ARG;
     if (!d_o.ptr || !dq || !dk || !dv || !dg || !dbeta || !ws) return TT_E_ARG;
     const int64_t gran = p->dtype == TT_DTYPE_BF16 ? 8 : 4;
     if (d_o.stride_tok < 128 || d_o.stride_head < 128 || (d_o.stride_tok % gran) || (d_o.stride_head % gran) ||
         !aligned(d_o.ptr, 16))
         return TT_E_ARG;
-    if (ws_bytes < tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v)) return TT_E_WORKSPACE;
     if (!aligned(dq, 16) || !aligned(dk, 16) || !aligned(dv, 16) || !aligned(ws, 16) || !aligned(dg, 4) ||
         !aligned(dbeta, 4))
         return TT_E_ARG;
+    return TT_OK;
+}
+
+int tt_gdn_tree_bwd(const tt_gdn_problem* p, tt_tensor d_o, void* dq, void* dk, void* dv, float* dg, float* dbeta,
+                    void* ws, size_t ws_bytes, void* stream) {
+    GdnDev d;
+    int rc = gdn_problem(p, d);
+    if (rc != TT_OK) return rc;
+    if ((rc = gdn_bwd_args(p, d_o, dq, dk, dv, dg, dbeta, ws)) != TT_OK) return rc;
+    if (ws_bytes < tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v, true)) return TT_E_WORKSPACE;
     return tt_gdn_bwd_launch(d, p->level_offsets, p->n_levels, d_o.ptr, d_o.stride_tok, d_o.stride_head, dq, dk,
-                             dv, dg, dbeta, (float*)ws, (hipStream_t)stream);
+                             dv, dg, dbeta, nullptr, (float*)ws, (hipStream_t)stream);
+}
+
+int tt_gdn_tree_bwd_saved(const tt_gdn_problem* p, tt_tensor d_o, void* dq, void* dk, void* dv, float* dg,
+                          float* dbeta, const void* saved, size_t saved_bytes, void* ws, size_t ws_bytes,
+                          void* stream) {
+    GdnDev d;
+    int rc = gdn_problem(p, d);
+    if (rc != TT_OK) return rc;
+    if ((rc = gdn_bwd_args(p, d_o, dq, dk, dv, dg, dbeta, ws)) != TT_OK) return rc;
+    if (!saved || !aligned(saved, 16)) return TT_E_ARG;
+    if (saved_bytes < tt_gdn_saved_bytes_impl(p->n_chunks, p->n_heads_v)) return TT_E_WORKSPACE;
+    if (ws_bytes < tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v, false)) return TT_E_WORKSPACE;
+    return tt_gdn_bwd_launch(d, p->level_offsets, p->n_levels, d_o.ptr, d_o.stride_tok, d_o.stride_head, dq, dk,
+                             dv, dg, dbeta, (const float*)saved, (float*)ws, (hipStream_t)stream);
 }
 
 }  // extern "C"

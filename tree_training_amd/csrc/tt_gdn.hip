@@ -1057,50 +1057,91 @@ int tt_gdn_fwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_level
     return TT_OK;
 }
 
-// Backward workspace, floats, in order: prep terms [n_chunks, Hv][kWsChunk];
-// per (chunk, v head) S and dS [128 x 128], V', dV', X, dW, dK~ [32 x 128];
-// per (node, v head) the node's final state and its dS at entry [128 x 128];
-// <S, dS> per (chunk, v head).
+// The backward's float buffers. "Saved" (what the forward can keep for it):
+// per (chunk, v head) the prep terms [kWsChunk], the chunk's initial state S
+// [128 x 128] and V' [32 x 128]. Scratch: per (chunk, v head) dS [128 x 128],
+// dV', X, dW, dK~ [32 x 128]; per (node, v head) dS at entry [128 x 128]; when
+// the backward recomputes the forward, the node states [128 x 128]; <S, dS>
+// per (chunk, v head) last (it breaks 16-byte alignment).
 namespace {
 struct GdnBwdWs {
-    float *prep, *sin, *dso, *vp, *dvp, *x, *dw, *dkt, *nstate, *dsn, *sdot;
+    float *prep, *sin, *vp, *dso, *dvp, *x, *dw, *dkt, *dsn, *nstate, *sdot;
 };
-GdnBwdWs gdn_bwd_carve(float* base, size_t n_chunks, size_t n_nodes, size_t hv) {
+size_t gdn_saved_floats(size_t ch) { return ch * (kWsChunk + GD * GD + GC * GD); }
+size_t gdn_scratch_floats(size_t ch, size_t nd, bool recompute) {
+    return ch * (GD * GD + 4 * GC * GD + 1) + nd * GD * GD * (recompute ? 2 : 1);
+}
+GdnBwdWs gdn_bwd_carve(float* saved, float* scratch, size_t n_chunks, size_t n_nodes, size_t hv, bool recompute) {
     const size_t ch = n_chunks * hv, nd = n_nodes * hv;
     GdnBwdWs w;
-    float* q = base;
+    float* q = saved;
     w.prep = q; q += ch * kWsChunk;
     w.sin = q; q += ch * GD * GD;
+    w.vp = q;
+    q = scratch;
     w.dso = q; q += ch * GD * GD;
-    w.vp = q; q += ch * GC * GD;
     w.dvp = q; q += ch * GC * GD;
     w.x = q; q += ch * GC * GD;
     w.dw = q; q += ch * GC * GD;
     w.dkt = q; q += ch * GC * GD;
-    w.nstate = q; q += nd * GD * GD;
     w.dsn = q; q += nd * GD * GD;
-    w.sdot = q; q += ch;
+    w.nstate = nullptr;
+    if (recompute) { w.nstate = q; q += nd * GD * GD; }
+    w.sdot = q;
     return w;
 }
 }  // namespace
 
-size_t tt_gdn_bwd_ws_bytes_impl(int n_chunks, int n_nodes, int n_heads_v) {
+size_t tt_gdn_saved_bytes_impl(int n_chunks, int n_heads_v) {
+    return gdn_saved_floats((size_t)n_chunks * n_heads_v) * sizeof(float);
+}
+size_t tt_gdn_bwd_ws_bytes_impl(int n_chunks, int n_nodes, int n_heads_v, bool recompute) {
     const size_t ch = (size_t)n_chunks * n_heads_v, nd = (size_t)n_nodes * n_heads_v;
-    return (ch * (kWsChunk + 2 * GD * GD + 5 * GC * GD + 1) + nd * 2 * GD * GD) * sizeof(float);
+    return ((recompute ? gdn_saved_floats(ch) : 0) + gdn_scratch_floats(ch, nd, recompute)) * sizeof(float);
 }
 
-template <typename TIn>
-static int gdn_bwd_run(const GdnDev& d, const int32_t* level_offsets, int n_levels, const TIn* d_o, int64_t do_st,
-                       int64_t do_sh, TIn* dq, TIn* dk, TIn* dv, float* dg, float* dbeta, float* ws, hipStream_t s) {
-    const GdnBwdWs w = gdn_bwd_carve(ws, d.n_chunks, d.n_nodes, d.hv);
-    hipLaunchKernelGGL(gdn_prep_kernel<TIn>, dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, w.prep);
+int tt_gdn_fwd_save_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, void* out, float* states,
+                           float* saved, hipStream_t s) {
+    const GdnBwdWs w = gdn_bwd_carve(saved, nullptr, d.n_chunks, d.n_nodes, d.hv, false);
+    if (d.dtype == TT_DTYPE_BF16)
+        hipLaunchKernelGGL(gdn_prep_kernel<__bf16>, dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, w.prep);
+    else
+        hipLaunchKernelGGL(gdn_prep_kernel<float>, dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, w.prep);
     if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     for (int l = 0; l < n_levels; ++l) {
         const int b = level_offsets[l], n = level_offsets[l + 1] - b;
         if (n <= 0) continue;
-        hipLaunchKernelGGL(gdn_scan_kernel<TIn>, dim3(n, d.hv), dim3(GT), 0, s, d, b, w.prep, (TIn*)nullptr,
-                           w.nstate, w.sin, w.vp);
+        if (d.dtype == TT_DTYPE_BF16)
+            hipLaunchKernelGGL(gdn_scan_kernel<__bf16>, dim3(n, d.hv), dim3(GT), 0, s, d, b, w.prep, (__bf16*)out,
+                               states, w.sin, w.vp);
+        else
+            hipLaunchKernelGGL(gdn_scan_kernel<float>, dim3(n, d.hv), dim3(GT), 0, s, d, b, w.prep, (float*)out,
+                               states, w.sin, w.vp);
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+    }
+    return TT_OK;
+}
+
+// saved == nullptr: recompute the forward into the front of ws; otherwise
+// saved holds what tt_gdn_fwd_save_launch wrote for the same problem.
+template <typename TIn>
+static int gdn_bwd_run(const GdnDev& d, const int32_t* level_offsets, int n_levels, const TIn* d_o, int64_t do_st,
+                       int64_t do_sh, TIn* dq, TIn* dk, TIn* dv, float* dg, float* dbeta, const float* saved,
+                       float* ws, hipStream_t s) {
+    const bool recompute = saved == nullptr;
+    float* sv = recompute ? ws : const_cast<float*>(saved);
+    float* scratch = recompute ? ws + gdn_saved_floats((size_t)d.n_chunks * d.hv) : ws;
+    const GdnBwdWs w = gdn_bwd_carve(sv, scratch, d.n_chunks, d.n_nodes, d.hv, recompute);
+    if (recompute) {
+        hipLaunchKernelGGL(gdn_prep_kernel<TIn>, dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, w.prep);
+        if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+        for (int l = 0; l < n_levels; ++l) {
+            const int b = level_offsets[l], n = level_offsets[l + 1] - b;
+            if (n <= 0) continue;
+            hipLaunchKernelGGL(gdn_scan_kernel<TIn>, dim3(n, d.hv), dim3(GT), 0, s, d, b, w.prep, (TIn*)nullptr,
+                               w.nstate, w.sin, w.vp);
+            if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+        }
     }
     for (int l = n_levels - 1; l >= 0; --l) {
         const int b = level_offsets[l], n = level_offsets[l + 1] - b;
@@ -1119,11 +1160,11 @@ static int gdn_bwd_run(const GdnDev& d, const int32_t* level_offsets, int n_leve
 }
 
 int tt_gdn_bwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, const void* d_o, int64_t do_st,
-                      int64_t do_sh, void* dq, void* dk, void* dv, float* dg, float* dbeta, float* ws,
-                      hipStream_t s) {
+                      int64_t do_sh, void* dq, void* dk, void* dv, float* dg, float* dbeta, const float* saved,
+                      float* ws, hipStream_t s) {
     if (d.dtype == TT_DTYPE_BF16)
         return gdn_bwd_run<__bf16>(d, level_offsets, n_levels, (const __bf16*)d_o, do_st, do_sh, (__bf16*)dq,
-                                   (__bf16*)dk, (__bf16*)dv, dg, dbeta, ws, s);
+                                   (__bf16*)dk, (__bf16*)dv, dg, dbeta, saved, ws, s);
     return gdn_bwd_run<float>(d, level_offsets, n_levels, (const float*)d_o, do_st, do_sh, (float*)dq, (float*)dk,
-                              (float*)dv, dg, dbeta, ws, s);
+                              (float*)dv, dg, dbeta, saved, ws, s);
 }

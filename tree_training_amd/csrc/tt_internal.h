@@ -100,10 +100,13 @@ int tt_ce_rows_launch(int dtype, const void* logits, int64_t ld, int n_rows, int
 size_t tt_gdn_ws_bytes_impl(int n_chunks, int n_heads_v);
 int tt_gdn_fwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, void* out, float* states,
                       float* ws, hipStream_t s);
-size_t tt_gdn_bwd_ws_bytes_impl(int n_chunks, int n_nodes, int n_heads_v);
+size_t tt_gdn_saved_bytes_impl(int n_chunks, int n_heads_v);
+int tt_gdn_fwd_save_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, void* out, float* states,
+                           float* saved, hipStream_t s);
+size_t tt_gdn_bwd_ws_bytes_impl(int n_chunks, int n_nodes, int n_heads_v, bool recompute);
 int tt_gdn_bwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, const void* d_o, int64_t do_st,
-                      int64_t do_sh, void* dq, void* dk, void* dv, float* dg, float* dbeta, float* ws,
-                      hipStream_t s);
+                      int64_t do_sh, void* dq, void* dk, void* dv, float* dg, float* dbeta, const float* saved,
+                      float* ws, hipStream_t s);
 
 size_t tt_meta_ws_bytes_impl(int n);
 int tt_meta_build_impl(const int32_t* len, const int32_t* par, int n, int T, int pos_offset, int32_t* start,

@@ -169,28 +169,48 @@ def _problem(q, k, v, g, beta, tree: GdnTree, scale, l2norm):
     return p, (q, k, v, g, beta)
 
 
-def gdn_tree_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
-                     tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True):
-    """o [T, Hv, 128] (dtype of v) and node_states [n_nodes, Hv, 128, 128]
-    (float32; the state after each node)."""
+# Whether the autograd Function keeps the forward's per-chunk terms and states
+# for the backward (tt_gdn_tree_fwd_save / tt_gdn_tree_bwd_saved: about 123 KiB
+# per (32-token chunk, v head) held from forward to backward, 2.1 GB for a
+# 16K-token tree with 32 v heads) instead of recomputing them in the backward.
+KEEP_FORWARD_STATES = True
+
+
+def _gdn_forward(q, k, v, g, beta, tree: GdnTree, scale, l2norm, keep: bool):
     p, (q, k, v, g, beta) = _problem(q, k, v, g, beta, tree, scale, l2norm)
     T, Hv = v.shape[0], v.shape[1]
     dev = require_device(q.device)
     o = torch.empty((T, Hv, HEAD_DIM), dtype=v.dtype, device=dev)
     states = torch.empty((tree.n_nodes, Hv, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=dev)
     lib = _lib.lib()
+    if keep:
+        saved_bytes = lib.tt_gdn_saved_bytes(ctypes.byref(p))
+        saved = torch.empty(saved_bytes, dtype=torch.uint8, device=dev)
+        _lib.check(lib.tt_gdn_tree_fwd_save(ctypes.byref(p), _ptr(o), _ptr(states), _ptr(saved), saved_bytes,
+                                            _stream(dev)), "tt_gdn_tree_fwd_save")
+        return o, states, saved
     ws_bytes = lib.tt_gdn_workspace_bytes(ctypes.byref(p))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     _lib.check(lib.tt_gdn_tree_fwd(ctypes.byref(p), _ptr(o), _ptr(states), _ptr(ws), ws_bytes, _stream(dev)),
                "tt_gdn_tree_fwd")
+    return o, states, None
+
+
+def gdn_tree_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
+                     tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True):
+    """o [T, Hv, 128] (dtype of v) and node_states [n_nodes, Hv, 128, 128]
+    (float32; the state after each node)."""
+    o, states, _ = _gdn_forward(q, k, v, g, beta, tree, scale, l2norm, False)
     return o, states
 
 
 def gdn_tree_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
-                      d_o: torch.Tensor, tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True):
+                      d_o: torch.Tensor, tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True,
+                      saved: Optional[torch.Tensor] = None):
     """Gradients of sum(o * d_o) for ``gdn_tree_forward``'s o: dq, dk [T, Hk,
     128] and dv [T, Hv, 128] in the dtype of v, dg and dbeta [T, Hv] float32.
-    Recomputes the forward internally (tt_gdn_tree_bwd)."""
+    Recomputes the forward internally (tt_gdn_tree_bwd) unless ``saved`` holds
+    what tt_gdn_tree_fwd_save kept for the same inputs (tt_gdn_tree_bwd_saved)."""
     p, (q, k, v, g, beta) = _problem(q, k, v, g, beta, tree, scale, l2norm)
     d_o = _tok_heads(d_o, "d_o").to(v.dtype)
     T, Hk, Hv = q.shape[0], q.shape[1], v.shape[1]
@@ -203,36 +223,53 @@ def gdn_tree_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torc
     dg = torch.empty((T, Hv), dtype=torch.float32, device=dev)
     dbeta = torch.empty_like(dg)
     lib = _lib.lib()
+    dot = _lib.TTTensor(d_o.data_ptr(), d_o.stride(0), d_o.stride(1))
+    if saved is not None:
+        ws_bytes = lib.tt_gdn_bwd_saved_workspace_bytes(ctypes.byref(p))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        _lib.check(lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), dot, _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg),
+                                             _ptr(dbeta), _ptr(saved), saved.numel(), _ptr(ws), ws_bytes,
+                                             _stream(dev)), "tt_gdn_tree_bwd_saved")
+        return dq, dk, dv, dg, dbeta
     ws_bytes = lib.tt_gdn_bwd_workspace_bytes(ctypes.byref(p))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    _lib.check(lib.tt_gdn_tree_bwd(ctypes.byref(p), _lib.TTTensor(d_o.data_ptr(), d_o.stride(0), d_o.stride(1)),
-                                   _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(dbeta), _ptr(ws), ws_bytes,
-                                   _stream(dev)), "tt_gdn_tree_bwd")
+    _lib.check(lib.tt_gdn_tree_bwd(ctypes.byref(p), dot, _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(dbeta),
+                                   _ptr(ws), ws_bytes, _stream(dev)), "tt_gdn_tree_bwd")
     return dq, dk, dv, dg, dbeta
 
 
 class GdnTreeFunction(torch.autograd.Function):
-    """Differentiable tree GDN: forward ``tt_gdn_tree_fwd``, backward
-    ``tt_gdn_tree_bwd`` (the node states are returned without a gradient)."""
+    """Differentiable tree GDN: forward ``tt_gdn_tree_fwd_save`` (or
+    ``tt_gdn_tree_fwd``), backward ``tt_gdn_tree_bwd_saved`` (or the
+    recomputing ``tt_gdn_tree_bwd``), as ``KEEP_FORWARD_STATES`` says. The
+    node states are returned without a gradient."""
 
     @staticmethod
     def forward(ctx, q, k, v, g, beta, tree, scale, l2norm):
-        o, states = gdn_tree_forward(q, k, v, g, beta, tree, scale, l2norm)
+        keep = bool(KEEP_FORWARD_STATES)
+        o, states, saved = _gdn_forward(q, k, v, g, beta, tree, scale, l2norm, keep)
         ctx.save_for_backward(q, k, v, g, beta)
         ctx.tree, ctx.scale, ctx.l2norm = tree, scale, l2norm
+        ctx.gdn_saved = saved
         ctx.mark_non_differentiable(states)
         return o, states
 
     @staticmethod
     def backward(ctx, d_o, _d_states):
         q, k, v, g, beta = ctx.saved_tensors
-        dq, dk, dv, dg, dbeta = gdn_tree_backward(q, k, v, g, beta, d_o, ctx.tree, ctx.scale, ctx.l2norm)
+        dq, dk, dv, dg, dbeta = gdn_tree_backward(q, k, v, g, beta, d_o, ctx.tree, ctx.scale, ctx.l2norm,
+                                                  saved=ctx.gdn_saved)
+        ctx.gdn_saved = None
         return (dq.reshape(q.shape).to(q.dtype), dk.reshape(k.shape).to(k.dtype), dv.reshape(v.shape).to(v.dtype),
                 dg.reshape(g.shape).to(g.dtype), dbeta.reshape(beta.shape).to(beta.dtype), None, None, None)
 
 
 def gdn_tree(q, k, v, g, beta, tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True):
-    """Autograd-aware ``gdn_tree_forward``: (o, node_states)."""
+    """Autograd-aware ``gdn_tree_forward``: (o, node_states). When any input
+    requires a gradient and ``KEEP_FORWARD_STATES`` is set, the forward keeps
+    its chunk terms and states for the backward."""
+    if not (torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, g, beta))):
+        return gdn_tree_forward(q, k, v, g, beta, tree, scale, l2norm)
     return GdnTreeFunction.apply(q, k, v, g, beta, tree, scale, l2norm)
 
 
