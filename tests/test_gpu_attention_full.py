@@ -1,0 +1,191 @@
+"""Full-size parity of the bf16 tree attention (the 16K agent tree and the 48K
+rollout tree, 32 q / 8 kv heads, d 128), through size-independent properties.
+
+A DFS-packed tree attention restricted to one root-to-leaf path is plain
+causal attention over that path's tokens. So for sampled leaves:
+  * the tree forward's outputs and log-sum-exps on the path's tokens equal
+    causal GQA attention over the path (torch, float32, on the same
+    bf16-rounded inputs);
+  * with dO non-zero only on the path, the tree backward's dq, dk, dv on the
+    path equal that attention's gradients, and every other token's dq, dk, dv
+    is exactly zero (no other query carries a gradient, and no other key is
+    seen by a path query).
+And the 16K tree cut into tree_grad_hybrid's 4096-token partitions, each
+attending to its gateway prefix, gives the whole tree's outputs and gradients
+(gateway gradients accumulated in fp32 and scattered back to their tokens).
+Bars: bf16 max_rel < 2e-2 (max |error| over max |reference|) for o, dq, dk,
+dv; |lse error| < 2e-2.
+"""
+import numpy as np
+import pytest
+import torch
+
+from tree_training_amd import workloads
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+HQ, HKV, D = 32, 8, 128
+REP = HQ // HKV
+
+
+def _path_tokens(lens, par, leaf):
+    starts = np.concatenate([[0], np.cumsum(lens)[:-1]])
+    path, j = [], leaf
+    while j >= 0:
+        path.append(j)
+        j = par[j]
+    return np.concatenate([np.arange(starts[i], starts[i] + lens[i]) for i in path[::-1]])
+
+
+def _causal_reference(q, k, v, do, scale):
+    """Causal GQA attention over one sequence and its gradients, float32:
+    q, do [L, HQ, D]; k, v [L, HKV, D]. Returns o, lse [HQ, L], dq, dk, dv."""
+    L = q.shape[0]
+    causal = torch.ones(L, L, dtype=torch.bool, device=q.device).tril()
+    o = torch.empty_like(q)
+    lse = torch.empty(HQ, L, device=q.device)
+    dq = torch.empty_like(q)
+    dk = torch.zeros_like(k)
+    dv = torch.zeros_like(v)
+    for h in range(HQ):
+        g = h // REP
+        qh, kh, vh, doh = (q[:, h].contiguous(), k[:, g].contiguous(), v[:, g].contiguous(),
+                           do[:, h].contiguous())
+        s = (qh @ kh.t().contiguous()) * scale
+        s = s.masked_fill(~causal, float("-inf"))
+        m = s.max(dim=1, keepdim=True).values
+        e = torch.exp(s - m)
+        z = e.sum(dim=1, keepdim=True)
+        p = e / z
+        oh = p @ vh
+        o[:, h] = oh
+        lse[h] = (m + torch.log(z))[:, 0]
+        dp = doh @ vh.t().contiguous()
+        ds = p * (dp - (doh * oh).sum(dim=1, keepdim=True))
+        dq[:, h] = (ds @ kh) * scale
+        dk[:, g] += (ds.t().contiguous() @ qh) * scale
+        dv[:, g] += p.t().contiguous() @ doh
+    return o, lse, dq, dk, dv
+
+
+def _max_rel(ref, got):
+    return float((got - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
+
+
+@pytest.mark.parametrize("workload,n_paths", [("agent16k", 3), ("rollout48k", 2)])
+def test_attention_full_size_per_path(workload, n_paths):
+    from tree_training_amd.attention import attn_backward, attn_forward
+    from tree_training_amd.meta import KeyPlan, TreeMetaDevice
+    lens, par = workloads.agent_tree(0) if workload == "agent16k" else workloads.rollout_tree(0)
+    T = sum(lens)
+    g = torch.Generator(device=DEV).manual_seed(3)
+    bf = torch.bfloat16
+    q = torch.randn(T, HQ, D, device=DEV, generator=g, dtype=bf)
+    k = torch.randn(T, HKV, D, device=DEV, generator=g, dtype=bf)
+    v = torch.randn(T, HKV, D, device=DEV, generator=g, dtype=bf)
+    scale = D ** -0.5
+    meta = TreeMetaDevice(lens, par, device=DEV)
+    plan = KeyPlan(meta.horizon, None)
+    view = lambda x: x[None].transpose(1, 2)   # [1, H, T, D] views of token-major storage
+    o, lse = attn_forward(view(q), view(k), view(v), plan, scale)
+    leaves = [i for i in range(len(lens)) if i not in set(par)]
+    rng = np.random.default_rng(7)
+    for leaf in rng.choice(leaves, size=n_paths, replace=False):
+        idx = _path_tokens(lens, par, int(leaf))
+        print(f"{workload}: leaf {leaf}, path of {len(idx)} tokens", flush=True)
+        ti = torch.from_numpy(idx).to(DEV)
+        do = torch.zeros(T, HQ, D, device=DEV, dtype=bf)
+        do[ti] = torch.randn(len(idx), HQ, D, device=DEV, generator=g, dtype=bf)
+        dq, dk, dv = attn_backward(view(q), view(k), view(v), plan, scale, o, lse, do[None])
+        ro, rlse, rdq, rdk, rdv = _causal_reference(q[ti].float(), k[ti].float(), v[ti].float(),
+                                                    do[ti].float(), scale)
+        torch.cuda.synchronize()
+        assert _max_rel(ro, o[ti].float()) < 2e-2
+        assert float((lse[:, ti] - rlse).abs().max()) < 2e-2
+        for name, ref, got in (("dq", rdq, dq), ("dk", rdk, dk), ("dv", rdv, dv)):
+            gf = got.float()
+            assert torch.isfinite(gf).all(), name
+            r = _max_rel(ref, gf[ti])
+            assert r < 2e-2, (workload, int(leaf), name, r)
+            off = torch.ones(T, dtype=torch.bool, device=DEV)
+            off[ti] = False
+            assert not gf[off].any(), (workload, int(leaf), name, "non-zero off the path")
+
+
+def test_attention_gateway_partitions_full_size():
+    """The 16K agent tree split with max_tokens=4096 (tree_grad_hybrid's
+    partitions; each child partition attends to its gateway: the parent's
+    gateway plus the parent's tokens up to the cut node, with the inherited
+    ancestor-aware bias) gives the whole tree's attention: per partition, o and
+    dq on its tokens equal the whole-tree run's, and each token's dk, dv —
+    its own partition's plus what every descendant partition accumulated into
+    its gateway entry (fp32) — equal the whole-tree run's."""
+    from tree_training_amd.attention import attn_backward, attn_forward
+    from tree_training_amd.hybrid import _flatten_partition, hybrid_plan, partition_tree
+    from tree_training_amd.meta import KeyPlan, TreeMetaDevice
+    from tree_training_amd.tree import TreeNode
+    topo = workloads.agent_tree(0)
+    lens, par = topo
+    T = sum(lens)
+    starts = np.concatenate([[0], np.cumsum(lens)[:-1]])
+    roots, nodes = workloads.forest_from_topology(topo, TreeNode)
+    gidx = {id(n): i for i, n in enumerate(nodes)}
+    parts = partition_tree(roots, 4096)
+    plans = hybrid_plan(roots, 4096)
+    assert len(parts) == len(plans) > 1
+    g = torch.Generator(device=DEV).manual_seed(5)
+    bf = torch.bfloat16
+    q = torch.randn(T, HQ, D, device=DEV, generator=g, dtype=bf)
+    k = torch.randn(T, HKV, D, device=DEV, generator=g, dtype=bf)
+    v = torch.randn(T, HKV, D, device=DEV, generator=g, dtype=bf)
+    do = torch.randn(T, HQ, D, device=DEV, generator=g, dtype=bf)
+    scale = D ** -0.5
+    view = lambda x: x[None].transpose(1, 2)
+    plan = KeyPlan(TreeMetaDevice(lens, par, device=DEV).horizon, None)
+    o, lse = attn_forward(view(q), view(k), view(v), plan, scale)
+    dq, dk, dv = attn_backward(view(q), view(k), view(v), plan, scale, o, lse, do[None])
+
+    own_tokens, prefix_tokens = {}, {}
+    sum_dk = torch.zeros(T, HKV, D, device=DEV)
+    sum_dv = torch.zeros(T, HKV, D, device=DEV)
+    for p, pl in zip(parts, plans):
+        node_len, parent, pnodes = _flatten_partition(p)
+        assert node_len == pl["node_len"] and parent == pl["parent"]
+        tok = np.concatenate([np.arange(starts[gidx[id(n)]], starts[gidx[id(n)]] + len(n.token_ids))
+                              for n in pnodes])
+        own_tokens[id(p)] = tok
+        if p.parent is None:
+            pre = np.zeros(0, np.int64)
+        else:
+            pp = p.parent
+            pn = _flatten_partition(pp)[2]
+            cut_pos = [i for i, n in enumerate(pn) if n is p.parent_cut_node][0]
+            # the gateway ends with the cut node's own tokens (its end in the parent's DFS order)
+            cut_end = int(sum(len(n.token_ids) for n in pn[:cut_pos + 1]))
+            pre = np.concatenate([prefix_tokens[id(pp)], own_tokens[id(pp)][:cut_end]])
+        prefix_tokens[id(p)] = pre
+        assert len(pre) == pl["past_len"]
+        ti = torch.from_numpy(tok).to(DEV)
+        kp = vp = bias = acc = None
+        if len(pre):
+            tp = torch.from_numpy(pre).to(DEV)
+            kp, vp = view(k[tp].contiguous()), view(v[tp].contiguous())
+            bias = pl["bias"].to(DEV)
+            acc = (torch.zeros(len(pre), HKV, D, device=DEV), torch.zeros(len(pre), HKV, D, device=DEV))
+        pplan = KeyPlan(TreeMetaDevice(node_len, parent, device=DEV).horizon, bias)
+        qi, ki, vi = view(q[ti].contiguous()), view(k[ti].contiguous()), view(v[ti].contiguous())
+        po, plse = attn_forward(qi, ki, vi, pplan, scale, kp, vp)
+        pdq, pdk, pdv = attn_backward(qi, ki, vi, pplan, scale, po, plse, do[ti][None].contiguous(), kp, vp, acc)
+        print(f"partition: {len(tok)} tokens, gateway {len(pre)}", flush=True)
+        assert _max_rel(o[ti].float(), po.float()) < 2e-2
+        assert _max_rel(dq[ti].float(), pdq.float()) < 2e-2
+        sum_dk.index_add_(0, ti, pdk.float())
+        sum_dv.index_add_(0, ti, pdv.float())
+        if acc is not None:
+            sum_dk.index_add_(0, tp, acc[0])
+            sum_dv.index_add_(0, tp, acc[1])
+    assert sorted(np.concatenate(list(own_tokens.values())).tolist()) == list(range(T))
+    torch.cuda.synchronize()
+    assert _max_rel(dk.float(), sum_dk) < 2e-2
+    assert _max_rel(dv.float(), sum_dv) < 2e-2
