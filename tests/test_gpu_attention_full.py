@@ -189,4 +189,3 @@ def test_attention_gateway_partitions_full_size():
     torch.cuda.synchronize()
     assert _max_rel(dk.float(), sum_dk) < 2e-2
     assert _max_rel(dv.float(), sum_dv) < 2e-2
-
