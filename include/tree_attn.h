@@ -137,7 +137,8 @@ int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* stream);
  * tree_grad_hybrid.py:220-225, kept on the device); pass NULL to drop them.
  * ws must be 16-byte aligned. float32 problems are deterministic (one writer
  * per output element). bf16 problems are too, except that keys whose visible
- * query range spans more than 2048 queries (split into several work items)
+ * query range spans more than 4096 queries (2048 for problems of fewer than 8192
+ * queries; split into several work items)
  * sum their dK/dV partials with fp32 atomics, so their rounding can vary
  * from run to run. */
 size_t tt_attn_bwd_workspace_bytes(const tt_attn_problem* p);

@@ -172,7 +172,7 @@ CASES = {
     "forest7": workloads.random_forest(7, node_len=(1, 90)),
     "agent_small": workloads.agent_tree(3, max_tokens=1500),
     # key tiles whose visible query range exceeds one dK/dV work item (split + fp32 sums)
-    "long_prompt": ([2600, 300, 250, 410], [-1, 0, 0, 0]),
+    "long_prompt": ([4400, 300, 250, 410], [-1, 0, 0, 0]),
 }
 
 
@@ -195,7 +195,7 @@ def test_attention_parity(case, dtype):
 def test_attention_gateway(dtype, shape):
     # "split": the gateway keys are seen by more queries than one dK/dV work item covers
     lens, par, n_past = {"short": ([40, 70, 33], [-1, 0, 0], 150),
-                         "split": ([1200, 900, 700], [-1, 0, 0], 300)}[shape]
+                         "split": ([2400, 1500, 1400], [-1, 0, 0], 300)}[shape]
     rng = np.random.default_rng(5)
     past_vis = [bool(x) for x in (rng.random(n_past) < 0.6)]
     say(f"attention gateway dtype={dtype} Lp={len(past_vis)}")

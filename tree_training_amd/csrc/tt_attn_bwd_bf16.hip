@@ -218,9 +218,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
         const int chunk = __builtin_amdgcn_readfirstlane(item - a.kb_base[lo_r]);
         const int qlo = __builtin_amdgcn_readfirstlane(a.kb_qlo[kb]);
         const int qhi = __builtin_amdgcn_readfirstlane(a.kb_qhi[kb]);
-        const bool split = tt_kb_items(qlo, qhi) > 1;
+        const int qch = tt_qch(a.n_q);
+        const bool split = tt_kb_items(qlo, qhi, qch) > 1;
         int q_start, q_stop;
-        tt_kb_item_range(qlo, qhi, chunk, q_start, q_stop);
+        tt_kb_item_range(qlo, qhi, qch, chunk, q_start, q_stop);
 
         // V rows of the tile's 128 keys go to LDS (read as MFMA operands every
         // step); K of the lane's key stays in registers. Keys past the end alias
@@ -369,7 +370,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
 // rows are 128 floats)
 __global__ __launch_bounds__(256) void bwd_split_zero_kernel(AttnDev a, BwdDev bw) {
     const int kb = blockIdx.x, g = blockIdx.y;
-    if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb]) <= 1) return;
+    if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb], tt_qch(a.n_q)) <= 1) return;
     const int nk = min(TT_BKB, a.n_keys - kb * TT_BKB);
     for (int e = threadIdx.x; e < nk * (D / 4); e += 256) {
         const int key = kb * TT_BKB + e / (D / 4);
@@ -382,7 +383,7 @@ __global__ __launch_bounds__(256) void bwd_split_zero_kernel(AttnDev a, BwdDev b
 // ... and convert them after it (own keys -> dk/dv, gateway keys -> fp32 accumulators).
 __global__ __launch_bounds__(256) void bwd_split_finalize_kernel(AttnDev a, BwdDev bw) {
     const int kb = blockIdx.x, g = blockIdx.y;
-    if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb]) <= 1) return;
+    if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb], tt_qch(a.n_q)) <= 1) return;
     const int nk = min(TT_BKB, a.n_keys - kb * TT_BKB);
     for (int e = threadIdx.x; e < nk * (D / 4); e += 256) {
         const int key = kb * TT_BKB + e / (D / 4), d = 4 * (e % (D / 4));
@@ -431,9 +432,12 @@ int tt_selftest_mfma_launch(const void* a, const void* b, float* d, hipStream_t 
 }
 
 // Persistent grid for the dK/dV pass: a multiple of Hkv so every workgroup
-// keeps one kv head (and, with Hkv = 8, one XCD).
+// keeps one kv head (and, with Hkv = 8, one XCD). 2048 workgroups (four per
+// resident slot) leave at most one work item per workgroup on the 16K tree,
+// so the hardware's dispatch balances the uneven items (6 % faster than 1024,
+// which pairs items statically).
 static int dkdv_grid(const AttnDev& a) {
-    const int target = 256 * 4;
+    const int target = 2048;
     const int gsz = (target / a.hkv) * a.hkv;
     return gsz > 0 ? gsz : a.hkv;
 }

@@ -21,38 +21,43 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 //   forward / dQ pass: a workgroup owns TT_BQ queries of one q head, its four
 //   waves own 32 queries each; key tiles hold TT_BK keys.
 //   dK/dV pass: a workgroup owns TT_BKB keys of one kv head (32 per wave) and
-//   walks at most TT_QCH queries of their visible range (one work item), in
-//   blocks of TT_BQB; longer ranges are split into several items.
+//   walks at most tt_qch(n_q) queries of their visible range (one work item),
+//   in blocks of TT_BQB; longer ranges are split into several items.
 #define TT_BQ 128
 #define TT_BK 64
 #define TT_BKB 128
 #define TT_BQB 32
-#define TT_QCH 2048
 #define TT_GDN_CHUNK 32
 
 __host__ __device__ inline int tt_cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// Query window of one dK/dV work item. Long windows mean fewer split key tiles
+// (fewer V reloads and fp32 partial sums); short ones mean more, shorter items
+// to balance over the chip. 4096 for trees of 8192 queries or more, 2048 below
+// (a 4096-query partition then still splits its gateway tiles in two).
+__host__ __device__ inline int tt_qch(int n_q) { return n_q >= 8192 ? 4096 : 2048; }
+
 // dK/dV work items of a key tile whose visible queries are [qlo, qhi). A range
-// of at most TT_QCH queries is one item; a longer one is cut at multiples of
-// TT_QCH in absolute query index, so workgroups busy with different key tiles
-// at the same time walk the same query windows (and share them in L2).
-__host__ __device__ inline int tt_kb_items(int qlo, int qhi) {
-    if (qhi - qlo <= TT_QCH) return 1;
-    return (qhi - 1) / TT_QCH - qlo / TT_QCH + 1;
+// of at most qch queries is one item; a longer one is cut at multiples of qch
+// in absolute query index, so workgroups busy with different key tiles at the
+// same time walk the same query windows (and share them in L2).
+__host__ __device__ inline int tt_kb_items(int qlo, int qhi, int qch) {
+    if (qhi - qlo <= qch) return 1;
+    return (qhi - 1) / qch - qlo / qch + 1;
 }
 // Query range [q_start, q_stop) of item `item`; q_start is a multiple of TT_BQB.
-__host__ __device__ inline void tt_kb_item_range(int qlo, int qhi, int item, int& q_start, int& q_stop) {
+__host__ __device__ inline void tt_kb_item_range(int qlo, int qhi, int qch, int item, int& q_start, int& q_stop) {
     q_start = q_stop = 0;
     if (qhi <= qlo) return;
     const int a = (qlo / TT_BQB) * TT_BQB;
-    if (qhi - qlo <= TT_QCH) {
+    if (qhi - qlo <= qch) {
         q_start = a;
         q_stop = qhi;
         return;
     }
-    const int w = qlo / TT_QCH + item;
-    q_start = a > w * TT_QCH ? a : w * TT_QCH;
-    q_stop = qhi < (w + 1) * TT_QCH ? qhi : (w + 1) * TT_QCH;
+    const int w = qlo / qch + item;
+    q_start = a > w * qch ? a : w * qch;
+    q_stop = qhi < (w + 1) * qch ? qhi : (w + 1) * qch;
 }
 
 // Plan buffer layout. Header (bytes): [0,8) uint64 visible pairs per head;

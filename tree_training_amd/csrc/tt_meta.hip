@@ -285,7 +285,8 @@ __global__ void plan_kb_order_kernel(const int32_t* __restrict__ kb_qlo, const i
 __global__ __launch_bounds__(1024) void plan_kb_base_kernel(const int32_t* __restrict__ kb_qlo,
                                                             const int32_t* __restrict__ kb_qhi,
                                                             const int32_t* __restrict__ kb_order, int n_kb,
-                                                            int32_t* __restrict__ kb_base, int32_t* __restrict__ n_items) {
+                                                            int qch, int32_t* __restrict__ kb_base,
+                                                            int32_t* __restrict__ n_items) {
     __shared__ int s_scan[1024];
     __shared__ int s_carry;
     const int tid = threadIdx.x;
@@ -296,7 +297,7 @@ __global__ __launch_bounds__(1024) void plan_kb_base_kernel(const int32_t* __res
         int v = 0;
         if (r < n_kb) {
             const int kb = kb_order[r];
-            v = tt_kb_items(kb_qlo[kb], kb_qhi[kb]);
+            v = tt_kb_items(kb_qlo[kb], kb_qhi[kb], qch);
         }
         s_scan[tid] = v;
         __syncthreads();
@@ -378,7 +379,7 @@ int tt_plan_build_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys,
                        n_q, L.n_kb, kb_qlo, kb_qhi);
     hipLaunchKernelGGL(plan_kb_order_kernel, dim3(tt_cdiv(L.n_kb, 256)), dim3(256), 0, s, kb_qlo, kb_qhi, L.n_kb,
                        kb_order);
-    hipLaunchKernelGGL(plan_kb_base_kernel, dim3(1), dim3(1024), 0, s, kb_qlo, kb_qhi, kb_order, L.n_kb, kb_base,
-                       hdr + 5);
+    hipLaunchKernelGGL(plan_kb_base_kernel, dim3(1), dim3(1024), 0, s, kb_qlo, kb_qhi, kb_order, L.n_kb, tt_qch(n_q),
+                       kb_base, hdr + 5);
     return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
 }
