@@ -553,8 +553,8 @@ def run_gdn(args):
                    "parallelism": "single GPU"},
         "wall_s_timed": round(wall, 3),
         "roofline": {"bound": "mfma", "kernel": "whole step (conv, prep, level scans, reverse scans, gradient "
-                                                 "kernels); fp32 products (scans on fp32 MFMA, the rest on the "
-                                                 "vector ALUs), ceiling = fp32 peak",
+                                                 "kernels); fp32 products (scans and state products on fp32 MFMA, "
+                                                 "the rest on the vector ALUs), ceiling = fp32 peak",
                      "achieved": round(tfs, 2), "peak": PEAK_FP32_TFS, "unit": "TFLOP/s",
                      "frac": round(tfs / PEAK_FP32_TFS, 5), "traffic": None, "flops_per_step": flops},
         "cpu_baseline": cpu,
