@@ -15,11 +15,18 @@ with HIP events on the launch stream; the CPU baseline times the dense-mask
 restatement of the reference path (additive mask + repeat_kv + SDPA + autograd)
 on a bounded sample on the host cores.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload agent16k|gateway16k|rollout48k|gdn16k]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload agent16k|gateway16k|rollout48k|gdn16k|prologue16k|leafce16k]
 
-``gdn16k`` times the tree gated-delta-rule forward instead (the same 16K tree,
-16 q/k heads, 32 v heads, head_dim 128, bf16 q/k/v, fp32 gates and state) and
-reports packed tokens/s with the HBM roofline of the scan.
+Other workloads, each on the same 16K tree unless named:
+  gateway16k   the tree cut into 4096-token partitions (tree_grad_hybrid), each
+               partition's attention fwd+bwd over its gateway prefix;
+  rollout48k   one 8K prompt with 64 leaves (50,109 tokens);
+  gdn16k       one GDN layer core (tree conv + gated-delta-rule scan) fwd+bwd,
+               16 q/k heads, 32 v heads, fp32 state; packed tokens/s against
+               the fp32 peak;
+  prologue16k  the fused q/k RMSNorm + rotary fwd+bwd (HBM roofline);
+  leafce16k    the fused leaf loss (chunked lm_head + row-wise CE) fwd+bwd.
 """
 from __future__ import annotations
 

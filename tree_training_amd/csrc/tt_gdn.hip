@@ -33,9 +33,6 @@ constexpr int GC = TT_GDN_CHUNK;  // chunk length (32)
 constexpr int GT = 256;           // threads per workgroup
 constexpr int RS = GD + 4;        // row stride of [GC x GD] tiles (floats): rows 4 banks apart
 constexpr int MS = GC + 4;        // row stride of [GC x GC] matrices
-constexpr int NSL = 4;            // value-column slices in the scan
-constexpr int VS = GD / NSL;      // columns per slice
-constexpr int VP = VS + 4;        // row stride of [* x VS] tiles
 
 // Workspace per (chunk, v head), floats: W [GC][GD], U [GC][GD], A [GC][GC],
 // T [GC][GC] (the inverse, for the backward), G [GC].
