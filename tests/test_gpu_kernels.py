@@ -205,3 +205,45 @@ def test_attention_gateway(dtype, shape):
         if name == "lse":
             continue
         check_close(name, ref, got, tol)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("hq,hkv", [(16, 16), (32, 4), (12, 4), (2, 1)])
+def test_attention_head_layouts(hq, hkv, dtype):
+    """Other GQA layouts than Qwen3-4B's 32/8: MHA (16/16), 8 q heads per kv
+    head (32/4), a q-head count that is not a multiple of 8 (12/4: the
+    workgroup -> head mapping without the per-XCD grouping) and a single kv
+    head (2/1), with a gateway prefix, against the fp64 oracle."""
+    from tree_training_amd.attention import attn_backward, attn_forward
+    from tree_training_amd.meta import KeyPlan
+    lens, par = workloads.random_forest(21, node_len=(1, 70))
+    T, Lp = sum(lens), 45
+    say(f"attention head layout hq={hq} hkv={hkv} dtype={dtype} T={T}")
+    g = torch.Generator().manual_seed(hq * 100 + hkv)
+    q = torch.randn(1, T, hq, D, generator=g).to(dtype)
+    k = torch.randn(1, T, hkv, D, generator=g).to(dtype)
+    v = torch.randn(1, T, hkv, D, generator=g).to(dtype)
+    do = torch.randn(1, T, hq, D, generator=g).to(dtype)
+    kp = torch.randn(1, Lp, hkv, D, generator=g).to(dtype)
+    vp = torch.randn(1, Lp, hkv, D, generator=g).to(dtype)
+    vis = [(i % 4) != 2 for i in range(Lp)]
+    bias = torch.tensor([0.0 if b else -math.inf for b in vis], device=DEV)
+    m = _meta(lens, par)
+    plan = KeyPlan(m.horizon, bias, validate=True)
+    tr = lambda x: x.to(DEV).transpose(1, 2)
+    acc = (torch.zeros(Lp, hkv, D, device=DEV), torch.zeros(Lp, hkv, D, device=DEV))
+    scale = D ** -0.5
+    o, lse = attn_forward(tr(q), tr(k), tr(v), plan, scale, tr(kp), tr(vp))
+    dq, dk, dv = attn_backward(tr(q), tr(k), tr(v), plan, scale, o, lse, do.to(DEV), tr(kp), tr(vp), acc)
+    torch.cuda.synchronize()
+    cf = meta_closed_form(lens, par)
+    mask = key_interval_mask([0] * Lp + list(range(T)), [T if b else 0 for b in vis] + list(cf["horizon"]), T)
+    f64 = lambda x: x[0].double().numpy()
+    kk = np.concatenate([f64(kp), f64(k)], axis=0)
+    vv = np.concatenate([f64(vp), f64(v)], axis=0)
+    ro, _ = attn_fwd(f64(q), kk, vv, mask, scale)
+    rdq, rdk, rdv = attn_bwd(f64(q), kk, vv, mask, scale, f64(do))
+    tol = TOL[dtype]
+    for name, ref, got in (("o", ro, o), ("dq", rdq, dq), ("dk", rdk[Lp:], dk), ("dv", rdv[Lp:], dv),
+                           ("dk_past", rdk[:Lp], acc[0]), ("dv_past", rdv[:Lp], acc[1])):
+        check_close(name, ref, got.float().cpu().numpy(), tol)
