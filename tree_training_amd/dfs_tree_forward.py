@@ -17,6 +17,7 @@ import torch
 import torch.nn.functional as F
 
 from .hf_adapter import TreeAttnContext, tree_attention_mode
+from .meta import upload_i32
 from .tree import DFSTreeInfo, TreeNode, build_dfs_tree_info
 
 
@@ -65,7 +66,7 @@ def run_tree_model(model, info: DFSTreeInfo, dev, pos_offset: int = 0, cache=Non
                          f"[{min(info.dfs_token_ids)}, {max(info.dfs_token_ids)}]")
     meta = info.device_meta(dev, pos_offset)
     plan = info.key_plan(dev, past_bias, pos_offset)
-    ids_t = torch.tensor([info.dfs_token_ids], device=dev)
+    ids_t = upload_i32([info.dfs_token_ids], dev).long()
     pos_t = meta.pos.long().unsqueeze(0)
     ctx = TreeAttnContext(plan=plan, cache=cache, accumulators=accumulators)
     with tree_attention_mode(model, linear_attention_patched):

@@ -23,7 +23,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .meta import _ptr, _stream, require_device
+from .meta import _ptr, _stream, require_device, upload_i32
 
 HEAD_DIM = 128
 CHUNK = 32        # TT_GDN_CHUNK
@@ -76,15 +76,10 @@ class GdnTree:
             chunk_node.extend([i] * ((L + CHUNK - 1) // CHUNK))
         self.n_chunks = len(chunk_node)
         dev = require_device(device)
-        i32 = dict(dtype=torch.int32, device=dev)
-        self.d_start = torch.tensor(start, **i32)
-        self.d_len = torch.tensor(self.node_len, **i32)
-        self.d_parent = torch.tensor(self.parent, **i32)
-        self.d_levels = torch.tensor(order, **i32)
-        self.d_chunk0 = torch.tensor(chunk0, **i32)
-        self.d_chunk_node = torch.tensor(chunk_node, **i32)
-        self.d_child_off = torch.tensor(child_off, **i32)
-        self.d_child = torch.tensor(child, **i32)
+        parts = [start, self.node_len, self.parent, order, chunk0, chunk_node, child_off, child]
+        flat = upload_i32(np.concatenate([np.asarray(x, dtype=np.int32) for x in parts]), dev)
+        (self.d_start, self.d_len, self.d_parent, self.d_levels, self.d_chunk0, self.d_chunk_node,
+         self.d_child_off, self.d_child) = torch.split(flat, [len(x) for x in parts])
         self.device = dev
 
     def token_links(self):
@@ -101,9 +96,9 @@ class GdnTree:
             nxt = np.arange(T, dtype=np.int64)[has][order]
             off = np.zeros(T + 1, dtype=np.int64)
             np.cumsum(np.bincount(prev[has], minlength=T), out=off[1:])
-            i32 = dict(dtype=torch.int32, device=self.device)
-            self._links = (torch.tensor(prev, **i32), torch.tensor(off, **i32),
-                           torch.tensor(nxt if len(nxt) else np.zeros(1, np.int64), **i32))
+            nxt = nxt if len(nxt) else np.zeros(1, np.int64)
+            flat = upload_i32(np.concatenate([prev, off, nxt]), self.device)
+            self._links = tuple(torch.split(flat, [len(prev), len(off), len(nxt)]))
         return self._links
 
     @classmethod

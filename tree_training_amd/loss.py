@@ -24,7 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .meta import _ptr, _stream, require_device
+from .meta import _ptr, _stream, require_device, to_device
 
 
 def ce_rows(logits: torch.Tensor, labels: torch.Tensor, row_scale: torch.Tensor, ignore_index: int = -100,
@@ -36,8 +36,8 @@ def ce_rows(logits: torch.Tensor, labels: torch.Tensor, row_scale: torch.Tensor,
     N, V = logits.shape
     grad = logits if grad is None else grad
     dev = require_device(logits.device)
-    lab = labels.to(device=dev, dtype=torch.int32).contiguous()
-    sc = row_scale.to(device=dev, dtype=torch.float32).contiguous()
+    lab = to_device(labels, dev, torch.int32)
+    sc = to_device(row_scale, dev, torch.float32)
     loss = torch.empty(N, dtype=torch.float32, device=dev)
     code = _lib.TT_DTYPE_BF16 if logits.dtype == torch.bfloat16 else _lib.TT_DTYPE_F32
     if logits.dtype not in (torch.bfloat16, torch.float32) or grad.dtype != logits.dtype:
@@ -109,14 +109,18 @@ class TreeCELoss:
         dev = hidden.device
         rows, labels, scales, empty = [], [], [], False
         for s, e, node in spans:
-            lab = self.label_map[id(node)].to(dev).reshape(-1)
-            n_valid = int((lab != self.ignore_index).sum())
+            lab = self.label_map[id(node)].reshape(-1)
+            n_valid = int((lab != self.ignore_index).sum())   # no device round trip for host labels
             empty = empty or n_valid == 0
             rows.append(torch.arange(s, e, device=dev))
             labels.append(lab)
             scales.append(torch.full((e - s,), 1.0 / (max(n_valid, 1) * self.n_leaves), dtype=torch.float32,
                                      device=dev))
         idx = torch.cat(rows)
-        loss = fused_linear_ce(hidden.index_select(0, idx), lm_head_weight, torch.cat(labels), torch.cat(scales),
+        if all(lab.device.type == "cpu" for lab in labels):
+            lab_all = to_device(torch.cat(labels), dev, torch.int32)
+        else:
+            lab_all = torch.cat([lab.to(dev) for lab in labels])
+        loss = fused_linear_ce(hidden.index_select(0, idx), lm_head_weight, lab_all, torch.cat(scales),
                                self.ignore_index)
         return loss * float("nan") if empty else loss    # F.cross_entropy's mean over no tokens is NaN

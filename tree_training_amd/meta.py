@@ -16,6 +16,7 @@ from __future__ import annotations
 import ctypes
 from typing import Optional, Sequence
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -28,6 +29,26 @@ def _ptr(t: Optional[torch.Tensor]):
 
 def _stream(device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def upload_i32(rows, device) -> torch.Tensor:
+    """Host integers (a sequence, or equal-length rows) as a device int32 tensor,
+    without synchronising the stream.
+
+    ``torch.tensor(..., device=cuda)`` copies from pageable memory and then waits
+    for the whole stream, so every upload would drain the launch queue. Staged
+    through pinned memory, the copy is queued like a kernel; torch's caching
+    host allocator keeps the pinned block until the copy has run."""
+    return to_device(torch.from_numpy(np.ascontiguousarray(np.asarray(rows, dtype=np.int32))), device,
+                     torch.int32)
+
+
+def to_device(t: torch.Tensor, device, dtype: torch.dtype) -> torch.Tensor:
+    """``t`` as a contiguous ``dtype`` tensor on ``device``; a host tensor goes
+    through pinned memory with a non-blocking copy (no stream synchronisation)."""
+    if t.device.type == "cpu":
+        return t.to(dtype).contiguous().pin_memory().to(device, non_blocking=True)
+    return t.to(device=device, dtype=dtype).contiguous()
 
 
 def require_device(device=None) -> torch.device:
@@ -54,7 +75,7 @@ class TreeMetaDevice:
         T = int(sum(node_len))
         self.device, self.n_nodes, self.T, self.pos_offset = dev, n, T, int(pos_offset)
         i32 = dict(dtype=torch.int32, device=dev)
-        lp = torch.tensor([list(node_len), list(parent)], **i32)
+        lp = upload_i32([list(node_len), list(parent)], dev)
         self.node_len, self.parent = lp[0], lp[1]
         nodes = torch.empty((3, n), **i32)
         self.node_start, self.node_off, self.node_hend = nodes[0], nodes[1], nodes[2]
@@ -88,7 +109,7 @@ class KeyPlan:
         n_q = int(horizon.numel())
         n_past = 0 if past_bias is None else int(past_bias.numel())
         if past_bias is not None:
-            past_bias = past_bias.to(device=dev, dtype=torch.float32).contiguous()
+            past_bias = to_device(past_bias, dev, torch.float32)
         self.device, self.n_q, self.n_past, self.n_keys = dev, n_q, n_past, n_q + n_past
         keys = torch.empty((2, self.n_keys), dtype=torch.int32, device=dev)
         self.key_lo, self.key_hi = keys[0], keys[1]
