@@ -83,8 +83,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         stg.commit(a, g, S.K, S.V);
         store_bounds(nb, S.lo, S.hi);
         __syncthreads();
-        if (it + 1 < cnt) {
-            const int kt1 = list[it + 1] >> 1;
+        {   // the last step re-stages its own tile: the loads are unconditional
+            const int kt1 = list[it + 1 < cnt ? it + 1 : it] >> 1;
             stg.begin(a, kt1, g);
             fetch_bounds(a, kt1, nb);
         }

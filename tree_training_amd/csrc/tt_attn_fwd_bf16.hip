@@ -61,18 +61,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         stg.commit(a, g, S.K, S.V);
         store_bounds(nb, S.lo, S.hi);
         __syncthreads();
-        if (it + 1 < cnt) {
-            const int kt1 = __builtin_amdgcn_readfirstlane(list[it + 1] >> 1);
+        {   // the last step re-stages its own tile: the loads are unconditional
+            const int kt1 = __builtin_amdgcn_readfirstlane(list[it + 1 < cnt ? it + 1 : it] >> 1);
             stg.begin(a, kt1, g);
             fetch_bounds(a, kt1, nb);
         }
 
         f32x16 s[2];
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            s[b] = (f32x16){};
-#pragma unroll
-            for (int t = 0; t < 8; ++t) s[b] = mfma32(read_row_operand(S.K, 32 * b + col, 16 * t + 8 * half), qa[t], s[b]);
+        {
+            // K operand reads run AH MFMAs ahead of their use (the scheduler
+            // would otherwise issue them two at a time, just before use).
+            constexpr int AH = 4;
+            bf16x8 kop[16];
+            static_for<AH>([&](auto i) {
+                constexpr int n = decltype(i)::value;
+                kop[n] = read_row_operand(S.K, 32 * (n >> 3) + col, 16 * (n & 7) + 8 * half);
+            });
+            s[0] = (f32x16){};
+            s[1] = (f32x16){};
+            static_for<16>([&](auto i) {
+                constexpr int n = decltype(i)::value;
+                if constexpr (n + AH < 16)
+                    kop[n + AH] = read_row_operand(S.K, 32 * ((n + AH) >> 3) + col, 16 * ((n + AH) & 7) + 8 * half);
+                __builtin_amdgcn_sched_barrier(0);
+                s[n >> 3] = mfma32(kop[n], qa[n & 7], s[n >> 3]);
+                __builtin_amdgcn_sched_barrier(0);
+            });
         }
         if (!full) mask_scores(s, S.lo, S.hi, qi, half);
 

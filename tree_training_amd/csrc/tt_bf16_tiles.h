@@ -233,6 +233,13 @@ struct KvTileStager {
             fetch_rows_buf(v, threadIdx.x, (const bf16*)a.v + t0 * a.v_st + g * a.v_sh, 2 * a.v_st);
         } else {
             direct = true;
+            // Defined on every path, so the staged values of consecutive tiles
+            // share registers (no copies at the loop latch).
+#pragma unroll
+            for (int i = 0; i < TT_BK / 16; ++i) {
+                k.x[i] = zero8();
+                v.x[i] = zero8();
+            }
         }
     }
     __device__ __forceinline__ void commit(const AttnDev& a, int g, bf16* K, bf16* V) {
