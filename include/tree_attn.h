@@ -137,10 +137,10 @@ int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* stream);
  * tree_grad_hybrid.py:220-225, kept on the device); pass NULL to drop them.
  * ws must be 16-byte aligned. float32 problems are deterministic (one writer
  * per output element). bf16 problems are too, except that keys whose visible
- * query range spans more than 4096 queries (2048 for problems of fewer than 8192
- * queries; split into several work items)
- * sum their dK/dV partials with fp32 atomics, so their rounding can vary
- * from run to run. */
+ * query range spans more than W queries, W = half the largest power of two
+ * <= n_q clamped to [256, 4096] (split into several work items), sum their
+ * dK/dV partials with fp32 atomics, so their rounding can vary from run to
+ * run. */
 size_t tt_attn_bwd_workspace_bytes(const tt_attn_problem* p);
 int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_tensor d_o,
                 void* dq, void* dk, void* dv, float* dk_past_acc, float* dv_past_acc,

@@ -23,8 +23,9 @@
 // (for a DFS-packed tree the range is contiguous: [first key, subtree end))
 // for the Hq/Hkv q heads of the group, with Q and dO blocks staged in LDS
 // (double-buffered) and read both row-wise and transposed. Ranges longer than
-// tt_qch(n_q) queries (4096, or 2048 for trees under 8192 queries) are split
-// into several work items; a persistent grid walks the items widest-first.
+// tt_qch(n_q) queries (half the largest power of two <= n_q, within
+// [256, 4096]) are split into several work items; a persistent grid walks the
+// items widest-first.
 // Unsplit tiles write dK/dV directly; split tiles add fp32 partial sums into a
 // workspace that a finalize pass converts.
 //

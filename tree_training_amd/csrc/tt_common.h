@@ -31,12 +31,16 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __host__ __device__ inline int tt_cdiv(int a, int b) { return (a + b - 1) / b; }
 
-// Query window of one dK/dV work item. Long windows mean fewer split key tiles
-// (fewer V reloads and fp32 partial sums); short ones mean more, shorter items
-// to balance over the chip. 4096 for trees of 8192 queries or more, 2048 below
-// (a 4096-query partition then still splits its gateway tiles in two).
-__host__ __device__ inline int tt_qch(int n_q) { return n_q >= 8192 ? 4096 : 2048; }
-
+// Query window of one dK/dV work item: half the largest power of two <= n_q,
+// clamped to [256, 4096] (a multiple of TT_BQB). Long windows mean fewer split
+// key tiles (fewer V reloads and fp32 partial sums); short ones mean more,
+// shorter items to balance over the chip, which small problems need: a
+// partition of a few hundred queries under a gateway of thousands of keys has
+// few key tiles, each a long serial walk if it is not split.
+__host__ __device__ inline int tt_qch(int n_q) {
+    const int half = n_q >= 2 ? (1 << (31 - __builtin_clz((unsigned)n_q))) / 2 : 0;   // half the largest power of 2 <= n_q
+    return half > 4096 ? 4096 : (half < 256 ? 256 : half);
+}
 // dK/dV work items of a key tile whose visible queries are [qlo, qhi). A range
 // of at most qch queries is one item; a longer one is cut at multiples of qch
 // in absolute query index, so workgroups busy with different key tiles at the
