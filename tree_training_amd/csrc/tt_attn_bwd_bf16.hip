@@ -346,14 +346,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
                 const int d = 32 * db + col;
                 const float gk = dk[db][r] * a.scale, gv = dv[db][r];
                 const size_t widx = ((size_t)key * a.hkv + g) * D + d;
-                if (split) {
+                if (key < a.n_past) {   // gateway key: fp32, added to the caller's accumulators
+                    if (bw.dk_acc) {
+                        if (split) {
+                            atomicAdd(bw.dk_acc + widx, gk);
+                            atomicAdd(bw.dv_acc + widx, gv);
+                        } else {
+                            bw.dk_acc[widx] += gk;
+                            bw.dv_acc[widx] += gv;
+                        }
+                    }
+                } else if (split) {
                     atomicAdd(bw.dk_ws + widx, gk);
                     atomicAdd(bw.dv_ws + widx, gv);
-                } else if (key < a.n_past) {
-                    if (bw.dk_acc) {
-                        bw.dk_acc[widx] += gk;
-                        bw.dv_acc[widx] += gv;
-                    }
                 } else {
                     const size_t idx = ((size_t)(key - a.n_past) * a.hkv + g) * D + d;
                     ((bf16*)bw.dk)[idx] = (bf16)gk;
@@ -365,46 +370,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
     }
 }
 
-// Split key tiles: zero their fp32 sums before the dK/dV pass ... (16-byte
-// vectors: the workspace and the gateway accumulators are 16-byte aligned and
-// rows are 128 floats)
+// Split key tiles: zero the fp32 sums of their own keys before the dK/dV pass
+// (split gateway keys add straight into the caller's fp32 accumulators) ...
+// (16-byte vectors: the workspace and the gateway accumulators are 16-byte
+// aligned and rows are 128 floats)
 __global__ __launch_bounds__(256) void bwd_split_zero_kernel(AttnDev a, BwdDev bw) {
     const int kb = blockIdx.x, g = blockIdx.y;
     if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb], tt_qch(a.n_q)) <= 1) return;
-    const int nk = min(TT_BKB, a.n_keys - kb * TT_BKB);
-    for (int e = threadIdx.x; e < nk * (D / 4); e += 256) {
-        const int key = kb * TT_BKB + e / (D / 4);
+    const int k_first = max(kb * TT_BKB, a.n_past), k_end = min(kb * TT_BKB + TT_BKB, a.n_keys);
+    for (int e = threadIdx.x; e < (k_end - k_first) * (D / 4); e += 256) {
+        const int key = k_first + e / (D / 4);
         const size_t idx = ((size_t)key * a.hkv + g) * D + 4 * (e % (D / 4));
         *(f32x4*)(bw.dk_ws + idx) = (f32x4){};
         *(f32x4*)(bw.dv_ws + idx) = (f32x4){};
     }
 }
 
-// ... and convert them after it (own keys -> dk/dv, gateway keys -> fp32 accumulators).
+// ... and convert them to dk/dv after it.
 __global__ __launch_bounds__(256) void bwd_split_finalize_kernel(AttnDev a, BwdDev bw) {
     const int kb = blockIdx.x, g = blockIdx.y;
     if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb], tt_qch(a.n_q)) <= 1) return;
-    const int nk = min(TT_BKB, a.n_keys - kb * TT_BKB);
-    for (int e = threadIdx.x; e < nk * (D / 4); e += 256) {
-        const int key = kb * TT_BKB + e / (D / 4), d = 4 * (e % (D / 4));
+    const int k_first = max(kb * TT_BKB, a.n_past), k_end = min(kb * TT_BKB + TT_BKB, a.n_keys);
+    for (int e = threadIdx.x; e < (k_end - k_first) * (D / 4); e += 256) {
+        const int key = k_first + e / (D / 4), d = 4 * (e % (D / 4));
         const size_t widx = ((size_t)key * a.hkv + g) * D + d;
         const f32x4 gk = *(const f32x4*)(bw.dk_ws + widx), gv = *(const f32x4*)(bw.dv_ws + widx);
-        if (key < a.n_past) {
-            if (bw.dk_acc) {
-                *(f32x4*)(bw.dk_acc + widx) += gk;
-                *(f32x4*)(bw.dv_acc + widx) += gv;
-            }
-        } else {
-            const size_t idx = ((size_t)(key - a.n_past) * a.hkv + g) * D + d;
-            bf16x4 wk, wv;
+        const size_t idx = ((size_t)(key - a.n_past) * a.hkv + g) * D + d;
+        bf16x4 wk, wv;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                wk[i] = (bf16)gk[i];
-                wv[i] = (bf16)gv[i];
-            }
-            *(bf16x4*)((bf16*)bw.dk + idx) = wk;
-            *(bf16x4*)((bf16*)bw.dv + idx) = wv;
+        for (int i = 0; i < 4; ++i) {
+            wk[i] = (bf16)gk[i];
+            wv[i] = (bf16)gv[i];
         }
+        *(bf16x4*)((bf16*)bw.dk + idx) = wk;
+        *(bf16x4*)((bf16*)bw.dv + idx) = wv;
     }
 }
 
