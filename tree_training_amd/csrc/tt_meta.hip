@@ -196,20 +196,24 @@ __global__ void plan_pairs_kernel(const int32_t* __restrict__ key_lo, const int3
     if (threadIdx.x == 0 && s_sum) atomicAdd(pairs, s_sum);
 }
 
-__global__ void plan_classify_kernel(const int32_t* __restrict__ key_lo, const int32_t* __restrict__ key_hi,
-                                     int n_keys, int n_q, int n_qb, int n_kt, uint8_t* __restrict__ cls) {
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= n_qb * n_kt) return;
-    const int qb = idx / n_kt, kt = idx - qb * n_kt;
+// One wave per (query block, key tile) pair, one lane per key of the tile.
+static_assert(TT_BK == 64, "plan_classify_kernel maps the keys of a tile to the lanes of a wave");
+__global__ __launch_bounds__(256) void plan_classify_kernel(const int32_t* __restrict__ key_lo,
+                                                            const int32_t* __restrict__ key_hi, int n_keys, int n_q,
+                                                            int n_qb, int n_kt, uint8_t* __restrict__ cls) {
+    const int pair = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (pair >= n_qb * n_kt) return;   // wave-uniform
+    const int qb = pair / n_kt, kt = pair - qb * n_kt;
     const int i0 = qb * TT_BQ, i1 = min(i0 + TT_BQ, n_q);
-    bool any = false, all = true;
-    for (int j = kt * TT_BK; j < kt * TT_BK + TT_BK; ++j) {
-        if (j >= n_keys) { all = false; continue; }
+    const int j = kt * TT_BK + lane;
+    bool some = false, every = false;
+    if (j < n_keys) {
         const int lo = key_lo[j], hi = key_hi[j];
-        if (max(lo, i0) < min(hi, i1)) any = true;
-        if (!(lo <= i0 && hi >= i1)) all = false;
+        some = max(lo, i0) < min(hi, i1);
+        every = lo <= i0 && hi >= i1;
     }
-    cls[idx] = any ? (all ? 2 : 1) : 0;
+    const bool any = __ballot(some) != 0, all = __ballot(every) == ~0ull;
+    if (lane == 0) cls[pair] = any ? (all ? 2 : 1) : 0;
 }
 
 // One wave per query block: compacts the non-empty key tiles, ascending.
@@ -369,7 +373,7 @@ int tt_plan_build_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys,
     hipLaunchKernelGGL(plan_header_kernel, dim3(1), dim3(64), 0, s, base, L.n_qb, L.n_kt, L.n_kb);
     hipLaunchKernelGGL(plan_pairs_kernel, dim3(tt_cdiv(n_keys, 256)), dim3(256), 0, s, key_lo, key_hi, n_keys,
                        n_q, reinterpret_cast<unsigned long long*>(base));
-    hipLaunchKernelGGL(plan_classify_kernel, dim3(tt_cdiv(L.n_qb * L.n_kt, 256)), dim3(256), 0, s, key_lo, key_hi,
+    hipLaunchKernelGGL(plan_classify_kernel, dim3(tt_cdiv(L.n_qb * L.n_kt, 4)), dim3(256), 0, s, key_lo, key_hi,
                        n_keys, n_q, L.n_qb, L.n_kt, cls);
     hipLaunchKernelGGL(plan_compact_kernel, dim3(tt_cdiv(L.n_qb, 4)), dim3(256), 0, s, cls, L.n_qb, L.n_kt,
                        row_cnt, row_list);
