@@ -173,18 +173,16 @@ def main():
         rec(0)
         _lib.check(lib.tt_attn_fwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), st), "fwd")
         rec(1)
-        pb.s.bwd_parts = _lib.TT_BWD_DELTA
+        # delta and dQ in one call (the dQ kernel computes delta), then dK/dV:
+        # the same work as bwd_parts=0, split only to time the passes
+        pb.s.bwd_parts = _lib.TT_BWD_DELTA | _lib.TT_BWD_DQ
         _lib.check(lib.tt_attn_bwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), dt, _ptr(dq), _ptr(dk), _ptr(dv),
-                                   _ptr(ak), _ptr(av), _ptr(ws), ws_bytes, st), "bwd delta")
+                                   _ptr(ak), _ptr(av), _ptr(ws), ws_bytes, st), "bwd delta+dq")
         rec(2)
-        pb.s.bwd_parts = _lib.TT_BWD_DQ
-        _lib.check(lib.tt_attn_bwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), dt, _ptr(dq), _ptr(dk), _ptr(dv),
-                                   _ptr(ak), _ptr(av), _ptr(ws), ws_bytes, st), "bwd dq")
-        rec(3)
         pb.s.bwd_parts = _lib.TT_BWD_DKDV
         _lib.check(lib.tt_attn_bwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), dt, _ptr(dq), _ptr(dk), _ptr(dv),
                                    _ptr(ak), _ptr(av), _ptr(ws), ws_bytes, st), "bwd dkdv")
-        rec(4)
+        rec(3)
         return o, dq, dk, dv
 
     def step(ev=None):
@@ -207,7 +205,7 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
     t0 = time.perf_counter()
     start_ev = torch.cuda.Event(enable_timing=True)
     end_ev = torch.cuda.Event(enable_timing=True)
@@ -225,8 +223,8 @@ def main():
     kernels = {}
     roofline = None
     if segments is None:
-        names = ["fwd_bf16_kernel", "bwd_delta_bf16_kernel", "bwd_dq_bf16_kernel", "bwd_dkdv_bf16_kernel"]
-        useful = [4.0 * D * HQ * P, 0.0, 4.0 * D * HQ * P, 4.0 * D * HQ * P]
+        names = ["fwd_bf16_kernel", "bwd_dq_bf16_kernel", "bwd_dkdv_bf16_kernel"]
+        useful = [4.0 * D * HQ * P, 4.0 * D * HQ * P, 4.0 * D * HQ * P]
         for j, name in enumerate(names):
             ms = statistics.mean(e[j].elapsed_time(e[j + 1]) for e in evs)
             kernels[name] = {"ms": round(ms, 4),

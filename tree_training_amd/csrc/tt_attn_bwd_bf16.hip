@@ -37,6 +37,9 @@ struct DqStage {
     int hi[TT_BK];
 };
 
+// FUSE_DELTA: the kernel also computes delta = rowsum(dO * O) of its rows (and
+// stores it for the dK/dV pass) instead of reading it.
+template <bool FUSE_DELTA>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_dq_bf16_kernel(AttnDev a, BwdDev bw) {
     __shared__ __attribute__((aligned(16))) DqStage st[2];
 
@@ -59,7 +62,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             da[t] = *(const bf16x8*)(dp + 16 * t);
         }
         lse2 = bw.lse[(size_t)h * a.n_q + qi] * TT_LOG2E;
-        dlt = bw.delta[(size_t)h * a.n_q + qi];
+        if constexpr (FUSE_DELTA) {
+            // lanes l and l ^ 32 hold the two halves of the row (same query)
+            const bf16* op = (const bf16*)bw.o + ((size_t)qi * a.hq + h) * D + 8 * half;
+            float acc = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const bf16x8 ov = *(const bf16x8*)(op + 16 * t);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc += (float)ov[e] * (float)da[t][e];
+            }
+            dlt = halves_sum(acc);
+            if (half == 0) bw.delta[(size_t)h * a.n_q + qi] = dlt;
+        } else {
+            dlt = bw.delta[(size_t)h * a.n_q + qi];
+        }
     } else {
 #pragma unroll
         for (int t = 0; t < 8; ++t) { qa[t] = zero8(); da[t] = zero8(); }
@@ -443,12 +460,17 @@ static int dkdv_grid(const AttnDev& a) {
 
 int tt_bwd_bf16_launch(const AttnDev& a, const BwdDev& b, hipStream_t s) {
     const int rows = a.n_q * a.hq;
-    if (b.parts & TT_BWD_DELTA) {
+    // delta and dQ requested together: the dQ kernel computes delta itself
+    const bool fuse = (b.parts & TT_BWD_DELTA) && (b.parts & TT_BWD_DQ);
+    if ((b.parts & TT_BWD_DELTA) && !fuse) {
         hipLaunchKernelGGL(bwd_delta_bf16_kernel, dim3(tt_cdiv(rows, 16)), dim3(256), 0, s, a, b);
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     if (b.parts & TT_BWD_DQ) {
-        hipLaunchKernelGGL(bwd_dq_bf16_kernel, dim3(a.n_qb * a.hq), dim3(256), 0, s, a, b);
+        if (fuse)
+            hipLaunchKernelGGL(bwd_dq_bf16_kernel<true>, dim3(a.n_qb * a.hq), dim3(256), 0, s, a, b);
+        else
+            hipLaunchKernelGGL(bwd_dq_bf16_kernel<false>, dim3(a.n_qb * a.hq), dim3(256), 0, s, a, b);
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     if (b.parts & TT_BWD_DKDV) {
