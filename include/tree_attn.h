@@ -37,7 +37,9 @@ enum {
 enum { TT_DTYPE_F32 = 0, TT_DTYPE_BF16 = 1 };
 
 /* Parts of the backward (tt_attn_problem.bwd_parts); they must run in this
- * order, each after the previous one on the same stream. */
+ * order, each after the previous one on the same stream. Requested in one
+ * call, TT_BWD_DELTA and TT_BWD_DQ run as one bf16 kernel (the dQ pass
+ * computes the row sums it needs and stores them for TT_BWD_DKDV). */
 enum {
     TT_BWD_DELTA = 1,   /* rowsum(dO * O) into the workspace */
     TT_BWD_DQ = 2,      /* dQ (reads the workspace) */
