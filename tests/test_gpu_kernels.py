@@ -113,7 +113,7 @@ def _qkv(T, Lp, dtype, seed):
     return q, k, v, do, kp, vp
 
 
-def _run(lens, par, dtype, seed=0, past_vis=None):
+def _run(lens, par, dtype, seed=0, past_vis=None, parts=(0,)):
     from tree_training_amd.attention import attn_backward, attn_forward
     from tree_training_amd.meta import KeyPlan
     T = sum(lens)
@@ -130,7 +130,8 @@ def _run(lens, par, dtype, seed=0, past_vis=None):
     if Lp:
         acc = (torch.zeros(Lp, HKV, D, device=DEV), torch.zeros(Lp, HKV, D, device=DEV))
     o, lse = attn_forward(tr(q), tr(k), tr(v), plan, scale, tr(kp), tr(vp))
-    dq, dk, dv = attn_backward(tr(q), tr(k), tr(v), plan, scale, o, lse, do.to(DEV), tr(kp), tr(vp), acc)
+    dq, dk, dv = attn_backward(tr(q), tr(k), tr(v), plan, scale, o, lse, do.to(DEV), tr(kp), tr(vp), acc,
+                               parts=parts)
     torch.cuda.synchronize()
     # oracle on the same (rounded) inputs, fp64
     cf = meta_closed_form(lens, par)
@@ -200,6 +201,24 @@ def test_attention_gateway(dtype, shape):
     past_vis = [bool(x) for x in (rng.random(n_past) < 0.6)]
     say(f"attention gateway dtype={dtype} Lp={len(past_vis)}")
     res = _run(lens, par, dtype, seed=11, past_vis=past_vis)
+    tol = TOL[dtype]
+    for name, (ref, got) in res.items():
+        if name == "lse":
+            continue
+        check_close(name, ref, got, tol)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("parts", [(1, 2, 4), (3, 4), (1, 6)], ids=["delta,dq,dkdv", "delta+dq,dkdv", "delta,dq+dkdv"])
+def test_attention_backward_parts(parts, dtype):
+    """The backward run as separate tt_attn_bwd calls (bwd_parts in order):
+    delta by its own kernel or fused into the dQ pass, with a gateway whose
+    keys split into several dK/dV work items; against the fp64 oracle."""
+    lens, par, n_past = [2400, 1500, 1400], [-1, 0, 0], 300
+    rng = np.random.default_rng(6)
+    past_vis = [bool(x) for x in (rng.random(n_past) < 0.6)]
+    say(f"attention backward parts={parts} dtype={dtype}")
+    res = _run(lens, par, dtype, seed=12, past_vis=past_vis, parts=parts)
     tol = TOL[dtype]
     for name, (ref, got) in res.items():
         if name == "lse":

@@ -106,9 +106,10 @@ def attn_forward(q, k, v, plan: KeyPlan, scale: float, k_past=None, v_past=None)
 
 
 def attn_backward(q, k, v, plan: KeyPlan, scale: float, o, lse, d_o, k_past=None, v_past=None,
-                  gate_acc=None):
+                  gate_acc=None, parts=(0,)):
     """Returns (dq [N,Hq,D], dk [N,Hkv,D], dv [N,Hkv,D]); gateway grads are
-    added to ``gate_acc`` when given."""
+    added to ``gate_acc`` when given. ``parts``: the ``bwd_parts`` of one
+    ``tt_attn_bwd`` call each, run in order (default: one call, every part)."""
     pb = _Problem(q, k, v, k_past, v_past, plan, scale)
     dev = q.device
     d_o = d_o.reshape(1, pb.N, pb.Hq, pb.D) if d_o.dim() != 4 else d_o
@@ -124,10 +125,12 @@ def attn_backward(q, k, v, plan: KeyPlan, scale: float, o, lse, d_o, k_past=None
         for a in (acc_k, acc_v):
             if a.dtype != torch.float32 or not a.is_contiguous() or a.numel() != pb.n_past * pb.Hkv * pb.D:
                 raise TreeAttnError("gateway accumulators must be contiguous float32 [Lp, Hkv, D]")
-    rc = lib().tt_attn_bwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), TTTensor(d_o.data_ptr(), dst, dsh),
-                           _ptr(dq), _ptr(dk), _ptr(dv), _ptr(acc_k), _ptr(acc_v), _ptr(ws), ws_bytes,
-                           _stream(dev))
-    check(rc, "tt_attn_bwd")
+    for part in parts:
+        pb.s.bwd_parts = part
+        rc = lib().tt_attn_bwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), TTTensor(d_o.data_ptr(), dst, dsh),
+                               _ptr(dq), _ptr(dk), _ptr(dv), _ptr(acc_k), _ptr(acc_v), _ptr(ws), ws_bytes,
+                               _stream(dev))
+        check(rc, "tt_attn_bwd")
     return dq, dk, dv
 
 
