@@ -47,7 +47,10 @@ def to_device(t: torch.Tensor, device, dtype: torch.dtype) -> torch.Tensor:
     """``t`` as a contiguous ``dtype`` tensor on ``device``; a host tensor goes
     through pinned memory with a non-blocking copy (no stream synchronisation)."""
     if t.device.type == "cpu":
-        return t.to(dtype).contiguous().pin_memory().to(device, non_blocking=True)
+        h = t.to(dtype).contiguous()
+        # a fresh pinned copy: the caller may reuse its own (pinned) tensor at once
+        h = h.clone().pin_memory() if h.is_pinned() else h.pin_memory()
+        return h.to(device, non_blocking=True)
     return t.to(device=device, dtype=dtype).contiguous()
 
 
