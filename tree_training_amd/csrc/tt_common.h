@@ -77,11 +77,13 @@ __host__ __device__ inline void tt_kb_item_range(int qlo, int qhi, int qch, int 
 #define TT_PLAN_HDR 64
 struct PlanLayout {
     int n_qb, n_kt, n_kb;
-    size_t row_cnt, row_order, row_list, kb_qlo, kb_qhi, kb_order, kb_base, cls, total;
+    int n_pb;   // 256-key blocks of the pair count
+    size_t row_cnt, row_order, row_list, kb_qlo, kb_qhi, kb_order, kb_base, pair_part, cls, total;
     __host__ __device__ PlanLayout(int n_q, int n_keys) {
         n_qb = tt_cdiv(n_q, TT_BQ);
         n_kt = tt_cdiv(n_keys, TT_BK);
         n_kb = tt_cdiv(n_keys, TT_BKB);
+        n_pb = tt_cdiv(n_keys, 256);
         size_t o = TT_PLAN_HDR;
         row_cnt = o;   o += 4 * (size_t)n_qb;
         row_order = o; o += 4 * (size_t)n_qb;
@@ -90,6 +92,8 @@ struct PlanLayout {
         kb_qhi = o;    o += 4 * (size_t)n_kb;
         kb_order = o;  o += 4 * (size_t)n_kb;
         kb_base = o;   o += 4 * ((size_t)n_kb + 1);
+        o = (o + 7) & ~(size_t)7;
+        pair_part = o; o += 8 * (size_t)n_pb;
         cls = o;       o += (size_t)n_qb * n_kt;
         total = (o + 255) & ~(size_t)255;
     }

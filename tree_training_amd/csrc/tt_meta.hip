@@ -170,38 +170,29 @@ __global__ void dense_mask_kernel(const int32_t* __restrict__ key_lo, const int3
     mask[(size_t)i * n_keys + j] = (key_lo[j] <= i && i < key_hi[j]) ? 1 : 0;
 }
 
-__global__ void plan_header_kernel(uint8_t* plan, int n_qb, int n_kt, int n_kb) {
-    if (threadIdx.x == 0) {
-        *reinterpret_cast<unsigned long long*>(plan) = 0ull;
-        reinterpret_cast<int32_t*>(plan)[2] = n_qb;
-        reinterpret_cast<int32_t*>(plan)[3] = n_kt;
-        reinterpret_cast<int32_t*>(plan)[4] = n_kb;
-        reinterpret_cast<int32_t*>(plan)[5] = 0;
-    }
-}
-
-__global__ void plan_pairs_kernel(const int32_t* __restrict__ key_lo, const int32_t* __restrict__ key_hi,
-                                  int n_keys, int n_q, unsigned long long* __restrict__ pairs) {
+// Visible (query, key) pairs of 256 keys per workgroup, one partial per workgroup.
+__device__ __forceinline__ void plan_pairs_part(const int32_t* __restrict__ key_lo, const int32_t* __restrict__ key_hi,
+                                                int n_keys, int n_q, int blk, unsigned long long* __restrict__ part) {
     __shared__ unsigned long long s_sum;
     if (threadIdx.x == 0) s_sum = 0;
     __syncthreads();
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    const int j = blk * 256 + threadIdx.x;
     long long c = 0;
     if (j < n_keys) {
-        int a = max(key_lo[j], 0), b = min(key_hi[j], n_q);
+        const int a = max(key_lo[j], 0), b = min(key_hi[j], n_q);
         c = b > a ? (long long)(b - a) : 0;
     }
     atomicAdd(&s_sum, (unsigned long long)c);
     __syncthreads();
-    if (threadIdx.x == 0 && s_sum) atomicAdd(pairs, s_sum);
+    if (threadIdx.x == 0) part[blk] = s_sum;
 }
 
 // One wave per (query block, key tile) pair, one lane per key of the tile.
-static_assert(TT_BK == 64, "plan_classify_kernel maps the keys of a tile to the lanes of a wave");
-__global__ __launch_bounds__(256) void plan_classify_kernel(const int32_t* __restrict__ key_lo,
-                                                            const int32_t* __restrict__ key_hi, int n_keys, int n_q,
-                                                            int n_qb, int n_kt, uint8_t* __restrict__ cls) {
-    const int pair = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+static_assert(TT_BK == 64, "plan_classify maps the keys of a tile to the lanes of a wave");
+__device__ __forceinline__ void plan_classify(const int32_t* __restrict__ key_lo, const int32_t* __restrict__ key_hi,
+                                              int n_keys, int n_q, int n_qb, int n_kt, int blk,
+                                              uint8_t* __restrict__ cls) {
+    const int pair = blk * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (pair >= n_qb * n_kt) return;   // wave-uniform
     const int qb = pair / n_kt, kt = pair - qb * n_kt;
     const int i0 = qb * TT_BQ, i1 = min(i0 + TT_BQ, n_q);
@@ -236,8 +227,9 @@ __global__ void plan_compact_kernel(const uint8_t* __restrict__ cls, int n_qb, i
 
 // Query blocks ranked by decreasing tile count (ties by index): heavy blocks
 // are dispatched first.
-__global__ void plan_row_order_kernel(const int32_t* __restrict__ row_cnt, int n_qb, int32_t* __restrict__ row_order) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void plan_row_order(const int32_t* __restrict__ row_cnt, int n_qb, int blk,
+                                               int32_t* __restrict__ row_order) {
+    const int i = blk * 256 + threadIdx.x;
     if (i >= n_qb) return;
     const int c = row_cnt[i];
     int rank = 0;
@@ -250,10 +242,10 @@ __global__ void plan_row_order_kernel(const int32_t* __restrict__ row_cnt, int n
 
 // One wave per 128-key tile: the union of its keys' visible query intervals,
 // which is a single range (consecutive lower bounds, non-empty intervals).
-__global__ void plan_kv_range_kernel(const int32_t* __restrict__ key_lo, const int32_t* __restrict__ key_hi,
-                                     int n_keys, int n_q, int n_kb, int32_t* __restrict__ kb_qlo,
-                                     int32_t* __restrict__ kb_qhi) {
-    const int kb = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+__device__ __forceinline__ void plan_kv_range(const int32_t* __restrict__ key_lo, const int32_t* __restrict__ key_hi,
+                                              int n_keys, int n_q, int n_kb, int blk, int32_t* __restrict__ kb_qlo,
+                                              int32_t* __restrict__ kb_qhi) {
+    const int kb = blk * 4 + threadIdx.x / 64;
     const int lane = threadIdx.x & 63;
     if (kb >= n_kb) return;
     int lo = n_q, hi = 0;
@@ -272,9 +264,9 @@ __global__ void plan_kv_range_kernel(const int32_t* __restrict__ key_lo, const i
     }
 }
 
-__global__ void plan_kb_order_kernel(const int32_t* __restrict__ kb_qlo, const int32_t* __restrict__ kb_qhi, int n_kb,
-                                     int32_t* __restrict__ kb_order) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void plan_kb_order(const int32_t* __restrict__ kb_qlo, const int32_t* __restrict__ kb_qhi,
+                                              int n_kb, int blk, int32_t* __restrict__ kb_order) {
+    const int i = blk * 256 + threadIdx.x;
     if (i >= n_kb) return;
     const int c = kb_qhi[i] - kb_qlo[i];
     int rank = 0;
@@ -286,16 +278,56 @@ __global__ void plan_kb_order_kernel(const int32_t* __restrict__ kb_qlo, const i
 }
 
 // Exclusive prefix sum of work items per key tile, in kb_order order (one workgroup).
+// Plan pass 1: tile classes, per-128-key-tile query ranges and partial pair
+// counts, three independent reads of the key intervals in one launch
+// (workgroup ranges [0, nb_cls), [nb_cls, nb_cls + nb_kv), then the pairs).
+__global__ __launch_bounds__(256) void plan_keys_pass_kernel(const int32_t* __restrict__ key_lo,
+                                                             const int32_t* __restrict__ key_hi, int n_keys, int n_q,
+                                                             int n_qb, int n_kt, int n_kb, int nb_cls, int nb_kv,
+                                                             uint8_t* __restrict__ cls, int32_t* __restrict__ kb_qlo,
+                                                             int32_t* __restrict__ kb_qhi,
+                                                             unsigned long long* __restrict__ pair_part) {
+    const int b = blockIdx.x;
+    if (b < nb_cls)
+        plan_classify(key_lo, key_hi, n_keys, n_q, n_qb, n_kt, b, cls);
+    else if (b < nb_cls + nb_kv)
+        plan_kv_range(key_lo, key_hi, n_keys, n_q, n_kb, b - nb_cls, kb_qlo, kb_qhi);
+    else
+        plan_pairs_part(key_lo, key_hi, n_keys, n_q, b - nb_cls - nb_kv, pair_part);
+}
+
+// Plan pass 3: the query-block order and the key-tile order (heaviest first).
+__global__ __launch_bounds__(256) void plan_orders_kernel(const int32_t* __restrict__ row_cnt, int n_qb, int nb_ro,
+                                                          const int32_t* __restrict__ kb_qlo,
+                                                          const int32_t* __restrict__ kb_qhi, int n_kb,
+                                                          int32_t* __restrict__ row_order,
+                                                          int32_t* __restrict__ kb_order) {
+    if ((int)blockIdx.x < nb_ro)
+        plan_row_order(row_cnt, n_qb, blockIdx.x, row_order);
+    else
+        plan_kb_order(kb_qlo, kb_qhi, n_kb, blockIdx.x - nb_ro, kb_order);
+}
+
+// Plan pass 4: the dK/dV work-item offsets of the ordered key tiles, then the
+// header (pairs P, n_qb, n_kt, n_kb, n_items).
 __global__ __launch_bounds__(1024) void plan_kb_base_kernel(const int32_t* __restrict__ kb_qlo,
                                                             const int32_t* __restrict__ kb_qhi,
                                                             const int32_t* __restrict__ kb_order, int n_kb,
                                                             int qch, int32_t* __restrict__ kb_base,
-                                                            int32_t* __restrict__ n_items) {
+                                                            const unsigned long long* __restrict__ pair_part,
+                                                            int n_pb, int n_qb, int n_kt, uint8_t* __restrict__ plan) {
+    __shared__ unsigned long long s_pairs;
     __shared__ int s_scan[1024];
     __shared__ int s_carry;
     const int tid = threadIdx.x;
-    if (tid == 0) s_carry = 0;
+    if (tid == 0) {
+        s_carry = 0;
+        s_pairs = 0;
+    }
     __syncthreads();
+    unsigned long long pairs = 0;
+    for (int i = tid; i < n_pb; i += 1024) pairs += pair_part[i];
+    atomicAdd(&s_pairs, pairs);
     for (int base = 0; base < n_kb; base += 1024) {
         const int r = base + tid;
         int v = 0;
@@ -316,9 +348,15 @@ __global__ __launch_bounds__(1024) void plan_kb_base_kernel(const int32_t* __res
         if (tid == 1023) s_carry += s_scan[tid];
         __syncthreads();
     }
+    __syncthreads();
     if (tid == 0) {
         kb_base[n_kb] = s_carry;
-        *n_items = s_carry;
+        *reinterpret_cast<unsigned long long*>(plan) = s_pairs;
+        int32_t* hdr = reinterpret_cast<int32_t*>(plan);
+        hdr[2] = n_qb;
+        hdr[3] = n_kt;
+        hdr[4] = n_kb;
+        hdr[5] = s_carry;
     }
 }
 
@@ -361,7 +399,6 @@ int tt_plan_build_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys,
                        hipStream_t s) {
     const PlanLayout L(n_q, n_keys);
     uint8_t* base = reinterpret_cast<uint8_t*>(plan);
-    int32_t* hdr = reinterpret_cast<int32_t*>(base);
     int32_t* row_cnt = reinterpret_cast<int32_t*>(base + L.row_cnt);
     int32_t* row_order = reinterpret_cast<int32_t*>(base + L.row_order);
     int32_t* row_list = reinterpret_cast<int32_t*>(base + L.row_list);
@@ -370,20 +407,16 @@ int tt_plan_build_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys,
     int32_t* kb_order = reinterpret_cast<int32_t*>(base + L.kb_order);
     int32_t* kb_base = reinterpret_cast<int32_t*>(base + L.kb_base);
     uint8_t* cls = base + L.cls;
-    hipLaunchKernelGGL(plan_header_kernel, dim3(1), dim3(64), 0, s, base, L.n_qb, L.n_kt, L.n_kb);
-    hipLaunchKernelGGL(plan_pairs_kernel, dim3(tt_cdiv(n_keys, 256)), dim3(256), 0, s, key_lo, key_hi, n_keys,
-                       n_q, reinterpret_cast<unsigned long long*>(base));
-    hipLaunchKernelGGL(plan_classify_kernel, dim3(tt_cdiv(L.n_qb * L.n_kt, 4)), dim3(256), 0, s, key_lo, key_hi,
-                       n_keys, n_q, L.n_qb, L.n_kt, cls);
+    unsigned long long* pair_part = reinterpret_cast<unsigned long long*>(base + L.pair_part);
+    const int nb_cls = tt_cdiv(L.n_qb * L.n_kt, 4), nb_kv = tt_cdiv(L.n_kb, 4);
+    hipLaunchKernelGGL(plan_keys_pass_kernel, dim3(nb_cls + nb_kv + L.n_pb), dim3(256), 0, s, key_lo, key_hi, n_keys,
+                       n_q, L.n_qb, L.n_kt, L.n_kb, nb_cls, nb_kv, cls, kb_qlo, kb_qhi, pair_part);
     hipLaunchKernelGGL(plan_compact_kernel, dim3(tt_cdiv(L.n_qb, 4)), dim3(256), 0, s, cls, L.n_qb, L.n_kt,
                        row_cnt, row_list);
-    hipLaunchKernelGGL(plan_row_order_kernel, dim3(tt_cdiv(L.n_qb, 256)), dim3(256), 0, s, row_cnt, L.n_qb,
-                       row_order);
-    hipLaunchKernelGGL(plan_kv_range_kernel, dim3(tt_cdiv(L.n_kb, 4)), dim3(256), 0, s, key_lo, key_hi, n_keys,
-                       n_q, L.n_kb, kb_qlo, kb_qhi);
-    hipLaunchKernelGGL(plan_kb_order_kernel, dim3(tt_cdiv(L.n_kb, 256)), dim3(256), 0, s, kb_qlo, kb_qhi, L.n_kb,
-                       kb_order);
+    const int nb_ro = tt_cdiv(L.n_qb, 256);
+    hipLaunchKernelGGL(plan_orders_kernel, dim3(nb_ro + tt_cdiv(L.n_kb, 256)), dim3(256), 0, s, row_cnt, L.n_qb,
+                       nb_ro, kb_qlo, kb_qhi, L.n_kb, row_order, kb_order);
     hipLaunchKernelGGL(plan_kb_base_kernel, dim3(1), dim3(1024), 0, s, kb_qlo, kb_qhi, kb_order, L.n_kb, tt_qch(n_q),
-                       kb_base, hdr + 5);
+                       kb_base, pair_part, L.n_pb, L.n_qb, L.n_kt, base);
     return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
 }
