@@ -100,6 +100,91 @@ def test_meta_rejects_bad_input():
         TreeMetaDevice([2, 0, 1], [-1, 0, 0], device=DEV, validate=True)  # empty node
 
 
+# --------------------------------------------------------------------------- tile plan
+def _plan_expected(lo, hi, n_q):
+    """The tile plan restated in numpy from the key intervals [lo, hi): header,
+    per 128-query block the ascending non-empty 64-key tiles tagged full, the
+    heaviest-first block order, per 128-key tile the visible query range, its
+    heaviest-first order and the dK/dV work-item offsets."""
+    lo, hi = np.asarray(lo, np.int64), np.asarray(hi, np.int64)
+    n_keys = len(lo)
+    n_qb, n_kt, n_kb = -(-n_q // 128), -(-n_keys // 64), -(-n_keys // 128)
+    a, b = np.maximum(lo, 0), np.minimum(hi, n_q)
+    P = int(np.clip(b - a, 0, None).sum())
+    rows = []
+    for qb in range(n_qb):
+        i0, i1 = 128 * qb, min(128 * qb + 128, n_q)
+        lst = []
+        for kt in range(n_kt):
+            j = np.arange(64 * kt, min(64 * kt + 64, n_keys))
+            some = (np.maximum(lo[j], i0) < np.minimum(hi[j], i1)).any()
+            every = len(j) == 64 and ((lo[j] <= i0) & (hi[j] >= i1)).all()
+            if some:
+                lst.append((kt << 1) | int(every))
+        rows.append(lst)
+    cnt = np.array([len(r) for r in rows])
+    row_order = sorted(range(n_qb), key=lambda i: (-cnt[i], i))
+    qlo, qhi = np.zeros(n_kb, np.int64), np.zeros(n_kb, np.int64)
+    for kb in range(n_kb):
+        j = np.arange(128 * kb, min(128 * kb + 128, n_keys))
+        vis = a[j] < b[j]
+        if vis.any():
+            qlo[kb], qhi[kb] = a[j][vis].min(), b[j][vis].max()
+    kb_order = sorted(range(n_kb), key=lambda i: (-(qhi[i] - qlo[i]), i))
+    half = (1 << (n_q.bit_length() - 1)) // 2 if n_q >= 2 else 0
+    qch = 4096 if half > 4096 else max(half, 256)
+    items = [1 if qhi[k] - qlo[k] <= qch else (qhi[k] - 1) // qch - qlo[k] // qch + 1 for k in kb_order]
+    kb_base = np.concatenate([[0], np.cumsum(items)])
+    return dict(P=P, n_qb=n_qb, n_kt=n_kt, n_kb=n_kb, rows=rows, row_order=row_order, qlo=qlo, qhi=qhi,
+                kb_order=kb_order, kb_base=kb_base)
+
+
+def _plan_decode(buf, n_q, n_keys):
+    """The device plan buffer split at PlanLayout's offsets (64-byte header)."""
+    n_qb, n_kt, n_kb = -(-n_q // 128), -(-n_keys // 64), -(-n_keys // 128)
+    i32 = lambda off, n: np.frombuffer(buf, np.int32, n, off)
+    o = 64
+    row_cnt = i32(o, n_qb); o += 4 * n_qb
+    row_order = i32(o, n_qb); o += 4 * n_qb
+    row_list = i32(o, n_qb * n_kt).reshape(n_qb, n_kt); o += 4 * n_qb * n_kt
+    qlo = i32(o, n_kb); o += 4 * n_kb
+    qhi = i32(o, n_kb); o += 4 * n_kb
+    kb_order = i32(o, n_kb); o += 4 * n_kb
+    kb_base = i32(o, n_kb + 1)
+    hdr = i32(8, 4)
+    return dict(P=int(np.frombuffer(buf, np.uint64, 1, 0)[0]), n_qb=int(hdr[0]), n_kt=int(hdr[1]),
+                n_kb=int(hdr[2]), n_items=int(hdr[3]),
+                rows=[list(row_list[q, :row_cnt[q]]) for q in range(n_qb)], row_order=list(row_order),
+                qlo=qlo, qhi=qhi, kb_order=list(kb_order), kb_base=kb_base)
+
+
+@pytest.mark.parametrize("case", ["forest", "agent16k", "gateway"])
+def test_plan_matches_numpy(case):
+    """Every field of the device tile plan equals the numpy restatement
+    (bit-exact: it is index work)."""
+    from tree_training_amd.meta import KeyPlan
+    bias = None
+    if case == "forest":
+        lens, par = workloads.random_forest(4, node_len=(1, 300))
+    elif case == "agent16k":
+        lens, par = workloads.agent_tree(0)
+    else:
+        lens, par = [700, 500, 300], [-1, 0, 0]
+        vis = np.random.default_rng(3).random(1300) < 0.7
+        bias = torch.tensor(np.where(vis, 0.0, -np.inf), dtype=torch.float32, device=DEV)
+    say(f"plan case={case} T={sum(lens)}")
+    m = _meta(lens, par)
+    plan = KeyPlan(m.horizon, bias, validate=True)
+    n_q, n_keys = plan.n_q, plan.n_keys
+    got = _plan_decode(plan.plan.cpu().numpy().tobytes(), n_q, n_keys)
+    exp = _plan_expected(plan.key_lo.cpu().numpy(), plan.key_hi.cpu().numpy(), n_q)
+    for k in ("P", "n_qb", "n_kt", "n_kb", "rows", "row_order", "kb_order"):
+        assert got[k] == exp[k], k
+    for k in ("qlo", "qhi", "kb_base"):
+        assert np.array_equal(got[k], exp[k]), k
+    assert got["n_items"] == exp["kb_base"][-1]
+
+
 # --------------------------------------------------------------------------- attention
 def _qkv(T, Lp, dtype, seed):
     g = torch.Generator().manual_seed(seed)
