@@ -49,7 +49,8 @@ enum {
 /* Device-side status bits written by tt_meta_build / tt_keys_build. */
 enum {
     TT_STATUS_BAD_LEN = 1,      /* a node with length < 1 */
-    TT_STATUS_BAD_PARENT = 2,   /* parent not in [-1, self) (not DFS pre-order) */
+    TT_STATUS_BAD_PARENT = 2,   /* not DFS pre-order: a parent outside [-1, self), or a node that
+                                   comes after its parent's subtree has closed (parents [-1, 0, 0, 1]) */
     TT_STATUS_BAD_TOTAL = 4,    /* sum of node lengths != n_tokens */
     TT_STATUS_BAD_BIAS = 8      /* a gateway bias that is neither 0 nor -inf */
 };
@@ -63,7 +64,9 @@ const char* tt_strerror(int code);
  * per-token subtree horizon h. Also the per-partition position offset of
  * tree_grad_hybrid.py:307-310 (pos_offset).
  * Input: node_len[n_nodes], node_parent[n_nodes] in DFS pre-order
- * (parent < child, -1 for a root). Output (int32):
+ * (-1 for a root; parent < child, and every node between a parent and its
+ * child is a descendant of that parent: the order build_dfs_tree_info
+ * produces). Output (int32):
  *   node_start[n], node_off[n] (sum of ancestor lengths), node_hend[n]
  *   (exclusive end token of the node's subtree), pos[T] = pos_offset +
  *   node_off + offset-in-node, node_of[T], horizon[T] = node_hend[node_of].
@@ -137,6 +140,11 @@ int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* stream);
  * Gateway gradients are ADDED in float32 to dk_past_acc/dv_past_acc
  * [n_past, Hkv, D] contiguous, 16-byte aligned (the fp32 hook accumulation of
  * tree_grad_hybrid.py:220-225, kept on the device); pass NULL to drop them.
+ * Within one call every accumulator element has one writer at a time (plain
+ * read-add-write, or fp32 atomics where a key's query range is split), so
+ * calls may share accumulators only when ordered on one stream: two calls in
+ * flight at once on different streams must not add into the same
+ * accumulators.
  * ws must be 16-byte aligned. float32 problems are deterministic (one writer
  * per output element). bf16 problems are too, except that keys whose visible
  * query range spans more than W queries, W = half the largest power of two

@@ -239,3 +239,34 @@ def test_gdn_autograd_keep_and_recompute_agree():
     ref = _oracle_grads(q, k, v, g, beta, d_o, lens, par)
     for name, a, b in zip(BWD_NAMES, grads[0], ref):
         assert _rel(a.cpu().numpy(), b) < 1e-5, (name, _rel(a.cpu().numpy(), b))
+
+
+def test_gdn_retain_graph_backwards_reuse_saved_forward(monkeypatch):
+    """Under the reference's per-leaf schedule (several backward calls through
+    one graph with retain_graph=True) every backward takes the kept forward
+    terms (no recompute), and each gives the same gradients."""
+    from tree_training_amd import gdn as tgdn
+    c = CASES["forest_multi_chunk"]
+    lens, par = c["topo"]()
+    T = sum(lens)
+    q, k, v, g, beta = _inputs(T, c["Hk"], c["Hv"], 78)
+    d_o = np.random.default_rng(15).standard_normal((T, c["Hv"], D)).astype(np.float32)
+    dev = torch.device("cuda", 0)
+    tree = GdnTree(lens, par, dev)
+    seen = []
+    real = tgdn.gdn_tree_backward
+
+    def spy(*a, **kw):
+        seen.append(kw.get("saved") is not None)
+        return real(*a, **kw)
+
+    monkeypatch.setattr(tgdn, "gdn_tree_backward", spy)
+    tt = [torch.from_numpy(x).to(dev).requires_grad_(True) for x in (q, k, v, g, beta)]
+    o, _ = tgdn.gdn_tree(*tt, tree)
+    loss = (o * torch.from_numpy(d_o).to(dev)).sum()
+    grads = [torch.autograd.grad(loss, tt, retain_graph=True) for _ in range(3)]
+    torch.cuda.synchronize()
+    assert seen == [True, True, True]
+    for gr in grads[1:]:
+        for name, a, b in zip(BWD_NAMES, grads[0], gr):
+            assert torch.equal(a, b), name

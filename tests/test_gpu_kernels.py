@@ -98,6 +98,20 @@ def test_meta_rejects_bad_input():
         TreeMetaDevice([2, 3], [-1, 1], device=DEV, validate=True)   # parent not before child
     with pytest.raises(ValueError):
         TreeMetaDevice([2, 0, 1], [-1, 0, 0], device=DEV, validate=True)  # empty node
+    with pytest.raises(ValueError):
+        TreeMetaDevice([1, 1, 1, 1], [-1, 0, 0, 1], device=DEV, validate=True)   # not pre-order
+
+
+def test_meta_status_flags_non_preorder():
+    """The device check alone (host check skipped): parent < i holds for
+    parents [-1, 0, 0, 1] but node 3 follows its parent's closed subtree."""
+    from tree_training_amd._lib import TT_STATUS_BAD_PARENT
+    from tree_training_amd.meta import TreeMetaDevice
+    m = TreeMetaDevice([1, 1, 1, 1], [-1, 0, 0, 1], device=DEV, validate=False)
+    assert int(m.status.item()) & TT_STATUS_BAD_PARENT
+    for lens, par in [([3, 4, 3, 4, 5, 3, 3, 4, 4, 3, 4, 3, 4], [-1, 0, 1, 2, 3, 3, 2, 6, -1, 8, 9, 8, 11]),
+                      ([1, 1, 1, 1, 1], [-1, 0, 1, 1, 0])]:
+        assert int(TreeMetaDevice(lens, par, device=DEV, validate=False).status.item()) == 0
 
 
 # --------------------------------------------------------------------------- tile plan

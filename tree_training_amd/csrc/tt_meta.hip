@@ -124,6 +124,18 @@ __global__ __launch_bounds__(kNodeThreads) void meta_nodes_kernel(
         }
         hend[c] = (i < n) ? start[i] : T;
     }
+    __syncthreads();   // hend of every node visible
+
+    // 4. pre-order: parent < i alone admits orders such as parents [-1, 0, 0, 1],
+    // where node 3's parent subtree has closed (node 2, depth 1, comes first).
+    // Given parent < i, a node that starts inside its parent's subtree range
+    // for every node is exactly DFS pre-order (every node between a parent and
+    // its child is then a descendant of that parent).
+    for (int i = tid; i < n; i += kNodeThreads) {
+        const int p = par[i];
+        if (p >= 0 && p < i && start[i] >= hend[p]) atomicOr(&s_err, TT_STATUS_BAD_PARENT);
+    }
+    __syncthreads();
     if (tid == 0 && s_err) atomicOr(status, s_err);
 }
 

@@ -1,8 +1,7 @@
-"""Gateway KV between partitions — drop-in for ``GatewayCache`` and ``SubtreeGateway``.
+"""Gateway KV between partitions — drop-in for ``GatewayCache``.
 
 ``GatewayCache`` keeps the HF-Cache duck type of tree_grad_ckpt_opath.py:66-195
-(``update``, ``get_seq_length``, ``get_mask_sizes``, ``_full_kv``,
-``make_child_gates``). Under the tree-attention implementation it runs in
+(``update``, ``get_seq_length``, ``get_mask_sizes``, ``_full_kv``). Under the tree-attention implementation it runs in
 *segmented* mode: ``update`` records the gateway and the new K/V as two segments
 and returns the new K/V unchanged; the attention kernel reads both segments in
 place, so the per-layer ``cat`` of the reference never happens.
@@ -15,7 +14,6 @@ gradients into it in float32, with no host round trip.
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
 from typing import Dict, List, Optional, Tuple
 
 import torch
@@ -115,61 +113,3 @@ class GatewayCache:
     @property
     def is_compileable(self) -> bool:
         return False
-
-    # -- next-level gates (tree_grad_ckpt_opath.py:137-195) -------------------
-    def make_child_gates(self):
-        """Detached leaves of this pass's full KV, with device fp32 gradient
-        accumulation. Returns (child_cache, raw_tensors, gate_tensors, fp32_accum)
-        where fp32_accum[i] is a one-element list holding the fp32 sum (or None)."""
-        layers = sorted(self._full_kv.keys())
-        n_layers = (max(layers) + 1) if layers else 0
-        gate_next, raws, gates, accs = [], [], [], []
-        for l in range(n_layers):
-            if l not in self._full_kv:
-                gate_next.append((None, None))
-                continue
-            fk, fv = self._full_kv[l]
-            if fk.grad_fn is None:
-                gate_next.append((fk, fv))
-                continue
-            gk = fk.detach().requires_grad_(True)
-            gv = fv.detach().requires_grad_(True)
-            ak, av = [None], [None]
-
-            def _hook(acc):
-                def hook(g):
-                    g32 = g.detach().float()
-                    acc[0] = g32 if acc[0] is None else acc[0] + g32
-                    return torch.zeros_like(g)
-                return hook
-
-            gk.register_hook(_hook(ak))
-            gv.register_hook(_hook(av))
-            raws += [fk, fv]
-            gates += [gk, gv]
-            accs += [ak, av]
-            gate_next.append((gk, gv))
-        return GatewayCache(gate_next, segmented=self.segmented), raws, gates, accs
-
-
-@dataclass
-class SubtreeGateway:
-    """Gateway from a parent partition to the child partitions of one cut node
-    (tree_grad_hybrid.py:160-171). ``fp32_k/fp32_v`` are device accumulators."""
-    key_gates: List[torch.Tensor]        # detached leaves [1, Hkv, past_len, D]
-    val_gates: List[torch.Tensor]
-    raw_keys: List[torch.Tensor]         # same slices with grad_fn into the parent
-    raw_vals: List[torch.Tensor]
-    fp32_acc: List[GatewayAccumulator]
-    past_len: int
-    attn_bias: torch.Tensor              # [past_len] float32, 0 or -inf
-    pos_offset: int
-    ssm: Optional[object] = None
-
-    @property
-    def fp32_k(self):
-        return [[a.k if a.touched else None] for a in self.fp32_acc]
-
-    @property
-    def fp32_v(self):
-        return [[a.v if a.touched else None] for a in self.fp32_acc]

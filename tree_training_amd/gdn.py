@@ -243,18 +243,20 @@ class GdnTreeFunction(torch.autograd.Function):
     def forward(ctx, q, k, v, g, beta, tree, scale, l2norm):
         keep = bool(KEEP_FORWARD_STATES)
         o, states, saved = _gdn_forward(q, k, v, g, beta, tree, scale, l2norm, keep)
-        ctx.save_for_backward(q, k, v, g, beta)
+        # The kept forward terms go through save_for_backward as well: autograd
+        # then frees them with the graph (after a backward without retain_graph,
+        # or when the graph is dropped), and every backward of a graph run
+        # with retain_graph (the reference's per-leaf schedule) reuses them.
+        ctx.save_for_backward(q, k, v, g, beta, *(() if saved is None else (saved,)))
         ctx.tree, ctx.scale, ctx.l2norm = tree, scale, l2norm
-        ctx.gdn_saved = saved
         ctx.mark_non_differentiable(states)
         return o, states
 
     @staticmethod
     def backward(ctx, d_o, _d_states):
-        q, k, v, g, beta = ctx.saved_tensors
+        q, k, v, g, beta, *kept = ctx.saved_tensors
         dq, dk, dv, dg, dbeta = gdn_tree_backward(q, k, v, g, beta, d_o, ctx.tree, ctx.scale, ctx.l2norm,
-                                                  saved=ctx.gdn_saved)
-        ctx.gdn_saved = None
+                                                  saved=kept[0] if kept else None)
         return (dq.reshape(q.shape).to(q.dtype), dk.reshape(k.shape).to(k.dtype), dv.reshape(v.shape).to(v.dtype),
                 dg.reshape(g.shape).to(g.dtype), dbeta.reshape(beta.shape).to(beta.dtype), None, None, None)
 

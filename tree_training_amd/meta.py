@@ -21,6 +21,7 @@ import torch
 
 from . import _lib
 from ._lib import check, lib
+from .tree import preorder_violation
 
 
 def _ptr(t: Optional[torch.Tensor]):
@@ -71,10 +72,14 @@ class TreeMetaDevice:
 
     def __init__(self, node_len: Sequence[int], parent: Sequence[int], pos_offset: int = 0,
                  device=None, validate: bool = False):
-        dev = require_device(device)
         n = len(node_len)
         if n < 1:
             raise ValueError("empty forest")
+        if validate:
+            bad = preorder_violation(parent)
+            if bad is not None:
+                raise ValueError(f"node {bad}: parent {parent[bad]} breaks DFS pre-order")
+        dev = require_device(device)
         T = int(sum(node_len))
         self.device, self.n_nodes, self.T, self.pos_offset = dev, n, T, int(pos_offset)
         i32 = dict(dtype=torch.int32, device=dev)
@@ -100,7 +105,8 @@ class TreeMetaDevice:
         st = int(self.status.item())
         if st:
             raise ValueError(f"invalid tree metadata input (status bits {st:#x}): "
-                             "node lengths must be >= 1 and parents must precede children (DFS pre-order)")
+                             "node lengths must be >= 1, lengths must sum to the token count and the "
+                             "parents must form a DFS pre-order (each node inside its parent's subtree range)")
 
 
 class KeyPlan:

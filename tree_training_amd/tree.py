@@ -12,7 +12,7 @@ never builds the [N, N] mask.
 from __future__ import annotations
 
 from dataclasses import dataclass, field
-from typing import List, Optional, Tuple
+from typing import List, Optional, Sequence, Tuple
 
 import torch
 
@@ -112,6 +112,24 @@ class DFSTreeInfo:
         if self._mask_cache is None:
             self._mask_cache = self.key_plan().dense_mask().cpu()
         return self._mask_cache
+
+
+def preorder_violation(parent: Sequence[int]) -> Optional[int]:
+    """First node index whose parent list position breaks DFS pre-order, or
+    None. ``parent[i] < i`` is necessary but not sufficient: in pre-order every
+    node between a parent and its child is a descendant of that parent, i.e.
+    the parent is still on the open root-to-node path when the child comes."""
+    path: List[int] = []
+    for i, p in enumerate(parent):
+        p = int(p)
+        if p < -1 or p >= i:
+            return i
+        while path and path[-1] != p:
+            path.pop()
+        if p >= 0 and not path:
+            return i
+        path.append(i)
+    return None
 
 
 def info_from_flat(node_len: List[int], parent: List[int], nodes: list) -> DFSTreeInfo:
