@@ -6,7 +6,8 @@
  * caller supplies every workspace). Arguments are validated on the host before
  * any HIP call; a failed check returns a negative TT_E_* code and launches
  * nothing. No C++ exception crosses this boundary. The library keeps no
- * mutable global state.
+ * mutable global state, except the per-GPU scratch array of
+ * tt_attn_bwd_noalloc (the one entry point that takes no workspace).
  *
  * Visibility model. A problem has n_q query tokens (the DFS-packed tokens of
  * one tree or one partition) and n_keys = n_past + n_q keys: first the
@@ -155,6 +156,26 @@ size_t tt_attn_bwd_workspace_bytes(const tt_attn_problem* p);
 int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_tensor d_o,
                 void* dq, void* dk, void* dv, float* dk_past_acc, float* dv_past_acc,
                 void* ws, size_t ws_bytes, void* stream);
+
+/* No counterpart in the reference: tt_attn_bwd for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments, results and validation as
+ * tt_attn_bwd, without ws / ws_bytes: the workspace is a scratch array of
+ * TT_NOALLOC_SCRATCH_MB MiB that the library holds on each GPU it runs on
+ * until the process ends (the current device's, hipGetDevice; `stream` must
+ * belong to it). A problem whose tt_attn_bwd_workspace_bytes exceeds it
+ * returns TT_E_WORKSPACE (bf16 needs 128 * Hq * n_q + 1024 * Hkv * (n_q +
+ * n_past) bytes: about 8K keys at Hq = 32, Hkv = 8). The call allocates and
+ * frees nothing (no hipMalloc, no hipMemsetAsync: what must start at zero is
+ * cleared by a kernel). Every call on one GPU uses that GPU's one scratch
+ * array, which keeps the last call's contents: calls that overlap on one GPU
+ * (other streams, other threads) race and must not be issued; a TT_BWD_*
+ * sequence split over several calls must not be interleaved with another
+ * call on the same GPU. */
+#define TT_NOALLOC_SCRATCH_MB 64
+size_t tt_noalloc_scratch_bytes(void);
+int tt_attn_bwd_noalloc(const tt_attn_problem* p, const void* o, const float* lse, tt_tensor d_o,
+                        void* dq, void* dk, void* dv, float* dk_past_acc, float* dv_past_acc, void* stream);
 
 /* ---- attention prologue: q/k RMSNorm + rotary embedding -------------------
  * Replaces the per-head q_norm / k_norm and apply_rotary_pos_emb that

@@ -84,6 +84,20 @@ def test_bwd_validation():
     assert lib.tt_attn_bwd(ctypes.byref(p), V, V, d_o, V, V, V, None, None, V, 8, None) == _lib.TT_E_WORKSPACE
 
 
+def test_bwd_noalloc_validation():
+    """The no-allocation backward: a 64 MiB scratch, null problems rejected,
+    and a problem whose workspace exceeds the scratch refused on the host
+    (no HIP call: these run without a GPU)."""
+    lib = _lib.lib()
+    assert lib.tt_noalloc_scratch_bytes() == 64 << 20
+    d_o = _lib.TTTensor(16, 32 * 128, 128)
+    V = ctypes.c_void_p(16)
+    assert lib.tt_attn_bwd_noalloc(None, V, V, d_o, V, V, V, None, None, None) == _lib.TT_E_ARG
+    big = _problem(n_q=40000)
+    assert lib.tt_attn_bwd_workspace_bytes(ctypes.byref(big)) > lib.tt_noalloc_scratch_bytes()
+    assert lib.tt_attn_bwd_noalloc(ctypes.byref(big), V, V, d_o, V, V, V, None, None, None) == _lib.TT_E_WORKSPACE
+
+
 def test_meta_and_plan_validation():
     lib = _lib.lib()
     V = ctypes.c_void_p(16)

@@ -1,0 +1,124 @@
+"""tt_attn_bwd_noalloc (the backward without a workspace argument, for callers
+that cannot allocate) against tt_attn_bwd on the same inputs, through the C
+ABI: two calls in a row on one GPU, the second with a smaller problem, so the
+shared scratch array is reused with stale contents from the first.
+
+Bars: float32 results bitwise equal (both entry points run the same
+deterministic kernels); bf16 dq bitwise equal, dk / dv / gateway accumulators
+within the bf16 bar (max_rel < 2e-2; fp32 atomics of split key tiles may round
+differently between runs)."""
+import ctypes
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from tree_training_amd import _lib, workloads
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0)
+HQ, HKV, D = 32, 8, 128
+
+
+def _rel(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return float((a - b).abs().max() / max(float(b.abs().max()), 1e-30))
+
+
+def _case(lens, par, n_past, dtype, seed):
+    from tree_training_amd.attention import _Problem
+    from tree_training_amd.meta import KeyPlan, TreeMetaDevice
+    T = sum(lens)
+    g = torch.Generator().manual_seed(seed)
+    mk = lambda *s: torch.randn(*s, generator=g).to(dtype).to(DEV)
+    q, k, v, do = mk(1, T, HQ, D), mk(1, T, HKV, D), mk(1, T, HKV, D), mk(1, T, HQ, D)
+    kp = vp = bias = None
+    if n_past:
+        kp, vp = mk(1, n_past, HKV, D), mk(1, n_past, HKV, D)
+        bias = torch.tensor([0.0 if (i % 5) != 2 else -math.inf for i in range(n_past)])
+    meta = TreeMetaDevice(lens, par, device=DEV, validate=True)
+    plan = KeyPlan(meta.horizon, bias, validate=True)
+    tr = lambda x: None if x is None else x.transpose(1, 2)
+    pb = _Problem(tr(q), tr(k), tr(v), tr(kp), tr(vp), plan, D ** -0.5)
+    o = torch.empty((T, HQ, D), dtype=dtype, device=DEV)
+    lse = torch.empty((HQ, T), dtype=torch.float32, device=DEV)
+    st = ctypes.c_void_p(torch.cuda.current_stream(DEV).cuda_stream)
+    _lib.check(_lib.lib().tt_attn_fwd(ctypes.byref(pb.s), ctypes.c_void_p(o.data_ptr()),
+                                      ctypes.c_void_p(lse.data_ptr()), st), "tt_attn_fwd")
+    return dict(pb=pb, o=o, lse=lse, do=do, T=T, n_past=n_past, dtype=dtype, keep=(meta, plan))
+
+
+def _bwd(c, noalloc):
+    lib = _lib.lib()
+    T, n_past, dtype = c["T"], c["n_past"], c["dtype"]
+    dq = torch.full((T, HQ, D), float("nan"), dtype=dtype, device=DEV)
+    dk = torch.full((T, HKV, D), float("nan"), dtype=dtype, device=DEV)
+    dv = torch.full((T, HKV, D), float("nan"), dtype=dtype, device=DEV)
+    acc = [torch.zeros(max(n_past, 1), HKV, D, device=DEV) for _ in range(2)]
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    d_o = _lib.TTTensor(c["do"].data_ptr(), HQ * D, D)
+    st = ctypes.c_void_p(torch.cuda.current_stream(DEV).cuda_stream)
+    accp = [P(a) if n_past else None for a in acc]
+    if noalloc:
+        rc = lib.tt_attn_bwd_noalloc(ctypes.byref(c["pb"].s), P(c["o"]), P(c["lse"]), d_o, P(dq), P(dk), P(dv),
+                                     accp[0], accp[1], st)
+        what = "tt_attn_bwd_noalloc"
+    else:
+        ws_bytes = lib.tt_attn_bwd_workspace_bytes(ctypes.byref(c["pb"].s))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+        rc = lib.tt_attn_bwd(ctypes.byref(c["pb"].s), P(c["o"]), P(c["lse"]), d_o, P(dq), P(dk), P(dv),
+                             accp[0], accp[1], P(ws), ws_bytes, st)
+        what = "tt_attn_bwd"
+    _lib.check(rc, what)
+    torch.cuda.synchronize()
+    return dq, dk, dv, acc[0][:n_past], acc[1][:n_past]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_noalloc_backward_matches_workspace_backward(dtype):
+    big = (workloads.random_forest(14, node_len=(40, 300)), 700)       # ragged forest + gateway
+    small = (([70, 45, 90, 33], [-1, 0, 0, 2]), 0)                      # smaller, no gateway
+    for step, ((lens, par), n_past) in enumerate((big, small)):
+        print(f"noalloc {dtype} call {step}: T={sum(lens)} n_past={n_past}", flush=True)
+        sys.stdout.flush()
+        c = _case(lens, par, n_past, dtype, seed=40 + step)
+        need = _lib.lib().tt_attn_bwd_workspace_bytes(ctypes.byref(c["pb"].s))
+        assert 0 < need <= _lib.lib().tt_noalloc_scratch_bytes()
+        ref = _bwd(c, noalloc=False)
+        got = _bwd(c, noalloc=True)
+        names = ("dq", "dk", "dv", "dk_gateway", "dv_gateway")
+        for name, a, b in zip(names, got, ref):
+            assert a.shape == b.shape, name
+            if a.numel() == 0:      # gateway slices of the call without a gateway
+                continue
+            assert torch.isfinite(a).all(), name
+            if dtype == torch.float32 or name == "dq":
+                assert torch.equal(a, b), name
+            else:
+                assert _rel(a, b) < 2e-2, (name, _rel(a, b))
+
+
+def test_noalloc_rejects_problems_beyond_the_scratch():
+    """A problem whose workspace exceeds the scratch array returns
+    TT_E_WORKSPACE and launches nothing (outputs untouched)."""
+    from tree_training_amd.attention import _Problem
+    from tree_training_amd.meta import KeyPlan, TreeMetaDevice
+    lib = _lib.lib()
+    T = 40000
+    meta = TreeMetaDevice([T], [-1], device=DEV, validate=True)
+    plan = KeyPlan(meta.horizon)
+    x = torch.zeros(1, HQ, T, D, dtype=torch.bfloat16, device=DEV)
+    kv = torch.zeros(1, HKV, T, D, dtype=torch.bfloat16, device=DEV)
+    pb = _Problem(x, kv, kv, None, None, plan, D ** -0.5)
+    assert lib.tt_attn_bwd_workspace_bytes(ctypes.byref(pb.s)) > lib.tt_noalloc_scratch_bytes()
+    out = torch.full((T, HQ, D), 7.0, dtype=torch.bfloat16, device=DEV)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    rc = lib.tt_attn_bwd_noalloc(ctypes.byref(pb.s), P(out), P(out), _lib.TTTensor(out.data_ptr(), HQ * D, D),
+                                 P(out), P(out), P(out), None, None,
+                                 ctypes.c_void_p(torch.cuda.current_stream(DEV).cuda_stream))
+    assert rc == _lib.TT_E_WORKSPACE
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())

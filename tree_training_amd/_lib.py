@@ -38,7 +38,7 @@ EXPORTS = (
     "tt_gdn_bwd_workspace_bytes", "tt_gdn_tree_bwd", "tt_gdn_saved_bytes", "tt_gdn_tree_fwd_save",
     "tt_gdn_bwd_saved_workspace_bytes", "tt_gdn_tree_bwd_saved", "tt_tree_conv_fwd", "tt_tree_conv_bwd_workspace_bytes",
     "tt_tree_conv_bwd", "tt_qk_prologue_fwd", "tt_qk_prologue_bwd_workspace_bytes", "tt_qk_prologue_bwd", "tt_ce_rows",
-    "tt_selftest_mfma32",
+    "tt_selftest_mfma32", "tt_noalloc_scratch_bytes", "tt_attn_bwd_noalloc",
 )
 
 
@@ -133,6 +133,8 @@ def _declare(lib):
         "tt_tree_conv_bwd": (ctypes.c_int, [ctypes.POINTER(TTConvProblem), P, ctypes.c_int64, P, P, P, P, SZ,
                                             VP]),
         "tt_selftest_mfma32": (ctypes.c_int, [P, P, P, VP]),
+        "tt_noalloc_scratch_bytes": (SZ, []),
+        "tt_attn_bwd_noalloc": (ctypes.c_int, [ctypes.POINTER(TTAttnProblem), P, P, TTTensor, P, P, P, P, P, VP]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

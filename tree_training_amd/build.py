@@ -19,7 +19,7 @@ LIBDIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIBDIR, "libtree_attn.so")
 SOURCES = ["tt_meta.hip", "tt_attn_fwd_bf16.hip", "tt_attn_bwd_bf16.hip", "tt_attn_f32.hip", "tt_gdn.hip",
            "tt_conv.hip", "tt_prologue.hip", "tt_ce.hip",
-           "tt_api.hip"]
+           "tt_api.hip", "tt_noalloc.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17",
