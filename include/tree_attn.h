@@ -216,11 +216,18 @@ int tt_qk_prologue_bwd(const tt_prologue_problem* p, tt_tensor dq_out, tt_tensor
  * Replaces torch_chunk_gated_delta_rule_tree_varlen (tree_dfs_ssm.py:38-156;
  * twin dfs_tree_forward.py:253-353) as called from the patched GDN layer
  * (tree_dfs_ssm.py:399-414): q/k/v of the packed tree, per-node parent-state
- * routing (chunk_parent_map, :131-132). Semantics: the exact gated delta rule
- * along every root-to-leaf path (the function's stated contract, :49-52),
- * evaluated in 32-token chunks; the reference's own evaluation truncates the
- * within-node correction to I + R + R^2 (:114-121) and differs for nodes of
- * more than 3 tokens.
+ * routing (chunk_parent_map, :131-132). Two semantics:
+ *  - reference_truncated = 0: the exact gated delta rule along every
+ *    root-to-leaf path (the function's stated contract, :49-52), evaluated in
+ *    32-token chunks;
+ *  - reference_truncated = 1: what the reference function itself returns. It
+ *    treats each whole node as one chunk and builds the within-node
+ *    correction from the uncorrected rows (:120-126), A = I + R + R^2 with
+ *    R = -strictly_lower(beta k k^T * exp(G_i - G_j)) over the node, G the
+ *    node's cumulative log decay: U = A (beta v), W = A (beta e^G k),
+ *    V' = U - W S_parent, O = e^G q S_parent + lower(q k^T * D) V'. It equals
+ *    the exact rule for nodes of at most 3 tokens (R^3 = 0) and differs for
+ *    longer ones.
  *
  * Nodes are in DFS pre-order (parent[i] < i, -1 for a root); node i owns
  * tokens [node_start[i], node_start[i] + node_len[i]) and is cut into
@@ -259,10 +266,12 @@ typedef struct tt_gdn_problem {
      * tt_gdn_tree_bwd only (may be NULL for the forward). */
     const int32_t* node_child_off;
     const int32_t* node_child;
+    int32_t reference_truncated;  /* 0: exact delta rule; 1: the reference's I + R + R^2 per node */
 } tt_gdn_problem;
 
 /* Workspace of tt_gdn_tree_fwd: per (chunk, v head) the state-independent
- * chunk terms (U, W, A, G) in float32. */
+ * chunk terms (U, W, A, G) in float32; with reference_truncated also the
+ * node-level decay and R (beta [v | e^G k]) rows (about 33 KiB more). */
 size_t tt_gdn_workspace_bytes(const tt_gdn_problem* p);
 /* o: [T, Hv, 128] contiguous, problem dtype. node_states: [n_nodes, Hv, 128,
  * 128] float32, the state after each node (its children's initial state;

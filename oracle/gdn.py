@@ -233,6 +233,49 @@ def gdn_tree_torch(q, k, v, g, beta, node_len, parent, l2=True, eps=1e-6):
     return torch.stack(outs, 0)
 
 
+def gdn_tree_reference_torch(q, k, v, g, beta, node_len, parent, l2=True, eps=1e-6, return_states=False):
+    """The reference's own evaluation (``gdn_tree`` mode="reference": every
+    whole node one chunk, within-node correction A = I + R + R^2 built from
+    the uncorrected rows, R/tree_dfs_ssm.py:100-150) in torch, differentiable:
+    the backward oracle of that mode (autograd on float64). Same arguments and
+    result as ``gdn_tree_torch`` (plus the node final states [n_nodes, Hv, Dk,
+    Dv] with ``return_states``); in the inputs' dtype, so float32 inputs give
+    the precision the reference's own float32 code reaches."""
+    import torch
+    T, Hk, Dk = q.shape
+    Hv, Dv = v.shape[1], v.shape[2]
+    rep = Hv // Hk
+    if l2:
+        q = q * torch.rsqrt((q * q).sum(-1, keepdim=True) + eps)
+        k = k * torch.rsqrt((k * k).sum(-1, keepdim=True) + eps)
+    q = (q * Dk ** -0.5).repeat_interleave(rep, dim=1).transpose(0, 1)    # [Hv, T, Dk]
+    k = k.repeat_interleave(rep, dim=1).transpose(0, 1)
+    v = v.transpose(0, 1)
+    g, beta = g.transpose(0, 1), beta.transpose(0, 1)                     # [Hv, T]
+    starts = node_starts(node_len)
+    finals = [None] * len(node_len)
+    outs = []
+    for i in range(len(node_len)):
+        s0, L = int(starts[i]), int(node_len[i])
+        qi, ki, vi = q[:, s0:s0 + L], k[:, s0:s0 + L], v[:, s0:s0 + L]
+        gi, bi = g[:, s0:s0 + L], beta[:, s0:s0 + L]
+        S = finals[parent[i]] if parent[i] >= 0 else torch.zeros(Hv, Dk, Dv, dtype=q.dtype)
+        G = gi.cumsum(-1)
+        lower = torch.tril(torch.ones(L, L, dtype=torch.bool))
+        D = torch.where(lower, torch.exp(torch.where(lower, G[:, :, None] - G[:, None, :], 0.0)), 0.0)
+        R = -torch.tril((bi[:, :, None] * ki) @ ki.transpose(1, 2) * D, -1)
+        A = torch.eye(L, dtype=q.dtype) + R + R @ R
+        u = A @ (bi[:, :, None] * vi)
+        w = A @ (bi[:, :, None] * ki * torch.exp(G)[:, :, None])
+        vn = u - w @ S
+        o = (qi * torch.exp(G)[:, :, None]) @ S + (qi @ ki.transpose(1, 2) * D) @ vn
+        finals[i] = S * torch.exp(G[:, -1])[:, None, None] + \
+            (ki * torch.exp(G[:, -1:] - G)[:, :, None]).transpose(1, 2) @ vn
+        outs.append(o)
+    out = torch.cat(outs, 1).transpose(0, 1)
+    return (out, torch.stack(finals)) if return_states else out
+
+
 def token_prev(node_len, parent):
     """Path predecessor of every token: t - 1 inside a node, the parent's
     last token for a node's first token, -1 before a root."""
@@ -261,14 +304,15 @@ def tree_conv_torch(x, weight, bias, node_len, parent):
     return acc * torch.sigmoid(acc)
 
 
-def gdn_layer_torch(ssm, hidden, node_len, parent):
+def gdn_layer_torch(ssm, hidden, node_len, parent, reference_truncated=False):
     """The tree-aware GatedDeltaNet layer in float64 torch, differentiable:
     projections, ``tree_conv_torch``, gates, ``gdn_tree_torch`` (exact rule,
     q/k heads shared by Hv/Hk v heads), gated RMSNorm and out_proj, with the
     parameters of ``ssm`` (a transformers Qwen3_5MoeGatedDeltaNet, whose
     attributes this reads: the layer of R/tree_dfs_ssm.py:355-423 and
     R/dfs_tree_forward.py:360-435). hidden [T, d] float64; the module's
-    parameters are used in float64. Returns [T, d]."""
+    parameters are used in float64. ``reference_truncated`` takes the
+    reference's own I + R + R^2 scan instead of the exact rule. Returns [T, d]."""
     import torch
     P = {n: p.double() for n, p in ssm.named_parameters()}
     lin = lambda x, n: x @ P[n + ".weight"].T
@@ -285,7 +329,8 @@ def gdn_layer_torch(ssm, hidden, node_len, parent):
     v = v.reshape(T, -1, ssm.head_v_dim)
     beta = torch.sigmoid(b)
     g = -torch.exp(P["A_log"]) * torch.nn.functional.softplus(a + P["dt_bias"])
-    o = gdn_tree_torch(q, k, v, g, beta, node_len, parent)
+    scan = gdn_tree_reference_torch if reference_truncated else gdn_tree_torch
+    o = scan(q, k, v, g, beta, node_len, parent)
     o = o.reshape(-1, ssm.head_v_dim)
     zz = z.reshape(-1, ssm.head_v_dim)
     o = o * torch.rsqrt(o.pow(2).mean(-1, keepdim=True) + ssm.norm.variance_epsilon)

@@ -138,12 +138,32 @@ def _gdn_problem(offsets=(0, 1, 3), **kw):
     ("g_stride_tok", 8, _lib.TT_E_ARG),           # rows of g overlap
     ("node_parent", None, _lib.TT_E_ARG),
     ("q", _lib.TTTensor(18, 16 * 128, 128), _lib.TT_E_ARG),   # misaligned
+    ("reference_truncated", 2, _lib.TT_E_ARG),   # a flag: 0 or 1
 ])
 def test_gdn_validation(field, value, code):
     lib = _lib.lib()
     p = _gdn_problem(**{field: value})
     V = ctypes.c_void_p(16)
     assert lib.tt_gdn_tree_fwd(ctypes.byref(p), V, V, V, 1 << 30, None) == code
+
+
+def test_gdn_reference_truncated_workspace():
+    """The reference's per-node correction needs the node-level terms on top of
+    the exact rule's workspaces: 32 decays and 32 x 256 R-rows per (chunk, v
+    head) in the forward and saved buffers, and two more such rows plus the
+    correction's dk and dG in the backward scratch."""
+    lib = _lib.lib()
+    ex, tr = _gdn_problem(), _gdn_problem(reference_truncated=1)
+    ch = 5 * 32
+    assert lib.tt_gdn_workspace_bytes(ctypes.byref(tr)) - lib.tt_gdn_workspace_bytes(ctypes.byref(ex)) == \
+        ch * (32 + 32 * 256) * 4
+    assert lib.tt_gdn_saved_bytes(ctypes.byref(tr)) - lib.tt_gdn_saved_bytes(ctypes.byref(ex)) == \
+        ch * (32 + 32 * 256) * 4
+    extra_scratch = ch * (2 * 32 * 256 + 32 * 128 + 32) * 4
+    assert lib.tt_gdn_bwd_saved_workspace_bytes(ctypes.byref(tr)) - \
+        lib.tt_gdn_bwd_saved_workspace_bytes(ctypes.byref(ex)) == extra_scratch
+    assert lib.tt_gdn_bwd_workspace_bytes(ctypes.byref(tr)) - lib.tt_gdn_bwd_workspace_bytes(ctypes.byref(ex)) == \
+        extra_scratch + ch * (32 + 32 * 256) * 4
 
 
 def test_gdn_level_offsets_validation():

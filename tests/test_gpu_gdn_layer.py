@@ -2,7 +2,8 @@
 kernels, torch projections and norm) against the float64 layer oracle
 (oracle/gdn.py ``gdn_layer_torch``, pinned to transformers' module per path
 in tests/test_gdn_layer.py): forward output and the gradients with respect to
-the input and every parameter.
+the input and every parameter, with the exact scan and with the reference's
+own I + R + R^2 scan (reference_truncated).
 
 Bars: float32 max_rel < 1e-5 per tensor; bf16 < 2e-2.
 """
@@ -25,8 +26,9 @@ def _rel(a, b):
     return float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
 
 
+@pytest.mark.parametrize("reference_truncated", [False, True], ids=["exact", "reference"])
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
-def test_patched_layer_matches_oracle(dtype, tol):
+def test_patched_layer_matches_oracle(dtype, tol, reference_truncated):
     lens, par = random_forest(5, node_len=(1, 45))
     T = sum(lens)
     starts = np.concatenate([[0], np.cumsum(lens)[:-1]])
@@ -41,15 +43,15 @@ def test_patched_layer_matches_oracle(dtype, tol):
                 p_ref.copy_(p.double().cpu())
         h64 = h64.bfloat16().double()
     dy64 = torch.randn(T, 256, dtype=torch.float64, generator=torch.Generator().manual_seed(5))
-    print(f"gdn layer {dtype}: T={T} nodes={len(lens)}", flush=True)
+    print(f"gdn layer {dtype} reference_truncated={reference_truncated}: T={T} nodes={len(lens)}", flush=True)
 
-    fwd = gdn_layer._make_dfs_ssm_forward(ssm, bounds, par)
+    fwd = gdn_layer._make_dfs_ssm_forward(ssm, bounds, par, reference_truncated=reference_truncated)
     h = h64.to(DEV, dtype).requires_grad_(True)
     y = fwd(h[None])[0]
     y.backward(dy64.to(DEV, dtype))
 
     hr = h64.clone().requires_grad_(True)
-    yr = ogdn.gdn_layer_torch(ref_ssm, hr, lens, par)
+    yr = ogdn.gdn_layer_torch(ref_ssm, hr, lens, par, reference_truncated)
     yr.backward(dy64)
 
     assert _rel(y.detach().double().cpu(), yr.detach()) < tol

@@ -195,3 +195,49 @@ def test_tree_conv_torch_matches_numpy_and_grads_match_finite_differences(seed):
             f = lambda arr: (gdn.tree_conv(*[arr if z is a else z for z in (x, w, b)], lens, par) * dy).sum()
             fd = (f(ap) - f(am)) / 2e-6
             assert abs(fd - float(gr[i])) < 1e-6 * max(1.0, abs(fd))
+
+
+def test_reference_torch_oracle_matches_numpy_and_grads_match_finite_differences():
+    """The differentiable restatement of the reference's node-as-chunk rule
+    (the backward oracle of reference_truncated) equals the numpy literal
+    restatement (row-by-row correction loop) and its autograd gradients equal
+    central finite differences of that numpy forward; nodes of 1 to 7 tokens,
+    so the R^2 term is exercised and the R^3 term it drops is not zero."""
+    lens, par = [7, 2, 5, 1, 6], [-1, 0, 0, 2, -1]
+    T = sum(lens)
+    q, k, v, g, beta = _inputs(T, 1, 2, 6, 5, 21, g_scale=0.5)
+    tt = [torch.from_numpy(x).requires_grad_(True) for x in (q, k, v, g, beta)]
+    o = gdn.gdn_tree_reference_torch(*tt, lens, par)
+    o_np, _ = gdn.gdn_tree(q, k, v, g, beta, lens, par, mode="reference")
+    assert _rel(o.detach().numpy(), o_np) < 1e-12
+    o_exact, _ = gdn.gdn_tree(q, k, v, g, beta, lens, par, mode="exact")
+    assert _rel(o_np, o_exact) > 1e-6              # a different function from the exact rule
+    w = torch.from_numpy(np.random.default_rng(3).standard_normal(o.shape))
+    grads = torch.autograd.grad((o * w).sum(), tt)
+    rng = np.random.default_rng(4)
+    for x, gr in zip((q, k, v, g, beta), grads):
+        for _ in range(4):
+            idx = tuple(int(rng.integers(0, s)) for s in x.shape)
+            h = 1e-6
+            xp, xm = x.copy(), x.copy()
+            xp[idx] += h
+            xm[idx] -= h
+            f = lambda arr: (gdn.gdn_tree(*[arr if a is x else a for a in (q, k, v, g, beta)], lens, par,
+                                          mode="reference")[0] * w.numpy()).sum()
+            fd = (f(xp) - f(xm)) / (2 * h)
+            assert abs(fd - float(gr[idx])) < 1e-6 * max(1.0, abs(fd))
+
+
+def test_reference_truncated_is_opt_in():
+    """Every drop-in entry point keeps the exact rule unless asked for the
+    reference's truncation."""
+    import inspect
+    from tree_training_amd import gdn as tgdn
+    from tree_training_amd import gdn_layer
+    for fn, name in [(tgdn.torch_chunk_gated_delta_rule_tree_varlen, "reference_truncated"),
+                     (tgdn.gdn_tree, "reference_truncated"), (tgdn.gdn_tree_forward, "reference_truncated"),
+                     (tgdn.gdn_tree_backward, "reference_truncated"),
+                     (gdn_layer.patch_ssm_for_dfs, "reference_truncated"),
+                     (gdn_layer._patch_ssm, "reference_truncated"),
+                     (__import__("tree_training_amd").dfs_tree_forward, "gdn_reference_truncated")]:
+        assert inspect.signature(fn).parameters[name].default is False, fn.__name__

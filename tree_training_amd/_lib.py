@@ -28,7 +28,7 @@ TT_STATUS_BAD_PARENT = 2
 TT_STATUS_BAD_TOTAL = 4
 TT_STATUS_BAD_BIAS = 8
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # Every symbol include/tree_attn.h declares, for the export check.
 EXPORTS = (
@@ -70,6 +70,7 @@ class TTGdnProblem(ctypes.Structure):
         ("n_levels", ctypes.c_int32), ("n_chunks", ctypes.c_int32),
         ("node_chunk0", ctypes.c_void_p), ("chunk_node", ctypes.c_void_p),
         ("node_child_off", ctypes.c_void_p), ("node_child", ctypes.c_void_p),
+        ("reference_truncated", ctypes.c_int32),
     ]
 
 

@@ -17,7 +17,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 LIBDIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIBDIR, "libtree_attn.so")
-SOURCES = ["tt_meta.hip", "tt_attn_fwd_bf16.hip", "tt_attn_bwd_bf16.hip", "tt_attn_f32.hip", "tt_gdn.hip",
+SOURCES = ["tt_meta.hip", "tt_attn_fwd_bf16.hip", "tt_attn_bwd_bf16.hip", "tt_attn_f32.hip", "tt_gdn.hip", "tt_gdn_trunc.hip",
            "tt_conv.hip", "tt_prologue.hip", "tt_ce.hip",
            "tt_api.hip", "tt_noalloc.hip"]
 

@@ -6,7 +6,7 @@
 
 namespace {
 
-constexpr int kAbiVersion = 1;
+constexpr int kAbiVersion = 2;
 constexpr int64_t kMaxTokStride = int64_t(1) << 23;   // elements
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
@@ -196,7 +196,7 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
 
 size_t tt_gdn_workspace_bytes(const tt_gdn_problem* p) {
     if (!p || p->n_chunks < 1 || p->n_heads_v < 1) return 0;
-    return tt_gdn_ws_bytes_impl(p->n_chunks, p->n_heads_v);
+    return tt_gdn_ws_bytes_impl(p->n_chunks, p->n_heads_v, p->reference_truncated != 0);
 }
 
 }  // extern "C"
@@ -248,6 +248,8 @@ static int gdn_problem(const tt_gdn_problem* p, GdnDev& d) {
     d.hv = p->n_heads_v;
     d.rep = p->n_heads_v / p->n_heads_k;
     d.l2 = p->l2norm ? 1 : 0;
+    if (p->reference_truncated != 0 && p->reference_truncated != 1) return TT_E_ARG;
+    d.trunc = p->reference_truncated;
     d.scale = p->scale;
     return TT_OK;
 }
@@ -260,19 +262,19 @@ int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* 
     const int rc = gdn_problem(p, d);
     if (rc != TT_OK) return rc;
     if (!o || !node_states || !ws) return TT_E_ARG;
-    if (ws_bytes < tt_gdn_ws_bytes_impl(p->n_chunks, p->n_heads_v)) return TT_E_WORKSPACE;
+    if (ws_bytes < tt_gdn_ws_bytes_impl(p->n_chunks, p->n_heads_v, p->reference_truncated != 0)) return TT_E_WORKSPACE;
     if (!aligned(o, 16) || !aligned(node_states, 16) || !aligned(ws, 16)) return TT_E_ARG;
     return tt_gdn_fwd_launch(d, p->level_offsets, p->n_levels, o, node_states, (float*)ws, (hipStream_t)stream);
 }
 
 size_t tt_gdn_bwd_workspace_bytes(const tt_gdn_problem* p) {
     if (!p || p->n_chunks < 1 || p->n_nodes < 1 || p->n_heads_v < 1) return 0;
-    return tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v, true);
+    return tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v, true, p->reference_truncated != 0);
 }
 
 size_t tt_gdn_saved_bytes(const tt_gdn_problem* p) {
     if (!p || p->n_chunks < 1 || p->n_heads_v < 1) return 0;
-    return tt_gdn_saved_bytes_impl(p->n_chunks, p->n_heads_v);
+    return tt_gdn_saved_bytes_impl(p->n_chunks, p->n_heads_v, p->reference_truncated != 0);
 }
 
 int tt_gdn_tree_fwd_save(const tt_gdn_problem* p, void* o, float* node_states, void* saved, size_t saved_bytes,
@@ -281,7 +283,7 @@ int tt_gdn_tree_fwd_save(const tt_gdn_problem* p, void* o, float* node_states, v
     const int rc = gdn_problem(p, d);
     if (rc != TT_OK) return rc;
     if (!o || !node_states || !saved) return TT_E_ARG;
-    if (saved_bytes < tt_gdn_saved_bytes_impl(p->n_chunks, p->n_heads_v)) return TT_E_WORKSPACE;
+    if (saved_bytes < tt_gdn_saved_bytes_impl(p->n_chunks, p->n_heads_v, p->reference_truncated != 0)) return TT_E_WORKSPACE;
     if (!aligned(o, 16) || !aligned(node_states, 16) || !aligned(saved, 16)) return TT_E_ARG;
     return tt_gdn_fwd_save_launch(d, p->level_offsets, p->n_levels, o, node_states, (float*)saved,
                                   (hipStream_t)stream);
@@ -289,7 +291,7 @@ int tt_gdn_tree_fwd_save(const tt_gdn_problem* p, void* o, float* node_states, v
 
 size_t tt_gdn_bwd_saved_workspace_bytes(const tt_gdn_problem* p) {
     if (!p || p->n_chunks < 1 || p->n_nodes < 1 || p->n_heads_v < 1) return 0;
-    return tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v, false);
+    return tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v, false, p->reference_truncated != 0);
 }
 
 // Shared argument checks of the two backward entry points.
@@ -313,7 +315,7 @@ int tt_gdn_tree_bwd(const tt_gdn_problem* p, tt_tensor d_o, void* dq, void* dk, 
     int rc = gdn_problem(p, d);
     if (rc != TT_OK) return rc;
     if ((rc = gdn_bwd_args(p, d_o, dq, dk, dv, dg, dbeta, ws)) != TT_OK) return rc;
-    if (ws_bytes < tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v, true)) return TT_E_WORKSPACE;
+    if (ws_bytes < tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v, true, p->reference_truncated != 0)) return TT_E_WORKSPACE;
     return tt_gdn_bwd_launch(d, p->level_offsets, p->n_levels, d_o.ptr, d_o.stride_tok, d_o.stride_head, dq, dk,
                              dv, dg, dbeta, nullptr, (float*)ws, (hipStream_t)stream);
 }
@@ -326,8 +328,8 @@ int tt_gdn_tree_bwd_saved(const tt_gdn_problem* p, tt_tensor d_o, void* dq, void
     if (rc != TT_OK) return rc;
     if ((rc = gdn_bwd_args(p, d_o, dq, dk, dv, dg, dbeta, ws)) != TT_OK) return rc;
     if (!saved || !aligned(saved, 16)) return TT_E_ARG;
-    if (saved_bytes < tt_gdn_saved_bytes_impl(p->n_chunks, p->n_heads_v)) return TT_E_WORKSPACE;
-    if (ws_bytes < tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v, false)) return TT_E_WORKSPACE;
+    if (saved_bytes < tt_gdn_saved_bytes_impl(p->n_chunks, p->n_heads_v, p->reference_truncated != 0)) return TT_E_WORKSPACE;
+    if (ws_bytes < tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v, false, p->reference_truncated != 0)) return TT_E_WORKSPACE;
     return tt_gdn_bwd_launch(d, p->level_offsets, p->n_levels, d_o.ptr, d_o.stride_tok, d_o.stride_head, dq, dk,
                              dv, dg, dbeta, (const float*)saved, (float*)ws, (hipStream_t)stream);
 }

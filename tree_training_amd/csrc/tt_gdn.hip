@@ -23,111 +23,10 @@
 //    per value column) and walks the node's chunks.
 // fp32 end to end: the prep on the vector ALUs, the scans on fp32 MFMA
 // (v_mfma_f32_32x32x2_f32).
-#include "tt_common.h"
-#include "tt_internal.h"
+#include "tt_gdn_common.h"
 
 namespace {
 
-constexpr int GD = 128;           // head dim (Dk = Dv)
-constexpr int GC = TT_GDN_CHUNK;  // chunk length (32)
-constexpr int GT = 256;           // threads per workgroup
-constexpr int RS = GD + 4;        // row stride of [GC x GD] tiles (floats): rows 4 banks apart
-constexpr int MS = GC + 4;        // row stride of [GC x GC] matrices
-
-// Workspace per (chunk, v head), floats: W [GC][GD], U [GC][GD], A [GC][GC],
-// T [GC][GC] (the inverse, for the backward), G [GC].
-constexpr size_t kWsW = 0, kWsU = GC * GD, kWsA = 2 * GC * GD, kWsT = kWsA + GC * GC, kWsG = kWsT + GC * GC;
-constexpr size_t kWsChunk = kWsG + GC;
-
-template <int I>
-struct IntC4 {
-    static constexpr int value = I;
-};
-
-template <typename T>
-__device__ __forceinline__ void load16(const T* p, float (&x)[16]) {
-    if constexpr (sizeof(T) == 2) {
-        const bf16x8 a = *(const bf16x8*)p, b = *(const bf16x8*)(p + 8);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            x[e] = (float)a[e];
-            x[8 + e] = (float)b[e];
-        }
-    } else {
-#pragma unroll
-        for (int e = 0; e < 16; e += 4) {
-            const f32x4 a = *(const f32x4*)(p + e);
-            x[e] = a[0]; x[e + 1] = a[1]; x[e + 2] = a[2]; x[e + 3] = a[3];
-        }
-    }
-}
-
-template <typename T>
-__device__ __forceinline__ void store4(T* p, const f32x4& x) {
-    if constexpr (sizeof(T) == 2) {
-        bf16x4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = (__bf16)x[e];
-        *(bf16x4*)p = w;
-    } else {
-        *(f32x4*)p = x;
-    }
-}
-
-// Sum over the 8 consecutive lanes that hold one row.
-__device__ __forceinline__ float row8_sum(float x) {
-    x += __shfl_xor(x, 1);
-    x += __shfl_xor(x, 2);
-    x += __shfl_xor(x, 4);
-    return x;
-}
-
-// Chunk `c` -> (first token, length); false for a malformed chunk list.
-__device__ __forceinline__ bool chunk_span(const GdnDev& p, int c, int& start, int& len) {
-    const int node = p.chunk_node[c];
-    if (node < 0 || node >= p.n_nodes) return false;
-    const int ci = c - p.node_chunk0[node];
-    const int ns = p.node_start[node], nl = p.node_len[node];
-    if (ns < 0 || nl < 0 || ns > p.n_tokens - nl || ci < 0 || GC * ci >= nl) return false;
-    start = ns + GC * ci;
-    len = min(GC, nl - GC * ci);
-    return true;
-}
-
-// Rows of one chunk (zeros past its length): l2-normalised q (times scale),
-// k, and, when V is given, v; thread t handles row t/8, 16 dims.
-template <typename TIn>
-__device__ __forceinline__ void load_chunk_rows(const GdnDev& p, int start, int len, int h, float* Q, float* K,
-                                                float* V) {
-    const int t = threadIdx.x, i = t >> 3, d0 = 16 * (t & 7), hk = h / p.rep;
-    const bool valid = i < len;
-    const int64_t tok = start + i;
-    float qv[16], kv[16], vv[16];
-    if (valid) {
-        load16((const TIn*)p.q + tok * p.q_st + hk * p.q_sh + d0, qv);
-        load16((const TIn*)p.k + tok * p.k_st + hk * p.k_sh + d0, kv);
-        if (V) load16((const TIn*)p.v + tok * p.v_st + h * p.v_sh + d0, vv);
-    } else {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) qv[e] = kv[e] = vv[e] = 0.0f;
-    }
-    float sq = 0.0f, sk = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        sq = fmaf(qv[e], qv[e], sq);
-        sk = fmaf(kv[e], kv[e], sk);
-    }
-    sq = row8_sum(sq);
-    sk = row8_sum(sk);
-    const float fq = (p.l2 ? 1.0f / sqrtf(sq + 1e-6f) : 1.0f) * p.scale;
-    const float fk = p.l2 ? 1.0f / sqrtf(sk + 1e-6f) : 1.0f;
-#pragma unroll
-    for (int e = 0; e < 16; e += 4) {
-        *(f32x4*)&Q[i * RS + d0 + e] = (f32x4){qv[e] * fq, qv[e + 1] * fq, qv[e + 2] * fq, qv[e + 3] * fq};
-        *(f32x4*)&K[i * RS + d0 + e] = (f32x4){kv[e] * fk, kv[e + 1] * fk, kv[e + 2] * fk, kv[e + 3] * fk};
-        if (V) *(f32x4*)&V[i * RS + d0 + e] = (f32x4){vv[e], vv[e + 1], vv[e + 2], vv[e + 3]};
-    }
-}
 
 // ----------------------------------------------------------------------------
 // prep: per (chunk, v head) A, T, U, W, G
@@ -143,7 +42,9 @@ struct PrepLds {
     float beta[GC];
 };
 
-template <typename TIn>
+// TRUNC (the reference's per-node correction): only A and G here; U and W
+// come from the node-level kernels of tt_gdn_trunc.hip.
+template <typename TIn, bool TRUNC>
 __global__ __launch_bounds__(GT) void gdn_prep_kernel(GdnDev p, float* __restrict__ ws) {
     __shared__ __attribute__((aligned(16))) PrepLds L;
     const int c = blockIdx.x, h = blockIdx.y;
@@ -195,6 +96,7 @@ __global__ __launch_bounds__(GT) void gdn_prep_kernel(GdnDev p, float* __restric
         L.N[i * MS + j] = nij;
         L.Tm[i * MS + j] = nij + (i == j ? 1.0f : 0.0f);
     }
+    if constexpr (TRUNC) return;
     __syncthreads();
 
     // T = (I - N)^-1. N is strictly lower triangular (N^32 = 0), so
@@ -267,52 +169,6 @@ __global__ __launch_bounds__(GT) void gdn_prep_kernel(GdnDev p, float* __restric
 // ----------------------------------------------------------------------------
 // scan: per (node, v head), the node's chunks in order, on fp32 MFMA
 // ----------------------------------------------------------------------------
-// v_mfma_f32_32x32x2_f32: D[32x32] += A[32x2] B[2x32]; lane l supplies
-// A[l & 31][l >> 5] and B[l >> 5][l & 31], and accumulator element r of lane l
-// is D[acc_row(r, l >> 5)][l & 31]. The contraction order is free, so step r
-// of a 32-deep contraction pairs k = acc_row(r, 0) (lanes 0-31) with
-// k = acc_row(r, 1) (lanes 32-63): a matrix held as accumulators (rows k,
-// columns j) is then directly the B operand, element r of each lane.
-__device__ __forceinline__ f32x16 mfma_f32(float a, float b, const f32x16& c) {
-    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
-}
-
-// Accumulator-layout access to a row-major fp32 matrix of GD-float rows:
-// element r of lane l is row ROW0 + acc_row(r, l >> 5), column `col`. One
-// buffer resource (scalar registers), four lane offsets (rows r % 4); the
-// uniform part of the row, ROW0 + 8 (r / 4), goes in the scalar offset.
-struct AccMat {
-    __amdgpu_buffer_rsrc_t rs;
-    int vo[4];
-};
-__device__ __forceinline__ AccMat acc_mat(const float* base, int rows, int half, int col) {
-    AccMat m;
-    m.rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, rows * GD * 4, 0x00020000);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) m.vo[k] = ((4 * half + k) * GD + col) * 4;
-    return m;
-}
-template <int ROW0>
-__device__ __forceinline__ f32x16 load_acc(const AccMat& m) {
-    f32x16 v;
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-        v[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(m.rs, m.vo[r & 3], (ROW0 + 8 * (r >> 2)) * GD * 4, 0));
-    return v;
-}
-template <int ROW0>
-__device__ __forceinline__ void store_acc(const AccMat& m, const f32x16& v) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[r]), m.rs, m.vo[r & 3], (ROW0 + 8 * (r >> 2)) * GD * 4, 0);
-}
-template <typename F>
-__device__ __forceinline__ void for_tiles(F&& f) {
-    f(IntC4<0>{});
-    f(IntC4<1>{});
-    f(IntC4<2>{});
-    f(IntC4<3>{});
-}
 
 struct ScanLds {
     float W[GC * RS];     // W [token][state row]
@@ -331,8 +187,12 @@ struct ScanLds {
 // out may be null (the backward's recompute); chunk_sin / chunk_vp, when
 // given, receive each chunk's initial state and V' ([n_chunks, Hv, 128, 128]
 // and [n_chunks, Hv, 32, 128] floats).
-template <typename TIn>
-__global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_scan_kernel(GdnDev p, int lvl_begin, const float* __restrict__ ws,
+// TRUNC (the reference's per-node correction): V' = U - W S0 with S0 the
+// node's initial state for every chunk of the node. A first pass over the
+// node's chunks, while the state registers still hold S0, replaces each
+// chunk's U by its V' in the workspace; the scan proper then reads V' there.
+template <typename TIn, bool TRUNC>
+__global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_scan_kernel(GdnDev p, int lvl_begin, float* __restrict__ ws,
                                                       TIn* __restrict__ out, float* __restrict__ states,
                                                       float* __restrict__ chunk_sin, float* __restrict__ chunk_vp) {
     __shared__ __attribute__((aligned(16))) ScanLds L;
@@ -356,6 +216,33 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         for (int rb = 0; rb < 4; ++rb) S[rb] = (f32x16){};
     }
 
+    if constexpr (TRUNC) {
+        // V' = U - W S0 for every chunk (a root's S0 is zero: V' = U as it is).
+        for (int c0 = 0; par >= 0 && c0 < len; c0 += GC) {
+            float* cw = ws + ((size_t)(chunk0 + c0 / GC) * p.hv + h) * kWsChunk;
+            __syncthreads();   // readers of the previous chunk's W are done
+            {
+                const int i = t >> 3, d0 = 16 * (t & 7);
+#pragma unroll
+                for (int e = 0; e < 16; e += 4)
+                    *(f32x4*)&L.W[i * RS + d0 + e] = *(const f32x4*)(cw + kWsW + i * GD + d0 + e);
+            }
+            const AccMat um = acc_mat(cw + kWsU, GC, half, j);
+            f32x16 vp = load_acc<0>(um);
+            __syncthreads();
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+                for (int r4 = 0; r4 < 16; r4 += 4) {
+                    const f32x4 wv = *(const f32x4*)&L.W[col * RS + 32 * rb + 8 * (r4 >> 2) + 4 * half];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) vp = mfma_f32(-wv[e], S[rb][r4 + e], vp);
+                }
+            }
+            store_acc<0>(um, vp);   // read back by this same lane below
+        }
+    }
+
     for (int c0 = 0; c0 < len; c0 += GC) {
         const int Lc = min(GC, len - c0);
         const size_t ch = (size_t)(chunk0 + c0 / GC) * p.hv + h;
@@ -372,7 +259,8 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma unroll
             for (int e = 0; e < 16; e += 4) {   // rows written by this thread just above
                 *(f32x4*)&L.K[i * RS + d0 + e] *= ek;
-                *(f32x4*)&L.W[i * RS + d0 + e] = *(const f32x4*)(cw + kWsW + i * GD + d0 + e);
+                if constexpr (!TRUNC)
+                    *(f32x4*)&L.W[i * RS + d0 + e] = *(const f32x4*)(cw + kWsW + i * GD + d0 + e);
             }
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -381,6 +269,7 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             }
             if (t < GC) L.G[t] = cw[kWsG + t];
         }
+        // U (TRUNC: V', written by the first pass)
         f32x16 vp = load_acc<0>(acc_mat(cw + kWsU, GC, half, j)), qs = {};
         __syncthreads();
 
@@ -390,13 +279,14 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma unroll
             for (int r4 = 0; r4 < 16; r4 += 4) {
                 const int k0 = 32 * rb + 8 * (r4 >> 2) + 4 * half;          // acc_row(r4 .. r4+3, half)
-                const f32x4 wv = *(const f32x4*)&L.W[col * RS + k0];
                 const f32x4 qv = *(const f32x4*)&L.Q[col * RS + k0];
+                if constexpr (!TRUNC) {
+                    const f32x4 wv = *(const f32x4*)&L.W[col * RS + k0];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    vp = mfma_f32(-wv[e], S[rb][r4 + e], vp);
-                    qs = mfma_f32(qv[e], S[rb][r4 + e], qs);
+                    for (int e = 0; e < 4; ++e) vp = mfma_f32(-wv[e], S[rb][r4 + e], vp);
                 }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) qs = mfma_f32(qv[e], S[rb][r4 + e], qs);
             }
             __builtin_amdgcn_sched_barrier(0);   // keep operand prefetch within one row tile (registers)
         }
@@ -468,35 +358,6 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 //    dv, dbeta, dg (reverse cumulative sum of dG within the chunk), and
 //    dq, dk summed over the v heads of the group, then through the l2 norm.
 
-template <typename T>
-__device__ __forceinline__ f32x4 load4(const T* p) {
-    if constexpr (sizeof(T) == 2) {
-        const bf16x4 a = *(const bf16x4*)p;
-        return (f32x4){(float)a[0], (float)a[1], (float)a[2], (float)a[3]};
-    } else {
-        return *(const f32x4*)p;
-    }
-}
-
-__device__ __forceinline__ float dot4(const f32x4& a, const f32x4& b) {
-    return fmaf(a[0], b[0], fmaf(a[1], b[1], fmaf(a[2], b[2], a[3] * b[3])));
-}
-
-// Rows of a [GC x GD] tile into LDS (stride RS): thread t copies row t/8,
-// dims 16*(t%8)..+15; rows at or past `len` are zero.
-template <typename T>
-__device__ __forceinline__ void tile_in(const T* base, int64_t row_stride, int len, float* dst) {
-    const int i = threadIdx.x >> 3, d0 = 16 * (threadIdx.x & 7);
-    float x[16];
-    if (i < len) {
-        load16(base + i * row_stride + d0, x);
-    } else {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) x[e] = 0.0f;
-    }
-#pragma unroll
-    for (int e = 0; e < 16; e += 4) *(f32x4*)&dst[i * RS + d0 + e] = (f32x4){x[e], x[e + 1], x[e + 2], x[e + 3]};
-}
 
 struct RscanLds {
     float Q[GC * RS];     // e^G q^ * scale
@@ -510,7 +371,10 @@ struct RscanLds {
 // four accumulator tiles (as the forward's state), dO of the chunk is loaded
 // in accumulator layout (rows = tokens), and dV' is produced in it, so all
 // three are used straight from registers as MFMA B operands.
-template <typename TIn>
+// TRUNC (V' = U - W S0 with the node's initial state S0): the walk leaves out
+// the W term, and a second pass over the node's chunks subtracts
+// sum_c W_c^T dV'_c from the state gradient at the node's entry.
+template <typename TIn, bool TRUNC>
 __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_rscan_kernel(
         GdnDev p, int lvl_begin, const float* __restrict__ ws, const TIn* __restrict__ d_o, int64_t do_st,
         int64_t do_sh, float* __restrict__ chunk_dso, float* __restrict__ chunk_dvp, float* __restrict__ node_dsin) {
@@ -556,7 +420,8 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             for (int e = 0; e < 16; e += 4) {   // rows written by this thread just above
                 *(f32x4*)&L.Q[i * RS + d0 + e] *= eq;
                 *(f32x4*)&L.K[i * RS + d0 + e] *= ek;
-                *(f32x4*)&L.W[i * RS + d0 + e] = *(const f32x4*)(cw + kWsW + i * GD + d0 + e);
+                if constexpr (!TRUNC)
+                    *(f32x4*)&L.W[i * RS + d0 + e] = *(const f32x4*)(cw + kWsW + i * GD + d0 + e);
             }
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -601,9 +466,30 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             for (int r = 0; r < 16; ++r) {
                 const int i = acc_row(r, half);
                 dS[rb] = mfma_f32(L.Q[i * RS + 32 * rb + col], dov[r], dS[rb]);
-                dS[rb] = mfma_f32(-L.W[i * RS + 32 * rb + col], dv[r], dS[rb]);
+                if constexpr (!TRUNC) dS[rb] = mfma_f32(-L.W[i * RS + 32 * rb + col], dv[r], dS[rb]);
             }
             __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    if constexpr (TRUNC) {
+        for (int ci = 0; ci < tt_cdiv(len, GC); ++ci) {
+            const size_t chn = (size_t)(chunk0 + ci) * p.hv + h;
+            const float* cw = ws + chn * kWsChunk;
+            __syncthreads();   // readers of the previous chunk's W are done
+            {
+                const int i = t >> 3, d0 = 16 * (t & 7);
+#pragma unroll
+                for (int e = 0; e < 16; e += 4)
+                    *(f32x4*)&L.W[i * RS + d0 + e] = *(const f32x4*)(cw + kWsW + i * GD + d0 + e);
+            }
+            const f32x16 dv = load_acc<0>(acc_mat(chunk_dvp + chn * GC * GD, GC, half, j));   // this lane's own writes
+            __syncthreads();
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    dS[rb] = mfma_f32(-L.W[acc_row(r, half) * RS + 32 * rb + col], dv[r], dS[rb]);
+            }
         }
     }
     // dS at the node's entry, summed into its parent by the next (shallower) level.
@@ -769,6 +655,47 @@ __global__ __launch_bounds__(GT) void gdn_bwd_state_kernel(GdnDev p, const TIn* 
     }
 }
 
+// The reference's per-node correction (V' = U - W S0 for every chunk of a
+// node): dW = -dV' S0^T with S0 the node's initial state (its first chunk's
+// S), per (chunk, v head); it replaces the dW of gdn_bwd_state_kernel, whose
+// S is the chunk's own. Same staging as there: per 32-column chunk of the
+// value dimension, all 128 rows of S0 and the 32 rows of dV' in LDS rows of
+// SCS floats; wave w produces columns 32w .. 32w+31.
+__global__ __launch_bounds__(GT) void gdn_dw_s0_kernel(GdnDev p, const float* __restrict__ chunk_sin,
+                                                       const float* __restrict__ chunk_dvp,
+                                                       float* __restrict__ dwo) {
+    __shared__ __attribute__((aligned(16))) StateGradLds L;
+    const int c = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
+    int start, len;
+    if (!chunk_span(p, c, start, len)) return;
+    const size_t chn = (size_t)c * p.hv + h;
+    const int wave = t >> 6, lane = t & 63, col = lane & 31, half = lane >> 5;
+    const float* S0 = chunk_sin + ((size_t)p.node_chunk0[p.chunk_node[c]] * p.hv + h) * GD * GD;
+    const float* dVp = chunk_dvp + chn * GC * GD;
+    const int sr = t >> 1, sc = 16 * (t & 1);      // S0 staging: row, first column
+    const int ar = t >> 3, ac = 4 * (t & 7);       // dV' staging: row, first column
+    f32x16 w = {};
+#pragma unroll 1
+    for (int k = 0; k < 4; ++k) {
+        const int v0 = GC * k;
+        __syncthreads();   // the previous chunk's readers are done
+#pragma unroll
+        for (int e = 0; e < 16; e += 4) {   // rows of SCS floats: 8-byte aligned stores
+            const f32x4 x4 = *(const f32x4*)(S0 + sr * GD + v0 + sc + e);
+            *(float2*)&L.S[sr * SCS + sc + e] = (float2){x4[0], x4[1]};
+            *(float2*)&L.S[sr * SCS + sc + e + 2] = (float2){x4[2], x4[3]};
+        }
+        const f32x4 a2 = *(const f32x4*)(dVp + ar * GD + v0 + ac);
+        *(float2*)&L.A2[ar * SCS + ac] = (float2){a2[0], a2[1]};
+        *(float2*)&L.A2[ar * SCS + ac + 2] = (float2){a2[2], a2[3]};
+        __syncthreads();
+#pragma unroll
+        for (int st = 0; st < GC / 2; ++st)
+            w = mfma_f32(L.A2[col * SCS + half + 2 * st], L.S[(32 * wave + col) * SCS + half + 2 * st], w);
+    }
+    store_acc<0>(acc_mat(dwo + chn * GC * GD, GC, half, 32 * wave + col), -w);
+}
+
 struct ChunkGradLds {
     float Qs[GC * RS];    // q^ * scale
     float Ks[GC * RS];    // k^
@@ -787,7 +714,11 @@ struct ChunkGradLds {
 
 // Thread t owns row i = t/8 of every [GC x *] result; in [GC x GD] results the
 // columns 32m + 4s + e (s = t%8, m, e < 4), in [GC x GC] results s + 8e.
-template <typename TIn>
+// TRUNC (the reference's per-node correction): U and W do not come from the
+// chunk's T, so the T part is left out; dv and dbeta are complete already
+// (tt_gdn_trunc.hip), and trk (dk^ of the correction, [chunk, Hv, 32, 128])
+// and trg (the node-level suffix sums of its dG, [chunk, Hv, 32]) are added.
+template <typename TIn, bool TRUNC>
 __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* __restrict__ d_o, int64_t do_st,
                                                            int64_t do_sh, const float* __restrict__ ws,
                                                            const float* __restrict__ chunk_vp,
@@ -796,7 +727,8 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
                                                            const float* __restrict__ dkto,
                                                            const float* __restrict__ sdot, TIn* __restrict__ dq,
                                                            TIn* __restrict__ dk, TIn* __restrict__ dv,
-                                                           float* __restrict__ dg, float* __restrict__ dbeta) {
+                                                           float* __restrict__ dg, float* __restrict__ dbeta,
+                                                           const float* __restrict__ trk, const float* __restrict__ trg) {
     __shared__ __attribute__((aligned(16))) ChunkGradLds L;
     const int c = blockIdx.x, hk = blockIdx.y, t = threadIdx.x;
     int start, len;
@@ -838,7 +770,7 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
         for (int e = 0; e < 4; ++e) {
             const int j = s + 8 * e;
             L.M1[i * MS + j] = cw[kWsA + i * GC + j];
-            L.M2[i * MS + j] = cw[kWsT + i * GC + j];
+            if constexpr (!TRUNC) L.M2[i * MS + j] = cw[kWsT + i * GC + j];
         }
         __syncthreads();
         const float gi = L.G[i], gl = L.G[GC - 1], egi = expf(gi), bi = L.B[i];
@@ -893,118 +825,128 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
                 }
             }
         }
-        __syncthreads();   // P1, P2, M1 free
-        tile_in(chunk_dvp + chn * GC * GD, GD, GC, L.P1);
-        tile_in(dwo + chn * GC * GD, GD, GC, L.P2);
-        tile_in((const TIn*)p.v + (int64_t)start * p.v_st + (int64_t)h * p.v_sh, p.v_st, len, L.P3);
-        __syncthreads();
+        if constexpr (!TRUNC) {
+            __syncthreads();   // P1, P2, M1 free
+            tile_in(chunk_dvp + chn * GC * GD, GD, GC, L.P1);
+            tile_in(dwo + chn * GC * GD, GD, GC, L.P2);
+            tile_in((const TIn*)p.v + (int64_t)start * p.v_st + (int64_t)h * p.v_sh, p.v_st, len, L.P3);
+            __syncthreads();
 
-        // dBv = T^T dV', dBk = T^T dW; dv = beta dBv; dbeta, dk^, dG from
-        // U = T (beta v) and W = T (beta e^G k^).
-        {
-            float dbv[16], dbk[16];
-#pragma unroll
-            for (int e = 0; e < 16; ++e) dbv[e] = dbk[e] = 0.0f;
-#pragma unroll 2
-            for (int j = 0; j < GC; ++j) {
-                const float tji = L.M2[j * MS + i];
-#pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    const f32x4 a = *(const f32x4*)&L.P1[j * RS + 32 * m + 4 * s];
-                    const f32x4 b = *(const f32x4*)&L.P2[j * RS + 32 * m + 4 * s];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        dbv[4 * m + e] = fmaf(tji, a[e], dbv[4 * m + e]);
-                        dbk[4 * m + e] = fmaf(tji, b[e], dbk[4 * m + e]);
+            // dBv = T^T dV', dBk = T^T dW; dv = beta dBv; dbeta, dk^, dG from
+            // U = T (beta v) and W = T (beta e^G k^).
+            {
+                float dbv[16], dbk[16];
+    #pragma unroll
+                for (int e = 0; e < 16; ++e) dbv[e] = dbk[e] = 0.0f;
+    #pragma unroll 2
+                for (int j = 0; j < GC; ++j) {
+                    const float tji = L.M2[j * MS + i];
+    #pragma unroll
+                    for (int m = 0; m < 4; ++m) {
+                        const f32x4 a = *(const f32x4*)&L.P1[j * RS + 32 * m + 4 * s];
+                        const f32x4 b = *(const f32x4*)&L.P2[j * RS + 32 * m + 4 * s];
+    #pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            dbv[4 * m + e] = fmaf(tji, a[e], dbv[4 * m + e]);
+                            dbk[4 * m + e] = fmaf(tji, b[e], dbk[4 * m + e]);
+                        }
                     }
                 }
+                float vb = 0.0f, kb = 0.0f;
+                const float bge = bi * egi;
+    #pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const f32x4 vv = *(const f32x4*)&L.P3[i * RS + 32 * m + 4 * s];
+                    const f32x4 kv = *(const f32x4*)&L.Ks[i * RS + 32 * m + 4 * s];
+                    f32x4 o;
+    #pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        vb = fmaf(vv[e], dbv[4 * m + e], vb);
+                        kb = fmaf(kv[e], dbk[4 * m + e], kb);
+                        dka[4 * m + e] = fmaf(bge, dbk[4 * m + e], dka[4 * m + e]);
+                        o[e] = bi * dbv[4 * m + e];
+                    }
+                    if (valid) store4(dv + (tok * p.hv + h) * GD + 32 * m + 4 * s, o);
+                }
+                dbp += vb + egi * kb;
+                dgp = fmaf(bge, kb, dgp);
             }
-            float vb = 0.0f, kb = 0.0f;
-            const float bge = bi * egi;
+            // dT = dV' (beta v)^T + dW (beta e^G k^)^T
+            {
+                float t1[4] = {}, t2[4] = {};
+    #pragma unroll 4
+                for (int d = 0; d < GD; d += 4) {
+                    const f32x4 a = *(const f32x4*)&L.P1[i * RS + d];
+                    const f32x4 b = *(const f32x4*)&L.P2[i * RS + d];
+    #pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        t1[e] += dot4(a, *(const f32x4*)&L.P3[(s + 8 * e) * RS + d]);
+                        t2[e] += dot4(b, *(const f32x4*)&L.Ks[(s + 8 * e) * RS + d]);
+                    }
+                }
+    #pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int j = s + 8 * e;
+                    const float bj = L.B[j];
+                    L.M1[i * MS + j] = bj * t1[e] + bj * expf(L.G[j]) * t2[e];
+                }
+            }
+            __syncthreads();   // dT complete; P1..P3 free
+            // Y = T^T dT into P3 (stride MS)
+            {
+                float y[4] = {};
+    #pragma unroll 4
+                for (int m = 0; m < GC; ++m) {
+                    const float tmi = L.M2[m * MS + i];
+    #pragma unroll
+                    for (int e = 0; e < 4; ++e) y[e] = fmaf(tmi, L.M1[m * MS + s + 8 * e], y[e]);
+                }
+    #pragma unroll
+                for (int e = 0; e < 4; ++e) L.P3[i * MS + s + 8 * e] = y[e];
+            }
+            __syncthreads();
+            // dN = Y T^T (strictly lower): dbeta, dG and E = dL/d(k^ k^T) from
+            // N = -beta (k^ k^T) * D.
+            {
+                float ev[4];
+    #pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int j = s + 8 * e;
+                    float dn = 0.0f;
+    #pragma unroll 4
+                    for (int m = 0; m < GC; ++m) dn = fmaf(L.P3[i * MS + m], L.M2[j * MS + m], dn);
+                    ev[e] = 0.0f;
+                    if (j < i) {
+                        const float dd = expf(gi - L.G[j]), kk = L.KK[i * MS + j];
+                        const float pa = dn * (-bi * kk * dd);
+                        dbp = fmaf(dn, -kk * dd, dbp);
+                        ev[e] = -dn * bi * dd;
+                        dgp += pa;
+                        L.M3[i * MS + j] += pa;
+                    }
+                }
+    #pragma unroll
+                for (int e = 0; e < 4; ++e) L.M1[i * MS + s + 8 * e] = ev[e];   // dT's readers passed the last barrier
+            }
+            __syncthreads();
+            // dk^ += (E + E^T) k^
+    #pragma unroll 2
+            for (int j = 0; j < GC; ++j) {
+                const float ej = L.M1[i * MS + j] + L.M1[j * MS + i];
+    #pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const f32x4 kj = *(const f32x4*)&L.Ks[j * RS + 32 * m + 4 * s];
+    #pragma unroll
+                    for (int e = 0; e < 4; ++e) dka[4 * m + e] = fmaf(ej, kj[e], dka[4 * m + e]);
+                }
+            }
+        } else {   // the correction's dk^ (its dv, dbeta are complete)
+            const float* kr = trk + (chn * GC + i) * GD;
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-                const f32x4 vv = *(const f32x4*)&L.P3[i * RS + 32 * m + 4 * s];
-                const f32x4 kv = *(const f32x4*)&L.Ks[i * RS + 32 * m + 4 * s];
-                f32x4 o;
+                const f32x4 x = *(const f32x4*)(kr + 32 * m + 4 * s);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    vb = fmaf(vv[e], dbv[4 * m + e], vb);
-                    kb = fmaf(kv[e], dbk[4 * m + e], kb);
-                    dka[4 * m + e] = fmaf(bge, dbk[4 * m + e], dka[4 * m + e]);
-                    o[e] = bi * dbv[4 * m + e];
-                }
-                if (valid) store4(dv + (tok * p.hv + h) * GD + 32 * m + 4 * s, o);
-            }
-            dbp += vb + egi * kb;
-            dgp = fmaf(bge, kb, dgp);
-        }
-        // dT = dV' (beta v)^T + dW (beta e^G k^)^T
-        {
-            float t1[4] = {}, t2[4] = {};
-#pragma unroll 4
-            for (int d = 0; d < GD; d += 4) {
-                const f32x4 a = *(const f32x4*)&L.P1[i * RS + d];
-                const f32x4 b = *(const f32x4*)&L.P2[i * RS + d];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    t1[e] += dot4(a, *(const f32x4*)&L.P3[(s + 8 * e) * RS + d]);
-                    t2[e] += dot4(b, *(const f32x4*)&L.Ks[(s + 8 * e) * RS + d]);
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int j = s + 8 * e;
-                const float bj = L.B[j];
-                L.M1[i * MS + j] = bj * t1[e] + bj * expf(L.G[j]) * t2[e];
-            }
-        }
-        __syncthreads();   // dT complete; P1..P3 free
-        // Y = T^T dT into P3 (stride MS)
-        {
-            float y[4] = {};
-#pragma unroll 4
-            for (int m = 0; m < GC; ++m) {
-                const float tmi = L.M2[m * MS + i];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) y[e] = fmaf(tmi, L.M1[m * MS + s + 8 * e], y[e]);
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) L.P3[i * MS + s + 8 * e] = y[e];
-        }
-        __syncthreads();
-        // dN = Y T^T (strictly lower): dbeta, dG and E = dL/d(k^ k^T) from
-        // N = -beta (k^ k^T) * D.
-        {
-            float ev[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int j = s + 8 * e;
-                float dn = 0.0f;
-#pragma unroll 4
-                for (int m = 0; m < GC; ++m) dn = fmaf(L.P3[i * MS + m], L.M2[j * MS + m], dn);
-                ev[e] = 0.0f;
-                if (j < i) {
-                    const float dd = expf(gi - L.G[j]), kk = L.KK[i * MS + j];
-                    const float pa = dn * (-bi * kk * dd);
-                    dbp = fmaf(dn, -kk * dd, dbp);
-                    ev[e] = -dn * bi * dd;
-                    dgp += pa;
-                    L.M3[i * MS + j] += pa;
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) L.M1[i * MS + s + 8 * e] = ev[e];   // dT's readers passed the last barrier
-        }
-        __syncthreads();
-        // dk^ += (E + E^T) k^
-#pragma unroll 2
-        for (int j = 0; j < GC; ++j) {
-            const float ej = L.M1[i * MS + j] + L.M1[j * MS + i];
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                const f32x4 kj = *(const f32x4*)&L.Ks[j * RS + 32 * m + 4 * s];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) dka[4 * m + e] = fmaf(ej, kj[e], dka[4 * m + e]);
+                for (int e = 0; e < 4; ++e) dka[4 * m + e] += x[e];
             }
         }
         // The output state S_out = e^{G_L} S + (e^{G_L - G} k^)^T V': dk^ and dG.
@@ -1029,7 +971,7 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
         if (s == 0) {
             L.Grow[i] = dgp;
             L.Crow[i] = cp;
-            if (valid) dbeta[tok * p.hv + h] = dbp;
+            if (!TRUNC && valid) dbeta[tok * p.hv + h] = dbp;
         }
         __syncthreads();
         if (t < GC) {
@@ -1047,6 +989,7 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
                 const float up = __shfl_down(dG, o, GC);
                 if (t + o < GC) dG += up;
             }
+            if constexpr (TRUNC) dG += trg[chn * GC + t];
             if (t < len) dg[(int64_t)(start + t) * p.hv + h] = dG;
         }
     }
@@ -1097,58 +1040,109 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
 
 }  // namespace
 
-size_t tt_gdn_ws_bytes_impl(int n_chunks, int n_heads_v) {
-    return (size_t)n_chunks * (size_t)n_heads_v * kWsChunk * sizeof(float);
+// Float counts per (chunk, v head) of the truncated mode's node-level terms:
+// the node-level decay [32] and R (beta [v | e^G k]) rows [32 x 256].
+constexpr size_t kTrGn = GC, kTrY1 = (size_t)GC * 2 * GD;
+
+size_t tt_gdn_ws_bytes_impl(int n_chunks, int n_heads_v, bool trunc) {
+    return (size_t)n_chunks * (size_t)n_heads_v * (kWsChunk + (trunc ? kTrGn + kTrY1 : 0)) * sizeof(float);
 }
 
-int tt_gdn_fwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, void* out, float* states,
-                      float* ws, hipStream_t s) {
-    if (d.dtype == TT_DTYPE_BF16)
-        hipLaunchKernelGGL(gdn_prep_kernel<__bf16>, dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, ws);
-    else
-        hipLaunchKernelGGL(gdn_prep_kernel<float>, dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, ws);
+namespace {
+template <typename TIn, bool TRUNC>
+void launch_prep(const GdnDev& d, float* prep, hipStream_t s) {
+    hipLaunchKernelGGL((gdn_prep_kernel<TIn, TRUNC>), dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, prep);
+}
+template <typename TIn, bool TRUNC>
+void launch_scan(const GdnDev& d, int b, int n, float* prep, TIn* out, float* states, float* sin, float* vp,
+                 hipStream_t s) {
+    hipLaunchKernelGGL((gdn_scan_kernel<TIn, TRUNC>), dim3(n, d.hv), dim3(GT), 0, s, d, b, prep, out, states, sin,
+                       vp);
+}
+
+// The forward: chunk terms (prep; TRUNC: plus the node-level U, W), then one
+// scan launch per tree level. gn, y1: TRUNC scratch.
+template <typename TIn, bool TRUNC>
+int gdn_forward(const GdnDev& d, const int32_t* level_offsets, int n_levels, TIn* out, float* states, float* prep,
+                float* sin, float* vp, float* gn, float* y1, hipStream_t s) {
+    launch_prep<TIn, TRUNC>(d, prep, s);
     if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+    if constexpr (TRUNC) {
+        const int rc = tt_gdn_trunc_fwd_launch(d, prep, gn, y1, s);
+        if (rc != TT_OK) return rc;
+    }
     for (int l = 0; l < n_levels; ++l) {
         const int b = level_offsets[l], n = level_offsets[l + 1] - b;
         if (n <= 0) continue;
-        if (d.dtype == TT_DTYPE_BF16)
-            hipLaunchKernelGGL(gdn_scan_kernel<__bf16>, dim3(n, d.hv), dim3(GT), 0, s, d, b, ws, (__bf16*)out,
-                               states, nullptr, nullptr);
-        else
-            hipLaunchKernelGGL(gdn_scan_kernel<float>, dim3(n, d.hv), dim3(GT), 0, s, d, b, ws, (float*)out,
-                               states, nullptr, nullptr);
+        launch_scan<TIn, TRUNC>(d, b, n, prep, out, states, sin, vp, s);
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     return TT_OK;
 }
 
+template <typename TIn>
+int gdn_forward_any(const GdnDev& d, const int32_t* level_offsets, int n_levels, TIn* out, float* states,
+                    float* prep, float* sin, float* vp, float* gn, float* y1, hipStream_t s) {
+    return d.trunc ? gdn_forward<TIn, true>(d, level_offsets, n_levels, out, states, prep, sin, vp, gn, y1, s)
+                   : gdn_forward<TIn, false>(d, level_offsets, n_levels, out, states, prep, sin, vp, gn, y1, s);
+}
+}  // namespace
+
+int tt_gdn_fwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, void* out, float* states,
+                      float* ws, hipStream_t s) {
+    const size_t ch = (size_t)d.n_chunks * d.hv;
+    float* gn = ws + ch * kWsChunk;
+    float* y1 = gn + ch * kTrGn;
+    if (d.dtype == TT_DTYPE_BF16)
+        return gdn_forward_any<__bf16>(d, level_offsets, n_levels, (__bf16*)out, states, ws, nullptr, nullptr, gn,
+                                       y1, s);
+    return gdn_forward_any<float>(d, level_offsets, n_levels, (float*)out, states, ws, nullptr, nullptr, gn, y1, s);
+}
+
 // The backward's float buffers. "Saved" (what the forward can keep for it):
 // per (chunk, v head) the prep terms [kWsChunk], the chunk's initial state S
-// [128 x 128] and V' [32 x 128]. Scratch: per (chunk, v head) dS [128 x 128],
-// dV', X, dW, dK~ [32 x 128]; per (node, v head) dS at entry [128 x 128]; when
-// the backward recomputes the forward, the node states [128 x 128]; <S, dS>
-// per (chunk, v head) last (it breaks 16-byte alignment).
+// [128 x 128] and V' [32 x 128]; TRUNC: also the node-level decay [32] and
+// R-rows y1 [32 x 256]. Scratch: per (chunk, v head) dS [128 x 128], dV', X,
+// dW, dK~ [32 x 128]; TRUNC: dF1, dY0 [32 x 256], the correction's dk^
+// [32 x 128] and dG [32]; per (node, v head) dS at entry [128 x 128]; when the
+// backward recomputes the forward, the node states [128 x 128]; <S, dS> per
+// (chunk, v head) last (it breaks 16-byte alignment).
 namespace {
 struct GdnBwdWs {
-    float *prep, *sin, *vp, *dso, *dvp, *x, *dw, *dkt, *dsn, *nstate, *sdot;
+    float *prep, *sin, *vp, *gn, *y1, *dso, *dvp, *x, *dw, *dkt, *df1, *dy0, *dkr, *dgn, *dsn, *nstate, *sdot;
 };
-size_t gdn_saved_floats(size_t ch) { return ch * (kWsChunk + GD * GD + GC * GD); }
-size_t gdn_scratch_floats(size_t ch, size_t nd, bool recompute) {
-    return ch * (GD * GD + 4 * GC * GD + 1) + nd * GD * GD * (recompute ? 2 : 1);
+size_t gdn_saved_floats(size_t ch, bool trunc) {
+    return ch * (kWsChunk + GD * GD + GC * GD + (trunc ? kTrGn + kTrY1 : 0));
 }
-GdnBwdWs gdn_bwd_carve(float* saved, float* scratch, size_t n_chunks, size_t n_nodes, size_t hv, bool recompute) {
+size_t gdn_scratch_floats(size_t ch, size_t nd, bool recompute, bool trunc) {
+    return ch * (GD * GD + 4 * GC * GD + 1 + (trunc ? 2 * kTrY1 + GC * GD + GC : 0)) +
+           nd * GD * GD * (recompute ? 2 : 1);
+}
+GdnBwdWs gdn_bwd_carve(float* saved, float* scratch, size_t n_chunks, size_t n_nodes, size_t hv, bool recompute,
+                       bool trunc) {
     const size_t ch = n_chunks * hv, nd = n_nodes * hv;
-    GdnBwdWs w;
+    GdnBwdWs w = {};
     float* q = saved;
     w.prep = q; q += ch * kWsChunk;
     w.sin = q; q += ch * GD * GD;
-    w.vp = q;
+    w.vp = q; q += ch * GC * GD;
+    if (trunc) {
+        w.gn = q; q += ch * kTrGn;
+        w.y1 = q; q += ch * kTrY1;
+    }
     q = scratch;
+    if (!q) return w;
     w.dso = q; q += ch * GD * GD;
     w.dvp = q; q += ch * GC * GD;
     w.x = q; q += ch * GC * GD;
     w.dw = q; q += ch * GC * GD;
     w.dkt = q; q += ch * GC * GD;
+    if (trunc) {
+        w.df1 = q; q += ch * kTrY1;
+        w.dy0 = q; q += ch * kTrY1;
+        w.dkr = q; q += ch * GC * GD;
+        w.dgn = q; q += ch * GC;
+    }
     w.dsn = q; q += nd * GD * GD;
     w.nstate = nullptr;
     if (recompute) { w.nstate = q; q += nd * GD * GD; }
@@ -1157,79 +1151,78 @@ GdnBwdWs gdn_bwd_carve(float* saved, float* scratch, size_t n_chunks, size_t n_n
 }
 }  // namespace
 
-size_t tt_gdn_saved_bytes_impl(int n_chunks, int n_heads_v) {
-    return gdn_saved_floats((size_t)n_chunks * n_heads_v) * sizeof(float);
+size_t tt_gdn_saved_bytes_impl(int n_chunks, int n_heads_v, bool trunc) {
+    return gdn_saved_floats((size_t)n_chunks * n_heads_v, trunc) * sizeof(float);
 }
-size_t tt_gdn_bwd_ws_bytes_impl(int n_chunks, int n_nodes, int n_heads_v, bool recompute) {
+size_t tt_gdn_bwd_ws_bytes_impl(int n_chunks, int n_nodes, int n_heads_v, bool recompute, bool trunc) {
     const size_t ch = (size_t)n_chunks * n_heads_v, nd = (size_t)n_nodes * n_heads_v;
-    return ((recompute ? gdn_saved_floats(ch) : 0) + gdn_scratch_floats(ch, nd, recompute)) * sizeof(float);
+    return ((recompute ? gdn_saved_floats(ch, trunc) : 0) + gdn_scratch_floats(ch, nd, recompute, trunc)) *
+           sizeof(float);
 }
 
 int tt_gdn_fwd_save_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, void* out, float* states,
                            float* saved, hipStream_t s) {
-    const GdnBwdWs w = gdn_bwd_carve(saved, nullptr, d.n_chunks, d.n_nodes, d.hv, false);
+    const GdnBwdWs w = gdn_bwd_carve(saved, nullptr, d.n_chunks, d.n_nodes, d.hv, false, d.trunc);
     if (d.dtype == TT_DTYPE_BF16)
-        hipLaunchKernelGGL(gdn_prep_kernel<__bf16>, dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, w.prep);
-    else
-        hipLaunchKernelGGL(gdn_prep_kernel<float>, dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, w.prep);
-    if (hipGetLastError() != hipSuccess) return TT_E_HIP;
-    for (int l = 0; l < n_levels; ++l) {
-        const int b = level_offsets[l], n = level_offsets[l + 1] - b;
-        if (n <= 0) continue;
-        if (d.dtype == TT_DTYPE_BF16)
-            hipLaunchKernelGGL(gdn_scan_kernel<__bf16>, dim3(n, d.hv), dim3(GT), 0, s, d, b, w.prep, (__bf16*)out,
-                               states, w.sin, w.vp);
-        else
-            hipLaunchKernelGGL(gdn_scan_kernel<float>, dim3(n, d.hv), dim3(GT), 0, s, d, b, w.prep, (float*)out,
-                               states, w.sin, w.vp);
-        if (hipGetLastError() != hipSuccess) return TT_E_HIP;
-    }
-    return TT_OK;
+        return gdn_forward_any<__bf16>(d, level_offsets, n_levels, (__bf16*)out, states, w.prep, w.sin, w.vp, w.gn,
+                                       w.y1, s);
+    return gdn_forward_any<float>(d, level_offsets, n_levels, (float*)out, states, w.prep, w.sin, w.vp, w.gn, w.y1,
+                                  s);
 }
 
 // saved == nullptr: recompute the forward into the front of ws; otherwise
 // saved holds what tt_gdn_fwd_save_launch wrote for the same problem.
-template <typename TIn>
+template <typename TIn, bool TRUNC>
 static int gdn_bwd_run(const GdnDev& d, const int32_t* level_offsets, int n_levels, const TIn* d_o, int64_t do_st,
                        int64_t do_sh, TIn* dq, TIn* dk, TIn* dv, float* dg, float* dbeta, const float* saved,
                        float* ws, hipStream_t s) {
     const bool recompute = saved == nullptr;
     float* sv = recompute ? ws : const_cast<float*>(saved);
-    float* scratch = recompute ? ws + gdn_saved_floats((size_t)d.n_chunks * d.hv) : ws;
-    const GdnBwdWs w = gdn_bwd_carve(sv, scratch, d.n_chunks, d.n_nodes, d.hv, recompute);
+    float* scratch = recompute ? ws + gdn_saved_floats((size_t)d.n_chunks * d.hv, TRUNC) : ws;
+    const GdnBwdWs w = gdn_bwd_carve(sv, scratch, d.n_chunks, d.n_nodes, d.hv, recompute, TRUNC);
     if (recompute) {
-        hipLaunchKernelGGL(gdn_prep_kernel<TIn>, dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, w.prep);
-        if (hipGetLastError() != hipSuccess) return TT_E_HIP;
-        for (int l = 0; l < n_levels; ++l) {
-            const int b = level_offsets[l], n = level_offsets[l + 1] - b;
-            if (n <= 0) continue;
-            hipLaunchKernelGGL(gdn_scan_kernel<TIn>, dim3(n, d.hv), dim3(GT), 0, s, d, b, w.prep, (TIn*)nullptr,
-                               w.nstate, w.sin, w.vp);
-            if (hipGetLastError() != hipSuccess) return TT_E_HIP;
-        }
+        const int rc = gdn_forward<TIn, TRUNC>(d, level_offsets, n_levels, (TIn*)nullptr, w.nstate, w.prep, w.sin,
+                                               w.vp, w.gn, w.y1, s);
+        if (rc != TT_OK) return rc;
     }
     for (int l = n_levels - 1; l >= 0; --l) {
         const int b = level_offsets[l], n = level_offsets[l + 1] - b;
         if (n <= 0) continue;
-        hipLaunchKernelGGL(gdn_rscan_kernel<TIn>, dim3(n, d.hv), dim3(GT), 0, s, d, b, w.prep, d_o, do_st, do_sh,
-                           w.dso, w.dvp, w.dsn);
+        hipLaunchKernelGGL((gdn_rscan_kernel<TIn, TRUNC>), dim3(n, d.hv), dim3(GT), 0, s, d, b, w.prep, d_o, do_st,
+                           do_sh, w.dso, w.dvp, w.dsn);
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     hipLaunchKernelGGL(gdn_bwd_state_kernel<TIn>, dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, d_o, do_st, do_sh,
                        w.sin, w.dso, w.vp, w.dvp, w.x, w.dw, w.dkt, w.sdot);
     if (hipGetLastError() != hipSuccess) return TT_E_HIP;
-    hipLaunchKernelGGL(gdn_bwd_chunk_kernel<TIn>, dim3(d.n_chunks, d.hk), dim3(GT), 0, s, d, d_o, do_st, do_sh,
-                       w.prep, w.vp, w.dvp, w.x, w.dw, w.dkt, w.sdot, dq, dk, dv, dg, dbeta);
+    if constexpr (TRUNC) {
+        hipLaunchKernelGGL(gdn_dw_s0_kernel, dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, w.sin, w.dvp, w.dw);
+        const GdnTruncBwd tb{w.gn, w.y1, w.dvp, w.dw, w.df1, w.dy0, w.dkr, w.dgn};
+        const int rc = tt_gdn_trunc_bwd_launch(d, tb, dv, dbeta, s);
+        if (rc != TT_OK) return rc;
+    }
+    hipLaunchKernelGGL((gdn_bwd_chunk_kernel<TIn, TRUNC>), dim3(d.n_chunks, d.hk), dim3(GT), 0, s, d, d_o, do_st,
+                       do_sh, w.prep, w.vp, w.dvp, w.x, w.dw, w.dkt, w.sdot, dq, dk, dv, dg, dbeta, w.dkr, w.dgn);
     if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     return TT_OK;
+}
+
+template <typename TIn>
+static int gdn_bwd_any(const GdnDev& d, const int32_t* level_offsets, int n_levels, const TIn* d_o, int64_t do_st,
+                       int64_t do_sh, TIn* dq, TIn* dk, TIn* dv, float* dg, float* dbeta, const float* saved,
+                       float* ws, hipStream_t s) {
+    return d.trunc ? gdn_bwd_run<TIn, true>(d, level_offsets, n_levels, d_o, do_st, do_sh, dq, dk, dv, dg, dbeta,
+                                            saved, ws, s)
+                   : gdn_bwd_run<TIn, false>(d, level_offsets, n_levels, d_o, do_st, do_sh, dq, dk, dv, dg, dbeta,
+                                             saved, ws, s);
 }
 
 int tt_gdn_bwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, const void* d_o, int64_t do_st,
                       int64_t do_sh, void* dq, void* dk, void* dv, float* dg, float* dbeta, const float* saved,
                       float* ws, hipStream_t s) {
     if (d.dtype == TT_DTYPE_BF16)
-        return gdn_bwd_run<__bf16>(d, level_offsets, n_levels, (const __bf16*)d_o, do_st, do_sh, (__bf16*)dq,
+        return gdn_bwd_any<__bf16>(d, level_offsets, n_levels, (const __bf16*)d_o, do_st, do_sh, (__bf16*)dq,
                                    (__bf16*)dk, (__bf16*)dv, dg, dbeta, saved, ws, s);
-    return gdn_bwd_run<float>(d, level_offsets, n_levels, (const float*)d_o, do_st, do_sh, (float*)dq, (float*)dk,
+    return gdn_bwd_any<float>(d, level_offsets, n_levels, (const float*)d_o, do_st, do_sh, (float*)dq, (float*)dk,
                               (float*)dv, dg, dbeta, saved, ws, s);
 }

@@ -58,6 +58,7 @@ struct GdnDev {
     const int32_t* child_off;              // children of node i: child[child_off[i] .. child_off[i+1]) (backward)
     const int32_t* child;
     int dtype, n_tokens, n_nodes, n_chunks, hk, hv, rep, l2;
+    int trunc;                             // the reference's I + R + R^2 per node (else the exact rule)
     float scale;
 };
 
@@ -97,16 +98,33 @@ int tt_ce_rows_launch(int dtype, const void* logits, int64_t ld, int n_rows, int
                       const float* row_scale, int ignore_index, float* loss, void* grad, int64_t ldg,
                       hipStream_t s);
 
-size_t tt_gdn_ws_bytes_impl(int n_chunks, int n_heads_v);
+size_t tt_gdn_ws_bytes_impl(int n_chunks, int n_heads_v, bool trunc);
 int tt_gdn_fwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, void* out, float* states,
                       float* ws, hipStream_t s);
-size_t tt_gdn_saved_bytes_impl(int n_chunks, int n_heads_v);
+size_t tt_gdn_saved_bytes_impl(int n_chunks, int n_heads_v, bool trunc);
 int tt_gdn_fwd_save_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, void* out, float* states,
                            float* saved, hipStream_t s);
-size_t tt_gdn_bwd_ws_bytes_impl(int n_chunks, int n_nodes, int n_heads_v, bool recompute);
+size_t tt_gdn_bwd_ws_bytes_impl(int n_chunks, int n_nodes, int n_heads_v, bool recompute, bool trunc);
 int tt_gdn_bwd_launch(const GdnDev& d, const int32_t* level_offsets, int n_levels, const void* d_o, int64_t do_st,
                       int64_t do_sh, void* dq, void* dk, void* dv, float* dg, float* dbeta, const float* saved,
                       float* ws, hipStream_t s);
+
+// The truncated (reference) mode's node-level terms (tt_gdn_trunc.hip). The
+// forward part fills the U and W slots of the chunk terms in `prep`; the
+// backward part turns dF = [dV' | dW] into dv, dbeta (complete) and the
+// correction's dk^ and node-level dG suffix sums, which the chunk backward adds.
+struct GdnTruncBwd {
+    float* gn;            // [chunk, Hv, 32] node-level decay (from the forward)
+    float* y1;            // [chunk, Hv, 32, 256] R Y0 (from the forward)
+    float* dvp;           // [chunk, Hv, 32, 128] dV'
+    float* dw;            // [chunk, Hv, 32, 128] dW
+    float* df1;           // [chunk, Hv, 32, 256] scratch
+    float* dy0;           // [chunk, Hv, 32, 256] scratch
+    float* dkr;           // [chunk, Hv, 32, 128] out
+    float* dgn;           // [chunk, Hv, 32] out
+};
+int tt_gdn_trunc_fwd_launch(const GdnDev& d, float* prep, float* gn, float* y1, hipStream_t s);
+int tt_gdn_trunc_bwd_launch(const GdnDev& d, const GdnTruncBwd& w, void* dv, float* dbeta, hipStream_t s);
 
 size_t tt_meta_ws_bytes_impl(int n);
 int tt_meta_build_impl(const int32_t* len, const int32_t* par, int n, int T, int pos_offset, int32_t* start,

@@ -8,11 +8,12 @@ inputs — q, k ``[B=1, T, Hk, D]``, v ``[1, T, Hv, D]``, g, beta ``[1, T, Hv]``
 ``tt_gdn_tree_fwd``: one parallel HIP launch over all 32-token chunks for the
 state-independent terms, then one scan launch per tree level.
 
-Semantics: the exact gated delta rule along every root-to-leaf path (what the
-reference function states it computes, tree_dfs_ssm.py:49-52). The reference's
-own evaluation truncates the within-node correction to I + R + R^2
-(tree_dfs_ssm.py:114-121), which agrees with this for nodes of at most three
-tokens and deviates for longer ones.
+Semantics: by default the exact gated delta rule along every root-to-leaf
+path (what the reference function states it computes, tree_dfs_ssm.py:49-52).
+With ``reference_truncated=True`` it returns what the reference function itself
+computes: every whole node one chunk, the within-node correction built from
+the uncorrected rows, A = I + R + R^2 (tree_dfs_ssm.py:120-126). The two agree
+for nodes of at most three tokens and differ for longer ones.
 """
 from __future__ import annotations
 
@@ -138,7 +139,7 @@ def _tok_vec(x: torch.Tensor, name: str) -> torch.Tensor:
     return x
 
 
-def _problem(q, k, v, g, beta, tree: GdnTree, scale, l2norm):
+def _problem(q, k, v, g, beta, tree: GdnTree, scale, l2norm, reference_truncated=False):
     q, k, v = _tok_heads(q, "q"), _tok_heads(k, "k"), _tok_heads(v, "v")
     g, beta = _tok_vec(g, "g"), _tok_vec(beta, "beta")
     T, Hk, _ = q.shape
@@ -160,7 +161,8 @@ def _problem(q, k, v, g, beta, tree: GdnTree, scale, l2norm):
         node_start=_ptr(tree.d_start), node_len=_ptr(tree.d_len), node_parent=_ptr(tree.d_parent),
         level_nodes=_ptr(tree.d_levels), level_offsets=tree.level_offsets, n_levels=tree.n_levels,
         n_chunks=tree.n_chunks, node_chunk0=_ptr(tree.d_chunk0), chunk_node=_ptr(tree.d_chunk_node),
-        node_child_off=_ptr(tree.d_child_off), node_child=_ptr(tree.d_child))
+        node_child_off=_ptr(tree.d_child_off), node_child=_ptr(tree.d_child),
+        reference_truncated=1 if reference_truncated else 0)
     return p, (q, k, v, g, beta)
 
 
@@ -171,8 +173,8 @@ def _problem(q, k, v, g, beta, tree: GdnTree, scale, l2norm):
 KEEP_FORWARD_STATES = True
 
 
-def _gdn_forward(q, k, v, g, beta, tree: GdnTree, scale, l2norm, keep: bool):
-    p, (q, k, v, g, beta) = _problem(q, k, v, g, beta, tree, scale, l2norm)
+def _gdn_forward(q, k, v, g, beta, tree: GdnTree, scale, l2norm, keep: bool, reference_truncated=False):
+    p, (q, k, v, g, beta) = _problem(q, k, v, g, beta, tree, scale, l2norm, reference_truncated)
     T, Hv = v.shape[0], v.shape[1]
     dev = require_device(q.device)
     o = torch.empty((T, Hv, HEAD_DIM), dtype=v.dtype, device=dev)
@@ -192,21 +194,22 @@ def _gdn_forward(q, k, v, g, beta, tree: GdnTree, scale, l2norm, keep: bool):
 
 
 def gdn_tree_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
-                     tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True):
+                     tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True,
+                     reference_truncated: bool = False):
     """o [T, Hv, 128] (dtype of v) and node_states [n_nodes, Hv, 128, 128]
     (float32; the state after each node)."""
-    o, states, _ = _gdn_forward(q, k, v, g, beta, tree, scale, l2norm, False)
+    o, states, _ = _gdn_forward(q, k, v, g, beta, tree, scale, l2norm, False, reference_truncated)
     return o, states
 
 
 def gdn_tree_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
                       d_o: torch.Tensor, tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True,
-                      saved: Optional[torch.Tensor] = None):
+                      saved: Optional[torch.Tensor] = None, reference_truncated: bool = False):
     """Gradients of sum(o * d_o) for ``gdn_tree_forward``'s o: dq, dk [T, Hk,
     128] and dv [T, Hv, 128] in the dtype of v, dg and dbeta [T, Hv] float32.
     Recomputes the forward internally (tt_gdn_tree_bwd) unless ``saved`` holds
     what tt_gdn_tree_fwd_save kept for the same inputs (tt_gdn_tree_bwd_saved)."""
-    p, (q, k, v, g, beta) = _problem(q, k, v, g, beta, tree, scale, l2norm)
+    p, (q, k, v, g, beta) = _problem(q, k, v, g, beta, tree, scale, l2norm, reference_truncated)
     d_o = _tok_heads(d_o, "d_o").to(v.dtype)
     T, Hk, Hv = q.shape[0], q.shape[1], v.shape[1]
     if d_o.shape != v.shape:
@@ -240,15 +243,15 @@ class GdnTreeFunction(torch.autograd.Function):
     node states are returned without a gradient."""
 
     @staticmethod
-    def forward(ctx, q, k, v, g, beta, tree, scale, l2norm):
+    def forward(ctx, q, k, v, g, beta, tree, scale, l2norm, reference_truncated):
         keep = bool(KEEP_FORWARD_STATES)
-        o, states, saved = _gdn_forward(q, k, v, g, beta, tree, scale, l2norm, keep)
+        o, states, saved = _gdn_forward(q, k, v, g, beta, tree, scale, l2norm, keep, reference_truncated)
         # The kept forward terms go through save_for_backward as well: autograd
         # then frees them with the graph (after a backward without retain_graph,
         # or when the graph is dropped), and every backward of a graph run
         # with retain_graph (the reference's per-leaf schedule) reuses them.
         ctx.save_for_backward(q, k, v, g, beta, *(() if saved is None else (saved,)))
-        ctx.tree, ctx.scale, ctx.l2norm = tree, scale, l2norm
+        ctx.tree, ctx.scale, ctx.l2norm, ctx.trunc = tree, scale, l2norm, reference_truncated
         ctx.mark_non_differentiable(states)
         return o, states
 
@@ -256,29 +259,32 @@ class GdnTreeFunction(torch.autograd.Function):
     def backward(ctx, d_o, _d_states):
         q, k, v, g, beta, *kept = ctx.saved_tensors
         dq, dk, dv, dg, dbeta = gdn_tree_backward(q, k, v, g, beta, d_o, ctx.tree, ctx.scale, ctx.l2norm,
-                                                  saved=kept[0] if kept else None)
+                                                  saved=kept[0] if kept else None, reference_truncated=ctx.trunc)
         return (dq.reshape(q.shape).to(q.dtype), dk.reshape(k.shape).to(k.dtype), dv.reshape(v.shape).to(v.dtype),
-                dg.reshape(g.shape).to(g.dtype), dbeta.reshape(beta.shape).to(beta.dtype), None, None, None)
+                dg.reshape(g.shape).to(g.dtype), dbeta.reshape(beta.shape).to(beta.dtype), None, None, None, None)
 
 
-def gdn_tree(q, k, v, g, beta, tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True):
+def gdn_tree(q, k, v, g, beta, tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True,
+             reference_truncated: bool = False):
     """Autograd-aware ``gdn_tree_forward``: (o, node_states). When any input
     requires a gradient and ``KEEP_FORWARD_STATES`` is set, the forward keeps
     its chunk terms and states for the backward."""
     if not (torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, g, beta))):
-        return gdn_tree_forward(q, k, v, g, beta, tree, scale, l2norm)
-    return GdnTreeFunction.apply(q, k, v, g, beta, tree, scale, l2norm)
+        return gdn_tree_forward(q, k, v, g, beta, tree, scale, l2norm, reference_truncated)
+    return GdnTreeFunction.apply(q, k, v, g, beta, tree, scale, l2norm, bool(reference_truncated))
 
 
 def torch_chunk_gated_delta_rule_tree_varlen(query, key, value, g, beta, chunk_boundaries, chunk_parent_map,
                                              initial_state=None, output_final_state=False,
-                                             use_qk_l2norm_in_kernel=False):
+                                             use_qk_l2norm_in_kernel=False, reference_truncated=False):
     """Signature of tree_dfs_ssm.py:38-46 (no initial state), differentiable in
     q, k, v, g and beta. Returns (core_out [1, T, Hv, 128], None or the last
-    node's state)."""
+    node's state). ``reference_truncated=True`` gives the reference function's
+    own numbers (I + R + R^2 per node) instead of the exact rule."""
     if initial_state is not None:
         raise NotImplementedError("initial_state is not supported (the reference drivers pass None)")
     tree = GdnTree.from_boundaries(chunk_boundaries, chunk_parent_map, query.device)
-    o, states = gdn_tree(query, key, value, g, beta, tree, l2norm=use_qk_l2norm_in_kernel)
+    o, states = gdn_tree(query, key, value, g, beta, tree, l2norm=use_qk_l2norm_in_kernel,
+                         reference_truncated=reference_truncated)
     last = states[-1][None] if output_final_state else None
     return o[None], last

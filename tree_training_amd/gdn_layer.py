@@ -12,8 +12,9 @@ norm, out_proj, key_dim, value_dim, head_k_dim, head_v_dim) runs:
                 ancestors' last K-1 inputs), token-major rows
   gates         beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias) (torch)
   scan          tt_gdn_tree_fwd / _bwd (exact gated delta rule per root-to-leaf
-                path; v head h reads q/k head h / (Hv/Hk), the reference's
-                repeat_interleave, without materialising the repeat)
+                path, or with reference_truncated the reference function's
+                own I + R + R^2 per node; v head h reads q/k head h / (Hv/Hk),
+                the reference's repeat_interleave, without materialising it)
   output        the module's own RMSNormGated and out_proj over all tokens
 
 The reference projects node by node so that bf16 GEMM shapes match separate
@@ -33,7 +34,7 @@ from .conv import tree_conv
 from .gdn import GdnTree, gdn_tree
 
 
-def _tree_ssm_forward(ssm, hidden_states: torch.Tensor, tree: GdnTree) -> torch.Tensor:
+def _tree_ssm_forward(ssm, hidden_states: torch.Tensor, tree: GdnTree, reference_truncated: bool = False) -> torch.Tensor:
     B, S, _ = hidden_states.shape
     if B != 1:
         raise ValueError("the tree forward packs one forest per batch row; batch size must be 1")
@@ -51,7 +52,7 @@ def _tree_ssm_forward(ssm, hidden_states: torch.Tensor, tree: GdnTree) -> torch.
     v = v.reshape(S, -1, ssm.head_v_dim)
     beta = b.sigmoid()
     g = -ssm.A_log.float().exp() * F.softplus(a.float() + ssm.dt_bias)
-    o, _ = gdn_tree(q, k, v, g, beta, tree, None, True)          # [T, Hv, Dv]
+    o, _ = gdn_tree(q, k, v, g, beta, tree, None, True, reference_truncated)   # [T, Hv, Dv]
     o = ssm.norm(o.reshape(-1, ssm.head_v_dim), z.reshape(-1, ssm.head_v_dim))
     return ssm.out_proj(o.reshape(1, S, -1))
 
@@ -73,13 +74,13 @@ class _LazyTree:
 
 
 def _make_dfs_ssm_forward(ssm_layer, chunk_boundaries: Sequence[Tuple[int, int]], chunk_parent_map: Sequence[int],
-                          tree: _LazyTree = None):
+                          tree: _LazyTree = None, reference_truncated: bool = False):
     """Patched forward for one GatedDeltaNet layer (dfs_tree_forward.py:360,
     tree_dfs_ssm.py:355). ``tree`` may be shared by all layers of a model."""
     tree = tree or _LazyTree(chunk_boundaries, chunk_parent_map)
 
     def patched_forward(hidden_states, cache_params=None, cache_position=None, attention_mask=None, **kwargs):
-        return _tree_ssm_forward(ssm_layer, hidden_states, tree.on(hidden_states.device))
+        return _tree_ssm_forward(ssm_layer, hidden_states, tree.on(hidden_states.device), reference_truncated)
 
     return patched_forward
 
@@ -88,14 +89,14 @@ def _ssm_layers(model):
     return [layer.linear_attn for layer in model.model.layers if hasattr(layer, "linear_attn")]
 
 
-def _patch_ssm(model, chunk_boundaries, chunk_parent_map) -> Dict:
+def _patch_ssm(model, chunk_boundaries, chunk_parent_map, reference_truncated: bool = False) -> Dict:
     """Patch every GatedDeltaNet layer (dfs_tree_forward.py:442-462): the
     accelerate-wrapped ``_old_forward`` when present, else ``forward``.
     Returns what ``_unpatch_ssm`` restores."""
     saved = {}
     tree = _LazyTree(chunk_boundaries, chunk_parent_map)
     for ssm in _ssm_layers(model):
-        patched = _make_dfs_ssm_forward(ssm, chunk_boundaries, chunk_parent_map, tree)
+        patched = _make_dfs_ssm_forward(ssm, chunk_boundaries, chunk_parent_map, tree, reference_truncated)
         attr = "_old_forward" if hasattr(ssm, "_old_forward") else "forward"
         saved[ssm] = (attr, ssm.__dict__.get(attr, None))
         setattr(ssm, attr, patched)
@@ -111,9 +112,9 @@ def _unpatch_ssm(saved: Dict) -> None:
             setattr(ssm, attr, orig)
 
 
-def patch_ssm_for_dfs(model, chunk_boundaries, chunk_parent_map) -> Dict:
+def patch_ssm_for_dfs(model, chunk_boundaries, chunk_parent_map, reference_truncated: bool = False) -> Dict:
     """tree_dfs_ssm.py:432 name for ``_patch_ssm``."""
-    return _patch_ssm(model, chunk_boundaries, chunk_parent_map)
+    return _patch_ssm(model, chunk_boundaries, chunk_parent_map, reference_truncated)
 
 
 def unpatch_ssm(saved: Dict) -> None:
