@@ -106,34 +106,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             fetch_bounds(a, kt1, nb);
         }
 
-        f32x16 s[2], dp[2];
+        // The tile as two 32-key halves: scores, dS and the dQ update of one
+        // half before the next. Half the score registers are live at a time
+        // (234 VGPRs without spills, against 256 and a spill for the whole
+        // tile at once), so the operand reads run further ahead of their MFMAs.
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-            s[b] = (f32x16){};
-            dp[b] = (f32x16){};
+            f32x16 sh = (f32x16){}, dph = (f32x16){};
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-                s[b] = mfma32(read_row_operand(S.K, 32 * b + col, 16 * t + 8 * half), qa[t], s[b]);
-                dp[b] = mfma32(read_row_operand(S.V, 32 * b + col, 16 * t + 8 * half), da[t], dp[b]);
+                sh = mfma32(read_row_operand(S.K, 32 * b + col, 16 * t + 8 * half), qa[t], sh);
+                dph = mfma32(read_row_operand(S.V, 32 * b + col, 16 * t + 8 * half), da[t], dph);
             }
-        }
-        if (!full) mask_scores(s, S.lo, S.hi, qi, half);
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
+            if (!full) mask_half(sh, S.lo + 32 * b, S.hi + 32 * b, qi, half);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float p = fast_exp2(fmaf(s[b][r], c, -lse2));
-                s[b][r] = p * (dp[b][r] - dlt);   // dS^T
+                const float p = fast_exp2(fmaf(sh[r], c, -lse2));
+                sh[r] = p * (dph[r] - dlt);   // dS^T
             }
 #pragma unroll
-        for (int stp = 0; stp < 4; ++stp) {
-            const f32x16& sb = s[stp >> 1];
-            const int r0 = 8 * (stp & 1);
-            const bf16x8 pk = pack8(sb[r0 + 0], sb[r0 + 1], sb[r0 + 2], sb[r0 + 3], sb[r0 + 4], sb[r0 + 5],
-                                    sb[r0 + 6], sb[r0 + 7]);
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const int r0 = 8 * s2;
+                const bf16x8 pk = pack8(sh[r0 + 0], sh[r0 + 1], sh[r0 + 2], sh[r0 + 3], sh[r0 + 4], sh[r0 + 5],
+                                        sh[r0 + 6], sh[r0 + 7]);
 #pragma unroll
-            for (int db = 0; db < 4; ++db)
-                dq[db] = mfma32(read_tr_operand(S.K, 16 * stp, 32 * db, lane), pk, dq[db]);
+                for (int db = 0; db < 4; ++db)
+                    dq[db] = mfma32(read_tr_operand(S.K, 16 * (2 * b + s2), 32 * db, lane), pk, dq[db]);
+            }
         }
     }
 
@@ -337,18 +336,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
                     }
             }
             // dV += P^T dO, dK += dS^T Q: contraction over the 32 queries.
+            {   // P and dS packed at once (the score registers die here); the
+                // transposed dO / Q operands of MFMA pair i + 1 are read before
+                // pair i issues, so the LDS latency hides behind the MFMAs.
+                bf16x8 pa[2], sa[2];
 #pragma unroll
-            for (int stp = 0; stp < 2; ++stp) {
-                const int r0 = 8 * stp;
-                const bf16x8 pa = pack8(sc[r0 + 0], sc[r0 + 1], sc[r0 + 2], sc[r0 + 3], sc[r0 + 4], sc[r0 + 5],
-                                        sc[r0 + 6], sc[r0 + 7]);
-                const bf16x8 sa = pack8(dp[r0 + 0], dp[r0 + 1], dp[r0 + 2], dp[r0 + 3], dp[r0 + 4],
-                                        dp[r0 + 5], dp[r0 + 6], dp[r0 + 7]);
-#pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    dv[db] = mfma32(pa, read_trx(S.Dn, tro, 16 * stp, 32 * db), dv[db]);
-                    dk[db] = mfma32(sa, read_trx(S.Q, tro, 16 * stp, 32 * db), dk[db]);
+                for (int stp = 0; stp < 2; ++stp) {
+                    const int r0 = 8 * stp;
+                    pa[stp] = pack8(sc[r0 + 0], sc[r0 + 1], sc[r0 + 2], sc[r0 + 3], sc[r0 + 4], sc[r0 + 5],
+                                    sc[r0 + 6], sc[r0 + 7]);
+                    sa[stp] = pack8(dp[r0 + 0], dp[r0 + 1], dp[r0 + 2], dp[r0 + 3], dp[r0 + 4], dp[r0 + 5],
+                                    dp[r0 + 6], dp[r0 + 7]);
                 }
+                bf16x8 od[2], oq[2];
+                od[0] = read_trx(S.Dn, tro, 0, 0);
+                oq[0] = read_trx(S.Q, tro, 0, 0);
+                static_for<8>([&](auto ii) {   // pair i: query half i / 4, d block i % 4
+                    constexpr int i = decltype(ii)::value, n = i + 1;
+                    if constexpr (n < 8) {
+                        od[n % 2] = read_trx(S.Dn, tro, 16 * (n / 4), 32 * (n % 4));
+                        oq[n % 2] = read_trx(S.Q, tro, 16 * (n / 4), 32 * (n % 4));
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    dv[i % 4] = mfma32(pa[i / 4], od[i % 2], dv[i % 4]);
+                    dk[i % 4] = mfma32(sa[i / 4], oq[i % 2], dk[i % 4]);
+                });
             }
         }
 

@@ -286,6 +286,21 @@ __device__ __forceinline__ void mask_scores(f32x16 (&s)[2], const int* s_lo, con
     }
 }
 
+// As mask_scores, for one 32-key half of the tile (lo/hi point at its first key).
+__device__ __forceinline__ void mask_half(f32x16& s, const int* s_lo, const int* s_hi, int qi, int half) {
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp) {
+        const int k0 = 8 * grp + 4 * half;
+        const i32x4 lo = *(const i32x4*)(s_lo + k0);
+        const i32x4 hi = *(const i32x4*)(s_hi + k0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const bool vis = lo[e] <= qi && qi < hi[e];
+            s[4 * grp + e] = vis ? s[4 * grp + e] : -INFINITY;
+        }
+    }
+}
+
 // blockIdx.x -> (query block, q head). Workgroups are dispatched round-robin
 // over the 8 XCDs; each XCD gets the q heads of whole kv-head groups so their
 // K/V stay in its L2, and the heaviest query blocks go first.
