@@ -240,7 +240,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(topo, args.cpu_runs)
+        cpu = cpu_baseline(topo, args.cpu_runs, args.workload)
 
     line = {
         "metric": "tree-attn fwd+bwd useful TFLOP/s (16K-token DFS tree, bf16)",
@@ -354,7 +354,7 @@ def leafce_cpu_baseline(runs):
     in rows/s (the GEMMs are not included)."""
     import torch
     import torch.nn.functional as F
-    cores = min(16, os.cpu_count() or 1)
+    cores = cpu_threads()
     torch.set_num_threads(cores)
     g = torch.Generator().manual_seed(0)
     x = torch.randn(64, 151936, generator=g).requires_grad_(True)
@@ -461,7 +461,7 @@ def prologue_cpu_baseline(runs):
     16 host threads, median of ``runs`` after a warm-up, in tokens/s."""
     import torch
     from oracle.prologue import qk_prologue
-    cores = min(16, os.cpu_count() or 1)
+    cores = cpu_threads()
     torch.set_num_threads(cores)
     g = torch.Generator().manual_seed(0)
     n = 512
@@ -604,7 +604,44 @@ def gdn_cpu_baseline(lens, par, runs):
             "seconds_per_sample": round(t, 3)}
 
 
-def cpu_baseline(topo, runs):
+def cpu_threads():
+    """Host threads for the CPU baselines: the job's CPU share when the
+    launcher states it (OMP_NUM_THREADS, set to the cores granted to this
+    process on a shared host), else os.cpu_count()."""
+    n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return min(n, int(env)) if env.isdigit() and int(env) > 0 else n
+
+
+C1_TOPOLOGY = ([3, 4, 3, 4, 5, 3, 3, 4, 4, 3, 4, 3, 4], [-1, 0, 1, 2, 3, 3, 2, 6, -1, 8, 9, 8, 11])
+
+
+def literal_metadata_seconds(workload, topo):
+    """Host time of the reference's metadata as its literal loops (the
+    restatement of build_dfs_tree_info's per-pair mask loop; for the gateway
+    workload the whole partition schedule: partitions, per-partition DFS info
+    and gateway biases), on the 47-token two-root tree and on the workload's
+    tree. The 48K rollout tree (3.9e8 mask writes) is not timed."""
+    from oracle.partition import hybrid_schedule
+    from oracle.tree_meta import build_dfs_tree_info_literal
+    from tree_training_amd.tree import TreeNode
+    from tree_training_amd.workloads import forest_from_topology
+    out = {}
+    for name, tp in (("c1_47_tokens", C1_TOPOLOGY), (workload, topo)):
+        if name == "rollout48k":
+            out[name] = None
+            continue
+        roots, _ = forest_from_topology(tp, TreeNode)
+        t0 = time.perf_counter()
+        if name == "gateway16k":
+            hybrid_schedule(roots, 4096)
+        else:
+            build_dfs_tree_info_literal(roots)
+        out[name] = round(time.perf_counter() - t0, 4)
+    return out
+
+
+def cpu_baseline(topo, runs, workload="agent16k"):
     """Dense-mask restatement of the reference path on the host cores, on one
     kv-head group (4 q heads + 1 kv head) of the same tree: median of ``runs``
     fwd+bwd after one warm-up. Reported in the metric's unit (useful TFLOP/s
@@ -613,7 +650,7 @@ def cpu_baseline(topo, runs):
     from oracle.dense_path import additive_mask, dense_fwd_bwd
     from oracle.tree_meta import mask_from_horizon, meta_closed_form
     from tree_training_amd.workloads import visible_pairs
-    cores = min(16, os.cpu_count() or 1)
+    cores = cpu_threads()
     torch.set_num_threads(cores)
     lens, par = topo
     m = meta_closed_form(lens, par)
@@ -650,7 +687,9 @@ def cpu_baseline(topo, runs):
             "sample": f"1 of 8 kv-head groups (4 q heads) of the full {T}-token tree, dense additive mask + "
                       f"repeat_kv + SDPA fwd+bwd in bf16 (torch CPU), median of {runs} after 1 warm-up",
             "seconds_per_sample": round(t, 3), "mask_build_s": round(t_mask, 3),
-            "tokens_per_s_full_layer": round(T / (t * HKV), 1), "cpu_model": model}
+            "metadata_literal_s": literal_metadata_seconds(workload, topo),
+            "tokens_per_s_full_layer": round(T / (t * HKV), 1), "cpu_model": model,
+            "os_cpu_count": os.cpu_count()}
 
 
 if __name__ == "__main__":

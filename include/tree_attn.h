@@ -44,7 +44,10 @@ enum { TT_DTYPE_F32 = 0, TT_DTYPE_BF16 = 1 };
 enum {
     TT_BWD_DELTA = 1,   /* rowsum(dO * O) into the workspace */
     TT_BWD_DQ = 2,      /* dQ (reads the workspace) */
-    TT_BWD_DKDV = 4     /* dK, dV and gateway accumulation (reads the workspace) */
+    TT_BWD_DKDV = 4,    /* dK, dV and gateway accumulation (reads the workspace) */
+    TT_BWD_DETERMINISTIC = 8   /* modifier, OR'ed with the parts (alone: every part): bf16 dK/dV and
+                                  gateway sums in a fixed order, so repeated calls on the same inputs
+                                  are bitwise equal (more workspace; see tt_attn_bwd) */
 };
 
 /* Device-side status bits written by tt_meta_build / tt_keys_build. */
@@ -151,7 +154,13 @@ int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* stream);
  * query range spans more than W queries, W = half the largest power of two
  * <= n_q clamped to [256, 4096] (split into several work items), sum their
  * dK/dV partials with fp32 atomics, so their rounding can vary from run to
- * run. */
+ * run. With TT_BWD_DETERMINISTIC in bwd_parts each of those work items
+ * stores its partial sums in a slot of its own and one pass adds them in
+ * work-item order: no atomics, bitwise-repeatable dk, dv and gateway sums.
+ * The workspace (tt_attn_bwd_workspace_bytes of the problem with the bit set)
+ * then grows by 2 * n_kb * floor((n_q - 1) / W) * 128 * Hkv * 512 bytes, n_kb
+ * = ceil((n_past + n_q) / 128) (about 4x the bf16 workspace at n_q = 16K).
+ * Only the TT_BWD_DKDV part depends on the bit. */
 size_t tt_attn_bwd_workspace_bytes(const tt_attn_problem* p);
 int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_tensor d_o,
                 void* dq, void* dk, void* dv, float* dk_past_acc, float* dv_past_acc,

@@ -84,6 +84,38 @@ def test_bwd_validation():
     assert lib.tt_attn_bwd(ctypes.byref(p), V, V, d_o, V, V, V, None, None, V, 8, None) == _lib.TT_E_WORKSPACE
 
 
+def _qch(n_q):
+    half = (1 << (n_q.bit_length() - 1)) // 2 if n_q >= 2 else 0
+    return min(4096, max(256, half))
+
+
+@pytest.mark.parametrize("n_q,n_past", [(100, 0), (600, 0), (16318, 0), (5300, 300), (50109, 0)])
+def test_bwd_deterministic_workspace(n_q, n_past):
+    """TT_BWD_DETERMINISTIC adds, for bf16, one dK and one dV slot of 128 keys
+    x Hkv x 128 fp32 for each possible work item beyond the first of a key
+    tile: ceil(n_keys / 128) * floor((n_q - 1) / W) of them (W: the work
+    item's query window); fp32 problems need nothing more."""
+    lib = _lib.lib()
+    base = _problem(n_q=n_q, n_past=n_past)
+    det = _problem(n_q=n_q, n_past=n_past, bwd_parts=_lib.TT_BWD_DETERMINISTIC)
+    n_kb = -(-(n_q + n_past) // 128)
+    extra = 2 * n_kb * ((n_q - 1) // _qch(n_q)) * 128 * 8 * 128 * 4
+    assert lib.tt_attn_bwd_workspace_bytes(ctypes.byref(det)) - \
+        lib.tt_attn_bwd_workspace_bytes(ctypes.byref(base)) == extra
+    assert (extra == 0) == (n_q <= 256 or n_q - 1 < _qch(n_q))
+    for p in (base, det):
+        p.dtype = _lib.TT_DTYPE_F32
+    assert lib.tt_attn_bwd_workspace_bytes(ctypes.byref(det)) == lib.tt_attn_bwd_workspace_bytes(ctypes.byref(base))
+
+
+def test_bwd_parts_validation():
+    lib = _lib.lib()
+    d_o = _lib.TTTensor(16, 32 * 128, 128)
+    V = ctypes.c_void_p(16)
+    p = _problem(bwd_parts=16)
+    assert lib.tt_attn_bwd(ctypes.byref(p), V, V, d_o, V, V, V, None, None, V, 1 << 40, None) == _lib.TT_E_ARG
+
+
 def test_bwd_noalloc_validation():
     """The no-allocation backward: a 64 MiB scratch, null problems rejected,
     and a problem whose workspace exceeds the scratch refused on the host

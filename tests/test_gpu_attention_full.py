@@ -189,3 +189,40 @@ def test_attention_gateway_partitions_full_size():
     torch.cuda.synchronize()
     assert _max_rel(dk.float(), sum_dk) < 2e-2
     assert _max_rel(dv.float(), sum_dv) < 2e-2
+
+
+def test_attention_deterministic_full_size():
+    """The 16K agent tree under a 4096-key gateway that every query sees (so
+    the gateway tiles and the root's tiles split into several dK/dV work
+    items): with TT_BWD_DETERMINISTIC two backwards are bitwise equal (dq, dk,
+    dv and the fp32 gateway sums), and they agree with the default (atomic)
+    backward to bf16 rounding (max_rel < 1e-2)."""
+    from tree_training_amd.attention import attn_backward, attn_forward
+    from tree_training_amd.meta import KeyPlan, TreeMetaDevice
+    lens, par = workloads.agent_tree(0)
+    T, Lp = sum(lens), 4096
+    g = torch.Generator(device=DEV).manual_seed(9)
+    bf = torch.bfloat16
+    q = torch.randn(T, HQ, D, device=DEV, generator=g, dtype=bf)
+    k = torch.randn(T, HKV, D, device=DEV, generator=g, dtype=bf)
+    v = torch.randn(T, HKV, D, device=DEV, generator=g, dtype=bf)
+    kp = torch.randn(Lp, HKV, D, device=DEV, generator=g, dtype=bf)
+    vp = torch.randn(Lp, HKV, D, device=DEV, generator=g, dtype=bf)
+    do = torch.randn(T, HQ, D, device=DEV, generator=g, dtype=bf)
+    scale = D ** -0.5
+    view = lambda x: x[None].transpose(1, 2)
+    plan = KeyPlan(TreeMetaDevice(lens, par, device=DEV).horizon, torch.zeros(Lp, device=DEV))
+    o, lse = attn_forward(view(q), view(k), view(v), plan, scale, view(kp), view(vp))
+    outs = []
+    for det in (True, True, False):
+        acc = (torch.zeros(Lp, HKV, D, device=DEV), torch.zeros(Lp, HKV, D, device=DEV))
+        dq, dk, dv = attn_backward(view(q), view(k), view(v), plan, scale, o, lse, do[None], view(kp), view(vp),
+                                   acc, deterministic=det)
+        outs.append((dq, dk, dv, acc[0], acc[1]))
+        print(f"agent16k + gateway {Lp}: backward deterministic={det} done", flush=True)
+    torch.cuda.synchronize()
+    names = ("dq", "dk", "dv", "dk_past", "dv_past")
+    for name, a, b, c in zip(names, *outs):
+        assert torch.equal(a, b), f"{name}: two deterministic runs differ"
+        assert torch.isfinite(a.float()).all(), name
+        assert _max_rel(c.float(), a.float()) < 1e-2, name

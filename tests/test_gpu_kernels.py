@@ -212,7 +212,7 @@ def _qkv(T, Lp, dtype, seed):
     return q, k, v, do, kp, vp
 
 
-def _run(lens, par, dtype, seed=0, past_vis=None, parts=(0,)):
+def _run(lens, par, dtype, seed=0, past_vis=None, parts=(0,), deterministic=None):
     from tree_training_amd.attention import attn_backward, attn_forward
     from tree_training_amd.meta import KeyPlan
     T = sum(lens)
@@ -230,7 +230,7 @@ def _run(lens, par, dtype, seed=0, past_vis=None, parts=(0,)):
         acc = (torch.zeros(Lp, HKV, D, device=DEV), torch.zeros(Lp, HKV, D, device=DEV))
     o, lse = attn_forward(tr(q), tr(k), tr(v), plan, scale, tr(kp), tr(vp))
     dq, dk, dv = attn_backward(tr(q), tr(k), tr(v), plan, scale, o, lse, do.to(DEV), tr(kp), tr(vp), acc,
-                               parts=parts)
+                               parts=parts, deterministic=deterministic)
     torch.cuda.synchronize()
     # oracle on the same (rounded) inputs, fp64
     cf = meta_closed_form(lens, par)
@@ -323,6 +323,29 @@ def test_attention_backward_parts(parts, dtype):
         if name == "lse":
             continue
         check_close(name, ref, got, tol)
+
+
+@pytest.mark.parametrize("case", ["long_prompt", "gateway_split", "gateway_split_parts"])
+def test_attention_deterministic_bf16(case):
+    """TT_BWD_DETERMINISTIC: keys whose query range is split over several
+    dK/dV work items (own keys of the long prompt; gateway keys seen by every
+    query) sum their partials in work-item order, so two backwards of the same
+    inputs are bitwise equal, and both match the fp64 oracle."""
+    past_vis, parts = None, (0,)
+    if case == "long_prompt":
+        lens, par = CASES["long_prompt"]
+    else:
+        lens, par = [2400, 1500, 1400], [-1, 0, 0]
+        past_vis = [bool(x) for x in (np.random.default_rng(8).random(300) < 0.6)]
+        if case == "gateway_split_parts":
+            parts = (3, 4)
+    say(f"attention deterministic case={case} T={sum(lens)}")
+    runs = [_run(lens, par, torch.bfloat16, seed=21, past_vis=past_vis, parts=parts, deterministic=True)
+            for _ in range(2)]
+    for name, (ref, got) in runs[0].items():
+        assert np.array_equal(got, runs[1][name][1]), f"{name}: two deterministic runs differ"
+        if name != "lse":
+            check_close(name, ref, got, TOL[torch.bfloat16])
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])

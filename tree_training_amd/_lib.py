@@ -23,6 +23,7 @@ TT_DTYPE_BF16 = 1
 TT_BWD_DELTA = 1
 TT_BWD_DQ = 2
 TT_BWD_DKDV = 4
+TT_BWD_DETERMINISTIC = 8
 TT_STATUS_BAD_LEN = 1
 TT_STATUS_BAD_PARENT = 2
 TT_STATUS_BAD_TOTAL = 4

@@ -23,7 +23,8 @@ from typing import Optional, Tuple
 
 import torch
 
-from ._lib import (TT_DTYPE_BF16, TT_DTYPE_F32, TreeAttnError, TTAttnProblem, TTTensor, check, lib)
+from ._lib import (TT_BWD_DETERMINISTIC, TT_DTYPE_BF16, TT_DTYPE_F32, TreeAttnError, TTAttnProblem, TTTensor,
+                   check, lib)
 from .meta import KeyPlan, _ptr, _stream
 
 _DTYPES = {torch.bfloat16: TT_DTYPE_BF16, torch.float32: TT_DTYPE_F32}
@@ -106,11 +107,17 @@ def attn_forward(q, k, v, plan: KeyPlan, scale: float, k_past=None, v_past=None)
 
 
 def attn_backward(q, k, v, plan: KeyPlan, scale: float, o, lse, d_o, k_past=None, v_past=None,
-                  gate_acc=None, parts=(0,)):
+                  gate_acc=None, parts=(0,), deterministic: Optional[bool] = None):
     """Returns (dq [N,Hq,D], dk [N,Hkv,D], dv [N,Hkv,D]); gateway grads are
     added to ``gate_acc`` when given. ``parts``: the ``bwd_parts`` of one
-    ``tt_attn_bwd`` call each, run in order (default: one call, every part)."""
+    ``tt_attn_bwd`` call each, run in order (default: one call, every part).
+    ``deterministic`` (default: ``torch.are_deterministic_algorithms_enabled()``)
+    adds TT_BWD_DETERMINISTIC: bitwise-repeatable bf16 dk/dv and gateway sums."""
+    if deterministic is None:
+        deterministic = torch.are_deterministic_algorithms_enabled()
+    det = TT_BWD_DETERMINISTIC if deterministic else 0
     pb = _Problem(q, k, v, k_past, v_past, plan, scale)
+    pb.s.bwd_parts = det
     dev = q.device
     d_o = d_o.reshape(1, pb.N, pb.Hq, pb.D) if d_o.dim() != 4 else d_o
     d_o, dst, dsh = _tok_view(d_o)
@@ -126,7 +133,7 @@ def attn_backward(q, k, v, plan: KeyPlan, scale: float, o, lse, d_o, k_past=None
             if a.dtype != torch.float32 or not a.is_contiguous() or a.numel() != pb.n_past * pb.Hkv * pb.D:
                 raise TreeAttnError("gateway accumulators must be contiguous float32 [Lp, Hkv, D]")
     for part in parts:
-        pb.s.bwd_parts = part
+        pb.s.bwd_parts = part | det
         rc = lib().tt_attn_bwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), TTTensor(d_o.data_ptr(), dst, dsh),
                                _ptr(dq), _ptr(dk), _ptr(dv), _ptr(acc_k), _ptr(acc_v), _ptr(ws), ws_bytes,
                                _stream(dev))

@@ -142,16 +142,26 @@ int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* stream) {
 
 // Workspace: delta [Hq, n_q] fp32, then (bf16 problems) the fp32 dK and dV
 // sums of key tiles whose query range is split over several work items,
-// [n_keys, Hkv, head_dim] each.
+// [n_keys, Hkv, head_dim] each, then (bf16, TT_BWD_DETERMINISTIC) the dK and
+// dV slots of those tiles' later items, [tt_det_slots, 128, Hkv, head_dim] each.
 static size_t delta_bytes(const tt_attn_problem* p) {
     return ((size_t)p->n_heads_q * (size_t)p->n_q * sizeof(float) + 255) & ~(size_t)255;
+}
+static size_t split_rows_bytes(const tt_attn_problem* p) {
+    return (size_t)(p->n_q + p->n_past) * (size_t)p->n_heads_kv * 128 * sizeof(float);
+}
+static size_t det_slot_bytes(const tt_attn_problem* p) {
+    return (size_t)tt_det_slots(p->n_q, p->n_q + p->n_past) * TT_BKB * (size_t)p->n_heads_kv * 128 * sizeof(float);
 }
 
 size_t tt_attn_bwd_workspace_bytes(const tt_attn_problem* p) {
     if (!p || p->n_q < 1 || p->n_heads_q < 1 || p->n_heads_kv < 1 || p->n_past < 0) return 0;
+    if ((int64_t)p->n_q + p->n_past > 0x3fffffff) return 0;
     size_t b = delta_bytes(p);
-    if (p->dtype == TT_DTYPE_BF16)
-        b += 2 * (size_t)(p->n_q + p->n_past) * (size_t)p->n_heads_kv * 128 * sizeof(float);
+    if (p->dtype == TT_DTYPE_BF16) {
+        b += 2 * split_rows_bytes(p);
+        if (p->bwd_parts & TT_BWD_DETERMINISTIC) b += 2 * det_slot_bytes(p);
+    }
     return b;
 }
 
@@ -183,13 +193,20 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
     b.dk_acc = p->n_past > 0 ? dk_past_acc : nullptr;
     b.dv_acc = p->n_past > 0 ? dv_past_acc : nullptr;
     b.delta = reinterpret_cast<float*>(ws);
-    b.dk_ws = b.dv_ws = nullptr;
+    if (p->bwd_parts & ~(TT_BWD_DELTA | TT_BWD_DQ | TT_BWD_DKDV | TT_BWD_DETERMINISTIC)) return TT_E_ARG;
+    b.det = (p->bwd_parts & TT_BWD_DETERMINISTIC) ? 1 : 0;
+    b.dk_ws = b.dv_ws = b.dk_slot = b.dv_slot = nullptr;
     if (p->dtype == TT_DTYPE_BF16) {
-        b.dk_ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + delta_bytes(p));
-        b.dv_ws = b.dk_ws + (size_t)a.n_keys * a.hkv * 128;
+        uint8_t* w = reinterpret_cast<uint8_t*>(ws) + delta_bytes(p);
+        b.dk_ws = reinterpret_cast<float*>(w);
+        b.dv_ws = reinterpret_cast<float*>(w + split_rows_bytes(p));
+        if (b.det) {
+            b.dk_slot = reinterpret_cast<float*>(w + 2 * split_rows_bytes(p));
+            b.dv_slot = reinterpret_cast<float*>(w + 2 * split_rows_bytes(p) + det_slot_bytes(p));
+        }
     }
-    if (p->bwd_parts & ~(TT_BWD_DELTA | TT_BWD_DQ | TT_BWD_DKDV)) return TT_E_ARG;
-    b.parts = p->bwd_parts ? p->bwd_parts : (TT_BWD_DELTA | TT_BWD_DQ | TT_BWD_DKDV);
+    const int parts = p->bwd_parts & (TT_BWD_DELTA | TT_BWD_DQ | TT_BWD_DKDV);
+    b.parts = parts ? parts : (TT_BWD_DELTA | TT_BWD_DQ | TT_BWD_DKDV);
     if (p->dtype == TT_DTYPE_BF16) return tt_bwd_bf16_launch(a, b, (hipStream_t)stream);
     return tt_bwd_f32_launch(a, b, (hipStream_t)stream);
 }

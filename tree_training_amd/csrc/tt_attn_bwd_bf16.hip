@@ -364,7 +364,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
             }
         }
 
-        // Epilogue: rows of dk/dv = this wave's keys, columns = d.
+        // Epilogue: rows of dk/dv = this wave's keys, columns = d. In the
+        // deterministic mode a split tile's first item stores its partial sums
+        // in the fp32 rows and each later item in its own slot (item - rank - 1
+        // counts the items before it that are not the first of their tile);
+        // the finalize pass adds them in item order.
+        const bool det_split = split && bw.det;
+        float* const sk = chunk == 0 ? bw.dk_ws : bw.dk_slot;
+        float* const sv = chunk == 0 ? bw.dv_ws : bw.dv_slot;
+        const int64_t srow = chunk == 0 ? 0 : (int64_t)(item - lo_r - 1) * TT_BKB - kb * TT_BKB;
         const int kbase = kb * TT_BKB + wave * 32;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -375,7 +383,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
                 const int d = 32 * db + col;
                 const float gk = dk[db][r] * a.scale, gv = dv[db][r];
                 const size_t widx = ((size_t)key * a.hkv + g) * D + d;
-                if (key < a.n_past) {   // gateway key: fp32, added to the caller's accumulators
+                if (det_split) {
+                    const size_t sidx = ((size_t)(srow + key) * a.hkv + g) * D + d;
+                    sk[sidx] = gk;
+                    sv[sidx] = gv;
+                } else if (key < a.n_past) {   // gateway key: fp32, added to the caller's accumulators
                     if (bw.dk_acc) {
                         if (split) {
                             atomicAdd(bw.dk_acc + widx, gk);
@@ -424,6 +436,44 @@ __global__ __launch_bounds__(256) void bwd_split_finalize_kernel(AttnDev a, BwdD
         const int key = k_first + e / (D / 4), d = 4 * (e % (D / 4));
         const size_t widx = ((size_t)key * a.hkv + g) * D + d;
         const f32x4 gk = *(const f32x4*)(bw.dk_ws + widx), gv = *(const f32x4*)(bw.dv_ws + widx);
+        const size_t idx = ((size_t)(key - a.n_past) * a.hkv + g) * D + d;
+        bf16x4 wk, wv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            wk[i] = (bf16)gk[i];
+            wv[i] = (bf16)gv[i];
+        }
+        *(bf16x4*)((bf16*)bw.dk + idx) = wk;
+        *(bf16x4*)((bf16*)bw.dv + idx) = wv;
+    }
+}
+
+// Deterministic mode: one workgroup per (key tile rank, kv head) sums a split
+// tile's partials in item order (first item's in the fp32 rows, then the
+// slots) and writes dk/dv, or adds gateway keys' sums to the accumulators.
+__global__ __launch_bounds__(256) void bwd_split_finalize_det_kernel(AttnDev a, BwdDev bw) {
+    const int rank = blockIdx.x, g = blockIdx.y;
+    const int kb = a.kb_order[rank];
+    const int m = tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb], tt_qch(a.n_q));
+    if (m <= 1) return;
+    const int k_first = kb * TT_BKB, k_end = min(kb * TT_BKB + TT_BKB, a.n_keys);
+    const int64_t slot0 = (int64_t)(a.kb_base[rank] - rank) * TT_BKB;   // slot rows of the tile's second item
+    for (int e = threadIdx.x; e < (k_end - k_first) * (D / 4); e += 256) {
+        const int key = k_first + e / (D / 4), d = 4 * (e % (D / 4));
+        const size_t widx = ((size_t)key * a.hkv + g) * D + d;
+        f32x4 gk = *(const f32x4*)(bw.dk_ws + widx), gv = *(const f32x4*)(bw.dv_ws + widx);
+        for (int c = 1; c < m; ++c) {
+            const size_t sidx = ((size_t)(slot0 + (int64_t)(c - 1) * TT_BKB + key - k_first) * a.hkv + g) * D + d;
+            gk += *(const f32x4*)(bw.dk_slot + sidx);
+            gv += *(const f32x4*)(bw.dv_slot + sidx);
+        }
+        if (key < a.n_past) {
+            if (bw.dk_acc) {
+                *(f32x4*)(bw.dk_acc + widx) += gk;
+                *(f32x4*)(bw.dv_acc + widx) += gv;
+            }
+            continue;
+        }
         const size_t idx = ((size_t)(key - a.n_past) * a.hkv + g) * D + d;
         bf16x4 wk, wv;
 #pragma unroll
@@ -486,9 +536,14 @@ int tt_bwd_bf16_launch(const AttnDev& a, const BwdDev& b, hipStream_t s) {
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     if (b.parts & TT_BWD_DKDV) {
-        hipLaunchKernelGGL(bwd_split_zero_kernel, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
-        hipLaunchKernelGGL(bwd_dkdv_bf16_kernel, dim3(dkdv_grid(a)), dim3(256), 0, s, a, b);
-        hipLaunchKernelGGL(bwd_split_finalize_kernel, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
+        if (b.det) {
+            hipLaunchKernelGGL(bwd_dkdv_bf16_kernel, dim3(dkdv_grid(a)), dim3(256), 0, s, a, b);
+            hipLaunchKernelGGL(bwd_split_finalize_det_kernel, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
+        } else {
+            hipLaunchKernelGGL(bwd_split_zero_kernel, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
+            hipLaunchKernelGGL(bwd_dkdv_bf16_kernel, dim3(dkdv_grid(a)), dim3(256), 0, s, a, b);
+            hipLaunchKernelGGL(bwd_split_finalize_kernel, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
+        }
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     return TT_OK;

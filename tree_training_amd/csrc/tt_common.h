@@ -49,6 +49,12 @@ __host__ __device__ inline int tt_kb_items(int qlo, int qhi, int qch) {
     if (qhi - qlo <= qch) return 1;
     return (qhi - 1) / qch - qlo / qch + 1;
 }
+// Upper bound on the dK/dV work items beyond the first of each key tile
+// (n_kb tiles): a tile's items never exceed (n_q - 1) / qch + 1, whatever its
+// visible range. The deterministic backward keeps one partial-sum slot for each.
+__host__ __device__ inline int64_t tt_det_slots(int n_q, int n_keys) {
+    return (int64_t)tt_cdiv(n_keys, TT_BKB) * ((n_q - 1) / tt_qch(n_q));
+}
 // Query range [q_start, q_stop) of item `item`; q_start is a multiple of TT_BQB.
 __host__ __device__ inline void tt_kb_item_range(int qlo, int qhi, int qch, int item, int& q_start, int& q_stop) {
     q_start = q_stop = 0;

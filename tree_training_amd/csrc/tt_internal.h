@@ -39,7 +39,10 @@ struct BwdDev {
     float* delta;             // workspace [hq, n_q]: rowsum(dO * O)
     float* dk_ws;             // workspace [n_keys, hkv, 128] fp32: split key tiles' dK
     float* dv_ws;             // workspace [n_keys, hkv, 128] fp32: split key tiles' dV
-    int parts;                // OR of TT_BWD_* (never 0 here)
+    float* dk_slot;           // deterministic mode: [tt_det_slots, 128, hkv, 128] fp32, chunks >= 1
+    float* dv_slot;           //   of split key tiles (null otherwise)
+    int parts;                // OR of TT_BWD_DELTA / _DQ / _DKDV (never 0 here)
+    int det;                  // TT_BWD_DETERMINISTIC given (bf16: split tiles summed in chunk order)
 };
 
 // Device-side view of a tt_gdn_problem.
