@@ -64,6 +64,20 @@ def profiled_traffic(kernel, workload):
     return None
 
 
+def profiled_step_traffic(profile):
+    """HBM bytes per step of the library's kernels, from a committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (its "**N bytes**" total);
+    None when the summary is absent."""
+    import re
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", profile)
+    try:
+        with open(path) as f:
+            m = re.search(r"\*\*(\d+) bytes\*\*", f.read())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -561,7 +575,10 @@ def run_gdn(args):
                                                  "kernels); fp32 products (scans and state products on fp32 MFMA, "
                                                  "the rest on the vector ALUs), ceiling = fp32 peak",
                      "achieved": round(tfs, 2), "peak": PEAK_FP32_TFS, "unit": "TFLOP/s",
-                     "frac": round(tfs / PEAK_FP32_TFS, 5), "traffic": None, "flops_per_step": flops},
+                     "frac": round(tfs / PEAK_FP32_TFS, 5),
+                     "traffic": profiled_step_traffic("gdn16k_counters.md"),
+                     "traffic_unit": "HBM bytes per step, library kernels (rocprofv3 FETCH_SIZE / WRITE_SIZE, "
+                                     "copy-calibrated)", "flops_per_step": flops},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
