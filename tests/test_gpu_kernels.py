@@ -153,6 +153,39 @@ def _plan_expected(lo, hi, n_q):
                 kb_order=kb_order, kb_base=kb_base)
 
 
+def _plan_expected_fast(lo, hi, n_q):
+    """_plan_expected vectorised over the query blocks (one numpy pass per
+    64-key tile), for trees too large for the per-pair loop."""
+    lo, hi = np.asarray(lo, np.int64), np.asarray(hi, np.int64)
+    n_keys = len(lo)
+    n_qb, n_kt, n_kb = -(-n_q // 128), -(-n_keys // 64), -(-n_keys // 128)
+    a, b = np.maximum(lo, 0), np.minimum(hi, n_q)
+    i0 = 128 * np.arange(n_qb)
+    i1 = np.minimum(i0 + 128, n_q)
+    cls = np.zeros((n_qb, n_kt), np.int64)
+    for kt in range(n_kt):
+        j = np.arange(64 * kt, min(64 * kt + 64, n_keys))
+        some = (np.maximum(lo[j][:, None], i0[None]) < np.minimum(hi[j][:, None], i1[None])).any(0)
+        every = ((lo[j][:, None] <= i0[None]) & (hi[j][:, None] >= i1[None])).all(0) & (len(j) == 64)
+        cls[:, kt] = np.where(some, np.where(every, 2, 1), 0)
+    rows = [[(int(kt) << 1) | int(cls[q, kt] == 2) for kt in np.nonzero(cls[q])[0]] for q in range(n_qb)]
+    cnt = (cls != 0).sum(1)
+    row_order = sorted(range(n_qb), key=lambda i: (-cnt[i], i))
+    qlo, qhi = np.zeros(n_kb, np.int64), np.zeros(n_kb, np.int64)
+    for kb in range(n_kb):
+        j = np.arange(128 * kb, min(128 * kb + 128, n_keys))
+        vis = a[j] < b[j]
+        if vis.any():
+            qlo[kb], qhi[kb] = a[j][vis].min(), b[j][vis].max()
+    kb_order = sorted(range(n_kb), key=lambda i: (-(qhi[i] - qlo[i]), i))
+    half = (1 << (n_q.bit_length() - 1)) // 2 if n_q >= 2 else 0
+    qch = 4096 if half > 4096 else max(half, 256)
+    items = [1 if qhi[k] - qlo[k] <= qch else (qhi[k] - 1) // qch - qlo[k] // qch + 1 for k in kb_order]
+    kb_base = np.concatenate([[0], np.cumsum(items)])
+    return dict(P=int(np.clip(b - a, 0, None).sum()), n_qb=n_qb, n_kt=n_kt, n_kb=n_kb, rows=rows,
+                row_order=row_order, qlo=qlo, qhi=qhi, kb_order=kb_order, kb_base=kb_base)
+
+
 def _plan_decode(buf, n_q, n_keys):
     """The device plan buffer split at PlanLayout's offsets (64-byte header)."""
     n_qb, n_kt, n_kb = -(-n_q // 128), -(-n_keys // 64), -(-n_keys // 128)
@@ -172,16 +205,21 @@ def _plan_decode(buf, n_q, n_keys):
                 qlo=qlo, qhi=qhi, kb_order=list(kb_order), kb_base=kb_base)
 
 
-@pytest.mark.parametrize("case", ["forest", "agent16k", "gateway"])
+@pytest.mark.parametrize("case", ["forest", "agent16k", "gateway", "rollout270k"])
 def test_plan_matches_numpy(case):
     """Every field of the device tile plan equals the numpy restatement
-    (bit-exact: it is index work)."""
+    (bit-exact: it is index work). Up to 2048 query blocks and key tiles the
+    plan's last passes run as one workgroup; the 270K-token rollout (2112 of
+    each, and more than 65536 tokens for the metadata) takes the multi-launch
+    paths."""
     from tree_training_amd.meta import KeyPlan
     bias = None
     if case == "forest":
         lens, par = workloads.random_forest(4, node_len=(1, 300))
     elif case == "agent16k":
         lens, par = workloads.agent_tree(0)
+    elif case == "rollout270k":
+        lens, par = [8192] + [1024] * 256, [-1] + [0] * 256
     else:
         lens, par = [700, 500, 300], [-1, 0, 0]
         vis = np.random.default_rng(3).random(1300) < 0.7
@@ -191,7 +229,19 @@ def test_plan_matches_numpy(case):
     plan = KeyPlan(m.horizon, bias, validate=True)
     n_q, n_keys = plan.n_q, plan.n_keys
     got = _plan_decode(plan.plan.cpu().numpy().tobytes(), n_q, n_keys)
-    exp = _plan_expected(plan.key_lo.cpu().numpy(), plan.key_hi.cpu().numpy(), n_q)
+    lo, hi = plan.key_lo.cpu().numpy(), plan.key_hi.cpu().numpy()
+    exp = _plan_expected_fast(lo, hi, n_q)
+    if n_q < 20000:   # the vectorised restatement against the per-pair loop
+        ref = _plan_expected(lo, hi, n_q)
+        for k in ("P", "rows", "row_order", "kb_order"):
+            assert exp[k] == ref[k], k
+        for k in ("qlo", "qhi", "kb_base"):
+            assert np.array_equal(exp[k], ref[k]), k
+    if case == "rollout270k":
+        ref = meta_closed_form(lens, par)
+        assert np.array_equal(m.pos.cpu().numpy(), ref["pos"])
+        assert np.array_equal(m.horizon.cpu().numpy(), ref["horizon"])
+        assert exp["n_qb"] > 2048 and exp["n_kb"] > 2048 and n_q > 65536
     for k in ("P", "n_qb", "n_kt", "n_kb", "rows", "row_order", "kb_order"):
         assert got[k] == exp[k], k
     for k in ("qlo", "qhi", "kb_base"):

@@ -20,7 +20,10 @@ __host__ __device__ inline int sparse_levels(int n) {
     return L;
 }
 
-__global__ __launch_bounds__(kNodeThreads) void meta_nodes_kernel(
+// Node-level metadata in one workgroup of kNodeThreads threads; ends with a
+// barrier after which start, off and hend of every node are visible to the
+// whole workgroup.
+__device__ __forceinline__ void meta_nodes_body(
     const int32_t* __restrict__ len, const int32_t* __restrict__ par, int n, int T,
     int32_t* __restrict__ start, int32_t* __restrict__ off, int32_t* __restrict__ hend,
     int32_t* __restrict__ status, int32_t* __restrict__ ws) {
@@ -137,6 +140,35 @@ __global__ __launch_bounds__(kNodeThreads) void meta_nodes_kernel(
     }
     __syncthreads();
     if (tid == 0 && s_err) atomicOr(status, s_err);
+}
+
+__global__ __launch_bounds__(kNodeThreads) void meta_nodes_kernel(
+    const int32_t* __restrict__ len, const int32_t* __restrict__ par, int n, int T,
+    int32_t* __restrict__ start, int32_t* __restrict__ off, int32_t* __restrict__ hend,
+    int32_t* __restrict__ status, int32_t* __restrict__ ws) {
+    meta_nodes_body(len, par, n, T, start, off, hend, status, ws);
+}
+
+// Nodes and tokens in one launch (trees of up to kFusedTokens tokens): after
+// the node work, each wave writes the tokens of every 16th node, its lanes
+// 64 consecutive tokens at a time (no per-token search).
+constexpr int kFusedTokens = 1 << 16;
+__global__ __launch_bounds__(kNodeThreads) void meta_tree_kernel(
+    const int32_t* __restrict__ len, const int32_t* __restrict__ par, int n, int T, int pos_offset,
+    int32_t* __restrict__ start, int32_t* __restrict__ off, int32_t* __restrict__ hend,
+    int32_t* __restrict__ pos, int32_t* __restrict__ node_of, int32_t* __restrict__ horizon,
+    int32_t* __restrict__ status, int32_t* __restrict__ ws) {
+    meta_nodes_body(len, par, n, T, start, off, hend, status, ws);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int c = wave; c < n; c += kNodeThreads / 64) {
+        // a node outside [0, T) (bad lengths, flagged in status) writes nothing
+        const int s0 = start[c], e0 = min(s0 + max(len[c], 0), T), o = pos_offset + off[c], h = hend[c];
+        for (int i = max(s0, 0) + lane; i < e0; i += 64) {
+            pos[i] = o + (i - s0);
+            if (node_of) node_of[i] = c;
+            horizon[i] = h;
+        }
+    }
 }
 
 __global__ void meta_tokens_kernel(const int32_t* __restrict__ start, const int32_t* __restrict__ off,
@@ -372,6 +404,102 @@ __global__ __launch_bounds__(1024) void plan_kb_base_kernel(const int32_t* __res
     }
 }
 
+// Plan passes 2-4 in one workgroup (plans of up to kFinishMax query blocks and
+// key tiles): compaction of every query block's tile list (a wave per block),
+// both heaviest-first orders (a thread per block / tile), then the work-item
+// scan and the header, with the counts and the key-tile order kept in LDS.
+constexpr int kFinishMax = 2048;
+__global__ __launch_bounds__(1024) void plan_finish_kernel(const uint8_t* __restrict__ cls, int n_qb, int n_kt,
+                                                           const int32_t* __restrict__ kb_qlo,
+                                                           const int32_t* __restrict__ kb_qhi, int n_kb, int qch,
+                                                           const unsigned long long* __restrict__ pair_part, int n_pb,
+                                                           int32_t* __restrict__ row_cnt, int32_t* __restrict__ row_list,
+                                                           int32_t* __restrict__ row_order,
+                                                           int32_t* __restrict__ kb_order,
+                                                           int32_t* __restrict__ kb_base, uint8_t* __restrict__ plan) {
+    __shared__ int s_cnt[kFinishMax];
+    __shared__ int s_kbo[kFinishMax];
+    __shared__ int s_scan[1024];
+    __shared__ int s_carry;
+    __shared__ unsigned long long s_pairs;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if (tid == 0) {
+        s_carry = 0;
+        s_pairs = 0;
+    }
+    // compaction: a wave per query block
+    const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int row = wave; row < n_qb; row += 16) {
+        int cnt = 0;
+        for (int base = 0; base < n_kt; base += 64) {
+            const int kt = base + lane;
+            const int c = kt < n_kt ? cls[(size_t)row * n_kt + kt] : 0;
+            const unsigned long long m = __ballot(c != 0);
+            if (c) row_list[(size_t)row * n_kt + cnt + __popcll(m & below)] = (kt << 1) | (c == 2 ? 1 : 0);
+            cnt += __popcll(m);
+        }
+        if (lane == 0) {
+            s_cnt[row] = cnt;
+            row_cnt[row] = cnt;
+        }
+    }
+    __syncthreads();
+    // orders: rank = number of heavier entries (ties by index)
+    for (int i = tid; i < n_qb; i += 1024) {
+        const int c = s_cnt[i];
+        int rank = 0;
+        for (int j = 0; j < n_qb; ++j) {
+            const int cj = s_cnt[j];
+            rank += (cj > c) || (cj == c && j < i);
+        }
+        row_order[rank] = i;
+    }
+    for (int i = tid; i < n_kb; i += 1024) {
+        const int c = kb_qhi[i] - kb_qlo[i];
+        int rank = 0;
+        for (int j = 0; j < n_kb; ++j) {
+            const int cj = kb_qhi[j] - kb_qlo[j];
+            rank += (cj > c) || (cj == c && j < i);
+        }
+        s_kbo[rank] = i;
+        kb_order[rank] = i;
+    }
+    unsigned long long pairs = 0;
+    for (int i = tid; i < n_pb; i += 1024) pairs += pair_part[i];
+    atomicAdd(&s_pairs, pairs);
+    __syncthreads();
+    // work-item offsets of the ordered key tiles
+    for (int base = 0; base < n_kb; base += 1024) {
+        const int r = base + tid;
+        int v = 0;
+        if (r < n_kb) {
+            const int kb = s_kbo[r];
+            v = tt_kb_items(kb_qlo[kb], kb_qhi[kb], qch);
+        }
+        s_scan[tid] = v;
+        __syncthreads();
+        for (int o = 1; o < 1024; o <<= 1) {
+            const int t = tid >= o ? s_scan[tid - o] : 0;
+            __syncthreads();
+            s_scan[tid] += t;
+            __syncthreads();
+        }
+        if (r < n_kb) kb_base[r] = s_carry + s_scan[tid] - v;
+        __syncthreads();
+        if (tid == 1023) s_carry += s_scan[tid];
+        __syncthreads();
+    }
+    if (tid == 0) {
+        kb_base[n_kb] = s_carry;
+        *reinterpret_cast<unsigned long long*>(plan) = s_pairs;
+        int32_t* hdr = reinterpret_cast<int32_t*>(plan);
+        hdr[2] = n_qb;
+        hdr[3] = n_kt;
+        hdr[4] = n_kb;
+        hdr[5] = s_carry;
+    }
+}
+
 }  // namespace
 
 size_t tt_meta_ws_bytes_impl(int n) {
@@ -382,6 +510,11 @@ size_t tt_meta_ws_bytes_impl(int n) {
 int tt_meta_build_impl(const int32_t* len, const int32_t* par, int n, int T, int pos_offset,
                        int32_t* start, int32_t* off, int32_t* hend, int32_t* pos, int32_t* node_of,
                        int32_t* horizon, int32_t* status, void* ws, hipStream_t s) {
+    if (T <= kFusedTokens) {
+        hipLaunchKernelGGL(meta_tree_kernel, dim3(1), dim3(kNodeThreads), 0, s, len, par, n, T, pos_offset, start,
+                           off, hend, pos, node_of, horizon, status, reinterpret_cast<int32_t*>(ws));
+        return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
+    }
     hipLaunchKernelGGL(meta_nodes_kernel, dim3(1), dim3(kNodeThreads), 0, s, len, par, n, T, start, off,
                        hend, status, reinterpret_cast<int32_t*>(ws));
     if (hipGetLastError() != hipSuccess) return TT_E_HIP;
@@ -423,6 +556,11 @@ int tt_plan_build_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys,
     const int nb_cls = tt_cdiv(L.n_qb * L.n_kt, 4), nb_kv = tt_cdiv(L.n_kb, 4);
     hipLaunchKernelGGL(plan_keys_pass_kernel, dim3(nb_cls + nb_kv + L.n_pb), dim3(256), 0, s, key_lo, key_hi, n_keys,
                        n_q, L.n_qb, L.n_kt, L.n_kb, nb_cls, nb_kv, cls, kb_qlo, kb_qhi, pair_part);
+    if (L.n_qb <= kFinishMax && L.n_kb <= kFinishMax) {
+        hipLaunchKernelGGL(plan_finish_kernel, dim3(1), dim3(1024), 0, s, cls, L.n_qb, L.n_kt, kb_qlo, kb_qhi, L.n_kb,
+                           tt_qch(n_q), pair_part, L.n_pb, row_cnt, row_list, row_order, kb_order, kb_base, base);
+        return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
+    }
     hipLaunchKernelGGL(plan_compact_kernel, dim3(tt_cdiv(L.n_qb, 4)), dim3(256), 0, s, cls, L.n_qb, L.n_kt,
                        row_cnt, row_list);
     const int nb_ro = tt_cdiv(L.n_qb, 256);
