@@ -19,7 +19,8 @@ on a bounded sample on the host cores.
                     [--workload agent16k|gateway16k|rollout48k|gdn16k|prologue16k|leafce16k]
 
 Other workloads, each on the same 16K tree unless named:
-  gateway16k   the tree cut into 4096-token partitions (tree_grad_hybrid), each
+  gateway16k   the tree cut into 4096-token partitions (tree_grad_hybrid): every
+               partition's metadata and plan in one batched build, then each
                partition's attention fwd+bwd over its gateway prefix;
   rollout48k   one 8K prompt with 64 leaves (50,109 tokens);
   gdn16k       one GDN layer core (tree conv + gated-delta-rule scan) fwd+bwd,
@@ -125,7 +126,7 @@ def main():
     import torch
     from tree_training_amd import _lib
     from tree_training_amd.attention import _Problem, attn_forward
-    from tree_training_amd.meta import KeyPlan, TreeMetaDevice, _ptr, _stream
+    from tree_training_amd.meta import KeyPlan, TreeMetaDevice, _ptr, _stream, build_trees
     from tree_training_amd.workloads import visible_pairs
     import ctypes
 
@@ -163,9 +164,11 @@ def main():
                 seg["bias_dev"] = seg["bias"].to(dev)
             segments.append(seg)
 
-    def run_problem(lens_, par_, qq, kk, vv, dd, kp=None, vp=None, bias=None, acc=None, ev=None, pos_off=0):
-        meta = TreeMetaDevice(lens_, par_, pos_offset=pos_off, device=dev)
-        plan = KeyPlan(meta.horizon, bias)
+    def run_problem(lens_, par_, qq, kk, vv, dd, kp=None, vp=None, bias=None, acc=None, ev=None, pos_off=0,
+                    plan=None):
+        if plan is None:
+            meta = TreeMetaDevice(lens_, par_, pos_offset=pos_off, device=dev)
+            plan = KeyPlan(meta.horizon, bias)
         pb = _Problem(qq, kk, vv, kp, vp, plan, scale)
         N = pb.N
         o = torch.empty((N, HQ, D), dtype=bf, device=dev)
@@ -203,10 +206,14 @@ def main():
         if segments is None:
             run_problem(lens, par, q, k, v, do, ev=ev)
             return
-        for seg in segments:   # partitions in creation order (parents first)
+        # every partition's metadata and plan in one batched build (topology only),
+        # as tree_grad_hybrid does, then the partitions in creation order
+        built = build_trees([(seg["node_len"], seg["parent"], seg["pos_offset"], seg.get("bias_dev"))
+                             for seg in segments], dev)
+        for seg, (_, plan) in zip(segments, built):
             run_problem(seg["node_len"], seg["parent"], seg["q"], seg["k"], seg["v"], seg["do"],
                         seg.get("kp"), seg.get("vp"), seg.get("bias_dev"), seg.get("acc"),
-                        ev=None, pos_off=seg["pos_offset"])
+                        ev=None, pos_off=seg["pos_offset"], plan=plan)
 
     if args.calibrate_copy_mb:
         src = torch.empty(args.calibrate_copy_mb << 20, dtype=torch.uint8, device=dev)

@@ -105,6 +105,39 @@ size_t tt_plan_bytes(int32_t n_q, int32_t n_keys);
 int tt_plan_build(const int32_t* key_lo, const int32_t* key_hi, int32_t n_keys, int32_t n_q,
                   void* plan, size_t plan_bytes, void* stream);
 
+/* ---- several trees in one call --------------------------------------------
+ * tt_meta_build + tt_keys_build + tt_plan_build for up to TT_TREE_JOBS_MAX
+ * trees in three launches in all: the per-partition DFS info and gateway
+ * masks of tree_grad_hybrid (_dfs_info_for_partition and the bias assembly,
+ * tree_grad_hybrid.py:102-153, :193-209, :312-317) for every partition of a
+ * step at once. Each job has the inputs and outputs of the three calls, with
+ * two differences: key_lo/key_hi are filled from the metadata directly, and
+ * *status is overwritten (not OR-ed; no zeroing needed). A job must have
+ * n_tokens <= 65536 and at most 2048 query blocks of 128 and key tiles of 128
+ * (n_past + n_tokens <= 262144); larger trees use the separate calls
+ * (TT_E_UNSUPPORTED). */
+#define TT_TREE_JOBS_MAX 16
+typedef struct tt_tree_job {
+    const int32_t* node_len;    /* [n_nodes], DFS pre-order as for tt_meta_build */
+    const int32_t* node_parent;
+    const float* past_bias;     /* [n_past] 0 or -inf; NULL when n_past == 0 */
+    int32_t* node_start;        /* [n_nodes] each */
+    int32_t* node_off;
+    int32_t* node_hend;
+    int32_t* pos;               /* [n_tokens] each; node_of may be NULL */
+    int32_t* node_of;
+    int32_t* horizon;
+    int32_t* key_lo;            /* [n_past + n_tokens] each */
+    int32_t* key_hi;
+    int32_t* status;            /* one int32, overwritten with the TT_STATUS_* bits */
+    void* plan;                 /* tt_plan_bytes(n_tokens, n_past + n_tokens) */
+    size_t plan_bytes;
+    void* ws;                   /* tt_meta_workspace_bytes(n_nodes) */
+    size_t ws_bytes;
+    int32_t n_nodes, n_tokens, pos_offset, n_past;
+} tt_tree_job;
+int tt_trees_build(const tt_tree_job* jobs, int32_t n_jobs, void* stream);
+
 /* ---- (2)+(3) tree-masked GQA attention -------------------------------------
  * Replaces repeat_kv + F.scaled_dot_product_attention(attn_mask=dense) and its
  * autograd backward (transformers integrations/sdpa_attention.py:79-175,

@@ -130,6 +130,44 @@ def test_bwd_noalloc_validation():
     assert lib.tt_attn_bwd_noalloc(ctypes.byref(big), V, V, d_o, V, V, V, None, None, None) == _lib.TT_E_WORKSPACE
 
 
+def _tree_job(**kw):
+    V = 16
+    j = _lib.TTTreeJob(**{n: V for n in ("node_len", "node_parent", "node_start", "node_off", "node_hend", "pos",
+                                        "node_of", "horizon", "key_lo", "key_hi", "status", "plan", "ws")})
+    j.past_bias = None
+    j.n_nodes, j.n_tokens, j.pos_offset, j.n_past = 2, 10, 0, 0
+    j.plan_bytes = _lib.lib().tt_plan_bytes(10, 10)
+    j.ws_bytes = _lib.lib().tt_meta_workspace_bytes(2)
+    for k, v in kw.items():
+        setattr(j, k, v)
+    return j
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(n_nodes=0), _lib.TT_E_ARG),
+    (dict(n_tokens=1), _lib.TT_E_ARG),                 # fewer tokens than nodes
+    (dict(n_past=5), _lib.TT_E_ARG),                   # gateway without a bias
+    (dict(pos=None), _lib.TT_E_ARG),
+    (dict(plan_bytes=8), _lib.TT_E_WORKSPACE),
+    (dict(ws_bytes=4), _lib.TT_E_WORKSPACE),
+    (dict(n_tokens=70000, n_nodes=1), _lib.TT_E_UNSUPPORTED),   # beyond one workgroup per tree
+])
+def test_trees_build_validation(kw, code):
+    """tt_trees_build checks every job on the host (no GPU call on these
+    paths): sizes, pointers, buffer sizes and the batched limits."""
+    lib = _lib.lib()
+    jobs = (_lib.TTTreeJob * 2)(_tree_job(), _tree_job(**kw))
+    assert lib.tt_trees_build(jobs, 2, None) == code
+
+
+def test_trees_build_job_count():
+    lib = _lib.lib()
+    jobs = (_lib.TTTreeJob * 17)(*[_tree_job() for _ in range(17)])
+    assert lib.tt_trees_build(jobs, 0, None) == _lib.TT_E_ARG
+    assert lib.tt_trees_build(jobs, 17, None) == _lib.TT_E_ARG
+    assert ctypes.sizeof(_lib.TTTreeJob) == 144
+
+
 def test_meta_and_plan_validation():
     lib = _lib.lib()
     V = ctypes.c_void_p(16)

@@ -205,6 +205,46 @@ def _plan_decode(buf, n_q, n_keys):
                 qlo=qlo, qhi=qhi, kb_order=list(kb_order), kb_base=kb_base)
 
 
+def test_build_trees_matches_separate_calls():
+    """meta.build_trees (tt_trees_build, three launches per 16 trees) gives
+    bit-for-bit the metadata, key intervals and plan of the separate calls
+    (tt_meta_build + tt_keys_build + tt_plan_build): 21 trees (two batches),
+    the 16K tree's hybrid partitions with their gateway biases, a bias with a
+    bad value (status bit), and a 70K-token tree beyond the batched limit."""
+    from tree_training_amd._lib import TT_STATUS_BAD_BIAS
+    from tree_training_amd.hybrid import hybrid_plan
+    from tree_training_amd.meta import KeyPlan, TreeMetaDevice, build_trees
+    from tree_training_amd.tree import TreeNode
+    specs = [(*workloads.random_forest(s, node_len=(1, 200)), 0, None) for s in range(12)]
+    roots, _ = workloads.forest_from_topology(workloads.agent_tree(0), TreeNode)
+    for pl in hybrid_plan(roots, 4096):
+        specs.append((pl["node_len"], pl["parent"], pl["pos_offset"],
+                      None if pl["bias"] is None else pl["bias"].to(DEV)))
+    bad = torch.zeros(40)
+    bad[3] = 1.0
+    specs.append(([30, 20], [-1, 0], 7, bad))
+    specs.append(([70000], [-1], 0, None))
+    say(f"build_trees: {len(specs)} trees")
+    built = build_trees(specs, DEV)
+    for i, ((nl, pa, po, pb), (meta, plan)) in enumerate(zip(specs, built)):
+        m2 = TreeMetaDevice(nl, pa, pos_offset=po, device=DEV)
+        p2 = KeyPlan(m2.horizon, pb)
+        for f in ("node_start", "node_off", "node_hend", "pos", "node_of", "horizon"):
+            assert torch.equal(getattr(meta, f), getattr(m2, f)), (i, f)
+        assert torch.equal(plan.key_lo, p2.key_lo) and torch.equal(plan.key_hi, p2.key_hi), i
+        n_q, n_keys = plan.n_q, plan.n_keys
+        a = _plan_decode(plan.plan.cpu().numpy().tobytes(), n_q, n_keys)
+        b = _plan_decode(p2.plan.cpu().numpy().tobytes(), n_q, n_keys)
+        for k in ("P", "n_qb", "n_kt", "n_kb", "n_items", "rows", "row_order", "kb_order"):
+            assert a[k] == b[k], (i, k)
+        for k in ("qlo", "qhi", "kb_base"):
+            assert np.array_equal(a[k], b[k]), (i, k)
+        st = int(meta.status.item())
+        want = int(m2.status.item()) | int(p2.status.item())
+        assert st == want, (i, st, want)
+        assert (st == TT_STATUS_BAD_BIAS) == (i == len(specs) - 2), (i, st)
+
+
 @pytest.mark.parametrize("case", ["forest", "agent16k", "gateway", "rollout270k"])
 def test_plan_matches_numpy(case):
     """Every field of the device tile plan equals the numpy restatement

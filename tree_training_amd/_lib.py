@@ -29,7 +29,7 @@ TT_STATUS_BAD_PARENT = 2
 TT_STATUS_BAD_TOTAL = 4
 TT_STATUS_BAD_BIAS = 8
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # Every symbol include/tree_attn.h declares, for the export check.
 EXPORTS = (
@@ -39,12 +39,22 @@ EXPORTS = (
     "tt_gdn_bwd_workspace_bytes", "tt_gdn_tree_bwd", "tt_gdn_saved_bytes", "tt_gdn_tree_fwd_save",
     "tt_gdn_bwd_saved_workspace_bytes", "tt_gdn_tree_bwd_saved", "tt_tree_conv_fwd", "tt_tree_conv_bwd_workspace_bytes",
     "tt_tree_conv_bwd", "tt_qk_prologue_fwd", "tt_qk_prologue_bwd_workspace_bytes", "tt_qk_prologue_bwd", "tt_ce_rows",
-    "tt_selftest_mfma32", "tt_noalloc_scratch_bytes", "tt_attn_bwd_noalloc",
+    "tt_selftest_mfma32", "tt_noalloc_scratch_bytes", "tt_attn_bwd_noalloc", "tt_trees_build",
 )
+
+TT_TREE_JOBS_MAX = 16
 
 
 class TTTensor(ctypes.Structure):
     _fields_ = [("ptr", ctypes.c_void_p), ("stride_tok", ctypes.c_int64), ("stride_head", ctypes.c_int64)]
+
+
+class TTTreeJob(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "node_len", "node_parent", "past_bias", "node_start", "node_off", "node_hend", "pos", "node_of", "horizon",
+        "key_lo", "key_hi", "status", "plan")] + [("plan_bytes", ctypes.c_size_t), ("ws", ctypes.c_void_p),
+                                                   ("ws_bytes", ctypes.c_size_t)] + \
+        [(n, ctypes.c_int32) for n in ("n_nodes", "n_tokens", "pos_offset", "n_past")]
 
 
 class TTAttnProblem(ctypes.Structure):
@@ -112,6 +122,7 @@ def _declare(lib):
         "tt_meta_dense_mask": (ctypes.c_int, [P, P, I32, I32, P, VP]),
         "tt_plan_bytes": (SZ, [I32, I32]),
         "tt_plan_build": (ctypes.c_int, [P, P, I32, I32, P, SZ, VP]),
+        "tt_trees_build": (ctypes.c_int, [ctypes.POINTER(TTTreeJob), I32, VP]),
         "tt_attn_fwd": (ctypes.c_int, [ctypes.POINTER(TTAttnProblem), P, P, VP]),
         "tt_attn_bwd_workspace_bytes": (SZ, [ctypes.POINTER(TTAttnProblem)]),
         "tt_attn_bwd": (ctypes.c_int, [ctypes.POINTER(TTAttnProblem), P, P, TTTensor, P, P, P, P, P, P, SZ,

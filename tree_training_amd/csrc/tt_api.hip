@@ -6,7 +6,7 @@
 
 namespace {
 
-constexpr int kAbiVersion = 2;
+constexpr int kAbiVersion = 3;
 constexpr int64_t kMaxTokStride = int64_t(1) << 23;   // elements
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
@@ -126,6 +126,25 @@ int tt_plan_build(const int32_t* key_lo, const int32_t* key_hi, int32_t n_keys, 
     if (n_q < 1 || n_keys < n_q || n_keys > 0x3fffffff || !key_lo || !key_hi || !plan) return TT_E_ARG;
     if (plan_bytes < tt_plan_bytes_impl(n_q, n_keys)) return TT_E_WORKSPACE;
     return tt_plan_build_impl(key_lo, key_hi, n_keys, n_q, plan, (hipStream_t)stream);
+}
+
+static_assert(sizeof(tt_tree_job) == 144, "tt_tree_job layout (bindings mirror it)");
+
+int tt_trees_build(const tt_tree_job* jobs, int32_t n_jobs, void* stream) {
+    if (!jobs || n_jobs < 1 || n_jobs > TT_TREE_JOBS_MAX) return TT_E_ARG;
+    for (int i = 0; i < n_jobs; ++i) {
+        const tt_tree_job& t = jobs[i];
+        if (t.n_nodes < 1 || t.n_tokens < t.n_nodes || t.n_past < 0 || t.pos_offset < 0) return TT_E_ARG;
+        if ((int64_t)t.n_tokens + t.n_past > 0x3fffffff) return TT_E_ARG;
+        if (!t.node_len || !t.node_parent || !t.node_start || !t.node_off || !t.node_hend || !t.pos || !t.horizon ||
+            !t.key_lo || !t.key_hi || !t.status || !t.plan || !t.ws || (t.n_past > 0 && !t.past_bias))
+            return TT_E_ARG;
+        if (!tt_trees_job_fits(t.n_tokens, t.n_tokens + t.n_past)) return TT_E_UNSUPPORTED;
+        if (t.plan_bytes < tt_plan_bytes_impl(t.n_tokens, t.n_tokens + t.n_past) ||
+            t.ws_bytes < tt_meta_ws_bytes_impl(t.n_nodes))
+            return TT_E_WORKSPACE;
+    }
+    return tt_trees_build_impl(jobs, n_jobs, (hipStream_t)stream);
 }
 
 int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* stream) {

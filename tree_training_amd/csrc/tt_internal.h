@@ -138,6 +138,8 @@ int tt_keys_build_impl(const float* bias, int n_past, const int32_t* horizon, in
 int tt_dense_mask_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys, int n_q, uint8_t* mask,
                        hipStream_t s);
 size_t tt_plan_bytes_impl(int n_q, int n_keys);
+int tt_trees_build_impl(const tt_tree_job* jobs, int n_jobs, hipStream_t s);
+bool tt_trees_job_fits(int n_tokens, int n_keys);
 int tt_plan_build_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys, int n_q, void* plan,
                        hipStream_t s);
 

@@ -20,16 +20,16 @@ __host__ __device__ inline int sparse_levels(int n) {
     return L;
 }
 
-// Node-level metadata in one workgroup of kNodeThreads threads; ends with a
-// barrier after which start, off and hend of every node are visible to the
-// whole workgroup.
+// Node-level metadata in one workgroup of kNodeThreads threads. TT_STATUS_*
+// bits are OR-ed into s_err (an LDS word the caller zeroes before the call);
+// ends with a barrier after which start, off, hend and s_err are visible to
+// the whole workgroup.
 __device__ __forceinline__ void meta_nodes_body(
     const int32_t* __restrict__ len, const int32_t* __restrict__ par, int n, int T,
     int32_t* __restrict__ start, int32_t* __restrict__ off, int32_t* __restrict__ hend,
-    int32_t* __restrict__ status, int32_t* __restrict__ ws) {
+    int& s_err, int32_t* __restrict__ ws) {
     __shared__ int s_scan[kNodeThreads];
     __shared__ int s_carry;
-    __shared__ int s_err;
     const int tid = threadIdx.x;
     int32_t* anc0 = ws;
     int32_t* anc1 = ws + n;
@@ -37,7 +37,7 @@ __device__ __forceinline__ void meta_nodes_body(
     int32_t* dep0 = ws + 3 * n;
     int32_t* dep1 = ws + 4 * n;
     int32_t* st = ws + 5 * n;   // sparse-table levels 1..L-1, n ints each
-    if (tid == 0) { s_carry = 0; s_err = 0; }
+    if (tid == 0) s_carry = 0;
     __syncthreads();
 
     // 1. exclusive prefix sum of node lengths -> node_start; validate input.
@@ -139,14 +139,42 @@ __device__ __forceinline__ void meta_nodes_body(
         if (p >= 0 && p < i && start[i] >= hend[p]) atomicOr(&s_err, TT_STATUS_BAD_PARENT);
     }
     __syncthreads();
-    if (tid == 0 && s_err) atomicOr(status, s_err);
+}
+
+// Tokens of every node: wave w writes the tokens of nodes w, w + 16, ..., its
+// lanes 64 consecutive tokens at a time (no per-token search); with
+// key_lo/key_hi, also the own keys' visibility intervals after n_past gateway
+// keys. A node outside [0, T) (bad lengths, flagged in the status) writes
+// nothing.
+__device__ __forceinline__ void meta_tokens_body(const int32_t* __restrict__ len, int n, int T, int pos_offset,
+                                                 const int32_t* __restrict__ start, const int32_t* __restrict__ off,
+                                                 const int32_t* __restrict__ hend, int32_t* __restrict__ pos,
+                                                 int32_t* __restrict__ node_of, int32_t* __restrict__ horizon,
+                                                 int n_past, int32_t* __restrict__ key_lo,
+                                                 int32_t* __restrict__ key_hi) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int c = wave; c < n; c += kNodeThreads / 64) {
+        const int s0 = start[c], e0 = min(s0 + max(len[c], 0), T), o = pos_offset + off[c], h = hend[c];
+        for (int i = max(s0, 0) + lane; i < e0; i += 64) {
+            pos[i] = o + (i - s0);
+            if (node_of) node_of[i] = c;
+            horizon[i] = h;
+            if (key_lo) {
+                key_lo[n_past + i] = i;
+                key_hi[n_past + i] = h;
+            }
+        }
+    }
 }
 
 __global__ __launch_bounds__(kNodeThreads) void meta_nodes_kernel(
     const int32_t* __restrict__ len, const int32_t* __restrict__ par, int n, int T,
     int32_t* __restrict__ start, int32_t* __restrict__ off, int32_t* __restrict__ hend,
     int32_t* __restrict__ status, int32_t* __restrict__ ws) {
-    meta_nodes_body(len, par, n, T, start, off, hend, status, ws);
+    __shared__ int s_err;
+    if (threadIdx.x == 0) s_err = 0;
+    meta_nodes_body(len, par, n, T, start, off, hend, s_err, ws);
+    if (threadIdx.x == 0 && s_err) atomicOr(status, s_err);
 }
 
 // Nodes and tokens in one launch (trees of up to kFusedTokens tokens): after
@@ -158,17 +186,11 @@ __global__ __launch_bounds__(kNodeThreads) void meta_tree_kernel(
     int32_t* __restrict__ start, int32_t* __restrict__ off, int32_t* __restrict__ hend,
     int32_t* __restrict__ pos, int32_t* __restrict__ node_of, int32_t* __restrict__ horizon,
     int32_t* __restrict__ status, int32_t* __restrict__ ws) {
-    meta_nodes_body(len, par, n, T, start, off, hend, status, ws);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int c = wave; c < n; c += kNodeThreads / 64) {
-        // a node outside [0, T) (bad lengths, flagged in status) writes nothing
-        const int s0 = start[c], e0 = min(s0 + max(len[c], 0), T), o = pos_offset + off[c], h = hend[c];
-        for (int i = max(s0, 0) + lane; i < e0; i += 64) {
-            pos[i] = o + (i - s0);
-            if (node_of) node_of[i] = c;
-            horizon[i] = h;
-        }
-    }
+    __shared__ int s_err;
+    if (threadIdx.x == 0) s_err = 0;
+    meta_nodes_body(len, par, n, T, start, off, hend, s_err, ws);
+    if (threadIdx.x == 0 && s_err) atomicOr(status, s_err);
+    meta_tokens_body(len, n, T, pos_offset, start, off, hend, pos, node_of, horizon, 0, nullptr, nullptr);
 }
 
 __global__ void meta_tokens_kernel(const int32_t* __restrict__ start, const int32_t* __restrict__ off,
@@ -409,14 +431,13 @@ __global__ __launch_bounds__(1024) void plan_kb_base_kernel(const int32_t* __res
 // both heaviest-first orders (a thread per block / tile), then the work-item
 // scan and the header, with the counts and the key-tile order kept in LDS.
 constexpr int kFinishMax = 2048;
-__global__ __launch_bounds__(1024) void plan_finish_kernel(const uint8_t* __restrict__ cls, int n_qb, int n_kt,
-                                                           const int32_t* __restrict__ kb_qlo,
-                                                           const int32_t* __restrict__ kb_qhi, int n_kb, int qch,
-                                                           const unsigned long long* __restrict__ pair_part, int n_pb,
-                                                           int32_t* __restrict__ row_cnt, int32_t* __restrict__ row_list,
-                                                           int32_t* __restrict__ row_order,
-                                                           int32_t* __restrict__ kb_order,
-                                                           int32_t* __restrict__ kb_base, uint8_t* __restrict__ plan) {
+__device__ __forceinline__ void plan_finish_body(const uint8_t* __restrict__ cls, int n_qb, int n_kt,
+                                                 const int32_t* __restrict__ kb_qlo,
+                                                 const int32_t* __restrict__ kb_qhi, int n_kb, int qch,
+                                                 const unsigned long long* __restrict__ pair_part, int n_pb,
+                                                 int32_t* __restrict__ row_cnt, int32_t* __restrict__ row_list,
+                                                 int32_t* __restrict__ row_order, int32_t* __restrict__ kb_order,
+                                                 int32_t* __restrict__ kb_base, uint8_t* __restrict__ plan) {
     __shared__ int s_cnt[kFinishMax];
     __shared__ int s_kbo[kFinishMax];
     __shared__ int s_scan[1024];
@@ -500,7 +521,148 @@ __global__ __launch_bounds__(1024) void plan_finish_kernel(const uint8_t* __rest
     }
 }
 
+__global__ __launch_bounds__(1024) void plan_finish_kernel(const uint8_t* __restrict__ cls, int n_qb, int n_kt,
+                                                           const int32_t* __restrict__ kb_qlo,
+                                                           const int32_t* __restrict__ kb_qhi, int n_kb, int qch,
+                                                           const unsigned long long* __restrict__ pair_part, int n_pb,
+                                                           int32_t* __restrict__ row_cnt, int32_t* __restrict__ row_list,
+                                                           int32_t* __restrict__ row_order,
+                                                           int32_t* __restrict__ kb_order,
+                                                           int32_t* __restrict__ kb_base, uint8_t* __restrict__ plan) {
+    plan_finish_body(cls, n_qb, n_kt, kb_qlo, kb_qhi, n_kb, qch, pair_part, n_pb, row_cnt, row_list, row_order,
+                     kb_order, kb_base, plan);
+}
+
+// ---------------------------------------------------------------------------
+// Several trees (the partitions of a hybrid step) in three launches: nodes,
+// tokens and keys (a workgroup per tree), the plan's key pass (grid y = tree),
+// the plan's finish (a workgroup per tree). The jobs travel as a kernel
+// argument.
+// ---------------------------------------------------------------------------
+struct TreeJobDev {
+    const int32_t* len;
+    const int32_t* par;
+    const float* bias;
+    int32_t* start;
+    int32_t* off;
+    int32_t* hend;
+    int32_t* pos;
+    int32_t* node_of;
+    int32_t* horizon;
+    int32_t* key_lo;
+    int32_t* key_hi;
+    int32_t* status;
+    uint8_t* plan;
+    int32_t* ws;
+    int n, T, pos_offset, n_past;
+};
+struct TreeJobsDev {
+    TreeJobDev j[TT_TREE_JOBS_MAX];
+    int n;
+};
+static_assert(sizeof(TreeJobsDev) <= 3072, "the jobs travel as one kernel argument");
+
+struct PlanPtrs {
+    PlanLayout L;
+    int32_t *row_cnt, *row_order, *row_list, *kb_qlo, *kb_qhi, *kb_order, *kb_base;
+    uint8_t* cls;
+    unsigned long long* pair_part;
+    int nb_cls, nb_kv;
+    __host__ __device__ PlanPtrs(uint8_t* base, int n_q, int n_keys) : L(n_q, n_keys) {
+        row_cnt = reinterpret_cast<int32_t*>(base + L.row_cnt);
+        row_order = reinterpret_cast<int32_t*>(base + L.row_order);
+        row_list = reinterpret_cast<int32_t*>(base + L.row_list);
+        kb_qlo = reinterpret_cast<int32_t*>(base + L.kb_qlo);
+        kb_qhi = reinterpret_cast<int32_t*>(base + L.kb_qhi);
+        kb_order = reinterpret_cast<int32_t*>(base + L.kb_order);
+        kb_base = reinterpret_cast<int32_t*>(base + L.kb_base);
+        cls = base + L.cls;
+        pair_part = reinterpret_cast<unsigned long long*>(base + L.pair_part);
+        nb_cls = tt_cdiv(L.n_qb * L.n_kt, 4);
+        nb_kv = tt_cdiv(L.n_kb, 4);
+    }
+    __host__ __device__ int pass_blocks() const { return nb_cls + nb_kv + L.n_pb; }
+};
+
+__global__ __launch_bounds__(kNodeThreads) void trees_meta_keys_kernel(TreeJobsDev J) {
+    const TreeJobDev& jb = J.j[blockIdx.x];
+    __shared__ int s_err;
+    if (threadIdx.x == 0) s_err = 0;
+    meta_nodes_body(jb.len, jb.par, jb.n, jb.T, jb.start, jb.off, jb.hend, s_err, jb.ws);
+    meta_tokens_body(jb.len, jb.n, jb.T, jb.pos_offset, jb.start, jb.off, jb.hend, jb.pos, jb.node_of, jb.horizon,
+                     jb.n_past, jb.key_lo, jb.key_hi);
+    for (int j = threadIdx.x; j < jb.n_past; j += kNodeThreads) {   // gateway keys: bias 0 or -inf
+        const float b = jb.bias[j];
+        if (b != 0.0f && !(__builtin_isinf(b) && b < 0.0f)) atomicOr(&s_err, TT_STATUS_BAD_BIAS);
+        jb.key_lo[j] = 0;
+        jb.key_hi[j] = b == 0.0f ? jb.T : 0;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) *jb.status = s_err;
+}
+
+__global__ __launch_bounds__(256) void trees_plan_pass_kernel(TreeJobsDev J) {
+    const TreeJobDev& jb = J.j[blockIdx.y];
+    const int n_keys = jb.n_past + jb.T;
+    const PlanPtrs P(jb.plan, jb.T, n_keys);
+    const int b = blockIdx.x;
+    if (b >= P.pass_blocks()) return;   // workgroup-uniform
+    if (b < P.nb_cls)
+        plan_classify(jb.key_lo, jb.key_hi, n_keys, jb.T, P.L.n_qb, P.L.n_kt, b, P.cls);
+    else if (b < P.nb_cls + P.nb_kv)
+        plan_kv_range(jb.key_lo, jb.key_hi, n_keys, jb.T, P.L.n_kb, b - P.nb_cls, P.kb_qlo, P.kb_qhi);
+    else
+        plan_pairs_part(jb.key_lo, jb.key_hi, n_keys, jb.T, b - P.nb_cls - P.nb_kv, P.pair_part);
+}
+
+__global__ __launch_bounds__(1024) void trees_plan_finish_kernel(TreeJobsDev J) {
+    const TreeJobDev& jb = J.j[blockIdx.x];
+    const PlanPtrs P(jb.plan, jb.T, jb.n_past + jb.T);
+    plan_finish_body(P.cls, P.L.n_qb, P.L.n_kt, P.kb_qlo, P.kb_qhi, P.L.n_kb, tt_qch(jb.T), P.pair_part, P.L.n_pb,
+                     P.row_cnt, P.row_list, P.row_order, P.kb_order, P.kb_base, jb.plan);
+}
+
 }  // namespace
+
+int tt_trees_build_impl(const tt_tree_job* jobs, int n_jobs, hipStream_t s) {
+    TreeJobsDev J{};
+    J.n = n_jobs;
+    int max_blocks = 1;
+    for (int i = 0; i < n_jobs; ++i) {
+        const tt_tree_job& t = jobs[i];
+        TreeJobDev& d = J.j[i];
+        d.len = t.node_len;
+        d.par = t.node_parent;
+        d.bias = t.past_bias;
+        d.start = t.node_start;
+        d.off = t.node_off;
+        d.hend = t.node_hend;
+        d.pos = t.pos;
+        d.node_of = t.node_of;
+        d.horizon = t.horizon;
+        d.key_lo = t.key_lo;
+        d.key_hi = t.key_hi;
+        d.status = t.status;
+        d.plan = reinterpret_cast<uint8_t*>(t.plan);
+        d.ws = reinterpret_cast<int32_t*>(t.ws);
+        d.n = t.n_nodes;
+        d.T = t.n_tokens;
+        d.pos_offset = t.pos_offset;
+        d.n_past = t.n_past;
+        const PlanPtrs P(nullptr, t.n_tokens, t.n_past + t.n_tokens);
+        max_blocks = max(max_blocks, P.pass_blocks());
+    }
+    hipLaunchKernelGGL(trees_meta_keys_kernel, dim3(n_jobs), dim3(kNodeThreads), 0, s, J);
+    hipLaunchKernelGGL(trees_plan_pass_kernel, dim3(max_blocks, n_jobs), dim3(256), 0, s, J);
+    hipLaunchKernelGGL(trees_plan_finish_kernel, dim3(n_jobs), dim3(1024), 0, s, J);
+    return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
+}
+
+// Limits of the batched build (each tree's metadata and plan in one workgroup).
+bool tt_trees_job_fits(int n_tokens, int n_keys) {
+    const PlanLayout L(n_tokens, n_keys);
+    return n_tokens <= kFusedTokens && L.n_qb <= kFinishMax && L.n_kb <= kFinishMax;
+}
 
 size_t tt_meta_ws_bytes_impl(int n) {
     if (n <= 0) return 0;

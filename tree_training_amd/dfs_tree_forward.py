@@ -54,10 +54,11 @@ def fused_ce_capable(model, leaf_loss_fn) -> bool:
 
 def run_tree_model(model, info: DFSTreeInfo, dev, pos_offset: int = 0, cache=None, accumulators=None,
                    past_bias: Optional[torch.Tensor] = None, linear_attention_patched: bool = False,
-                   hidden_only: bool = False):
+                   hidden_only: bool = False, plan=None):
     """One model forward over a DFS-packed forest (or partition) with tree
     attention. Returns the model output (the decoder's, with the final hidden
-    states and no logits, when ``hidden_only``)."""
+    states and no logits, when ``hidden_only``). ``plan``: a KeyPlan already
+    built for this tree and gateway (``meta.build_trees``), else built here."""
     vocab = getattr(getattr(model, "config", None), "vocab_size", None)
     if vocab is not None and info.dfs_token_ids and not (0 <= min(info.dfs_token_ids) and
                                                          max(info.dfs_token_ids) < vocab):
@@ -65,7 +66,8 @@ def run_tree_model(model, info: DFSTreeInfo, dev, pos_offset: int = 0, cache=Non
         raise ValueError(f"token ids must lie in [0, {vocab}) (the model's vocabulary); got "
                          f"[{min(info.dfs_token_ids)}, {max(info.dfs_token_ids)}]")
     meta = info.device_meta(dev, pos_offset)
-    plan = info.key_plan(dev, past_bias, pos_offset)
+    if plan is None:
+        plan = info.key_plan(dev, past_bias, pos_offset)
     ids_t = upload_i32([info.dfs_token_ids], dev).long()
     pos_t = meta.pos.long().unsqueeze(0)
     ctx = TreeAttnContext(plan=plan, cache=cache, accumulators=accumulators)

@@ -261,20 +261,54 @@ def _chain_gateway_grads(gw: SubtreeGateway, retain_graph: bool = False, collect
 # 4. one partition forward
 # ---------------------------------------------------------------------------
 def _subtree_forward(model, partition: SubtreePartition, gateway: Optional[SubtreeGateway], dev, dtype,
-                     hidden_only: bool = False):
+                     hidden_only: bool = False, prebuilt=None):
     """Forward of one partition with its gateway (tree_grad_hybrid.py:279-427).
+    ``prebuilt``: (DFS info tuple, KeyPlan) from ``_prebuild_partitions``.
 
     Returns (logits, or the final hidden states when ``hidden_only``, dfs_info,
     own_kv, start, end, par, chunk_idx, copy_to_orig)."""
-    info, start, end, par, cidx, c2o = _dfs_info_for_partition(partition)
+    if prebuilt is not None:
+        (info, start, end, par, cidx, c2o), plan = prebuilt
+    else:
+        (info, start, end, par, cidx, c2o), plan = _dfs_info_for_partition(partition), None
     gate_kv = list(zip(gateway.key_gates, gateway.val_gates)) if gateway is not None else []
     cache = GatewayCache(gate_kv, segmented=True)
     out = run_tree_model(model, info, dev, pos_offset=partition.pos_offset, cache=cache,
                          accumulators=gateway.fp32_acc if gateway is not None else None,
-                         past_bias=gateway.attn_bias if gateway is not None else None, hidden_only=hidden_only)
+                         past_bias=gateway.attn_bias if gateway is not None else None, hidden_only=hidden_only,
+                         plan=plan)
     own_kv = [cache.own_kv(l) for l in sorted(cache._segments)]
     res = out.last_hidden_state if hidden_only else out.logits
     return res, info, own_kv, start, end, par, cidx, c2o
+
+
+def _prebuild_partitions(partitions, children_of, dev, legacy: bool):
+    """Host DFS info of every partition and, in one ``meta.build_trees`` call,
+    their device metadata and tile plans (positions, horizons, gateway key
+    intervals): all of it depends on the topology alone, so the whole step's
+    metadata is built up front in a few launches instead of per partition.
+    Returns {id(partition): ((info, start, end, par, cidx, c2o), KeyPlan)}."""
+    from .meta import build_trees
+    infos, gws, specs = {}, {}, []
+    for p in partitions:                                   # parents before children
+        gw = gws.get(id(p))
+        pos_offset = gw[2] if gw is not None else 0
+        infos[id(p)] = _dfs_info_for_partition(p)
+        info, start, end, par, cidx, _ = infos[id(p)]
+        specs.append((info.node_len, info.chunk_parent_map, pos_offset, gw[1] if gw is not None else None))
+        made = {}
+        for cn, child in children_of[id(p)]:
+            if id(cn) not in made:
+                made[id(cn)] = gateway_bias_and_offset(info, start, end, par, cidx, cn, pos_offset,
+                                                       gw[0] if gw else 0, gw[1] if gw else None, legacy)
+            gws[id(child)] = made[id(cn)]
+    built = build_trees(specs, dev)
+    out = {}
+    for p, spec, (meta, plan) in zip(partitions, specs, built):
+        info = infos[id(p)][0]
+        info._meta[(str(meta.device), spec[2])] = meta
+        out[id(p)] = (infos[id(p)], plan)
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -309,13 +343,14 @@ def tree_grad_hybrid(model, roots: List[TreeNode], leaf_loss_fn: Callable[[torch
         if p.parent is not None:
             children_of[id(p.parent)].append((p.parent_cut_node, p))
 
+    prebuilt = _prebuild_partitions(partitions, children_of, dev, legacy_gateway_bias)
     gateways: Dict[int, Optional[SubtreeGateway]] = {}
     fwd_cache: Dict[int, tuple] = {}
     for p in partitions:                                   # top-down forward
         gw = gateways.get(id(p))
         p.pos_offset = gw.pos_offset if gw is not None else 0
-        logits, info, own_kv, s_map, e_map, par_map, ci_map, c2o = _subtree_forward(model, p, gw, dev, dtype,
-                                                                                     hidden_only=fused)
+        logits, info, own_kv, s_map, e_map, par_map, ci_map, c2o = _subtree_forward(
+            model, p, gw, dev, dtype, hidden_only=fused, prebuilt=prebuilt.pop(id(p)))
         fwd_cache[id(p)] = (logits, info, c2o)
         seen, cuts = set(), []
         for cn, _ in children_of[id(p)]:
