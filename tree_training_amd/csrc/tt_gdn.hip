@@ -696,6 +696,8 @@ __global__ __launch_bounds__(GT) void gdn_dw_s0_kernel(GdnDev p, const float* __
     store_acc<0>(acc_mat(dwo + chn * GC * GD, GC, half, 32 * wave + col), -w);
 }
 
+constexpr int RR = GC + 1;        // row stride of the per-wave 32 x 32 partials
+
 struct ChunkGradLds {
     float Qs[GC * RS];    // q^ * scale
     float Ks[GC * RS];    // k^
@@ -703,17 +705,49 @@ struct ChunkGradLds {
     float P2[GC * RS];
     float P3[GC * RS];    // v; later Y = T^T dT (stride MS)
     float KK[GC * MS];    // k^ k^T
-    float M1[GC * MS];    // A -> dA * D -> dT -> E
+    float M1[GC * MS];    // A -> dP -> dT -> E
     float M2[GC * MS];    // T
     float M3[GC * MS];    // dA * A + dN * N (for the column sums of dG)
+    float R[4][GC * RR];  // per-wave partial 32 x 32 products (contraction split over the waves)
     float G[GC];
     float B[GC];
     float Grow[GC];
     float Crow[GC];
 };
 
-// Thread t owns row i = t/8 of every [GC x *] result; in [GC x GD] results the
-// columns 32m + 4s + e (s = t%8, m, e < 4), in [GC x GC] results s + 8e.
+// fp32 MFMA operands from LDS, in the k order of mfma_f32 (step r pairs
+// k = acc_row(r, 0) on lanes 0-31 with k = acc_row(r, 1) on lanes 32-63).
+// Row operand X[col][kb + k]: four steps per 16-byte read.
+__device__ __forceinline__ f32x4 op_row4(const float* X, int stride, int col, int half, int kb, int m) {
+    return *(const f32x4*)&X[col * stride + kb + 8 * m + 4 * half];
+}
+// Column operand X[kb + k][c0 + col], one step.
+__device__ __forceinline__ float op_col(const float* X, int stride, int half, int kb, int r, int c0, int col) {
+    return X[(kb + acc_row(r, half)) * stride + c0 + col];
+}
+// 32 x 32 partial product over this wave's quarter of a 128-deep contraction:
+// D[i][j] = sum_k A[i][k] B[j][k] (both read as rows), B scaled by bs (a
+// per-column factor), added to acc.
+__device__ __forceinline__ f32x16 quarter_nt(const float* A, const float* B, float bs, int col, int half, int wave,
+                                             f32x16 acc) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const f32x4 a = op_row4(A, RS, col, half, 32 * wave, m), b = op_row4(B, RS, col, half, 32 * wave, m);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = mfma_f32(a[e], b[e] * bs, acc);
+    }
+    return acc;
+}
+__device__ __forceinline__ void put_partial(float* R, const f32x16& acc, int col, int half) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) R[acc_row(r, half) * RR + col] = acc[r];
+}
+
+// Thread t owns row i = t/8 of the element-wise work: in [GC x GD] results
+// the columns 32m + 4s + e (s = t%8, m, e < 4), in [GC x GC] results s + 8e.
+// The products run on fp32 MFMA: a [GC x GD] result is split by columns
+// (wave w: columns 32w .. 32w+31, in accumulator layout), a [GC x GC] one by
+// contraction (wave w: k in [32w, 32w+32), partials summed through LDS).
 // TRUNC (the reference's per-node correction): U and W do not come from the
 // chunk's T, so the T part is left out; dv and dbeta are complete already
 // (tt_gdn_trunc.hip), and trk (dk^ of the correction, [chunk, Hv, 32, 128])
@@ -734,25 +768,23 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
     int start, len;
     if (!chunk_span(p, c, start, len)) return;
     const int i = t >> 3, s = t & 7;
+    const int wave = t >> 6, lane = t & 63, col = lane & 31, half = lane >> 5, cw0 = 32 * wave;
     const bool valid = i < len;
     const int64_t tok = start + i;
 
     load_chunk_rows<TIn>(p, start, len, hk * p.rep, L.Qs, L.Ks, nullptr);
     __syncthreads();
-    {
-        float kk[4] = {};
-#pragma unroll 4
-        for (int d = 0; d < GD; d += 4) {
-            const f32x4 a = *(const f32x4*)&L.Ks[i * RS + d];
+    put_partial(L.R[wave], quarter_nt(L.Ks, L.Ks, 1.0f, col, half, wave, (f32x16){}), col, half);   // k^ k^T
+    __syncthreads();
 #pragma unroll
-            for (int e = 0; e < 4; ++e) kk[e] += dot4(a, *(const f32x4*)&L.Ks[(s + 8 * e) * RS + d]);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) L.KK[i * MS + s + 8 * e] = kk[e];
+    for (int e = 0; e < 4; ++e) {
+        const int j = s + 8 * e;
+        L.KK[i * MS + j] = L.R[0][i * RR + j] + L.R[1][i * RR + j] + L.R[2][i * RR + j] + L.R[3][i * RR + j];
     }
-    float dqa[16], dka[16];
+    float dqa[16], dka[16];   // element-wise terms (row layout)
 #pragma unroll
     for (int e = 0; e < 16; ++e) dqa[e] = dka[e] = 0.0f;
+    f32x16 dqm = {}, dkm = {};   // product terms (accumulator layout, columns cw0 + col)
 
 #pragma unroll 1
     for (int hh = 0; hh < p.rep; ++hh) {
@@ -773,27 +805,22 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
             if constexpr (!TRUNC) L.M2[i * MS + j] = cw[kWsT + i * GC + j];
         }
         __syncthreads();
+        // dA = dO V'^T (partials per wave)
+        put_partial(L.R[wave], quarter_nt(L.P1, L.P2, 1.0f, col, half, wave, (f32x16){}), col, half);
+        __syncthreads();
         const float gi = L.G[i], gl = L.G[GC - 1], egi = expf(gi), bi = L.B[i];
         float dgp = 0.0f, dbp = 0.0f, cp = 0.0f;   // this thread's share of row i's dG, dbeta, c
 
-        // dA = dO V'^T (j <= i): dG from A = (q^ k^T) * D, then dP = dA * D.
-        {
-            float da[4] = {};
-#pragma unroll 4
-            for (int d = 0; d < GD; d += 4) {
-                const f32x4 a = *(const f32x4*)&L.P1[i * RS + d];
+        // dG from A = (q^ k^T) * D, then dP = dA * D (j <= i).
 #pragma unroll
-                for (int e = 0; e < 4; ++e) da[e] += dot4(a, *(const f32x4*)&L.P2[(s + 8 * e) * RS + d]);
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int j = s + 8 * e;
-                const float dae = j <= i ? da[e] : 0.0f;
-                const float pa = dae * L.M1[i * MS + j];
-                dgp += pa;
-                L.M3[i * MS + j] = pa;
-                L.M1[i * MS + j] = j <= i ? dae * expf(gi - L.G[j]) : 0.0f;
-            }
+        for (int e = 0; e < 4; ++e) {
+            const int j = s + 8 * e;
+            const float da = L.R[0][i * RR + j] + L.R[1][i * RR + j] + L.R[2][i * RR + j] + L.R[3][i * RR + j];
+            const float dae = j <= i ? da : 0.0f;
+            const float pa = dae * L.M1[i * MS + j];
+            dgp += pa;
+            L.M3[i * MS + j] = pa;
+            L.M1[i * MS + j] = j <= i ? dae * expf(gi - L.G[j]) : 0.0f;
         }
         // O's state term e^G q^ S: dq^ += e^G X, dG += e^G q^ . X.
         {
@@ -810,98 +837,85 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
             dgp = fmaf(egi, xq, dgp);
         }
         __syncthreads();   // dP complete
-        // dq^ += dP k^, dk^ += dP^T q^.
-#pragma unroll 2
-        for (int j = 0; j < GC; ++j) {
-            const float pij = L.M1[i * MS + j], pji = L.M1[j * MS + i];
+        // dq^ += dP k^, dk^ += dP^T q^ (contraction over the chunk's 32 tokens).
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                const f32x4 kj = *(const f32x4*)&L.Ks[j * RS + 32 * m + 4 * s];
-                const f32x4 qj = *(const f32x4*)&L.Qs[j * RS + 32 * m + 4 * s];
+        for (int m = 0; m < 4; ++m) {
+            const f32x4 a = op_row4(L.M1, MS, col, half, 0, m);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    dqa[4 * m + e] = fmaf(pij, kj[e], dqa[4 * m + e]);
-                    dka[4 * m + e] = fmaf(pji, qj[e], dka[4 * m + e]);
-                }
+            for (int e = 0; e < 4; ++e) {
+                const int r = 4 * m + e;
+                dqm = mfma_f32(a[e], op_col(L.Ks, RS, half, 0, r, cw0, col), dqm);
+                dkm = mfma_f32(op_col(L.M1, MS, half, 0, r, 0, col), op_col(L.Qs, RS, half, 0, r, cw0, col), dkm);
             }
         }
         if constexpr (!TRUNC) {
-            __syncthreads();   // P1, P2, M1 free
+            __syncthreads();   // P1, P2 and R readers are done
             tile_in(chunk_dvp + chn * GC * GD, GD, GC, L.P1);
             tile_in(dwo + chn * GC * GD, GD, GC, L.P2);
             tile_in((const TIn*)p.v + (int64_t)start * p.v_st + (int64_t)h * p.v_sh, p.v_st, len, L.P3);
             __syncthreads();
 
-            // dBv = T^T dV', dBk = T^T dW; dv = beta dBv; dbeta, dk^, dG from
-            // U = T (beta v) and W = T (beta e^G k^).
+            // dT = dV' (beta v)^T + dW (beta e^G k^)^T (partials per wave); dBv =
+            // T^T dV', dBk = T^T dW (columns of this wave).
             {
-                float dbv[16], dbk[16];
-    #pragma unroll
-                for (int e = 0; e < 16; ++e) dbv[e] = dbk[e] = 0.0f;
-    #pragma unroll 2
-                for (int j = 0; j < GC; ++j) {
-                    const float tji = L.M2[j * MS + i];
-    #pragma unroll
-                    for (int m = 0; m < 4; ++m) {
-                        const f32x4 a = *(const f32x4*)&L.P1[j * RS + 32 * m + 4 * s];
-                        const f32x4 b = *(const f32x4*)&L.P2[j * RS + 32 * m + 4 * s];
-    #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            dbv[4 * m + e] = fmaf(tji, a[e], dbv[4 * m + e]);
-                            dbk[4 * m + e] = fmaf(tji, b[e], dbk[4 * m + e]);
-                        }
-                    }
-                }
+                const float bj = L.B[col], bgj = bj * expf(L.G[col]);
+                f32x16 tp = quarter_nt(L.P1, L.P3, bj, col, half, wave, (f32x16){});
+                tp = quarter_nt(L.P2, L.Ks, bgj, col, half, wave, tp);
+                put_partial(L.R[wave], tp, col, half);
+            }
+            f32x16 dbvm = {}, dbkm = {};
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float a = op_col(L.M2, MS, half, 0, r, 0, col);
+                dbvm = mfma_f32(a, op_col(L.P1, RS, half, 0, r, cw0, col), dbvm);
+                dbkm = mfma_f32(a, op_col(L.P2, RS, half, 0, r, cw0, col), dbkm);
+            }
+            __syncthreads();   // R complete; P1, P2 readers are done
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                L.P1[acc_row(r, half) * RS + cw0 + col] = dbvm[r];
+                L.P2[acc_row(r, half) * RS + cw0 + col] = dbkm[r];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = s + 8 * e;
+                L.M1[i * MS + j] = L.R[0][i * RR + j] + L.R[1][i * RR + j] + L.R[2][i * RR + j] + L.R[3][i * RR + j];
+            }
+            __syncthreads();   // dBv, dBk and dT complete
+            // dv = beta dBv; dbeta, dk^, dG from U = T (beta v) and W = T (beta e^G k^).
+            {
                 float vb = 0.0f, kb = 0.0f;
                 const float bge = bi * egi;
-    #pragma unroll
+#pragma unroll
                 for (int m = 0; m < 4; ++m) {
                     const f32x4 vv = *(const f32x4*)&L.P3[i * RS + 32 * m + 4 * s];
                     const f32x4 kv = *(const f32x4*)&L.Ks[i * RS + 32 * m + 4 * s];
+                    const f32x4 dbv = *(const f32x4*)&L.P1[i * RS + 32 * m + 4 * s];
+                    const f32x4 dbk = *(const f32x4*)&L.P2[i * RS + 32 * m + 4 * s];
                     f32x4 o;
-    #pragma unroll
+#pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        vb = fmaf(vv[e], dbv[4 * m + e], vb);
-                        kb = fmaf(kv[e], dbk[4 * m + e], kb);
-                        dka[4 * m + e] = fmaf(bge, dbk[4 * m + e], dka[4 * m + e]);
-                        o[e] = bi * dbv[4 * m + e];
+                        vb = fmaf(vv[e], dbv[e], vb);
+                        kb = fmaf(kv[e], dbk[e], kb);
+                        dka[4 * m + e] = fmaf(bge, dbk[e], dka[4 * m + e]);
+                        o[e] = bi * dbv[e];
                     }
                     if (valid) store4(dv + (tok * p.hv + h) * GD + 32 * m + 4 * s, o);
                 }
                 dbp += vb + egi * kb;
                 dgp = fmaf(bge, kb, dgp);
             }
-            // dT = dV' (beta v)^T + dW (beta e^G k^)^T
-            {
-                float t1[4] = {}, t2[4] = {};
-    #pragma unroll 4
-                for (int d = 0; d < GD; d += 4) {
-                    const f32x4 a = *(const f32x4*)&L.P1[i * RS + d];
-                    const f32x4 b = *(const f32x4*)&L.P2[i * RS + d];
-    #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        t1[e] += dot4(a, *(const f32x4*)&L.P3[(s + 8 * e) * RS + d]);
-                        t2[e] += dot4(b, *(const f32x4*)&L.Ks[(s + 8 * e) * RS + d]);
-                    }
-                }
-    #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int j = s + 8 * e;
-                    const float bj = L.B[j];
-                    L.M1[i * MS + j] = bj * t1[e] + bj * expf(L.G[j]) * t2[e];
-                }
-            }
-            __syncthreads();   // dT complete; P1..P3 free
+            __syncthreads();   // P3 (v) readers are done
             // Y = T^T dT into P3 (stride MS)
             {
                 float y[4] = {};
-    #pragma unroll 4
+#pragma unroll 4
                 for (int m = 0; m < GC; ++m) {
                     const float tmi = L.M2[m * MS + i];
-    #pragma unroll
+#pragma unroll
                     for (int e = 0; e < 4; ++e) y[e] = fmaf(tmi, L.M1[m * MS + s + 8 * e], y[e]);
                 }
-    #pragma unroll
+#pragma unroll
                 for (int e = 0; e < 4; ++e) L.P3[i * MS + s + 8 * e] = y[e];
             }
             __syncthreads();
@@ -909,11 +923,11 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
             // N = -beta (k^ k^T) * D.
             {
                 float ev[4];
-    #pragma unroll
+#pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int j = s + 8 * e;
                     float dn = 0.0f;
-    #pragma unroll 4
+#pragma unroll 4
                     for (int m = 0; m < GC; ++m) dn = fmaf(L.P3[i * MS + m], L.M2[j * MS + m], dn);
                     ev[e] = 0.0f;
                     if (j < i) {
@@ -925,19 +939,19 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
                         L.M3[i * MS + j] += pa;
                     }
                 }
-    #pragma unroll
+#pragma unroll
                 for (int e = 0; e < 4; ++e) L.M1[i * MS + s + 8 * e] = ev[e];   // dT's readers passed the last barrier
             }
             __syncthreads();
             // dk^ += (E + E^T) k^
-    #pragma unroll 2
-            for (int j = 0; j < GC; ++j) {
-                const float ej = L.M1[i * MS + j] + L.M1[j * MS + i];
-    #pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    const f32x4 kj = *(const f32x4*)&L.Ks[j * RS + 32 * m + 4 * s];
-    #pragma unroll
-                    for (int e = 0; e < 4; ++e) dka[4 * m + e] = fmaf(ej, kj[e], dka[4 * m + e]);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const f32x4 a = op_row4(L.M1, MS, col, half, 0, m);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * m + e;
+                    const float ae = a[e] + op_col(L.M1, MS, half, 0, r, 0, col);
+                    dkm = mfma_f32(ae, op_col(L.Ks, RS, half, 0, r, cw0, col), dkm);
                 }
             }
         } else {   // the correction's dk^ (its dv, dbeta are complete)
@@ -975,13 +989,13 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
         }
         __syncthreads();
         if (t < GC) {
-            float col = 0.0f, ctot = 0.0f;
+            float colsum = 0.0f, ctot = 0.0f;
 #pragma unroll 4
             for (int r = 0; r < GC; ++r) {
-                col += L.M3[r * MS + t];
+                colsum += L.M3[r * MS + t];
                 ctot += L.Crow[r];
             }
-            float dG = L.Grow[t] - col;
+            float dG = L.Grow[t] - colsum;
             if (t == GC - 1) dG += expf(gl) * sdot[chn] + ctot;
             // dg_t = sum of dG_u over u >= t within the chunk (G is its cumulative sum)
 #pragma unroll
@@ -991,6 +1005,25 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
             }
             if constexpr (TRUNC) dG += trg[chn * GC + t];
             if (t < len) dg[(int64_t)(start + t) * p.hv + h] = dG;
+        }
+    }
+
+    // The product terms join the element-wise ones (through P1, P2).
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        L.P1[acc_row(r, half) * RS + cw0 + col] = dqm[r];
+        L.P2[acc_row(r, half) * RS + cw0 + col] = dkm[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const f32x4 a = *(const f32x4*)&L.P1[i * RS + 32 * m + 4 * s];
+        const f32x4 b = *(const f32x4*)&L.P2[i * RS + 32 * m + 4 * s];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            dqa[4 * m + e] += a[e];
+            dka[4 * m + e] += b[e];
         }
     }
 
