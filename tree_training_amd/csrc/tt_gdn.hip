@@ -32,28 +32,31 @@ namespace {
 // prep: per (chunk, v head) A, T, U, W, G
 // ----------------------------------------------------------------------------
 struct PrepLds {
-    float Q[GC * RS];
+    float Q[GC * RS];     // q^ * scale; v once A is done
     float K[GC * RS];
-    float V[GC * RS];
-    float A[GC * MS];
+    float R[4][GC * RR];  // partial products: A (waves 0, 1), k^ k^T (waves 2, 3)
     float N[GC * MS];     // N = -strictly_lower(beta k^ k^T * D), then its powers N^(2^r)
     float Tm[GC * MS];    // T = (I - N)^-1, built as (I + N)(I + N^2)(I + N^4)...
     float G[GC];
     float beta[GC];
+    float bg[GC];         // beta e^G
 };
 
+// q^ k^T and k^ k^T on fp32 MFMA (waves 0-1 and 2-3, each half of the
+// 128-deep contraction), the inverse T on the vector ALUs, then U and W on
+// fp32 MFMA, split by columns over the waves.
 // TRUNC (the reference's per-node correction): only A and G here; U and W
 // come from the node-level kernels of tt_gdn_trunc.hip.
 template <typename TIn, bool TRUNC>
 __global__ __launch_bounds__(GT) void gdn_prep_kernel(GdnDev p, float* __restrict__ ws) {
     __shared__ __attribute__((aligned(16))) PrepLds L;
     const int c = blockIdx.x, h = blockIdx.y;
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, col = lane & 31, half = lane >> 5;
     int start, len;
     if (!chunk_span(p, c, start, len)) return;
     float* out = ws + ((size_t)c * p.hv + h) * kWsChunk;
 
-    load_chunk_rows<TIn>(p, start, len, h, L.Q, L.K, L.V);
+    load_chunk_rows<TIn>(p, start, len, h, L.Q, L.K, nullptr);
     if (wave == 0) {
         // cumulative decay over the chunk (lanes 0..31; padded rows add 0)
         const bool valid = lane < len;
@@ -68,30 +71,30 @@ __global__ __launch_bounds__(GT) void gdn_prep_kernel(GdnDev p, float* __restric
         if (lane < GC) {
             L.G[lane] = gv;
             L.beta[lane] = bv;
+            L.bg[lane] = bv * expf(gv);
             out[kWsG + lane] = gv;
         }
     }
     __syncthreads();
+    {
+        const float* X = wave < 2 ? L.Q : L.K;
+        const int q0 = 2 * (wave & 1);
+        f32x16 acc = quarter_nt(X, L.K, 1.0f, col, half, q0, (f32x16){});
+        acc = quarter_nt(X, L.K, 1.0f, col, half, q0 + 1, acc);
+        put_partial(L.R[wave], acc, col, half);
+    }
+    __syncthreads();
+    if constexpr (!TRUNC)   // Q's readers are done
+        tile_in((const TIn*)p.v + (int64_t)start * p.v_st + (int64_t)h * p.v_sh, p.v_st, len, L.Q);
 
     // A = lower_incl(q^ k^T * D), N = -strictly_lower(beta k^ k^T * D).
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int pi = t + GT * u, i = pi >> 5, j = pi & 31;
-        float dqk = 0.0f, dkk = 0.0f;
-#pragma unroll 2
-        for (int d = 0; d < GD; d += 4) {
-            const f32x4 qi = *(const f32x4*)&L.Q[i * RS + d];
-            const f32x4 ki = *(const f32x4*)&L.K[i * RS + d];
-            const f32x4 kj = *(const f32x4*)&L.K[j * RS + d];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                dqk = fmaf(qi[e], kj[e], dqk);
-                dkk = fmaf(ki[e], kj[e], dkk);
-            }
-        }
+        const float dqk = L.R[0][i * RR + j] + L.R[1][i * RR + j];
+        const float dkk = L.R[2][i * RR + j] + L.R[3][i * RR + j];
         const float dec = j <= i ? expf(L.G[i] - L.G[j]) : 0.0f;
         const float nij = j < i ? -L.beta[i] * dkk * dec : 0.0f;
-        L.A[i * MS + j] = dqk * dec;
         out[kWsA + i * GC + j] = dqk * dec;
         L.N[i * MS + j] = nij;
         L.Tm[i * MS + j] = nij + (i == j ? 1.0f : 0.0f);
@@ -132,37 +135,25 @@ __global__ __launch_bounds__(GT) void gdn_prep_kernel(GdnDev p, float* __restric
         *(f32x4*)(out + kWsT + ti * GC + tc) = *(const f32x4*)&L.Tm[ti * MS + tc];
     }
 
-    // U = T (beta v), W = T (beta e^G k^): thread t owns rows oi0..+3, columns oc0..+3.
-    const int oi0 = 4 * (t >> 5), oc0 = 4 * (t & 31);
-    f32x4 u[4], w[4];
+    // U = T (beta v), W = T (beta e^G k^): wave w produces columns 32w .. 32w+31.
+    {
+        const int cw0 = 32 * wave;
+        f32x16 u = {}, w = {};
 #pragma unroll
-    for (int a = 0; a < 4; ++a) u[a] = w[a] = (f32x4){};
-#pragma unroll 1
-    for (int j0 = 0; j0 < GC; j0 += 4) {
-        f32x4 tr[4];
+        for (int m = 0; m < 4; ++m) {
+            const f32x4 a = op_row4(L.Tm, MS, col, half, 0, m);
 #pragma unroll
-        for (int a = 0; a < 4; ++a) tr[a] = *(const f32x4*)&L.Tm[(oi0 + a) * MS + j0];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            const int j = j0 + jj;
-            const float bj = L.beta[j], bgj = bj * expf(L.G[j]);
-            const f32x4 vj = *(const f32x4*)&L.V[j * RS + oc0];
-            const f32x4 kj = *(const f32x4*)&L.K[j * RS + oc0];
-#pragma unroll
-            for (int a = 0; a < 4; ++a) {
-                const float ta = tr[a][jj];
-#pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    u[a][b] = fmaf(ta * bj, vj[b], u[a][b]);
-                    w[a][b] = fmaf(ta * bgj, kj[b], w[a][b]);
-                }
+            for (int e = 0; e < 4; ++e) {
+                const int r = 4 * m + e, k = acc_row(r, half);
+                u = mfma_f32(a[e], L.beta[k] * L.Q[k * RS + cw0 + col], u);
+                w = mfma_f32(a[e], L.bg[k] * L.K[k * RS + cw0 + col], w);
             }
         }
-    }
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-        *(f32x4*)(out + kWsW + (oi0 + a) * GD + oc0) = w[a];
-        *(f32x4*)(out + kWsU + (oi0 + a) * GD + oc0) = u[a];
+        for (int r = 0; r < 16; ++r) {
+            out[kWsU + acc_row(r, half) * GD + cw0 + col] = u[r];
+            out[kWsW + acc_row(r, half) * GD + cw0 + col] = w[r];
+        }
     }
 }
 
@@ -696,8 +687,6 @@ __global__ __launch_bounds__(GT) void gdn_dw_s0_kernel(GdnDev p, const float* __
     store_acc<0>(acc_mat(dwo + chn * GC * GD, GC, half, 32 * wave + col), -w);
 }
 
-constexpr int RR = GC + 1;        // row stride of the per-wave 32 x 32 partials
-
 struct ChunkGradLds {
     float Qs[GC * RS];    // q^ * scale
     float Ks[GC * RS];    // k^
@@ -714,34 +703,6 @@ struct ChunkGradLds {
     float Grow[GC];
     float Crow[GC];
 };
-
-// fp32 MFMA operands from LDS, in the k order of mfma_f32 (step r pairs
-// k = acc_row(r, 0) on lanes 0-31 with k = acc_row(r, 1) on lanes 32-63).
-// Row operand X[col][kb + k]: four steps per 16-byte read.
-__device__ __forceinline__ f32x4 op_row4(const float* X, int stride, int col, int half, int kb, int m) {
-    return *(const f32x4*)&X[col * stride + kb + 8 * m + 4 * half];
-}
-// Column operand X[kb + k][c0 + col], one step.
-__device__ __forceinline__ float op_col(const float* X, int stride, int half, int kb, int r, int c0, int col) {
-    return X[(kb + acc_row(r, half)) * stride + c0 + col];
-}
-// 32 x 32 partial product over this wave's quarter of a 128-deep contraction:
-// D[i][j] = sum_k A[i][k] B[j][k] (both read as rows), B scaled by bs (a
-// per-column factor), added to acc.
-__device__ __forceinline__ f32x16 quarter_nt(const float* A, const float* B, float bs, int col, int half, int wave,
-                                             f32x16 acc) {
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        const f32x4 a = op_row4(A, RS, col, half, 32 * wave, m), b = op_row4(B, RS, col, half, 32 * wave, m);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc = mfma_f32(a[e], b[e] * bs, acc);
-    }
-    return acc;
-}
-__device__ __forceinline__ void put_partial(float* R, const f32x16& acc, int col, int half) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) R[acc_row(r, half) * RR + col] = acc[r];
-}
 
 // Thread t owns row i = t/8 of the element-wise work: in [GC x GD] results
 // the columns 32m + 4s + e (s = t%8, m, e < 4), in [GC x GC] results s + 8e.

@@ -13,6 +13,7 @@ constexpr int GC = TT_GDN_CHUNK;  // chunk length (32)
 constexpr int GT = 256;           // threads per workgroup
 constexpr int RS = GD + 4;        // row stride of [GC x GD] tiles (floats): rows 4 banks apart
 constexpr int MS = GC + 4;        // row stride of [GC x GC] matrices
+constexpr int RR = GC + 1;        // row stride of per-wave 32 x 32 partial products
 
 // Workspace per (chunk, v head), floats: W [GC][GD], U [GC][GD], A [GC][GC],
 // T [GC][GC] (the inverse, for the backward), G [GC].
@@ -184,6 +185,34 @@ __device__ __forceinline__ void tile_in(const T* base, int64_t row_stride, int l
     }
 #pragma unroll
     for (int e = 0; e < 16; e += 4) *(f32x4*)&dst[i * RS + d0 + e] = (f32x4){x[e], x[e + 1], x[e + 2], x[e + 3]};
+}
+
+// fp32 MFMA operands from LDS, in the k order of mfma_f32 (step r pairs
+// k = acc_row(r, 0) on lanes 0-31 with k = acc_row(r, 1) on lanes 32-63).
+// Row operand X[col][kb + k]: four steps per 16-byte read.
+__device__ __forceinline__ f32x4 op_row4(const float* X, int stride, int col, int half, int kb, int m) {
+    return *(const f32x4*)&X[col * stride + kb + 8 * m + 4 * half];
+}
+// Column operand X[kb + k][c0 + col], one step.
+__device__ __forceinline__ float op_col(const float* X, int stride, int half, int kb, int r, int c0, int col) {
+    return X[(kb + acc_row(r, half)) * stride + c0 + col];
+}
+// 32 x 32 partial product over this wave's quarter of a 128-deep contraction:
+// D[i][j] = sum_k A[i][k] B[j][k] (both read as rows), B scaled by bs (a
+// per-column factor), added to acc.
+__device__ __forceinline__ f32x16 quarter_nt(const float* A, const float* B, float bs, int col, int half, int wave,
+                                             f32x16 acc) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const f32x4 a = op_row4(A, RS, col, half, 32 * wave, m), b = op_row4(B, RS, col, half, 32 * wave, m);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = mfma_f32(a[e], b[e] * bs, acc);
+    }
+    return acc;
+}
+__device__ __forceinline__ void put_partial(float* R, const f32x16& acc, int col, int half) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) R[acc_row(r, half) * RR + col] = acc[r];
 }
 
 }  // namespace
