@@ -86,6 +86,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="agent16k",
                     choices=["agent16k", "gateway16k", "rollout48k", "gdn16k", "prologue16k", "leafce16k"])
+    ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp32"],
+                    help="attention workloads: element type of q/k/v/dO and the kernels' operands")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=3)
     ap.add_argument("--calibrate-copy-mb", type=int, default=0,
@@ -137,7 +139,7 @@ def main():
     T = sum(lens)
     P = visible_pairs(topo)
     g = torch.Generator(device=dev).manual_seed(0)
-    bf = torch.bfloat16
+    bf = torch.bfloat16 if args.dtype == "bf16" else torch.float32
     # token-major storage viewed as [1, H, T, D] (transformers layout)
     q = torch.randn(1, T, HQ, D, device=dev, generator=g, dtype=bf).transpose(1, 2)
     k = torch.randn(1, T, HKV, D, device=dev, generator=g, dtype=bf).transpose(1, 2)
@@ -244,7 +246,9 @@ def main():
     kernels = {}
     roofline = None
     if segments is None:
-        names = ["fwd_bf16_kernel", "bwd_dq_bf16_kernel", "bwd_dkdv_bf16_kernel"]
+        sfx = "bf16" if args.dtype == "bf16" else "f32"
+        names = [f"fwd_{sfx}_kernel", f"bwd_dq_{sfx}_kernel", f"bwd_dkdv_{sfx}_kernel"]
+        peak = PEAK_BF16_TFLOPS if args.dtype == "bf16" else PEAK_FP32_TFS
         useful = [4.0 * D * HQ * P, 4.0 * D * HQ * P, 4.0 * D * HQ * P]
         for j, name in enumerate(names):
             ms = statistics.mean(e[j].elapsed_time(e[j + 1]) for e in evs)
@@ -252,19 +256,21 @@ def main():
                              "useful_tflops": round(useful[j] / (ms * 1e-3) / 1e12, 2) if useful[j] else None}
         dom = max((n for n in names if kernels[n]["useful_tflops"]), key=lambda n: kernels[n]["ms"])
         ach = kernels[dom]["useful_tflops"]
-        roofline = {"bound": "mfma", "kernel": dom, "achieved": ach, "peak": PEAK_BF16_TFLOPS,
-                    "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4),
-                    "traffic": profiled_traffic(dom, args.workload),
+        roofline = {"bound": "mfma", "kernel": dom, "achieved": ach, "peak": peak,
+                    "unit": "TFLOP/s", "frac": round(ach / peak, 4),
+                    "traffic": profiled_traffic(dom, args.workload) if args.dtype == "bf16" else None,
                     "flops_per_launch": useful[names.index(dom)]}
         if dom == "bwd_dkdv_bf16_kernel":
             roofline["timed"] = "dK/dV pass: split-sum zero + bwd_dkdv_bf16_kernel + split-sum finalize"
+        if dom == "bwd_dq_f32_kernel":
+            roofline["timed"] = "dQ pass: bwd_delta_f32_kernel + bwd_dq_f32_kernel"
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.dtype == "bf16":
         cpu = cpu_baseline(topo, args.cpu_runs, args.workload)
 
     line = {
-        "metric": "tree-attn fwd+bwd useful TFLOP/s (16K-token DFS tree, bf16)",
+        "metric": f"tree-attn fwd+bwd useful TFLOP/s (16K-token DFS tree, {args.dtype})",
         "value": round(tflops, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -274,13 +280,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": args.dtype,
         "data": "synthetic (seeded topology and N(0,1) q/k/v/dO)",
         "config": {"workload": args.workload, "packed_tokens": T, "visible_pairs_per_head": P,
                    "n_nodes": len(lens), "heads_q": HQ, "heads_kv": HKV, "head_dim": D,
                    "layer": "one Qwen3-4B-shaped GQA attention layer", "parallelism": "single GPU"},
         "tokens_per_s": round(tokens_s, 1),
-        "frac_of_bf16_peak": round(tflops / PEAK_BF16_TFLOPS, 4),
+        "frac_of_peak": round(tflops / (PEAK_BF16_TFLOPS if args.dtype == "bf16" else PEAK_FP32_TFS), 4),
         "wall_s_timed": round(wall, 3),
         "kernels": kernels,
         "roofline": roofline,

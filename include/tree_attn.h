@@ -147,8 +147,8 @@ int tt_trees_build(const tt_tree_job* jobs, int32_t n_jobs, void* stream);
  * the `k_past/v_past` segment, read in place. */
 typedef struct tt_tensor {
     const void* ptr;        /* element [t][h][d] at ptr + t*stride_tok + h*stride_head + d */
-    int64_t stride_tok;     /* in elements; >= 128, and < 2^23 for bf16 */
-    int64_t stride_head;    /* in elements; >= 128 */
+    int64_t stride_tok;     /* in elements; >= 128, a multiple of 8 (bf16) or 4 (fp32), < 2^23 (bf16) or 2^22 (fp32) */
+    int64_t stride_head;    /* in elements; >= 128, a multiple of 8 (bf16) or 4 (fp32); ptr 16-byte aligned */
 } tt_tensor;
 
 typedef struct tt_attn_problem {
@@ -182,12 +182,12 @@ int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* stream);
  * calls may share accumulators only when ordered on one stream: two calls in
  * flight at once on different streams must not add into the same
  * accumulators.
- * ws must be 16-byte aligned. float32 problems are deterministic (one writer
- * per output element). bf16 problems are too, except that keys whose visible
- * query range spans more than W queries, W = half the largest power of two
- * <= n_q clamped to [256, 4096] (split into several work items), sum their
- * dK/dV partials with fp32 atomics, so their rounding can vary from run to
- * run. With TT_BWD_DETERMINISTIC in bwd_parts each of those work items
+ * ws must be 16-byte aligned. dq has one writer per element (deterministic);
+ * so do dk and dv, except that keys whose visible query range spans more
+ * than W queries, W = half the largest power of two <= n_q clamped to
+ * [256, 4096] (split into several work items), sum their dK/dV partials
+ * with fp32 atomics, so their rounding can vary from run to run (both
+ * dtypes). With TT_BWD_DETERMINISTIC in bwd_parts each of those work items
  * stores its partial sums in a slot of its own and one pass adds them in
  * work-item order: no atomics, bitwise-repeatable dk, dv and gateway sums.
  * The workspace (tt_attn_bwd_workspace_bytes of the problem with the bit set)
@@ -206,7 +206,7 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
  * TT_NOALLOC_SCRATCH_MB MiB that the library holds on each GPU it runs on
  * until the process ends (the current device's, hipGetDevice; `stream` must
  * belong to it). A problem whose tt_attn_bwd_workspace_bytes exceeds it
- * returns TT_E_WORKSPACE (bf16 needs 128 * Hq * n_q + 1024 * Hkv * (n_q +
+ * returns TT_E_WORKSPACE (either dtype needs 128 * Hq * n_q + 1024 * Hkv * (n_q +
  * n_past) bytes: about 8K keys at Hq = 32, Hkv = 8). The call allocates and
  * frees nothing (no hipMalloc, no hipMemsetAsync: what must start at zero is
  * cleared by a kernel). Every call on one GPU uses that GPU's one scratch

@@ -91,10 +91,10 @@ def _qch(n_q):
 
 @pytest.mark.parametrize("n_q,n_past", [(100, 0), (600, 0), (16318, 0), (5300, 300), (50109, 0)])
 def test_bwd_deterministic_workspace(n_q, n_past):
-    """TT_BWD_DETERMINISTIC adds, for bf16, one dK and one dV slot of 128 keys
-    x Hkv x 128 fp32 for each possible work item beyond the first of a key
-    tile: ceil(n_keys / 128) * floor((n_q - 1) / W) of them (W: the work
-    item's query window); fp32 problems need nothing more."""
+    """TT_BWD_DETERMINISTIC adds one dK and one dV slot of 128 keys x Hkv x
+    128 fp32 for each possible work item beyond the first of a key tile:
+    ceil(n_keys / 128) * floor((n_q - 1) / W) of them (W: the work item's
+    query window); bf16 and fp32 problems share the layout."""
     lib = _lib.lib()
     base = _problem(n_q=n_q, n_past=n_past)
     det = _problem(n_q=n_q, n_past=n_past, bwd_parts=_lib.TT_BWD_DETERMINISTIC)
@@ -103,9 +103,10 @@ def test_bwd_deterministic_workspace(n_q, n_past):
     assert lib.tt_attn_bwd_workspace_bytes(ctypes.byref(det)) - \
         lib.tt_attn_bwd_workspace_bytes(ctypes.byref(base)) == extra
     assert (extra == 0) == (n_q <= 256 or n_q - 1 < _qch(n_q))
+    sizes = [lib.tt_attn_bwd_workspace_bytes(ctypes.byref(p)) for p in (base, det)]
     for p in (base, det):
         p.dtype = _lib.TT_DTYPE_F32
-    assert lib.tt_attn_bwd_workspace_bytes(ctypes.byref(det)) == lib.tt_attn_bwd_workspace_bytes(ctypes.byref(base))
+    assert [lib.tt_attn_bwd_workspace_bytes(ctypes.byref(p)) for p in (base, det)] == sizes
 
 
 def test_bwd_parts_validation():

@@ -13,8 +13,9 @@ causal attention over that path's tokens. So for sampled leaves:
 And the 16K tree cut into tree_grad_hybrid's 4096-token partitions, each
 attending to its gateway prefix, gives the whole tree's outputs and gradients
 (gateway gradients accumulated in fp32 and scattered back to their tokens).
-Bars: bf16 max_rel < 2e-2 (max |error| over max |reference|) for o, dq, dk,
-dv; |lse error| < 2e-2.
+Bars: max_rel (max |error| over max |reference|) < 2e-2 for bf16, 1e-5 for
+fp32 (the 16K tree only), for o, dq, dk, dv; |lse error| < 2e-2 (bf16), 1e-4
+(fp32, natural-log units of values near 8).
 """
 import numpy as np
 import pytest
@@ -73,14 +74,16 @@ def _max_rel(ref, got):
     return float((got - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
 
 
-@pytest.mark.parametrize("workload,n_paths", [("agent16k", 3), ("rollout48k", 2)])
-def test_attention_full_size_per_path(workload, n_paths):
+@pytest.mark.parametrize("workload,n_paths,dt", [("agent16k", 3, "bf16"), ("rollout48k", 2, "bf16"),
+                                                 ("agent16k", 3, "fp32")])
+def test_attention_full_size_per_path(workload, n_paths, dt):
     from tree_training_amd.attention import attn_backward, attn_forward
     from tree_training_amd.meta import KeyPlan, TreeMetaDevice
     lens, par = workloads.agent_tree(0) if workload == "agent16k" else workloads.rollout_tree(0)
     T = sum(lens)
     g = torch.Generator(device=DEV).manual_seed(3)
-    bf = torch.bfloat16
+    bf = torch.bfloat16 if dt == "bf16" else torch.float32
+    bar = 2e-2 if dt == "bf16" else 1e-5
     q = torch.randn(T, HQ, D, device=DEV, generator=g, dtype=bf)
     k = torch.randn(T, HKV, D, device=DEV, generator=g, dtype=bf)
     v = torch.randn(T, HKV, D, device=DEV, generator=g, dtype=bf)
@@ -101,13 +104,16 @@ def test_attention_full_size_per_path(workload, n_paths):
         ro, rlse, rdq, rdk, rdv = _causal_reference(q[ti].float(), k[ti].float(), v[ti].float(),
                                                     do[ti].float(), scale)
         torch.cuda.synchronize()
-        assert _max_rel(ro, o[ti].float()) < 2e-2
-        assert float((lse[:, ti] - rlse).abs().max()) < 2e-2
+        r = _max_rel(ro, o[ti].float())
+        print(f"  o max_rel {r:.2e}", flush=True)
+        assert r < bar
+        assert float((lse[:, ti] - rlse).abs().max()) < (2e-2 if dt == "bf16" else 1e-4)
         for name, ref, got in (("dq", rdq, dq), ("dk", rdk, dk), ("dv", rdv, dv)):
             gf = got.float()
             assert torch.isfinite(gf).all(), name
             r = _max_rel(ref, gf[ti])
-            assert r < 2e-2, (workload, int(leaf), name, r)
+            print(f"  {name} max_rel {r:.2e}", flush=True)
+            assert r < bar, (workload, int(leaf), name, r)
             off = torch.ones(T, dtype=torch.bool, device=DEV)
             off[ti] = False
             assert not gf[off].any(), (workload, int(leaf), name, "non-zero off the path")

@@ -7,7 +7,8 @@
 namespace {
 
 constexpr int kAbiVersion = 3;
-constexpr int64_t kMaxTokStride = int64_t(1) << 23;   // elements
+constexpr int64_t kMaxTokStride = int64_t(1) << 23;   // elements (bf16; half that for fp32)
+inline int64_t max_tok_stride(int dtype) { return dtype == TT_DTYPE_BF16 ? kMaxTokStride : kMaxTokStride / 2; }
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
@@ -25,17 +26,17 @@ int make_dev(const tt_attn_problem* p, AttnDev* a) {
     if (p->n_past > 0 && (!p->k_past.ptr || !p->v_past.ptr)) return TT_E_ARG;
     const int n_keys = p->n_q + p->n_past;
     if (p->plan_bytes < tt_plan_bytes_impl(p->n_q, n_keys)) return TT_E_WORKSPACE;
-    // bf16 kernels read 16-byte vectors: 8-element granularity for strides.
-    const int64_t gran = p->dtype == TT_DTYPE_BF16 ? 8 : 1;
-    const size_t ealign = p->dtype == TT_DTYPE_BF16 ? 16 : 4;
+    // the kernels read 16-byte vectors: 8 (bf16) or 4 (fp32) element granularity for strides
+    const int64_t gran = p->dtype == TT_DTYPE_BF16 ? 8 : 4;
+    const size_t ealign = 16;
     const tt_tensor* ts[5] = {&p->q, &p->k, &p->v, &p->k_past, &p->v_past};
     const int nt = p->n_past > 0 ? 5 : 3;
     for (int i = 0; i < nt; ++i) {
         const tt_tensor* t = ts[i];
         if (t->stride_tok < 128 || t->stride_head < 128 || (t->stride_tok % gran) || (t->stride_head % gran))
             return TT_E_ARG;
-        // bf16 kernels address a tile of up to 128 rows with 32-bit byte offsets
-        if (p->dtype == TT_DTYPE_BF16 && t->stride_tok >= kMaxTokStride) return TT_E_ARG;
+        // the kernels address a tile of up to 128 rows with 32-bit byte offsets
+        if (t->stride_tok >= max_tok_stride(p->dtype)) return TT_E_ARG;
         if (!aligned(t->ptr, ealign)) return TT_E_ARG;
     }
     a->q = p->q.ptr; a->q_st = p->q.stride_tok; a->q_sh = p->q.stride_head;
@@ -152,10 +153,8 @@ int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* stream) {
     int rc = make_dev(p, &a);
     if (rc != TT_OK) return rc;
     if (!o || !lse) return TT_E_ARG;
-    if (p->dtype == TT_DTYPE_BF16) {
-        if (!aligned(o, 16)) return TT_E_ARG;
-        return tt_fwd_bf16_launch(a, o, lse, (hipStream_t)stream);
-    }
+    if (!aligned(o, 16)) return TT_E_ARG;
+    if (p->dtype == TT_DTYPE_BF16) return tt_fwd_bf16_launch(a, o, lse, (hipStream_t)stream);
     return tt_fwd_f32_launch(a, o, lse, (hipStream_t)stream);
 }
 
@@ -176,11 +175,8 @@ static size_t det_slot_bytes(const tt_attn_problem* p) {
 size_t tt_attn_bwd_workspace_bytes(const tt_attn_problem* p) {
     if (!p || p->n_q < 1 || p->n_heads_q < 1 || p->n_heads_kv < 1 || p->n_past < 0) return 0;
     if ((int64_t)p->n_q + p->n_past > 0x3fffffff) return 0;
-    size_t b = delta_bytes(p);
-    if (p->dtype == TT_DTYPE_BF16) {
-        b += 2 * split_rows_bytes(p);
-        if (p->bwd_parts & TT_BWD_DETERMINISTIC) b += 2 * det_slot_bytes(p);
-    }
+    size_t b = delta_bytes(p) + 2 * split_rows_bytes(p);
+    if (p->bwd_parts & TT_BWD_DETERMINISTIC) b += 2 * det_slot_bytes(p);
     return b;
 }
 
@@ -192,11 +188,11 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
     if (!o || !lse || !d_o.ptr || !dq || !dk || !dv || !ws) return TT_E_ARG;
     if ((dk_past_acc == nullptr) != (dv_past_acc == nullptr)) return TT_E_ARG;
     if (ws_bytes < tt_attn_bwd_workspace_bytes(p)) return TT_E_WORKSPACE;
-    const int64_t gran = p->dtype == TT_DTYPE_BF16 ? 8 : 1;
-    const size_t ealign = p->dtype == TT_DTYPE_BF16 ? 16 : 4;
+    const int64_t gran = p->dtype == TT_DTYPE_BF16 ? 8 : 4;
+    const size_t ealign = 16;
     if (d_o.stride_tok < 128 || d_o.stride_head < 128 || (d_o.stride_tok % gran) || (d_o.stride_head % gran))
         return TT_E_ARG;
-    if (p->dtype == TT_DTYPE_BF16 && d_o.stride_tok >= kMaxTokStride) return TT_E_ARG;
+    if (d_o.stride_tok >= max_tok_stride(p->dtype)) return TT_E_ARG;
     if (!aligned(d_o.ptr, ealign) || !aligned(o, ealign) || !aligned(dq, ealign) || !aligned(dk, ealign) ||
         !aligned(dv, ealign) || !aligned(ws, 16) || !aligned(dk_past_acc, 16) || !aligned(dv_past_acc, 16))
         return TT_E_ARG;
@@ -215,7 +211,7 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
     if (p->bwd_parts & ~(TT_BWD_DELTA | TT_BWD_DQ | TT_BWD_DKDV | TT_BWD_DETERMINISTIC)) return TT_E_ARG;
     b.det = (p->bwd_parts & TT_BWD_DETERMINISTIC) ? 1 : 0;
     b.dk_ws = b.dv_ws = b.dk_slot = b.dv_slot = nullptr;
-    if (p->dtype == TT_DTYPE_BF16) {
+    {
         uint8_t* w = reinterpret_cast<uint8_t*>(ws) + delta_bytes(p);
         b.dk_ws = reinterpret_cast<float*>(w);
         b.dv_ws = reinterpret_cast<float*>(w + split_rows_bytes(p));

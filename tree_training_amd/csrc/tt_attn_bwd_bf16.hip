@@ -411,81 +411,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
     }
 }
 
-// Split key tiles: zero the fp32 sums of their own keys before the dK/dV pass
-// (split gateway keys add straight into the caller's fp32 accumulators) ...
-// (16-byte vectors: the workspace and the gateway accumulators are 16-byte
-// aligned and rows are 128 floats)
-__global__ __launch_bounds__(256) void bwd_split_zero_kernel(AttnDev a, BwdDev bw) {
-    const int kb = blockIdx.x, g = blockIdx.y;
-    if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb], tt_qch(a.n_q)) <= 1) return;
-    const int k_first = max(kb * TT_BKB, a.n_past), k_end = min(kb * TT_BKB + TT_BKB, a.n_keys);
-    for (int e = threadIdx.x; e < (k_end - k_first) * (D / 4); e += 256) {
-        const int key = k_first + e / (D / 4);
-        const size_t idx = ((size_t)key * a.hkv + g) * D + 4 * (e % (D / 4));
-        *(f32x4*)(bw.dk_ws + idx) = (f32x4){};
-        *(f32x4*)(bw.dv_ws + idx) = (f32x4){};
-    }
-}
-
-// ... and convert them to dk/dv after it.
-__global__ __launch_bounds__(256) void bwd_split_finalize_kernel(AttnDev a, BwdDev bw) {
-    const int kb = blockIdx.x, g = blockIdx.y;
-    if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb], tt_qch(a.n_q)) <= 1) return;
-    const int k_first = max(kb * TT_BKB, a.n_past), k_end = min(kb * TT_BKB + TT_BKB, a.n_keys);
-    for (int e = threadIdx.x; e < (k_end - k_first) * (D / 4); e += 256) {
-        const int key = k_first + e / (D / 4), d = 4 * (e % (D / 4));
-        const size_t widx = ((size_t)key * a.hkv + g) * D + d;
-        const f32x4 gk = *(const f32x4*)(bw.dk_ws + widx), gv = *(const f32x4*)(bw.dv_ws + widx);
-        const size_t idx = ((size_t)(key - a.n_past) * a.hkv + g) * D + d;
-        bf16x4 wk, wv;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            wk[i] = (bf16)gk[i];
-            wv[i] = (bf16)gv[i];
-        }
-        *(bf16x4*)((bf16*)bw.dk + idx) = wk;
-        *(bf16x4*)((bf16*)bw.dv + idx) = wv;
-    }
-}
-
-// Deterministic mode: one workgroup per (key tile rank, kv head) sums a split
-// tile's partials in item order (first item's in the fp32 rows, then the
-// slots) and writes dk/dv, or adds gateway keys' sums to the accumulators.
-__global__ __launch_bounds__(256) void bwd_split_finalize_det_kernel(AttnDev a, BwdDev bw) {
-    const int rank = blockIdx.x, g = blockIdx.y;
-    const int kb = a.kb_order[rank];
-    const int m = tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb], tt_qch(a.n_q));
-    if (m <= 1) return;
-    const int k_first = kb * TT_BKB, k_end = min(kb * TT_BKB + TT_BKB, a.n_keys);
-    const int64_t slot0 = (int64_t)(a.kb_base[rank] - rank) * TT_BKB;   // slot rows of the tile's second item
-    for (int e = threadIdx.x; e < (k_end - k_first) * (D / 4); e += 256) {
-        const int key = k_first + e / (D / 4), d = 4 * (e % (D / 4));
-        const size_t widx = ((size_t)key * a.hkv + g) * D + d;
-        f32x4 gk = *(const f32x4*)(bw.dk_ws + widx), gv = *(const f32x4*)(bw.dv_ws + widx);
-        for (int c = 1; c < m; ++c) {
-            const size_t sidx = ((size_t)(slot0 + (int64_t)(c - 1) * TT_BKB + key - k_first) * a.hkv + g) * D + d;
-            gk += *(const f32x4*)(bw.dk_slot + sidx);
-            gv += *(const f32x4*)(bw.dv_slot + sidx);
-        }
-        if (key < a.n_past) {
-            if (bw.dk_acc) {
-                *(f32x4*)(bw.dk_acc + widx) += gk;
-                *(f32x4*)(bw.dv_acc + widx) += gv;
-            }
-            continue;
-        }
-        const size_t idx = ((size_t)(key - a.n_past) * a.hkv + g) * D + d;
-        bf16x4 wk, wv;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            wk[i] = (bf16)gk[i];
-            wv[i] = (bf16)gv[i];
-        }
-        *(bf16x4*)((bf16*)bw.dk + idx) = wk;
-        *(bf16x4*)((bf16*)bw.dv + idx) = wv;
-    }
-}
-
 // Device self-test of the MFMA lane layout every bf16 kernel above relies on:
 // D = A[32x16] * B[16x32] (row-major bf16), written back through acc_row().
 __global__ __launch_bounds__(64) void selftest_mfma_kernel(const bf16* __restrict__ A, const bf16* __restrict__ B,
@@ -538,11 +463,11 @@ int tt_bwd_bf16_launch(const AttnDev& a, const BwdDev& b, hipStream_t s) {
     if (b.parts & TT_BWD_DKDV) {
         if (b.det) {
             hipLaunchKernelGGL(bwd_dkdv_bf16_kernel, dim3(dkdv_grid(a)), dim3(256), 0, s, a, b);
-            hipLaunchKernelGGL(bwd_split_finalize_det_kernel, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
+            hipLaunchKernelGGL(bwd_split_finalize_det_kernel<bf16>, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
         } else {
             hipLaunchKernelGGL(bwd_split_zero_kernel, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
             hipLaunchKernelGGL(bwd_dkdv_bf16_kernel, dim3(dkdv_grid(a)), dim3(256), 0, s, a, b);
-            hipLaunchKernelGGL(bwd_split_finalize_kernel, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
+            hipLaunchKernelGGL(bwd_split_finalize_kernel<bf16>, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
         }
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }

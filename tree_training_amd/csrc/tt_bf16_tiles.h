@@ -321,4 +321,83 @@ __device__ __forceinline__ void decode_qblock(const AttnDev& a, int& qb, int& h)
 }
 
 
+// Four fp32 values into element idx.. of a bf16 or fp32 output.
+template <typename TOut>
+__device__ __forceinline__ void store_out4(void* base, size_t idx, const f32x4& x) {
+    if constexpr (sizeof(TOut) == 2) {
+        bf16x4 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = (bf16)x[i];
+        *(bf16x4*)((bf16*)base + idx) = w;
+    } else {
+        *(f32x4*)((float*)base + idx) = x;
+    }
+}
+
+// Split key tiles: zero the fp32 sums of their own keys before the dK/dV pass
+// (split gateway keys add straight into the caller's fp32 accumulators) ...
+// (16-byte vectors: the workspace and the gateway accumulators are 16-byte
+// aligned and rows are 128 floats)
+__global__ __launch_bounds__(256) void bwd_split_zero_kernel(AttnDev a, BwdDev bw) {
+    const int kb = blockIdx.x, g = blockIdx.y;
+    if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb], tt_qch(a.n_q)) <= 1) return;
+    const int k_first = max(kb * TT_BKB, a.n_past), k_end = min(kb * TT_BKB + TT_BKB, a.n_keys);
+    for (int e = threadIdx.x; e < (k_end - k_first) * (D / 4); e += 256) {
+        const int key = k_first + e / (D / 4);
+        const size_t idx = ((size_t)key * a.hkv + g) * D + 4 * (e % (D / 4));
+        *(f32x4*)(bw.dk_ws + idx) = (f32x4){};
+        *(f32x4*)(bw.dv_ws + idx) = (f32x4){};
+    }
+}
+
+// ... and convert them to dk/dv after it.
+template <typename TOut>
+__global__ __launch_bounds__(256) void bwd_split_finalize_kernel(AttnDev a, BwdDev bw) {
+    const int kb = blockIdx.x, g = blockIdx.y;
+    if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb], tt_qch(a.n_q)) <= 1) return;
+    const int k_first = max(kb * TT_BKB, a.n_past), k_end = min(kb * TT_BKB + TT_BKB, a.n_keys);
+    for (int e = threadIdx.x; e < (k_end - k_first) * (D / 4); e += 256) {
+        const int key = k_first + e / (D / 4), d = 4 * (e % (D / 4));
+        const size_t widx = ((size_t)key * a.hkv + g) * D + d;
+        const f32x4 gk = *(const f32x4*)(bw.dk_ws + widx), gv = *(const f32x4*)(bw.dv_ws + widx);
+        const size_t idx = ((size_t)(key - a.n_past) * a.hkv + g) * D + d;
+        store_out4<TOut>(bw.dk, idx, gk);
+        store_out4<TOut>(bw.dv, idx, gv);
+    }
+}
+
+// Deterministic mode: one workgroup per (key tile rank, kv head) sums a split
+// tile's partials in item order (first item's in the fp32 rows, then the
+// slots) and writes dk/dv, or adds gateway keys' sums to the accumulators.
+template <typename TOut>
+__global__ __launch_bounds__(256) void bwd_split_finalize_det_kernel(AttnDev a, BwdDev bw) {
+    const int rank = blockIdx.x, g = blockIdx.y;
+    const int kb = a.kb_order[rank];
+    const int m = tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb], tt_qch(a.n_q));
+    if (m <= 1) return;
+    const int k_first = kb * TT_BKB, k_end = min(kb * TT_BKB + TT_BKB, a.n_keys);
+    const int64_t slot0 = (int64_t)(a.kb_base[rank] - rank) * TT_BKB;   // slot rows of the tile's second item
+    for (int e = threadIdx.x; e < (k_end - k_first) * (D / 4); e += 256) {
+        const int key = k_first + e / (D / 4), d = 4 * (e % (D / 4));
+        const size_t widx = ((size_t)key * a.hkv + g) * D + d;
+        f32x4 gk = *(const f32x4*)(bw.dk_ws + widx), gv = *(const f32x4*)(bw.dv_ws + widx);
+        for (int c = 1; c < m; ++c) {
+            const size_t sidx = ((size_t)(slot0 + (int64_t)(c - 1) * TT_BKB + key - k_first) * a.hkv + g) * D + d;
+            gk += *(const f32x4*)(bw.dk_slot + sidx);
+            gv += *(const f32x4*)(bw.dv_slot + sidx);
+        }
+        if (key < a.n_past) {
+            if (bw.dk_acc) {
+                *(f32x4*)(bw.dk_acc + widx) += gk;
+                *(f32x4*)(bw.dv_acc + widx) += gv;
+            }
+            continue;
+        }
+        const size_t idx = ((size_t)(key - a.n_past) * a.hkv + g) * D + d;
+        store_out4<TOut>(bw.dk, idx, gk);
+        store_out4<TOut>(bw.dv, idx, gv);
+    }
+}
+
+
 }  // namespace
