@@ -278,7 +278,9 @@ int tt_qk_prologue_bwd(const tt_prologue_problem* p, tt_tensor dq_out, tt_tensor
  * node of chunk c (n_chunks in all). level_nodes lists every node once,
  * grouped by depth (roots first); level_offsets (HOST memory, n_levels + 1
  * entries, level_offsets[n_levels] = n_nodes) delimits the groups. A node
- * whose parent is not in an earlier group reads an undefined state. */
+ * whose parent is not in an earlier group reads an undefined state. Within a
+ * group the scans start nodes in the order given: longest first finishes a
+ * level soonest. */
 #define TT_GDN_CHUNK 32
 typedef struct tt_gdn_problem {
     int32_t dtype;          /* TT_DTYPE_BF16 or TT_DTYPE_F32 for q, k, v and o */

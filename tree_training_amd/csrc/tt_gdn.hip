@@ -187,9 +187,9 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                                                       TIn* __restrict__ out, float* __restrict__ states,
                                                       float* __restrict__ chunk_sin, float* __restrict__ chunk_vp) {
     __shared__ __attribute__((aligned(16))) ScanLds L;
-    const int node = p.level_nodes[lvl_begin + blockIdx.x];
+    const int node = p.level_nodes[lvl_begin + blockIdx.y];
     if (node < 0 || node >= p.n_nodes) return;
-    const int h = blockIdx.y;
+    const int h = blockIdx.x;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, col = lane & 31, half = lane >> 5;
     const int j = 32 * wave + col;                                        // this lane's value column
     const int start = p.node_start[node], len = p.node_len[node], chunk0 = p.node_chunk0[node];
@@ -370,9 +370,9 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         GdnDev p, int lvl_begin, const float* __restrict__ ws, const TIn* __restrict__ d_o, int64_t do_st,
         int64_t do_sh, float* __restrict__ chunk_dso, float* __restrict__ chunk_dvp, float* __restrict__ node_dsin) {
     __shared__ __attribute__((aligned(16))) RscanLds L;
-    const int node = p.level_nodes[lvl_begin + blockIdx.x];
+    const int node = p.level_nodes[lvl_begin + blockIdx.y];
     if (node < 0 || node >= p.n_nodes) return;
-    const int h = blockIdx.y;
+    const int h = blockIdx.x;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, col = lane & 31, half = lane >> 5;
     const int j = 32 * wave + col;
     const int start = p.node_start[node], len = p.node_len[node], chunk0 = p.node_chunk0[node];
@@ -1043,6 +1043,8 @@ size_t tt_gdn_ws_bytes_impl(int n_chunks, int n_heads_v, bool trunc) {
 }
 
 namespace {
+constexpr int kMaxGridY = 65535;   // grid y limit: a level's nodes beyond it go to further launches
+
 template <typename TIn, bool TRUNC>
 void launch_prep(const GdnDev& d, float* prep, hipStream_t s) {
     hipLaunchKernelGGL((gdn_prep_kernel<TIn, TRUNC>), dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, prep);
@@ -1050,8 +1052,10 @@ void launch_prep(const GdnDev& d, float* prep, hipStream_t s) {
 template <typename TIn, bool TRUNC>
 void launch_scan(const GdnDev& d, int b, int n, float* prep, TIn* out, float* states, float* sin, float* vp,
                  hipStream_t s) {
-    hipLaunchKernelGGL((gdn_scan_kernel<TIn, TRUNC>), dim3(n, d.hv), dim3(GT), 0, s, d, b, prep, out, states, sin,
-                       vp);
+    // grid (v head, node): all heads of a level's first (longest) nodes are dispatched first
+    for (int b0 = 0; b0 < n; b0 += kMaxGridY)
+        hipLaunchKernelGGL((gdn_scan_kernel<TIn, TRUNC>), dim3(d.hv, min(kMaxGridY, n - b0)), dim3(GT), 0, s, d,
+                           b + b0, prep, out, states, sin, vp);
 }
 
 // The forward: chunk terms (prep; TRUNC: plus the node-level U, W), then one
@@ -1182,8 +1186,9 @@ static int gdn_bwd_run(const GdnDev& d, const int32_t* level_offsets, int n_leve
     for (int l = n_levels - 1; l >= 0; --l) {
         const int b = level_offsets[l], n = level_offsets[l + 1] - b;
         if (n <= 0) continue;
-        hipLaunchKernelGGL((gdn_rscan_kernel<TIn, TRUNC>), dim3(n, d.hv), dim3(GT), 0, s, d, b, w.prep, d_o, do_st,
-                           do_sh, w.dso, w.dvp, w.dsn);
+        for (int b0 = 0; b0 < n; b0 += kMaxGridY)
+            hipLaunchKernelGGL((gdn_rscan_kernel<TIn, TRUNC>), dim3(d.hv, min(kMaxGridY, n - b0)), dim3(GT), 0, s, d,
+                               b + b0, w.prep, d_o, do_st, do_sh, w.dso, w.dvp, w.dsn);
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     hipLaunchKernelGGL(gdn_bwd_state_kernel<TIn>, dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, d_o, do_st, do_sh,

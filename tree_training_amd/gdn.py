@@ -57,6 +57,8 @@ class GdnTree:
         levels: List[List[int]] = [[] for _ in range(max(depth) + 1)]
         for i, d in enumerate(depth):
             levels[d].append(i)
+        for lv in levels:   # longest nodes first: the scan of a level dispatches them (all heads) first
+            lv.sort(key=lambda i: -self.node_len[i])
         order = [i for lv in levels for i in lv]
         offs = [0]
         for lv in levels:
