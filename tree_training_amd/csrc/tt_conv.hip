@@ -71,18 +71,42 @@ __device__ __forceinline__ void load_taps(const ConvDev& p, int c, float (&w)[4]
     }
 }
 
+// The window of consecutive tokens: when prev(t) is the previous token of the
+// run (inside a node), t's window is the last one shifted by a row, so only
+// x[t] is loaded; otherwise (a node's first token, the run's first) it is
+// gathered along the predecessor chain. The test is uniform over the
+// workgroup (every thread walks the same tokens).
 template <int K, typename T>
-__device__ __forceinline__ f32x4 preact(const ConvDev& p, int c, const int (&idx)[K], const float (&w)[4][K],
-                                        const float (&b)[4], f32x4 (&xv)[K]) {
-    f32x4 acc = {b[0], b[1], b[2], b[3]};
+struct SlidingWindow {
+    int idx[K];
+    f32x4 xv[K];
+    int last = -1;
+    __device__ __forceinline__ void advance(const ConvDev& p, int c, int t) {
+        if (last >= 0 && prev_of(p, t) == last) {
 #pragma unroll
-    for (int i = 0; i < K; ++i) {
-        xv[i] = idx[i] >= 0 ? ld4((const T*)p.x + (int64_t)idx[i] * p.x_st + c) : (f32x4){};
+            for (int i = 0; i < K - 1; ++i) {
+                idx[i] = idx[i + 1];
+                xv[i] = xv[i + 1];
+            }
+            idx[K - 1] = t;
+            xv[K - 1] = ld4((const T*)p.x + (int64_t)t * p.x_st + c);
+        } else {
+            window<K>(p, t, idx);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[e] = fmaf(w[e][i], xv[i][e], acc[e]);
+            for (int i = 0; i < K; ++i)
+                xv[i] = idx[i] >= 0 ? ld4((const T*)p.x + (int64_t)idx[i] * p.x_st + c) : (f32x4){};
+        }
+        last = t;
     }
-    return acc;
-}
+    __device__ __forceinline__ f32x4 preact(const float (&w)[4][K], const float (&b)[4]) const {
+        f32x4 acc = {b[0], b[1], b[2], b[3]};
+#pragma unroll
+        for (int i = 0; i < K; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = fmaf(w[e][i], xv[i][e], acc[e]);
+        return acc;
+    }
+};
 
 template <int K, typename T>
 __global__ __launch_bounds__(CT) void conv_fwd_kernel(ConvDev p, T* __restrict__ y, int64_t y_st) {
@@ -91,11 +115,10 @@ __global__ __launch_bounds__(CT) void conv_fwd_kernel(ConvDev p, T* __restrict__
     float w[4][K], b[4];
     load_taps<K, T>(p, c, w, b);
     const int t1 = min(p.n_tokens, (int)(blockIdx.x + 1) * CTOK);
+    SlidingWindow<K, T> win;
     for (int t = blockIdx.x * CTOK; t < t1; ++t) {
-        int idx[K];
-        window<K>(p, t, idx);
-        f32x4 xv[K];
-        const f32x4 z = preact<K, T>(p, c, idx, w, b, xv);
+        win.advance(p, c, t);
+        const f32x4 z = win.preact(w, b);
         f32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = z[e] / (1.0f + expf(-z[e]));
@@ -103,11 +126,12 @@ __global__ __launch_bounds__(CT) void conv_fwd_kernel(ConvDev p, T* __restrict__
     }
 }
 
-// gp = dy * silu'(pre) into the workspace, and per-workgroup partial sums of
+// gp = dy * silu'(pre) into the workspace (in the problem's dtype, as the
+// reference's bf16 autograd keeps this gradient), and per-workgroup partial sums of
 // dw (taps 0..K-1) and db (slot K): part[blockIdx.x][slot][c].
 template <int K, typename T>
 __global__ __launch_bounds__(CT) void conv_bwd_gp_kernel(ConvDev p, const T* __restrict__ dy, int64_t dy_st,
-                                                         float* __restrict__ gp, float* __restrict__ part) {
+                                                         T* __restrict__ gp, float* __restrict__ part) {
     const int c = 4 * (blockIdx.y * CT + threadIdx.x);
     if (c >= p.n_ch) return;
     float w[4][K], b[4];
@@ -116,11 +140,11 @@ __global__ __launch_bounds__(CT) void conv_bwd_gp_kernel(ConvDev p, const T* __r
 #pragma unroll
     for (int i = 0; i < K; ++i) aw[i] = (f32x4){};
     const int t1 = min(p.n_tokens, (int)(blockIdx.x + 1) * CTOK_W);
+    SlidingWindow<K, T> win;
     for (int t = blockIdx.x * CTOK_W; t < t1; ++t) {
-        int idx[K];
-        window<K>(p, t, idx);
-        f32x4 xv[K];
-        const f32x4 z = preact<K, T>(p, c, idx, w, b, xv);
+        win.advance(p, c, t);
+        const f32x4 z = win.preact(w, b);
+        const f32x4* xv = win.xv;
         const f32x4 d = ld4(dy + (int64_t)t * dy_st + c);
         f32x4 g;
 #pragma unroll
@@ -128,7 +152,7 @@ __global__ __launch_bounds__(CT) void conv_bwd_gp_kernel(ConvDev p, const T* __r
             const float s = 1.0f / (1.0f + expf(-z[e]));
             g[e] = d[e] * s * fmaf(z[e], 1.0f - s, 1.0f);
         }
-        *(f32x4*)(gp + (int64_t)t * p.n_ch + c) = g;
+        st4(gp + (int64_t)t * p.n_ch + c, g);
         ab += g;
 #pragma unroll
         for (int i = 0; i < K; ++i) aw[i] += g * xv[i];
@@ -141,14 +165,14 @@ __global__ __launch_bounds__(CT) void conv_bwd_gp_kernel(ConvDev p, const T* __r
 
 // dx[u] = sum over m < K of w[K-1-m] * (sum of gp over the tokens m steps after u).
 template <int K, typename T>
-__global__ __launch_bounds__(CT) void conv_bwd_dx_kernel(ConvDev p, const float* __restrict__ gp,
+__global__ __launch_bounds__(CT) void conv_bwd_dx_kernel(ConvDev p, const T* __restrict__ gp,
                                                          T* __restrict__ dx) {
     const int c = 4 * (blockIdx.y * CT + threadIdx.x);
     if (c >= p.n_ch) return;
     float w[4][K], b[4];
     load_taps<K, T>(p, c, w, b);
     const int t1 = min(p.n_tokens, (int)(blockIdx.x + 1) * CTOK);
-    auto g_at = [&](int t) { return *(const f32x4*)(gp + (int64_t)t * p.n_ch + c); };
+    auto g_at = [&](int t) { return ld4(gp + (int64_t)t * p.n_ch + c); };
     auto succ = [&](int t, int& lo, int& hi) {
         lo = max(p.next_off[t], 0);
         hi = min(p.next_off[t + 1], p.n_tokens);
@@ -217,13 +241,13 @@ template <int K, typename T>
 int conv_bwd_run(const ConvDev& d, const void* dy, int64_t dy_st, void* dx, float* dw, float* db, float* ws,
                  hipStream_t s) {
     const int n_parts = tt_cdiv(d.n_tokens, CTOK_W);
-    float* gp = ws;
+    T* gp = reinterpret_cast<T*>(ws);
     float* part = ws + (size_t)d.n_tokens * d.n_ch;
     hipLaunchKernelGGL((conv_bwd_gp_kernel<K, T>), dim3(n_parts, tt_cdiv(d.n_ch, CCH)), dim3(CT), 0, s, d,
                        (const T*)dy, dy_st, gp, part);
     if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     hipLaunchKernelGGL((conv_bwd_dx_kernel<K, T>), dim3(tt_cdiv(d.n_tokens, CTOK), tt_cdiv(d.n_ch, CCH)), dim3(CT),
-                       0, s, d, (const float*)gp, (T*)dx);
+                       0, s, d, (const T*)gp, (T*)dx);
     if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     hipLaunchKernelGGL(conv_bwd_reduce_kernel, dim3(tt_cdiv((K + 1) * d.n_ch, CT)), dim3(CT), 0, s,
                        (const float*)part, n_parts, d.n_ch, K, dw, db);
