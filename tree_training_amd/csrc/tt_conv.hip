@@ -219,13 +219,26 @@ __global__ __launch_bounds__(CT) void conv_bwd_dx_kernel(ConvDev p, const T* __r
 }
 
 // dw[c][i] and db[c] from the per-workgroup partials (fixed order: deterministic).
+// Sum of the per-workgroup partials: a workgroup takes RJ consecutive
+// (slot, channel) entries, its CT / RJ thread groups every (CT / RJ)-th partial
+// (in a fixed order: deterministic), summed through LDS.
+constexpr int RJ = 64;
 __global__ __launch_bounds__(CT) void conv_bwd_reduce_kernel(const float* __restrict__ part, int n_parts, int n_ch,
                                                              int K, float* __restrict__ dw, float* __restrict__ db) {
-    const int j = blockIdx.x * CT + threadIdx.x;
-    if (j >= (K + 1) * n_ch) return;
-    const int slot = j / n_ch, c = j - slot * n_ch;
+    __shared__ float red[CT];
+    const int total = (K + 1) * n_ch;
+    const int j = blockIdx.x * RJ + (threadIdx.x % RJ), grp = threadIdx.x / RJ;
     float s = 0.0f;
-    for (int b = 0; b < n_parts; ++b) s += part[(size_t)b * (K + 1) * n_ch + j];
+    if (j < total) {
+#pragma unroll 8
+        for (int b = grp; b < n_parts; b += CT / RJ) s += part[(size_t)b * total + j];
+    }
+    red[threadIdx.x] = s;
+    __syncthreads();
+    if (grp != 0 || j >= total) return;
+#pragma unroll
+    for (int g2 = 1; g2 < CT / RJ; ++g2) s += red[threadIdx.x + g2 * RJ];
+    const int slot = j / n_ch, c = j - slot * n_ch;
     if (slot < K) dw[(size_t)c * K + slot] = s;
     else if (db) db[c] = s;
 }
@@ -249,7 +262,7 @@ int conv_bwd_run(const ConvDev& d, const void* dy, int64_t dy_st, void* dx, floa
     hipLaunchKernelGGL((conv_bwd_dx_kernel<K, T>), dim3(tt_cdiv(d.n_tokens, CTOK), tt_cdiv(d.n_ch, CCH)), dim3(CT),
                        0, s, d, (const T*)gp, (T*)dx);
     if (hipGetLastError() != hipSuccess) return TT_E_HIP;
-    hipLaunchKernelGGL(conv_bwd_reduce_kernel, dim3(tt_cdiv((K + 1) * d.n_ch, CT)), dim3(CT), 0, s,
+    hipLaunchKernelGGL(conv_bwd_reduce_kernel, dim3(tt_cdiv((K + 1) * d.n_ch, RJ)), dim3(CT), 0, s,
                        (const float*)part, n_parts, d.n_ch, K, dw, db);
     return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
 }
