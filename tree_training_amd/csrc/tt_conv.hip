@@ -46,6 +46,12 @@ __device__ __forceinline__ void st4(T* p, const f32x4& x) {
     }
 }
 
+// sigmoid(z) = 1 / (1 + 2^(-z log2 e)) on the hardware exp2 and reciprocal
+// (v_exp_f32, v_rcp_f32: about 1 ulp each).
+__device__ __forceinline__ float sigmoid_fast(float z) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * TT_LOG2E));
+}
+
 __device__ __forceinline__ int prev_of(const ConvDev& p, int t) {
     if (t < 0) return -1;
     const int u = p.prev[t];
@@ -121,7 +127,7 @@ __global__ __launch_bounds__(CT) void conv_fwd_kernel(ConvDev p, T* __restrict__
         const f32x4 z = win.preact(w, b);
         f32x4 o;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = z[e] / (1.0f + expf(-z[e]));
+        for (int e = 0; e < 4; ++e) o[e] = z[e] * sigmoid_fast(z[e]);
         st4(y + (int64_t)t * y_st + c, o);
     }
 }
@@ -149,7 +155,7 @@ __global__ __launch_bounds__(CT) void conv_bwd_gp_kernel(ConvDev p, const T* __r
         f32x4 g;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const float s = 1.0f / (1.0f + expf(-z[e]));
+            const float s = sigmoid_fast(z[e]);
             g[e] = d[e] * s * fmaf(z[e], 1.0f - s, 1.0f);
         }
         st4(gp + (int64_t)t * p.n_ch + c, g);
