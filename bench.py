@@ -325,10 +325,13 @@ def run_leafce(args):
     labels = [torch.randint(0, V, (e - s,), device=dev, generator=gen) for s, e in spans]
     fn = TreeCELoss(labels, nodes, len(spans))
 
+    # Both paths start each step with unset gradients (zero_grad(set_to_none=True)).
     def fused_step():
+        hidden.grad = weight.grad = None
         fn.fused_spans(hidden, [(s, e, n) for (s, e), n in zip(spans, nodes)], weight).backward()
 
     def torch_step():
+        hidden.grad = weight.grad = None
         logits = (hidden @ weight.t())[None]
         loss = sum(fn(logits[:, s:e, :], n) for (s, e), n in zip(spans, nodes))
         loss.backward()
@@ -551,8 +554,11 @@ def run_gdn(args):
     tree = GdnTree(lens, par, dev)
 
     def step():
-        y = tree_conv(x, w, None, tree)
-        q, k, v = torch.split(y, [HK * D, HK * D, HV * D], dim=-1)
+        # Gradients start unset each step (an optimizer's zero_grad(set_to_none=True)),
+        # so backward writes them rather than adding into the last step's.
+        for t in (x, w, g, beta):
+            t.grad = None
+        q, k, v = tree_conv(x, w, None, tree, split_sizes=(HK * D, HK * D, HV * D))
         o, _ = gdn_tree(q.view(T, HK, D), k.view(T, HK, D), v.view(T, HV, D), g, beta, tree, None, True)
         o.backward(d_o)
 

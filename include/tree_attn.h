@@ -327,15 +327,20 @@ int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* 
 /* Backward of tt_gdn_tree_fwd's o (what autograd computes through the
  * reference's torch function, tree_dfs_ssm.py:38-156, for the exact rule):
  * given d_o [T, Hv, 128] (problem dtype, strided like q), writes dq, dk [T, Hk,
- * 128] and dv [T, Hv, 128] contiguous in the problem dtype, and dg, dbeta
- * [T, Hv] contiguous float32. The node states carry no incoming gradient. It
+ * 128] and dv [T, Hv, 128] in the problem dtype, each at its own token
+ * stride with contiguous heads (tt_tensor descriptors whose memory is
+ * written: stride_head 128, else TT_E_UNSUPPORTED; stride_tok by the rules
+ * of q and at most 2^30; e.g. the column blocks of one [T, 2 Hk 128 + Hv 128]
+ * row buffer, the gradient of a conv output that a q/k/v split reads, so that
+ * no concatenation follows), and dg, dbeta [T, Hv] contiguous float32. The
+ * node states carry no incoming gradient. It
  * recomputes the forward (keeping every chunk's initial state), runs one
  * reverse launch per tree level (deepest first) for the state gradient, then
  * two launches over all chunks. Workspace: tt_gdn_bwd_workspace_bytes (per
  * (chunk, v head) about 240 KiB; per (node, v head) 128 KiB). */
 size_t tt_gdn_bwd_workspace_bytes(const tt_gdn_problem* p);
-int tt_gdn_tree_bwd(const tt_gdn_problem* p, tt_tensor d_o, void* dq, void* dk, void* dv, float* dg, float* dbeta,
-                    void* ws, size_t ws_bytes, void* stream);
+int tt_gdn_tree_bwd(const tt_gdn_problem* p, tt_tensor d_o, tt_tensor dq, tt_tensor dk, tt_tensor dv, float* dg,
+                    float* dbeta, void* ws, size_t ws_bytes, void* stream);
 
 /* The same forward and backward without the backward's recompute of the
  * forward (what autograd keeps through the reference's torch function,
@@ -350,8 +355,8 @@ size_t tt_gdn_saved_bytes(const tt_gdn_problem* p);
 int tt_gdn_tree_fwd_save(const tt_gdn_problem* p, void* o, float* node_states, void* saved, size_t saved_bytes,
                          void* stream);
 size_t tt_gdn_bwd_saved_workspace_bytes(const tt_gdn_problem* p);
-int tt_gdn_tree_bwd_saved(const tt_gdn_problem* p, tt_tensor d_o, void* dq, void* dk, void* dv, float* dg,
-                          float* dbeta, const void* saved, size_t saved_bytes, void* ws, size_t ws_bytes,
+int tt_gdn_tree_bwd_saved(const tt_gdn_problem* p, tt_tensor d_o, tt_tensor dq, tt_tensor dk, tt_tensor dv,
+                          float* dg, float* dbeta, const void* saved, size_t saved_bytes, void* ws, size_t ws_bytes,
                           void* stream);
 
 /* ---- tree-correct short convolution --------------------------------------

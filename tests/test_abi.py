@@ -260,12 +260,33 @@ def test_gdn_bwd_validation():
     per_chunk = (2 * 32 * 128 + 2 * 32 * 32 + 32) + 2 * 128 * 128 + 5 * 32 * 128 + 1
     want = (5 * 32 * per_chunk + 3 * 32 * 2 * 128 * 128) * 4
     assert lib.tt_gdn_bwd_workspace_bytes(ctypes.byref(p)) == want
-    args = lambda ws_bytes: (V, V, V, V, V, V, ws_bytes, None)
+    DQ = _lib.TTTensor(16, 16 * 128, 128)
+    args = lambda ws_bytes, dq=DQ, dk=DQ, dv=DO: (dq, dk, dv, V, V, V, ws_bytes, None)
     assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, *args(want - 4)) == _lib.TT_E_WORKSPACE
     assert lib.tt_gdn_tree_bwd(ctypes.byref(_gdn_problem()), DO, *args(want)) == _lib.TT_E_ARG   # no children CSR
     assert lib.tt_gdn_tree_bwd(ctypes.byref(p), _lib.TTTensor(18, 32 * 128, 128), *args(want)) == _lib.TT_E_ARG
     assert lib.tt_gdn_tree_bwd(ctypes.byref(p), _lib.TTTensor(16, 64, 128), *args(want)) == _lib.TT_E_ARG
-    assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, V, V, V, ctypes.c_void_p(18), V, V, want, None) == _lib.TT_E_ARG
+    assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, DQ, DQ, DO, ctypes.c_void_p(18), V, V, want,
+                               None) == _lib.TT_E_ARG
+    # dq/dk/dv: the row rules of q (a null, misaligned or short-strided output is refused) ...
+    for bad in (_lib.TTTensor(None, 16 * 128, 128), _lib.TTTensor(24, 16 * 128, 128), _lib.TTTensor(16, 64, 128),
+                _lib.TTTensor(16, 16 * 128, 100)):
+        for i in range(3):
+            outs = [DQ, DQ, DO]
+            outs[i] = bad
+            assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, *args(want, *outs)) == _lib.TT_E_ARG
+    # heads must be contiguous; rows at most 2^30 elements apart
+    for i in range(3):
+        outs = [DQ, DQ, DO]
+        outs[i] = _lib.TTTensor(16, 64 * 128, 256)
+        assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, *args(want, *outs)) == _lib.TT_E_UNSUPPORTED
+        outs[i] = _lib.TTTensor(16, (1 << 30) + 8, 128)
+        assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, *args(want, *outs)) == _lib.TT_E_ARG
+    # ... and column blocks of one packed [T, (2 Hk + Hv) 128] row buffer pass them
+    W = (2 * 16 + 32) * 128
+    packed = (_lib.TTTensor(16, W, 128), _lib.TTTensor(16 + 16 * 128 * 2, W, 128),
+              _lib.TTTensor(16 + 32 * 128 * 2, W, 128))
+    assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, *args(want - 4, *packed)) == _lib.TT_E_WORKSPACE
     assert lib.tt_gdn_tree_bwd(ctypes.byref(_gdn_problem(head_dim=64, node_child_off=16, node_child=16)), DO,
                                *args(want)) == _lib.TT_E_UNSUPPORTED
 
@@ -287,13 +308,16 @@ def test_gdn_saved_validation():
     assert lib.tt_gdn_tree_fwd_save(ctypes.byref(p), V, V, V, saved - 4, None) == _lib.TT_E_WORKSPACE
     assert lib.tt_gdn_tree_fwd_save(ctypes.byref(p), V, V, None, saved, None) == _lib.TT_E_ARG
     assert lib.tt_gdn_tree_fwd_save(ctypes.byref(p), V, V, ctypes.c_void_p(20), saved, None) == _lib.TT_E_ARG
-    args = lambda sv, sb, wb: (V, V, V, V, V, sv, sb, V, wb, None)
+    DQ = _lib.TTTensor(16, 16 * 128, 128)
+    args = lambda sv, sb, wb: (DQ, DQ, DO, V, V, sv, sb, V, wb, None)
     assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), DO, *args(V, saved - 4, scratch)) == _lib.TT_E_WORKSPACE
     assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), DO, *args(V, saved, scratch - 4)) == _lib.TT_E_WORKSPACE
     assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), DO, *args(None, saved, scratch)) == _lib.TT_E_ARG
     assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(_gdn_problem()), DO, *args(V, saved, scratch)) == _lib.TT_E_ARG
     assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), _lib.TTTensor(18, 32 * 128, 128),
                                      *args(V, saved, scratch)) == _lib.TT_E_ARG
+    assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), DO, _lib.TTTensor(16, 64, 128), DQ, DO, V, V, V, saved, V,
+                                     scratch, None) == _lib.TT_E_ARG
 
 
 def _conv_problem(**kw):

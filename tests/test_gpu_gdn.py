@@ -270,3 +270,87 @@ def test_gdn_retain_graph_backwards_reuse_saved_forward(monkeypatch):
     for gr in grads[1:]:
         for name, a, b in zip(BWD_NAMES, grads[0], gr):
             assert torch.equal(a, b), name
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("saved_fwd", [False, True], ids=["recompute", "saved"])
+def test_gdn_packed_qkv_gradients(saved_fwd, dtype):
+    """q, k, v as the column blocks of one packed [T, (2 Hk + Hv) 128] row
+    buffer: dq, dk, dv come back as the same blocks of one new buffer
+    (strided outputs through the C ABI), bitwise equal to the gradients of
+    the same inputs held as separate contiguous tensors."""
+    from tree_training_amd import gdn as tgdn
+    c = CASES["c1_heads"]
+    lens, par = c["topo"]()
+    T, Hk, Hv = sum(lens), c["Hk"], c["Hv"]
+    q, k, v, g, beta = _inputs(T, Hk, Hv, 91, realistic_gates=True)
+    d_o = np.random.default_rng(16).standard_normal((T, Hv, D)).astype(np.float32)
+    dev = torch.device("cuda", 0)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    tree = GdnTree(lens, par, dev)
+    rows = t(np.concatenate([q.reshape(T, -1), k.reshape(T, -1), v.reshape(T, -1)], axis=1)).to(dtype)
+    nk = Hk * D
+    packed = (rows[:, :nk].view(T, Hk, D), rows[:, nk:2 * nk].view(T, Hk, D), rows[:, 2 * nk:].view(T, Hv, D))
+    sep = tuple(x.contiguous() for x in packed)
+    print(f"gdn packed qkv grads saved={saved_fwd} {dtype}: T={T}", flush=True)
+    res = []
+    for qkv in (packed, sep):
+        saved = tgdn._gdn_forward(*qkv, t(g), t(beta), tree, None, True, True)[2] if saved_fwd else None
+        res.append(gdn_tree_backward(*qkv, t(g), t(beta), t(d_o).to(dtype), tree, saved=saved))
+    torch.cuda.synchronize()
+    dq, dk, dv = res[0][:3]
+    e = dq.element_size()
+    assert dq.stride(0) == dk.stride(0) == dv.stride(0) == rows.shape[1]
+    assert dk.data_ptr() == dq.data_ptr() + nk * e and dv.data_ptr() == dk.data_ptr() + nk * e
+    assert res[1][0].is_contiguous()
+    for name, a, b in zip(BWD_NAMES, *res):
+        assert torch.equal(a, b), name
+
+
+def test_gdn_conv_split_autograd_matches_torch_split():
+    """tree_conv(split_sizes=...) feeding gdn_tree: the conv reads the q/k/v
+    gradients in place (no concatenation) and gives bitwise the gradients of
+    tree_conv + torch.split + gdn_tree."""
+    from tree_training_amd import conv as tconv
+    from tree_training_amd.gdn import gdn_tree
+    c = CASES["c1_heads"]
+    lens, par = c["topo"]()
+    T, Hk, Hv = sum(lens), c["Hk"], c["Hv"]
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(5)
+    C = (2 * Hk + Hv) * D
+    bf = torch.bfloat16
+    x0 = torch.randn(T, C, device=dev, generator=gen, dtype=bf)
+    w0 = (torch.randn(C, 4, device=dev, generator=gen) * 0.5).to(bf)
+    g0 = -torch.rand(T, Hv, device=dev, generator=gen) * 0.5
+    b0 = torch.rand(T, Hv, device=dev, generator=gen)
+    d_o = torch.randn(T, Hv, D, device=dev, generator=gen, dtype=bf)
+    tree = GdnTree(lens, par, dev)
+    sizes = (Hk * D, Hk * D, Hv * D)
+    joined = []
+    real_join = tconv._join_columns
+
+    def spy(grads, sz, like):
+        out = real_join(grads, sz, like)
+        joined.append(out.data_ptr() == grads[0].data_ptr())
+        return out
+
+    print(f"conv split + gdn autograd: T={T} C={C}", flush=True)
+    grads = []
+    for split in (True, False):
+        leaves = [z.clone().requires_grad_(True) for z in (x0, w0, g0, b0)]
+        x, w, g, beta = leaves
+        if split:
+            q, k, v = tconv.tree_conv(x, w, None, tree, split_sizes=sizes)
+        else:
+            q, k, v = torch.split(tconv.tree_conv(x, w, None, tree), list(sizes), dim=-1)
+        o, _ = gdn_tree(q.view(T, Hk, D), k.view(T, Hk, D), v.view(T, Hv, D), g, beta, tree, None, True)
+        tconv._join_columns = spy
+        try:
+            grads.append(torch.autograd.grad((o.float() * d_o.float()).sum(), leaves))
+        finally:
+            tconv._join_columns = real_join
+    torch.cuda.synchronize()
+    assert joined == [True]
+    for name, a, b in zip(("x", "weight", "g", "beta"), *grads):
+        assert torch.equal(a, b), name

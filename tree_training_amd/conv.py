@@ -14,7 +14,7 @@ token-major output, the layout the q/k/v split after it reads.
 from __future__ import annotations
 
 import ctypes
-from typing import Optional
+from typing import Optional, Sequence
 
 import torch
 
@@ -104,9 +104,63 @@ class TreeConvFunction(torch.autograd.Function):
                 db.to(bias.dtype) if bias is not None else None, None)
 
 
-def tree_conv(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], tree: GdnTree) -> torch.Tensor:
-    """Autograd-aware ``tree_conv_forward``."""
-    return TreeConvFunction.apply(x, weight, bias, tree)
+def _join_columns(grads, sizes: Sequence[int], like: torch.Tensor) -> torch.Tensor:
+    """dy [T, sum(sizes)] from the gradients of the column blocks: read in
+    place when they already are those blocks of one row-major buffer (what
+    gdn_tree_backward writes for a q/k/v split), else concatenated (zeros for
+    a block without a gradient)."""
+    T, W = like.shape[0], sum(sizes)
+    if all(g is not None for g in grads):
+        g0 = grads[0]
+        e, off, ok = g0.element_size(), 0, True
+        for g, n in zip(grads, sizes):
+            ok = ok and (g.dim() == 2 and g.shape == (T, n) and g.stride(1) == 1 and g.stride(0) == W and
+                         g.dtype == g0.dtype and g.untyped_storage().data_ptr() == g0.untyped_storage().data_ptr()
+                         and g.data_ptr() == g0.data_ptr() + off * e)
+            off += n
+        if ok and (g0.storage_offset() + T * W) * e <= g0.untyped_storage().nbytes():
+            return g0.as_strided((T, W), (W, 1))
+    return torch.cat([g if g is not None else torch.zeros((T, n), dtype=like.dtype, device=like.device)
+                      for g, n in zip(grads, sizes)], dim=1)
+
+
+class TreeConvSplitFunction(torch.autograd.Function):
+    """Tree conv whose output rows are handed out as column blocks (the q/k/v
+    split after the conv); the backward takes the blocks' gradients back as
+    one dy through ``_join_columns``."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, tree, sizes):
+        ctx.save_for_backward(x, weight, bias)
+        ctx.tree, ctx.sizes = tree, tuple(sizes)
+        ctx.set_materialize_grads(False)
+        y = tree_conv_forward(x, weight, bias, tree)
+        if y.shape[1] != sum(ctx.sizes):
+            raise ValueError(f"split sizes {ctx.sizes} do not add up to the {y.shape[1]} channels")
+        return tuple(torch.split(y, ctx.sizes, dim=1))
+
+    @staticmethod
+    def backward(ctx, *grads):
+        if all(g is None for g in grads):
+            return None, None, None, None, None
+        x, weight, bias = ctx.saved_tensors
+        dy = _join_columns(grads, ctx.sizes, x)
+        dx, dw, db = tree_conv_backward(x, weight, bias, dy, ctx.tree)
+        return (dx.to(x.dtype), dw.reshape(weight.shape).to(weight.dtype),
+                db.to(bias.dtype) if bias is not None else None, None, None)
+
+
+def tree_conv(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], tree: GdnTree,
+              split_sizes: Optional[Sequence[int]] = None):
+    """Autograd-aware ``tree_conv_forward``. With ``split_sizes`` the output
+    comes back as the tuple ``torch.split(y, split_sizes, dim=1)`` would give
+    (views of one [T, C] buffer), and the backward reads the blocks'
+    gradients in place when they are the matching blocks of one buffer (as
+    ``gdn_tree`` gives for q, k, v taken from those blocks) instead of
+    concatenating them."""
+    if split_sizes is None:
+        return TreeConvFunction.apply(x, weight, bias, tree)
+    return TreeConvSplitFunction.apply(x, weight, bias, tree, tuple(int(n) for n in split_sizes))
 
 
 def _tree_correct_conv_varlen(ssm, mixed_qkv_raw: torch.Tensor, chunk_boundaries, chunk_parent_map):

@@ -6,7 +6,7 @@
 
 namespace {
 
-constexpr int kAbiVersion = 3;
+constexpr int kAbiVersion = 4;
 constexpr int64_t kMaxTokStride = int64_t(1) << 23;   // elements (bf16; half that for fp32)
 inline int64_t max_tok_stride(int dtype) { return dtype == TT_DTYPE_BF16 ? kMaxTokStride : kMaxTokStride / 2; }
 
@@ -327,43 +327,56 @@ size_t tt_gdn_bwd_saved_workspace_bytes(const tt_gdn_problem* p) {
 }
 
 // Shared argument checks of the two backward entry points.
-static int gdn_bwd_args(const tt_gdn_problem* p, const tt_tensor& d_o, void* dq, void* dk, void* dv, float* dg,
-                        float* dbeta, void* ws) {
+// d_o and the dq/dk/dv outputs: rows of 128 elements at a token and a head
+// stride (at least 128, multiples of 16 bytes), 16-byte aligned.
+static bool gdn_rows_ok(const tt_tensor& t, int64_t gran) {
+    return t.ptr && t.stride_tok >= 128 && t.stride_head >= 128 && !(t.stride_tok % gran) &&
+           !(t.stride_head % gran) && aligned(t.ptr, 16);
+}
+
+static int gdn_bwd_args(const tt_gdn_problem* p, GdnDev& d, const tt_tensor& d_o, const tt_tensor& dq,
+                        const tt_tensor& dk, const tt_tensor& dv, float* dg, float* dbeta, void* ws) {
     if (!p->node_child_off || !p->node_child) return TT_E_ARG;
-    if (!d_o.ptr || !dq || !dk || !dv || !dg || !dbeta || !ws) return TT_E_ARG;
+    if (!dg || !dbeta || !ws) return TT_E_ARG;
     const int64_t gran = p->dtype == TT_DTYPE_BF16 ? 8 : 4;
-    if (d_o.stride_tok < 128 || d_o.stride_head < 128 || (d_o.stride_tok % gran) || (d_o.stride_head % gran) ||
-        !aligned(d_o.ptr, 16))
+    if (!gdn_rows_ok(d_o, gran) || !gdn_rows_ok(dq, gran) || !gdn_rows_ok(dk, gran) || !gdn_rows_ok(dv, gran))
         return TT_E_ARG;
-    if (!aligned(dq, 16) || !aligned(dk, 16) || !aligned(dv, 16) || !aligned(ws, 16) || !aligned(dg, 4) ||
-        !aligned(dbeta, 4))
-        return TT_E_ARG;
+    // the outputs' heads are contiguous and their rows at most 2^30 elements apart
+    const tt_tensor* outs[3] = {&dq, &dk, &dv};
+    for (const tt_tensor* t : outs) {
+        if (t->stride_head != 128) return TT_E_UNSUPPORTED;
+        if (t->stride_tok > (int64_t(1) << 30)) return TT_E_ARG;
+    }
+    if (!aligned(ws, 16) || !aligned(dg, 4) || !aligned(dbeta, 4)) return TT_E_ARG;
+    d.dq_st = (int)dq.stride_tok;
+    d.dk_st = (int)dk.stride_tok;
+    d.dv_st = (int)dv.stride_tok;
     return TT_OK;
 }
 
-int tt_gdn_tree_bwd(const tt_gdn_problem* p, tt_tensor d_o, void* dq, void* dk, void* dv, float* dg, float* dbeta,
-                    void* ws, size_t ws_bytes, void* stream) {
+int tt_gdn_tree_bwd(const tt_gdn_problem* p, tt_tensor d_o, tt_tensor dq, tt_tensor dk, tt_tensor dv, float* dg,
+                    float* dbeta, void* ws, size_t ws_bytes, void* stream) {
     GdnDev d;
     int rc = gdn_problem(p, d);
     if (rc != TT_OK) return rc;
-    if ((rc = gdn_bwd_args(p, d_o, dq, dk, dv, dg, dbeta, ws)) != TT_OK) return rc;
+    if ((rc = gdn_bwd_args(p, d, d_o, dq, dk, dv, dg, dbeta, ws)) != TT_OK) return rc;
     if (ws_bytes < tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v, true, p->reference_truncated != 0)) return TT_E_WORKSPACE;
-    return tt_gdn_bwd_launch(d, p->level_offsets, p->n_levels, d_o.ptr, d_o.stride_tok, d_o.stride_head, dq, dk,
-                             dv, dg, dbeta, nullptr, (float*)ws, (hipStream_t)stream);
+    return tt_gdn_bwd_launch(d, p->level_offsets, p->n_levels, d_o.ptr, d_o.stride_tok, d_o.stride_head,
+                             const_cast<void*>(dq.ptr), const_cast<void*>(dk.ptr), const_cast<void*>(dv.ptr), dg, dbeta, nullptr, (float*)ws, (hipStream_t)stream);
 }
 
-int tt_gdn_tree_bwd_saved(const tt_gdn_problem* p, tt_tensor d_o, void* dq, void* dk, void* dv, float* dg,
-                          float* dbeta, const void* saved, size_t saved_bytes, void* ws, size_t ws_bytes,
+int tt_gdn_tree_bwd_saved(const tt_gdn_problem* p, tt_tensor d_o, tt_tensor dq, tt_tensor dk, tt_tensor dv,
+                          float* dg, float* dbeta, const void* saved, size_t saved_bytes, void* ws, size_t ws_bytes,
                           void* stream) {
     GdnDev d;
     int rc = gdn_problem(p, d);
     if (rc != TT_OK) return rc;
-    if ((rc = gdn_bwd_args(p, d_o, dq, dk, dv, dg, dbeta, ws)) != TT_OK) return rc;
+    if ((rc = gdn_bwd_args(p, d, d_o, dq, dk, dv, dg, dbeta, ws)) != TT_OK) return rc;
     if (!saved || !aligned(saved, 16)) return TT_E_ARG;
     if (saved_bytes < tt_gdn_saved_bytes_impl(p->n_chunks, p->n_heads_v, p->reference_truncated != 0)) return TT_E_WORKSPACE;
     if (ws_bytes < tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v, false, p->reference_truncated != 0)) return TT_E_WORKSPACE;
-    return tt_gdn_bwd_launch(d, p->level_offsets, p->n_levels, d_o.ptr, d_o.stride_tok, d_o.stride_head, dq, dk,
-                             dv, dg, dbeta, (const float*)saved, (float*)ws, (hipStream_t)stream);
+    return tt_gdn_bwd_launch(d, p->level_offsets, p->n_levels, d_o.ptr, d_o.stride_tok, d_o.stride_head,
+                             const_cast<void*>(dq.ptr), const_cast<void*>(dk.ptr), const_cast<void*>(dv.ptr), dg, dbeta, (const float*)saved, (float*)ws, (hipStream_t)stream);
 }
 
 }  // extern "C"

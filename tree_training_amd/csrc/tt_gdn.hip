@@ -861,7 +861,7 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
                         dka[4 * m + e] = fmaf(bge, dbk[e], dka[4 * m + e]);
                         o[e] = bi * dbv[e];
                     }
-                    if (valid) store4(dv + (tok * p.hv + h) * GD + 32 * m + 4 * s, o);
+                    if (valid) store4(dv + tok * p.dv_st + h * GD + 32 * m + 4 * s, o);
                 }
                 dbp += vb + egi * kb;
                 dgp = fmaf(bge, kb, dgp);
@@ -1026,8 +1026,8 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
                 oq[e] = fmaf(aq, dqa[4 * m + e], bq * qv[m][e]);
                 ok[e] = fmaf(ak, dka[4 * m + e], bk * kv[m][e]);
             }
-            store4(dq + (tok * p.hk + hk) * GD + 32 * m + 4 * s, oq);
-            store4(dk + (tok * p.hk + hk) * GD + 32 * m + 4 * s, ok);
+            store4(dq + tok * p.dq_st + hk * GD + 32 * m + 4 * s, oq);
+            store4(dk + tok * p.dk_st + hk * GD + 32 * m + 4 * s, ok);
         }
     }
 }

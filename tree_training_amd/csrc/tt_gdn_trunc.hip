@@ -404,7 +404,7 @@ __global__ __launch_bounds__(GT) void gdn_erow_kernel(GdnDev p, EArgs a) {
         }
         if (in)
 #pragma unroll
-            for (int e4 = 0; e4 < 4; ++e4) store4((TIn*)a.dv + (tok * p.hv + h) * GD + d0 + 4 * e4, dvo[e4]);
+            for (int e4 = 0; e4 < 4; ++e4) store4((TIn*)a.dv + tok * p.dv_st + h * GD + d0 + 4 * e4, dvo[e4]);
         vdot = row8_sum(vdot);
         kdot = row8_sum(kdot);
         if ((t & 7) == 0) {

@@ -63,6 +63,11 @@ struct GdnDev {
     int dtype, n_tokens, n_nodes, n_chunks, hk, hv, rep, l2;
     int trunc;                             // the reference's I + R + R^2 per node (else the exact rule)
     float scale;
+    // Backward outputs dq, dk [T, Hk, 128] and dv [T, Hv, 128]: token
+    // strides in elements (heads contiguous; the pointers travel as launch
+    // arguments). 32-bit, as every scalar register kept live through the
+    // backward chunk kernel's loop costs it schedule quality.
+    int dq_st, dk_st, dv_st;
 };
 
 // Device-side view of a tt_conv_problem.

@@ -204,37 +204,65 @@ def gdn_tree_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch
     return o, states
 
 
+def _packed_qkv_width(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> Optional[int]:
+    """Row width W when q, k, v [T, H, 128] are the consecutive column blocks
+    [q | k | v] of one row-major [T, W] buffer (a conv output split three
+    ways) with contiguous heads, else None."""
+    st, e = q.stride(0), q.element_size()
+    widths = [t.shape[1] * t.shape[2] for t in (q, k, v)]
+    if any(t.stride(0) != st or t.stride(2) != 1 or t.stride(1) != t.shape[2] for t in (q, k, v)):
+        return None
+    if st != sum(widths) or len({t.untyped_storage().data_ptr() for t in (q, k, v)}) != 1:
+        return None
+    if k.data_ptr() != q.data_ptr() + widths[0] * e or v.data_ptr() != k.data_ptr() + widths[1] * e:
+        return None
+    return st
+
+
+def _tt(t: torch.Tensor):
+    return _lib.TTTensor(t.data_ptr(), t.stride(0), t.stride(1))
+
+
 def gdn_tree_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
                       d_o: torch.Tensor, tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True,
                       saved: Optional[torch.Tensor] = None, reference_truncated: bool = False):
     """Gradients of sum(o * d_o) for ``gdn_tree_forward``'s o: dq, dk [T, Hk,
     128] and dv [T, Hv, 128] in the dtype of v, dg and dbeta [T, Hv] float32.
-    Recomputes the forward internally (tt_gdn_tree_bwd) unless ``saved`` holds
-    what tt_gdn_tree_fwd_save kept for the same inputs (tt_gdn_tree_bwd_saved)."""
+    When q, k, v are the column blocks of one packed row buffer (the q/k/v
+    split of a conv output), dq, dk, dv are the same column blocks of one new
+    buffer, so the split's backward needs no concatenation. Recomputes the
+    forward internally (tt_gdn_tree_bwd) unless ``saved`` holds what
+    tt_gdn_tree_fwd_save kept for the same inputs (tt_gdn_tree_bwd_saved)."""
     p, (q, k, v, g, beta) = _problem(q, k, v, g, beta, tree, scale, l2norm, reference_truncated)
     d_o = _tok_heads(d_o, "d_o").to(v.dtype)
     T, Hk, Hv = q.shape[0], q.shape[1], v.shape[1]
     if d_o.shape != v.shape:
         raise ValueError(f"d_o: expected {tuple(v.shape)}, got {tuple(d_o.shape)}")
     dev = require_device(q.device)
-    dq = torch.empty((T, Hk, HEAD_DIM), dtype=v.dtype, device=dev)
-    dk = torch.empty_like(dq)
-    dv = torch.empty((T, Hv, HEAD_DIM), dtype=v.dtype, device=dev)
+    W = _packed_qkv_width(q, k, v)
+    if W is not None:
+        rows = torch.empty((T, W), dtype=v.dtype, device=dev)
+        nk = Hk * HEAD_DIM
+        dq = rows[:, :nk].view(T, Hk, HEAD_DIM)
+        dk = rows[:, nk:2 * nk].view(T, Hk, HEAD_DIM)
+        dv = rows[:, 2 * nk:].view(T, Hv, HEAD_DIM)
+    else:
+        dq = torch.empty((T, Hk, HEAD_DIM), dtype=v.dtype, device=dev)
+        dk = torch.empty_like(dq)
+        dv = torch.empty((T, Hv, HEAD_DIM), dtype=v.dtype, device=dev)
     dg = torch.empty((T, Hv), dtype=torch.float32, device=dev)
     dbeta = torch.empty_like(dg)
     lib = _lib.lib()
-    dot = _lib.TTTensor(d_o.data_ptr(), d_o.stride(0), d_o.stride(1))
+    outs = (_tt(d_o), _tt(dq), _tt(dk), _tt(dv), _ptr(dg), _ptr(dbeta))
     if saved is not None:
         ws_bytes = lib.tt_gdn_bwd_saved_workspace_bytes(ctypes.byref(p))
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        _lib.check(lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), dot, _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg),
-                                             _ptr(dbeta), _ptr(saved), saved.numel(), _ptr(ws), ws_bytes,
+        _lib.check(lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), *outs, _ptr(saved), saved.numel(), _ptr(ws), ws_bytes,
                                              _stream(dev)), "tt_gdn_tree_bwd_saved")
         return dq, dk, dv, dg, dbeta
     ws_bytes = lib.tt_gdn_bwd_workspace_bytes(ctypes.byref(p))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    _lib.check(lib.tt_gdn_tree_bwd(ctypes.byref(p), dot, _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(dbeta),
-                                   _ptr(ws), ws_bytes, _stream(dev)), "tt_gdn_tree_bwd")
+    _lib.check(lib.tt_gdn_tree_bwd(ctypes.byref(p), *outs, _ptr(ws), ws_bytes, _stream(dev)), "tt_gdn_tree_bwd")
     return dq, dk, dv, dg, dbeta
 
 
@@ -255,10 +283,14 @@ class GdnTreeFunction(torch.autograd.Function):
         ctx.save_for_backward(q, k, v, g, beta, *(() if saved is None else (saved,)))
         ctx.tree, ctx.scale, ctx.l2norm, ctx.trunc = tree, scale, l2norm, reference_truncated
         ctx.mark_non_differentiable(states)
+        # No zero-filled gradient is made for the states (or for an unused o).
+        ctx.set_materialize_grads(False)
         return o, states
 
     @staticmethod
     def backward(ctx, d_o, _d_states):
+        if d_o is None:
+            return (None,) * 9
         q, k, v, g, beta, *kept = ctx.saved_tensors
         dq, dk, dv, dg, dbeta = gdn_tree_backward(q, k, v, g, beta, d_o, ctx.tree, ctx.scale, ctx.l2norm,
                                                   saved=kept[0] if kept else None, reference_truncated=ctx.trunc)

@@ -9,7 +9,9 @@ norm, out_proj, key_dim, value_dim, head_k_dim, head_v_dim) runs:
 
   projections   one GEMM per projection over all T tokens (torch)
   conv          tt_tree_conv_fwd / _bwd (each node's window reaches into its
-                ancestors' last K-1 inputs), token-major rows
+                ancestors' last K-1 inputs), token-major rows; q, k, v are
+                its column blocks and their gradients come back as the same
+                blocks of one buffer (no concatenation)
   gates         beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias) (torch)
   scan          tt_gdn_tree_fwd / _bwd (exact gated delta rule per root-to-leaf
                 path, or with reference_truncated the reference function's
@@ -45,8 +47,8 @@ def _tree_ssm_forward(ssm, hidden_states: torch.Tensor, tree: GdnTree, reference
     z = ssm.in_proj_z(h)                                         # [T, value_dim]
     b = ssm.in_proj_b(h)
     a = ssm.in_proj_a(h)
-    mixed = tree_conv(mixed, ssm.conv1d.weight, ssm.conv1d.bias, tree)
-    q, k, v = torch.split(mixed, [ssm.key_dim, ssm.key_dim, ssm.value_dim], dim=-1)
+    q, k, v = tree_conv(mixed, ssm.conv1d.weight, ssm.conv1d.bias, tree,
+                        split_sizes=(ssm.key_dim, ssm.key_dim, ssm.value_dim))
     q = q.reshape(S, -1, ssm.head_k_dim)
     k = k.reshape(S, -1, ssm.head_k_dim)
     v = v.reshape(S, -1, ssm.head_v_dim)
