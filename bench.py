@@ -127,7 +127,7 @@ def main():
         return run_leafce(args)
     import torch
     from tree_training_amd import _lib
-    from tree_training_amd.attention import _Problem, attn_forward
+    from tree_training_amd.attention import _Problem, attn_forward, fwd_workspace
     from tree_training_amd.meta import KeyPlan, TreeMetaDevice, _ptr, _stream, build_trees
     from tree_training_amd.workloads import visible_pairs
     import ctypes
@@ -190,7 +190,9 @@ def main():
             if ev is not None:
                 ev[i].record(stream)
         rec(0)
-        _lib.check(lib.tt_attn_fwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), st), "fwd")
+        fws = fwd_workspace(pb, dev)
+        _lib.check(lib.tt_attn_fwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), _ptr(fws) if fws is not None else None,
+                                   fws.numel() if fws is not None else 0, st), "fwd")
         rec(1)
         # delta and dQ in one call (the dQ kernel computes delta), then dK/dV:
         # the same work as bwd_parts=0, split only to time the passes

@@ -169,8 +169,16 @@ typedef struct tt_attn_problem {
 } tt_attn_problem;
 
 /* o: [n_q, Hq, head_dim] contiguous, problem dtype; lse: [Hq, n_q] float32
- * (natural-log softmax normaliser, saved for the backward). */
-int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* stream);
+ * (natural-log softmax normaliser, saved for the backward).
+ * Small bf16 problems, with at most 256 (128-query block, q head) pairs,
+ * cut each pair's keys into S = 4 ranges computed in parallel and merged in
+ * a fixed order (deterministic; the rounding differs from an unsplit run).
+ * Their partials need a workspace of tt_attn_fwd_workspace_bytes: S * n_q *
+ * Hq * 520 bytes (each of three parts rounded up to 256), 0 for every other
+ * problem, when ws may be NULL. ws is 16-byte aligned; a smaller ws_bytes
+ * returns TT_E_WORKSPACE. */
+size_t tt_attn_fwd_workspace_bytes(const tt_attn_problem* p);
+int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* ws, size_t ws_bytes, void* stream);
 
 /* Backward for upstream gradient d_o (n_q x Hq, strides given). Writes
  * dq [n_q,Hq,D], dk/dv [n_q,Hkv,D] (contiguous, problem dtype, overwritten).
@@ -182,7 +190,10 @@ int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* stream);
  * calls may share accumulators only when ordered on one stream: two calls in
  * flight at once on different streams must not add into the same
  * accumulators.
- * ws must be 16-byte aligned. dq has one writer per element (deterministic);
+ * ws must be 16-byte aligned. dq has one writer per element (deterministic;
+ * the small bf16 problems whose forward splits keys, above, split the dQ
+ * pass the same way, with S * n_q * Hq * 512 more workspace bytes, and add
+ * the partials in a fixed order);
  * so do dk and dv, except that keys whose visible query range spans more
  * than W queries, W = half the largest power of two <= n_q clamped to
  * [256, 4096] (split into several work items), sum their dK/dV partials
@@ -207,7 +218,8 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
  * until the process ends (the current device's, hipGetDevice; `stream` must
  * belong to it). A problem whose tt_attn_bwd_workspace_bytes exceeds it
  * returns TT_E_WORKSPACE (either dtype needs 128 * Hq * n_q + 1024 * Hkv * (n_q +
- * n_past) bytes: about 8K keys at Hq = 32, Hkv = 8). The call allocates and
+ * n_past) bytes, plus the dQ key-split partials of small bf16 problems: about
+ * 8K keys at Hq = 32, Hkv = 8). The call allocates and
  * frees nothing (no hipMalloc, no hipMemsetAsync: what must start at zero is
  * cleared by a kernel). Every call on one GPU uses that GPU's one scratch
  * array, which keeps the last call's contents: calls that overlap on one GPU

@@ -58,17 +58,17 @@ def _problem(**kw):
 def test_attn_fwd_validation(field, value, code):
     lib = _lib.lib()
     p = _problem(**{field: value})
-    assert lib.tt_attn_fwd(ctypes.byref(p), ctypes.c_void_p(16), ctypes.c_void_p(16), None) == code
+    assert lib.tt_attn_fwd(ctypes.byref(p), ctypes.c_void_p(16), ctypes.c_void_p(16), None, 0, None) == code
 
 
 def test_attn_stride_and_alignment_validation():
     lib = _lib.lib()
     p = _problem(q=_lib.TTTensor(16, 100, 128))         # stride not a multiple of 8
-    assert lib.tt_attn_fwd(ctypes.byref(p), ctypes.c_void_p(16), ctypes.c_void_p(16), None) == _lib.TT_E_ARG
+    assert lib.tt_attn_fwd(ctypes.byref(p), ctypes.c_void_p(16), ctypes.c_void_p(16), None, 0, None) == _lib.TT_E_ARG
     p = _problem(q=_lib.TTTensor(18, 32 * 128, 128))    # not 16-byte aligned
-    assert lib.tt_attn_fwd(ctypes.byref(p), ctypes.c_void_p(16), ctypes.c_void_p(16), None) == _lib.TT_E_ARG
+    assert lib.tt_attn_fwd(ctypes.byref(p), ctypes.c_void_p(16), ctypes.c_void_p(16), None, 0, None) == _lib.TT_E_ARG
     p = _problem()
-    assert lib.tt_attn_fwd(ctypes.byref(p), None, ctypes.c_void_p(16), None) == _lib.TT_E_ARG
+    assert lib.tt_attn_fwd(ctypes.byref(p), None, ctypes.c_void_p(16), None, 0, None) == _lib.TT_E_ARG
 
 
 def test_bwd_validation():
@@ -94,7 +94,8 @@ def test_bwd_deterministic_workspace(n_q, n_past):
     """TT_BWD_DETERMINISTIC adds one dK and one dV slot of 128 keys x Hkv x
     128 fp32 for each possible work item beyond the first of a key tile:
     ceil(n_keys / 128) * floor((n_q - 1) / W) of them (W: the work item's
-    query window); bf16 and fp32 problems share the layout."""
+    query window); bf16 and fp32 problems share the layout up to the bf16
+    dQ key-split partials of small problems."""
     lib = _lib.lib()
     base = _problem(n_q=n_q, n_past=n_past)
     det = _problem(n_q=n_q, n_past=n_past, bwd_parts=_lib.TT_BWD_DETERMINISTIC)
@@ -103,10 +104,54 @@ def test_bwd_deterministic_workspace(n_q, n_past):
     assert lib.tt_attn_bwd_workspace_bytes(ctypes.byref(det)) - \
         lib.tt_attn_bwd_workspace_bytes(ctypes.byref(base)) == extra
     assert (extra == 0) == (n_q <= 256 or n_q - 1 < _qch(n_q))
-    sizes = [lib.tt_attn_bwd_workspace_bytes(ctypes.byref(p)) for p in (base, det)]
+    sizes = [lib.tt_attn_bwd_workspace_bytes(ctypes.byref(p)) - _dq_part_bytes(n_q) for p in (base, det)]
     for p in (base, det):
         p.dtype = _lib.TT_DTYPE_F32
     assert [lib.tt_attn_bwd_workspace_bytes(ctypes.byref(p)) for p in (base, det)] == sizes
+
+
+def _key_splits(n_q, hq=32):
+    return 4 if -(-n_q // 128) * hq <= 256 else 1
+
+
+def _r256(b):
+    return (b + 255) // 256 * 256
+
+
+def _dq_part_bytes(n_q, hq=32):
+    s = _key_splits(n_q, hq)
+    return _r256(s * n_q * hq * 128 * 4) if s > 1 else 0
+
+
+@pytest.mark.parametrize("n_q,splits", [(1, 4), (100, 4), (473, 4), (1024, 4), (1025, 1), (1603, 1), (2048, 1),
+                                        (16318, 1)])
+def test_key_split_workspaces(n_q, splits):
+    """Small bf16 problems (<= 256 pairs of 128-query block and q head) split
+    the forward and dQ passes' keys in 4 ranges: the
+    forward needs fp32 partial rows plus a row max and a row sum per split,
+    the backward the dQ partial rows; fp32 problems and larger ones none."""
+    lib = _lib.lib()
+    assert _key_splits(n_q) == splits
+    fwd = (_r256(splits * n_q * 32 * 512) + 2 * _r256(splits * 32 * n_q * 4)) if splits > 1 else 0
+    p = _problem(n_q=n_q)
+    assert lib.tt_attn_fwd_workspace_bytes(ctypes.byref(p)) == fwd
+    f32 = _problem(n_q=n_q, dtype=_lib.TT_DTYPE_F32)
+    assert lib.tt_attn_fwd_workspace_bytes(ctypes.byref(f32)) == 0
+    assert lib.tt_attn_bwd_workspace_bytes(ctypes.byref(p)) - \
+        lib.tt_attn_bwd_workspace_bytes(ctypes.byref(f32)) == _dq_part_bytes(n_q)
+
+
+def test_attn_fwd_workspace_validation():
+    """A split forward without its workspace: a null or misaligned ws is an
+    argument error, a short one TT_E_WORKSPACE (checked before any launch)."""
+    lib = _lib.lib()
+    p = _problem(n_q=100)
+    need = lib.tt_attn_fwd_workspace_bytes(ctypes.byref(p))
+    assert need > 0
+    V = ctypes.c_void_p(16)
+    assert lib.tt_attn_fwd(ctypes.byref(p), V, V, None, need, None) == _lib.TT_E_ARG
+    assert lib.tt_attn_fwd(ctypes.byref(p), V, V, ctypes.c_void_p(24), need, None) == _lib.TT_E_ARG
+    assert lib.tt_attn_fwd(ctypes.byref(p), V, V, V, need - 4, None) == _lib.TT_E_WORKSPACE
 
 
 def test_bwd_parts_validation():

@@ -1,4 +1,5 @@
 """GPU parity of the HIP kernels against the CPU oracle (through the C ABI)."""
+import ctypes
 import math
 import sys
 
@@ -478,3 +479,35 @@ def test_attention_head_layouts(hq, hkv, dtype):
     for name, ref, got in (("o", ro, o), ("dq", rdq, dq), ("dk", rdk[Lp:], dk), ("dv", rdv[Lp:], dv),
                            ("dk_past", rdk[:Lp], acc[0]), ("dv_past", rdv[:Lp], acc[1])):
         check_close(name, ref, got.float().cpu().numpy(), tol)
+
+
+@pytest.mark.parametrize("parts", [(0,), (3, 4)], ids=["one_call", "delta+dq,dkdv"])
+def test_attention_key_split_gateway_partition(parts):
+    """A gateway partition with few queries (473 tokens in two nodes, 4 query
+    blocks x 32 heads = 128 pairs) under 3,760 gateway keys of which two runs
+    are visible: the bf16 forward and dQ passes split each pair's keys four
+    ways and merge the fp32 partials (tt_attn_fwd_workspace_bytes > 0). The
+    result matches the fp64 oracle, and two runs are bitwise equal (the
+    merge adds the ranges in a fixed order)."""
+    from tree_training_amd import _lib
+    from tree_training_amd.attention import _Problem
+    from tree_training_amd.meta import KeyPlan
+    lens, par, n_past = [300, 173], [-1, 0], 3760
+    past_vis = [i < 1357 or i >= 3648 for i in range(n_past)]
+    T = sum(lens)
+    m = _meta(lens, par)
+    plan = KeyPlan(m.horizon, torch.tensor([0.0 if b else -math.inf for b in past_vis], device=DEV))
+    x = torch.zeros(1, HQ, T, D, dtype=torch.bfloat16, device=DEV)
+    kv = torch.zeros(1, HKV, T, D, dtype=torch.bfloat16, device=DEV)
+    kvp = torch.zeros(1, HKV, n_past, D, dtype=torch.bfloat16, device=DEV)
+    pb = _Problem(x, kv, kv, kvp, kvp, plan, D ** -0.5)
+    assert _lib.lib().tt_attn_fwd_workspace_bytes(ctypes.byref(pb.s)) > 0
+    say(f"attention key split gateway partition T={T} Lp={n_past} parts={parts}")
+    runs = [_run(lens, par, torch.bfloat16, seed=31, past_vis=past_vis, parts=parts) for _ in range(2)]
+    for name, (ref, got) in runs[0].items():
+        if name in ("o", "lse", "dq"):
+            assert np.array_equal(got, runs[1][name][1]), f"{name}: two runs differ"
+        if name == "lse":
+            assert np.abs(ref - got).max() < 2e-2, name
+            continue
+        check_close(name, ref, got, TOL[torch.bfloat16])

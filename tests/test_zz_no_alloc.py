@@ -28,7 +28,7 @@ def _rel(a, b):
 
 
 def _case(lens, par, n_past, dtype, seed):
-    from tree_training_amd.attention import _Problem
+    from tree_training_amd.attention import _Problem, fwd_workspace
     from tree_training_amd.meta import KeyPlan, TreeMetaDevice
     T = sum(lens)
     g = torch.Generator().manual_seed(seed)
@@ -45,8 +45,11 @@ def _case(lens, par, n_past, dtype, seed):
     o = torch.empty((T, HQ, D), dtype=dtype, device=DEV)
     lse = torch.empty((HQ, T), dtype=torch.float32, device=DEV)
     st = ctypes.c_void_p(torch.cuda.current_stream(DEV).cuda_stream)
+    fws = fwd_workspace(pb, DEV)
     _lib.check(_lib.lib().tt_attn_fwd(ctypes.byref(pb.s), ctypes.c_void_p(o.data_ptr()),
-                                      ctypes.c_void_p(lse.data_ptr()), st), "tt_attn_fwd")
+                                      ctypes.c_void_p(lse.data_ptr()),
+                                      ctypes.c_void_p(fws.data_ptr()) if fws is not None else None,
+                                      fws.numel() if fws is not None else 0, st), "tt_attn_fwd")
     return dict(pb=pb, o=o, lse=lse, do=do, T=T, n_past=n_past, dtype=dtype, keep=(meta, plan))
 
 

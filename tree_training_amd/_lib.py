@@ -29,12 +29,12 @@ TT_STATUS_BAD_PARENT = 2
 TT_STATUS_BAD_TOTAL = 4
 TT_STATUS_BAD_BIAS = 8
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # Every symbol include/tree_attn.h declares, for the export check.
 EXPORTS = (
     "tt_abi_version", "tt_strerror", "tt_meta_workspace_bytes", "tt_meta_build", "tt_keys_build",
-    "tt_meta_dense_mask", "tt_plan_bytes", "tt_plan_build", "tt_attn_fwd",
+    "tt_meta_dense_mask", "tt_plan_bytes", "tt_plan_build", "tt_attn_fwd_workspace_bytes", "tt_attn_fwd",
     "tt_attn_bwd_workspace_bytes", "tt_attn_bwd", "tt_gdn_workspace_bytes", "tt_gdn_tree_fwd",
     "tt_gdn_bwd_workspace_bytes", "tt_gdn_tree_bwd", "tt_gdn_saved_bytes", "tt_gdn_tree_fwd_save",
     "tt_gdn_bwd_saved_workspace_bytes", "tt_gdn_tree_bwd_saved", "tt_tree_conv_fwd", "tt_tree_conv_bwd_workspace_bytes",
@@ -123,7 +123,8 @@ def _declare(lib):
         "tt_plan_bytes": (SZ, [I32, I32]),
         "tt_plan_build": (ctypes.c_int, [P, P, I32, I32, P, SZ, VP]),
         "tt_trees_build": (ctypes.c_int, [ctypes.POINTER(TTTreeJob), I32, VP]),
-        "tt_attn_fwd": (ctypes.c_int, [ctypes.POINTER(TTAttnProblem), P, P, VP]),
+        "tt_attn_fwd_workspace_bytes": (SZ, [ctypes.POINTER(TTAttnProblem)]),
+        "tt_attn_fwd": (ctypes.c_int, [ctypes.POINTER(TTAttnProblem), P, P, P, SZ, VP]),
         "tt_attn_bwd_workspace_bytes": (SZ, [ctypes.POINTER(TTAttnProblem)]),
         "tt_attn_bwd": (ctypes.c_int, [ctypes.POINTER(TTAttnProblem), P, P, TTTensor, P, P, P, P, P, P, SZ,
                                        VP]),

@@ -97,12 +97,21 @@ class _Problem:
             plan_bytes=plan.plan_bytes)
 
 
+def fwd_workspace(pb: "_Problem", device) -> Optional[torch.Tensor]:
+    """The forward's workspace (key-split partials of small bf16 problems), or
+    None when the problem needs none."""
+    n = lib().tt_attn_fwd_workspace_bytes(ctypes.byref(pb.s))
+    return torch.empty(n, dtype=torch.uint8, device=device) if n else None
+
+
 def attn_forward(q, k, v, plan: KeyPlan, scale: float, k_past=None, v_past=None):
     """Returns (o [N, Hq, D], lse [Hq, N] float32)."""
     pb = _Problem(q, k, v, k_past, v_past, plan, scale)
     o = torch.empty((pb.N, pb.Hq, pb.D), dtype=pb.dtype, device=q.device)
     lse = torch.empty((pb.Hq, pb.N), dtype=torch.float32, device=q.device)
-    check(lib().tt_attn_fwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), _stream(q.device)), "tt_attn_fwd")
+    ws = fwd_workspace(pb, q.device)
+    check(lib().tt_attn_fwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), _ptr(ws) if ws is not None else None,
+                            ws.numel() if ws is not None else 0, _stream(q.device)), "tt_attn_fwd")
     return o, lse
 
 

@@ -6,7 +6,7 @@
 
 namespace {
 
-constexpr int kAbiVersion = 4;
+constexpr int kAbiVersion = 5;
 constexpr int64_t kMaxTokStride = int64_t(1) << 23;   // elements (bf16; half that for fp32)
 inline int64_t max_tok_stride(int dtype) { return dtype == TT_DTYPE_BF16 ? kMaxTokStride : kMaxTokStride / 2; }
 
@@ -148,20 +148,54 @@ int tt_trees_build(const tt_tree_job* jobs, int32_t n_jobs, void* stream) {
     return tt_trees_build_impl(jobs, n_jobs, (hipStream_t)stream);
 }
 
-int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* stream) {
+// Key-range splits of a problem's forward and dQ passes (bf16 only).
+static int key_splits(const tt_attn_problem* p) {
+    return p->dtype == TT_DTYPE_BF16 ? tt_key_splits(p->n_q, p->n_heads_q) : 1;
+}
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+// fp32 partial rows of a split pass: [splits, n_q, Hq, 128]
+static size_t split_part_bytes(const tt_attn_problem* p) {
+    const int s = key_splits(p);
+    return s > 1 ? align256((size_t)s * p->n_q * p->n_heads_q * 128 * sizeof(float)) : 0;
+}
+// row max and row sum of each split: [splits, Hq, n_q] each
+static size_t split_stat_bytes(const tt_attn_problem* p) {
+    const int s = key_splits(p);
+    return s > 1 ? align256((size_t)s * p->n_heads_q * p->n_q * sizeof(float)) : 0;
+}
+
+size_t tt_attn_fwd_workspace_bytes(const tt_attn_problem* p) {
+    if (!p || p->n_q < 1 || p->n_heads_q < 1) return 0;
+    return split_part_bytes(p) + 2 * split_stat_bytes(p);
+}
+
+int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* ws, size_t ws_bytes, void* stream) {
     AttnDev a;
     int rc = make_dev(p, &a);
     if (rc != TT_OK) return rc;
     if (!o || !lse) return TT_E_ARG;
     if (!aligned(o, 16)) return TT_E_ARG;
-    if (p->dtype == TT_DTYPE_BF16) return tt_fwd_bf16_launch(a, o, lse, (hipStream_t)stream);
+    const size_t need = tt_attn_fwd_workspace_bytes(p);
+    if (need > 0 && (!ws || !aligned(ws, 16))) return TT_E_ARG;
+    if (ws_bytes < need) return TT_E_WORKSPACE;
+    if (p->dtype == TT_DTYPE_BF16) {
+        FwdSplit sp{nullptr, nullptr, nullptr, key_splits(p)};
+        if (sp.n > 1) {
+            uint8_t* w = reinterpret_cast<uint8_t*>(ws);
+            sp.o = reinterpret_cast<float*>(w);
+            sp.m = reinterpret_cast<float*>(w + split_part_bytes(p));
+            sp.l = reinterpret_cast<float*>(w + split_part_bytes(p) + split_stat_bytes(p));
+        }
+        return tt_fwd_bf16_launch(a, o, lse, sp, (hipStream_t)stream);
+    }
     return tt_fwd_f32_launch(a, o, lse, (hipStream_t)stream);
 }
 
-// Workspace: delta [Hq, n_q] fp32, then (bf16 problems) the fp32 dK and dV
-// sums of key tiles whose query range is split over several work items,
-// [n_keys, Hkv, head_dim] each, then (bf16, TT_BWD_DETERMINISTIC) the dK and
-// dV slots of those tiles' later items, [tt_det_slots, 128, Hkv, head_dim] each.
+// Workspace: delta [Hq, n_q] fp32, then the fp32 dK and dV sums of key tiles
+// whose query range is split over several work items, [n_keys, Hkv, head_dim]
+// each, then (TT_BWD_DETERMINISTIC) the dK and dV slots of those tiles' later
+// items, [tt_det_slots, 128, Hkv, head_dim] each, then (bf16 problems with
+// tt_key_splits > 1) the dQ pass's fp32 partials [splits, n_q, Hq, head_dim].
 static size_t delta_bytes(const tt_attn_problem* p) {
     return ((size_t)p->n_heads_q * (size_t)p->n_q * sizeof(float) + 255) & ~(size_t)255;
 }
@@ -177,7 +211,7 @@ size_t tt_attn_bwd_workspace_bytes(const tt_attn_problem* p) {
     if ((int64_t)p->n_q + p->n_past > 0x3fffffff) return 0;
     size_t b = delta_bytes(p) + 2 * split_rows_bytes(p);
     if (p->bwd_parts & TT_BWD_DETERMINISTIC) b += 2 * det_slot_bytes(p);
-    return b;
+    return b + split_part_bytes(p);
 }
 
 int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_tensor d_o, void* dq, void* dk,
@@ -210,15 +244,19 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
     b.delta = reinterpret_cast<float*>(ws);
     if (p->bwd_parts & ~(TT_BWD_DELTA | TT_BWD_DQ | TT_BWD_DKDV | TT_BWD_DETERMINISTIC)) return TT_E_ARG;
     b.det = (p->bwd_parts & TT_BWD_DETERMINISTIC) ? 1 : 0;
-    b.dk_ws = b.dv_ws = b.dk_slot = b.dv_slot = nullptr;
+    b.dk_ws = b.dv_ws = b.dk_slot = b.dv_slot = b.dq_part = nullptr;
+    b.n_split = key_splits(p);
     {
         uint8_t* w = reinterpret_cast<uint8_t*>(ws) + delta_bytes(p);
         b.dk_ws = reinterpret_cast<float*>(w);
         b.dv_ws = reinterpret_cast<float*>(w + split_rows_bytes(p));
+        w += 2 * split_rows_bytes(p);
         if (b.det) {
-            b.dk_slot = reinterpret_cast<float*>(w + 2 * split_rows_bytes(p));
-            b.dv_slot = reinterpret_cast<float*>(w + 2 * split_rows_bytes(p) + det_slot_bytes(p));
+            b.dk_slot = reinterpret_cast<float*>(w);
+            b.dv_slot = reinterpret_cast<float*>(w + det_slot_bytes(p));
+            w += 2 * det_slot_bytes(p);
         }
+        if (b.n_split > 1) b.dq_part = reinterpret_cast<float*>(w);
     }
     const int parts = p->bwd_parts & (TT_BWD_DELTA | TT_BWD_DQ | TT_BWD_DKDV);
     b.parts = parts ? parts : (TT_BWD_DELTA | TT_BWD_DQ | TT_BWD_DKDV);

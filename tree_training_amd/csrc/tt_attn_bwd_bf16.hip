@@ -38,8 +38,11 @@ struct DqStage {
 };
 
 // FUSE_DELTA: the kernel also computes delta = rowsum(dO * O) of its rows (and
-// stores it for the dK/dV pass) instead of reading it.
-template <bool FUSE_DELTA>
+// stores it for the dK/dV pass) instead of reading it. SPLIT: workgroup
+// (pair, blockIdx.y) walks the blockIdx.y-th of bw.n_split contiguous ranges
+// of the pair's key tiles and writes its unscaled fp32 dQ partial for
+// bwd_dq_combine_kernel (split 0 stores delta).
+template <bool FUSE_DELTA, bool SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_dq_bf16_kernel(AttnDev a, BwdDev bw) {
     __shared__ __attribute__((aligned(16))) DqStage st[2];
 
@@ -73,7 +76,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 for (int e = 0; e < 8; ++e) acc += (float)ov[e] * (float)da[t][e];
             }
             dlt = halves_sum(acc);
-            if (half == 0) bw.delta[(size_t)h * a.n_q + qi] = dlt;
+            if (half == 0 && (!SPLIT || blockIdx.y == 0)) bw.delta[(size_t)h * a.n_q + qi] = dlt;
         } else {
             dlt = bw.delta[(size_t)h * a.n_q + qi];
         }
@@ -88,20 +91,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     const int cnt = a.row_cnt[qb];
     const int* list = a.row_list + (size_t)qb * a.n_kt;
+    int it0 = 0, it1 = cnt;
+    if constexpr (SPLIT) {
+        it0 = cnt * (int)blockIdx.y / bw.n_split;
+        it1 = cnt * ((int)blockIdx.y + 1) / bw.n_split;
+    }
     KvTileStager stg;
     Bounds nb;
-    if (cnt > 0) {
-        stg.begin(a, list[0] >> 1, g);
-        fetch_bounds(a, list[0] >> 1, nb);
+    if (it1 > it0) {
+        stg.begin(a, list[it0] >> 1, g);
+        fetch_bounds(a, list[it0] >> 1, nb);
     }
-    for (int it = 0; it < cnt; ++it) {
+    for (int it = it0; it < it1; ++it) {
         DqStage& S = st[it & 1];
         const bool full = list[it] & 1;
         stg.commit(a, g, S.K, S.V);
         store_bounds(nb, S.lo, S.hi);
         __syncthreads();
         {   // the last step re-stages its own tile: the loads are unconditional
-            const int kt1 = list[it + 1 < cnt ? it + 1 : it] >> 1;
+            const int kt1 = list[it + 1 < it1 ? it + 1 : it] >> 1;
             stg.begin(a, kt1, g);
             fetch_bounds(a, kt1, nb);
         }
@@ -136,6 +144,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     }
 
+    if constexpr (SPLIT) {
+        if (qi < a.n_q) {
+            float* op = bw.dq_part + (((size_t)blockIdx.y * a.n_q + qi) * a.hq + h) * D;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int grp = 0; grp < 4; ++grp) {
+                    f32x4 w;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) w[e] = dq[db][4 * grp + e];
+                    *(f32x4*)(op + 32 * db + 8 * grp + 4 * half) = w;
+                }
+        }
+        return;
+    }
     if (qi < a.n_q) {
         bf16* op = (bf16*)bw.dq + ((size_t)qi * a.hq + h) * D;
 #pragma unroll
@@ -148,6 +171,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 *(bf16x4*)(op + 32 * db + 8 * grp + 4 * half) = w;
             }
     }
+}
+
+// dQ = scale * (sum of the key-range partials, in range order), four
+// elements per thread.
+__global__ __launch_bounds__(256) void bwd_dq_combine_kernel(AttnDev a, BwdDev bw) {
+    const size_t n4 = (size_t)a.n_q * a.hq * (D / 4);
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const size_t stride = (size_t)a.n_q * a.hq * D;
+    f32x4 acc = *(const f32x4*)(bw.dq_part + 4 * i);
+    for (int s = 1; s < bw.n_split; ++s) {
+        const f32x4 v = *(const f32x4*)(bw.dq_part + s * stride + 4 * i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] += v[e];
+    }
+    bf16x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = (bf16)(acc[e] * a.scale);
+    *(bf16x4*)((bf16*)bw.dq + 4 * i) = w;
 }
 
 // ----------------------------------------------------------------------------
@@ -454,10 +496,19 @@ int tt_bwd_bf16_launch(const AttnDev& a, const BwdDev& b, hipStream_t s) {
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     if (b.parts & TT_BWD_DQ) {
-        if (fuse)
-            hipLaunchKernelGGL(bwd_dq_bf16_kernel<true>, dim3(a.n_qb * a.hq), dim3(256), 0, s, a, b);
-        else
-            hipLaunchKernelGGL(bwd_dq_bf16_kernel<false>, dim3(a.n_qb * a.hq), dim3(256), 0, s, a, b);
+        if (b.n_split > 1) {
+            const dim3 grid(a.n_qb * a.hq, b.n_split);
+            if (fuse)
+                hipLaunchKernelGGL((bwd_dq_bf16_kernel<true, true>), grid, dim3(256), 0, s, a, b);
+            else
+                hipLaunchKernelGGL((bwd_dq_bf16_kernel<false, true>), grid, dim3(256), 0, s, a, b);
+            const size_t n4 = (size_t)a.n_q * a.hq * (D / 4);
+            hipLaunchKernelGGL(bwd_dq_combine_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, a, b);
+        } else if (fuse) {
+            hipLaunchKernelGGL((bwd_dq_bf16_kernel<true, false>), dim3(a.n_qb * a.hq), dim3(256), 0, s, a, b);
+        } else {
+            hipLaunchKernelGGL((bwd_dq_bf16_kernel<false, false>), dim3(a.n_qb * a.hq), dim3(256), 0, s, a, b);
+        }
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     if (b.parts & TT_BWD_DKDV) {

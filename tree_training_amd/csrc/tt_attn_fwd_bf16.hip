@@ -18,7 +18,11 @@ struct FwdStage {
     int hi[TT_BK];
 };
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_bf16_kernel(AttnDev a, bf16* __restrict__ out, float* __restrict__ lse) {
+// SPLIT: workgroup (pair, blockIdx.y) walks the blockIdx.y-th of sp.n
+// contiguous ranges of the pair's key tiles and writes the unnormalised
+// output, row max and row sum of that range for fwd_combine_kernel.
+template <bool SPLIT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_bf16_kernel(AttnDev a, bf16* __restrict__ out, float* __restrict__ lse, FwdSplit sp) {
     __shared__ __attribute__((aligned(16))) FwdStage st[2];
 
     int qb, h;
@@ -48,21 +52,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // from them (tile bases, buffer descriptors) in scalar registers.
     const int cnt = __builtin_amdgcn_readfirstlane(a.row_cnt[qb]);
     const int* list = a.row_list + (size_t)qb * a.n_kt;
+    int it0 = 0, it1 = cnt;
+    if constexpr (SPLIT) {
+        it0 = cnt * (int)blockIdx.y / sp.n;
+        it1 = cnt * ((int)blockIdx.y + 1) / sp.n;
+    }
     KvTileStager stg;
     Bounds nb;
-    if (cnt > 0) {
-        const int kt0 = __builtin_amdgcn_readfirstlane(list[0] >> 1);
+    if (it1 > it0) {
+        const int kt0 = __builtin_amdgcn_readfirstlane(list[it0] >> 1);
         stg.begin(a, kt0, g);
         fetch_bounds(a, kt0, nb);
     }
-    for (int it = 0; it < cnt; ++it) {
+    for (int it = it0; it < it1; ++it) {
         FwdStage& S = st[it & 1];
         const bool full = __builtin_amdgcn_readfirstlane(list[it]) & 1;
         stg.commit(a, g, S.K, S.V);
         store_bounds(nb, S.lo, S.hi);
         __syncthreads();
         {   // the last step re-stages its own tile: the loads are unconditional
-            const int kt1 = __builtin_amdgcn_readfirstlane(list[it + 1 < cnt ? it + 1 : it] >> 1);
+            const int kt1 = __builtin_amdgcn_readfirstlane(list[it + 1 < it1 ? it + 1 : it] >> 1);
             stg.begin(a, kt1, g);
             fetch_bounds(a, kt1, nb);
         }
@@ -133,6 +142,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 
     const float l_tot = halves_sum(l_run);
+    if constexpr (SPLIT) {
+        if (qi < a.n_q) {
+            const int s = blockIdx.y;
+            float* op = sp.o + (((size_t)s * a.n_q + qi) * a.hq + h) * D;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int grp = 0; grp < 4; ++grp) {
+                    f32x4 w;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) w[e] = o[db][4 * grp + e];
+                    *(f32x4*)(op + 32 * db + 8 * grp + 4 * half) = w;
+                }
+            if (half == 0) {
+                const size_t mi = ((size_t)s * a.hq + h) * a.n_q + qi;
+                sp.m[mi] = (m_run == -INFINITY) ? 0.0f : m_run;
+                sp.l[mi] = l_tot;
+            }
+        }
+        return;
+    }
     if (qi < a.n_q) {
         const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
         bf16* op = out + ((size_t)qi * a.hq + h) * D;
@@ -152,9 +182,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
+// Merges the key-range partials of each (query, q head) row: with M the
+// largest row max of the ranges that saw a key, O = sum_s 2^(m_s - M) O_s /
+// sum_s 2^(m_s - M) l_s, lse = (M + log2 of that sum) ln 2, ranges added in
+// order. 32 threads per row, four columns each.
+__global__ __launch_bounds__(256) void fwd_combine_kernel(AttnDev a, bf16* __restrict__ out, float* __restrict__ lse,
+                                                          FwdSplit sp) {
+    const int row = blockIdx.x * 8 + (threadIdx.x >> 5);
+    if (row >= a.n_q * a.hq) return;
+    const int qi = row / a.hq, h = row - qi * a.hq;
+    const int c4 = (threadIdx.x & 31) * 4;
+    float mx = -INFINITY;
+    for (int s = 0; s < sp.n; ++s) {
+        const size_t mi = ((size_t)s * a.hq + h) * a.n_q + qi;
+        if (sp.l[mi] > 0.0f) mx = fmaxf(mx, sp.m[mi]);
+    }
+    float l_sum = 0.0f;
+    f32x4 acc = {};
+    for (int s = 0; s < sp.n; ++s) {
+        const size_t mi = ((size_t)s * a.hq + h) * a.n_q + qi;
+        const float l = sp.l[mi];
+        if (!(l > 0.0f)) continue;
+        const float w = exp2f(sp.m[mi] - mx);
+        l_sum = fmaf(w, l, l_sum);
+        const f32x4 v = *(const f32x4*)(sp.o + ((size_t)s * a.n_q + qi) * a.hq * D + (size_t)h * D + c4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = fmaf(w, v[e], acc[e]);
+    }
+    const float inv = l_sum > 0.0f ? 1.0f / l_sum : 0.0f;
+    bf16x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = (bf16)(acc[e] * inv);
+    *(bf16x4*)(out + ((size_t)qi * a.hq + h) * D + c4) = r;
+    if (c4 == 0) lse[(size_t)h * a.n_q + qi] = l_sum > 0.0f ? (mx + __log2f(l_sum)) * TT_LN2 : -INFINITY;
+}
+
 }  // namespace
 
-int tt_fwd_bf16_launch(const AttnDev& a, void* o, float* lse, hipStream_t s) {
-    hipLaunchKernelGGL(fwd_bf16_kernel, dim3(a.n_qb * a.hq), dim3(256), 0, s, a, (bf16*)o, lse);
+int tt_fwd_bf16_launch(const AttnDev& a, void* o, float* lse, const FwdSplit& sp, hipStream_t s) {
+    if (sp.n > 1) {
+        hipLaunchKernelGGL(fwd_bf16_kernel<true>, dim3(a.n_qb * a.hq, sp.n), dim3(256), 0, s, a, (bf16*)o, lse, sp);
+        hipLaunchKernelGGL(fwd_combine_kernel, dim3(tt_cdiv(a.n_q * a.hq, 8)), dim3(256), 0, s, a, (bf16*)o, lse,
+                           sp);
+    } else {
+        hipLaunchKernelGGL(fwd_bf16_kernel<false>, dim3(a.n_qb * a.hq), dim3(256), 0, s, a, (bf16*)o, lse, sp);
+    }
     return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
 }

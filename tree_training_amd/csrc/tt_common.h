@@ -41,6 +41,17 @@ __host__ __device__ inline int tt_qch(int n_q) {
     const int half = n_q >= 2 ? (1 << (31 - __builtin_clz((unsigned)n_q))) / 2 : 0;   // half the largest power of 2 <= n_q
     return half > 4096 ? 4096 : (half < 256 ? 256 : half);
 }
+// Key-range split of the bf16 forward and dQ passes. Their grids hold one
+// workgroup per (query block, q head) pair; with at most 256 pairs (one per
+// CU) half the chip's resident slots idle while each workgroup walks its whole
+// key list, as for a partition of a few hundred queries under a gateway of
+// thousands of keys. Such problems cut every pair's key tiles into 4
+// contiguous ranges, one workgroup each; a combine pass merges the fp32
+// partials in range order. (Splitting 257-511 pairs in two or three did not
+// pay for the partials' traffic and the combine launch.)
+__host__ __device__ inline int tt_key_splits(int n_q, int hq) {
+    return tt_cdiv(n_q, TT_BQ) * hq <= 256 ? 4 : 1;
+}
 // dK/dV work items of a key tile whose visible queries are [qlo, qhi). A range
 // of at most qch queries is one item; a longer one is cut at multiples of qch
 // in absolute query index, so workgroups busy with different key tiles at the

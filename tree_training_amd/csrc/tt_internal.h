@@ -43,6 +43,18 @@ struct BwdDev {
     float* dv_slot;           //   of split key tiles (null otherwise)
     int parts;                // OR of TT_BWD_DELTA / _DQ / _DKDV (never 0 here)
     int det;                  // TT_BWD_DETERMINISTIC given (bf16: split tiles summed in chunk order)
+    float* dq_part;           // bf16 with tt_key_splits > 1: [splits, n_q, hq, 128] fp32 dQ partials
+    int n_split;              // tt_key_splits of the problem (bf16), else 1
+};
+
+// Key-range split of the bf16 forward (tt_key_splits > 1): per split, the
+// unnormalised output [n_q, hq, 128] and the row max (log2 units) and row sum
+// [hq, n_q] it is taken against, all fp32.
+struct FwdSplit {
+    float* o;
+    float* m;
+    float* l;
+    int n;
 };
 
 // Device-side view of a tt_gdn_problem.
@@ -148,7 +160,7 @@ bool tt_trees_job_fits(int n_tokens, int n_keys);
 int tt_plan_build_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys, int n_q, void* plan,
                        hipStream_t s);
 
-int tt_fwd_bf16_launch(const AttnDev& a, void* o, float* lse, hipStream_t s);
+int tt_fwd_bf16_launch(const AttnDev& a, void* o, float* lse, const FwdSplit& sp, hipStream_t s);
 int tt_bwd_bf16_launch(const AttnDev& a, const BwdDev& b, hipStream_t s);
 int tt_fwd_f32_launch(const AttnDev& a, void* o, float* lse, hipStream_t s);
 int tt_bwd_f32_launch(const AttnDev& a, const BwdDev& b, hipStream_t s);
