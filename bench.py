@@ -194,6 +194,11 @@ def main():
         _lib.check(lib.tt_attn_fwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), _ptr(fws) if fws is not None else None,
                                    fws.numel() if fws is not None else 0, st), "fwd")
         rec(1)
+        if ev is None:   # one call, as the autograd backward makes it
+            pb.s.bwd_parts = 0
+            _lib.check(lib.tt_attn_bwd(ctypes.byref(pb.s), _ptr(o), _ptr(lse), dt, _ptr(dq), _ptr(dk), _ptr(dv),
+                                       _ptr(ak), _ptr(av), _ptr(ws), ws_bytes, st), "bwd")
+            return o, dq, dk, dv
         # delta and dQ in one call (the dQ kernel computes delta), then dK/dV:
         # the same work as bwd_parts=0, split only to time the passes
         pb.s.bwd_parts = _lib.TT_BWD_DELTA | _lib.TT_BWD_DQ

@@ -260,6 +260,7 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
     }
     const int parts = p->bwd_parts & (TT_BWD_DELTA | TT_BWD_DQ | TT_BWD_DKDV);
     b.parts = parts ? parts : (TT_BWD_DELTA | TT_BWD_DQ | TT_BWD_DKDV);
+    b.zero_in_dq = p->dtype == TT_DTYPE_BF16 && !b.det && (b.parts & TT_BWD_DQ) && (b.parts & TT_BWD_DKDV);
     if (p->dtype == TT_DTYPE_BF16) return tt_bwd_bf16_launch(a, b, (hipStream_t)stream);
     return tt_bwd_f32_launch(a, b, (hipStream_t)stream);
 }

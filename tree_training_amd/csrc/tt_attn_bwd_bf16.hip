@@ -157,9 +157,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     *(f32x4*)(op + 32 * db + 8 * grp + 4 * half) = w;
                 }
         }
-        return;
-    }
-    if (qi < a.n_q) {
+    } else if (qi < a.n_q) {
         bf16* op = (bf16*)bw.dq + ((size_t)qi * a.hq + h) * D;
 #pragma unroll
         for (int db = 0; db < 4; ++db)
@@ -170,6 +168,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 for (int e = 0; e < 4; ++e) w[e] = (bf16)(dq[db][4 * grp + e] * a.scale);
                 *(bf16x4*)(op + 32 * db + 8 * grp + 4 * half) = w;
             }
+    }
+    // The dK/dV pass of the same call needs its split sums cleared: each
+    // workgroup takes every n-th (key tile, kv head), which saves that pass a
+    // launch of its own.
+    if (bw.zero_in_dq) {
+        const int n_wg = gridDim.x * gridDim.y;
+        for (int t = blockIdx.x + blockIdx.y * gridDim.x; t < a.n_kb * a.hkv; t += n_wg)
+            split_zero_tile(a, bw, t / a.hkv, t % a.hkv);
     }
 }
 
@@ -516,7 +522,10 @@ int tt_bwd_bf16_launch(const AttnDev& a, const BwdDev& b, hipStream_t s) {
             hipLaunchKernelGGL(bwd_dkdv_bf16_kernel, dim3(dkdv_grid(a)), dim3(256), 0, s, a, b);
             hipLaunchKernelGGL(bwd_split_finalize_det_kernel<bf16>, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
         } else {
-            hipLaunchKernelGGL(bwd_split_zero_kernel, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
+            // split sums start at zero: cleared by the dQ pass of this call,
+            // else by a launch of their own
+            if (!b.zero_in_dq)
+                hipLaunchKernelGGL(bwd_split_zero_kernel, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
             hipLaunchKernelGGL(bwd_dkdv_bf16_kernel, dim3(dkdv_grid(a)), dim3(256), 0, s, a, b);
             hipLaunchKernelGGL(bwd_split_finalize_kernel<bf16>, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
         }

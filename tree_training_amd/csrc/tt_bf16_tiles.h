@@ -338,8 +338,9 @@ __device__ __forceinline__ void store_out4(void* base, size_t idx, const f32x4& 
 // (split gateway keys add straight into the caller's fp32 accumulators) ...
 // (16-byte vectors: the workspace and the gateway accumulators are 16-byte
 // aligned and rows are 128 floats)
-__global__ __launch_bounds__(256) void bwd_split_zero_kernel(AttnDev a, BwdDev bw) {
-    const int kb = blockIdx.x, g = blockIdx.y;
+// The zeroing of key tile kb, kv head g by one workgroup: the fp32 sums of its
+// own keys, if its query range is split.
+__device__ __forceinline__ void split_zero_tile(const AttnDev& a, const BwdDev& bw, int kb, int g) {
     if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb], tt_qch(a.n_q)) <= 1) return;
     const int k_first = max(kb * TT_BKB, a.n_past), k_end = min(kb * TT_BKB + TT_BKB, a.n_keys);
     for (int e = threadIdx.x; e < (k_end - k_first) * (D / 4); e += 256) {
@@ -350,11 +351,14 @@ __global__ __launch_bounds__(256) void bwd_split_zero_kernel(AttnDev a, BwdDev b
     }
 }
 
-// ... and convert them to dk/dv after it.
+__global__ __launch_bounds__(256) void bwd_split_zero_kernel(AttnDev a, BwdDev bw) {
+    split_zero_tile(a, bw, blockIdx.x, blockIdx.y);
+}
+
+// ... and convert them to dk/dv after it: the fp32 sums of tile kb's own
+// keys for kv head g, by one workgroup.
 template <typename TOut>
-__global__ __launch_bounds__(256) void bwd_split_finalize_kernel(AttnDev a, BwdDev bw) {
-    const int kb = blockIdx.x, g = blockIdx.y;
-    if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb], tt_qch(a.n_q)) <= 1) return;
+__device__ __forceinline__ void split_convert_tile(const AttnDev& a, const BwdDev& bw, int kb, int g) {
     const int k_first = max(kb * TT_BKB, a.n_past), k_end = min(kb * TT_BKB + TT_BKB, a.n_keys);
     for (int e = threadIdx.x; e < (k_end - k_first) * (D / 4); e += 256) {
         const int key = k_first + e / (D / 4), d = 4 * (e % (D / 4));
@@ -364,6 +368,13 @@ __global__ __launch_bounds__(256) void bwd_split_finalize_kernel(AttnDev a, BwdD
         store_out4<TOut>(bw.dk, idx, gk);
         store_out4<TOut>(bw.dv, idx, gv);
     }
+}
+
+template <typename TOut>
+__global__ __launch_bounds__(256) void bwd_split_finalize_kernel(AttnDev a, BwdDev bw) {
+    const int kb = blockIdx.x, g = blockIdx.y;
+    if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb], tt_qch(a.n_q)) <= 1) return;
+    split_convert_tile<TOut>(a, bw, kb, g);
 }
 
 // Deterministic mode: one workgroup per (key tile rank, kv head) sums a split

@@ -45,6 +45,7 @@ struct BwdDev {
     int det;                  // TT_BWD_DETERMINISTIC given (bf16: split tiles summed in chunk order)
     float* dq_part;           // bf16 with tt_key_splits > 1: [splits, n_q, hq, 128] fp32 dQ partials
     int n_split;              // tt_key_splits of the problem (bf16), else 1
+    int zero_in_dq;           // the dQ pass clears the split sums for the dK/dV pass of the same call
 };
 
 // Key-range split of the bf16 forward (tt_key_splits > 1): per split, the
