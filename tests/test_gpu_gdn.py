@@ -56,6 +56,8 @@ CASES = {
     "single_tokens": dict(topo=lambda: ([1] * 9, [-1, 0, 1, 1, 3, -1, 5, 5, 0]), Hk=1, Hv=1),
     "c1_heads": dict(topo=lambda: ([3, 4, 3, 4, 5, 3, 3, 4, 4, 3, 4, 3, 4],
                                    [-1, 0, 1, 2, 3, 3, 2, 6, -1, 8, 9, 8, 11]), Hk=16, Hv=32),
+    # a level of 20 nodes x 32 v heads under a 40-token root
+    "wide_level": dict(topo=lambda: ([40] + [7 + 3 * i for i in range(20)], [-1] + [0] * 20), Hk=16, Hv=32),
 }
 
 

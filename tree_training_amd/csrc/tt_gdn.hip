@@ -16,13 +16,13 @@
 //  * gdn_prep_kernel — one workgroup per (chunk, v head), all chunks at once:
 //    everything that does not depend on the state (A, T by a product of
 //    (I + N^(2^r)) factors, U, W, G) into the workspace.
-//  * gdn_scan_kernel — one workgroup per (node, v head), one launch per tree
-//    level so a node's parent state (in the caller's node_states buffer) is
-//    complete when it starts; each of its four waves holds a 128 x 32 value
-//    slice of the state in MFMA accumulators (the delta rule is independent
-//    per value column) and walks the node's chunks.
-// fp32 end to end: the prep on the vector ALUs, the scans on fp32 MFMA
-// (v_mfma_f32_32x32x2_f32).
+//  * gdn_scan_cols_kernel — per (node, v head) two workgroups of four waves,
+//    one launch per tree level so a node's parent state (in the caller's
+//    node_states buffer) is complete when it starts; each wave holds a
+//    128 x 16 value slice of the state in MFMA accumulators (the delta rule is
+//    independent per value column) and walks the node's chunks.
+// fp32 end to end: the prep on fp32 MFMA (v_mfma_f32_32x32x2_f32) and the
+// vector ALUs, the scans on v_mfma_f32_16x16x4_f32.
 #include "tt_gdn_common.h"
 
 namespace {
@@ -169,9 +169,33 @@ struct ScanLds {
     float G[GC];
 };
 
-// Wave w owns value columns 32w .. 32w+31 of one (node, v head): its 128 x 32
-// state slice lives in four accumulator tiles (rows 32 rb + acc_row(r, half))
-// for the whole node. Per chunk:
+// Column layout of the level scans. The value columns of the delta rule are
+// independent (column j of V', O and S depends only on column j of U, S and
+// V'); each wave owns 16 of them (16 x 16 fp32 MFMA tiles), and a (node,
+// v head) takes two workgroups of four waves (64 columns each) on different
+// CUs. A level with few nodes is a serial chain of chunks per node while most
+// CUs idle, and each chunk then runs on twice the MFMA pipes of one
+// workgroup. Workgroup x of a level launch takes a head and a column block;
+// with Hv a multiple of 8 the two blocks of a head are 8 apart (same XCD and
+// L2, dispatched together).
+constexpr int SCAN_COLS = 64;
+constexpr int kScanSplit = GD / SCAN_COLS;
+__device__ __forceinline__ void scan_block(const GdnDev& p, int& h, int& c0) {
+    const int bx = blockIdx.x;
+    int cs;
+    if ((p.hv & 7) == 0) {
+        h = ((bx >> 4) << 3) | (bx & 7);
+        cs = (bx >> 3) & 1;
+    } else {
+        h = bx >> 1;
+        cs = bx & 1;
+    }
+    c0 = SCAN_COLS * cs;
+}
+
+// Wave w owns value columns c0 + 16w .. +15 of one (node, v head): its
+// 128 x 16 state slice lives in eight 16 x 16 accumulator tiles (rows
+// 16 rb + 4 (l >> 4) + v) for the whole node. Per chunk (two 16-token tiles):
 //   V' = U - W S,  qS  (A = W / q^ rows from LDS, B = S from registers)
 //   O = e^G qS + A V'  (B = V' from registers)
 //   S <- e^{G_L} S + (k^ e^{G_L - G})^T V'  (A = k~ from LDS, B = V')
@@ -183,28 +207,31 @@ struct ScanLds {
 // node's chunks, while the state registers still hold S0, replaces each
 // chunk's U by its V' in the workspace; the scan proper then reads V' there.
 template <typename TIn, bool TRUNC>
-__global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_scan_kernel(GdnDev p, int lvl_begin, float* __restrict__ ws,
+__global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_scan_cols_kernel(GdnDev p, int lvl_begin, float* __restrict__ ws,
                                                       TIn* __restrict__ out, float* __restrict__ states,
                                                       float* __restrict__ chunk_sin, float* __restrict__ chunk_vp) {
     __shared__ __attribute__((aligned(16))) ScanLds L;
     const int node = p.level_nodes[lvl_begin + blockIdx.y];
     if (node < 0 || node >= p.n_nodes) return;
-    const int h = blockIdx.x;
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, col = lane & 31, half = lane >> 5;
-    const int j = 32 * wave + col;                                        // this lane's value column
+    int h, cb;
+    scan_block(p, h, cb);
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, c16 = lane & 15, g4 = 4 * (lane >> 4);
+    const int j = cb + 16 * wave + c16;                                   // this lane's value column
+    const int jt = cb + 16 * wave;                                        // the wave's first column
     const int start = p.node_start[node], len = p.node_len[node], chunk0 = p.node_chunk0[node];
     int par = p.parent[node];
     if (start < 0 || len < 0 || start > p.n_tokens - len) return;        // malformed node: skipped
     if (chunk0 < 0 || chunk0 > p.n_chunks - tt_cdiv(len, GC)) return;
     if (par >= node || par < -1) par = -1;                               // parents precede children
 
-    f32x16 S[4];
+    f32x4 S[8];
     if (par >= 0) {
-        const AccMat m = acc_mat(states + ((size_t)par * p.hv + h) * GD * GD, GD, half, j);
-        for_tiles([&](auto rb) { S[rb.value] = load_acc<32 * rb.value>(m); });
+        const float* sp = states + ((size_t)par * p.hv + h) * GD * GD + jt;
+#pragma unroll
+        for (int rb = 0; rb < 8; ++rb) S[rb] = load_t16(sp + 16 * rb * GD, lane);
     } else {
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) S[rb] = (f32x16){};
+        for (int rb = 0; rb < 8; ++rb) S[rb] = (f32x4){};
     }
 
     if constexpr (TRUNC) {
@@ -218,19 +245,20 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                 for (int e = 0; e < 16; e += 4)
                     *(f32x4*)&L.W[i * RS + d0 + e] = *(const f32x4*)(cw + kWsW + i * GD + d0 + e);
             }
-            const AccMat um = acc_mat(cw + kWsU, GC, half, j);
-            f32x16 vp = load_acc<0>(um);
+            f32x4 vp[2];
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) vp[tb] = load_t16(cw + kWsU + 16 * tb * GD + jt, lane);
             __syncthreads();
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
+            for (int rb = 0; rb < 8; ++rb)
 #pragma unroll
-                for (int r4 = 0; r4 < 16; r4 += 4) {
-                    const f32x4 wv = *(const f32x4*)&L.W[col * RS + 32 * rb + 8 * (r4 >> 2) + 4 * half];
+                for (int tb = 0; tb < 2; ++tb) {
+                    const f32x4 wv = *(const f32x4*)&L.W[(16 * tb + c16) * RS + 16 * rb + g4];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) vp = mfma_f32(-wv[e], S[rb][r4 + e], vp);
+                    for (int v = 0; v < 4; ++v) vp[tb] = mfma16_f32(-wv[v], S[rb][v], vp[tb]);
                 }
-            }
-            store_acc<0>(um, vp);   // read back by this same lane below
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) store_t16(cw + kWsU + 16 * tb * GD + jt, lane, vp[tb]);   // read back by this lane
         }
     }
 
@@ -239,8 +267,9 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         const size_t ch = (size_t)(chunk0 + c0 / GC) * p.hv + h;
         const float* cw = ws + ch * kWsChunk;
         if (chunk_sin) {
-            const AccMat m = acc_mat(chunk_sin + ch * GD * GD, GD, half, j);
-            for_tiles([&](auto rb) { store_acc<32 * rb.value>(m, S[rb.value]); });
+            float* sp = chunk_sin + ch * GD * GD + jt;
+#pragma unroll
+            for (int rb = 0; rb < 8; ++rb) store_t16(sp + 16 * rb * GD, lane, S[rb]);
         }
         __syncthreads();   // readers of the previous chunk's tiles are done
         load_chunk_rows<TIn>(p, start + c0, Lc, h, L.Q, L.K, nullptr);
@@ -261,54 +290,52 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             if (t < GC) L.G[t] = cw[kWsG + t];
         }
         // U (TRUNC: V', written by the first pass)
-        f32x16 vp = load_acc<0>(acc_mat(cw + kWsU, GC, half, j)), qs = {};
+        f32x4 vp[2], qs[2];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            vp[tb] = load_t16(cw + kWsU + 16 * tb * GD + jt, lane);
+            qs[tb] = (f32x4){};
+        }
         __syncthreads();
 
-        // V' = U - W S and q^ S: 4 row tiles of S x 16 steps.
+        // V' = U - W S and q^ S: 8 row tiles of S x 4 steps, for both token tiles.
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
+        for (int rb = 0; rb < 8; ++rb) {
 #pragma unroll
-            for (int r4 = 0; r4 < 16; r4 += 4) {
-                const int k0 = 32 * rb + 8 * (r4 >> 2) + 4 * half;          // acc_row(r4 .. r4+3, half)
-                const f32x4 qv = *(const f32x4*)&L.Q[col * RS + k0];
+            for (int tb = 0; tb < 2; ++tb) {
+                const int ro = (16 * tb + c16) * RS + 16 * rb + g4;
+                const f32x4 qv = *(const f32x4*)&L.Q[ro];
                 if constexpr (!TRUNC) {
-                    const f32x4 wv = *(const f32x4*)&L.W[col * RS + k0];
+                    const f32x4 wv = *(const f32x4*)&L.W[ro];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) vp = mfma_f32(-wv[e], S[rb][r4 + e], vp);
+                    for (int v = 0; v < 4; ++v) vp[tb] = mfma16_f32(-wv[v], S[rb][v], vp[tb]);
                 }
 #pragma unroll
-                for (int e = 0; e < 4; ++e) qs = mfma_f32(qv[e], S[rb][r4 + e], qs);
+                for (int v = 0; v < 4; ++v) qs[tb] = mfma16_f32(qv[v], S[rb][v], qs[tb]);
+                __builtin_amdgcn_sched_barrier(0);   // operand reads one step ahead at most (registers)
             }
-            __builtin_amdgcn_sched_barrier(0);   // keep operand prefetch within one row tile (registers)
         }
-        if (chunk_vp) store_acc<0>(acc_mat(chunk_vp + ch * GC * GD, GC, half, j), vp);
-        // O = e^G (q^ S) + A V'.
-        {
-            f32x16 o;
+        if (chunk_vp) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o[r] = qs[r] * expf(L.G[acc_row(r, half)]);
+            for (int tb = 0; tb < 2; ++tb) store_t16(chunk_vp + ch * GC * GD + 16 * tb * GD + jt, lane, vp[tb]);
+        }
+        // O = e^G (q^ S) + A V', token tile by token tile.
 #pragma unroll
-            for (int r4 = 0; r4 < 16; r4 += 4) {
-                const f32x4 av = *(const f32x4*)&L.A[col * MS + 8 * (r4 >> 2) + 4 * half];
+        for (int tb = 0; tb < 2; ++tb) {
+            f32x4 o;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) o = mfma_f32(av[e], vp[r4 + e], o);
+            for (int v = 0; v < 4; ++v) o[v] = qs[tb][v] * expf(L.G[16 * tb + g4 + v]);
+#pragma unroll
+            for (int tb2 = 0; tb2 < 2; ++tb2) {
+                const f32x4 av = *(const f32x4*)&L.A[(16 * tb + c16) * MS + 16 * tb2 + g4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) o = mfma16_f32(av[v], vp[tb2][v], o);
             }
-            if (out) {   // rows of the chunk; a buffer resource over them, lane offsets per row group
-                const int rs_b = p.hv * GD * (int)sizeof(TIn);
-                const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-                    out + (int64_t)(start + c0) * p.hv * GD, (short)0, Lc * rs_b, 0x00020000);
-                int vo[4];
+            if (out) {
 #pragma unroll
-                for (int k = 0; k < 4; ++k) vo[k] = (4 * half + k) * rs_b + (h * GD + j) * (int)sizeof(TIn);
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    if (acc_row(r, half) >= Lc) continue;
-                    const int so = 8 * (r >> 2) * rs_b;
-                    if constexpr (sizeof(TIn) == 2)
-                        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (TIn)o[r]), rs,
-                                                              vo[r & 3], so, 0);
-                    else
-                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o[r]), rs, vo[r & 3], so, 0);
+                for (int v = 0; v < 4; ++v) {
+                    const int i = 16 * tb + g4 + v;
+                    if (i < Lc) out[((int64_t)(start + c0 + i) * p.hv + h) * GD + j] = (TIn)o[v];
                 }
             }
         }
@@ -316,18 +343,23 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         {
             const float el = expf(L.G[GC - 1]);
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
+            for (int rb = 0; rb < 8; ++rb) {
                 S[rb] *= el;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) S[rb] = mfma_f32(L.K[acc_row(r, half) * RS + 32 * rb + col], vp[r], S[rb]);
-                __builtin_amdgcn_sched_barrier(0);
+                for (int tb = 0; tb < 2; ++tb) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        S[rb] = mfma16_f32(L.K[(16 * tb + g4 + v) * RS + 16 * rb + c16], vp[tb][v], S[rb]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
         }
     }
 
     // Final state of the node (the initial state of its children).
-    const AccMat m = acc_mat(states + ((size_t)node * p.hv + h) * GD * GD, GD, half, j);
-    for_tiles([&](auto rb) { store_acc<32 * rb.value>(m, S[rb.value]); });
+    float* sp = states + ((size_t)node * p.hv + h) * GD * GD + jt;
+#pragma unroll
+    for (int rb = 0; rb < 8; ++rb) store_t16(sp + 16 * rb * GD, lane, S[rb]);
 }
 
 // ----------------------------------------------------------------------------
@@ -335,7 +367,7 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 // ----------------------------------------------------------------------------
 // The backward recomputes the forward (prep + level scans, keeping each
 // chunk's initial state S and V'), then:
-//  * gdn_rscan_kernel — reverse level scan (deepest level first) of dS, the
+//  * gdn_rscan_cols_kernel — reverse level scan (deepest level first) of dS, the
 //    gradient of the state after a chunk, per (node, v head), on fp32 MFMA:
 //      dV' = A^T dO + (e^{G_L - G} k^) dS,
 //      dS <- e^{G_L} dS + (e^G q^)^T dO - W^T dV'.
@@ -358,38 +390,42 @@ struct RscanLds {
     float G[GC];
 };
 
-// Wave w owns value columns 32w .. 32w+31: its 128 x 32 slice of dS lives in
-// four accumulator tiles (as the forward's state), dO of the chunk is loaded
-// in accumulator layout (rows = tokens), and dV' is produced in it, so all
-// three are used straight from registers as MFMA B operands.
+// Column layout as gdn_scan_cols_kernel (scan_block). Wave w owns value
+// columns c0 + 16w .. +15: its 128 x 16 slice of dS lives in eight 16 x 16
+// accumulator tiles, dO of the chunk is loaded in accumulator layout (rows =
+// tokens, two 16-token tiles), and dV' is produced in it, so all three are
+// used straight from registers as MFMA B operands.
 // TRUNC (V' = U - W S0 with the node's initial state S0): the walk leaves out
 // the W term, and a second pass over the node's chunks subtracts
 // sum_c W_c^T dV'_c from the state gradient at the node's entry.
 template <typename TIn, bool TRUNC>
-__global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_rscan_kernel(
+__global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_rscan_cols_kernel(
         GdnDev p, int lvl_begin, const float* __restrict__ ws, const TIn* __restrict__ d_o, int64_t do_st,
         int64_t do_sh, float* __restrict__ chunk_dso, float* __restrict__ chunk_dvp, float* __restrict__ node_dsin) {
     __shared__ __attribute__((aligned(16))) RscanLds L;
     const int node = p.level_nodes[lvl_begin + blockIdx.y];
     if (node < 0 || node >= p.n_nodes) return;
-    const int h = blockIdx.x;
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, col = lane & 31, half = lane >> 5;
-    const int j = 32 * wave + col;
+    int h, cb;
+    scan_block(p, h, cb);
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, c16 = lane & 15, g4 = 4 * (lane >> 4);
+    const int j = cb + 16 * wave + c16;
+    const int jt = cb + 16 * wave;
     const int start = p.node_start[node], len = p.node_len[node], chunk0 = p.node_chunk0[node];
     if (start < 0 || len < 1 || start > p.n_tokens - len) return;        // malformed node: skipped
     if (chunk0 < 0 || chunk0 > p.n_chunks - tt_cdiv(len, GC)) return;
 
     // dS after the node: the sum over its children of their dS at entry.
-    f32x16 dS[4];
+    f32x4 dS[8];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) dS[rb] = (f32x16){};
+    for (int rb = 0; rb < 8; ++rb) dS[rb] = (f32x4){};
     {
         const int c_lo = max(p.child_off[node], 0), c_hi = min(p.child_off[node + 1], p.n_nodes);
         for (int ci = c_lo; ci < c_hi; ++ci) {
             const int child = p.child[ci];
             if (child <= node || child >= p.n_nodes) continue;          // children follow their parent
-            const AccMat m = acc_mat(node_dsin + ((size_t)child * p.hv + h) * GD * GD, GD, half, j);
-            for_tiles([&](auto rb) { dS[rb.value] += load_acc<32 * rb.value>(m); });
+            const float* sp = node_dsin + ((size_t)child * p.hv + h) * GD * GD + jt;
+#pragma unroll
+            for (int rb = 0; rb < 8; ++rb) dS[rb] += load_t16(sp + 16 * rb * GD, lane);
         }
     }
 
@@ -398,8 +434,9 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         const size_t chn = (size_t)(chunk0 + ci) * p.hv + h;
         const float* cw = ws + chn * kWsChunk;
         {   // the gradient of this chunk's output state
-            const AccMat m = acc_mat(chunk_dso + chn * GD * GD, GD, half, j);
-            for_tiles([&](auto rb) { store_acc<32 * rb.value>(m, dS[rb.value]); });
+            float* sp = chunk_dso + chn * GD * GD + jt;
+#pragma unroll
+            for (int rb = 0; rb < 8; ++rb) store_t16(sp + 16 * rb * GD, lane, dS[rb]);
         }
         __syncthreads();   // readers of the previous chunk's tiles are done
         load_chunk_rows<TIn>(p, start + c0, Lc, h, L.Q, L.K, nullptr);
@@ -421,45 +458,55 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
             }
             if (t < GC) L.G[t] = cw[kWsG + t];
         }
-        f32x16 dov;   // dO[token acc_row(r, half)][j], zero past the chunk
+        f32x4 dov[2];   // dO[token 16 tb + 4 (l >> 4) + v][j], zero past the chunk
         {
             const TIn* base = d_o + (int64_t)(start + c0) * do_st + (int64_t)h * do_sh + j;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int i = acc_row(r, half);
-                dov[r] = i < Lc ? (float)base[(int64_t)i * do_st] : 0.0f;
-            }
+            for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int i = 16 * tb + g4 + v;
+                    dov[tb][v] = i < Lc ? (float)base[(int64_t)i * do_st] : 0.0f;
+                }
         }
         __syncthreads();
 
         // dV' = A^T dO + k~ dS
-        f32x16 dv = {};
+        f32x4 dv[2];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) dv = mfma_f32(L.A[acc_row(r, half) * MS + col], dov[r], dv);
+        for (int tb = 0; tb < 2; ++tb) {
+            dv[tb] = (f32x4){};
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
+            for (int tb2 = 0; tb2 < 2; ++tb2)
 #pragma unroll
-            for (int r4 = 0; r4 < 16; r4 += 4) {
-                const f32x4 kv = *(const f32x4*)&L.K[col * RS + 32 * rb + 8 * (r4 >> 2) + 4 * half];
+                for (int v = 0; v < 4; ++v)
+                    dv[tb] = mfma16_f32(L.A[(16 * tb2 + g4 + v) * MS + 16 * tb + c16], dov[tb2][v], dv[tb]);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) dv = mfma_f32(kv[e], dS[rb][r4 + e], dv);
+            for (int rb = 0; rb < 8; ++rb) {
+                const f32x4 kv = *(const f32x4*)&L.K[(16 * tb + c16) * RS + 16 * rb + g4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) dv[tb] = mfma16_f32(kv[v], dS[rb][v], dv[tb]);
+                __builtin_amdgcn_sched_barrier(0);
             }
-            __builtin_amdgcn_sched_barrier(0);
         }
-        store_acc<0>(acc_mat(chunk_dvp + chn * GC * GD, GC, half, j), dv);
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) store_t16(chunk_dvp + chn * GC * GD + 16 * tb * GD + jt, lane, dv[tb]);
 
         // dS <- e^{G_L} dS + (e^G q^)^T dO - W^T dV'
         const float el = expf(L.G[GC - 1]);
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
+        for (int rb = 0; rb < 8; ++rb) {
             dS[rb] *= el;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int i = acc_row(r, half);
-                dS[rb] = mfma_f32(L.Q[i * RS + 32 * rb + col], dov[r], dS[rb]);
-                if constexpr (!TRUNC) dS[rb] = mfma_f32(-L.W[i * RS + 32 * rb + col], dv[r], dS[rb]);
+            for (int tb = 0; tb < 2; ++tb) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int ro = (16 * tb + g4 + v) * RS + 16 * rb + c16;
+                    dS[rb] = mfma16_f32(L.Q[ro], dov[tb][v], dS[rb]);
+                    if constexpr (!TRUNC) dS[rb] = mfma16_f32(-L.W[ro], dv[tb][v], dS[rb]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
-            __builtin_amdgcn_sched_barrier(0);
         }
     }
     if constexpr (TRUNC) {
@@ -473,19 +520,23 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
                 for (int e = 0; e < 16; e += 4)
                     *(f32x4*)&L.W[i * RS + d0 + e] = *(const f32x4*)(cw + kWsW + i * GD + d0 + e);
             }
-            const f32x16 dv = load_acc<0>(acc_mat(chunk_dvp + chn * GC * GD, GC, half, j));   // this lane's own writes
+            f32x4 dv[2];   // this lane's own writes
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) dv[tb] = load_t16(chunk_dvp + chn * GC * GD + 16 * tb * GD + jt, lane);
             __syncthreads();
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
+            for (int rb = 0; rb < 8; ++rb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    dS[rb] = mfma_f32(-L.W[acc_row(r, half) * RS + 32 * rb + col], dv[r], dS[rb]);
-            }
+                for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        dS[rb] = mfma16_f32(-L.W[(16 * tb + g4 + v) * RS + 16 * rb + c16], dv[tb][v], dS[rb]);
         }
     }
     // dS at the node's entry, summed into its parent by the next (shallower) level.
-    const AccMat m = acc_mat(node_dsin + ((size_t)node * p.hv + h) * GD * GD, GD, half, j);
-    for_tiles([&](auto rb) { store_acc<32 * rb.value>(m, dS[rb.value]); });
+    float* sp = node_dsin + ((size_t)node * p.hv + h) * GD * GD + jt;
+#pragma unroll
+    for (int rb = 0; rb < 8; ++rb) store_t16(sp + 16 * rb * GD, lane, dS[rb]);
 }
 
 // State products on fp32 MFMA. The contraction (value dimension, 128) runs in
@@ -1045,6 +1096,7 @@ size_t tt_gdn_ws_bytes_impl(int n_chunks, int n_heads_v, bool trunc) {
 namespace {
 constexpr int kMaxGridY = 65535;   // grid y limit: a level's nodes beyond it go to further launches
 
+
 template <typename TIn, bool TRUNC>
 void launch_prep(const GdnDev& d, float* prep, hipStream_t s) {
     hipLaunchKernelGGL((gdn_prep_kernel<TIn, TRUNC>), dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, prep);
@@ -1052,10 +1104,11 @@ void launch_prep(const GdnDev& d, float* prep, hipStream_t s) {
 template <typename TIn, bool TRUNC>
 void launch_scan(const GdnDev& d, int b, int n, float* prep, TIn* out, float* states, float* sin, float* vp,
                  hipStream_t s) {
-    // grid (v head, node): all heads of a level's first (longest) nodes are dispatched first
+    // grid (v head x column block, node): all heads of a level's first
+    // (longest) nodes are dispatched first
     for (int b0 = 0; b0 < n; b0 += kMaxGridY)
-        hipLaunchKernelGGL((gdn_scan_kernel<TIn, TRUNC>), dim3(d.hv, min(kMaxGridY, n - b0)), dim3(GT), 0, s, d,
-                           b + b0, prep, out, states, sin, vp);
+        hipLaunchKernelGGL((gdn_scan_cols_kernel<TIn, TRUNC>), dim3(d.hv * kScanSplit, min(kMaxGridY, n - b0)),
+                           dim3(GT), 0, s, d, b + b0, prep, out, states, sin, vp);
 }
 
 // The forward: chunk terms (prep; TRUNC: plus the node-level U, W), then one
@@ -1187,8 +1240,8 @@ static int gdn_bwd_run(const GdnDev& d, const int32_t* level_offsets, int n_leve
         const int b = level_offsets[l], n = level_offsets[l + 1] - b;
         if (n <= 0) continue;
         for (int b0 = 0; b0 < n; b0 += kMaxGridY)
-            hipLaunchKernelGGL((gdn_rscan_kernel<TIn, TRUNC>), dim3(d.hv, min(kMaxGridY, n - b0)), dim3(GT), 0, s, d,
-                               b + b0, w.prep, d_o, do_st, do_sh, w.dso, w.dvp, w.dsn);
+            hipLaunchKernelGGL((gdn_rscan_cols_kernel<TIn, TRUNC>), dim3(d.hv * kScanSplit, min(kMaxGridY, n - b0)),
+                               dim3(GT), 0, s, d, b + b0, w.prep, d_o, do_st, do_sh, w.dso, w.dvp, w.dsn);
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     hipLaunchKernelGGL(gdn_bwd_state_kernel<TIn>, dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, d_o, do_st, do_sh,

@@ -120,6 +120,30 @@ __device__ __forceinline__ f32x16 mfma_f32(float a, float b, const f32x16& c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
+// v_mfma_f32_16x16x4_f32: D[16x16] += A[16x4] B[4x16]; lane l supplies
+// A[l & 15][l >> 4] and B[l >> 4][l & 15], and accumulator element v of lane
+// l is D[4 (l >> 4) + v][l & 15]. Step v of a 16-deep contraction pairs
+// k = 4 (l >> 4) + v across the four lane groups, so a 16-row block held as
+// accumulators is directly the B operand, element v of each lane.
+__device__ __forceinline__ f32x4 mfma16_f32(float a, float b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// A 16 x 16 tile of a row-major fp32 matrix of GD-float rows in the layout
+// of mfma16_f32's accumulators: element v of lane l is row 4 (l >> 4) + v,
+// column l & 15, of the tile at `base`.
+__device__ __forceinline__ f32x4 load_t16(const float* base, int lane) {
+    const float* p = base + 4 * (lane >> 4) * GD + (lane & 15);
+    return (f32x4){p[0], p[GD], p[2 * GD], p[3 * GD]};
+}
+__device__ __forceinline__ void store_t16(float* base, int lane, const f32x4& x) {
+    float* p = base + 4 * (lane >> 4) * GD + (lane & 15);
+    p[0] = x[0];
+    p[GD] = x[1];
+    p[2 * GD] = x[2];
+    p[3 * GD] = x[3];
+}
+
 // Accumulator-layout access to a row-major fp32 matrix of GD-float rows:
 // element r of lane l is row ROW0 + acc_row(r, l >> 5), column `col`. One
 // buffer resource (scalar registers), four lane offsets (rows r % 4); the
