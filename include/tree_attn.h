@@ -323,6 +323,11 @@ typedef struct tt_gdn_problem {
     const int32_t* node_child_off;
     const int32_t* node_child;
     int32_t reference_truncated;  /* 0: exact delta rule; 1: the reference's I + R + R^2 per node */
+    /* The state every root starts from (the reference's initial_state,
+     * tree_dfs_ssm.py:84-90: all_states[0], read by every node whose parent
+     * is -1): device, [Hv, 128, 128] float32 contiguous, 16-byte aligned;
+     * NULL: zero. */
+    const float* initial_state;
 } tt_gdn_problem;
 
 /* Workspace of tt_gdn_tree_fwd: per (chunk, v head) the state-independent
@@ -344,15 +349,21 @@ int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* 
  * written: stride_head 128, else TT_E_UNSUPPORTED; stride_tok by the rules
  * of q and at most 2^30; e.g. the column blocks of one [T, 2 Hk 128 + Hv 128]
  * row buffer, the gradient of a conv output that a q/k/v split reads, so that
- * no concatenation follows), and dg, dbeta [T, Hv] contiguous float32. The
- * node states carry no incoming gradient. It
+ * no concatenation follows), and dg, dbeta [T, Hv] contiguous float32.
+ * d_node_states (NULL: none) is the incoming gradient of node_states ([n_nodes,
+ * Hv, 128, 128] float32; the reference's differentiable last_state,
+ * tree_dfs_ssm.py:155, is node n_nodes - 1); d_initial_state (NULL: not
+ * wanted) receives the gradient of p->initial_state ([Hv, 128, 128] float32,
+ * written whole; with a NULL initial_state, the gradient at the zero state).
+ * Both 16-byte aligned. It
  * recomputes the forward (keeping every chunk's initial state), runs one
  * reverse launch per tree level (deepest first) for the state gradient, then
  * two launches over all chunks. Workspace: tt_gdn_bwd_workspace_bytes (per
  * (chunk, v head) about 240 KiB; per (node, v head) 128 KiB). */
 size_t tt_gdn_bwd_workspace_bytes(const tt_gdn_problem* p);
 int tt_gdn_tree_bwd(const tt_gdn_problem* p, tt_tensor d_o, tt_tensor dq, tt_tensor dk, tt_tensor dv, float* dg,
-                    float* dbeta, void* ws, size_t ws_bytes, void* stream);
+                    float* dbeta, const float* d_node_states, float* d_initial_state, void* ws, size_t ws_bytes,
+                    void* stream);
 
 /* The same forward and backward without the backward's recompute of the
  * forward (what autograd keeps through the reference's torch function,
@@ -368,8 +379,8 @@ int tt_gdn_tree_fwd_save(const tt_gdn_problem* p, void* o, float* node_states, v
                          void* stream);
 size_t tt_gdn_bwd_saved_workspace_bytes(const tt_gdn_problem* p);
 int tt_gdn_tree_bwd_saved(const tt_gdn_problem* p, tt_tensor d_o, tt_tensor dq, tt_tensor dk, tt_tensor dv,
-                          float* dg, float* dbeta, const void* saved, size_t saved_bytes, void* ws, size_t ws_bytes,
-                          void* stream);
+                          float* dg, float* dbeta, const float* d_node_states, float* d_initial_state,
+                          const void* saved, size_t saved_bytes, void* ws, size_t ws_bytes, void* stream);
 
 /* ---- tree-correct short convolution --------------------------------------
  * Replaces _tree_correct_conv_varlen (tree_dfs_ssm.py:284-346; twin

@@ -26,9 +26,12 @@ equals the exact rule for nodes of at most 3 tokens (R^3 = 0) and deviates by
 the R^3 term otherwise.
 
 Pinned by (tests/test_oracle_gdn.py): transformers' recurrent and chunked
-gated-delta-rule routines (library), per-path equivalence of the tree
-outputs, chunk-size independence, the R^3 identity above, and
-torch.nn.functional.conv1d on every root-to-leaf path for the conv.
+gated-delta-rule routines (library; the recurrent one also from a given
+initial state), per-path equivalence of the tree outputs, chunk-size
+independence, the R^3 identity above, a tree cut below its root equalling its
+subtrees run from the root's final state, central finite differences for the
+torch restatements' gradients, and torch.nn.functional.conv1d on every
+root-to-leaf path for the conv.
 """
 from __future__ import annotations
 
@@ -112,7 +115,9 @@ def gdn_tree(q, k, v, g, beta, node_len, parent, mode="exact", chunk=64, l2=True
     q, k [T, Hk, Dk]; v [T, Hv, Dv]; g, beta [T, Hv]; nodes in DFS pre-order
     (parent[i] < i, -1 for roots). v head h reads q/k head h // (Hv // Hk)
     (the reference's repeat_interleave). q, k are l2-normalised when ``l2``
-    and q is scaled by Dk^-1/2 (R/tree_dfs_ssm.py:70-90).
+    and q is scaled by Dk^-1/2 (R/tree_dfs_ssm.py:70-90). ``initial_state``
+    [Hv, Dk, Dv]: the state every root starts from (zeros when None; the
+    reference's ``all_states[0]``, R/tree_dfs_ssm.py:84-90).
 
     Returns (o [T, Hv, Dv], final states [n_nodes, Hv, Dk, Dv]).
     """
@@ -205,10 +210,14 @@ def gdn_gates(a, b, A_log, dt_bias):
     return g, beta
 
 
-def gdn_tree_torch(q, k, v, g, beta, node_len, parent, l2=True, eps=1e-6):
+def gdn_tree_torch(q, k, v, g, beta, node_len, parent, l2=True, eps=1e-6, initial_state=None,
+                   return_states=False):
     """The exact tree gated delta rule (token recurrence, as ``gdn_tree``
     mode="exact") in torch, differentiable: the backward oracle (autograd on
-    float64). q, k [T, Hk, Dk]; v [T, Hv, Dv]; g, beta [T, Hv]. Returns o."""
+    float64). q, k [T, Hk, Dk]; v [T, Hv, Dv]; g, beta [T, Hv];
+    ``initial_state`` [Hv, Dk, Dv] (every root's state, zeros when None, as
+    R/tree_dfs_ssm.py:84-86). Returns o, and with ``return_states`` also the
+    node final states [n_nodes, Hv, Dk, Dv]."""
     import torch
     T, Hk, Dk = q.shape
     Hv, Dv = v.shape[1], v.shape[2]
@@ -223,24 +232,34 @@ def gdn_tree_torch(q, k, v, g, beta, node_len, parent, l2=True, eps=1e-6):
     finals = [None] * len(node_len)
     outs = []
     for i in range(len(node_len)):
-        S = finals[parent[i]] if parent[i] >= 0 else torch.zeros(Hv, Dk, Dv, dtype=q.dtype)
+        S = finals[parent[i]] if parent[i] >= 0 else _root_state(initial_state, Hv, Dk, Dv, q.dtype)
         for t in range(int(starts[i]), int(starts[i] + node_len[i])):
             S = S * torch.exp(g[t])[:, None, None]
             delta = (v[t] - torch.einsum("hk,hkv->hv", k[t], S)) * beta[t][:, None]
             S = S + k[t][:, :, None] * delta[:, None, :]
             outs.append(torch.einsum("hk,hkv->hv", q[t], S))
         finals[i] = S
-    return torch.stack(outs, 0)
+    out = torch.stack(outs, 0)
+    return (out, torch.stack(finals)) if return_states else out
 
 
-def gdn_tree_reference_torch(q, k, v, g, beta, node_len, parent, l2=True, eps=1e-6, return_states=False):
+def _root_state(initial_state, Hv, Dk, Dv, dtype):
+    import torch
+    if initial_state is None:
+        return torch.zeros(Hv, Dk, Dv, dtype=dtype)
+    return initial_state
+
+
+def gdn_tree_reference_torch(q, k, v, g, beta, node_len, parent, l2=True, eps=1e-6, return_states=False,
+                             initial_state=None):
     """The reference's own evaluation (``gdn_tree`` mode="reference": every
     whole node one chunk, within-node correction A = I + R + R^2 built from
     the uncorrected rows, R/tree_dfs_ssm.py:100-150) in torch, differentiable:
     the backward oracle of that mode (autograd on float64). Same arguments and
     result as ``gdn_tree_torch`` (plus the node final states [n_nodes, Hv, Dk,
-    Dv] with ``return_states``); in the inputs' dtype, so float32 inputs give
-    the precision the reference's own float32 code reaches."""
+    Dv] with ``return_states``; ``initial_state`` as there); in the inputs'
+    dtype, so float32 inputs give the precision the reference's own float32
+    code reaches."""
     import torch
     T, Hk, Dk = q.shape
     Hv, Dv = v.shape[1], v.shape[2]
@@ -259,7 +278,7 @@ def gdn_tree_reference_torch(q, k, v, g, beta, node_len, parent, l2=True, eps=1e
         s0, L = int(starts[i]), int(node_len[i])
         qi, ki, vi = q[:, s0:s0 + L], k[:, s0:s0 + L], v[:, s0:s0 + L]
         gi, bi = g[:, s0:s0 + L], beta[:, s0:s0 + L]
-        S = finals[parent[i]] if parent[i] >= 0 else torch.zeros(Hv, Dk, Dv, dtype=q.dtype)
+        S = finals[parent[i]] if parent[i] >= 0 else _root_state(initial_state, Hv, Dk, Dv, q.dtype)
         G = gi.cumsum(-1)
         lower = torch.tril(torch.ones(L, L, dtype=torch.bool))
         D = torch.where(lower, torch.exp(torch.where(lower, G[:, :, None] - G[:, None, :], 0.0)), 0.0)

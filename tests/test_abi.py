@@ -255,6 +255,7 @@ def _gdn_problem(offsets=(0, 1, 3), **kw):
     ("node_parent", None, _lib.TT_E_ARG),
     ("q", _lib.TTTensor(18, 16 * 128, 128), _lib.TT_E_ARG),   # misaligned
     ("reference_truncated", 2, _lib.TT_E_ARG),   # a flag: 0 or 1
+    ("initial_state", 20, _lib.TT_E_ARG),        # misaligned
 ])
 def test_gdn_validation(field, value, code):
     lib = _lib.lib()
@@ -306,13 +307,17 @@ def test_gdn_bwd_validation():
     want = (5 * 32 * per_chunk + 3 * 32 * 2 * 128 * 128) * 4
     assert lib.tt_gdn_bwd_workspace_bytes(ctypes.byref(p)) == want
     DQ = _lib.TTTensor(16, 16 * 128, 128)
-    args = lambda ws_bytes, dq=DQ, dk=DQ, dv=DO: (dq, dk, dv, V, V, V, ws_bytes, None)
+    args = lambda ws_bytes, dq=DQ, dk=DQ, dv=DO, ds=None, di=None: (dq, dk, dv, V, V, ds, di, V, ws_bytes, None)
     assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, *args(want - 4)) == _lib.TT_E_WORKSPACE
     assert lib.tt_gdn_tree_bwd(ctypes.byref(_gdn_problem()), DO, *args(want)) == _lib.TT_E_ARG   # no children CSR
     assert lib.tt_gdn_tree_bwd(ctypes.byref(p), _lib.TTTensor(18, 32 * 128, 128), *args(want)) == _lib.TT_E_ARG
     assert lib.tt_gdn_tree_bwd(ctypes.byref(p), _lib.TTTensor(16, 64, 128), *args(want)) == _lib.TT_E_ARG
-    assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, DQ, DQ, DO, ctypes.c_void_p(18), V, V, want,
+    assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, DQ, DQ, DO, ctypes.c_void_p(18), V, None, None, V, want,
                                None) == _lib.TT_E_ARG
+    # the node-state gradient in and the initial-state gradient out: optional, 16-byte aligned
+    assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, *args(want - 4, ds=V, di=V)) == _lib.TT_E_WORKSPACE
+    assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, *args(want, ds=ctypes.c_void_p(20))) == _lib.TT_E_ARG
+    assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, *args(want, di=ctypes.c_void_p(24))) == _lib.TT_E_ARG
     # dq/dk/dv: the row rules of q (a null, misaligned or short-strided output is refused) ...
     for bad in (_lib.TTTensor(None, 16 * 128, 128), _lib.TTTensor(24, 16 * 128, 128), _lib.TTTensor(16, 64, 128),
                 _lib.TTTensor(16, 16 * 128, 100)):
@@ -354,14 +359,16 @@ def test_gdn_saved_validation():
     assert lib.tt_gdn_tree_fwd_save(ctypes.byref(p), V, V, None, saved, None) == _lib.TT_E_ARG
     assert lib.tt_gdn_tree_fwd_save(ctypes.byref(p), V, V, ctypes.c_void_p(20), saved, None) == _lib.TT_E_ARG
     DQ = _lib.TTTensor(16, 16 * 128, 128)
-    args = lambda sv, sb, wb: (DQ, DQ, DO, V, V, sv, sb, V, wb, None)
+    args = lambda sv, sb, wb: (DQ, DQ, DO, V, V, None, None, sv, sb, V, wb, None)
     assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), DO, *args(V, saved - 4, scratch)) == _lib.TT_E_WORKSPACE
     assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), DO, *args(V, saved, scratch - 4)) == _lib.TT_E_WORKSPACE
     assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), DO, *args(None, saved, scratch)) == _lib.TT_E_ARG
     assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(_gdn_problem()), DO, *args(V, saved, scratch)) == _lib.TT_E_ARG
     assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), _lib.TTTensor(18, 32 * 128, 128),
                                      *args(V, saved, scratch)) == _lib.TT_E_ARG
-    assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), DO, _lib.TTTensor(16, 64, 128), DQ, DO, V, V, V, saved, V,
+    assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), DO, _lib.TTTensor(16, 64, 128), DQ, DO, V, V, None, None, V,
+                                     saved, V, scratch, None) == _lib.TT_E_ARG
+    assert lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), DO, DQ, DQ, DO, V, V, ctypes.c_void_p(20), None, V, saved, V,
                                      scratch, None) == _lib.TT_E_ARG
 
 

@@ -241,3 +241,68 @@ def test_reference_truncated_is_opt_in():
                      (gdn_layer._patch_ssm, "reference_truncated"),
                      (__import__("tree_training_amd").dfs_tree_forward, "gdn_reference_truncated")]:
         assert inspect.signature(fn).parameters[name].default is False, fn.__name__
+
+
+def test_initial_state_matches_transformers():
+    """A root continued from a given state: the output and the final state
+    equal transformers' recurrence started from that state."""
+    q, k, v, g, beta = _inputs(29, 2, 2, 16, 12, 7)
+    s0 = np.random.default_rng(8).standard_normal((2, 16, 12))
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x))[None]
+    o_hf, s_hf = hf.torch_recurrent_gated_delta_rule(t(q), t(k), t(v), t(g), t(beta), t(s0), True,
+                                                     use_qk_l2norm_in_kernel=True)
+    o, fin = gdn.gdn_tree(q, k, v, g, beta, [29], [-1], mode="exact", initial_state=s0)
+    assert _rel(o, o_hf[0].numpy()) < 1e-5
+    assert _rel(fin[0], s_hf[0].numpy()) < 1e-5
+    o_zero, _ = gdn.gdn_tree(q, k, v, g, beta, [29], [-1], mode="exact")
+    assert _rel(o, o_zero) > 1e-2                   # the state is used
+
+
+@pytest.mark.parametrize("mode", ["exact", "reference", "chunked"])
+def test_initial_state_continues_a_cut_tree(mode):
+    """A tree cut below its root: the subtrees under it, run as a forest of
+    their own from the root's final state, give the whole tree's outputs and
+    node states."""
+    lens, par = [5, 3, 4, 2, 6], [-1, 0, 1, 0, 3]
+    q, k, v, g, beta = _inputs(sum(lens), 1, 2, 6, 5, 9, g_scale=0.5)
+    o, fin = gdn.gdn_tree(q, k, v, g, beta, lens, par, mode=mode, chunk=4)
+    r = lens[0]
+    o0, f0 = gdn.gdn_tree(q[:r], k[:r], v[:r], g[:r], beta[:r], lens[:1], [-1], mode=mode, chunk=4)
+    o1, f1 = gdn.gdn_tree(q[r:], k[r:], v[r:], g[r:], beta[r:], lens[1:], [-1, 0, -1, 2], mode=mode, chunk=4,
+                          initial_state=f0[0])
+    assert _rel(np.concatenate([o0, o1]), o) < 1e-13
+    assert _rel(np.concatenate([f0, f1]), fin) < 1e-13
+
+
+@pytest.mark.parametrize("mode", ["exact", "reference"])
+def test_torch_oracles_initial_state_and_state_gradients(mode):
+    """The differentiable restatements with an initial state and a loss on
+    the node states: forward equal to the numpy oracle, and the gradients of
+    every input, the initial state included, equal to central finite
+    differences of the numpy forward."""
+    fn = gdn.gdn_tree_torch if mode == "exact" else gdn.gdn_tree_reference_torch
+    lens, par = [4, 3, 5], [-1, 0, -1]
+    q, k, v, g, beta = _inputs(sum(lens), 1, 2, 6, 5, 31, g_scale=0.5)
+    rng = np.random.default_rng(32)
+    s0 = rng.standard_normal((2, 6, 5))
+    xs = (q, k, v, g, beta, s0)
+    tt = [torch.from_numpy(x).requires_grad_(True) for x in xs]
+    o, st = fn(*tt[:5], lens, par, initial_state=tt[5], return_states=True)
+    o_np, st_np = gdn.gdn_tree(q, k, v, g, beta, lens, par, mode=mode, initial_state=s0)
+    assert _rel(o.detach().numpy(), o_np) < 1e-12
+    assert _rel(st.detach().numpy(), st_np) < 1e-12
+    wo, ws = rng.standard_normal(o.shape), rng.standard_normal(st.shape)
+    grads = torch.autograd.grad((o * torch.from_numpy(wo)).sum() + (st * torch.from_numpy(ws)).sum(), tt)
+
+    def f(args):
+        oo, ss = gdn.gdn_tree(*args[:5], lens, par, mode=mode, initial_state=args[5])
+        return (oo * wo).sum() + (ss * ws).sum()
+
+    for x, gr in zip(xs, grads):
+        for _ in range(3):
+            idx = tuple(int(rng.integers(0, s)) for s in x.shape)
+            xp, xm = x.copy(), x.copy()
+            xp[idx] += 1e-6
+            xm[idx] -= 1e-6
+            fd = (f([xp if a is x else a for a in xs]) - f([xm if a is x else a for a in xs])) / 2e-6
+            assert abs(fd - float(gr[idx])) < 1e-6 * max(1.0, abs(fd))

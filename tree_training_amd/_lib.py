@@ -29,7 +29,7 @@ TT_STATUS_BAD_PARENT = 2
 TT_STATUS_BAD_TOTAL = 4
 TT_STATUS_BAD_BIAS = 8
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # Every symbol include/tree_attn.h declares, for the export check.
 EXPORTS = (
@@ -81,7 +81,7 @@ class TTGdnProblem(ctypes.Structure):
         ("n_levels", ctypes.c_int32), ("n_chunks", ctypes.c_int32),
         ("node_chunk0", ctypes.c_void_p), ("chunk_node", ctypes.c_void_p),
         ("node_child_off", ctypes.c_void_p), ("node_child", ctypes.c_void_p),
-        ("reference_truncated", ctypes.c_int32),
+        ("reference_truncated", ctypes.c_int32), ("initial_state", ctypes.c_void_p),
     ]
 
 
@@ -132,12 +132,12 @@ def _declare(lib):
         "tt_gdn_tree_fwd": (ctypes.c_int, [ctypes.POINTER(TTGdnProblem), P, P, P, SZ, VP]),
         "tt_gdn_bwd_workspace_bytes": (SZ, [ctypes.POINTER(TTGdnProblem)]),
         "tt_gdn_tree_bwd": (ctypes.c_int, [ctypes.POINTER(TTGdnProblem), TTTensor, TTTensor, TTTensor, TTTensor, P,
-                                           P, P, SZ, VP]),
+                                           P, P, P, P, SZ, VP]),
         "tt_gdn_saved_bytes": (SZ, [ctypes.POINTER(TTGdnProblem)]),
         "tt_gdn_tree_fwd_save": (ctypes.c_int, [ctypes.POINTER(TTGdnProblem), P, P, P, SZ, VP]),
         "tt_gdn_bwd_saved_workspace_bytes": (SZ, [ctypes.POINTER(TTGdnProblem)]),
         "tt_gdn_tree_bwd_saved": (ctypes.c_int, [ctypes.POINTER(TTGdnProblem), TTTensor, TTTensor, TTTensor, TTTensor,
-                                                 P, P, P, SZ, P, SZ, VP]),
+                                                 P, P, P, P, P, SZ, P, SZ, VP]),
         "tt_tree_conv_fwd": (ctypes.c_int, [ctypes.POINTER(TTConvProblem), P, ctypes.c_int64, VP]),
         "tt_qk_prologue_fwd": (ctypes.c_int, [ctypes.POINTER(TTPrologueProblem), P, P, VP]),
         "tt_ce_rows": (ctypes.c_int, [I32, P, ctypes.c_int64, I32, I32, P, P, I32, P, P, ctypes.c_int64, VP]),

@@ -6,7 +6,7 @@
 
 namespace {
 
-constexpr int kAbiVersion = 5;
+constexpr int kAbiVersion = 6;
 constexpr int64_t kMaxTokStride = int64_t(1) << 23;   // elements (bf16; half that for fp32)
 inline int64_t max_tok_stride(int dtype) { return dtype == TT_DTYPE_BF16 ? kMaxTokStride : kMaxTokStride / 2; }
 
@@ -322,6 +322,10 @@ static int gdn_problem(const tt_gdn_problem* p, GdnDev& d) {
     if (p->reference_truncated != 0 && p->reference_truncated != 1) return TT_E_ARG;
     d.trunc = p->reference_truncated;
     d.scale = p->scale;
+    if (p->initial_state && !aligned(p->initial_state, 16)) return TT_E_ARG;
+    d.init = p->initial_state;
+    d.d_states = nullptr;
+    d.d_init = nullptr;
     return TT_OK;
 }
 
@@ -374,7 +378,8 @@ static bool gdn_rows_ok(const tt_tensor& t, int64_t gran) {
 }
 
 static int gdn_bwd_args(const tt_gdn_problem* p, GdnDev& d, const tt_tensor& d_o, const tt_tensor& dq,
-                        const tt_tensor& dk, const tt_tensor& dv, float* dg, float* dbeta, void* ws) {
+                        const tt_tensor& dk, const tt_tensor& dv, float* dg, float* dbeta,
+                        const float* d_node_states, float* d_initial_state, void* ws) {
     if (!p->node_child_off || !p->node_child) return TT_E_ARG;
     if (!dg || !dbeta || !ws) return TT_E_ARG;
     const int64_t gran = p->dtype == TT_DTYPE_BF16 ? 8 : 4;
@@ -387,30 +392,37 @@ static int gdn_bwd_args(const tt_gdn_problem* p, GdnDev& d, const tt_tensor& d_o
         if (t->stride_tok > (int64_t(1) << 30)) return TT_E_ARG;
     }
     if (!aligned(ws, 16) || !aligned(dg, 4) || !aligned(dbeta, 4)) return TT_E_ARG;
+    if ((d_node_states && !aligned(d_node_states, 16)) || (d_initial_state && !aligned(d_initial_state, 16)))
+        return TT_E_ARG;
     d.dq_st = (int)dq.stride_tok;
     d.dk_st = (int)dk.stride_tok;
     d.dv_st = (int)dv.stride_tok;
+    d.d_states = d_node_states;
+    d.d_init = d_initial_state;
     return TT_OK;
 }
 
 int tt_gdn_tree_bwd(const tt_gdn_problem* p, tt_tensor d_o, tt_tensor dq, tt_tensor dk, tt_tensor dv, float* dg,
-                    float* dbeta, void* ws, size_t ws_bytes, void* stream) {
+                    float* dbeta, const float* d_node_states, float* d_initial_state, void* ws, size_t ws_bytes,
+                    void* stream) {
     GdnDev d;
     int rc = gdn_problem(p, d);
     if (rc != TT_OK) return rc;
-    if ((rc = gdn_bwd_args(p, d, d_o, dq, dk, dv, dg, dbeta, ws)) != TT_OK) return rc;
+    if ((rc = gdn_bwd_args(p, d, d_o, dq, dk, dv, dg, dbeta, d_node_states, d_initial_state, ws)) != TT_OK)
+        return rc;
     if (ws_bytes < tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v, true, p->reference_truncated != 0)) return TT_E_WORKSPACE;
     return tt_gdn_bwd_launch(d, p->level_offsets, p->n_levels, d_o.ptr, d_o.stride_tok, d_o.stride_head,
                              const_cast<void*>(dq.ptr), const_cast<void*>(dk.ptr), const_cast<void*>(dv.ptr), dg, dbeta, nullptr, (float*)ws, (hipStream_t)stream);
 }
 
 int tt_gdn_tree_bwd_saved(const tt_gdn_problem* p, tt_tensor d_o, tt_tensor dq, tt_tensor dk, tt_tensor dv,
-                          float* dg, float* dbeta, const void* saved, size_t saved_bytes, void* ws, size_t ws_bytes,
-                          void* stream) {
+                          float* dg, float* dbeta, const float* d_node_states, float* d_initial_state,
+                          const void* saved, size_t saved_bytes, void* ws, size_t ws_bytes, void* stream) {
     GdnDev d;
     int rc = gdn_problem(p, d);
     if (rc != TT_OK) return rc;
-    if ((rc = gdn_bwd_args(p, d, d_o, dq, dk, dv, dg, dbeta, ws)) != TT_OK) return rc;
+    if ((rc = gdn_bwd_args(p, d, d_o, dq, dk, dv, dg, dbeta, d_node_states, d_initial_state, ws)) != TT_OK)
+        return rc;
     if (!saved || !aligned(saved, 16)) return TT_E_ARG;
     if (saved_bytes < tt_gdn_saved_bytes_impl(p->n_chunks, p->n_heads_v, p->reference_truncated != 0)) return TT_E_WORKSPACE;
     if (ws_bytes < tt_gdn_bwd_ws_bytes_impl(p->n_chunks, p->n_nodes, p->n_heads_v, false, p->reference_truncated != 0)) return TT_E_WORKSPACE;

@@ -2,8 +2,8 @@
 // over a DFS-packed tree: forward for gfx950.
 //
 // Semantics: the gated delta rule token by token along every root-to-leaf
-// path — each node continues from its parent's final state (zero state for a
-// root) — evaluated exactly in TT_GDN_CHUNK = 32-token chunks (a node is cut
+// path — each node continues from its parent's final state (a root from the
+// caller's initial state, or zero) — evaluated exactly in TT_GDN_CHUNK = 32-token chunks (a node is cut
 // into consecutive chunks; its last chunk may be short):
 //   G = cumsum(g), D[i][j] = exp(G_i - G_j) (j <= i),
 //   N = -strictly_lower(beta k k^T * D),  T = (I - N)^-1,
@@ -224,19 +224,21 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     if (chunk0 < 0 || chunk0 > p.n_chunks - tt_cdiv(len, GC)) return;
     if (par >= node || par < -1) par = -1;                               // parents precede children
 
+    // S0: the parent's final state; a root's is the initial state (or zero).
+    const float* s0 = par >= 0 ? states + ((size_t)par * p.hv + h) * GD * GD
+                               : (p.init ? p.init + (size_t)h * GD * GD : nullptr);
     f32x4 S[8];
-    if (par >= 0) {
-        const float* sp = states + ((size_t)par * p.hv + h) * GD * GD + jt;
+    if (s0) {
 #pragma unroll
-        for (int rb = 0; rb < 8; ++rb) S[rb] = load_t16(sp + 16 * rb * GD, lane);
+        for (int rb = 0; rb < 8; ++rb) S[rb] = load_t16(s0 + jt + 16 * rb * GD, lane);
     } else {
 #pragma unroll
         for (int rb = 0; rb < 8; ++rb) S[rb] = (f32x4){};
     }
 
     if constexpr (TRUNC) {
-        // V' = U - W S0 for every chunk (a root's S0 is zero: V' = U as it is).
-        for (int c0 = 0; par >= 0 && c0 < len; c0 += GC) {
+        // V' = U - W S0 for every chunk (with S0 zero: V' = U as it is).
+        for (int c0 = 0; s0 && c0 < len; c0 += GC) {
             float* cw = ws + ((size_t)(chunk0 + c0 / GC) * p.hv + h) * kWsChunk;
             __syncthreads();   // readers of the previous chunk's W are done
             {
@@ -371,9 +373,11 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 //    gradient of the state after a chunk, per (node, v head), on fp32 MFMA:
 //      dV' = A^T dO + (e^{G_L - G} k^) dS,
 //      dS <- e^{G_L} dS + (e^G q^)^T dO - W^T dV'.
-//    A node's last chunk starts from the sum of its children's dS at entry
-//    (zero for a leaf, whose final state is not an output that carries a
-//    gradient).
+//    A node's last chunk starts from the incoming gradient of its final
+//    state (if the caller gives one) plus the sum of its children's dS at
+//    entry.
+//  * gdn_init_grad_kernel — when the initial state's gradient is wanted: the
+//    sum of the roots' dS at entry.
 //  * gdn_bwd_state_kernel — per (chunk, v head), the products with the
 //    128 x 128 states: X = dO S^T, dW = -dV' S^T, dK~ = V' dS^T, <S, dS>.
 //  * gdn_bwd_chunk_kernel — per (chunk, q/k head, looping over its v heads),
@@ -414,10 +418,17 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     if (start < 0 || len < 1 || start > p.n_tokens - len) return;        // malformed node: skipped
     if (chunk0 < 0 || chunk0 > p.n_chunks - tt_cdiv(len, GC)) return;
 
-    // dS after the node: the sum over its children of their dS at entry.
+    // dS after the node: its state's incoming gradient, if any, plus the sum
+    // over its children of their dS at entry.
     f32x4 dS[8];
+    if (p.d_states) {
+        const float* sp = p.d_states + ((size_t)node * p.hv + h) * GD * GD + jt;
 #pragma unroll
-    for (int rb = 0; rb < 8; ++rb) dS[rb] = (f32x4){};
+        for (int rb = 0; rb < 8; ++rb) dS[rb] = load_t16(sp + 16 * rb * GD, lane);
+    } else {
+#pragma unroll
+        for (int rb = 0; rb < 8; ++rb) dS[rb] = (f32x4){};
+    }
     {
         const int c_lo = max(p.child_off[node], 0), c_hi = min(p.child_off[node + 1], p.n_nodes);
         for (int ci = c_lo; ci < c_hi; ++ci) {
@@ -537,6 +548,21 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     float* sp = node_dsin + ((size_t)node * p.hv + h) * GD * GD + jt;
 #pragma unroll
     for (int rb = 0; rb < 8; ++rb) store_t16(sp + 16 * rb * GD, lane, dS[rb]);
+}
+
+// Gradient of the initial state: the sum over the roots, in node order (the
+// order in which a node's children's terms are summed), of their state
+// gradient at entry. Thread: four consecutive floats of one v head's
+// 128 x 128 block.
+__global__ __launch_bounds__(GT) void gdn_init_grad_kernel(GdnDev p, const float* __restrict__ node_dsin) {
+    const int h = blockIdx.y;
+    const int e = 4 * (blockIdx.x * GT + threadIdx.x);
+    f32x4 acc = {};
+    for (int node = 0; node < p.n_nodes; ++node) {
+        if (p.parent[node] >= 0) continue;   // roots only
+        acc += *(const f32x4*)(node_dsin + ((size_t)node * p.hv + h) * GD * GD + e);
+    }
+    *(f32x4*)(p.d_init + (size_t)h * GD * GD + e) = acc;
 }
 
 // State products on fp32 MFMA. The contraction (value dimension, 128) runs in
@@ -1242,6 +1268,11 @@ static int gdn_bwd_run(const GdnDev& d, const int32_t* level_offsets, int n_leve
         for (int b0 = 0; b0 < n; b0 += kMaxGridY)
             hipLaunchKernelGGL((gdn_rscan_cols_kernel<TIn, TRUNC>), dim3(d.hv * kScanSplit, min(kMaxGridY, n - b0)),
                                dim3(GT), 0, s, d, b + b0, w.prep, d_o, do_st, do_sh, w.dso, w.dvp, w.dsn);
+        if (hipGetLastError() != hipSuccess) return TT_E_HIP;
+    }
+    if (d.d_init) {
+        static_assert(GD * GD % (4 * GT) == 0, "one f32x4 per thread");
+        hipLaunchKernelGGL(gdn_init_grad_kernel, dim3(GD * GD / (4 * GT), d.hv), dim3(GT), 0, s, d, w.dsn);
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     hipLaunchKernelGGL(gdn_bwd_state_kernel<TIn>, dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, d_o, do_st, do_sh,

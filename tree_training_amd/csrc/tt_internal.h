@@ -81,6 +81,13 @@ struct GdnDev {
     // arguments). 32-bit, as every scalar register kept live through the
     // backward chunk kernel's loop costs it schedule quality.
     int dq_st, dk_st, dv_st;
+    // The state every root starts from ([Hv, 128, 128] float32; null: zero),
+    // the incoming gradient of the node states ([n_nodes, Hv, 128, 128];
+    // null: none) and where the backward writes the gradient of the initial
+    // state ([Hv, 128, 128]; null: not wanted).
+    const float* init;
+    const float* d_states;
+    float* d_init;
 };
 
 // Device-side view of a tt_conv_problem.

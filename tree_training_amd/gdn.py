@@ -141,7 +141,16 @@ def _tok_vec(x: torch.Tensor, name: str) -> torch.Tensor:
     return x
 
 
-def _problem(q, k, v, g, beta, tree: GdnTree, scale, l2norm, reference_truncated=False):
+def _f32_block(x: Optional[torch.Tensor], shape: Tuple[int, ...], name: str) -> Optional[torch.Tensor]:
+    """x (None passes through) as a contiguous float32 tensor of ``shape``."""
+    if x is None:
+        return None
+    if tuple(x.shape) != shape:
+        raise ValueError(f"{name}: expected {shape}, got {tuple(x.shape)}")
+    return x.float().contiguous()
+
+
+def _problem(q, k, v, g, beta, tree: GdnTree, scale, l2norm, reference_truncated=False, initial_state=None):
     q, k, v = _tok_heads(q, "q"), _tok_heads(k, "k"), _tok_heads(v, "v")
     g, beta = _tok_vec(g, "g"), _tok_vec(beta, "beta")
     T, Hk, _ = q.shape
@@ -152,6 +161,11 @@ def _problem(q, k, v, g, beta, tree: GdnTree, scale, l2norm, reference_truncated
         raise ValueError(f"{T} tokens but the tree holds {tree.n_tokens}")
     if v.dtype not in (torch.bfloat16, torch.float32) or q.dtype != v.dtype or k.dtype != v.dtype:
         raise ValueError("q, k, v must share dtype bfloat16 or float32")
+    if initial_state is not None and initial_state.dim() == 4 and initial_state.shape[0] == 1:
+        initial_state = initial_state[0]          # the reference's [B = 1, Hv, 128, 128]
+    s0 = _f32_block(initial_state, (Hv, HEAD_DIM, HEAD_DIM), "initial_state")
+    if s0 is not None and s0.device != v.device:
+        raise ValueError("initial_state must be on the device of q, k, v")
     p = _lib.TTGdnProblem(
         dtype=_lib.TT_DTYPE_BF16 if v.dtype == torch.bfloat16 else _lib.TT_DTYPE_F32,
         n_tokens=T, n_nodes=tree.n_nodes, n_heads_k=Hk, n_heads_v=Hv, head_dim=HEAD_DIM,
@@ -164,8 +178,9 @@ def _problem(q, k, v, g, beta, tree: GdnTree, scale, l2norm, reference_truncated
         level_nodes=_ptr(tree.d_levels), level_offsets=tree.level_offsets, n_levels=tree.n_levels,
         n_chunks=tree.n_chunks, node_chunk0=_ptr(tree.d_chunk0), chunk_node=_ptr(tree.d_chunk_node),
         node_child_off=_ptr(tree.d_child_off), node_child=_ptr(tree.d_child),
-        reference_truncated=1 if reference_truncated else 0)
-    return p, (q, k, v, g, beta)
+        reference_truncated=1 if reference_truncated else 0,
+        initial_state=s0.data_ptr() if s0 is not None else None)
+    return p, (q, k, v, g, beta, s0)
 
 
 # Whether the autograd Function keeps the forward's per-chunk terms and states
@@ -175,8 +190,10 @@ def _problem(q, k, v, g, beta, tree: GdnTree, scale, l2norm, reference_truncated
 KEEP_FORWARD_STATES = True
 
 
-def _gdn_forward(q, k, v, g, beta, tree: GdnTree, scale, l2norm, keep: bool, reference_truncated=False):
-    p, (q, k, v, g, beta) = _problem(q, k, v, g, beta, tree, scale, l2norm, reference_truncated)
+def _gdn_forward(q, k, v, g, beta, tree: GdnTree, scale, l2norm, keep: bool, reference_truncated=False,
+                 initial_state=None):
+    p, (q, k, v, g, beta, _s0) = _problem(q, k, v, g, beta, tree, scale, l2norm, reference_truncated,
+                                          initial_state)
     T, Hv = v.shape[0], v.shape[1]
     dev = require_device(q.device)
     o = torch.empty((T, Hv, HEAD_DIM), dtype=v.dtype, device=dev)
@@ -197,10 +214,11 @@ def _gdn_forward(q, k, v, g, beta, tree: GdnTree, scale, l2norm, keep: bool, ref
 
 def gdn_tree_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
                      tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True,
-                     reference_truncated: bool = False):
+                     reference_truncated: bool = False, initial_state: Optional[torch.Tensor] = None):
     """o [T, Hv, 128] (dtype of v) and node_states [n_nodes, Hv, 128, 128]
-    (float32; the state after each node)."""
-    o, states, _ = _gdn_forward(q, k, v, g, beta, tree, scale, l2norm, False, reference_truncated)
+    (float32; the state after each node). ``initial_state`` [Hv, 128, 128]:
+    the state every root starts from (zero when None)."""
+    o, states, _ = _gdn_forward(q, k, v, g, beta, tree, scale, l2norm, False, reference_truncated, initial_state)
     return o, states
 
 
@@ -225,15 +243,22 @@ def _tt(t: torch.Tensor):
 
 def gdn_tree_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
                       d_o: torch.Tensor, tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True,
-                      saved: Optional[torch.Tensor] = None, reference_truncated: bool = False):
-    """Gradients of sum(o * d_o) for ``gdn_tree_forward``'s o: dq, dk [T, Hk,
-    128] and dv [T, Hv, 128] in the dtype of v, dg and dbeta [T, Hv] float32.
+                      saved: Optional[torch.Tensor] = None, reference_truncated: bool = False,
+                      initial_state: Optional[torch.Tensor] = None, d_states: Optional[torch.Tensor] = None,
+                      initial_state_grad: bool = False):
+    """Gradients of sum(o * d_o) + sum(node_states * d_states) for
+    ``gdn_tree_forward``'s outputs: dq, dk [T, Hk, 128] and dv [T, Hv, 128]
+    in the dtype of v, dg and dbeta [T, Hv] float32, and with
+    ``initial_state_grad`` also that of the initial state [Hv, 128, 128]
+    (float32). ``d_states`` [n_nodes, Hv, 128, 128] may be None (no gradient
+    reaches the node states).
     When q, k, v are the column blocks of one packed row buffer (the q/k/v
     split of a conv output), dq, dk, dv are the same column blocks of one new
     buffer, so the split's backward needs no concatenation. Recomputes the
     forward internally (tt_gdn_tree_bwd) unless ``saved`` holds what
     tt_gdn_tree_fwd_save kept for the same inputs (tt_gdn_tree_bwd_saved)."""
-    p, (q, k, v, g, beta) = _problem(q, k, v, g, beta, tree, scale, l2norm, reference_truncated)
+    p, (q, k, v, g, beta, _s0) = _problem(q, k, v, g, beta, tree, scale, l2norm, reference_truncated,
+                                          initial_state)
     d_o = _tok_heads(d_o, "d_o").to(v.dtype)
     T, Hk, Hv = q.shape[0], q.shape[1], v.shape[1]
     if d_o.shape != v.shape:
@@ -252,73 +277,89 @@ def gdn_tree_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torc
         dv = torch.empty((T, Hv, HEAD_DIM), dtype=v.dtype, device=dev)
     dg = torch.empty((T, Hv), dtype=torch.float32, device=dev)
     dbeta = torch.empty_like(dg)
+    ds = _f32_block(d_states, (tree.n_nodes, Hv, HEAD_DIM, HEAD_DIM), "d_states")
+    if ds is not None and ds.device != dev:
+        raise ValueError("d_states must be on the device of q, k, v")
+    d_init = torch.empty((Hv, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=dev) if initial_state_grad else None
     lib = _lib.lib()
-    outs = (_tt(d_o), _tt(dq), _tt(dk), _tt(dv), _ptr(dg), _ptr(dbeta))
+    outs = (_tt(d_o), _tt(dq), _tt(dk), _tt(dv), _ptr(dg), _ptr(dbeta), _ptr(ds), _ptr(d_init))
     if saved is not None:
         ws_bytes = lib.tt_gdn_bwd_saved_workspace_bytes(ctypes.byref(p))
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         _lib.check(lib.tt_gdn_tree_bwd_saved(ctypes.byref(p), *outs, _ptr(saved), saved.numel(), _ptr(ws), ws_bytes,
                                              _stream(dev)), "tt_gdn_tree_bwd_saved")
-        return dq, dk, dv, dg, dbeta
-    ws_bytes = lib.tt_gdn_bwd_workspace_bytes(ctypes.byref(p))
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    _lib.check(lib.tt_gdn_tree_bwd(ctypes.byref(p), *outs, _ptr(ws), ws_bytes, _stream(dev)), "tt_gdn_tree_bwd")
-    return dq, dk, dv, dg, dbeta
+    else:
+        ws_bytes = lib.tt_gdn_bwd_workspace_bytes(ctypes.byref(p))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        _lib.check(lib.tt_gdn_tree_bwd(ctypes.byref(p), *outs, _ptr(ws), ws_bytes, _stream(dev)), "tt_gdn_tree_bwd")
+    return (dq, dk, dv, dg, dbeta, d_init) if initial_state_grad else (dq, dk, dv, dg, dbeta)
 
 
 class GdnTreeFunction(torch.autograd.Function):
     """Differentiable tree GDN: forward ``tt_gdn_tree_fwd_save`` (or
     ``tt_gdn_tree_fwd``), backward ``tt_gdn_tree_bwd_saved`` (or the
-    recomputing ``tt_gdn_tree_bwd``), as ``KEEP_FORWARD_STATES`` says. The
-    node states are returned without a gradient."""
+    recomputing ``tt_gdn_tree_bwd``), as ``KEEP_FORWARD_STATES`` says. Both
+    outputs (o and the node states) carry gradients, and so does the
+    optional initial state."""
 
     @staticmethod
-    def forward(ctx, q, k, v, g, beta, tree, scale, l2norm, reference_truncated):
+    def forward(ctx, q, k, v, g, beta, initial_state, tree, scale, l2norm, reference_truncated):
         keep = bool(KEEP_FORWARD_STATES)
-        o, states, saved = _gdn_forward(q, k, v, g, beta, tree, scale, l2norm, keep, reference_truncated)
+        o, states, saved = _gdn_forward(q, k, v, g, beta, tree, scale, l2norm, keep, reference_truncated,
+                                        initial_state)
         # The kept forward terms go through save_for_backward as well: autograd
         # then frees them with the graph (after a backward without retain_graph,
         # or when the graph is dropped), and every backward of a graph run
         # with retain_graph (the reference's per-leaf schedule) reuses them.
-        ctx.save_for_backward(q, k, v, g, beta, *(() if saved is None else (saved,)))
+        ctx.save_for_backward(q, k, v, g, beta, initial_state, *(() if saved is None else (saved,)))
         ctx.tree, ctx.scale, ctx.l2norm, ctx.trunc = tree, scale, l2norm, reference_truncated
-        ctx.mark_non_differentiable(states)
-        # No zero-filled gradient is made for the states (or for an unused o).
+        # No zero-filled gradient is made for an output the loss does not use.
         ctx.set_materialize_grads(False)
         return o, states
 
     @staticmethod
-    def backward(ctx, d_o, _d_states):
+    def backward(ctx, d_o, d_states):
+        if d_o is None and d_states is None:
+            return (None,) * 10
+        q, k, v, g, beta, s0, *kept = ctx.saved_tensors
         if d_o is None:
-            return (None,) * 9
-        q, k, v, g, beta, *kept = ctx.saved_tensors
-        dq, dk, dv, dg, dbeta = gdn_tree_backward(q, k, v, g, beta, d_o, ctx.tree, ctx.scale, ctx.l2norm,
-                                                  saved=kept[0] if kept else None, reference_truncated=ctx.trunc)
+            d_o = torch.zeros(v.shape, dtype=v.dtype, device=v.device)
+        want_init = s0 is not None and ctx.needs_input_grad[5]
+        res = gdn_tree_backward(q, k, v, g, beta, d_o, ctx.tree, ctx.scale, ctx.l2norm,
+                                saved=kept[0] if kept else None, reference_truncated=ctx.trunc, initial_state=s0,
+                                d_states=d_states, initial_state_grad=want_init)
+        dq, dk, dv, dg, dbeta = res[:5]
+        d_init = res[5].reshape(s0.shape).to(s0.dtype) if want_init else None
         return (dq.reshape(q.shape).to(q.dtype), dk.reshape(k.shape).to(k.dtype), dv.reshape(v.shape).to(v.dtype),
-                dg.reshape(g.shape).to(g.dtype), dbeta.reshape(beta.shape).to(beta.dtype), None, None, None, None)
+                dg.reshape(g.shape).to(g.dtype), dbeta.reshape(beta.shape).to(beta.dtype), d_init,
+                None, None, None, None)
 
 
 def gdn_tree(q, k, v, g, beta, tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True,
-             reference_truncated: bool = False):
-    """Autograd-aware ``gdn_tree_forward``: (o, node_states). When any input
-    requires a gradient and ``KEEP_FORWARD_STATES`` is set, the forward keeps
-    its chunk terms and states for the backward."""
-    if not (torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, g, beta))):
-        return gdn_tree_forward(q, k, v, g, beta, tree, scale, l2norm, reference_truncated)
-    return GdnTreeFunction.apply(q, k, v, g, beta, tree, scale, l2norm, bool(reference_truncated))
+             reference_truncated: bool = False, initial_state: Optional[torch.Tensor] = None):
+    """Autograd-aware ``gdn_tree_forward``: (o, node_states), differentiable
+    in q, k, v, g, beta and ``initial_state`` ([Hv, 128, 128], or [1, Hv,
+    128, 128]; every root's state, zero when None). When any input requires
+    a gradient and ``KEEP_FORWARD_STATES`` is set, the forward keeps its chunk
+    terms and states for the backward."""
+    ins = (q, k, v, g, beta) + (() if initial_state is None else (initial_state,))
+    if not (torch.is_grad_enabled() and any(t.requires_grad for t in ins)):
+        return gdn_tree_forward(q, k, v, g, beta, tree, scale, l2norm, reference_truncated, initial_state)
+    return GdnTreeFunction.apply(q, k, v, g, beta, initial_state, tree, scale, l2norm, bool(reference_truncated))
 
 
 def torch_chunk_gated_delta_rule_tree_varlen(query, key, value, g, beta, chunk_boundaries, chunk_parent_map,
                                              initial_state=None, output_final_state=False,
                                              use_qk_l2norm_in_kernel=False, reference_truncated=False):
-    """Signature of tree_dfs_ssm.py:38-46 (no initial state), differentiable in
-    q, k, v, g and beta. Returns (core_out [1, T, Hv, 128], None or the last
-    node's state). ``reference_truncated=True`` gives the reference function's
-    own numbers (I + R + R^2 per node) instead of the exact rule."""
-    if initial_state is not None:
-        raise NotImplementedError("initial_state is not supported (the reference drivers pass None)")
+    """Signature of tree_dfs_ssm.py:38-46, differentiable in q, k, v, g, beta
+    and ``initial_state`` ([1, Hv, 128, 128], the state every root starts
+    from; zero when None, tree_dfs_ssm.py:84-86). Returns (core_out [1, T, Hv,
+    128], None or the last node's state [1, Hv, 128, 128], float32 and
+    differentiable as tree_dfs_ssm.py:155). ``reference_truncated=True``
+    gives the reference function's own numbers (I + R + R^2 per node) instead
+    of the exact rule."""
     tree = GdnTree.from_boundaries(chunk_boundaries, chunk_parent_map, query.device)
     o, states = gdn_tree(query, key, value, g, beta, tree, l2norm=use_qk_l2norm_in_kernel,
-                         reference_truncated=reference_truncated)
+                         reference_truncated=reference_truncated, initial_state=initial_state)
     last = states[-1][None] if output_final_state else None
     return o[None], last
