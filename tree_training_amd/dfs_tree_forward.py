@@ -78,20 +78,24 @@ def run_tree_model(model, info: DFSTreeInfo, dev, pos_offset: int = 0, cache=Non
 
 
 def dfs_tree_forward(model, roots: List[TreeNode], dtype: Optional[torch.dtype] = None,
-                     gdn_reference_truncated: bool = False) -> DFSTreeResult:
+                     gdn_reference_truncated: bool = False, gdn_per_node_projections: bool = False) -> DFSTreeResult:
     """One DFS-packed forward over a forest (dfs_tree_forward.py:513-576).
 
     ``dtype`` is accepted for signature compatibility; it only set the dense
     mask's dtype in the reference, and no dense mask is built here.
     ``gdn_reference_truncated`` makes the gated-delta-rule layers of hybrid
     models compute what the reference's scan computes (I + R + R^2 per node)
-    instead of the exact rule.
+    instead of the exact rule; ``gdn_per_node_projections`` makes them
+    project node by node as the reference does (same GEMM shapes as per-path
+    runs, so their outputs match those bit for bit) instead of one GEMM per
+    projection.
     """
     dev = next(model.parameters()).device
     info = build_dfs_tree_info(roots)
     # gated-delta-rule layers (hybrid models) run the tree-aware conv + scan
     from .gdn_layer import _patch_ssm, _unpatch_ssm
-    saved = _patch_ssm(model, info.chunk_boundaries, info.chunk_parent_map, gdn_reference_truncated)
+    saved = _patch_ssm(model, info.chunk_boundaries, info.chunk_parent_map, gdn_reference_truncated,
+                       gdn_per_node_projections)
     try:
         out = run_tree_model(model, info, dev, linear_attention_patched=True)
     finally:
