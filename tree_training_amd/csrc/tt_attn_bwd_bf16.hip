@@ -118,8 +118,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // half before the next. Half the score registers are live at a time
         // (234 VGPRs without spills, against 256 and a spill for the whole
         // tile at once), so the operand reads run further ahead of their MFMAs.
+        // A partial tile's half that no query of the wave sees is skipped.
+        const int run = full ? 3 : visible_halves(S.lo, S.hi, qb * TT_BQ + wave * 32, lane);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
+            if (!((run >> b) & 1)) continue;
             f32x16 sh = (f32x16){}, dph = (f32x16){};
 #pragma unroll
             for (int t = 0; t < 8; ++t) {

@@ -286,6 +286,16 @@ __device__ __forceinline__ void mask_scores(f32x16 (&s)[2], const int* s_lo, con
     }
 }
 
+// Which 32-key halves of a tile hold a key visible to any of the wave's 32
+// queries [q0, q0 + 32): bit b set for half b (lane l tests key l of the
+// tile). Wave-uniform. A half with no such key contributes nothing (every
+// score -inf, every probability and dS zero), so a wave skips it.
+__device__ __forceinline__ int visible_halves(const int* s_lo, const int* s_hi, int q0, int lane) {
+    const bool v = max(s_lo[lane], q0) < min(s_hi[lane], q0 + 32);
+    const unsigned long long b = __ballot(v);
+    return __builtin_amdgcn_readfirstlane(((unsigned)b != 0u ? 1 : 0) | ((unsigned)(b >> 32) != 0u ? 2 : 0));
+}
+
 // As mask_scores, for one 32-key half of the tile (lo/hi point at its first key).
 __device__ __forceinline__ void mask_half(f32x16& s, const int* s_lo, const int* s_hi, int qi, int half) {
 #pragma unroll
