@@ -169,6 +169,107 @@ struct ScanLds {
     float G[GC];
 };
 
+// A chunk's scan inputs, held in registers one chunk ahead of their use (the
+// loads of the next chunk are in flight while a chunk computes): this
+// thread's share of the q and k rows (row t/8, dims 16 (t%8) .. +15, in the
+// problem dtype), of W's rows, four entries of A and the decays, and this
+// lane's 16 x 16 operand tiles of U (forward) or dO (reverse).
+template <typename TIn>
+struct ScanAhead {
+    using Vec = typename std::conditional<sizeof(TIn) == 2, bf16x8, f32x4>::type;
+    static constexpr int NV = 16 * (int)sizeof(TIn) / 16;   // vectors per 16 elements
+    Vec q[NV], k[NV];
+    f32x4 w[4];
+    float a[4];
+    float gi, gl, gt;
+    f32x4 x[2];
+};
+
+// Loads the parts of chunk (start, len) that do not depend on the state: q/k
+// rows, W rows (with LOAD_W), A and the decays from its workspace slot cw.
+template <typename TIn, bool LOAD_W>
+__device__ __forceinline__ void scan_fetch_rows(const GdnDev& p, const float* cw, int start, int len, int h,
+                                                ScanAhead<TIn>& x) {
+    using Vec = typename ScanAhead<TIn>::Vec;
+    constexpr int NV = ScanAhead<TIn>::NV, EV = 16 / NV;
+    const int t = threadIdx.x, i = t >> 3, d0 = 16 * (t & 7), hk = h / p.rep;
+    if (i < len) {
+        const int64_t tok = start + i;
+        const TIn* qp = (const TIn*)p.q + tok * p.q_st + (int64_t)hk * p.q_sh + d0;
+        const TIn* kp = (const TIn*)p.k + tok * p.k_st + (int64_t)hk * p.k_sh + d0;
+#pragma unroll
+        for (int n = 0; n < NV; ++n) {
+            x.q[n] = *(const Vec*)(qp + EV * n);
+            x.k[n] = *(const Vec*)(kp + EV * n);
+        }
+    } else {
+#pragma unroll
+        for (int n = 0; n < NV; ++n) {
+#pragma unroll
+            for (int e = 0; e < EV; ++e) x.q[n][e] = x.k[n][e] = (TIn)0.0f;
+        }
+    }
+    if constexpr (LOAD_W) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x.w[e] = *(const f32x4*)(cw + kWsW + i * GD + d0 + 4 * e);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x.a[e] = cw[kWsA + t + GT * e];
+    x.gi = cw[kWsG + i];
+    x.gl = cw[kWsG + GC - 1];
+    x.gt = cw[kWsG + (t & (GC - 1))];
+}
+
+// Writes a fetched chunk to LDS: Q = q^ * scale * qmul_i, K = k^ * kmul_i
+// (each rounded after the normalisation, then after the multiplier), W with
+// STORE_W, A and G. qmul / kmul: e^{G_i} / e^{G_L - G_i} where the scan needs
+// them (1 for none: the forward's Q).
+template <typename TIn, bool STORE_W, bool QMUL>
+__device__ __forceinline__ void scan_stage_rows(const GdnDev& p, const ScanAhead<TIn>& x, float* Q, float* K,
+                                                float* W, float* A, float* G) {
+    constexpr int NV = ScanAhead<TIn>::NV, EV = 16 / NV;
+    const int t = threadIdx.x, i = t >> 3, d0 = 16 * (t & 7);
+    float qv[16], kv[16];
+#pragma unroll
+    for (int n = 0; n < NV; ++n)
+#pragma unroll
+        for (int e = 0; e < EV; ++e) {
+            qv[EV * n + e] = (float)x.q[n][e];
+            kv[EV * n + e] = (float)x.k[n][e];
+        }
+    float sq = 0.0f, sk = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        sq = fmaf(qv[e], qv[e], sq);
+        sk = fmaf(kv[e], kv[e], sk);
+    }
+    sq = row8_sum(sq);
+    sk = row8_sum(sk);
+    const float fq = (p.l2 ? 1.0f / sqrtf(sq + 1e-6f) : 1.0f) * p.scale;
+    const float fk = p.l2 ? 1.0f / sqrtf(sk + 1e-6f) : 1.0f;
+    const float eq = QMUL ? expf(x.gi) : 1.0f, ek = expf(x.gl - x.gi);
+#pragma unroll
+    for (int e = 0; e < 16; e += 4) {
+        f32x4 qo, ko;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            qo[v] = qv[e + v] * fq;
+            ko[v] = kv[e + v] * fk;
+            if constexpr (QMUL) qo[v] *= eq;
+            ko[v] *= ek;
+        }
+        *(f32x4*)&Q[i * RS + d0 + e] = qo;
+        *(f32x4*)&K[i * RS + d0 + e] = ko;
+        if constexpr (STORE_W) *(f32x4*)&W[i * RS + d0 + e] = x.w[e / 4];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int pi = t + GT * e;
+        A[(pi >> 5) * MS + (pi & 31)] = x.a[e];
+    }
+    if (t < GC) G[t] = x.gt;
+}
+
 // Column layout of the level scans. The value columns of the delta rule are
 // independent (column j of V', O and S depends only on column j of U, S and
 // V'); each wave owns 16 of them (16 x 16 fp32 MFMA tiles), and a (node,
@@ -264,39 +365,37 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         }
     }
 
-    for (int c0 = 0; c0 < len; c0 += GC) {
-        const int Lc = min(GC, len - c0);
-        const size_t ch = (size_t)(chunk0 + c0 / GC) * p.hv + h;
-        const float* cw = ws + ch * kWsChunk;
+    // U (TRUNC: V', written by the first pass) and the state-independent
+    // chunk terms, one chunk ahead.
+    const int n_ch = tt_cdiv(len, GC);
+    ScanAhead<TIn> nx;
+    {
+        const float* cw = ws + ((size_t)chunk0 * p.hv + h) * kWsChunk;
+        scan_fetch_rows<TIn, !TRUNC>(p, cw, start, min(GC, len), h, nx);
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) nx.x[tb] = load_t16(cw + kWsU + 16 * tb * GD + jt, lane);
+    }
+    for (int ci = 0; ci < n_ch; ++ci) {
+        const int c0 = GC * ci, Lc = min(GC, len - c0);
+        const size_t ch = (size_t)(chunk0 + ci) * p.hv + h;
         if (chunk_sin) {
             float* sp = chunk_sin + ch * GD * GD + jt;
 #pragma unroll
             for (int rb = 0; rb < 8; ++rb) store_t16(sp + 16 * rb * GD, lane, S[rb]);
         }
         __syncthreads();   // readers of the previous chunk's tiles are done
-        load_chunk_rows<TIn>(p, start + c0, Lc, h, L.Q, L.K, nullptr);
-        {
-            const int i = t >> 3, d0 = 16 * (t & 7);
-            const float ek = expf(cw[kWsG + GC - 1] - cw[kWsG + i]);
-#pragma unroll
-            for (int e = 0; e < 16; e += 4) {   // rows written by this thread just above
-                *(f32x4*)&L.K[i * RS + d0 + e] *= ek;
-                if constexpr (!TRUNC)
-                    *(f32x4*)&L.W[i * RS + d0 + e] = *(const f32x4*)(cw + kWsW + i * GD + d0 + e);
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int pi = t + GT * e;
-                L.A[(pi >> 5) * MS + (pi & 31)] = cw[kWsA + pi];
-            }
-            if (t < GC) L.G[t] = cw[kWsG + t];
-        }
-        // U (TRUNC: V', written by the first pass)
+        scan_stage_rows<TIn, !TRUNC, false>(p, nx, L.Q, L.K, L.W, L.A, L.G);
         f32x4 vp[2], qs[2];
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
-            vp[tb] = load_t16(cw + kWsU + 16 * tb * GD + jt, lane);
+            vp[tb] = nx.x[tb];
             qs[tb] = (f32x4){};
+        }
+        if (ci + 1 < n_ch) {
+            const float* cw = ws + (ch + p.hv) * kWsChunk;
+            scan_fetch_rows<TIn, !TRUNC>(p, cw, start + c0 + GC, min(GC, len - c0 - GC), h, nx);
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) nx.x[tb] = load_t16(cw + kWsU + 16 * tb * GD + jt, lane);
         }
         __syncthreads();
 
@@ -440,46 +539,36 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         }
     }
 
-    for (int ci = tt_cdiv(len, GC) - 1; ci >= 0; --ci) {
+    // The chunk terms and dO rows of a chunk, one chunk ahead (the walk runs
+    // backwards).
+    const int n_ch = tt_cdiv(len, GC);
+    auto fetch = [&](int ci, ScanAhead<TIn>& x) {
+        const int c0 = GC * ci, Lc = min(GC, len - c0);
+        const float* cw = ws + ((size_t)(chunk0 + ci) * p.hv + h) * kWsChunk;
+        scan_fetch_rows<TIn, !TRUNC>(p, cw, start + c0, Lc, h, x);
+        const TIn* base = d_o + (int64_t)(start + c0) * do_st + (int64_t)h * do_sh + j;
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {   // dO[token 16 tb + 4 (l >> 4) + v][j], zero past the chunk
+                const int i = 16 * tb + g4 + v;
+                x.x[tb][v] = i < Lc ? (float)base[(int64_t)i * do_st] : 0.0f;
+            }
+    };
+    ScanAhead<TIn> nx;
+    fetch(n_ch - 1, nx);
+    for (int ci = n_ch - 1; ci >= 0; --ci) {
         const int c0 = GC * ci, Lc = min(GC, len - c0);
         const size_t chn = (size_t)(chunk0 + ci) * p.hv + h;
-        const float* cw = ws + chn * kWsChunk;
         {   // the gradient of this chunk's output state
             float* sp = chunk_dso + chn * GD * GD + jt;
 #pragma unroll
             for (int rb = 0; rb < 8; ++rb) store_t16(sp + 16 * rb * GD, lane, dS[rb]);
         }
         __syncthreads();   // readers of the previous chunk's tiles are done
-        load_chunk_rows<TIn>(p, start + c0, Lc, h, L.Q, L.K, nullptr);
-        {
-            const int i = t >> 3, d0 = 16 * (t & 7);
-            const float gi = cw[kWsG + i], gl = cw[kWsG + GC - 1];
-            const float eq = expf(gi), ek = expf(gl - gi);
-#pragma unroll
-            for (int e = 0; e < 16; e += 4) {   // rows written by this thread just above
-                *(f32x4*)&L.Q[i * RS + d0 + e] *= eq;
-                *(f32x4*)&L.K[i * RS + d0 + e] *= ek;
-                if constexpr (!TRUNC)
-                    *(f32x4*)&L.W[i * RS + d0 + e] = *(const f32x4*)(cw + kWsW + i * GD + d0 + e);
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int pi = t + GT * e;
-                L.A[(pi >> 5) * MS + (pi & 31)] = cw[kWsA + pi];
-            }
-            if (t < GC) L.G[t] = cw[kWsG + t];
-        }
-        f32x4 dov[2];   // dO[token 16 tb + 4 (l >> 4) + v][j], zero past the chunk
-        {
-            const TIn* base = d_o + (int64_t)(start + c0) * do_st + (int64_t)h * do_sh + j;
-#pragma unroll
-            for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const int i = 16 * tb + g4 + v;
-                    dov[tb][v] = i < Lc ? (float)base[(int64_t)i * do_st] : 0.0f;
-                }
-        }
+        scan_stage_rows<TIn, !TRUNC, true>(p, nx, L.Q, L.K, L.W, L.A, L.G);
+        const f32x4 dov[2] = {nx.x[0], nx.x[1]};
+        if (ci > 0) fetch(ci - 1, nx);
         __syncthreads();
 
         // dV' = A^T dO + k~ dS
