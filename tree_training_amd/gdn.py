@@ -4,7 +4,9 @@ Drop-in for ``torch_chunk_gated_delta_rule_tree_varlen`` (tree_dfs_ssm.py:38-156
 twin ``_tree_gated_delta_net_varlen`` in dfs_tree_forward.py:253-353): the same
 inputs — q, k ``[B=1, T, Hk, D]``, v ``[1, T, Hv, D]``, g, beta ``[1, T, Hv]``,
 ``chunk_boundaries`` (one (start, end) per tree node, DFS order) and
-``chunk_parent_map`` (parent node index, -1 for a root) — computed through
+``chunk_parent_map`` (parent node index, -1 for a root), the optional
+``initial_state`` every root starts from and ``output_final_state`` (the last
+node's state, differentiable like the output) — computed through
 ``tt_gdn_tree_fwd``: one parallel HIP launch over all 32-token chunks for the
 state-independent terms, then one scan launch per tree level.
 
