@@ -336,8 +336,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             stg.begin(a, kt1, g);
             fetch_bounds(a, kt1, nb);
         }
+        // a partial tile's 32-key half that none of the wave's queries sees is skipped
+        const int run = full ? 3 : visible_halves(S.lo, S.hi, qb * TT_BQ + wave * 32, lane);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
+            if (!((run >> b) & 1)) continue;
             f32x16 sh = scores_t(S.K, 32 * b, q, col, half);
             f32x16 dph = {};
             {
@@ -424,7 +427,7 @@ struct QBlockStagerF {
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void bwd_dkdv_f32_kernel(AttnDev a,
                                                                                                      BwdDev bw) {
-    __shared__ __attribute__((aligned(16))) QStageF S;
+    __shared__ __attribute__((aligned(16))) QStageF St[2];
     __shared__ __attribute__((aligned(16))) float Vs[TT_BKB * ROWR];   // V rows of the item's keys
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -481,9 +484,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         if (n_steps > 0) stg.begin(a, bw, q0, g * a.rep);
         const float* vrow = Vs + (wave * 32 + col) * ROWR + 4 * half;
         for (int s = 0; s < n_steps; ++s) {
-            __syncthreads();   // the previous block's readers are done (and Vs written)
+            // Two stages: the one written here was last read in step s - 2, and
+            // every wave passed the barrier of step s - 1 after finishing it.
+            QStageF& S = St[s & 1];
             stg.commit(a, bw, S);
-            __syncthreads();
+            __syncthreads();   // the stage (and, at step 0, Vs) written
             const int q0_cur = q0;
             if (++hh == a.rep) {
                 hh = 0;
