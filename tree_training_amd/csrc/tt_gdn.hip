@@ -3,8 +3,9 @@
 //
 // Semantics: the gated delta rule token by token along every root-to-leaf
 // path — each node continues from its parent's final state (a root from the
-// caller's initial state, or zero) — evaluated exactly in TT_GDN_CHUNK = 32-token chunks (a node is cut
-// into consecutive chunks; its last chunk may be short):
+// caller's initial state, or zero) — evaluated exactly in TT_GDN_CHUNK =
+// 32-token chunks (a node is cut into consecutive chunks; its last chunk may
+// be short):
 //   G = cumsum(g), D[i][j] = exp(G_i - G_j) (j <= i),
 //   N = -strictly_lower(beta k k^T * D),  T = (I - N)^-1,
 //   U = T (beta v),  W = T (beta e^G k),  A = lower_incl(q k^T * D),
