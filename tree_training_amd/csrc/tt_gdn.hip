@@ -35,9 +35,9 @@ namespace {
 struct PrepLds {
     float Q[GC * RS];     // q^ * scale; v once A is done
     float K[GC * RS];
-    float R[4][GC * RR];  // partial products: A (waves 0, 1), k^ k^T (waves 2, 3)
-    float N[GC * MS];     // N = -strictly_lower(beta k^ k^T * D), then its powers N^(2^r)
-    float Tm[GC * MS];    // T = (I - N)^-1, built as (I + N)(I + N^2)(I + N^4)...
+    float R[4][GC * RR];  // partial products: A (waves 0, 1), k^ k^T (waves 2, 3); then T's 16 x 16 blocks
+    float N[GC * MS];     // N = -strictly_lower(beta k^ k^T * D)
+    float Tm[GC * MS];    // I + N, then T = (I - N)^-1
     float G[GC];
     float beta[GC];
     float bg[GC];         // beta e^G
@@ -103,36 +103,74 @@ __global__ __launch_bounds__(GT) void gdn_prep_kernel(GdnDev p, float* __restric
     if constexpr (TRUNC) return;
     __syncthreads();
 
-    // T = (I - N)^-1. N is strictly lower triangular (N^32 = 0), so
-    // (I - N)^-1 = (I + N)(I + N^2)(I + N^4)(I + N^8)(I + N^16): starting from
-    // T = I + N, P = N, four rounds of P <- P P, then T <- T + T P. Thread t
-    // owns row t/8, columns 4*(t%8)..+3 of each product.
+    // T = (I - N)^-1 by 16 x 16 blocks. With N = [[N11, 0], [N21, N22]],
+    // T = [[T11, 0], [T22 N21 T11, T22]] and, each Nbb strictly lower
+    // triangular (Nbb^16 = 0), Tbb = (I + Nbb)(I + Nbb^2)(I + Nbb^4)(I + Nbb^8):
+    // from T = I + Nbb, P = Nbb, three rounds of P <- P P, then T <- T + T P.
+    // Waves 0-1 take block 1, waves 2-3 block 2 (thread u: row u/8, columns
+    // 2 (u%8), +1), with double-buffered P and T in the partial-product
+    // buffer R (free again); then X = N21 T11 and T21 = T22 X, a thread an
+    // entry. A quarter of the work of squaring the whole 32 x 32 matrix.
     {
-        const int ti = t >> 3, tc = 4 * (t & 7);
-        for (int r = 0; r < 4; ++r) {
-            f32x4 pp = {};
-#pragma unroll 4
-            for (int m = 0; m < GC; ++m) {
-                const f32x4 pm = *(const f32x4*)&L.N[m * MS + tc];
-                const float pim = L.N[ti * MS + m];
+        constexpr int BS = 17;                                   // row stride of the 16 x 16 blocks
+        constexpr int B16 = 16 * BS;
+        float* sc = &L.R[0][0];
+        const int blk = t >> 7, u = t & 127, bi = u >> 3, bj = 2 * (u & 7), o = 16 * blk;
+        // block blk: P buffers at pb, pb + B16; T buffers at pb + 2 B16, pb + 3 B16
+        const int pb = blk * 4 * B16, tb = pb + 2 * B16;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) pp[e] = fmaf(pim, pm[e], pp[e]);
-            }
-            __syncthreads();
-            *(f32x4*)&L.N[ti * MS + tc] = pp;
-            __syncthreads();
-            f32x4 tp = {};
-#pragma unroll 4
-            for (int m = 0; m < GC; ++m) {
-                const f32x4 pm = *(const f32x4*)&L.N[m * MS + tc];
-                const float tim = L.Tm[ti * MS + m];
+        for (int e = 0; e < 2; ++e) {
+            const int j = bj + e;
+            const float n = L.N[(o + bi) * MS + o + j];
+            sc[pb + bi * BS + j] = n;
+            sc[tb + bi * BS + j] = n + (bi == j ? 1.0f : 0.0f);
+        }
+        __syncthreads();
 #pragma unroll
-                for (int e = 0; e < 4; ++e) tp[e] = fmaf(tim, pm[e], tp[e]);
+        for (int r = 0; r < 3; ++r) {
+            const int pc = pb + (r & 1) * B16, pn = pb + ((r + 1) & 1) * B16;
+            float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+            for (int m = 0; m < 16; ++m) {
+                const float pim = sc[pc + bi * BS + m];
+                a0 = fmaf(pim, sc[pc + m * BS + bj], a0);
+                a1 = fmaf(pim, sc[pc + m * BS + bj + 1], a1);
             }
+            sc[pn + bi * BS + bj] = a0;
+            sc[pn + bi * BS + bj + 1] = a1;
             __syncthreads();
-            *(f32x4*)&L.Tm[ti * MS + tc] += tp;
+            const int tc0 = tb + (r & 1) * B16, tn = tb + ((r + 1) & 1) * B16;
+            float t0 = sc[tc0 + bi * BS + bj], t1 = sc[tc0 + bi * BS + bj + 1];
+#pragma unroll
+            for (int m = 0; m < 16; ++m) {
+                const float tim = sc[tc0 + bi * BS + m];
+                t0 = fmaf(tim, sc[pn + m * BS + bj], t0);
+                t1 = fmaf(tim, sc[pn + m * BS + bj + 1], t1);
+            }
+            sc[tn + bi * BS + bj] = t0;
+            sc[tn + bi * BS + bj + 1] = t1;
             __syncthreads();
         }
+        // Tbb is in the second T buffer of its block; X = N21 T11 goes to
+        // block 1's first P buffer.
+        constexpr int T11 = 3 * B16, T22 = 4 * B16 + 3 * B16, X = 0;
+        const int xi = t >> 4, xj = t & 15;
+        {
+            float x = 0.0f;
+#pragma unroll
+            for (int m = 0; m < 16; ++m) x = fmaf(L.N[(16 + xi) * MS + m], sc[T11 + m * BS + xj], x);
+            sc[X + xi * BS + xj] = x;
+        }
+        __syncthreads();
+        float t21 = 0.0f;
+#pragma unroll
+        for (int m = 0; m < 16; ++m) t21 = fmaf(sc[T22 + xi * BS + m], sc[X + m * BS + xj], t21);
+        L.Tm[(16 + xi) * MS + xj] = t21;
+        L.Tm[xi * MS + 16 + xj] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) L.Tm[(o + bi) * MS + o + bj + e] = sc[tb + B16 + bi * BS + bj + e];
+        __syncthreads();
+        const int ti = t >> 3, tc = 4 * (t & 7);
         *(f32x4*)(out + kWsT + ti * GC + tc) = *(const f32x4*)&L.Tm[ti * MS + tc];
     }
 
