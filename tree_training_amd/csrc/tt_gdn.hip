@@ -695,28 +695,40 @@ __global__ __launch_bounds__(GT) void gdn_init_grad_kernel(GdnDev p, const float
 
 // State products on fp32 MFMA. The contraction (value dimension, 128) runs in
 // four 32-column chunks; per chunk the block stages, with coalesced loads,
-// columns v0..v0+31 of all 128 rows of S (or dS) and of the 32 rows of dO and
-// dV' (or V') into LDS rows of SCS = 34 floats: the MFMA operand reads (lane =
+// columns v0..v0+31 of all 128 rows of S and dS and of the 32 rows of dO, dV'
+// and V' into LDS rows of SCS = 34 floats: the MFMA operand reads (lane =
 // row, one float per lane, two adjacent columns per step) then reach all 64
 // banks once. Wave w produces columns 32w .. 32w+31 of X, dW and dK~ (rows of
 // S / dS 32w .. 32w+31) as accumulators.
 constexpr int SCS = 34;
-struct StateGradLds {
-    float S[GD * SCS];    // 32-column chunk of S or dS, all 128 rows
-    float A1[GC * SCS];   // chunk of dO, or of V'
-    float A2[GC * SCS];   // chunk of dV'
+struct StateGradLds {     // gdn_dw_s0_kernel: one chunk of S0 and of dV'
+    float S[GD * SCS];
+    float A1[GC * SCS];
+    float A2[GC * SCS];
     float red[GT / 64];
 };
 
-// Registers of one chunk: S / dS rows t/2 and t/2 + ... (thread t: row t >> 1,
-// columns 16 (t & 1) .. +15) and the 32-row tiles (row t >> 3, columns
-// 4 (t & 7) .. +3).
+// One 32-column slice of the value dimension of both S and dS (all 128 rows)
+// and the matching columns of dO, dV' and V', staged together: every input
+// is read once.
+struct StatePairLds {
+    float S[GD * SCS];
+    float dS[GD * SCS];
+    float A1[GC * SCS];   // dO
+    float A2[GC * SCS];   // dV'
+    float A3[GC * SCS];   // V'
+    float red[GT / 64];
+};
+
+// Registers of one slice: S and dS at the same positions (thread t: row
+// t >> 1, columns 16 (t & 1) .. +15) and the 32-row tiles (row t >> 3,
+// columns 4 (t & 7) .. +3).
 template <typename TIn>
 struct StateChunk {
     float s[16];
-    float s2[16];   // phase 1: the S elements matching s (for <S, dS>)
-    f32x4 a1, a2;
-    u32x4 d;        // dO of phase 0 as loaded (bf16: two per word; converted when committed)
+    float ds[16];
+    f32x4 vp, dvp;
+    u32x4 d;        // dO as loaded (bf16: two per word; converted when committed)
 };
 
 // X = dO S^T, dW = -dV' S^T, dK~ = V' dS^T ([GC x GD] each) and <S, dS>.
@@ -728,7 +740,7 @@ __global__ __launch_bounds__(GT) void gdn_bwd_state_kernel(GdnDev p, const TIn* 
                                                            const float* __restrict__ chunk_dvp,
                                                            float* __restrict__ xo, float* __restrict__ dwo,
                                                            float* __restrict__ dkto, float* __restrict__ sdot) {
-    __shared__ __attribute__((aligned(16))) StateGradLds L;
+    __shared__ __attribute__((aligned(16))) StatePairLds L;
     const int c = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
     int start, len;
     if (!chunk_span(p, c, start, len)) return;
@@ -744,96 +756,74 @@ __global__ __launch_bounds__(GT) void gdn_bwd_state_kernel(GdnDev p, const TIn* 
     const TIn* dor = d_o + (int64_t)(start + min(ar, len - 1)) * do_st + (int64_t)h * do_sh;
     const bool arow_in = ar < len;
 
-    // Chunk k of the value dimension into registers: phase 0, S with dO and
-    // dV'; phase 1, dS with V'.
-    auto fetch = [&](auto phase, int k, StateChunk<TIn>& r) {
+    auto fetch = [&](int k, StateChunk<TIn>& r) {
         const int v0 = GC * k;
-        const float* src = (phase.value == 0 ? Sin : dSo) + sr * GD + v0 + sc;
+        const int so = sr * GD + v0 + sc;
 #pragma unroll
         for (int e = 0; e < 16; e += 4) {
-            const f32x4 x4 = *(const f32x4*)(src + e);
+            const f32x4 x4 = *(const f32x4*)(Sin + so + e);
+            const f32x4 y4 = *(const f32x4*)(dSo + so + e);
             r.s[e] = x4[0]; r.s[e + 1] = x4[1]; r.s[e + 2] = x4[2]; r.s[e + 3] = x4[3];
+            r.ds[e] = y4[0]; r.ds[e + 1] = y4[1]; r.ds[e + 2] = y4[2]; r.ds[e + 3] = y4[3];
         }
-        if constexpr (phase.value == 0) {
-            if constexpr (sizeof(TIn) == 2) {
-                const u32x2 raw = *(const u32x2*)(dor + v0 + ac);
-                r.d = (u32x4){raw[0], raw[1], 0u, 0u};
-            } else {
-                r.d = *(const u32x4*)(dor + v0 + ac);
-            }
-            r.a2 = *(const f32x4*)(dVp + ar * GD + v0 + ac);
-            r.a1 = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int e = 0; e < 16; ++e) r.s2[e] = 0.0f;
-        } else {   // every field is defined in both phases (no undefined loop-carried values)
-            r.a1 = *(const f32x4*)(Vp + ar * GD + v0 + ac);
-            r.a2 = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-            r.d = (u32x4){0u, 0u, 0u, 0u};
-            const float* so = Sin + sr * GD + v0 + sc;
-#pragma unroll
-            for (int e = 0; e < 16; e += 4) {
-                const f32x4 x4 = *(const f32x4*)(so + e);
-                r.s2[e] = x4[0]; r.s2[e + 1] = x4[1]; r.s2[e + 2] = x4[2]; r.s2[e + 3] = x4[3];
-            }
-        }
-    };
-    auto commit = [&](auto phase, const StateChunk<TIn>& r) {
-#pragma unroll
-        for (int e = 0; e < 16; e += 2) *(float2*)&L.S[sr * SCS + sc + e] = (float2){r.s[e], r.s[e + 1]};
-        if constexpr (phase.value == 0) {   // A1 is dO: rows past the chunk are zero
-            const float z = arow_in ? 1.0f : 0.0f;
-            float dv4[4];
-            if constexpr (sizeof(TIn) == 2) {   // bf16 -> fp32: the high half of a float
-                dv4[0] = __uint_as_float(r.d[0] << 16);
-                dv4[1] = __uint_as_float(r.d[0] & 0xffff0000u);
-                dv4[2] = __uint_as_float(r.d[1] << 16);
-                dv4[3] = __uint_as_float(r.d[1] & 0xffff0000u);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) dv4[e] = __uint_as_float(r.d[e]);
-            }
-            *(float2*)&L.A1[ar * SCS + ac] = (float2){z * dv4[0], z * dv4[1]};
-            *(float2*)&L.A1[ar * SCS + ac + 2] = (float2){z * dv4[2], z * dv4[3]};
-            *(float2*)&L.A2[ar * SCS + ac] = (float2){r.a2[0], r.a2[1]};
-            *(float2*)&L.A2[ar * SCS + ac + 2] = (float2){r.a2[2], r.a2[3]};
+        if constexpr (sizeof(TIn) == 2) {
+            const u32x2 raw = *(const u32x2*)(dor + v0 + ac);
+            r.d = (u32x4){raw[0], raw[1], 0u, 0u};
         } else {
-            *(float2*)&L.A1[ar * SCS + ac] = (float2){r.a1[0], r.a1[1]};
-            *(float2*)&L.A1[ar * SCS + ac + 2] = (float2){r.a1[2], r.a1[3]};
+            r.d = *(const u32x4*)(dor + v0 + ac);
         }
+        r.dvp = *(const f32x4*)(dVp + ar * GD + v0 + ac);
+        r.vp = *(const f32x4*)(Vp + ar * GD + v0 + ac);
+    };
+    auto commit = [&](const StateChunk<TIn>& r) {
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+            *(float2*)&L.S[sr * SCS + sc + e] = (float2){r.s[e], r.s[e + 1]};
+            *(float2*)&L.dS[sr * SCS + sc + e] = (float2){r.ds[e], r.ds[e + 1]};
+        }
+        const float z = arow_in ? 1.0f : 0.0f;   // dO rows past the chunk are zero
+        float dv4[4];
+        if constexpr (sizeof(TIn) == 2) {   // bf16 -> fp32: the high half of a float
+            dv4[0] = __uint_as_float(r.d[0] << 16);
+            dv4[1] = __uint_as_float(r.d[0] & 0xffff0000u);
+            dv4[2] = __uint_as_float(r.d[1] << 16);
+            dv4[3] = __uint_as_float(r.d[1] & 0xffff0000u);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dv4[e] = __uint_as_float(r.d[e]);
+        }
+        *(float2*)&L.A1[ar * SCS + ac] = (float2){z * dv4[0], z * dv4[1]};
+        *(float2*)&L.A1[ar * SCS + ac + 2] = (float2){z * dv4[2], z * dv4[3]};
+        *(float2*)&L.A2[ar * SCS + ac] = (float2){r.dvp[0], r.dvp[1]};
+        *(float2*)&L.A2[ar * SCS + ac + 2] = (float2){r.dvp[2], r.dvp[3]};
+        *(float2*)&L.A3[ar * SCS + ac] = (float2){r.vp[0], r.vp[1]};
+        *(float2*)&L.A3[ar * SCS + ac + 2] = (float2){r.vp[2], r.vp[3]};
     };
 
     f32x16 x = (f32x16){}, w = (f32x16){}, kt = (f32x16){};
     float sd = 0.0f;
-    const float* brow = &L.S[(32 * wave + col) * SCS + half];   // B: S row 32w + col, columns 2 step + half
-    const float* arow1 = &L.A1[col * SCS + half];               // A: row col, columns 2 step + half
+    const float* brow = &L.S[(32 * wave + col) * SCS + half];    // B: S row 32w + col, columns 2 step + half
+    const float* dbrow = &L.dS[(32 * wave + col) * SCS + half];  // B: the same row of dS
+    const float* arow1 = &L.A1[col * SCS + half];                // A: row col, columns 2 step + half
     const float* arow2 = &L.A2[col * SCS + half];
+    const float* arow3 = &L.A3[col * SCS + half];
     StateChunk<TIn> cur, nxt;
-    fetch(IntC4<0>{}, 0, cur);
+    fetch(0, cur);
 #pragma unroll 1
     for (int k = 0; k < 4; ++k) {
-        __syncthreads();   // the previous chunk's readers are done
-        commit(IntC4<0>{}, cur);
+        __syncthreads();   // the previous slice's readers are done
+        commit(cur);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sd = fmaf(cur.s[e], cur.ds[e], sd);   // <S, dS>, this thread's share
         __syncthreads();
-        if (k + 1 < 4) fetch(IntC4<0>{}, k + 1, nxt);
-        else fetch(IntC4<1>{}, 0, nxt);
+        if (k + 1 < 4) fetch(k + 1, nxt);
 #pragma unroll
         for (int st = 0; st < GC / 2; ++st) {
             const float b = brow[2 * st];
             x = mfma_f32(arow1[2 * st], b, x);
             w = mfma_f32(arow2[2 * st], b, w);
+            kt = mfma_f32(arow3[2 * st], dbrow[2 * st], kt);
         }
-        cur = nxt;
-    }
-#pragma unroll 1
-    for (int k = 0; k < 4; ++k) {
-        __syncthreads();
-        commit(IntC4<1>{}, cur);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sd = fmaf(cur.s2[e], cur.s[e], sd);   // <S, dS>, this thread's share
-        __syncthreads();
-        if (k + 1 < 4) fetch(IntC4<1>{}, k + 1, nxt);
-#pragma unroll
-        for (int st = 0; st < GC / 2; ++st) kt = mfma_f32(arow1[2 * st], brow[2 * st], kt);
         cur = nxt;
     }
     // Accumulator element r: row acc_row(r, half) (token), column 32w + col.
