@@ -79,15 +79,17 @@ __device__ __forceinline__ void load_taps(const ConvDev& p, int c, float (&w)[4]
 
 // The window of consecutive tokens: when prev(t) is the previous token of the
 // run (inside a node), t's window is the last one shifted by a row, so only
-// x[t] is loaded; otherwise (a node's first token, the run's first) it is
-// gathered along the predecessor chain. The test is uniform over the
-// workgroup (every thread walks the same tokens).
+// x[t] is new; otherwise (a node's first token, the run's first) the rows
+// before it are gathered along the predecessor chain. The test is uniform over
+// the workgroup (every thread walks the same tokens). x[t] itself is passed
+// in: the callers load it one token ahead, so that a wave keeps the next
+// token's rows in flight while it computes the current one.
 template <int K, typename T>
 struct SlidingWindow {
     int idx[K];
     f32x4 xv[K];
     int last = -1;
-    __device__ __forceinline__ void advance(const ConvDev& p, int c, int t) {
+    __device__ __forceinline__ void advance(const ConvDev& p, int c, int t, const f32x4& xt) {
         if (last >= 0 && prev_of(p, t) == last) {
 #pragma unroll
             for (int i = 0; i < K - 1; ++i) {
@@ -95,13 +97,13 @@ struct SlidingWindow {
                 xv[i] = xv[i + 1];
             }
             idx[K - 1] = t;
-            xv[K - 1] = ld4((const T*)p.x + (int64_t)t * p.x_st + c);
         } else {
             window<K>(p, t, idx);
 #pragma unroll
-            for (int i = 0; i < K; ++i)
+            for (int i = 0; i < K - 1; ++i)
                 xv[i] = idx[i] >= 0 ? ld4((const T*)p.x + (int64_t)idx[i] * p.x_st + c) : (f32x4){};
         }
+        xv[K - 1] = xt;
         last = t;
     }
     __device__ __forceinline__ f32x4 preact(const float (&w)[4][K], const float (&b)[4]) const {
@@ -120,10 +122,14 @@ __global__ __launch_bounds__(CT) void conv_fwd_kernel(ConvDev p, T* __restrict__
     if (c >= p.n_ch) return;
     float w[4][K], b[4];
     load_taps<K, T>(p, c, w, b);
-    const int t1 = min(p.n_tokens, (int)(blockIdx.x + 1) * CTOK);
+    const int t0 = blockIdx.x * CTOK, t1 = min(p.n_tokens, t0 + CTOK);
+    const T* xc = (const T*)p.x + c;
     SlidingWindow<K, T> win;
-    for (int t = blockIdx.x * CTOK; t < t1; ++t) {
-        win.advance(p, c, t);
+    f32x4 xn = ld4(xc + (int64_t)t0 * p.x_st);    // t0 < n_tokens: the grid covers the tokens
+    for (int t = t0; t < t1; ++t) {
+        const f32x4 xt = xn;
+        if (t + 1 < t1) xn = ld4(xc + (int64_t)(t + 1) * p.x_st);
+        win.advance(p, c, t, xt);
         const f32x4 z = win.preact(w, b);
         f32x4 o;
 #pragma unroll
@@ -145,13 +151,20 @@ __global__ __launch_bounds__(CT) void conv_bwd_gp_kernel(ConvDev p, const T* __r
     f32x4 aw[K], ab = {};
 #pragma unroll
     for (int i = 0; i < K; ++i) aw[i] = (f32x4){};
-    const int t1 = min(p.n_tokens, (int)(blockIdx.x + 1) * CTOK_W);
+    const int t0 = blockIdx.x * CTOK_W, t1 = min(p.n_tokens, t0 + CTOK_W);
+    const T* xc = (const T*)p.x + c;
     SlidingWindow<K, T> win;
-    for (int t = blockIdx.x * CTOK_W; t < t1; ++t) {
-        win.advance(p, c, t);
+    f32x4 xn = ld4(xc + (int64_t)t0 * p.x_st);    // t0 < n_tokens: the grid covers the tokens
+    f32x4 dn = ld4(dy + (int64_t)t0 * dy_st + c);
+    for (int t = t0; t < t1; ++t) {
+        const f32x4 xt = xn, d = dn;
+        if (t + 1 < t1) {
+            xn = ld4(xc + (int64_t)(t + 1) * p.x_st);
+            dn = ld4(dy + (int64_t)(t + 1) * dy_st + c);
+        }
+        win.advance(p, c, t, xt);
         const f32x4 z = win.preact(w, b);
         const f32x4* xv = win.xv;
-        const f32x4 d = ld4(dy + (int64_t)t * dy_st + c);
         f32x4 g;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -169,7 +182,14 @@ __global__ __launch_bounds__(CT) void conv_bwd_gp_kernel(ConvDev p, const T* __r
     *(f32x4*)(pb + (size_t)K * p.n_ch) = ab;
 }
 
-// dx[u] = sum over m < K of w[K-1-m] * (sum of gp over the tokens m steps after u).
+// dx[u] = sum over m < K of w[K-1-m] * (sum of gp over the tokens m steps
+// after u). With D_m(u) that sum (D_0(u) = gp[u]), D_m(u) = D_{m-1}(u + 1) when
+// u's one successor is u + 1 (inside a node), so the workgroup walks its tokens
+// from the last down and, for such a token, shifts the sums of the token after
+// it: one new gp row per token, loaded one token ahead. Other tokens (a node's
+// last, the range's last) walk their successor lists. Either way every sum is
+// taken in the order of the successor lists, so the results do not depend on
+// the walk.
 template <int K, typename T>
 __global__ __launch_bounds__(CT) void conv_bwd_dx_kernel(ConvDev p, const T* __restrict__ gp,
                                                          T* __restrict__ dx) {
@@ -177,44 +197,55 @@ __global__ __launch_bounds__(CT) void conv_bwd_dx_kernel(ConvDev p, const T* __r
     if (c >= p.n_ch) return;
     float w[4][K], b[4];
     load_taps<K, T>(p, c, w, b);
-    const int t1 = min(p.n_tokens, (int)(blockIdx.x + 1) * CTOK);
+    const int u0 = blockIdx.x * CTOK, u1 = min(p.n_tokens, u0 + CTOK);
     auto g_at = [&](int t) { return ld4(gp + (int64_t)t * p.n_ch + c); };
     auto succ = [&](int t, int& lo, int& hi) {
         lo = max(p.next_off[t], 0);
         hi = min(p.next_off[t + 1], p.n_tokens);
     };
-    for (int u = blockIdx.x * CTOK; u < t1; ++u) {
-        f32x4 s[K];
+    f32x4 s[K];                       // D_m of the token after u (once `have`)
+    bool have = false;
+    f32x4 gn = g_at(u1 - 1);          // u0 < u1: the grid covers the tokens
+    for (int u = u1 - 1; u >= u0; --u) {
+        const f32x4 gu = gn;
+        if (u > u0) gn = g_at(u - 1);
+        int lo1, hi1;
+        succ(u, lo1, hi1);
+        if (have && hi1 - lo1 == 1 && p.next[lo1] == u + 1) {
 #pragma unroll
-        for (int m = 0; m < K; ++m) s[m] = (f32x4){};
-        s[0] = g_at(u);
-        if constexpr (K > 1) {
-            int lo1, hi1;
-            succ(u, lo1, hi1);
-            for (int a = lo1; a < hi1; ++a) {
-                const int ta = p.next[a];
-                if (ta < 0 || ta >= p.n_tokens) continue;
-                s[1] += g_at(ta);
-                if constexpr (K > 2) {
-                    int lo2, hi2;
-                    succ(ta, lo2, hi2);
-                    for (int bb = lo2; bb < hi2; ++bb) {
-                        const int tb = p.next[bb];
-                        if (tb < 0 || tb >= p.n_tokens) continue;
-                        s[2] += g_at(tb);
-                        if constexpr (K > 3) {
-                            int lo3, hi3;
-                            succ(tb, lo3, hi3);
-                            for (int cc = lo3; cc < hi3; ++cc) {
-                                const int tc = p.next[cc];
-                                if (tc < 0 || tc >= p.n_tokens) continue;
-                                s[3] += g_at(tc);
+            for (int m = K - 1; m >= 1; --m) s[m] = s[m - 1];
+            s[0] = gu;
+        } else {
+#pragma unroll
+            for (int m = 0; m < K; ++m) s[m] = (f32x4){};
+            s[0] = gu;
+            if constexpr (K > 1) {
+                for (int a = lo1; a < hi1; ++a) {
+                    const int ta = p.next[a];
+                    if (ta < 0 || ta >= p.n_tokens) continue;
+                    s[1] += g_at(ta);
+                    if constexpr (K > 2) {
+                        int lo2, hi2;
+                        succ(ta, lo2, hi2);
+                        for (int bb = lo2; bb < hi2; ++bb) {
+                            const int tb = p.next[bb];
+                            if (tb < 0 || tb >= p.n_tokens) continue;
+                            s[2] += g_at(tb);
+                            if constexpr (K > 3) {
+                                int lo3, hi3;
+                                succ(tb, lo3, hi3);
+                                for (int cc = lo3; cc < hi3; ++cc) {
+                                    const int tc = p.next[cc];
+                                    if (tc < 0 || tc >= p.n_tokens) continue;
+                                    s[3] += g_at(tc);
+                                }
                             }
                         }
                     }
                 }
             }
         }
+        have = true;
         f32x4 o = {};
 #pragma unroll
         for (int m = 0; m < K; ++m)
