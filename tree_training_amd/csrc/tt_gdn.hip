@@ -35,13 +35,14 @@ namespace {
 struct PrepLds {
     float Q[GC * RS];     // q^ * scale; v once A is done
     float K[GC * RS];
-    float R[4][GC * RR];  // partial products: A (waves 0, 1), k^ k^T (waves 2, 3); then T's 16 x 16 blocks
+    float R[8 * 16 * 17]; // q^ k^T at 0 and k^ k^T at GC * RR (rows of RR); then T's 16 x 16 blocks
     float N[GC * MS];     // N = -strictly_lower(beta k^ k^T * D)
     float Tm[GC * MS];    // I + N, then T = (I - N)^-1
     float G[GC];
     float beta[GC];
     float bg[GC];         // beta e^G
 };
+static_assert(2 * GC * RR <= 8 * 16 * 17, "the two 32 x 32 partial products fit the inverse's scratch");
 
 // q^ k^T and k^ k^T on fp32 MFMA (waves 0-1 and 2-3, each half of the
 // 128-deep contraction), the inverse T on the vector ALUs, then U and W on
@@ -77,23 +78,30 @@ __global__ __launch_bounds__(GT) void gdn_prep_kernel(GdnDev p, float* __restric
         }
     }
     __syncthreads();
-    {
+    {   // the odd wave of each pair stores its half of the contraction, the
+        // even one adds its own in place (two 32 x 32 buffers, not four)
         const float* X = wave < 2 ? L.Q : L.K;
         const int q0 = 2 * (wave & 1);
         f32x16 acc = quarter_nt(X, L.K, 1.0f, col, half, q0, (f32x16){});
         acc = quarter_nt(X, L.K, 1.0f, col, half, q0 + 1, acc);
-        put_partial(L.R[wave], acc, col, half);
+        float* Rw = L.R + (wave >> 1) * GC * RR;
+        if (wave & 1) put_partial(Rw, acc, col, half);
+        __syncthreads();
+        if constexpr (!TRUNC)   // Q's readers are done
+            tile_in((const TIn*)p.v + (int64_t)start * p.v_st + (int64_t)h * p.v_sh, p.v_st, len, L.Q);
+        if (!(wave & 1)) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) Rw[acc_row(r, half) * RR + col] += acc[r];
+        }
     }
     __syncthreads();
-    if constexpr (!TRUNC)   // Q's readers are done
-        tile_in((const TIn*)p.v + (int64_t)start * p.v_st + (int64_t)h * p.v_sh, p.v_st, len, L.Q);
 
     // A = lower_incl(q^ k^T * D), N = -strictly_lower(beta k^ k^T * D).
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int pi = t + GT * u, i = pi >> 5, j = pi & 31;
-        const float dqk = L.R[0][i * RR + j] + L.R[1][i * RR + j];
-        const float dkk = L.R[2][i * RR + j] + L.R[3][i * RR + j];
+        const float dqk = L.R[i * RR + j];
+        const float dkk = L.R[GC * RR + i * RR + j];
         const float dec = j <= i ? expf(L.G[i] - L.G[j]) : 0.0f;
         const float nij = j < i ? -L.beta[i] * dkk * dec : 0.0f;
         out[kWsA + i * GC + j] = dqk * dec;
@@ -114,7 +122,7 @@ __global__ __launch_bounds__(GT) void gdn_prep_kernel(GdnDev p, float* __restric
     {
         constexpr int BS = 17;                                   // row stride of the 16 x 16 blocks
         constexpr int B16 = 16 * BS;
-        float* sc = &L.R[0][0];
+        float* sc = L.R;
         const int blk = t >> 7, u = t & 127, bi = u >> 3, bj = 2 * (u & 7), o = 16 * blk;
         // block blk: P buffers at pb, pb + B16; T buffers at pb + 2 B16, pb + 3 B16
         const int pb = blk * 4 * B16, tb = pb + 2 * B16;
