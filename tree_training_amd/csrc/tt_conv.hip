@@ -21,7 +21,7 @@ namespace {
 
 constexpr int CT = 256;              // threads per workgroup
 constexpr int CCH = 4 * CT;          // channels per workgroup
-constexpr int CTOK = 32;             // tokens per workgroup (forward, dx)
+constexpr int CTOK = 64;             // tokens per workgroup (forward, dx)
 constexpr int CTOK_W = 64;           // tokens per workgroup (gp + weight-gradient partials)
 
 template <typename T>
