@@ -22,7 +22,7 @@ namespace {
 constexpr int CT = 256;              // threads per workgroup
 constexpr int CCH = 4 * CT;          // channels per workgroup
 constexpr int CTOK = 64;             // tokens per workgroup (forward, dx)
-constexpr int CTOK_W = 64;           // tokens per workgroup (gp + weight-gradient partials)
+constexpr int CTOK_W = 128;          // tokens per workgroup (gp + weight-gradient partials)
 
 template <typename T>
 __device__ __forceinline__ f32x4 ld4(const T* p) {
