@@ -133,7 +133,12 @@ def attn_backward(q, k, v, plan: KeyPlan, scale: float, o, lse, d_o, k_past=None
     dq = torch.empty((pb.N, pb.Hq, pb.D), dtype=pb.dtype, device=dev)
     dk = torch.empty((pb.N, pb.Hkv, pb.D), dtype=pb.dtype, device=dev)
     dv = torch.empty((pb.N, pb.Hkv, pb.D), dtype=pb.dtype, device=dev)
-    ws_bytes = lib().tt_attn_bwd_workspace_bytes(ctypes.byref(pb.s))
+    # the workspace layout depends on the parts of a call (every part at once
+    # runs the one-pass backward): size it for the largest of the calls
+    ws_bytes = 0
+    for part in parts:
+        pb.s.bwd_parts = part | det
+        ws_bytes = max(ws_bytes, lib().tt_attn_bwd_workspace_bytes(ctypes.byref(pb.s)))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     acc_k = acc_v = None
     if gate_acc is not None and pb.n_past > 0:

@@ -31,8 +31,8 @@ __global__ __launch_bounds__(256) void bwd_delta_bf16_kernel(AttnDev a, BwdDev b
 // backward: dQ (query-major, same tiling and pipeline as the forward)
 // ----------------------------------------------------------------------------
 struct DqStage {
-    bf16 K[TT_BK * ROW];
-    bf16 V[TT_BK * ROW];
+    bf16 K[TT_BK * ROWX];    // read as rows (S^T) and transposed (dQ^T): swizzled
+    bf16 V[TT_BK * ROW_R];   // read as rows only (dP^T)
     int lo[TT_BK];
     int hi[TT_BK];
 };
@@ -96,8 +96,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         it0 = cnt * (int)blockIdx.y / bw.n_split;
         it1 = cnt * ((int)blockIdx.y + 1) / bw.n_split;
     }
-    KvTileStager stg;
+    KvTileStager<SWZ, ROW_R> stg;
     Bounds nb;
+    const RowOffsX kro = row_offsx(col, half);   // this lane's key row in the K tile (either half)
+    const TrOffsX tro = tr_offsx(lane);
     if (it1 > it0) {
         stg.begin(a, list[it0] >> 1, g);
         fetch_bounds(a, list[it0] >> 1, nb);
@@ -124,11 +126,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int b = 0; b < 2; ++b) {
             if (!((run >> b) & 1)) continue;
             f32x16 sh = (f32x16){}, dph = (f32x16){};
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                sh = mfma32(read_row_operand(S.K, 32 * b + col, 16 * t + 8 * half), qa[t], sh);
-                dph = mfma32(read_row_operand(S.V, 32 * b + col, 16 * t + 8 * half), da[t], dph);
-            }
+            static_for<8>([&](auto tt) {
+                constexpr int t = decltype(tt)::value;
+                sh = mfma32(read_rowx<t>(S.K + 32 * b * ROWX, kro), qa[t], sh);
+                dph = mfma32(read_row_operand<ROW_R>(S.V, 32 * b + col, 16 * t + 8 * half), da[t], dph);
+            });
             if (!full) mask_half(sh, S.lo + 32 * b, S.hi + 32 * b, qi, half);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -142,7 +144,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                         sh[r0 + 6], sh[r0 + 7]);
 #pragma unroll
                 for (int db = 0; db < 4; ++db)
-                    dq[db] = mfma32(read_tr_operand(S.K, 16 * (2 * b + s2), 32 * db, lane), pk, dq[db]);
+                    dq[db] = mfma32(read_trx(S.K, tro, 16 * (2 * b + s2), 32 * db), pk, dq[db]);
             }
         }
     }
@@ -236,8 +238,8 @@ struct QBlockStager {
     }
     __device__ __forceinline__ void commit(const AttnDev& a, const BwdDev& bw, KvStage& S) {
         if (q0 + TT_BQB <= a.n_q) {
-            store_rows<TT_BQB, true>(q, threadIdx.x, S.Q);
-            store_rows<TT_BQB, true>(d, threadIdx.x, S.Dn);
+            store_rows<TT_BQB, SWZ>(q, threadIdx.x, S.Q);
+            store_rows<TT_BQB, SWZ>(d, threadIdx.x, S.Dn);
         } else {
             const int dc = (threadIdx.x & 15) * 8, r0 = threadIdx.x >> 4;
             for (int i = 0; i < TT_BQB / 16; ++i) {
@@ -262,7 +264,7 @@ struct QBlockStager {
 #endif
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAVES_PER_EU, TT_DKDV_WAVES_PER_EU))) void bwd_dkdv_bf16_kernel(AttnDev a, BwdDev bw) {
     __shared__ __attribute__((aligned(16))) KvStage st[2];
-    __shared__ __attribute__((aligned(16))) bf16 Vs[TT_BKB * ROW];   // V rows of the item's keys
+    __shared__ __attribute__((aligned(16))) bf16 Vs[TT_BKB * ROW_R];   // V rows of the item's keys (row reads only)
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int col = lane & 31, half = lane >> 5;
@@ -305,7 +307,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
                 auto vrow = [&](int r) { return key_row(a, min(k0 + r, a.n_keys - 1), g, true); };
                 fetch_rows(vr, threadIdx.x, vrow);
             }
-            store_rows(vr, threadIdx.x, Vs);
+            store_rows<TT_BKB, ROW_R>(vr, threadIdx.x, Vs);
         }
         const int kk = kb * TT_BKB + wave * 32 + col;   // this lane's key (MFMA column)
         int lo = 0, hi = 0;
@@ -358,7 +360,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
             static_for<8>([&](auto tt) {
                 constexpr int t = decltype(tt)::value;
                 sc = mfma32(read_rowx<t>(S.Q, qro), kbv[t], sc);
-                dp = mfma32(read_rowx<t>(S.Dn, qro), read_row_operand(Vs, wave * 32 + col, 16 * t + 8 * half), dp);
+                dp = mfma32(read_rowx<t>(S.Dn, qro), read_row_operand<ROW_R>(Vs, wave * 32 + col, 16 * t + 8 * half), dp);
             });
             // P = exp(S*scale - lse), dS = P (dP - delta); on the few steps where
             // some key of the wave is invisible to some query, those entries are

@@ -57,7 +57,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         it0 = cnt * (int)blockIdx.y / sp.n;
         it1 = cnt * ((int)blockIdx.y + 1) / sp.n;
     }
-    KvTileStager stg;
+    KvTileStager<ROW, ROW> stg;
     Bounds nb;
     if (it1 > it0) {
         const int kt0 = __builtin_amdgcn_readfirstlane(list[it0] >> 1);
@@ -84,14 +84,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             bf16x8 kop[16];
             static_for<AH>([&](auto i) {
                 constexpr int n = decltype(i)::value;
-                kop[n] = read_row_operand(S.K, 32 * (n >> 3) + col, 16 * (n & 7) + 8 * half);
+                kop[n] = read_row_operand<ROW>(S.K, 32 * (n >> 3) + col, 16 * (n & 7) + 8 * half);
             });
             s[0] = (f32x16){};
             s[1] = (f32x16){};
             static_for<16>([&](auto i) {
                 constexpr int n = decltype(i)::value;
                 if constexpr (n + AH < 16)
-                    kop[n + AH] = read_row_operand(S.K, 32 * ((n + AH) >> 3) + col, 16 * ((n + AH) & 7) + 8 * half);
+                    kop[n + AH] = read_row_operand<ROW>(S.K, 32 * ((n + AH) >> 3) + col, 16 * ((n + AH) & 7) + 8 * half);
                 __builtin_amdgcn_sched_barrier(0);
                 s[n >> 3] = mfma32(kop[n], qa[n & 7], s[n >> 3]);
                 __builtin_amdgcn_sched_barrier(0);
@@ -136,7 +136,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             ps1 = sum4_bf16(pk, 4, ps1);
 #pragma unroll
             for (int db = 0; db < 4; ++db)
-                o[db] = mfma32(read_tr_operand(S.V, 16 * stp, 32 * db, lane), pk, o[db]);
+                o[db] = mfma32(read_tr_operand<ROW>(S.V, 16 * stp, 32 * db, lane), pk, o[db]);
         }
         l_run += ps0 + ps1;
     }

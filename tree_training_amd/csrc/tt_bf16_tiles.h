@@ -43,13 +43,28 @@ typedef __bf16 bf16;
 
 constexpr int D = 128;
 
-// LDS tiles hold tokens in their natural [token][d] order, rows padded to 288
-// bytes. Each thread loads its slice of the next tile into registers while
-// the current one computes, then stores it. The padding puts consecutive rows
-// 8 banks apart, so 16-byte row reads, transposed reads and the stores all run
-// in at most two LDS passes.
+// LDS tiles hold tokens in their natural [token][d] order. Each thread loads
+// its slice of the next tile into registers while the current one computes,
+// then stores it. Row padding sets the bank pattern (64 banks x 4 bytes; a
+// 16-byte read serves 16 lanes per pass, a transposed 8-byte read 32):
+//   ROW_R = 272-byte rows for tiles read only as rows: 16 consecutive rows
+//           start on 16 different 16-byte bank groups, so a row operand read
+//           (16 lanes = 16 rows, one chunk) runs in one pass;
+//   ROW_T = 320-byte rows for tiles read only transposed: the 4 rows x 4
+//           chunks that 32 lanes of ds_read_b64_tr_b16 touch fall on 16
+//           different bank groups (4 r + c mod 16);
+//   tiles read both ways use the XOR-swizzled 320-byte layout below (ROWX);
+//   ROW = 288-byte rows (the forward's K and V tiles): row and transposed
+//           reads both run in two passes.
+// Stores (16 lanes = one whole row) are conflict-free in every layout. The
+// conflict-free layouts took the dQ and dK/dV passes' bank conflicts to zero
+// without changing their time, and made the forward 5 % slower than ROW: the
+// kernels are not bound by LDS bandwidth.
+constexpr int ROW_R = D + 8;
+constexpr int ROW_T = D + 32;
 constexpr int ROW = D + 16;
-__device__ __forceinline__ int tile_off(int r, int d) { return r * ROW + d; }
+template <int S>
+__device__ __forceinline__ int tile_off(int r, int d) { return r * S + d; }
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
@@ -92,16 +107,18 @@ __device__ __forceinline__ bf16x4 ds_read_tr(const bf16* p) {
 // X[r0 + kappa(e)][dbase + (l & 31)], kappa(e) = 8*(e/4) + 4*(l>>5) + (e%4) —
 // the accumulator row order, so it pairs with probabilities taken straight
 // from a score accumulator.
+template <int S>
 __device__ __forceinline__ bf16x8 read_tr_operand(const bf16* X, int r0, int dbase, int lane) {
     const int j = lane & 15, grp = lane >> 4;
     const int d = dbase + 16 * (grp & 1) + 4 * (j & 3);
     const int r = r0 + 4 * (grp >> 1) + (j >> 2);
-    return cat44(ds_read_tr(X + tile_off(r, d)), ds_read_tr(X + tile_off(r + 8, d)));
+    return cat44(ds_read_tr(X + tile_off<S>(r, d)), ds_read_tr(X + tile_off<S>(r + 8, d)));
 }
 
 // MFMA operand "row = token, k = 16 head dims": X[r][d0 .. d0+7], d0 % 8 == 0.
+template <int S>
 __device__ __forceinline__ bf16x8 read_row_operand(const bf16* X, int r, int d0) {
-    return *(const bf16x8*)(X + tile_off(r, d0));
+    return *(const bf16x8*)(X + tile_off<S>(r, d0));
 }
 
 // Swizzled layout for tiles read both row-wise and transposed many times
@@ -185,12 +202,19 @@ __device__ __forceinline__ void fetch_rows_buf(RowRegs<NROWS>& r, int tid, const
         r.x[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vo, (int)(16 * i * stb), 0));
 }
 
-template <int NROWS, bool SWZ = false>
+// Layout tag of the XOR-swizzled tiles (tile_offx) for store_rows and
+// KvTileStager; every other layout is given by its row stride.
+constexpr int SWZ = -1;
+template <int S>
+__device__ __forceinline__ int tile_at(int r, int d) { return S == SWZ ? tile_offx(r, d) : tile_off<S>(r, d); }
+
+// Stores staged rows in a tile of row stride S elements, or (S == SWZ) the
+// XOR-swizzled layout.
+template <int NROWS, int S>
 __device__ __forceinline__ void store_rows(const RowRegs<NROWS>& r, int tid, bf16* X) {
     const int dc = (tid & 15) * 8, r0 = tid >> 4;
 #pragma unroll
-    for (int i = 0; i < NROWS / 16; ++i)
-        *(bf16x8*)(X + (SWZ ? tile_offx(r0 + 16 * i, dc) : tile_off(r0 + 16 * i, dc))) = r.x[i];
+    for (int i = 0; i < NROWS / 16; ++i) *(bf16x8*)(X + tile_at<S>(r0 + 16 * i, dc)) = r.x[i];
 }
 
 __device__ __forceinline__ const bf16* key_row(const AttnDev& a, int kk, int g, bool isv) {
@@ -216,8 +240,10 @@ __device__ __forceinline__ void fetch_bounds(const AttnDev& a, int kt, Bounds& r
 }
 
 // Staging of the K and V rows of key tile kt (rows past the last key alias
-// it; their empty bounds mask them). begin() starts the loads for a
-// stage; commit() makes them resident in that stage (before the barrier).
+// it; their empty bounds mask them) into tiles of row strides KS and VS
+// (SWZ: swizzled). begin() starts the loads for a stage; commit() makes them
+// resident in that stage (before the barrier).
+template <int KS, int VS>
 struct KvTileStager {
     RowRegs<TT_BK> k, v;
     int k0;
@@ -245,8 +271,8 @@ struct KvTileStager {
     }
     __device__ __forceinline__ void commit(const AttnDev& a, int g, bf16* K, bf16* V) {
         if (!direct) {
-            store_rows(k, threadIdx.x, K);
-            store_rows(v, threadIdx.x, V);
+            store_rows<TT_BK, KS>(k, threadIdx.x, K);
+            store_rows<TT_BK, VS>(v, threadIdx.x, V);
             return;
         }
         // At most two tiles per launch take this path: copied row by row,
@@ -254,8 +280,8 @@ struct KvTileStager {
         const int dc = (threadIdx.x & 15) * 8, r0 = threadIdx.x >> 4;
         for (int i = 0; i < TT_BK / 16; ++i) {
             const int r = r0 + 16 * i, kk = min(k0 + r, a.n_keys - 1);
-            *(bf16x8*)(K + tile_off(r, dc)) = *(const bf16x8*)(key_row(a, kk, g, false) + dc);
-            *(bf16x8*)(V + tile_off(r, dc)) = *(const bf16x8*)(key_row(a, kk, g, true) + dc);
+            *(bf16x8*)(K + tile_at<KS>(r, dc)) = *(const bf16x8*)(key_row(a, kk, g, false) + dc);
+            *(bf16x8*)(V + tile_at<VS>(r, dc)) = *(const bf16x8*)(key_row(a, kk, g, true) + dc);
         }
     }
 };
