@@ -295,7 +295,7 @@ def test_gdn_level_offsets_validation():
     p = _gdn_problem(n_chunks=2)                      # fewer chunks than nodes
     assert lib.tt_gdn_tree_fwd(ctypes.byref(p), V, V, V, 1 << 30, None) == _lib.TT_E_ARG
     # per (chunk, v head): W, U [32 x 128], A, T [32 x 32], G [32] floats
-    assert lib.tt_gdn_workspace_bytes(ctypes.byref(_gdn_problem())) == 5 * 32 * (2 * 32 * 128 + 2 * 32 * 32 + 32) * 4
+    assert lib.tt_gdn_workspace_bytes(ctypes.byref(_gdn_problem())) == 5 * 32 * (2 * 32 * 128 + 2 * 32 * 32 + 2 * 32) * 4
 
 
 def test_gdn_bwd_validation():
@@ -303,7 +303,7 @@ def test_gdn_bwd_validation():
     V = ctypes.c_void_p(16)
     DO = _lib.TTTensor(16, 32 * 128, 128)
     p = _gdn_problem(node_child_off=16, node_child=16)
-    per_chunk = (2 * 32 * 128 + 2 * 32 * 32 + 32) + 2 * 128 * 128 + 5 * 32 * 128 + 1
+    per_chunk = (2 * 32 * 128 + 2 * 32 * 32 + 2 * 32) + 2 * 128 * 128 + 5 * 32 * 128 + 1
     want = (5 * 32 * per_chunk + 3 * 32 * 2 * 128 * 128) * 4
     assert lib.tt_gdn_bwd_workspace_bytes(ctypes.byref(p)) == want
     DQ = _lib.TTTensor(16, 16 * 128, 128)
@@ -348,7 +348,7 @@ def test_gdn_saved_validation():
     DO = _lib.TTTensor(16, 32 * 128, 128)
     p = _gdn_problem(node_child_off=16, node_child=16)
     # per (chunk, v head): prep terms, initial state [128 x 128], V' [32 x 128]
-    saved = 5 * 32 * ((2 * 32 * 128 + 2 * 32 * 32 + 32) + 128 * 128 + 32 * 128) * 4
+    saved = 5 * 32 * ((2 * 32 * 128 + 2 * 32 * 32 + 2 * 32) + 128 * 128 + 32 * 128) * 4
     assert lib.tt_gdn_saved_bytes(ctypes.byref(p)) == saved
     # scratch: dS [128 x 128], dV', X, dW, dK~ [32 x 128], <S, dS> per chunk; dS at entry per node
     scratch = (5 * 32 * (128 * 128 + 4 * 32 * 128 + 1) + 3 * 32 * 128 * 128) * 4

@@ -111,6 +111,26 @@ def test_gdn_16k_tree_per_path_equivalence():
         assert np.array_equal(st_p[-1], st[leaf])
 
 
+def test_gdn_agent16k_two_heads_matches_oracle():
+    """Full c5 topology (the agent tree: 16,318 tokens, 54 nodes of 64-512
+    tokens, root-to-leaf paths of up to 76 chunks), realistic gates, fp32, one
+    q/k head shared by two v heads, against the float64 exact-rule oracle
+    (oracle.gdn.gdn_tree mode="exact": the token recurrence continued from the
+    parent's final state). Outputs and node states: < 1e-5. Head 0's gates
+    decay hard (the cumulative decay reaches -570 within one 32-token chunk),
+    where a one-float prefix sum would put ~3e-5 relative error on the late
+    tokens' decays and so on the states; the kernels carry it in two floats."""
+    lens, par = agent_tree(0)
+    T = sum(lens)
+    q, k, v, g, beta = _inputs(T, 1, 2, 17, realistic_gates=True)
+    print(f"gdn exact fwd 16k: T={T} nodes={len(lens)}", flush=True)
+    o, st = _run(q, k, v, g, beta, lens, par, torch.float32)
+    o_ref, st_ref = ogdn.gdn_tree(q, k, v, g, beta, lens, par, mode="exact")
+    print(f"  o {_rel(o, o_ref):.2e}  states {_rel(st, st_ref):.2e}", flush=True)
+    assert _rel(o, o_ref) < 1e-5, _rel(o, o_ref)
+    assert _rel(st, st_ref) < 1e-5, _rel(st, st_ref)
+
+
 def _run_bwd(q, k, v, g, beta, d_o, lens, par, dtype):
     dev = torch.device("cuda", 0)
     t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)

@@ -39,6 +39,7 @@ struct PrepLds {
     float N[GC * MS];     // N = -strictly_lower(beta k^ k^T * D)
     float Tm[GC * MS];    // I + N, then T = (I - N)^-1
     float G[GC];
+    float Glo[GC];
     float beta[GC];
     float bg[GC];         // beta e^G
 };
@@ -60,21 +61,28 @@ __global__ __launch_bounds__(GT) void gdn_prep_kernel(GdnDev p, float* __restric
 
     load_chunk_rows<TIn>(p, start, len, h, L.Q, L.K, nullptr);
     if (wave == 0) {
-        // cumulative decay over the chunk (lanes 0..31; padded rows add 0)
+        // cumulative decay over the chunk (lanes 0..31; padded rows add 0),
+        // each step's rounding error (two-sum) carried in lo
         const bool valid = lane < len;
         const int64_t tok = start + lane;
-        float gv = valid ? p.g[tok * p.g_st + h] : 0.0f;
+        float gv = valid ? p.g[tok * p.g_st + h] : 0.0f, lo = 0.0f;
         const float bv = valid ? p.beta[tok * p.b_st + h] : 0.0f;
 #pragma unroll
         for (int o = 1; o < GC; o <<= 1) {
-            const float up = __shfl_up(gv, o, GC);
-            if ((lane & (GC - 1)) >= o) gv += up;
+            const float up = __shfl_up(gv, o, GC), up_lo = __shfl_up(lo, o, GC);
+            if ((lane & (GC - 1)) >= o) {
+                const float sum = gv + up, bp = sum - gv;
+                lo += up_lo + ((gv - (sum - bp)) + (up - bp));
+                gv = sum;
+            }
         }
         if (lane < GC) {
             L.G[lane] = gv;
+            L.Glo[lane] = lo;
             L.beta[lane] = bv;
-            L.bg[lane] = bv * expf(gv);
+            L.bg[lane] = bv * expf(gv + lo);
             out[kWsG + lane] = gv;
+            out[kWsGlo + lane] = lo;
         }
     }
     __syncthreads();
@@ -102,7 +110,7 @@ __global__ __launch_bounds__(GT) void gdn_prep_kernel(GdnDev p, float* __restric
         const int pi = t + GT * u, i = pi >> 5, j = pi & 31;
         const float dqk = L.R[i * RR + j];
         const float dkk = L.R[GC * RR + i * RR + j];
-        const float dec = j <= i ? expf(L.G[i] - L.G[j]) : 0.0f;
+        const float dec = j <= i ? expf(gdiff(L.G[i], L.Glo[i], L.G[j], L.Glo[j])) : 0.0f;
         const float nij = j < i ? -L.beta[i] * dkk * dec : 0.0f;
         out[kWsA + i * GC + j] = dqk * dec;
         L.N[i * MS + j] = nij;
@@ -228,7 +236,7 @@ struct ScanAhead {
     Vec q[NV], k[NV];
     f32x4 w[4];
     float a[4];
-    float gi, gl, gt;
+    float gi, gl, gt, gil, gll;   // G_i, G_L, G_t; low parts of G_i, G_L
     f32x4 x[2];
 };
 
@@ -265,6 +273,8 @@ __device__ __forceinline__ void scan_fetch_rows(const GdnDev& p, const float* cw
     x.gi = cw[kWsG + i];
     x.gl = cw[kWsG + GC - 1];
     x.gt = cw[kWsG + (t & (GC - 1))];
+    x.gil = cw[kWsGlo + i];
+    x.gll = cw[kWsGlo + GC - 1];
 }
 
 // Writes a fetched chunk to LDS: Q = q^ * scale * qmul_i, K = k^ * kmul_i
@@ -294,7 +304,7 @@ __device__ __forceinline__ void scan_stage_rows(const GdnDev& p, const ScanAhead
     sk = row8_sum(sk);
     const float fq = (p.l2 ? 1.0f / sqrtf(sq + 1e-6f) : 1.0f) * p.scale;
     const float fk = p.l2 ? 1.0f / sqrtf(sk + 1e-6f) : 1.0f;
-    const float eq = QMUL ? expf(x.gi) : 1.0f, ek = expf(x.gl - x.gi);
+    const float eq = QMUL ? expf(x.gi) : 1.0f, ek = expf(gdiff(x.gl, x.gll, x.gi, x.gil));
 #pragma unroll
     for (int e = 0; e < 16; e += 4) {
         f32x4 qo, ko;
@@ -902,6 +912,7 @@ struct ChunkGradLds {
     float M3[GC * MS];    // dA * A + dN * N (for the column sums of dG)
     float R[4][GC * RR];  // per-wave partial 32 x 32 products (contraction split over the waves)
     float G[GC];
+    float Glo[GC];
     float B[GC];
     float Grow[GC];
     float Crow[GC];
@@ -958,6 +969,7 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
         __syncthreads();   // the previous head's readers are done
         if (t < GC) {
             L.G[t] = cw[kWsG + t];
+            L.Glo[t] = cw[kWsGlo + t];
             L.B[t] = t < len ? p.beta[(int64_t)(start + t) * p.b_st + h] : 0.0f;
         }
         tile_in(d_o + (int64_t)start * do_st + (int64_t)h * do_sh, do_st, len, L.P1);
@@ -973,6 +985,7 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
         put_partial(L.R[wave], quarter_nt(L.P1, L.P2, 1.0f, col, half, wave, (f32x16){}), col, half);
         __syncthreads();
         const float gi = L.G[i], gl = L.G[GC - 1], egi = expf(gi), bi = L.B[i];
+        const float gil = L.Glo[i], gll = L.Glo[GC - 1];
         float dgp = 0.0f, dbp = 0.0f, cp = 0.0f;   // this thread's share of row i's dG, dbeta, c
 
         // dG from A = (q^ k^T) * D, then dP = dA * D (j <= i).
@@ -984,7 +997,7 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
             const float pa = dae * L.M1[i * MS + j];
             dgp += pa;
             L.M3[i * MS + j] = pa;
-            L.M1[i * MS + j] = j <= i ? dae * expf(gi - L.G[j]) : 0.0f;
+            L.M1[i * MS + j] = j <= i ? dae * expf(gdiff(gi, gil, L.G[j], L.Glo[j])) : 0.0f;
         }
         // O's state term e^G q^ S: dq^ += e^G X, dG += e^G q^ . X.
         {
@@ -1022,7 +1035,7 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
             // dT = dV' (beta v)^T + dW (beta e^G k^)^T (partials per wave); dBv =
             // T^T dV', dBk = T^T dW (columns of this wave).
             {
-                const float bj = L.B[col], bgj = bj * expf(L.G[col]);
+                const float bj = L.B[col], bgj = bj * expf(L.G[col] + L.Glo[col]);
                 f32x16 tp = quarter_nt(L.P1, L.P3, bj, col, half, wave, (f32x16){});
                 tp = quarter_nt(L.P2, L.Ks, bgj, col, half, wave, tp);
                 put_partial(L.R[wave], tp, col, half);
@@ -1095,7 +1108,7 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
                     for (int m = 0; m < GC; ++m) dn = fmaf(L.P3[i * MS + m], L.M2[j * MS + m], dn);
                     ev[e] = 0.0f;
                     if (j < i) {
-                        const float dd = expf(gi - L.G[j]), kk = L.KK[i * MS + j];
+                        const float dd = expf(gdiff(gi, gil, L.G[j], L.Glo[j])), kk = L.KK[i * MS + j];
                         const float pa = dn * (-bi * kk * dd);
                         dbp = fmaf(dn, -kk * dd, dbp);
                         ev[e] = -dn * bi * dd;
@@ -1130,7 +1143,7 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
         // The output state S_out = e^{G_L} S + (e^{G_L - G} k^)^T V': dk^ and dG.
         {
             const float* kr = dkto + chn * GC * GD + i * GD;
-            const float ed = expf(gl - gi);
+            const float ed = expf(gdiff(gl, gll, gi, gil));
             float kt = 0.0f;
 #pragma unroll
             for (int m = 0; m < 4; ++m) {

@@ -16,9 +16,21 @@ constexpr int MS = GC + 4;        // row stride of [GC x GC] matrices
 constexpr int RR = GC + 1;        // row stride of per-wave 32 x 32 partial products
 
 // Workspace per (chunk, v head), floats: W [GC][GD], U [GC][GD], A [GC][GC],
-// T [GC][GC] (the inverse, for the backward), G [GC].
+// T [GC][GC] (the inverse, for the backward), G [GC] and its low part Glo [GC].
 constexpr size_t kWsW = 0, kWsU = GC * GD, kWsA = 2 * GC * GD, kWsT = kWsA + GC * GC, kWsG = kWsT + GC * GC;
-constexpr size_t kWsChunk = kWsG + GC;
+constexpr size_t kWsGlo = kWsG + GC;
+constexpr size_t kWsChunk = kWsGlo + GC;
+
+// The cumulative decay G of a chunk is kept as an unevaluated sum hi + lo,
+// lo holding the rounding errors of the prefix sum. A strongly decaying head
+// reaches |G| of several hundred within 32 tokens, where one float rounds
+// G by up to |G| 2^-24 (3e-5 at 500): every factor e^{G_i - G_j} of two
+// late tokens that is not negligible would carry that as a relative error.
+// With both parts the difference is exact up to its own final rounding
+// (hi_i - hi_j is exact whenever it is not large, Sterbenz).
+__device__ __forceinline__ float gdiff(float hi_i, float lo_i, float hi_j, float lo_j) {
+    return (hi_i - hi_j) + (lo_i - lo_j);
+}
 
 template <int I>
 struct IntC4 {
