@@ -45,9 +45,9 @@ enum {
     TT_BWD_DELTA = 1,   /* rowsum(dO * O) into the workspace */
     TT_BWD_DQ = 2,      /* dQ (reads the workspace) */
     TT_BWD_DKDV = 4,    /* dK, dV and gateway accumulation (reads the workspace) */
-    TT_BWD_DETERMINISTIC = 8   /* modifier, OR'ed with the parts (alone: every part): bf16 dK/dV and
-                                  gateway sums in a fixed order, so repeated calls on the same inputs
-                                  are bitwise equal (more workspace; see tt_attn_bwd) */
+    TT_BWD_DETERMINISTIC = 8   /* modifier, OR'ed with the parts (alone: every part): dK/dV and
+                                  gateway sums in a fixed order (bf16 and fp32), so repeated calls on
+                                  the same inputs are bitwise equal (more workspace; see tt_attn_bwd) */
 };
 
 /* Device-side status bits written by tt_meta_build / tt_keys_build. */

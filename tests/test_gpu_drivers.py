@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from oracle.attention import max_rel
-from oracle.model_path import dense_leaf_logits, sequential_param_grads
+from oracle.model_path import dense_leaf_logits, hybrid_param_grads, sequential_param_grads
 from tests.conftest import forest_from_spec, load_golden, make_qwen3
 
 pytestmark = pytest.mark.gpu
@@ -148,6 +148,28 @@ def test_hybrid_chain_inherited_bias_equals_whole_tree():
     say(f"  inherited {r_inh:.3e} legacy {r_leg:.3e}")
     assert r_inh < 1e-5
     assert r_leg > 1e-3
+
+
+@pytest.mark.parametrize("tree,max_tokens", [("q1", 6), ("c1", 20), ("c1", 10)])
+def test_hybrid_legacy_bias_matches_literal_oracle(tree, max_tokens):
+    """legacy_gateway_bias=True reproduces the reference's own hybrid run, with
+    the literal gateway bias of tree_grad_hybrid.py:207: its fp32 parameter
+    gradients match the float64 restatement of that run
+    (oracle.model_path.hybrid_param_grads, legacy=True) to < 1e-5, on the Q1
+    chain too, where that run differs from the whole tree."""
+    from tree_training_amd.hybrid import tree_grad_hybrid
+    say(f"hybrid legacy bias vs literal oracle {tree} max_tokens={max_tokens}")
+    base = make_qwen3("tiny", layers=2)
+    ref_model = copy.deepcopy(base).double()
+    model = base.to(DEV)
+    roots, leaves = _tree(tree)
+    labels = _labels(leaves)
+    ref = hybrid_param_grads(ref_model, roots, labels, len(leaves), max_tokens, legacy=True)
+    new = _grads(model, lambda: tree_grad_hybrid(model, roots, _loss_fn(labels, len(leaves)), max_tokens,
+                                                 legacy_gateway_bias=True))
+    r = _max_rel_params(ref, new)
+    say(f"  max_rel {r:.3e}")
+    assert r < 1e-5, r
 
 
 def test_sequential_and_hybrid_bf16():

@@ -416,12 +416,14 @@ def test_attention_backward_parts(parts, dtype):
         check_close(name, ref, got, tol)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
 @pytest.mark.parametrize("case", ["long_prompt", "gateway_split", "gateway_split_parts"])
-def test_attention_deterministic_bf16(case):
-    """TT_BWD_DETERMINISTIC: keys whose query range is split over several
-    dK/dV work items (own keys of the long prompt; gateway keys seen by every
-    query) sum their partials in work-item order, so two backwards of the same
-    inputs are bitwise equal, and both match the fp64 oracle."""
+def test_attention_deterministic(case, dtype):
+    """TT_BWD_DETERMINISTIC, both dtypes: keys whose query range is split over
+    several dK/dV work items (own keys of the long prompt; gateway keys seen
+    by every query, added into the fp32 gateway sums) sum their partials in
+    work-item order, so two backwards of the same inputs are bitwise equal,
+    and both match the fp64 oracle (< 2e-2 bf16, < 1e-5 fp32)."""
     past_vis, parts = None, (0,)
     if case == "long_prompt":
         lens, par = CASES["long_prompt"]
@@ -430,13 +432,13 @@ def test_attention_deterministic_bf16(case):
         past_vis = [bool(x) for x in (np.random.default_rng(8).random(300) < 0.6)]
         if case == "gateway_split_parts":
             parts = (3, 4)
-    say(f"attention deterministic case={case} T={sum(lens)}")
-    runs = [_run(lens, par, torch.bfloat16, seed=21, past_vis=past_vis, parts=parts, deterministic=True)
+    say(f"attention deterministic case={case} dtype={dtype} T={sum(lens)}")
+    runs = [_run(lens, par, dtype, seed=21, past_vis=past_vis, parts=parts, deterministic=True)
             for _ in range(2)]
     for name, (ref, got) in runs[0].items():
         assert np.array_equal(got, runs[1][name][1]), f"{name}: two deterministic runs differ"
         if name != "lse":
-            check_close(name, ref, got, TOL[torch.bfloat16])
+            check_close(name, ref, got, TOL[dtype])
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])

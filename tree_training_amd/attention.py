@@ -121,7 +121,7 @@ def attn_backward(q, k, v, plan: KeyPlan, scale: float, o, lse, d_o, k_past=None
     added to ``gate_acc`` when given. ``parts``: the ``bwd_parts`` of one
     ``tt_attn_bwd`` call each, run in order (default: one call, every part).
     ``deterministic`` (default: ``torch.are_deterministic_algorithms_enabled()``)
-    adds TT_BWD_DETERMINISTIC: bitwise-repeatable bf16 dk/dv and gateway sums."""
+    adds TT_BWD_DETERMINISTIC: bitwise-repeatable dk/dv and gateway sums (both dtypes)."""
     if deterministic is None:
         deterministic = torch.are_deterministic_algorithms_enabled()
     det = TT_BWD_DETERMINISTIC if deterministic else 0
@@ -133,8 +133,9 @@ def attn_backward(q, k, v, plan: KeyPlan, scale: float, o, lse, d_o, k_past=None
     dq = torch.empty((pb.N, pb.Hq, pb.D), dtype=pb.dtype, device=dev)
     dk = torch.empty((pb.N, pb.Hkv, pb.D), dtype=pb.dtype, device=dev)
     dv = torch.empty((pb.N, pb.Hkv, pb.D), dtype=pb.dtype, device=dev)
-    # the workspace layout depends on the parts of a call (every part at once
-    # runs the one-pass backward): size it for the largest of the calls
+    # the workspace a call needs depends on its parts (the dQ pass's key-split
+    # partials, the deterministic slots of the dK/dV pass): size it for the
+    # largest of the calls
     ws_bytes = 0
     for part in parts:
         pb.s.bwd_parts = part | det

@@ -42,7 +42,7 @@ struct BwdDev {
     float* dk_slot;           // deterministic mode: [tt_det_slots, 128, hkv, 128] fp32, chunks >= 1
     float* dv_slot;           //   of split key tiles (null otherwise)
     int parts;                // OR of TT_BWD_DELTA / _DQ / _DKDV (never 0 here)
-    int det;                  // TT_BWD_DETERMINISTIC given (bf16: split tiles summed in chunk order)
+    int det;                  // TT_BWD_DETERMINISTIC given (split tiles summed in chunk order)
     float* dq_part;           // bf16 with tt_key_splits > 1: [splits, n_q, hq, 128] fp32 dQ partials
     int n_split;              // tt_key_splits of the problem (bf16), else 1
     int zero_in_dq;           // the dQ pass clears the split sums for the dK/dV pass of the same call
