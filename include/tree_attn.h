@@ -166,6 +166,8 @@ typedef struct tt_attn_problem {
     const int32_t* key_hi;
     const void* plan;       /* built by tt_plan_build for (key_lo, key_hi) */
     size_t plan_bytes;
+    int64_t det_slots;      /* tt_attn_bwd with TT_BWD_DETERMINISTIC: the partial-sum slots to reserve,
+                               from tt_attn_det_slots for the tree; 0: the bound that holds for any tree */
 } tt_attn_problem;
 
 /* o: [n_q, Hq, head_dim] contiguous, problem dtype; lse: [Hq, n_q] float32
@@ -202,10 +204,28 @@ int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* ws, size_t 
  * stores its partial sums in a slot of its own and one pass adds them in
  * work-item order: no atomics, bitwise-repeatable dk, dv and gateway sums.
  * The workspace (tt_attn_bwd_workspace_bytes of the problem with the bit set)
- * then grows by 2 * n_kb * floor((n_q - 1) / W) * 128 * Hkv * 512 bytes, n_kb
- * = ceil((n_past + n_q) / 128) (about 4x the bf16 workspace at n_q = 16K).
+ * then grows by 2 * S * 128 * Hkv * 512 bytes: S = det_slots, the exact count
+ * of such later work items that tt_attn_det_slots computes on the host from
+ * the topology (46 on the 16K agent tree), or with det_slots = 0 the bound
+ * n_kb * floor((n_q - 1) / W), n_kb = ceil((n_past + n_q) / 128) (about 4x
+ * the bf16 workspace at n_q = 16K). A det_slots below what the plan needs
+ * never writes past the workspace: the key tiles whose slots do not fit get
+ * NaN gradients (dk, dv, or the gateway accumulators).
  * Only the TT_BWD_DKDV part depends on the bit. */
 size_t tt_attn_bwd_workspace_bytes(const tt_attn_problem* p);
+
+/* Host only (no device work): the det_slots a DFS pre-order forest needs,
+ * from node_len/parent [n_nodes] and the gateway bias past_bias [n_past]
+ * (0 or -inf per gateway key, host memory; NULL: every gateway key visible),
+ * the visibility the tt_meta_build/tt_keys_build/tt_plan_build chain derives
+ * on the device: own key j is seen by queries [j, subtree end of its node),
+ * a visible gateway key by every query. No counterpart in the reference,
+ * whose determinism is torch.use_deterministic_algorithms
+ * (verify_hybrid.py:20-25); this sizes the workspace of ours by the tree.
+ * TT_OK, or TT_E_ARG for a null pointer, n_nodes < 1, n_past < 0, a length
+ * < 1, a parent outside [-1, node) or more than 2^30 keys. */
+int tt_attn_det_slots(const int32_t* node_len, const int32_t* parent, int n_nodes, const float* past_bias,
+                      int n_past, int64_t* slots);
 int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_tensor d_o,
                 void* dq, void* dk, void* dv, float* dk_past_acc, float* dv_past_acc,
                 void* ws, size_t ws_bytes, void* stream);

@@ -459,3 +459,67 @@ def test_ce_rows_validation():
     assert call(args(ld=999)) == _lib.TT_E_ARG          # shorter than a row
     assert call(args(ld=1004)) == _lib.TT_E_ARG         # rows not 16-byte aligned for bf16
     assert call(args(ldg=500)) == _lib.TT_E_ARG
+
+
+def _det_slots(lens, par, bias=None):
+    import numpy as np
+    nl, pa = np.asarray(lens, np.int32), np.asarray(par, np.int32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    out = ctypes.c_int64(-1)
+    rc = _lib.lib().tt_attn_det_slots(nl.ctypes.data, pa.ctypes.data, len(nl),
+                                      None if b is None else b.ctypes.data, 0 if b is None else len(b),
+                                      ctypes.byref(out))
+    return rc, out.value
+
+
+def test_det_slots_match_visibility_windows():
+    """tt_attn_det_slots (host only) against the dK/dV work-item rule applied
+    to the oracle's dense visibility: per 128-key tile the union of its keys'
+    visible queries is a range [lo, hi); a range longer than the window W
+    (half the largest power of two <= n_q, clamped to [256, 4096]) is one work
+    item per W-aligned window it touches, others one item; the slots are the
+    items beyond each tile's first. Forests with long nodes, with and without
+    a gateway (bias 0 = seen by every query, -inf = by none)."""
+    import numpy as np
+    from oracle.tree_meta import mask_from_horizon, meta_closed_form
+    from tree_training_amd import workloads
+    rng = np.random.default_rng(5)
+    for seed in range(6):
+        lens, par = workloads.random_forest(seed, n_roots=(1, 2), max_depth=4, max_branch=3, node_len=(40, 700))
+        T = sum(lens)
+        mask = mask_from_horizon(meta_closed_form(lens, par)["horizon"])   # [query, key]
+        for n_past in (0, 300):
+            bias = None
+            cols = mask
+            if n_past:
+                bias = np.where(rng.random(n_past) < 0.6, 0.0, -np.inf).astype(np.float32)
+                cols = np.concatenate([np.repeat((bias == 0)[None, :], T, axis=0), mask], axis=1)
+            half = (1 << (T.bit_length() - 1)) // 2
+            W = min(4096, max(256, half))
+            want = 0
+            for kb in range(0, cols.shape[1], 128):
+                rows = np.nonzero(cols[:, kb:kb + 128].any(axis=1))[0]
+                if len(rows) == 0:
+                    continue
+                lo, hi = rows[0], rows[-1] + 1
+                assert len(rows) == hi - lo        # one contiguous range
+                if hi - lo > W:
+                    want += (hi - 1) // W - lo // W
+            rc, got = _det_slots(lens, par, bias)
+            assert rc == _lib.TT_OK
+            assert got == want, (seed, n_past, got, want)
+    # the workloads: far below the topology-free bound n_kb * floor((n_q - 1) / W)
+    for (lens, par), n_past in ((workloads.agent_tree(0), 0), (workloads.agent_tree(0), 4096),
+                                (workloads.rollout_tree(0), 0)):
+        T = sum(lens)
+        W = min(4096, max(256, (1 << (T.bit_length() - 1)) // 2))
+        rc, got = _det_slots(lens, par, np.zeros(n_past) if n_past else None)
+        assert rc == _lib.TT_OK and 0 < got < -(-(T + n_past) // 128) * ((T - 1) // W) / 2
+
+
+def test_det_slots_rejects_bad_topology():
+    assert _det_slots([5, 0], [-1, 0])[0] == _lib.TT_E_ARG        # empty node
+    assert _det_slots([5, 5], [-1, 1])[0] == _lib.TT_E_ARG        # parent not before the node
+    assert _det_slots([5, 5], [-1, -2])[0] == _lib.TT_E_ARG
+    assert _det_slots([], [])[0] == _lib.TT_E_ARG
+    assert _det_slots([5, 5], [-1, 0])[1] == 0

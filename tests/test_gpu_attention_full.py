@@ -275,39 +275,117 @@ def test_attention_gateway_partitions_full_size():
     assert _max_rel(dv.float(), sum_dv) < 2e-2
 
 
-@pytest.mark.parametrize("dt", ["bf16", "fp32"])
-def test_attention_deterministic_full_size(dt):
-    """The 16K agent tree under a 4096-key gateway that every query sees (so
-    the gateway tiles and the root's tiles split into several dK/dV work
-    items): with TT_BWD_DETERMINISTIC two backwards are bitwise equal (dq, dk,
-    dv and the fp32 gateway sums), and they agree with the default (atomic)
-    backward to rounding (max_rel < 1e-2 bf16, < 1e-5 fp32)."""
+@pytest.mark.parametrize("workload,dt", [("agent16k", "bf16"), ("agent16k", "fp32"), ("rollout48k", "bf16")])
+def test_attention_deterministic_full_size(workload, dt):
+    """With TT_BWD_DETERMINISTIC and the workspace sized from the tree
+    (tt_attn_det_slots), two backwards are bitwise equal (dq, dk, dv and the
+    fp32 gateway sums), and they agree with the default (atomic) backward to
+    rounding (max_rel < 1e-2 bf16, < 1e-5 fp32). agent16k runs under a
+    4096-key gateway that every query sees (its tiles and the root's split
+    into several dK/dV work items); rollout48k is the 48K tree, whose 8192
+    prompt keys are seen by all 49,152 queries."""
     from tree_training_amd.attention import attn_backward, attn_forward
     from tree_training_amd.meta import KeyPlan, TreeMetaDevice
-    lens, par = workloads.agent_tree(0)
-    T, Lp = sum(lens), 4096
+    lens, par = workloads.agent_tree(0) if workload == "agent16k" else workloads.rollout_tree(0)
+    T, Lp = sum(lens), (4096 if workload == "agent16k" else 0)
     g = torch.Generator(device=DEV).manual_seed(9)
     bf = torch.bfloat16 if dt == "bf16" else torch.float32
     q = torch.randn(T, HQ, D, device=DEV, generator=g, dtype=bf)
     k = torch.randn(T, HKV, D, device=DEV, generator=g, dtype=bf)
     v = torch.randn(T, HKV, D, device=DEV, generator=g, dtype=bf)
-    kp = torch.randn(Lp, HKV, D, device=DEV, generator=g, dtype=bf)
-    vp = torch.randn(Lp, HKV, D, device=DEV, generator=g, dtype=bf)
+    kp = vp = None
+    if Lp:
+        kp = torch.randn(Lp, HKV, D, device=DEV, generator=g, dtype=bf)
+        vp = torch.randn(Lp, HKV, D, device=DEV, generator=g, dtype=bf)
     do = torch.randn(T, HQ, D, device=DEV, generator=g, dtype=bf)
     scale = D ** -0.5
-    view = lambda x: x[None].transpose(1, 2)
-    plan = KeyPlan(TreeMetaDevice(lens, par, device=DEV).horizon, torch.zeros(Lp, device=DEV))
+    view = lambda x: None if x is None else x[None].transpose(1, 2)
+    plan = KeyPlan(TreeMetaDevice(lens, par, device=DEV).horizon, torch.zeros(Lp, device=DEV) if Lp else None,
+                   topo=(lens, par))
+    assert plan.det_slots() == _plan_extra_items(plan) > 0
     o, lse = attn_forward(view(q), view(k), view(v), plan, scale, view(kp), view(vp))
     outs = []
     for det in (True, True, False):
-        acc = (torch.zeros(Lp, HKV, D, device=DEV), torch.zeros(Lp, HKV, D, device=DEV))
+        acc = (torch.zeros(Lp, HKV, D, device=DEV), torch.zeros(Lp, HKV, D, device=DEV)) if Lp else None
         dq, dk, dv = attn_backward(view(q), view(k), view(v), plan, scale, o, lse, do[None], view(kp), view(vp),
                                    acc, deterministic=det)
-        outs.append((dq, dk, dv, acc[0], acc[1]))
-        print(f"agent16k + gateway {Lp} {dt}: backward deterministic={det} done", flush=True)
+        outs.append((dq, dk, dv) + (tuple(acc) if acc else ()))
+        print(f"{workload} + gateway {Lp} {dt}: backward deterministic={det} done", flush=True)
     torch.cuda.synchronize()
     names = ("dq", "dk", "dv", "dk_past", "dv_past")
     for name, a, b, c in zip(names, *outs):
         assert torch.equal(a, b), f"{name}: two deterministic runs differ"
         assert torch.isfinite(a.float()).all(), name
         assert _max_rel(c.float(), a.float()) < (1e-2 if dt == "bf16" else 1e-5), name
+
+
+def _plan_extra_items(plan):
+    """dK/dV work items beyond the first of each key tile, read back from the
+    device plan (header: int32 n_kb at byte 16, n_items at byte 20)."""
+    hdr = plan.plan[:24].view(torch.int32).cpu()
+    return int(hdr[5]) - int(hdr[4])
+
+
+def test_attention_deterministic_workspace_from_tree():
+    """tt_attn_det_slots (host arithmetic on the topology) equals the extra
+    work items of the device-built plan on the workloads' trees, with and
+    without gateways; with it the deterministic backward's workspace at the
+    16K agent tree (32/8 heads, bf16) is at most 1.5x the default one, where
+    the topology-free bound is about 4x."""
+    from tree_training_amd._lib import TT_BWD_DETERMINISTIC, lib
+    from tree_training_amd.attention import _Problem
+    from tree_training_amd.meta import KeyPlan, TreeMetaDevice
+    import ctypes
+    cases = [("agent16k", workloads.agent_tree(0), 0), ("agent16k+gw", workloads.agent_tree(0), 4096),
+             ("rollout48k", workloads.rollout_tree(0), 0), ("agent_s3", workloads.agent_tree(3), 777)]
+    for name, (lens, par), Lp in cases:
+        bias = None
+        if Lp:
+            bias = torch.zeros(Lp)
+            bias[Lp // 3: Lp // 2] = float("-inf")
+        plan = KeyPlan(TreeMetaDevice(lens, par, device=DEV).horizon, bias, topo=(lens, par))
+        print(f"{name}: det_slots {plan.det_slots()} plan {_plan_extra_items(plan)}", flush=True)
+        assert plan.det_slots() == _plan_extra_items(plan), name
+    lens, par = workloads.agent_tree(0)
+    T = sum(lens)
+    plan = KeyPlan(TreeMetaDevice(lens, par, device=DEV).horizon, None, topo=(lens, par))
+    q = torch.empty(1, HQ, T, D, device=DEV, dtype=torch.bfloat16)
+    k = torch.empty(1, HKV, T, D, device=DEV, dtype=torch.bfloat16)
+    pb = _Problem(q, k, k, None, None, plan, D ** -0.5)
+    default = lib().tt_attn_bwd_workspace_bytes(ctypes.byref(pb.s))
+    pb.s.bwd_parts = TT_BWD_DETERMINISTIC
+    bound = lib().tt_attn_bwd_workspace_bytes(ctypes.byref(pb.s))
+    pb.s.det_slots = plan.det_slots()
+    exact = lib().tt_attn_bwd_workspace_bytes(ctypes.byref(pb.s))
+    print(f"agent16k workspace: default {default} deterministic {exact} (bound {bound})", flush=True)
+    assert exact <= 1.5 * default < bound
+
+
+def test_attention_deterministic_undersized_slots_poison_not_overrun():
+    """A det_slots below the tree's count writes nothing past the workspace:
+    the tiles whose later items lack a slot get NaN dk/dv, every other key's
+    gradients equal those of the exactly sized run bitwise."""
+    from tree_training_amd._lib import TT_BWD_DETERMINISTIC
+    from tree_training_amd.attention import attn_backward, attn_forward
+    from tree_training_amd.meta import KeyPlan, TreeMetaDevice
+    lens, par = [2048, 300, 900, 700], [-1, 0, 0, 2]
+    T = sum(lens)
+    g = torch.Generator(device=DEV).manual_seed(4)
+    q = torch.randn(T, HQ, D, device=DEV, generator=g, dtype=torch.bfloat16)
+    k = torch.randn(T, HKV, D, device=DEV, generator=g, dtype=torch.bfloat16)
+    v = torch.randn(T, HKV, D, device=DEV, generator=g, dtype=torch.bfloat16)
+    do = torch.randn(T, HQ, D, device=DEV, generator=g, dtype=torch.bfloat16)
+    view = lambda x: x[None].transpose(1, 2)
+    plan = KeyPlan(TreeMetaDevice(lens, par, device=DEV).horizon, None, topo=(lens, par))
+    need = plan.det_slots()
+    assert need >= 2
+    o, lse = attn_forward(view(q), view(k), view(v), plan, D ** -0.5)
+    full = attn_backward(view(q), view(k), view(v), plan, D ** -0.5, o, lse, do[None], deterministic=True)
+    plan._det = need - 1
+    short = attn_backward(view(q), view(k), view(v), plan, D ** -0.5, o, lse, do[None], deterministic=True)
+    torch.cuda.synchronize()
+    assert torch.equal(full[0], short[0])
+    for a, b in zip(full[1:], short[1:]):
+        bad = torch.isnan(b.float()).any(dim=2).any(dim=1)
+        assert bad.any() and not bad.all()
+        assert torch.equal(a[~bad], b[~bad])

@@ -127,6 +127,8 @@ def attn_backward(q, k, v, plan: KeyPlan, scale: float, o, lse, d_o, k_past=None
     det = TT_BWD_DETERMINISTIC if deterministic else 0
     pb = _Problem(q, k, v, k_past, v_past, plan, scale)
     pb.s.bwd_parts = det
+    if det:
+        pb.s.det_slots = plan.det_slots()
     dev = q.device
     d_o = d_o.reshape(1, pb.N, pb.Hq, pb.D) if d_o.dim() != 4 else d_o
     d_o, dst, dsh = _tok_view(d_o)

@@ -1,12 +1,15 @@
 // extern "C" entry points: host-side validation, then enqueue-only launches.
 #include <math.h>
 
+#include <algorithm>
+#include <vector>
+
 #include "tt_common.h"
 #include "tt_internal.h"
 
 namespace {
 
-constexpr int kAbiVersion = 6;
+constexpr int kAbiVersion = 7;
 constexpr int64_t kMaxTokStride = int64_t(1) << 23;   // elements (bf16; half that for fp32)
 inline int64_t max_tok_stride(int dtype) { return dtype == TT_DTYPE_BF16 ? kMaxTokStride : kMaxTokStride / 2; }
 
@@ -202,13 +205,17 @@ static size_t delta_bytes(const tt_attn_problem* p) {
 static size_t split_rows_bytes(const tt_attn_problem* p) {
     return (size_t)(p->n_q + p->n_past) * (size_t)p->n_heads_kv * 128 * sizeof(float);
 }
+// Slots of the deterministic mode: the caller's exact count, else the bound.
+static int64_t det_slot_count(const tt_attn_problem* p) {
+    return p->det_slots > 0 ? p->det_slots : tt_det_slots(p->n_q, p->n_q + p->n_past);
+}
 static size_t det_slot_bytes(const tt_attn_problem* p) {
-    return (size_t)tt_det_slots(p->n_q, p->n_q + p->n_past) * TT_BKB * (size_t)p->n_heads_kv * 128 * sizeof(float);
+    return (size_t)det_slot_count(p) * TT_BKB * (size_t)p->n_heads_kv * 128 * sizeof(float);
 }
 
 size_t tt_attn_bwd_workspace_bytes(const tt_attn_problem* p) {
     if (!p || p->n_q < 1 || p->n_heads_q < 1 || p->n_heads_kv < 1 || p->n_past < 0) return 0;
-    if ((int64_t)p->n_q + p->n_past > 0x3fffffff) return 0;
+    if ((int64_t)p->n_q + p->n_past > 0x3fffffff || p->det_slots < 0) return 0;
     size_t b = delta_bytes(p) + 2 * split_rows_bytes(p);
     if (p->bwd_parts & TT_BWD_DETERMINISTIC) b += 2 * det_slot_bytes(p);
     return b + split_part_bytes(p);
@@ -221,6 +228,7 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
     if (rc != TT_OK) return rc;
     if (!o || !lse || !d_o.ptr || !dq || !dk || !dv || !ws) return TT_E_ARG;
     if ((dk_past_acc == nullptr) != (dv_past_acc == nullptr)) return TT_E_ARG;
+    if (p->det_slots < 0) return TT_E_ARG;
     if (ws_bytes < tt_attn_bwd_workspace_bytes(p)) return TT_E_WORKSPACE;
     const int64_t gran = p->dtype == TT_DTYPE_BF16 ? 8 : 4;
     const size_t ealign = 16;
@@ -245,6 +253,7 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
     if (p->bwd_parts & ~(TT_BWD_DELTA | TT_BWD_DQ | TT_BWD_DKDV | TT_BWD_DETERMINISTIC)) return TT_E_ARG;
     b.det = (p->bwd_parts & TT_BWD_DETERMINISTIC) ? 1 : 0;
     b.dk_ws = b.dv_ws = b.dk_slot = b.dv_slot = b.dq_part = nullptr;
+    b.det_cap = b.det ? det_slot_count(p) : 0;
     b.n_split = key_splits(p);
     {
         uint8_t* w = reinterpret_cast<uint8_t*>(ws) + delta_bytes(p);
@@ -263,6 +272,44 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
     b.zero_in_dq = p->dtype == TT_DTYPE_BF16 && !b.det && (b.parts & TT_BWD_DQ) && (b.parts & TT_BWD_DKDV);
     if (p->dtype == TT_DTYPE_BF16) return tt_bwd_bf16_launch(a, b, (hipStream_t)stream);
     return tt_bwd_f32_launch(a, b, (hipStream_t)stream);
+}
+
+int tt_attn_det_slots(const int32_t* node_len, const int32_t* parent, int n_nodes, const float* past_bias,
+                      int n_past, int64_t* slots) {
+    if (!node_len || !parent || !slots || n_nodes < 1 || n_past < 0) return TT_E_ARG;
+    // subtree end per node: in DFS pre-order a node's subtree is the run of
+    // nodes after it, so children (later nodes) fold into their parents
+    std::vector<int64_t> start(n_nodes), end(n_nodes);
+    int64_t T = 0;
+    for (int u = 0; u < n_nodes; ++u) {
+        if (node_len[u] < 1 || parent[u] < -1 || parent[u] >= u) return TT_E_ARG;
+        start[u] = T;
+        T += node_len[u];
+        end[u] = T;
+        if (T + n_past > 0x3fffffff) return TT_E_ARG;
+    }
+    for (int u = n_nodes - 1; u > 0; --u)
+        if (parent[u] >= 0 && end[u] > end[parent[u]]) end[parent[u]] = end[u];
+    const int n_q = (int)T, n_keys = n_past + n_q, n_kb = tt_cdiv(n_keys, TT_BKB), qch = tt_qch(n_q);
+    std::vector<int> lo(n_kb, n_q), hi(n_kb, 0);
+    for (int j = 0; j < n_past; ++j)
+        if (!past_bias || past_bias[j] == 0.0f) {
+            lo[j / TT_BKB] = 0;
+            hi[j / TT_BKB] = n_q;
+        }
+    for (int u = 0; u < n_nodes; ++u)
+        for (int64_t t = start[u]; t < start[u] + node_len[u]; ++t) {
+            const int kb = (int)((n_past + t) / TT_BKB);
+            lo[kb] = std::min(lo[kb], (int)t);
+            hi[kb] = std::max(hi[kb], (int)end[u]);
+        }
+    int64_t extra = 0;
+    for (int kb = 0; kb < n_kb; ++kb) {
+        const bool any = lo[kb] < hi[kb];
+        extra += tt_kb_items(any ? lo[kb] : 0, any ? hi[kb] : 0, qch) - 1;
+    }
+    *slots = extra;
+    return TT_OK;
 }
 
 size_t tt_gdn_workspace_bytes(const tt_gdn_problem* p) {

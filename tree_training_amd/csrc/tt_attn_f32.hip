@@ -553,6 +553,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
         // Epilogue: rows of dk/dv = this wave's keys, columns = d (as the bf16 pass).
         const bool det_split = split && bw.det;
+        // a later item whose slot lies beyond the workspace writes nothing (its
+        // tile's gradients become NaN in the finalize)
+        const bool det_skip = det_split && chunk > 0 && (int64_t)(item - lo_r - 1) >= bw.det_cap;
         float* const sk = chunk == 0 ? bw.dk_ws : bw.dk_slot;
         float* const sv = chunk == 0 ? bw.dv_ws : bw.dv_slot;
         const int64_t srow = chunk == 0 ? 0 : (int64_t)(item - lo_r - 1) * TT_BKB - kb * TT_BKB;
@@ -560,7 +563,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int key = kbase + acc_row(r, half);
-            if (key >= a.n_keys) continue;
+            if (key >= a.n_keys || det_skip) continue;
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
                 const int d = 32 * db + col;

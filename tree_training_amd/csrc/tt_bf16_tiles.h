@@ -424,15 +424,19 @@ __global__ __launch_bounds__(256) void bwd_split_finalize_det_kernel(AttnDev a, 
     if (m <= 1) return;
     const int k_first = kb * TT_BKB, k_end = min(kb * TT_BKB + TT_BKB, a.n_keys);
     const int64_t slot0 = (int64_t)(a.kb_base[rank] - rank) * TT_BKB;   // slot rows of the tile's second item
+    // slots the workspace lacks (a det_slots below the tree's count): the
+    // work items wrote none, and the tile's gradients are NaN
+    const bool lacks = (int64_t)(a.kb_base[rank] - rank) + (m - 1) > bw.det_cap;
     for (int e = threadIdx.x; e < (k_end - k_first) * (D / 4); e += 256) {
         const int key = k_first + e / (D / 4), d = 4 * (e % (D / 4));
         const size_t widx = ((size_t)key * a.hkv + g) * D + d;
         f32x4 gk = *(const f32x4*)(bw.dk_ws + widx), gv = *(const f32x4*)(bw.dv_ws + widx);
-        for (int c = 1; c < m; ++c) {
+        for (int c = 1; c < (lacks ? 1 : m); ++c) {
             const size_t sidx = ((size_t)(slot0 + (int64_t)(c - 1) * TT_BKB + key - k_first) * a.hkv + g) * D + d;
             gk += *(const f32x4*)(bw.dk_slot + sidx);
             gv += *(const f32x4*)(bw.dv_slot + sidx);
         }
+        if (lacks) gk = gv = (f32x4){NAN, NAN, NAN, NAN};
         if (key < a.n_past) {
             if (bw.dk_acc) {
                 *(f32x4*)(bw.dk_acc + widx) += gk;

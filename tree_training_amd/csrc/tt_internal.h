@@ -41,6 +41,7 @@ struct BwdDev {
     float* dv_ws;             // workspace [n_keys, hkv, 128] fp32: split key tiles' dV
     float* dk_slot;           // deterministic mode: [tt_det_slots, 128, hkv, 128] fp32, chunks >= 1
     float* dv_slot;           //   of split key tiles (null otherwise)
+    int64_t det_cap;          // deterministic mode: slots the workspace holds (tiles beyond get NaN)
     int parts;                // OR of TT_BWD_DELTA / _DQ / _DKDV (never 0 here)
     int det;                  // TT_BWD_DETERMINISTIC given (split tiles summed in chunk order)
     float* dq_part;           // bf16 with tt_key_splits > 1: [splits, n_q, hq, 128] fp32 dQ partials

@@ -143,7 +143,7 @@ def build_trees(specs, device=None, validate: bool = False):
     for i, (nl, pa, po, pb) in enumerate(specs):
         if i not in built:
             meta = TreeMetaDevice(nl, pa, pos_offset=po, device=dev)
-            built[i] = (meta, KeyPlan(meta.horizon, pb))
+            built[i] = (meta, KeyPlan(meta.horizon, pb, topo=(nl, pa)))
         out.append(built[i])
     if validate:
         for meta, plan in out:
@@ -201,6 +201,7 @@ def _build_batch(specs, dev):
         kp.device, kp.n_q, kp.n_past, kp.n_keys = dev, T, P, T + P
         kp.key_lo, kp.key_hi, kp.status = keys[0], keys[1], status
         kp.plan_bytes, kp.plan, kp._bias = plan_bytes[j], plan, bias
+        kp._topo, kp._bias_src, kp._det = (nl, pa), pb, None
         out.append((meta, kp))
     check(lib().tt_trees_build(jobs, n, _stream(dev)), "tt_trees_build")
     return out
@@ -210,8 +211,11 @@ class KeyPlan:
     """Per-key visibility intervals over [gateway | own] keys plus the tile plan."""
 
     def __init__(self, horizon: torch.Tensor, past_bias: Optional[torch.Tensor] = None,
-                 validate: bool = False):
+                 validate: bool = False, topo=None):
+        """``topo``: the forest's host ``(node_len, parent)``, from which
+        ``det_slots`` sizes the deterministic backward's workspace exactly."""
         dev = horizon.device
+        self._topo, self._bias_src, self._det = topo, past_bias, None
         n_q = int(horizon.numel())
         n_past = 0 if past_bias is None else int(past_bias.numel())
         if past_bias is not None:
@@ -232,6 +236,26 @@ class KeyPlan:
             s = int(self.status.item())
             if s:
                 raise ValueError(f"gateway bias must be 0 or -inf (status bits {s:#x})")
+
+    def det_slots(self) -> int:
+        """Partial-sum slots of the deterministic backward for this tree
+        (``tt_attn_det_slots``, host arithmetic on the topology; a gateway bias
+        held on the device is copied once). 0 — the tree-independent bound —
+        when the plan was built without its topology."""
+        if self._det is None:
+            self._det = 0
+            if self._topo is not None:
+                nl = np.ascontiguousarray(self._topo[0], dtype=np.int32)
+                pa = np.ascontiguousarray(self._topo[1], dtype=np.int32)
+                bias = None
+                if self._bias_src is not None:
+                    bias = np.ascontiguousarray(torch.as_tensor(self._bias_src).detach().float().cpu().numpy())
+                out = ctypes.c_int64(0)
+                check(lib().tt_attn_det_slots(nl.ctypes.data, pa.ctypes.data, len(nl),
+                                              bias.ctypes.data if bias is not None else None, self.n_past,
+                                              ctypes.byref(out)), "tt_attn_det_slots")
+                self._det = int(out.value)
+        return self._det
 
     def visible_pairs(self) -> int:
         """Visible (query, key) pairs per head, P (synchronises)."""

@@ -95,7 +95,8 @@ class DFSTreeInfo:
 
     def key_plan(self, device=None, past_bias: Optional[torch.Tensor] = None, pos_offset: int = 0):
         from .meta import KeyPlan
-        return KeyPlan(self.device_meta(device, pos_offset).horizon, past_bias)
+        return KeyPlan(self.device_meta(device, pos_offset).horizon, past_bias,
+                       topo=(self.node_len, self.chunk_parent_map))
 
     # -- compatibility views (host copies, built on access) -------------------
     @property
