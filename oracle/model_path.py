@@ -8,6 +8,12 @@ Test infrastructure only. Restates, with the oracle's own literal metadata
   * ``sequential_param_grads`` — tree_grad_ckpt.py:193-261 with
     make_tree_loss_fn (:279-297) and the fp32 parameter-grad hooks of
     verify_hybrid.py:74-84: one backward per leaf in DFS order;
+  * ``tree_gdn_layers`` — the GatedDeltaNet patch the reference installs around
+    its whole-tree forward (dfs_tree_forward.py:442-467, tree_dfs_ssm.py:432-445):
+    every linear-attention layer computes ``gdn.gdn_layer_torch`` over the DFS
+    forest (the exact rule, or with ``reference_truncated`` the reference's own
+    I + R + R^2 scan), so the two functions above become the reference's
+    drivers on hybrid (Qwen3.5) models;
   * ``hybrid_param_grads`` — tree_grad_hybrid.py:434-539 (attention models):
     partitions forwarded top-down, each over its gateway KV with the gateway
     bias in the additive mask, then per partition bottom-up one backward per
@@ -19,9 +25,12 @@ checked against.
 """
 from __future__ import annotations
 
+import contextlib
+
 import torch
 import torch.nn.functional as F
 
+from .gdn import gdn_layer_torch
 from .partition import hybrid_schedule
 from .tree_meta import build_dfs_tree_info_literal
 
@@ -50,6 +59,31 @@ def dense_leaf_logits(model, roots):
         model.config._attn_implementation = saved
     out = [logits[:, s:e, :] for s, e in (info["chunk_boundaries"][c] for c in info["leaf_chunk_ids"])]
     return out, info["leaf_nodes"]
+
+
+@contextlib.contextmanager
+def tree_gdn_layers(model, roots, reference_truncated=False):
+    """Within the block every GatedDeltaNet layer of ``model`` (modules with
+    ``in_proj_qkv`` and ``A_log``, called as ``linear_attn(hidden_states=...)``)
+    runs ``gdn_layer_torch`` over the DFS-packed forest of ``roots``."""
+    info = build_dfs_tree_info_literal(roots)
+    lens = [e - s for s, e in info["chunk_boundaries"]]
+    par = list(info["chunk_parent_map"])
+    layers = [m for m in model.modules() if hasattr(m, "in_proj_qkv") and hasattr(m, "A_log")]
+
+    def make(ssm):
+        def forward(hidden_states=None, *args, **kwargs):
+            assert hidden_states.shape[0] == 1 and hidden_states.shape[1] == sum(lens)
+            return gdn_layer_torch(ssm, hidden_states[0], lens, par, reference_truncated)[None]
+        return forward
+
+    for m in layers:
+        m.forward = make(m)
+    try:
+        yield
+    finally:
+        for m in layers:
+            del m.forward
 
 
 def sequential_param_grads(model, roots, labels_by_id, n_leaves, ignore_index=-100):

@@ -150,13 +150,16 @@ def test_hybrid_chain_inherited_bias_equals_whole_tree():
     assert r_leg > 1e-3
 
 
+@pytest.mark.parametrize("switch", ["legacy_gateway_bias", "reference_literal"])
 @pytest.mark.parametrize("tree,max_tokens", [("q1", 6), ("c1", 20), ("c1", 10)])
-def test_hybrid_legacy_bias_matches_literal_oracle(tree, max_tokens):
+def test_hybrid_legacy_bias_matches_literal_oracle(tree, max_tokens, switch):
     """legacy_gateway_bias=True reproduces the reference's own hybrid run, with
     the literal gateway bias of tree_grad_hybrid.py:207: its fp32 parameter
     gradients match the float64 restatement of that run
     (oracle.model_path.hybrid_param_grads, legacy=True) to < 1e-5, on the Q1
-    chain too, where that run differs from the whole tree."""
+    chain too, where that run differs from the whole tree. reference_literal=True
+    (the legacy bias plus transformers' own prologue and logits + CE and the
+    per-leaf schedule) is held to the same oracle."""
     from tree_training_amd.hybrid import tree_grad_hybrid
     say(f"hybrid legacy bias vs literal oracle {tree} max_tokens={max_tokens}")
     base = make_qwen3("tiny", layers=2)
@@ -166,7 +169,7 @@ def test_hybrid_legacy_bias_matches_literal_oracle(tree, max_tokens):
     labels = _labels(leaves)
     ref = hybrid_param_grads(ref_model, roots, labels, len(leaves), max_tokens, legacy=True)
     new = _grads(model, lambda: tree_grad_hybrid(model, roots, _loss_fn(labels, len(leaves)), max_tokens,
-                                                 legacy_gateway_bias=True))
+                                                 **{switch: True}))
     r = _max_rel_params(ref, new)
     say(f"  max_rel {r:.3e}")
     assert r < 1e-5, r

@@ -202,3 +202,31 @@ def test_run_tree_model_rejects_token_ids_outside_the_vocabulary():
     model = types.SimpleNamespace(config=types.SimpleNamespace(vocab_size=1000))
     with pytest.raises(ValueError, match="vocabulary"):
         run_tree_model(model, info, "cpu")
+
+
+def test_reference_literal_sets_every_reference_option():
+    """literal_options: reference_literal=True forces the options each driver
+    takes to the reference's arithmetic and leaves them alone otherwise; the
+    drivers take the switch (a missing name in any of them fails here on CPU)."""
+    import inspect
+    from tree_training_amd.ckpt import tree_grad_ckpt_sequential
+    from tree_training_amd.dfs_tree_forward import dfs_tree_forward, literal_options
+    from tree_training_amd.hybrid import tree_grad_hybrid
+    opts = dict(legacy_gateway_bias=False, gdn_reference_truncated=False, gdn_per_node_projections=False,
+                fused_prologue=True, fused_leaf_ce=True)
+    assert literal_options(False, **opts) == opts
+    assert literal_options(True, **opts) == dict(legacy_gateway_bias=True, gdn_reference_truncated=True,
+                                                 gdn_per_node_projections=True, fused_prologue=False,
+                                                 fused_leaf_ce=False)
+    assert literal_options(True, fused_prologue=True) == dict(fused_prologue=False)
+    for fn, names in ((dfs_tree_forward, ("gdn_reference_truncated", "gdn_per_node_projections", "fused_prologue")),
+                      (tree_grad_ckpt_sequential, ("fused_leaf_ce", "gdn_reference_truncated",
+                                                   "gdn_per_node_projections", "fused_prologue")),
+                      (tree_grad_hybrid, ("legacy_gateway_bias", "fused_leaf_ce", "fused_prologue"))):
+        params = inspect.signature(fn).parameters
+        assert "reference_literal" in params and params["reference_literal"].default is False
+        for n in names:
+            assert n in params, (fn.__name__, n)
+    for mod in ("ckpt", "hybrid", "dfs_tree_forward"):     # every module-level name the drivers use resolves
+        m = __import__(f"tree_training_amd.{mod}", fromlist=["x"])
+        assert m.literal_options is literal_options

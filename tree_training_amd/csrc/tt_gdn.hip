@@ -909,7 +909,7 @@ struct ChunkGradLds {
     float KK[GC * MS];    // k^ k^T
     float M1[GC * MS];    // A -> dP -> dT -> E
     float M2[GC * MS];    // T
-    float M3[GC * MS];    // dA * A + dN * N (for the column sums of dG)
+    float M3[GC * MS];    // dA * A + dN * N (the pair terms of dG)
     float R[4][GC * RR];  // per-wave partial 32 x 32 products (contraction split over the waves)
     float G[GC];
     float Glo[GC];
@@ -986,7 +986,8 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
         __syncthreads();
         const float gi = L.G[i], gl = L.G[GC - 1], egi = expf(gi), bi = L.B[i];
         const float gil = L.Glo[i], gll = L.Glo[GC - 1];
-        float dgp = 0.0f, dbp = 0.0f, cp = 0.0f;   // this thread's share of row i's dG, dbeta, c
+        // this thread's share of row i's own dG terms (those of e^{G_i} alone), dbeta, c
+        float dgp = 0.0f, dbp = 0.0f, cp = 0.0f;
 
         // dG from A = (q^ k^T) * D, then dP = dA * D (j <= i).
 #pragma unroll
@@ -995,7 +996,6 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
             const float da = L.R[0][i * RR + j] + L.R[1][i * RR + j] + L.R[2][i * RR + j] + L.R[3][i * RR + j];
             const float dae = j <= i ? da : 0.0f;
             const float pa = dae * L.M1[i * MS + j];
-            dgp += pa;
             L.M3[i * MS + j] = pa;
             L.M1[i * MS + j] = j <= i ? dae * expf(gdiff(gi, gil, L.G[j], L.Glo[j])) : 0.0f;
         }
@@ -1112,7 +1112,6 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
                         const float pa = dn * (-bi * kk * dd);
                         dbp = fmaf(dn, -kk * dd, dbp);
                         ev[e] = -dn * bi * dd;
-                        dgp += pa;
                         L.M3[i * MS + j] += pa;
                     }
                 }
@@ -1154,7 +1153,6 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
                 for (int e = 0; e < 4; ++e) dka[4 * m + e] = fmaf(ed, x[e], dka[4 * m + e]);
             }
             cp = ed * kt;
-            dgp -= cp;
         }
         dgp = row8_sum(dgp);
         dbp = row8_sum(dbp);
@@ -1164,22 +1162,37 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
             L.Crow[i] = cp;
             if (!TRUNC && valid) dbeta[tok * p.hv + h] = dbp;
         }
+        // dg_t = sum of dG_u over u >= t within the chunk (G is its cumulative
+        // sum). A pair term p_ij (M3, i > j: the factors e^{G_i - G_j} of A and
+        // N) adds to dG_i and subtracts from dG_j, so it reaches dg_t exactly
+        // when i >= t > j; a term c_i of the output state's e^{G_L - G_i}
+        // (Crow) reaches it when i < t; e^{G_L} S's reaches every t. Summing
+        // just those sets, rather than suffix sums of row minus column sums
+        // in which the pairs inside [t, L] cancel only up to rounding, keeps
+        // dg accurate relative to its own size. First M3's rows become
+        // exclusive prefix sums, M3[i][c] = sum_{j < c} p_ij.
         __syncthreads();
         if (t < GC) {
-            float colsum = 0.0f, ctot = 0.0f;
+            float run = 0.0f;
 #pragma unroll 4
-            for (int r = 0; r < GC; ++r) {
-                colsum += L.M3[r * MS + t];
-                ctot += L.Crow[r];
+            for (int c = 0; c < GC; ++c) {
+                const float x = L.M3[t * MS + c];
+                L.M3[t * MS + c] = run;
+                run += x;
             }
-            float dG = L.Grow[t] - colsum;
-            if (t == GC - 1) dG += expf(gl) * sdot[chn] + ctot;
-            // dg_t = sum of dG_u over u >= t within the chunk (G is its cumulative sum)
+        }
+        __syncthreads();
+        if (t < GC) {
+            float cross = 0.0f, cpre = 0.0f;
+            for (int r = t; r < GC; ++r) cross += L.M3[r * MS + t];
+            for (int r = 0; r < t; ++r) cpre += L.Crow[r];
+            float dG = L.Grow[t];
 #pragma unroll
             for (int o = 1; o < GC; o <<= 1) {
                 const float up = __shfl_down(dG, o, GC);
                 if (t + o < GC) dG += up;
             }
+            dG += cross + cpre + expf(gl) * sdot[chn];
             if constexpr (TRUNC) dG += trg[chn * GC + t];
             if (t < len) dg[(int64_t)(start + t) * p.hv + h] = dG;
         }

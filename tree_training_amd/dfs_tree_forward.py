@@ -54,11 +54,13 @@ def fused_ce_capable(model, leaf_loss_fn) -> bool:
 
 def run_tree_model(model, info: DFSTreeInfo, dev, pos_offset: int = 0, cache=None, accumulators=None,
                    past_bias: Optional[torch.Tensor] = None, linear_attention_patched: bool = False,
-                   hidden_only: bool = False, plan=None):
+                   hidden_only: bool = False, plan=None, fused_prologue: bool = True):
     """One model forward over a DFS-packed forest (or partition) with tree
     attention. Returns the model output (the decoder's, with the final hidden
     states and no logits, when ``hidden_only``). ``plan``: a KeyPlan already
-    built for this tree and gateway (``meta.build_trees``), else built here."""
+    built for this tree and gateway (``meta.build_trees``), else built here.
+    ``fused_prologue``: the fused q/k RMSNorm + rotary kernel in place of the
+    model's own modules (False: transformers' own ops, as the reference)."""
     vocab = getattr(getattr(model, "config", None), "vocab_size", None)
     if vocab is not None and info.dfs_token_ids and not (0 <= min(info.dfs_token_ids) and
                                                          max(info.dfs_token_ids) < vocab):
@@ -71,14 +73,29 @@ def run_tree_model(model, info: DFSTreeInfo, dev, pos_offset: int = 0, cache=Non
     ids_t = upload_i32([info.dfs_token_ids], dev).long()
     pos_t = meta.pos.long().unsqueeze(0)
     ctx = TreeAttnContext(plan=plan, cache=cache, accumulators=accumulators)
-    with tree_attention_mode(model, linear_attention_patched):
+    with tree_attention_mode(model, linear_attention_patched, fused_prologue):
         body = model.model if hidden_only else model
         return body(input_ids=ids_t, attention_mask=None, position_ids=pos_t,
                     past_key_values=cache, use_cache=cache is not None, tree_ctx=ctx)
 
 
+def literal_options(reference_literal: bool, **opts) -> dict:
+    """The drivers' options, with every one that departs from the reference's
+    arithmetic switched to the reference's when ``reference_literal``: the
+    legacy gateway bias (tree_grad_hybrid.py:206-209), the truncated
+    whole-node GDN correction I + R + R^2 (tree_dfs_ssm.py:114-126), node by
+    node GDN projections, and transformers' own q/k norm + rotary and
+    lm_head + cross-entropy instead of the fused kernels."""
+    if reference_literal:
+        lit = dict(legacy_gateway_bias=True, gdn_reference_truncated=True, gdn_per_node_projections=True,
+                   fused_prologue=False, fused_leaf_ce=False)
+        opts.update({k: v for k, v in lit.items() if k in opts})
+    return opts
+
+
 def dfs_tree_forward(model, roots: List[TreeNode], dtype: Optional[torch.dtype] = None,
-                     gdn_reference_truncated: bool = False, gdn_per_node_projections: bool = False) -> DFSTreeResult:
+                     gdn_reference_truncated: bool = False, gdn_per_node_projections: bool = False,
+                     fused_prologue: bool = True, reference_literal: bool = False) -> DFSTreeResult:
     """One DFS-packed forward over a forest (dfs_tree_forward.py:513-576).
 
     ``dtype`` is accepted for signature compatibility; it only set the dense
@@ -88,16 +105,20 @@ def dfs_tree_forward(model, roots: List[TreeNode], dtype: Optional[torch.dtype] 
     instead of the exact rule; ``gdn_per_node_projections`` makes them
     project node by node as the reference does (same GEMM shapes as per-path
     runs, so their outputs match those bit for bit) instead of one GEMM per
-    projection.
+    projection. ``fused_prologue`` False runs transformers' own q/k norm and
+    rotary. ``reference_literal`` sets all three to the reference's arithmetic
+    (``literal_options``).
     """
+    o = literal_options(reference_literal, gdn_reference_truncated=gdn_reference_truncated,
+                        gdn_per_node_projections=gdn_per_node_projections, fused_prologue=fused_prologue)
     dev = next(model.parameters()).device
     info = build_dfs_tree_info(roots)
     # gated-delta-rule layers (hybrid models) run the tree-aware conv + scan
     from .gdn_layer import _patch_ssm, _unpatch_ssm
-    saved = _patch_ssm(model, info.chunk_boundaries, info.chunk_parent_map, gdn_reference_truncated,
-                       gdn_per_node_projections)
+    saved = _patch_ssm(model, info.chunk_boundaries, info.chunk_parent_map, o["gdn_reference_truncated"],
+                       o["gdn_per_node_projections"])
     try:
-        out = run_tree_model(model, info, dev, linear_attention_patched=True)
+        out = run_tree_model(model, info, dev, linear_attention_patched=True, fused_prologue=o["fused_prologue"])
     finally:
         _unpatch_ssm(saved)       # always restored, even if the forward raises
     logits = out.logits

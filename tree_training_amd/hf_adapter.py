@@ -77,11 +77,12 @@ def tree_attention_mode(model, linear_attention_patched: bool = False, fused_pro
     (linear_attn) layers must have been patched with the tree-aware forward
     (``gdn_layer._patch_ssm``, done by dfs_tree_forward); the partitioned
     drivers do not carry their recurrent state across partitions and refuse
-    such models."""
+    such models (dfs_tree_forward and tree_grad_ckpt_sequential patch them)."""
     from .prologue import patch_attention_prologue, unpatch_attention_prologue
     register()
     if not linear_attention_patched and _has_linear_attention(model):
-        raise NotImplementedError("gated-delta-rule (linear_attn) layers are supported by dfs_tree_forward only")
+        raise NotImplementedError("gated-delta-rule (linear_attn) layers are supported by dfs_tree_forward and "
+                                  "tree_grad_ckpt_sequential, not by the partitioned drivers")
     cfg = model.config
     saved = cfg._attn_implementation
     cfg._attn_implementation = ATTN_IMPL

@@ -29,7 +29,7 @@ from typing import Callable, Dict, List, Optional, Tuple
 import torch
 import torch.nn.functional as F
 
-from .dfs_tree_forward import fused_ce_capable, run_tree_model
+from .dfs_tree_forward import fused_ce_capable, literal_options, run_tree_model
 from .loss import TreeCELoss
 from .gateway import GatewayAccumulator, GatewayCache
 from .tree import DFSTreeInfo, TreeNode, info_from_flat
@@ -261,7 +261,7 @@ def _chain_gateway_grads(gw: SubtreeGateway, retain_graph: bool = False, collect
 # 4. one partition forward
 # ---------------------------------------------------------------------------
 def _subtree_forward(model, partition: SubtreePartition, gateway: Optional[SubtreeGateway], dev, dtype,
-                     hidden_only: bool = False, prebuilt=None):
+                     hidden_only: bool = False, prebuilt=None, fused_prologue: bool = True):
     """Forward of one partition with its gateway (tree_grad_hybrid.py:279-427).
     ``prebuilt``: (DFS info tuple, KeyPlan) from ``_prebuild_partitions``.
 
@@ -276,7 +276,7 @@ def _subtree_forward(model, partition: SubtreePartition, gateway: Optional[Subtr
     out = run_tree_model(model, info, dev, pos_offset=partition.pos_offset, cache=cache,
                          accumulators=gateway.fp32_acc if gateway is not None else None,
                          past_bias=gateway.attn_bias if gateway is not None else None, hidden_only=hidden_only,
-                         plan=plan)
+                         plan=plan, fused_prologue=fused_prologue)
     own_kv = [cache.own_kv(l) for l in sorted(cache._segments)]
     res = out.last_hidden_state if hidden_only else out.logits
     return res, info, own_kv, start, end, par, cidx, c2o
@@ -316,7 +316,8 @@ def _prebuild_partitions(partitions, children_of, dev, legacy: bool):
 # ---------------------------------------------------------------------------
 def tree_grad_hybrid(model, roots: List[TreeNode], leaf_loss_fn: Callable[[torch.Tensor, TreeNode], torch.Tensor],
                      max_tokens: int, legacy_gateway_bias: bool = False, summed_backward: bool = False,
-                     fused_leaf_ce: bool = True) -> None:
+                     fused_leaf_ce: bool = True, fused_prologue: bool = True,
+                     reference_literal: bool = False) -> None:
     """Hybrid tree training (tree_grad_hybrid.py:434-539); grads accumulate in ``.grad``.
 
     model        : HF causal LM (Qwen3 family), train mode, zero_grad() already called
@@ -333,7 +334,17 @@ def tree_grad_hybrid(model, roots: List[TreeNode], leaf_loss_fn: Callable[[torch
                    the final hidden states through the chunked lm_head + fused
                    cross-entropy (no [T, V] logits), one backward per partition
                    as with ``summed_backward``; other losses get logits.
+    fused_prologue : the fused q/k RMSNorm + rotary kernel (False: transformers'
+                   own modules).
+    reference_literal : every option at the reference's arithmetic — the legacy
+                   gateway bias, transformers' prologue and logits + CE, the
+                   per-leaf backward schedule (``literal_options``).
     """
+    o = literal_options(reference_literal, legacy_gateway_bias=legacy_gateway_bias,
+                        fused_leaf_ce=fused_leaf_ce, fused_prologue=fused_prologue)
+    legacy_gateway_bias, fused_leaf_ce = o["legacy_gateway_bias"], o["fused_leaf_ce"]
+    if reference_literal:
+        summed_backward = False
     dev = next(model.parameters()).device
     dtype = next(model.parameters()).dtype
     fused = fused_leaf_ce and fused_ce_capable(model, leaf_loss_fn)
@@ -350,7 +361,8 @@ def tree_grad_hybrid(model, roots: List[TreeNode], leaf_loss_fn: Callable[[torch
         gw = gateways.get(id(p))
         p.pos_offset = gw.pos_offset if gw is not None else 0
         logits, info, own_kv, s_map, e_map, par_map, ci_map, c2o = _subtree_forward(
-            model, p, gw, dev, dtype, hidden_only=fused, prebuilt=prebuilt.pop(id(p)))
+            model, p, gw, dev, dtype, hidden_only=fused, prebuilt=prebuilt.pop(id(p)),
+            fused_prologue=o["fused_prologue"])
         fwd_cache[id(p)] = (logits, info, c2o)
         seen, cuts = set(), []
         for cn, _ in children_of[id(p)]:
