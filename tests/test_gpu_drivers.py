@@ -177,7 +177,9 @@ def test_hybrid_legacy_bias_matches_literal_oracle(tree, max_tokens, switch):
 
 def test_sequential_and_hybrid_bf16():
     """bf16 model: hybrid vs sequential (the reference's own differential test,
-    threshold 5e-2 from verify_hybrid.py:143), and sequential vs the fp64 oracle."""
+    whose pass threshold is 5e-2, verify_hybrid.py:143) and sequential vs the
+    fp64 oracle, both held to the tighter bf16 bar of 2e-2 (measured 1.2e-2
+    and 1.6e-2: the model's own bf16 torch ops dominate both)."""
     from tree_training_amd.ckpt import tree_grad_ckpt_sequential
     from tree_training_amd.hybrid import tree_grad_hybrid
     say("bf16 sequential / hybrid")
@@ -191,9 +193,9 @@ def test_sequential_and_hybrid_bf16():
     ref = sequential_param_grads(ref_model, roots, labels, len(leaves))
     r_ref = _max_rel_params(ref, seq)
     say(f"  sequential bf16 vs fp64 oracle {r_ref:.3e}")
-    assert r_ref < 5e-2
+    assert r_ref < 2e-2
     for mt in (1000, 20, 10):
         hyb = _grads(model, lambda: tree_grad_hybrid(model, roots, fn, mt))
         r = _max_rel_params(seq, hyb)
         say(f"  hybrid bf16 max_tokens={mt} vs sequential {r:.3e}")
-        assert r < 5e-2
+        assert r < 2e-2
