@@ -245,7 +245,10 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
  * array, which keeps the last call's contents: calls that overlap on one GPU
  * (other streams, other threads) race and must not be issued; a TT_BWD_*
  * sequence split over several calls must not be interleaved with another
- * call on the same GPU. */
+ * call on the same GPU. The first call on each GPU resolves the array's
+ * device address (hipGetSymbolAddress, once per device, cached): make that
+ * first call outside stream capture, e.g. an ordinary warm-up call before a
+ * graph is captured; later calls make no such lookup. */
 #define TT_NOALLOC_SCRATCH_MB 64
 size_t tt_noalloc_scratch_bytes(void);
 int tt_attn_bwd_noalloc(const tt_attn_problem* p, const void* o, const float* lse, tt_tensor d_o,
@@ -348,6 +351,10 @@ typedef struct tt_gdn_problem {
      * is -1): device, [Hv, 128, 128] float32 contiguous, 16-byte aligned;
      * NULL: zero. */
     const float* initial_state;
+    /* tt_gdn_tree_bwd*: 1 when d_node_states holds the gradient of the last
+     * node's state alone ([Hv, 128, 128]: the reference's differentiable
+     * last_state, tree_dfs_ssm.py:155), 0 when it holds all [n_nodes, ...]. */
+    int32_t d_states_last_only;
 } tt_gdn_problem;
 
 /* Workspace of tt_gdn_tree_fwd: per (chunk, v head) the state-independent
@@ -372,7 +379,8 @@ int tt_gdn_tree_fwd(const tt_gdn_problem* p, void* o, float* node_states, void* 
  * no concatenation follows), and dg, dbeta [T, Hv] contiguous float32.
  * d_node_states (NULL: none) is the incoming gradient of node_states ([n_nodes,
  * Hv, 128, 128] float32; the reference's differentiable last_state,
- * tree_dfs_ssm.py:155, is node n_nodes - 1); d_initial_state (NULL: not
+ * tree_dfs_ssm.py:155, is node n_nodes - 1), or with p->d_states_last_only
+ * that of the last node's state alone ([Hv, 128, 128]); d_initial_state (NULL: not
  * wanted) receives the gradient of p->initial_state ([Hv, 128, 128] float32,
  * written whole; with a NULL initial_state, the gradient at the zero state).
  * Both 16-byte aligned. It

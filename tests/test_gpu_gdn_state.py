@@ -172,3 +172,25 @@ def test_gdn_16k_tree_cut_below_its_trunk_continues_from_initial_state():
     for name, a_w, b_r, b_0 in zip(NAMES, gw, g1, g0):
         assert torch.equal(a_w[r:], b_r), name
         assert torch.equal(a_w[:r], b_0), name
+
+
+@pytest.mark.parametrize("mode", ["exact", "reference"])
+def test_gdn_last_state_gradient_alone_equals_full_buffer(mode):
+    """d_last_state (tt_gdn_problem.d_states_last_only) gives bitwise the
+    gradients of a full d_states buffer that is zero except for the last
+    node, with the saved forward and with the recomputing backward."""
+    T = sum(LENS)
+    q, k, v, g, beta, s0, d_o, d_st = _inputs(T, 2, 4, len(LENS), 21, 0.3)
+    tree = GdnTree(LENS, PAR, torch.device("cuda", 0))
+    ins = [_dev(x) for x in (q, k, v, g, beta)]
+    full = torch.zeros(len(LENS), 4, D, D, device="cuda:0")
+    full[-1] = _dev(d_st[-1])
+    trunc = mode == "reference"
+    _, _, saved = tgdn._gdn_forward(*ins, tree, None, True, True, trunc, None)
+    for kept in (saved, None):
+        a = tgdn.gdn_tree_backward(*ins, _dev(d_o), tree, saved=kept, reference_truncated=trunc, d_states=full)
+        b = tgdn.gdn_tree_backward(*ins, _dev(d_o), tree, saved=kept, reference_truncated=trunc,
+                                   d_last_state=_dev(d_st[-1]))
+        torch.cuda.synchronize()
+        for name, x, y in zip(NAMES, a, b):
+            assert torch.equal(x, y), (mode, kept is None, name)

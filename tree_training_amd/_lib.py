@@ -29,7 +29,7 @@ TT_STATUS_BAD_PARENT = 2
 TT_STATUS_BAD_TOTAL = 4
 TT_STATUS_BAD_BIAS = 8
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # Every symbol include/tree_attn.h declares, for the export check.
 EXPORTS = (
@@ -82,6 +82,7 @@ class TTGdnProblem(ctypes.Structure):
         ("node_chunk0", ctypes.c_void_p), ("chunk_node", ctypes.c_void_p),
         ("node_child_off", ctypes.c_void_p), ("node_child", ctypes.c_void_p),
         ("reference_truncated", ctypes.c_int32), ("initial_state", ctypes.c_void_p),
+        ("d_states_last_only", ctypes.c_int32),
     ]
 
 

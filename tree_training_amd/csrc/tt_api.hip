@@ -9,7 +9,7 @@
 
 namespace {
 
-constexpr int kAbiVersion = 7;
+constexpr int kAbiVersion = 8;
 constexpr int64_t kMaxTokStride = int64_t(1) << 23;   // elements (bf16; half that for fp32)
 inline int64_t max_tok_stride(int dtype) { return dtype == TT_DTYPE_BF16 ? kMaxTokStride : kMaxTokStride / 2; }
 
@@ -372,6 +372,7 @@ static int gdn_problem(const tt_gdn_problem* p, GdnDev& d) {
     if (p->initial_state && !aligned(p->initial_state, 16)) return TT_E_ARG;
     d.init = p->initial_state;
     d.d_states = nullptr;
+    d.d_states_last = 0;
     d.d_init = nullptr;
     return TT_OK;
 }
@@ -444,7 +445,9 @@ static int gdn_bwd_args(const tt_gdn_problem* p, GdnDev& d, const tt_tensor& d_o
     d.dq_st = (int)dq.stride_tok;
     d.dk_st = (int)dk.stride_tok;
     d.dv_st = (int)dv.stride_tok;
+    if (p->d_states_last_only != 0 && p->d_states_last_only != 1) return TT_E_ARG;
     d.d_states = d_node_states;
+    d.d_states_last = p->d_states_last_only;
     d.d_init = d_initial_state;
     return TT_OK;
 }

@@ -577,8 +577,8 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     // dS after the node: its state's incoming gradient, if any, plus the sum
     // over its children of their dS at entry.
     f32x4 dS[8];
-    if (p.d_states) {
-        const float* sp = p.d_states + ((size_t)node * p.hv + h) * GD * GD + jt;
+    if (p.d_states && (!p.d_states_last || node == p.n_nodes - 1)) {
+        const float* sp = p.d_states + ((size_t)(p.d_states_last ? 0 : node) * p.hv + h) * GD * GD + jt;
 #pragma unroll
         for (int rb = 0; rb < 8; ++rb) dS[rb] = load_t16(sp + 16 * rb * GD, lane);
     } else {
@@ -705,7 +705,8 @@ __global__ __launch_bounds__(GT) void gdn_init_grad_kernel(GdnDev p, const float
     const int e = 4 * (blockIdx.x * GT + threadIdx.x);
     f32x4 acc = {};
     for (int node = 0; node < p.n_nodes; ++node) {
-        if (p.parent[node] >= 0) continue;   // roots only
+        const int par = p.parent[node];
+        if (par >= 0 && par < node) continue;   // roots only, by the forward scan's rule
         acc += *(const f32x4*)(node_dsin + ((size_t)node * p.hv + h) * GD * GD + e);
     }
     *(f32x4*)(p.d_init + (size_t)h * GD * GD + e) = acc;

@@ -88,6 +88,7 @@ struct GdnDev {
     // state ([Hv, 128, 128]; null: not wanted).
     const float* init;
     const float* d_states;
+    int d_states_last;                     // d_states is the last node's [Hv, 128, 128] alone
     float* d_init;
 };
 

@@ -247,13 +247,14 @@ def gdn_tree_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torc
                       d_o: torch.Tensor, tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True,
                       saved: Optional[torch.Tensor] = None, reference_truncated: bool = False,
                       initial_state: Optional[torch.Tensor] = None, d_states: Optional[torch.Tensor] = None,
-                      initial_state_grad: bool = False):
+                      initial_state_grad: bool = False, d_last_state: Optional[torch.Tensor] = None):
     """Gradients of sum(o * d_o) + sum(node_states * d_states) for
     ``gdn_tree_forward``'s outputs: dq, dk [T, Hk, 128] and dv [T, Hv, 128]
     in the dtype of v, dg and dbeta [T, Hv] float32, and with
     ``initial_state_grad`` also that of the initial state [Hv, 128, 128]
     (float32). ``d_states`` [n_nodes, Hv, 128, 128] may be None (no gradient
-    reaches the node states).
+    reaches the node states); ``d_last_state`` [Hv, 128, 128] instead gives
+    the gradient of the last node's state alone (no [n_nodes, ...] buffer).
     When q, k, v are the column blocks of one packed row buffer (the q/k/v
     split of a conv output), dq, dk, dv are the same column blocks of one new
     buffer, so the split's backward needs no concatenation. Recomputes the
@@ -279,7 +280,13 @@ def gdn_tree_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torc
         dv = torch.empty((T, Hv, HEAD_DIM), dtype=v.dtype, device=dev)
     dg = torch.empty((T, Hv), dtype=torch.float32, device=dev)
     dbeta = torch.empty_like(dg)
-    ds = _f32_block(d_states, (tree.n_nodes, Hv, HEAD_DIM, HEAD_DIM), "d_states")
+    if d_states is not None and d_last_state is not None:
+        raise ValueError("give d_states or d_last_state, not both")
+    if d_last_state is not None:
+        ds = _f32_block(d_last_state, (Hv, HEAD_DIM, HEAD_DIM), "d_last_state")
+        p.d_states_last_only = 1
+    else:
+        ds = _f32_block(d_states, (tree.n_nodes, Hv, HEAD_DIM, HEAD_DIM), "d_states")
     if ds is not None and ds.device != dev:
         raise ValueError("d_states must be on the device of q, k, v")
     d_init = torch.empty((Hv, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=dev) if initial_state_grad else None
@@ -302,10 +309,12 @@ class GdnTreeFunction(torch.autograd.Function):
     ``tt_gdn_tree_fwd``), backward ``tt_gdn_tree_bwd_saved`` (or the
     recomputing ``tt_gdn_tree_bwd``), as ``KEEP_FORWARD_STATES`` says. Both
     outputs (o and the node states) carry gradients, and so does the
-    optional initial state."""
+    optional initial state. With ``last_only`` the second output is the last
+    node's state alone ([Hv, 128, 128]), whose gradient goes to the kernel as
+    it is, without a zero-filled [n_nodes, ...] buffer around it."""
 
     @staticmethod
-    def forward(ctx, q, k, v, g, beta, initial_state, tree, scale, l2norm, reference_truncated):
+    def forward(ctx, q, k, v, g, beta, initial_state, tree, scale, l2norm, reference_truncated, last_only=False):
         keep = bool(KEEP_FORWARD_STATES)
         o, states, saved = _gdn_forward(q, k, v, g, beta, tree, scale, l2norm, keep, reference_truncated,
                                         initial_state)
@@ -315,39 +324,45 @@ class GdnTreeFunction(torch.autograd.Function):
         # with retain_graph (the reference's per-leaf schedule) reuses them.
         ctx.save_for_backward(q, k, v, g, beta, initial_state, *(() if saved is None else (saved,)))
         ctx.tree, ctx.scale, ctx.l2norm, ctx.trunc = tree, scale, l2norm, reference_truncated
+        ctx.last_only = last_only
         # No zero-filled gradient is made for an output the loss does not use.
         ctx.set_materialize_grads(False)
-        return o, states
+        return o, (states[-1].clone() if last_only else states)
 
     @staticmethod
     def backward(ctx, d_o, d_states):
         if d_o is None and d_states is None:
-            return (None,) * 10
+            return (None,) * 11
         q, k, v, g, beta, s0, *kept = ctx.saved_tensors
         if d_o is None:
             d_o = torch.zeros(v.shape, dtype=v.dtype, device=v.device)
         want_init = s0 is not None and ctx.needs_input_grad[5]
         res = gdn_tree_backward(q, k, v, g, beta, d_o, ctx.tree, ctx.scale, ctx.l2norm,
                                 saved=kept[0] if kept else None, reference_truncated=ctx.trunc, initial_state=s0,
-                                d_states=d_states, initial_state_grad=want_init)
+                                d_states=None if ctx.last_only else d_states, initial_state_grad=want_init,
+                                d_last_state=d_states if ctx.last_only else None)
         dq, dk, dv, dg, dbeta = res[:5]
         d_init = res[5].reshape(s0.shape).to(s0.dtype) if want_init else None
         return (dq.reshape(q.shape).to(q.dtype), dk.reshape(k.shape).to(k.dtype), dv.reshape(v.shape).to(v.dtype),
                 dg.reshape(g.shape).to(g.dtype), dbeta.reshape(beta.shape).to(beta.dtype), d_init,
-                None, None, None, None)
+                None, None, None, None, None)
 
 
 def gdn_tree(q, k, v, g, beta, tree: GdnTree, scale: Optional[float] = None, l2norm: bool = True,
-             reference_truncated: bool = False, initial_state: Optional[torch.Tensor] = None):
+             reference_truncated: bool = False, initial_state: Optional[torch.Tensor] = None,
+             last_state_only: bool = False):
     """Autograd-aware ``gdn_tree_forward``: (o, node_states), differentiable
     in q, k, v, g, beta and ``initial_state`` ([Hv, 128, 128], or [1, Hv,
     128, 128]; every root's state, zero when None). When any input requires
     a gradient and ``KEEP_FORWARD_STATES`` is set, the forward keeps its chunk
-    terms and states for the backward."""
+    terms and states for the backward. ``last_state_only``: the second output
+    is the last node's state [Hv, 128, 128] instead of all node states."""
     ins = (q, k, v, g, beta) + (() if initial_state is None else (initial_state,))
     if not (torch.is_grad_enabled() and any(t.requires_grad for t in ins)):
-        return gdn_tree_forward(q, k, v, g, beta, tree, scale, l2norm, reference_truncated, initial_state)
-    return GdnTreeFunction.apply(q, k, v, g, beta, initial_state, tree, scale, l2norm, bool(reference_truncated))
+        o, states = gdn_tree_forward(q, k, v, g, beta, tree, scale, l2norm, reference_truncated, initial_state)
+        return o, (states[-1] if last_state_only else states)
+    return GdnTreeFunction.apply(q, k, v, g, beta, initial_state, tree, scale, l2norm, bool(reference_truncated),
+                                 bool(last_state_only))
 
 
 def torch_chunk_gated_delta_rule_tree_varlen(query, key, value, g, beta, chunk_boundaries, chunk_parent_map,
@@ -361,7 +376,7 @@ def torch_chunk_gated_delta_rule_tree_varlen(query, key, value, g, beta, chunk_b
     gives the reference function's own numbers (I + R + R^2 per node) instead
     of the exact rule."""
     tree = GdnTree.from_boundaries(chunk_boundaries, chunk_parent_map, query.device)
-    o, states = gdn_tree(query, key, value, g, beta, tree, l2norm=use_qk_l2norm_in_kernel,
-                         reference_truncated=reference_truncated, initial_state=initial_state)
-    last = states[-1][None] if output_final_state else None
+    o, last = gdn_tree(query, key, value, g, beta, tree, l2norm=use_qk_l2norm_in_kernel,
+                       reference_truncated=reference_truncated, initial_state=initial_state, last_state_only=True)
+    last = last[None] if output_final_state else None
     return o[None], last
