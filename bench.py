@@ -19,7 +19,8 @@ on a bounded sample on the host cores.
                     [--workload agent16k|gateway16k|rollout48k|gdn16k|prologue16k|leafce16k]
 
 Other workloads, each on the same 16K tree unless named:
-  gateway16k   the tree cut into 4096-token partitions (tree_grad_hybrid): every
+  gateway16k   the tree cut into 4096-token partitions (tree_grad_hybrid, with
+               the partitions of one cut node packed while they fit: 6), every
                partition's metadata and plan in one batched build, then each
                partition's attention fwd+bwd over its gateway prefix;
   rollout48k   one 8K prompt with 64 leaves (50,109 tokens);
@@ -291,7 +292,8 @@ def main():
         "data": "synthetic (seeded topology and N(0,1) q/k/v/dO)",
         "config": {"workload": args.workload, "packed_tokens": T, "visible_pairs_per_head": P,
                    "n_nodes": len(lens), "heads_q": HQ, "heads_kv": HKV, "head_dim": D,
-                   "layer": "one Qwen3-4B-shaped GQA attention layer", "parallelism": "single GPU"},
+                   "layer": "one Qwen3-4B-shaped GQA attention layer", "parallelism": "single GPU",
+                   **({"max_tokens": 4096, "partitions": len(segments)} if segments is not None else {})},
         "tokens_per_s": round(tokens_s, 1),
         "frac_of_peak": round(tflops / (PEAK_BF16_TFLOPS if args.dtype == "bf16" else PEAK_FP32_TFS), 4),
         "wall_s_timed": round(wall, 3),

@@ -216,7 +216,7 @@ def test_attention_gateway_partitions_full_size():
     roots, nodes = workloads.forest_from_topology(topo, TreeNode)
     gidx = {id(n): i for i, n in enumerate(nodes)}
     parts = partition_tree(roots, 4096)
-    plans = hybrid_plan(roots, 4096)
+    plans = hybrid_plan(roots, 4096, pack_siblings=False)
     assert len(parts) == len(plans) > 1
     g = torch.Generator(device=DEV).manual_seed(5)
     bf = torch.bfloat16

@@ -131,7 +131,7 @@ def test_hybrid_plan_gateways_match_oracle(legacy, c1_spec, q1_spec):
     for _ in range(40):
         cases.append((random_forest(rng, n_roots=rng.randint(1, 2), max_depth=6, max_len=6), rng.randint(2, 16)))
     for roots, mt in cases:
-        ours = H.hybrid_plan(roots, mt, legacy=legacy)
+        ours = H.hybrid_plan(roots, mt, legacy=legacy, pack_siblings=False)
         ref = hybrid_schedule(roots, mt, legacy=legacy)
         assert len(ours) == len(ref)
         for o, r in zip(ours, ref):
@@ -219,10 +219,12 @@ def test_reference_literal_sets_every_reference_option():
                                                  gdn_per_node_projections=True, fused_prologue=False,
                                                  fused_leaf_ce=False)
     assert literal_options(True, fused_prologue=True) == dict(fused_prologue=False)
+    assert literal_options(True, pack_siblings=True) == dict(pack_siblings=False)
     for fn, names in ((dfs_tree_forward, ("gdn_reference_truncated", "gdn_per_node_projections", "fused_prologue")),
                       (tree_grad_ckpt_sequential, ("fused_leaf_ce", "gdn_reference_truncated",
                                                    "gdn_per_node_projections", "fused_prologue")),
-                      (tree_grad_hybrid, ("legacy_gateway_bias", "fused_leaf_ce", "fused_prologue"))):
+                      (tree_grad_hybrid, ("legacy_gateway_bias", "fused_leaf_ce", "fused_prologue",
+                                          "pack_siblings"))):
         params = inspect.signature(fn).parameters
         assert "reference_literal" in params and params["reference_literal"].default is False
         for n in names:
@@ -230,3 +232,68 @@ def test_reference_literal_sets_every_reference_option():
     for mod in ("ckpt", "hybrid", "dfs_tree_forward"):     # every module-level name the drivers use resolves
         m = __import__(f"tree_training_amd.{mod}", fromlist=["x"])
         assert m.literal_options is literal_options
+
+
+def test_packed_partitions_see_exactly_the_whole_tree(c1_spec):
+    """pack_sibling_partitions merges only partitions of one cut node of one
+    parent, within max_tokens, keeps every node in exactly one partition and
+    parents before children; and with the inherited gateway bias every query
+    of every packed partition sees (gateway keys with bias 0, plus its own
+    partition's tree mask) exactly its ancestors-or-self in the whole forest,
+    token by token — so packed and unpacked runs compute the same attention."""
+    from oracle.tree_meta import mask_from_horizon, meta_closed_form
+    cases = [(forest_from_spec(c1_spec["nodes"], TreeNode)[0], mt) for mt in (1000, 20, 10, 6)]
+    rng = random.Random(11)
+    for _ in range(30):
+        cases.append((random_forest(rng, n_roots=rng.randint(1, 2), max_depth=5, max_len=6), rng.randint(3, 20)))
+    merged_any = False
+    for roots, mt in cases:
+        parent_of, order = {}, []
+        stack = list(reversed(roots))
+        while stack:
+            n = stack.pop()
+            order.append(n)
+            for c in reversed(n.children):
+                parent_of[id(c)] = n
+                stack.append(c)
+        raw = H.partition_tree(roots, mt)
+        parts = H.pack_sibling_partitions(H.partition_tree(roots, mt), mt)
+        merged_any |= len(parts) < len(raw)
+        assert sorted(id(n) for p in parts for n in p.dfs_nodes) == sorted(id(n) for n in order)
+        pos = {id(p): i for i, p in enumerate(parts)}
+        for i, p in enumerate(parts):
+            if p.parent is not None:
+                assert pos[id(p.parent)] < i
+            if len(p.entry_nodes) > 1:
+                assert p.token_count <= mt
+                assert all(parent_of[id(e)] is p.parent_cut_node for e in p.entry_nodes)
+        plans = H.hybrid_plan(roots, mt)
+        assert len(plans) == len(parts)
+
+        def ancestors_or_self(n):
+            out = set()
+            while n is not None:
+                out.add(id(n))
+                n = parent_of.get(id(n))
+            return out
+
+        gw_tokens = {}
+        for p, pl in zip(parts, plans):
+            node_len, par, nodes = H._flatten_partition(p)
+            own = [(id(n), j) for n in nodes for j in range(len(n.token_ids))]
+            gtok = gw_tokens.get(id(p), [])
+            assert len(gtok) == pl["past_len"]
+            vis_g = [t for t, b in zip(gtok, pl["bias"].tolist() if gtok else []) if b == 0.0]
+            mask = mask_from_horizon(meta_closed_form(node_len, par)["horizon"])
+            for qi, (nid, j) in enumerate(own):
+                node = next(n for n in nodes if id(n) == nid)
+                anc = ancestors_or_self(node)
+                want = {(m, k) for m in anc for k in range(len(next(x for x in order if id(x) == m).token_ids))
+                        if m != nid or k <= j}
+                got = set(vis_g) | {own[kj] for kj in np.nonzero(mask[qi])[0]}
+                assert got == want, (mt, qi)
+            _, _, end, _, _, _ = H._dfs_info_for_partition(p)
+            for child in parts:
+                if child.parent is p:
+                    gw_tokens[id(child)] = gtok + own[:end[id(child.parent_cut_node)]]
+    assert merged_any

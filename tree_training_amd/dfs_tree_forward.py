@@ -84,11 +84,12 @@ def literal_options(reference_literal: bool, **opts) -> dict:
     arithmetic switched to the reference's when ``reference_literal``: the
     legacy gateway bias (tree_grad_hybrid.py:206-209), the truncated
     whole-node GDN correction I + R + R^2 (tree_dfs_ssm.py:114-126), node by
-    node GDN projections, and transformers' own q/k norm + rotary and
-    lm_head + cross-entropy instead of the fused kernels."""
+    node GDN projections, transformers' own q/k norm + rotary and
+    lm_head + cross-entropy instead of the fused kernels, and the reference's
+    partition list (no sibling packing)."""
     if reference_literal:
         lit = dict(legacy_gateway_bias=True, gdn_reference_truncated=True, gdn_per_node_projections=True,
-                   fused_prologue=False, fused_leaf_ce=False)
+                   fused_prologue=False, fused_leaf_ce=False, pack_siblings=False)
         opts.update({k: v for k, v in lit.items() if k in opts})
     return opts
 

@@ -87,6 +87,38 @@ def partition_tree(roots: List[TreeNode], max_tokens: int) -> List[SubtreePartit
     return partitions
 
 
+def pack_sibling_partitions(partitions: List[SubtreePartition], max_tokens: int) -> List[SubtreePartition]:
+    """Merges partitions that hang off the same cut node of the same parent
+    partition into one partition with several entry nodes (the reference's
+    ``SubtreePartition.entry_nodes`` is a list), consecutive siblings while
+    their token counts sum to at most ``max_tokens``. Siblings see the same
+    gateway, so a merged partition computes what its members compute, in one
+    model pass instead of several small ones (the reference gives every
+    over-budget child of a cut node a partition of its own,
+    tree_grad_hybrid.py:93-94). Parents still precede children; the merged
+    partition takes the place of its first member."""
+    out: List[SubtreePartition] = []
+    holder: Dict[int, SubtreePartition] = {}     # id(original) -> partition that holds it now
+    open_bin: Dict[Tuple[int, int], SubtreePartition] = {}
+    for p in partitions:
+        if p.parent is not None:
+            p.parent = holder[id(p.parent)]
+            key = (id(p.parent), id(p.parent_cut_node))
+            b = open_bin.get(key)
+            if b is not None and b.token_count + p.token_count <= max_tokens:
+                b.entry_nodes = list(b.entry_nodes) + list(p.entry_nodes)
+                b.dfs_nodes.extend(p.dfs_nodes)
+                b.cut_node_set |= p.cut_node_set
+                b.leaf_node_set |= p.leaf_node_set
+                b.token_count += p.token_count
+                holder[id(p)] = b
+                continue
+            open_bin[key] = p
+        holder[id(p)] = p
+        out.append(p)
+    return out
+
+
 # ---------------------------------------------------------------------------
 # 2. DFS info of one partition
 # ---------------------------------------------------------------------------
@@ -317,7 +349,7 @@ def _prebuild_partitions(partitions, children_of, dev, legacy: bool):
 def tree_grad_hybrid(model, roots: List[TreeNode], leaf_loss_fn: Callable[[torch.Tensor, TreeNode], torch.Tensor],
                      max_tokens: int, legacy_gateway_bias: bool = False, summed_backward: bool = False,
                      fused_leaf_ce: bool = True, fused_prologue: bool = True,
-                     reference_literal: bool = False) -> None:
+                     reference_literal: bool = False, pack_siblings: bool = True) -> None:
     """Hybrid tree training (tree_grad_hybrid.py:434-539); grads accumulate in ``.grad``.
 
     model        : HF causal LM (Qwen3 family), train mode, zero_grad() already called
@@ -336,12 +368,16 @@ def tree_grad_hybrid(model, roots: List[TreeNode], leaf_loss_fn: Callable[[torch
                    as with ``summed_backward``; other losses get logits.
     fused_prologue : the fused q/k RMSNorm + rotary kernel (False: transformers'
                    own modules).
+    pack_siblings : merge the partitions of one cut node while they fit
+                   ``max_tokens`` (``pack_sibling_partitions``; the same
+                   gradients up to summation order, fewer and larger model
+                   passes); False keeps the reference's partition list.
     reference_literal : every option at the reference's arithmetic — the legacy
                    gateway bias, transformers' prologue and logits + CE, the
                    per-leaf backward schedule (``literal_options``).
     """
     o = literal_options(reference_literal, legacy_gateway_bias=legacy_gateway_bias,
-                        fused_leaf_ce=fused_leaf_ce, fused_prologue=fused_prologue)
+                        fused_leaf_ce=fused_leaf_ce, fused_prologue=fused_prologue, pack_siblings=pack_siblings)
     legacy_gateway_bias, fused_leaf_ce = o["legacy_gateway_bias"], o["fused_leaf_ce"]
     if reference_literal:
         summed_backward = False
@@ -349,6 +385,8 @@ def tree_grad_hybrid(model, roots: List[TreeNode], leaf_loss_fn: Callable[[torch
     dtype = next(model.parameters()).dtype
     fused = fused_leaf_ce and fused_ce_capable(model, leaf_loss_fn)
     partitions = partition_tree(roots, max_tokens)
+    if o["pack_siblings"]:
+        partitions = pack_sibling_partitions(partitions, max_tokens)
     children_of: Dict[int, List[Tuple[TreeNode, SubtreePartition]]] = {id(p): [] for p in partitions}
     for p in partitions:
         if p.parent is not None:
@@ -424,11 +462,15 @@ def make_tree_loss_fn(leaf_labels: List[torch.Tensor], leaf_nodes: List[TreeNode
 # ---------------------------------------------------------------------------
 # 6. model-free schedule (benchmarks, inspection)
 # ---------------------------------------------------------------------------
-def hybrid_plan(roots: List[TreeNode], max_tokens: int, legacy: bool = False) -> List[dict]:
+def hybrid_plan(roots: List[TreeNode], max_tokens: int, legacy: bool = False,
+                pack_siblings: bool = True) -> List[dict]:
     """Per-partition attention problems of ``tree_grad_hybrid`` without a model:
     partition-local (node_len, parent), pos_offset, and the gateway length and
-    bias each partition attends to, in creation order."""
+    bias each partition attends to, in creation order (``pack_siblings`` as in
+    ``tree_grad_hybrid``)."""
     partitions = partition_tree(roots, max_tokens)
+    if pack_siblings:
+        partitions = pack_sibling_partitions(partitions, max_tokens)
     gw_of: Dict[int, dict] = {}
     children_of: Dict[int, list] = {id(p): [] for p in partitions}
     for p in partitions:
