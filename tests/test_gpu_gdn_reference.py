@@ -168,10 +168,11 @@ def test_reference_mode_saved_forward_equals_recompute(dtype):
 def test_reference_mode_agent16k_two_heads_matches_oracle():
     """Full c5 topology (agent tree, 16,318 tokens, 54 nodes of 64-512 tokens,
     realistic gates), fp32, one q/k head shared by two v heads, against the
-    literal float64 oracle. Outputs: < 1e-5. Node states after 512-token
-    nodes: within twice what the reference's own float32 evaluation of the
-    same rule reaches against float64 (measured in the test, about 3e-5),
-    the best a float32 drop-in can be held to at this size."""
+    literal float64 oracle. Outputs and node states: < 1e-5 — tighter than
+    the reference's own float32 evaluation of the same rule, which the test
+    measures too (about 3e-5 on the states after 512-token nodes: its
+    cumulative decays lose ~|G| 2^-24 in one float; the kernels carry them in
+    two)."""
     lens, par = agent_tree(0)
     T = sum(lens)
     q, k, v, g, beta = _inputs(T, 1, 2, 17, realistic_gates=True)
@@ -181,10 +182,10 @@ def test_reference_mode_agent16k_two_heads_matches_oracle():
     with torch.no_grad():
         _, st32 = ogdn.gdn_tree_reference_torch(*[torch.from_numpy(x) for x in (q, k, v, g, beta)], lens, par,
                                                 return_states=True)
-    st_bar = max(1e-5, 2 * _rel(st32.double().numpy(), st_ref))
-    print(f"  o {_rel(o, o_ref):.2e}  states {_rel(st, st_ref):.2e} (bar {st_bar:.2e})", flush=True)
+    print(f"  o {_rel(o, o_ref):.2e}  states {_rel(st, st_ref):.2e} (the reference's own float32: "
+          f"{_rel(st32.double().numpy(), st_ref):.2e})", flush=True)
     assert _rel(o, o_ref) < 1e-5, _rel(o, o_ref)
-    assert _rel(st, st_ref) < st_bar, (_rel(st, st_ref), st_bar)
+    assert _rel(st, st_ref) < 1e-5, _rel(st, st_ref)
 
 
 def test_reference_mode_16k_tree_per_path_equivalence():
