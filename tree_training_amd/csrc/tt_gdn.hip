@@ -967,6 +967,8 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
         const int h = hk * p.rep + hh;
         const size_t chn = (size_t)c * p.hv + h;
         const float* cw = ws + chn * kWsChunk;
+        // e^{G_L} <S, dS> for dg, loaded here so its latency hides behind the head's work
+        const float gsd = t < GC ? sdot[chn] : 0.0f;
         __syncthreads();   // the previous head's readers are done
         if (t < GC) {
             L.G[t] = cw[kWsG + t];
@@ -1140,6 +1142,27 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
                 for (int e = 0; e < 4; ++e) dka[4 * m + e] += x[e];
             }
         }
+        // M3 holds every pair term of dG (its last writers passed a barrier):
+        // its rows become exclusive prefix sums, M3[i][c] = sum_{j < c} p_ij
+        // (thread (i, s): four columns, a scan over the row's eight threads),
+        // for the dg sums below.
+        {
+            f32x4 v = *(const f32x4*)&L.M3[i * MS + 4 * s];
+            const float tot = v[0] + v[1] + v[2] + v[3];
+            float pre = __shfl_up(tot, 1, 8);
+            if (s == 0) pre = 0.0f;
+#pragma unroll
+            for (int o = 1; o < 8; o <<= 1) {
+                const float up = __shfl_up(pre, o, 8);
+                if (s >= o) pre += up;
+            }
+            f32x4 x;
+            x[0] = pre;
+            x[1] = pre + v[0];
+            x[2] = x[1] + v[1];
+            x[3] = x[2] + v[2];
+            *(f32x4*)&L.M3[i * MS + 4 * s] = x;
+        }
         // The output state S_out = e^{G_L} S + (e^{G_L - G} k^)^T V': dk^ and dG.
         {
             const float* kr = dkto + chn * GC * GD + i * GD;
@@ -1170,30 +1193,24 @@ __global__ __launch_bounds__(GT) void gdn_bwd_chunk_kernel(GdnDev p, const TIn* 
         // (Crow) reaches it when i < t; e^{G_L} S's reaches every t. Summing
         // just those sets, rather than suffix sums of row minus column sums
         // in which the pairs inside [t, L] cancel only up to rounding, keeps
-        // dg accurate relative to its own size. First M3's rows become
-        // exclusive prefix sums, M3[i][c] = sum_{j < c} p_ij.
-        __syncthreads();
-        if (t < GC) {
-            float run = 0.0f;
-#pragma unroll 4
-            for (int c = 0; c < GC; ++c) {
-                const float x = L.M3[t * MS + c];
-                L.M3[t * MS + c] = run;
-                run += x;
-            }
-        }
+        // dg accurate relative to its own size: dg_t = sum_{i >= t} M3[i][t]
+        // + sum_{i < t} c_i + the e^{G_L} term + the suffix sum of the terms
+        // of e^{G_i} alone.
         __syncthreads();
         if (t < GC) {
             float cross = 0.0f, cpre = 0.0f;
-            for (int r = t; r < GC; ++r) cross += L.M3[r * MS + t];
-            for (int r = 0; r < t; ++r) cpre += L.Crow[r];
+#pragma unroll 4
+            for (int r = 0; r < GC; ++r) {
+                cross += r >= t ? L.M3[r * MS + t] : 0.0f;
+                cpre += r < t ? L.Crow[r] : 0.0f;
+            }
             float dG = L.Grow[t];
 #pragma unroll
             for (int o = 1; o < GC; o <<= 1) {
                 const float up = __shfl_down(dG, o, GC);
                 if (t + o < GC) dG += up;
             }
-            dG += cross + cpre + expf(gl) * sdot[chn];
+            dG += cross + cpre + expf(gl) * gsd;
             if constexpr (TRUNC) dG += trg[chn * GC + t];
             if (t < len) dg[(int64_t)(start + t) * p.hv + h] = dG;
         }
