@@ -117,8 +117,9 @@ def gateway_split(topo, max_tokens=4096):
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: the tree-attention path has no multi-GPU mode in this build "
-              "(see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: the tree-attention path has no multi-GPU mode (a tree's "
+              "key tiles would shard by kv-head group or by subtree across GPUs); run with --gpus 1",
+              file=sys.stderr)
         sys.exit(2)
     if args.workload == "gdn16k":
         return run_gdn(args)
