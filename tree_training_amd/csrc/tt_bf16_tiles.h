@@ -436,7 +436,10 @@ __global__ __launch_bounds__(256) void bwd_split_finalize_det_kernel(AttnDev a, 
             gk += *(const f32x4*)(bw.dk_slot + sidx);
             gv += *(const f32x4*)(bw.dv_slot + sidx);
         }
-        if (lacks) gk = gv = (f32x4){NAN, NAN, NAN, NAN};
+        if (lacks) {   // a quiet NaN by its bits (this header is also built without NaN semantics)
+            const float qnan = __int_as_float(0x7fc00000);
+            gk = gv = (f32x4){qnan, qnan, qnan, qnan};
+        }
         if (key < a.n_past) {
             if (bw.dk_acc) {
                 *(f32x4*)(bw.dk_acc + widx) += gk;
