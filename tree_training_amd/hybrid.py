@@ -96,7 +96,9 @@ def pack_sibling_partitions(partitions: List[SubtreePartition], max_tokens: int)
     model pass instead of several small ones (the reference gives every
     over-budget child of a cut node a partition of its own,
     tree_grad_hybrid.py:93-94). Parents still precede children; the merged
-    partition takes the place of its first member."""
+    partition takes the place of its first member. The partitions are updated
+    in place (a merged partition is its first member, extended; the children
+    of any member point at it), so pass a fresh ``partition_tree`` list."""
     out: List[SubtreePartition] = []
     holder: Dict[int, SubtreePartition] = {}     # id(original) -> partition that holds it now
     open_bin: Dict[Tuple[int, int], SubtreePartition] = {}
