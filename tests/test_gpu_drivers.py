@@ -199,3 +199,43 @@ def test_sequential_and_hybrid_bf16():
         r = _max_rel_params(seq, hyb)
         say(f"  hybrid bf16 max_tokens={mt} vs sequential {r:.3e}")
         assert r < 2e-2
+
+
+def test_drivers_deterministic_mode_is_bitwise_repeatable():
+    """Under torch.use_deterministic_algorithms the drivers' attention backward
+    takes TT_BWD_DETERMINISTIC with the workspace sized from the tree
+    (KeyPlan.det_slots): on a 2,112-token forest whose 1,024-token root is
+    seen by every query (so its key tiles split into several dK/dV work
+    items), and cut at max_tokens=1,200 (gateway tiles split too), two
+    tree_grad_hybrid runs and two tree_grad_ckpt_sequential runs give bitwise
+    equal parameter gradients, within 1e-5 of the default (atomic) runs."""
+    from tree_training_amd.ckpt import tree_grad_ckpt_sequential
+    from tree_training_amd.hybrid import tree_grad_hybrid
+    from tree_training_amd.tree import TreeNode
+    from tree_training_amd.workloads import forest_from_topology
+    topo = ([1024, 300, 200, 288, 150, 150], [-1, 0, 1, 0, 3, 0])
+    roots, nodes = forest_from_topology(topo, TreeNode, vocab=1000, seed=3)
+    leaves = [n for n in nodes if not n.children]
+    labels = _labels(leaves)
+    fn = _loss_fn(labels, len(leaves))
+    model = make_qwen3("tiny", layers=2).to(DEV)
+    runs = {}
+    prev = torch.are_deterministic_algorithms_enabled()
+    for det in (True, False):
+        torch.use_deterministic_algorithms(det, warn_only=True)
+        try:
+            for name, run in (("hybrid", lambda: tree_grad_hybrid(model, roots, fn, 1200)),
+                              ("sequential", lambda: tree_grad_ckpt_sequential(model, roots, fn))):
+                say(f"{name} deterministic={det}")
+                runs[(name, det, 0)] = _grads(model, run)
+                if det:
+                    runs[(name, det, 1)] = _grads(model, run)
+        finally:
+            torch.use_deterministic_algorithms(prev)
+    for name in ("hybrid", "sequential"):
+        a, b, c = runs[(name, True, 0)], runs[(name, True, 1)], runs[(name, False, 0)]
+        for k in a:
+            assert torch.equal(a[k], b[k]), (name, k)
+        r = _max_rel_params(c, a)
+        say(f"  {name}: deterministic vs atomic max_rel {r:.3e}")
+        assert r < 1e-5, (name, r)
