@@ -318,6 +318,10 @@ def test_gdn_bwd_validation():
     assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, *args(want - 4, ds=V, di=V)) == _lib.TT_E_WORKSPACE
     assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, *args(want, ds=ctypes.c_void_p(20))) == _lib.TT_E_ARG
     assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, *args(want, di=ctypes.c_void_p(24))) == _lib.TT_E_ARG
+    # d_states_last_only: a flag (0: all node states' gradients, 1: the last node's alone)
+    p.d_states_last_only = 2
+    assert lib.tt_gdn_tree_bwd(ctypes.byref(p), DO, *args(want, ds=V)) == _lib.TT_E_ARG
+    p.d_states_last_only = 0
     # dq/dk/dv: the row rules of q (a null, misaligned or short-strided output is refused) ...
     for bad in (_lib.TTTensor(None, 16 * 128, 128), _lib.TTTensor(24, 16 * 128, 128), _lib.TTTensor(16, 64, 128),
                 _lib.TTTensor(16, 16 * 128, 100)):
