@@ -50,17 +50,21 @@ __device__ __forceinline__ void meta_nodes_body(
             if (v < 1) atomicOr(&s_err, TT_STATUS_BAD_LEN);
             if (p < -1 || p >= i) atomicOr(&s_err, TT_STATUS_BAD_PARENT);
         }
-        s_scan[tid] = v;
-        __syncthreads();
-        for (int o = 1; o < kNodeThreads; o <<= 1) {
-            int t = tid >= o ? s_scan[tid - o] : 0;
-            __syncthreads();
-            s_scan[tid] += t;
-            __syncthreads();
+        // a scan within each wave (shuffles), then over the waves' totals
+        const int lane = tid & 63, wave = tid >> 6;
+        int incl = v;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int up = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += up;
         }
-        if (i < n) start[i] = s_carry + s_scan[tid] - v;
+        if (lane == 63) s_scan[wave] = incl;
         __syncthreads();
-        if (tid == kNodeThreads - 1) s_carry += s_scan[tid];
+        int before = s_carry;
+        for (int w = 0; w < wave; ++w) before += s_scan[w];
+        if (i < n) start[i] = before + incl - v;
+        __syncthreads();
+        if (tid == kNodeThreads - 1) s_carry = before + incl;
         __syncthreads();
     }
     if (tid == 0 && s_carry != T) atomicOr(&s_err, TT_STATUS_BAD_TOTAL);
@@ -440,6 +444,7 @@ __device__ __forceinline__ void plan_finish_body(const uint8_t* __restrict__ cls
                                                  int32_t* __restrict__ kb_base, uint8_t* __restrict__ plan) {
     __shared__ int s_cnt[kFinishMax];
     __shared__ int s_kbo[kFinishMax];
+    __shared__ int s_kbw[kFinishMax];   // query range width of each key tile
     __shared__ int s_scan[1024];
     __shared__ int s_carry;
     __shared__ unsigned long long s_pairs;
@@ -448,16 +453,26 @@ __device__ __forceinline__ void plan_finish_body(const uint8_t* __restrict__ cls
         s_carry = 0;
         s_pairs = 0;
     }
-    // compaction: a wave per query block
+    for (int i = tid; i < n_kb; i += 1024) s_kbw[i] = kb_qhi[i] - kb_qlo[i];
+    // compaction: a wave per query block; the classes of 256 tiles are loaded
+    // at once, so a row waits on memory once per 256 tiles, not per 64
     const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     for (int row = wave; row < n_qb; row += 16) {
         int cnt = 0;
-        for (int base = 0; base < n_kt; base += 64) {
-            const int kt = base + lane;
-            const int c = kt < n_kt ? cls[(size_t)row * n_kt + kt] : 0;
-            const unsigned long long m = __ballot(c != 0);
-            if (c) row_list[(size_t)row * n_kt + cnt + __popcll(m & below)] = (kt << 1) | (c == 2 ? 1 : 0);
-            cnt += __popcll(m);
+        for (int base = 0; base < n_kt; base += 256) {
+            int cv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int kt = base + 64 * u + lane;
+                cv[u] = kt < n_kt ? cls[(size_t)row * n_kt + kt] : 0;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int kt = base + 64 * u + lane, c = cv[u];
+                const unsigned long long m = __ballot(c != 0);
+                if (c) row_list[(size_t)row * n_kt + cnt + __popcll(m & below)] = (kt << 1) | (c == 2 ? 1 : 0);
+                cnt += __popcll(m);
+            }
         }
         if (lane == 0) {
             s_cnt[row] = cnt;
@@ -476,10 +491,10 @@ __device__ __forceinline__ void plan_finish_body(const uint8_t* __restrict__ cls
         row_order[rank] = i;
     }
     for (int i = tid; i < n_kb; i += 1024) {
-        const int c = kb_qhi[i] - kb_qlo[i];
+        const int c = s_kbw[i];
         int rank = 0;
         for (int j = 0; j < n_kb; ++j) {
-            const int cj = kb_qhi[j] - kb_qlo[j];
+            const int cj = s_kbw[j];
             rank += (cj > c) || (cj == c && j < i);
         }
         s_kbo[rank] = i;
@@ -489,7 +504,8 @@ __device__ __forceinline__ void plan_finish_body(const uint8_t* __restrict__ cls
     for (int i = tid; i < n_pb; i += 1024) pairs += pair_part[i];
     atomicAdd(&s_pairs, pairs);
     __syncthreads();
-    // work-item offsets of the ordered key tiles
+    // work-item offsets of the ordered key tiles: a scan within each wave
+    // (shuffles), then over the 16 waves' totals
     for (int base = 0; base < n_kb; base += 1024) {
         const int r = base + tid;
         int v = 0;
@@ -497,17 +513,19 @@ __device__ __forceinline__ void plan_finish_body(const uint8_t* __restrict__ cls
             const int kb = s_kbo[r];
             v = tt_kb_items(kb_qlo[kb], kb_qhi[kb], qch);
         }
-        s_scan[tid] = v;
-        __syncthreads();
-        for (int o = 1; o < 1024; o <<= 1) {
-            const int t = tid >= o ? s_scan[tid - o] : 0;
-            __syncthreads();
-            s_scan[tid] += t;
-            __syncthreads();
+        int incl = v;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int up = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += up;
         }
-        if (r < n_kb) kb_base[r] = s_carry + s_scan[tid] - v;
+        if (lane == 63) s_scan[wave] = incl;
         __syncthreads();
-        if (tid == 1023) s_carry += s_scan[tid];
+        int before = s_carry;
+        for (int w = 0; w < wave; ++w) before += s_scan[w];
+        if (r < n_kb) kb_base[r] = before + incl - v;
+        __syncthreads();
+        if (tid == 1023) s_carry = before + incl;
         __syncthreads();
     }
     if (tid == 0) {
