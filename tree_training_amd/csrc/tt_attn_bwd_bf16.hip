@@ -209,53 +209,59 @@ __global__ __launch_bounds__(256) void bwd_dq_combine_kernel(AttnDev a, BwdDev b
 struct KvStage {
     bf16 Q[TT_BQB * ROWX];     // swizzled: read row-wise and transposed
     bf16 Dn[TT_BQB * ROWX];
-    float lse[TT_BQB];     // log2 units
-    float ndlt[TT_BQB];    // -delta
+    float nlse[TT_BQB];    // -lse / scale: the score accumulators start here
+    float ndlt[TT_BQB];    // -delta: the dP accumulators start here
 };
 
-// Staging of the Q and dO rows of a 32-query block of head h, plus the
-// block's lse (log2 units, loaded by wave 0) and delta (wave 1). Loads are
-// unconditional within a wave, so nothing waits on the prefetch before
-// commit(). The last block of the queries (rows past n_q alias the last
-// query; their lse is +inf so they contribute nothing) is copied in commit().
+// Staging of a 32-query block of q head h: the Q and dO rows move straight
+// from global memory into the swizzled tiles (direct loads: waves 0-1 move Q,
+// waves 2-3 dO, five 1 KB pieces of the 10 KB tile each; the pieces' buffer
+// offsets per lane are fixed for the kernel, the padding bytes of each row
+// take row data that nothing reads); rows past the last query read as zeros.
+// The block's lse (wave 0) and delta (wave 1) come through registers.
 struct QBlockStager {
-    RowRegs<TT_BQB> q, d;
+    uint32_t vo[5];   // this lane's buffer offset in each of its wave's pieces
     float sv;
-    int q0, h;
-    __device__ __forceinline__ void begin(const AttnDev& a, const BwdDev& bw, int q0_, int h_) {
-        q0 = q0_;
-        h = h_;
-        if (q0 + TT_BQB <= a.n_q) {              // uniform branch
-            fetch_rows_buf(q, threadIdx.x, (const bf16*)a.q + (int64_t)q0 * a.q_st + h * a.q_sh, 2 * a.q_st);
-            fetch_rows_buf(d, threadIdx.x, (const bf16*)bw.dout + (int64_t)q0 * bw.do_st + h * bw.do_sh,
-                          2 * bw.do_st);
+    int q0;
+    __device__ __forceinline__ void init(const AttnDev& a, const BwdDev& bw) {
+        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+        const uint32_t stb = 2u * (uint32_t)(wave < 2 ? a.q_st : bw.do_st);
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            const int byte = 1024 * (5 * (wave & 1) + i) + 16 * lane;   // in the tile
+            const int r = byte / (2 * ROWX), b = byte - r * (2 * ROWX);
+            const int c = b < 2 * D ? ((b >> 4) ^ ((r >> 2) & 3)) : 0;   // 16-byte chunk of row r (tile_offx)
+            vo[i] = (uint32_t)r * stb + 16u * (uint32_t)c;
         }
-        const int wave = threadIdx.x >> 6;
+    }
+    // Issues the direct loads of query block q0_, q head h into stage S.
+    __device__ __forceinline__ void begin(const AttnDev& a, const BwdDev& bw, int q0_, int h, KvStage& S) {
+        q0 = q0_;
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const int rows = min(TT_BQB, a.n_q - q0);
+        const bool isq = wave < 2;
+        const uint32_t stb = 2u * (uint32_t)(isq ? a.q_st : bw.do_st);
+        const bf16* base = isq ? (const bf16*)a.q + (int64_t)q0 * a.q_st + h * a.q_sh
+                               : (const bf16*)bw.dout + (int64_t)q0 * bw.do_st + h * bw.do_sh;
+        const i32x4 rs = dma_rsrc(base, (uint32_t)(rows - 1) * stb + 2u * D);
+        const uint32_t l0 = lds_addr(isq ? S.Q : S.Dn) + 5120u * (uint32_t)(wave & 1);
+#pragma unroll
+        for (int i = 0; i < 5; ++i) lds_dma16(rs, l0 + 1024u * i, vo[i]);
         if (wave < 2) {
             const float* src = (wave == 0 ? bw.lse : bw.delta) + (size_t)h * a.n_q;
             sv = src[min(q0 + (int)(threadIdx.x & 31), a.n_q - 1)];
         }
     }
-    __device__ __forceinline__ void commit(const AttnDev& a, const BwdDev& bw, KvStage& S) {
-        if (q0 + TT_BQB <= a.n_q) {
-            store_rows<TT_BQB, SWZ>(q, threadIdx.x, S.Q);
-            store_rows<TT_BQB, SWZ>(d, threadIdx.x, S.Dn);
-        } else {
-            const int dc = (threadIdx.x & 15) * 8, r0 = threadIdx.x >> 4;
-            for (int i = 0; i < TT_BQB / 16; ++i) {
-                const int r = r0 + 16 * i;
-                const int64_t qq = min(q0 + r, a.n_q - 1);
-                *(bf16x8*)(S.Q + tile_offx(r, dc)) = *(const bf16x8*)((const bf16*)a.q + qq * a.q_st + h * a.q_sh + dc);
-                *(bf16x8*)(S.Dn + tile_offx(r, dc)) =
-                    *(const bf16x8*)((const bf16*)bw.dout + qq * bw.do_st + h * bw.do_sh + dc);
-            }
-        }
+    // Completes the stage (before the barrier that publishes it). Rows past
+    // the last query get -inf for -lse / scale, so they contribute nothing.
+    __device__ __forceinline__ void commit(const AttnDev& a, KvStage& S) {
         const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
         if (wave < 2 && lane < TT_BQB) {
             const bool in = q0 + lane < a.n_q;
-            if (wave == 0) S.lse[lane] = in ? sv * TT_LOG2E : INFINITY;
+            if (wave == 0) S.nlse[lane] = in ? -sv / a.scale : -INFINITY;
             else S.ndlt[lane] = in ? -sv : 0.0f;
         }
+        wait_vmem();
     }
 };
 
@@ -337,46 +343,69 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
         const int q_top = (q_stop > q_start) ? ((q_stop - 1) / TT_BQB) * TT_BQB : 0;
         const int n_steps = (q_stop > q_start) ? ((q_top - q_start) / TT_BQB + 1) * a.rep : 0;
         QBlockStager stg;
+        stg.init(a, bw);
         // step s covers query block q0 of q head g*rep + hh; (q0, hh) of the next
         // step are kept incrementally
         int q0 = q_top, hh = 0;
-        if (n_steps > 0) stg.begin(a, bw, q0, g * a.rep);
+        if (n_steps > 0) stg.begin(a, bw, q0, g * a.rep, st[0]);
         for (int s = 0; s < n_steps; ++s) {
             KvStage& S = st[s & 1];
-            stg.commit(a, bw, S);
+            stg.commit(a, S);
             __syncthreads();
             const int q0_cur = q0;
             if (++hh == a.rep) {
                 hh = 0;
                 q0 -= TT_BQB;
             }
-            if (s + 1 < n_steps) stg.begin(a, bw, q0, g * a.rep + hh);
+            // the other stage was last read in step s - 1, which every wave has left
+            if (s + 1 < n_steps) stg.begin(a, bw, q0, g * a.rep + hh, st[(s + 1) & 1]);
             const int q1 = min(q0_cur + TT_BQB, a.n_q);
             if (!((q0_cur < w_hi) && (q1 > w_lo))) continue;   // no key of this wave is seen here
             const bool full = w_all_vis && (w_maxlo <= q0_cur) && (w_minhi >= q1);
 
-            // S = Q K^T and dP = dO V^T: rows = queries, lane = key column.
-            f32x16 sc = (f32x16){}, dp = (f32x16){};
-            static_for<8>([&](auto tt) {
-                constexpr int t = decltype(tt)::value;
-                sc = mfma32(read_rowx<t>(S.Q, qro), kbv[t], sc);
-                dp = mfma32(read_rowx<t>(S.Dn, qro), read_row_operand<ROW_R>(Vs, wave * 32 + col, 16 * t + 8 * half), dp);
-            });
+            // S = Q K^T and dP = dO V^T (rows = queries, lane = key column),
+            // the accumulators started at -lse / scale and -delta of their rows:
+            // P = exp2(c S') and dS = P dP' need no row terms afterwards. The
+            // operands of MFMA pair t + 1 are read before pair t issues.
+            f32x16 sc, dp;
+#pragma unroll
+            for (int grp = 0; grp < 4; ++grp) {
+                const int r0 = 8 * grp + 4 * half;
+                const f32x4 nl = *(const f32x4*)(S.nlse + r0);
+                const f32x4 nd = *(const f32x4*)(S.ndlt + r0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    sc[4 * grp + e] = nl[e];
+                    dp[4 * grp + e] = nd[e];
+                }
+            }
+            {
+                bf16x8 qo[2], doo[2], vo[2];
+                qo[0] = read_rowx<0>(S.Q, qro);
+                doo[0] = read_rowx<0>(S.Dn, qro);
+                vo[0] = read_row_operand<ROW_R>(Vs, wave * 32 + col, 8 * half);
+                static_for<8>([&](auto tt) {
+                    constexpr int t = decltype(tt)::value;
+                    if constexpr (t + 1 < 8) {
+                        qo[(t + 1) & 1] = read_rowx<t + 1>(S.Q, qro);
+                        doo[(t + 1) & 1] = read_rowx<t + 1>(S.Dn, qro);
+                        vo[(t + 1) & 1] = read_row_operand<ROW_R>(Vs, wave * 32 + col, 16 * (t + 1) + 8 * half);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    sc = mfma32(qo[t & 1], kbv[t], sc);
+                    dp = mfma32(doo[t & 1], vo[t & 1], dp);
+                    __builtin_amdgcn_sched_barrier(0);
+                });
+            }
             // P = exp(S*scale - lse), dS = P (dP - delta); on the few steps where
             // some key of the wave is invisible to some query, those entries are
             // then zeroed (selects, so an overflowing exp of an invisible score
             // never propagates).
 #pragma unroll
-            for (int grp = 0; grp < 4; ++grp) {
-                const int r0 = 8 * grp + 4 * half;
-                const f32x4 l2 = *(const f32x4*)(S.lse + r0);
-                const f32x4 nd = *(const f32x4*)(S.ndlt + r0);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float p = fast_exp2(fmaf(sc[4 * grp + e], c, -l2[e]));
-                    sc[4 * grp + e] = p;
-                    dp[4 * grp + e] = p * (dp[4 * grp + e] + nd[e]);
-                }
+            for (int i = 0; i < 16; ++i) {
+                const float p = fast_exp2(sc[i] * c);
+                sc[i] = p;
+                dp[i] = p * dp[i];
             }
             if (!full) {
 #pragma unroll

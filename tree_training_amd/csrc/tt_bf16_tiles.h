@@ -18,11 +18,12 @@
 // out of the other LDS stage; one barrier per tile.
 //
 // dK/dV pass (key-major): a workgroup owns TT_BKB = 128 keys of one kv head;
-// each wave keeps K and V of 32 keys as MFMA operands and dK, dV of those
-// keys in fp32 accumulators, and walks a range of queries that can see them
-// (for a DFS-packed tree the range is contiguous: [first key, subtree end))
-// for the Hq/Hkv q heads of the group, with Q and dO blocks staged in LDS
-// (double-buffered) and read both row-wise and transposed. Ranges longer than
+// each wave keeps K of 32 keys in registers (V of the 128 keys sits in LDS)
+// and dK, dV of those keys in fp32 accumulators, and walks a range of queries
+// that can see them (for a DFS-packed tree the range is contiguous: [first
+// key, subtree end)) for the Hq/Hkv q heads of the group, with Q and dO blocks
+// moved into LDS by direct global -> LDS loads (double-buffered) and read both
+// row-wise and transposed. Ranges longer than
 // tt_qch(n_q) queries (half the largest power of two <= n_q, within
 // [256, 4096]) are split into several work items; a persistent grid walks the
 // items widest-first.
@@ -172,6 +173,33 @@ __device__ __forceinline__ void static_for(F&& f) {
     }
 }
 
+
+// Direct global -> LDS staging (buffer_load ... lds): no staging registers and
+// no LDS store instructions. One wave instruction moves 64 x 16 bytes from
+// per-lane buffer offsets to 1 KB of consecutive LDS bytes (lane l: byte 16 l
+// from the LDS address in M0). The loads are issued as inline assembly, so
+// the compiler's wait insertion neither tracks nor orders them: the issuing
+// wave waits for them (wait_vmem) before the barrier that publishes the data.
+// An operation the compiler does not count can only make its own vmcnt waits
+// stricter, never too weak, since the counter retires operations in issue
+// order.
+//
+// Raw buffer resource over [base, base + bytes); loads past the end read zeros.
+__device__ __forceinline__ i32x4 dma_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t p = (uint64_t)base;
+    return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)p),
+                 __builtin_amdgcn_readfirstlane((int)((uint32_t)(p >> 32) & 0xffff)),
+                 __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+}
+// (The compiler sets M0; the s_nop is the wait state between that write and
+// the load that reads it.)
+__device__ __forceinline__ void lds_dma16(const i32x4& rsrc, uint32_t lds, uint32_t voff) {
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_void*)p; }
+// s_waitcnt vmcnt(0): every vector memory operation of the wave, direct loads
+// included, has completed.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
 // Register staging: thread t holds rows (t/16) + 16*i (i < NROWS/16) at head
 // dims 8*(t%16) .. +7 of a tile; 16 lanes cover one 256-byte row, and a wave
