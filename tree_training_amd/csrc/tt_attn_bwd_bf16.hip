@@ -28,11 +28,12 @@ __global__ __launch_bounds__(256) void bwd_delta_bf16_kernel(AttnDev a, BwdDev b
 }
 
 // ----------------------------------------------------------------------------
-// backward: dQ (query-major, same tiling and pipeline as the forward)
+// backward: dQ (query-major, same tiling as the forward; key tiles staged by
+// direct global -> LDS loads)
 // ----------------------------------------------------------------------------
 struct DqStage {
-    bf16 K[TT_BK * ROWX];    // read as rows (S^T) and transposed (dQ^T): swizzled
-    bf16 V[TT_BK * ROW_R];   // read as rows only (dP^T)
+    bf16 K[TT_BK / 4 * GPITCH];   // read as rows (S^T) and transposed (dQ^T)
+    bf16 V[TT_BK / 4 * GPITCH];   // read as rows (dP^T)
     int lo[TT_BK];
     int hi[TT_BK];
 };
@@ -96,12 +97,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         it0 = cnt * (int)blockIdx.y / bw.n_split;
         it1 = cnt * ((int)blockIdx.y + 1) / bw.n_split;
     }
-    KvTileStager<SWZ, ROW_R> stg;
+    KvTileDma stg;
     Bounds nb;
-    const RowOffsX kro = row_offsx(col, half);   // this lane's key row in the K tile (either half)
-    const TrOffsX tro = tr_offsx(lane);
+    const RowOffsG kro = row_offsg(col, half);   // this lane's key row in either 32-key half of a tile
+    const TrOffsG tro = tr_offsg(lane);
     if (it1 > it0) {
-        stg.begin(a, list[it0] >> 1, g);
+        stg.begin(a, list[it0] >> 1, g, st[it0 & 1].K, st[it0 & 1].V);
         fetch_bounds(a, list[it0] >> 1, nb);
     }
     for (int it = it0; it < it1; ++it) {
@@ -110,27 +111,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         stg.commit(a, g, S.K, S.V);
         store_bounds(nb, S.lo, S.hi);
         __syncthreads();
-        {   // the last step re-stages its own tile: the loads are unconditional
-            const int kt1 = list[it + 1 < it1 ? it + 1 : it] >> 1;
-            stg.begin(a, kt1, g);
+        if (it + 1 < it1) {   // the other stage was last read in step it - 1, which every wave has left
+            const int kt1 = list[it + 1] >> 1;
+            stg.begin(a, kt1, g, st[(it + 1) & 1].K, st[(it + 1) & 1].V);
             fetch_bounds(a, kt1, nb);
         }
 
         // The tile as two 32-key halves: scores, dS and the dQ update of one
         // half before the next. Half the score registers are live at a time
-        // (234 VGPRs without spills, against 256 and a spill for the whole
-        // tile at once), so the operand reads run further ahead of their MFMAs.
-        // A partial tile's half that no query of the wave sees is skipped.
+        // (the whole tile at once spills), which leaves room for operand
+        // reads ahead of their MFMAs. A partial tile's half that no query of
+        // the wave sees is skipped.
         const int run = full ? 3 : visible_halves(S.lo, S.hi, qb * TT_BQ + wave * 32, lane);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             if (!((run >> b) & 1)) continue;
             f32x16 sh = (f32x16){}, dph = (f32x16){};
-            static_for<8>([&](auto tt) {
-                constexpr int t = decltype(tt)::value;
-                sh = mfma32(read_rowx<t>(S.K + 32 * b * ROWX, kro), qa[t], sh);
-                dph = mfma32(read_row_operand<ROW_R>(S.V, 32 * b + col, 16 * t + 8 * half), da[t], dph);
-            });
+            {   // the K / V operands of MFMA pair t + 1 are read before pair t issues
+                const bf16* kh = S.K + 8 * b * GPITCH;
+                const bf16* vh = S.V + 8 * b * GPITCH;
+                bf16x8 ko[2], vo[2];
+                ko[0] = read_rowg<0>(kh, kro);
+                vo[0] = read_rowg<0>(vh, kro);
+                static_for<8>([&](auto tt) {
+                    constexpr int t = decltype(tt)::value;
+                    if constexpr (t + 1 < 8) {
+                        ko[(t + 1) & 1] = read_rowg<t + 1>(kh, kro);
+                        vo[(t + 1) & 1] = read_rowg<t + 1>(vh, kro);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    sh = mfma32(ko[t & 1], qa[t], sh);
+                    dph = mfma32(vo[t & 1], da[t], dph);
+                    __builtin_amdgcn_sched_barrier(0);
+                });
+            }
             if (!full) mask_half(sh, S.lo + 32 * b, S.hi + 32 * b, qi, half);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -144,7 +158,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                         sh[r0 + 6], sh[r0 + 7]);
 #pragma unroll
                 for (int db = 0; db < 4; ++db)
-                    dq[db] = mfma32(read_trx(S.K, tro, 16 * (2 * b + s2), 32 * db), pk, dq[db]);
+                    dq[db] = mfma32(read_trg(S.K, tro, 16 * (2 * b + s2), db), pk, dq[db]);
             }
         }
     }

@@ -75,7 +75,7 @@ struct KvStageF {
     int hi[TT_BK];
 };
 
-// As KvTileStager: rows past the last key alias it (their empty bounds mask
+// Rows past the last key alias it (their empty bounds mask
 // them); a tile straddling gateway and own keys is copied at commit.
 struct KvTileStagerF {
     RowRegsF<TT_BK> k, v;

@@ -12,8 +12,8 @@ namespace {
 // forward
 // ----------------------------------------------------------------------------
 struct FwdStage {
-    bf16 K[TT_BK * ROW];
-    bf16 V[TT_BK * ROW];
+    bf16 K[TT_BK / 4 * GPITCH];   // row-group tiles: K read as rows, V transposed
+    bf16 V[TT_BK / 4 * GPITCH];
     int lo[TT_BK];
     int hi[TT_BK];
 };
@@ -57,11 +57,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         it0 = cnt * (int)blockIdx.y / sp.n;
         it1 = cnt * ((int)blockIdx.y + 1) / sp.n;
     }
-    KvTileStager<ROW, ROW> stg;
+    KvTileDma stg;
     Bounds nb;
+    const RowOffsG kro = row_offsg(col, half);   // this lane's key row in either 32-key half of a tile
+    const TrOffsG tro = tr_offsg(lane);
     if (it1 > it0) {
         const int kt0 = __builtin_amdgcn_readfirstlane(list[it0] >> 1);
-        stg.begin(a, kt0, g);
+        stg.begin(a, kt0, g, st[it0 & 1].K, st[it0 & 1].V);
         fetch_bounds(a, kt0, nb);
     }
     for (int it = it0; it < it1; ++it) {
@@ -70,9 +72,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         stg.commit(a, g, S.K, S.V);
         store_bounds(nb, S.lo, S.hi);
         __syncthreads();
-        {   // the last step re-stages its own tile: the loads are unconditional
-            const int kt1 = __builtin_amdgcn_readfirstlane(list[it + 1 < it1 ? it + 1 : it] >> 1);
-            stg.begin(a, kt1, g);
+        if (it + 1 < it1) {   // the other stage was last read in step it - 1, which every wave has left
+            const int kt1 = __builtin_amdgcn_readfirstlane(list[it + 1] >> 1);
+            stg.begin(a, kt1, g, st[(it + 1) & 1].K, st[(it + 1) & 1].V);
             fetch_bounds(a, kt1, nb);
         }
 
@@ -84,14 +86,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             bf16x8 kop[16];
             static_for<AH>([&](auto i) {
                 constexpr int n = decltype(i)::value;
-                kop[n] = read_row_operand<ROW>(S.K, 32 * (n >> 3) + col, 16 * (n & 7) + 8 * half);
+                kop[n] = read_rowg<n & 7>(S.K + 8 * (n >> 3) * GPITCH, kro);
             });
             s[0] = (f32x16){};
             s[1] = (f32x16){};
             static_for<16>([&](auto i) {
                 constexpr int n = decltype(i)::value;
                 if constexpr (n + AH < 16)
-                    kop[n + AH] = read_row_operand<ROW>(S.K, 32 * ((n + AH) >> 3) + col, 16 * ((n + AH) & 7) + 8 * half);
+                    kop[n + AH] = read_rowg<(n + AH) & 7>(S.K + 8 * ((n + AH) >> 3) * GPITCH, kro);
                 __builtin_amdgcn_sched_barrier(0);
                 s[n >> 3] = mfma32(kop[n], qa[n & 7], s[n >> 3]);
                 __builtin_amdgcn_sched_barrier(0);
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             ps1 = sum4_bf16(pk, 4, ps1);
 #pragma unroll
             for (int db = 0; db < 4; ++db)
-                o[db] = mfma32(read_tr_operand<ROW>(S.V, 16 * stp, 32 * db, lane), pk, o[db]);
+                o[db] = mfma32(read_trg(S.V, tro, 16 * stp, db), pk, o[db]);
         }
         l_run += ps0 + ps1;
     }

@@ -1,6 +1,6 @@
 // Device code shared by the bf16 tree-attention kernels (forward in
 // tt_attn_fwd_bf16.hip, backward in tt_attn_bwd_bf16.hip): LDS tile layout,
-// MFMA operand reads, global -> register -> LDS staging, visibility masks and
+// MFMA operand reads, global -> LDS staging, visibility masks and
 // the workgroup -> tile mapping.
 //
 // Tree-masked GQA flash attention for gfx950, bf16 in / fp32 accumulate.
@@ -13,9 +13,9 @@
 // probabilities feed O^T = V^T P^T straight from the accumulators. K and V
 // tiles sit in LDS in their natural [key][d] layout; the V^T (and, for dQ,
 // K^T) operands come out of them through gfx950's transposing LDS read
-// (ds_read_b64_tr_b16). Tiles are software-pipelined: the next tile's
-// global loads are in flight (in registers) while the current tile computes
-// out of the other LDS stage; one barrier per tile.
+// (ds_read_b64_tr_b16). Tiles are software-pipelined: the next tile's direct
+// global -> LDS loads are in flight while the current tile computes out of
+// the other LDS stage; one barrier per tile.
 //
 // dK/dV pass (key-major): a workgroup owns TT_BKB = 128 keys of one kv head;
 // each wave keeps K of 32 keys in registers (V of the 128 keys sits in LDS)
@@ -44,26 +44,18 @@ typedef __bf16 bf16;
 
 constexpr int D = 128;
 
-// LDS tiles hold tokens in their natural [token][d] order. Each thread loads
-// its slice of the next tile into registers while the current one computes,
-// then stores it. Row padding sets the bank pattern (64 banks x 4 bytes; a
-// 16-byte read serves 16 lanes per pass, a transposed 8-byte read 32):
-//   ROW_R = 272-byte rows for tiles read only as rows: 16 consecutive rows
-//           start on 16 different 16-byte bank groups, so a row operand read
-//           (16 lanes = 16 rows, one chunk) runs in one pass;
-//   ROW_T = 320-byte rows for tiles read only transposed: the 4 rows x 4
-//           chunks that 32 lanes of ds_read_b64_tr_b16 touch fall on 16
-//           different bank groups (4 r + c mod 16);
-//   tiles read both ways use the XOR-swizzled 320-byte layout below (ROWX);
-//   ROW = 288-byte rows (the forward's K and V tiles): row and transposed
-//           reads both run in two passes.
-// Stores (16 lanes = one whole row) are conflict-free in every layout. The
-// conflict-free layouts took the dQ and dK/dV passes' bank conflicts to zero
-// without changing their time, and made the forward 5 % slower than ROW: the
-// kernels are not bound by LDS bandwidth.
+// LDS tiles hold tokens in their natural [token][d] order. Layouts (64 banks
+// x 4 bytes; a 16-byte read serves 16 lanes per LDS pass, a transposed 8-byte
+// read 32):
+//   ROW_R = 272-byte rows (the dK/dV pass's V, read only as rows): 16
+//           consecutive rows start on 16 different 16-byte bank groups, so a
+//           row operand read (16 lanes = 16 rows, one chunk) runs in one pass;
+//   ROWX, the XOR-swizzled 320-byte rows below (the dK/dV pass's Q and dO
+//           blocks, read both ways);
+//   row groups (GPITCH below: the forward's and the dQ pass's K and V tiles,
+//           read both ways and filled by direct loads).
+// Every layout is free of bank conflicts for the reads made of it.
 constexpr int ROW_R = D + 8;
-constexpr int ROW_T = D + 32;
-constexpr int ROW = D + 16;
 template <int S>
 __device__ __forceinline__ int tile_off(int r, int d) { return r * S + d; }
 
@@ -104,18 +96,6 @@ __device__ __forceinline__ bf16x4 ds_read_tr(const bf16* p) {
     return __builtin_bit_cast(bf16x4, r);
 }
 
-// MFMA operand "column = head dim, k = 16 tokens" from a tile X: lane l gets
-// X[r0 + kappa(e)][dbase + (l & 31)], kappa(e) = 8*(e/4) + 4*(l>>5) + (e%4) —
-// the accumulator row order, so it pairs with probabilities taken straight
-// from a score accumulator.
-template <int S>
-__device__ __forceinline__ bf16x8 read_tr_operand(const bf16* X, int r0, int dbase, int lane) {
-    const int j = lane & 15, grp = lane >> 4;
-    const int d = dbase + 16 * (grp & 1) + 4 * (j & 3);
-    const int r = r0 + 4 * (grp >> 1) + (j >> 2);
-    return cat44(ds_read_tr(X + tile_off<S>(r, d)), ds_read_tr(X + tile_off<S>(r + 8, d)));
-}
-
 // MFMA operand "row = token, k = 16 head dims": X[r][d0 .. d0+7], d0 % 8 == 0.
 template <int S>
 __device__ __forceinline__ bf16x8 read_row_operand(const bf16* X, int r, int d0) {
@@ -146,8 +126,11 @@ template <int T>
 __device__ __forceinline__ bf16x8 read_rowx(const bf16* X, const RowOffsX& ro) {
     return *(const bf16x8*)(X + ((T & 1) ? ro.o : ro.e) + 32 * (T >> 1));
 }
-// Transposed operand (as read_tr_operand) from a swizzled tile: lane l gets
-// X[r0 + kappa(e)][dbase + (l & 31)], r0 % 16 == 0, dbase % 32 == 0.
+// Transposed operand "column = head dim, k = 16 tokens" from a swizzled tile:
+// lane l gets X[r0 + kappa(e)][dbase + (l & 31)], kappa(e) = 8*(e/4) +
+// 4*(l>>5) + (e%4) -- the accumulator row order, so it pairs with
+// probabilities taken straight from a score accumulator; r0 % 16 == 0,
+// dbase % 32 == 0.
 struct TrOffsX {
     int a, b;   // rows +0..7 and +8..15 of the 16-row group
 };
@@ -159,6 +142,51 @@ __device__ __forceinline__ TrOffsX tr_offsx(int lane) {
 }
 __device__ __forceinline__ bf16x8 read_trx(const bf16* X, const TrOffsX& to, int r0, int dbase) {
     return cat44(ds_read_tr(X + to.a + r0 * ROWX + dbase), ds_read_tr(X + to.b + r0 * ROWX + dbase));
+}
+
+// Row-group layout (the forward's and the dQ pass's key tiles): rows in groups
+// of four (1 KB, one direct-load instruction each) at a pitch of 1040 bytes;
+// 16-byte chunk c of row r sits at chunk c ^ 4 (r & 3) of its row. Row reads (16 lanes = 16 rows, one
+// chunk) and transposed reads (32 lanes = 4 rows x 4 chunks) both reach every
+// bank once per LDS pass.
+constexpr int GPITCH = 520;   // elements per group of four rows
+__device__ __forceinline__ int tile_offg(int r, int d) {
+    return (r >> 2) * GPITCH + (r & 3) * D + ((((d >> 3) ^ ((r & 3) << 2))) << 3) + (d & 7);
+}
+// Row operand of the lane's key row (col of a 32-row half) for head dims
+// 16 t + 8 half .. +7: at base[t >> 2][(t >> 1) & 1] + 16 (t & 1).
+struct RowOffsG {
+    int b[4];
+};
+__device__ __forceinline__ RowOffsG row_offsg(int col, int half) {
+    const int f = col & 3, rb = (col >> 2) * GPITCH + f * D + 8 * half;
+    RowOffsG o;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int v = 0; v < 2; ++v) o.b[2 * u + v] = rb + 64 * (u ^ (f >> 1)) + 32 * (v ^ (f & 1));
+    return o;
+}
+template <int T>
+__device__ __forceinline__ bf16x8 read_rowg(const bf16* X, const RowOffsG& ro) {
+    return *(const bf16x8*)(X + ro.b[T >> 1] + 16 * (T & 1));
+}
+// Transposed operand (as read_trx) of rows r0 .. r0 + 15 (r0 % 16 == 0), head
+// dims 32 db .. +31: at base[db] + (r0 / 4) GPITCH (+ 2 GPITCH: rows + 8).
+struct TrOffsG {
+    int b[4];
+};
+__device__ __forceinline__ TrOffsG tr_offsg(int lane) {
+    const int j = lane & 15, grp = lane >> 4, h = grp >> 1, q = j >> 2;
+    const int c = 2 * (grp & 1) + ((j & 3) >> 1), p = 4 * (j & 1);
+    TrOffsG o;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o.b[db] = h * GPITCH + q * D + 32 * (db ^ q) + 8 * c + p;
+    return o;
+}
+__device__ __forceinline__ bf16x8 read_trg(const bf16* X, const TrOffsG& to, int r0, int db) {
+    const bf16* x = X + to.b[db] + (r0 >> 2) * GPITCH;
+    return cat44(ds_read_tr(x), ds_read_tr(x + 2 * GPITCH));
 }
 
 template <int I>
@@ -196,6 +224,13 @@ __device__ __forceinline__ i32x4 dma_rsrc(const void* base, uint32_t bytes) {
 __device__ __forceinline__ void lds_dma16(const i32x4& rsrc, uint32_t lds, uint32_t voff) {
     asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
 }
+// Same, with a uniform byte offset (scalar register) added to every lane's.
+__device__ __forceinline__ void lds_dma16s(const i32x4& rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :
+                 : "v"(voff), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(soff)), "{m0}"(lds)
+                 : "memory");
+}
 __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_void*)p; }
 // s_waitcnt vmcnt(0): every vector memory operation of the wave, direct loads
 // included, has completed.
@@ -230,19 +265,12 @@ __device__ __forceinline__ void fetch_rows_buf(RowRegs<NROWS>& r, int tid, const
         r.x[i] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vo, (int)(16 * i * stb), 0));
 }
 
-// Layout tag of the XOR-swizzled tiles (tile_offx) for store_rows and
-// KvTileStager; every other layout is given by its row stride.
-constexpr int SWZ = -1;
-template <int S>
-__device__ __forceinline__ int tile_at(int r, int d) { return S == SWZ ? tile_offx(r, d) : tile_off<S>(r, d); }
-
-// Stores staged rows in a tile of row stride S elements, or (S == SWZ) the
-// XOR-swizzled layout.
+// Stores staged rows in a tile of row stride S elements.
 template <int NROWS, int S>
 __device__ __forceinline__ void store_rows(const RowRegs<NROWS>& r, int tid, bf16* X) {
     const int dc = (tid & 15) * 8, r0 = tid >> 4;
 #pragma unroll
-    for (int i = 0; i < NROWS / 16; ++i) *(bf16x8*)(X + tile_at<S>(r0 + 16 * i, dc)) = r.x[i];
+    for (int i = 0; i < NROWS / 16; ++i) *(bf16x8*)(X + tile_off<S>(r0 + 16 * i, dc)) = r.x[i];
 }
 
 __device__ __forceinline__ const bf16* key_row(const AttnDev& a, int kk, int g, bool isv) {
@@ -267,49 +295,43 @@ __device__ __forceinline__ void fetch_bounds(const AttnDev& a, int kt, Bounds& r
     }
 }
 
-// Staging of the K and V rows of key tile kt (rows past the last key alias
-// it; their empty bounds mask them) into tiles of row strides KS and VS
-// (SWZ: swizzled). begin() starts the loads for a stage; commit() makes them
-// resident in that stage (before the barrier).
-template <int KS, int VS>
-struct KvTileStager {
-    RowRegs<TT_BK> k, v;
+// Staging of key tile kt into row-group tiles: waves 0-1 move K, waves 2-3
+// V, eight 4-row groups each, by direct loads when the tile lies wholly in the gateway or wholly
+// in the own keys; a tile that straddles the two or runs past the last key
+// is copied in commit() (rows past the last key alias it; their empty bounds
+// mask them).
+struct KvTileDma {
     int k0;
-    bool direct;   // straddles gateway and own keys, or runs past the last key: loaded in commit()
-    __device__ __forceinline__ void begin(const AttnDev& a, int kt, int g) {
+    bool direct;
+    __device__ __forceinline__ void begin(const AttnDev& a, int kt, int g, bf16* K, bf16* V) {
         k0 = kt * TT_BK;
-        direct = false;
-        if (k0 + TT_BK <= a.n_past) {            // all gateway keys (uniform branch)
-            fetch_rows_buf(k, threadIdx.x, (const bf16*)a.kp + k0 * a.kp_st + g * a.kp_sh, 2 * a.kp_st);
-            fetch_rows_buf(v, threadIdx.x, (const bf16*)a.vp + k0 * a.vp_st + g * a.vp_sh, 2 * a.vp_st);
-        } else if (k0 >= a.n_past && k0 + TT_BK <= a.n_keys) {   // all own keys
-            const int64_t t0 = k0 - a.n_past;
-            fetch_rows_buf(k, threadIdx.x, (const bf16*)a.k + t0 * a.k_st + g * a.k_sh, 2 * a.k_st);
-            fetch_rows_buf(v, threadIdx.x, (const bf16*)a.v + t0 * a.v_st + g * a.v_sh, 2 * a.v_st);
-        } else {
-            direct = true;
-            // Defined on every path, so the staged values of consecutive tiles
-            // share registers (no copies at the loop latch).
+        const bool past = k0 + TT_BK <= a.n_past;
+        direct = !(past || (k0 >= a.n_past && k0 + TT_BK <= a.n_keys));
+        if (direct) return;   // uniform
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+        const bool isk = wave < 2;
+        const int64_t st = past ? (isk ? a.kp_st : a.vp_st) : (isk ? a.k_st : a.v_st);
+        const int64_t sh = past ? (isk ? a.kp_sh : a.vp_sh) : (isk ? a.k_sh : a.v_sh);
+        const bf16* t = (const bf16*)(past ? (isk ? a.kp : a.vp) : (isk ? a.k : a.v));
+        const int r0 = 32 * (wave & 1);                       // first row of this wave's groups
+        const int64_t row0 = (past ? k0 : k0 - a.n_past) + r0;
+        const uint32_t stb = 2u * (uint32_t)st;
+        const i32x4 rs = dma_rsrc(t + row0 * st + g * sh, 31u * stb + 2u * D);
+        const uint32_t vo = (uint32_t)(lane >> 4) * stb + 16u * (uint32_t)((lane & 15) ^ ((lane >> 4) << 2));
+        const uint32_t l0 = lds_addr(isk ? K : V) + 2u * GPITCH * (uint32_t)(r0 >> 2);
 #pragma unroll
-            for (int i = 0; i < TT_BK / 16; ++i) {
-                k.x[i] = zero8();
-                v.x[i] = zero8();
-            }
-        }
+        for (int i = 0; i < 8; ++i) lds_dma16s(rs, l0 + 2u * GPITCH * i, vo, 4u * i * stb);
     }
     __device__ __forceinline__ void commit(const AttnDev& a, int g, bf16* K, bf16* V) {
         if (!direct) {
-            store_rows<TT_BK, KS>(k, threadIdx.x, K);
-            store_rows<TT_BK, VS>(v, threadIdx.x, V);
+            wait_vmem();
             return;
         }
-        // At most two tiles per launch take this path: copied row by row,
-        // without prefetch (short register live ranges).
         const int dc = (threadIdx.x & 15) * 8, r0 = threadIdx.x >> 4;
         for (int i = 0; i < TT_BK / 16; ++i) {
             const int r = r0 + 16 * i, kk = min(k0 + r, a.n_keys - 1);
-            *(bf16x8*)(K + tile_at<KS>(r, dc)) = *(const bf16x8*)(key_row(a, kk, g, false) + dc);
-            *(bf16x8*)(V + tile_at<VS>(r, dc)) = *(const bf16x8*)(key_row(a, kk, g, true) + dc);
+            *(bf16x8*)(K + tile_offg(r, dc)) = *(const bf16x8*)(key_row(a, kk, g, false) + dc);
+            *(bf16x8*)(V + tile_offg(r, dc)) = *(const bf16x8*)(key_row(a, kk, g, true) + dc);
         }
     }
 };
