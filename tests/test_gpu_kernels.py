@@ -74,13 +74,36 @@ def test_meta_random_forests(seed):
     assert np.array_equal(m.node_off.cpu().numpy(), ref["node_off"])
 
 
-@pytest.mark.parametrize("name", ["agent16k", "rollout48k", "chain", "star"])
+def _branchy(n):
+    """n nodes, parents drawn below each node (pre-order), lengths 1..9."""
+    rng = np.random.default_rng(n)
+    par = [-1]
+    for i in range(1, n):
+        par.append(int(rng.integers(max(0, i - 6), i)))
+    # pre-order: regroup children after their parent (depth-first walk)
+    kids = [[] for _ in range(n)]
+    for i in range(1, n):
+        kids[par[i]].append(i)
+    order, stack = [], [0]
+    while stack:
+        v = stack.pop()
+        order.append(v)
+        stack.extend(reversed(kids[v]))
+    new = {v: k for k, v in enumerate(order)}
+    lens = [int(rng.integers(1, 10)) for _ in range(n)]
+    return [lens[v] for v in order], [-1 if par[v] < 0 else new[par[v]] for v in order]
+
+
+# 512 and 513 nodes: the largest tree whose node arrays sit in LDS, and the smallest in the workspace
+@pytest.mark.parametrize("name", ["agent16k", "rollout48k", "chain", "star", "branchy512", "branchy513"])
 def test_meta_large(name):
     topo = {
         "agent16k": lambda: workloads.agent_tree(0),
         "rollout48k": lambda: workloads.rollout_tree(0),
         "chain": lambda: ([3] * 3000, [-1] + list(range(2999))),
         "star": lambda: ([5] + [2] * 5000, [-1] + [0] * 5000),
+        "branchy512": lambda: _branchy(512),
+        "branchy513": lambda: _branchy(513),
     }[name]()
     lens, par = topo
     say(f"meta large {name} n={len(lens)} T={sum(lens)}")
@@ -88,6 +111,7 @@ def test_meta_large(name):
     ref = meta_closed_form(lens, par)
     assert np.array_equal(m.pos.cpu().numpy(), ref["pos"])
     assert np.array_equal(m.horizon.cpu().numpy(), ref["horizon"])
+    assert np.array_equal(m.node_off.cpu().numpy(), ref["node_off"])
     from tree_training_amd.meta import KeyPlan
     kp = KeyPlan(m.horizon)
     assert kp.visible_pairs() == workloads.visible_pairs(topo) == int((ref["pos"] + 1).sum())

@@ -578,7 +578,7 @@ int tt_bwd_bf16_launch(const AttnDev& a, const BwdDev& b, hipStream_t s) {
             if (!b.zero_in_dq)
                 hipLaunchKernelGGL(bwd_split_zero_kernel, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
             hipLaunchKernelGGL(bwd_dkdv_bf16_kernel, dim3(dkdv_grid(a)), dim3(256), 0, s, a, b);
-            hipLaunchKernelGGL(bwd_split_finalize_kernel<bf16>, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
+            hipLaunchKernelGGL(bwd_split_finalize_kernel<bf16>, dim3(a.n_kb, a.hkv, 4), dim3(256), 0, s, a, b);
         }
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }

@@ -626,7 +626,7 @@ int tt_bwd_f32_launch(const AttnDev& a, const BwdDev& b, hipStream_t s) {
         } else {
             hipLaunchKernelGGL(bwd_split_zero_kernel, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
             hipLaunchKernelGGL(bwd_dkdv_f32_kernel, dim3(grid), dim3(256), 0, s, a, b);
-            hipLaunchKernelGGL(bwd_split_finalize_kernel<float>, dim3(a.n_kb, a.hkv), dim3(256), 0, s, a, b);
+            hipLaunchKernelGGL(bwd_split_finalize_kernel<float>, dim3(a.n_kb, a.hkv, 4), dim3(256), 0, s, a, b);
         }
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }

@@ -441,26 +441,41 @@ __global__ __launch_bounds__(256) void bwd_split_zero_kernel(AttnDev a, BwdDev b
     split_zero_tile(a, bw, blockIdx.x, blockIdx.y);
 }
 
-// ... and convert them to dk/dv after it: the fp32 sums of tile kb's own
-// keys for kv head g, by one workgroup.
+// ... and convert them to dk/dv after it: the fp32 sums of a quarter (32
+// keys) of tile kb's own keys for kv head g, by one workgroup. Each thread
+// issues its four loads before its first store, so the loads' latency is
+// paid once rather than four times in a row.
 template <typename TOut>
-__device__ __forceinline__ void split_convert_tile(const AttnDev& a, const BwdDev& bw, int kb, int g) {
-    const int k_first = max(kb * TT_BKB, a.n_past), k_end = min(kb * TT_BKB + TT_BKB, a.n_keys);
-    for (int e = threadIdx.x; e < (k_end - k_first) * (D / 4); e += 256) {
-        const int key = k_first + e / (D / 4), d = 4 * (e % (D / 4));
-        const size_t widx = ((size_t)key * a.hkv + g) * D + d;
-        const f32x4 gk = *(const f32x4*)(bw.dk_ws + widx), gv = *(const f32x4*)(bw.dv_ws + widx);
-        const size_t idx = ((size_t)(key - a.n_past) * a.hkv + g) * D + d;
-        store_out4<TOut>(bw.dk, idx, gk);
-        store_out4<TOut>(bw.dv, idx, gv);
+__device__ __forceinline__ void split_convert_quarter(const AttnDev& a, const BwdDev& bw, int kb, int g, int qt) {
+    const int k_first = max(kb * TT_BKB + 32 * qt, a.n_past), k_end = min(kb * TT_BKB + 32 * qt + 32, a.n_keys);
+    const int n = (k_end - k_first) * (D / 4);
+    f32x4 gk[4], gv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = threadIdx.x + 256 * i;
+        if (e < n) {
+            const size_t widx = ((size_t)(k_first + e / (D / 4)) * a.hkv + g) * D + 4 * (e % (D / 4));
+            gk[i] = *(const f32x4*)(bw.dk_ws + widx);
+            gv[i] = *(const f32x4*)(bw.dv_ws + widx);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = threadIdx.x + 256 * i;
+        if (e < n) {
+            const size_t idx = ((size_t)(k_first + e / (D / 4) - a.n_past) * a.hkv + g) * D + 4 * (e % (D / 4));
+            store_out4<TOut>(bw.dk, idx, gk[i]);
+            store_out4<TOut>(bw.dv, idx, gv[i]);
+        }
     }
 }
 
+// Grid (n_kb, Hkv, 4): workgroup z converts the z-th quarter of a split tile.
 template <typename TOut>
 __global__ __launch_bounds__(256) void bwd_split_finalize_kernel(AttnDev a, BwdDev bw) {
     const int kb = blockIdx.x, g = blockIdx.y;
     if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb], tt_qch(a.n_q)) <= 1) return;
-    split_convert_tile<TOut>(a, bw, kb, g);
+    split_convert_quarter<TOut>(a, bw, kb, g, blockIdx.z);
 }
 
 // Deterministic mode: one workgroup per (key tile rank, kv head) sums a split

@@ -13,30 +13,53 @@
 namespace {
 
 constexpr int kNodeThreads = 1024;
+constexpr int kLdsNodes = 512;    // node arrays in LDS up to this many nodes
 
-__host__ __device__ inline int sparse_levels(int n) {
+__host__ __device__ constexpr int sparse_levels(int n) {
     int L = 1;
     while ((1 << L) <= n) ++L;   // levels r = 0..L-1 with 2^r <= n
     return L;
 }
 
+constexpr int kLdsLevels = sparse_levels(kLdsNodes) - 1;   // sparse-table levels 1..L-1 of the largest such tree
+
+// Where a workgroup's node arrays can be read after meta_nodes_body: LDS
+// copies for trees of at most kLdsNodes nodes, else the global outputs.
+struct NodeView {
+    const int32_t* len;
+    const int32_t* start;
+    const int32_t* off;
+    const int32_t* hend;
+};
+
 // Node-level metadata in one workgroup of kNodeThreads threads. TT_STATUS_*
 // bits are OR-ed into s_err (an LDS word the caller zeroes before the call);
-// ends with a barrier after which start, off, hend and s_err are visible to
-// the whole workgroup.
-__device__ __forceinline__ void meta_nodes_body(
+// ends with a barrier after which start, off, hend (and the arrays of the
+// returned view) and s_err are visible to the whole workgroup.
+__device__ __forceinline__ NodeView meta_nodes_body(
     const int32_t* __restrict__ len, const int32_t* __restrict__ par, int n, int T,
     int32_t* __restrict__ start, int32_t* __restrict__ off, int32_t* __restrict__ hend,
     int& s_err, int32_t* __restrict__ ws) {
     __shared__ int s_scan[kNodeThreads];
     __shared__ int s_carry;
+    // Trees of at most kLdsNodes nodes keep the node arrays in LDS (every
+    // pointer-jumping round, sparse-table level and read-back is then an LDS
+    // round trip, not a global one); larger ones use the workspace and the
+    // global outputs.
+    __shared__ int32_t s_nodes[(9 + kLdsLevels) * kLdsNodes];
     const int tid = threadIdx.x;
-    int32_t* anc0 = ws;
-    int32_t* anc1 = ws + n;
-    int32_t* offb1 = ws + 2 * n;
-    int32_t* dep0 = ws + 3 * n;
-    int32_t* dep1 = ws + 4 * n;
-    int32_t* st = ws + 5 * n;   // sparse-table levels 1..L-1, n ints each
+    const bool in_lds = n <= kLdsNodes;
+    int32_t* const b = in_lds ? s_nodes : ws;
+    int32_t* anc0 = b;
+    int32_t* anc1 = b + n;
+    int32_t* offb1 = b + 2 * n;
+    int32_t* dep0 = b + 3 * n;
+    int32_t* dep1 = b + 4 * n;
+    int32_t* offb0 = in_lds ? b + 5 * n : off;     // first pointer-jumping buffer of off
+    int32_t* w_len = in_lds ? b + 6 * n : nullptr;
+    int32_t* w_start = in_lds ? b + 7 * n : start;
+    int32_t* w_hend = in_lds ? b + 8 * n : hend;
+    int32_t* st = b + (in_lds ? 9 : 5) * n;        // sparse-table levels 1..L-1, n ints each
     if (tid == 0) s_carry = 0;
     __syncthreads();
 
@@ -46,6 +69,7 @@ __device__ __forceinline__ void meta_nodes_body(
         int v = 0;
         if (i < n) {
             v = len[i];
+            if (in_lds) w_len[i] = v;
             int p = par[i];
             if (v < 1) atomicOr(&s_err, TT_STATUS_BAD_LEN);
             if (p < -1 || p >= i) atomicOr(&s_err, TT_STATUS_BAD_PARENT);
@@ -62,24 +86,28 @@ __device__ __forceinline__ void meta_nodes_body(
         __syncthreads();
         int before = s_carry;
         for (int w = 0; w < wave; ++w) before += s_scan[w];
-        if (i < n) start[i] = before + incl - v;
+        if (i < n) {
+            start[i] = before + incl - v;
+            if (in_lds) w_start[i] = before + incl - v;
+        }
         __syncthreads();
         if (tid == kNodeThreads - 1) s_carry = before + incl;
         __syncthreads();
     }
     if (tid == 0 && s_carry != T) atomicOr(&s_err, TT_STATUS_BAD_TOTAL);
+    const int32_t* lenv = in_lds ? w_len : len;
 
     // 2. pointer jumping: off = sum of ancestor lengths, dep = ancestor count.
     for (int i = tid; i < n; i += kNodeThreads) {
         int p = par[i];
         if (p < -1 || p >= i) p = -1;   // flagged above; keep the walk in bounds
         anc0[i] = p;
-        off[i] = p >= 0 ? len[p] : 0;
+        offb0[i] = p >= 0 ? lenv[p] : 0;
         dep0[i] = p >= 0 ? 1 : 0;
     }
     __syncthreads();
     int32_t* a_cur = anc0; int32_t* a_nxt = anc1;
-    int32_t* o_cur = off;  int32_t* o_nxt = offb1;
+    int32_t* o_cur = offb0; int32_t* o_nxt = offb1;
     int32_t* d_cur = dep0; int32_t* d_nxt = dep1;
     for (;;) {
         int any = 0;
@@ -97,7 +125,7 @@ __device__ __forceinline__ void meta_nodes_body(
                 a_nxt[i] = -1;
             }
         }
-        __syncthreads();                // global-memory writes of this round visible
+        __syncthreads();                // writes of this round visible
         any = __syncthreads_or(any);
         int32_t* t;
         t = a_cur; a_cur = a_nxt; a_nxt = t;
@@ -129,7 +157,9 @@ __device__ __forceinline__ void meta_nodes_body(
                 if (lev[i] > thr) i += w;
             }
         }
-        hend[c] = (i < n) ? start[i] : T;
+        const int he = (i < n) ? w_start[i] : T;
+        hend[c] = he;
+        if (in_lds) w_hend[c] = he;
     }
     __syncthreads();   // hend of every node visible
 
@@ -140,9 +170,10 @@ __device__ __forceinline__ void meta_nodes_body(
     // its child is then a descendant of that parent).
     for (int i = tid; i < n; i += kNodeThreads) {
         const int p = par[i];
-        if (p >= 0 && p < i && start[i] >= hend[p]) atomicOr(&s_err, TT_STATUS_BAD_PARENT);
+        if (p >= 0 && p < i && w_start[i] >= w_hend[p]) atomicOr(&s_err, TT_STATUS_BAD_PARENT);
     }
     __syncthreads();
+    return NodeView{lenv, w_start, o_cur, w_hend};
 }
 
 // Tokens of every node: wave w writes the tokens of nodes w, w + 16, ..., its
@@ -192,9 +223,9 @@ __global__ __launch_bounds__(kNodeThreads) void meta_tree_kernel(
     int32_t* __restrict__ status, int32_t* __restrict__ ws) {
     __shared__ int s_err;
     if (threadIdx.x == 0) s_err = 0;
-    meta_nodes_body(len, par, n, T, start, off, hend, s_err, ws);
+    const NodeView v = meta_nodes_body(len, par, n, T, start, off, hend, s_err, ws);
     if (threadIdx.x == 0 && s_err) atomicOr(status, s_err);
-    meta_tokens_body(len, n, T, pos_offset, start, off, hend, pos, node_of, horizon, 0, nullptr, nullptr);
+    meta_tokens_body(v.len, n, T, pos_offset, v.start, v.off, v.hend, pos, node_of, horizon, 0, nullptr, nullptr);
 }
 
 __global__ void meta_tokens_kernel(const int32_t* __restrict__ start, const int32_t* __restrict__ off,
@@ -442,9 +473,9 @@ __device__ __forceinline__ void plan_finish_body(const uint8_t* __restrict__ cls
                                                  int32_t* __restrict__ row_cnt, int32_t* __restrict__ row_list,
                                                  int32_t* __restrict__ row_order, int32_t* __restrict__ kb_order,
                                                  int32_t* __restrict__ kb_base, uint8_t* __restrict__ plan) {
-    __shared__ int s_cnt[kFinishMax];
+    __shared__ __attribute__((aligned(16))) int s_cnt[kFinishMax];
     __shared__ int s_kbo[kFinishMax];
-    __shared__ int s_kbw[kFinishMax];   // query range width of each key tile
+    __shared__ __attribute__((aligned(16))) int s_kbw[kFinishMax];   // query range width of each key tile
     __shared__ int s_scan[1024];
     __shared__ int s_carry;
     __shared__ unsigned long long s_pairs;
@@ -454,51 +485,70 @@ __device__ __forceinline__ void plan_finish_body(const uint8_t* __restrict__ cls
         s_pairs = 0;
     }
     for (int i = tid; i < n_kb; i += 1024) s_kbw[i] = kb_qhi[i] - kb_qlo[i];
-    // compaction: a wave per query block; the classes of 256 tiles are loaded
-    // at once, so a row waits on memory once per 256 tiles, not per 64
+    // compaction: a wave per query block, eight of its blocks (rows wave,
+    // wave + 16, ...) at a time; the classes of 256 tiles of all eight rows
+    // are loaded at once, so a wave waits on memory once per 256 tiles of
+    // eight rows
     const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    for (int row = wave; row < n_qb; row += 16) {
-        int cnt = 0;
+    constexpr int RB = 8;
+    for (int row0 = wave; row0 < n_qb; row0 += 16 * RB) {
+        int cnt[RB];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) cnt[r] = 0;
         for (int base = 0; base < n_kt; base += 256) {
-            int cv[4];
+            int cv[RB][4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int kt = base + 64 * u + lane;
-                cv[u] = kt < n_kt ? cls[(size_t)row * n_kt + kt] : 0;
-            }
+            for (int r = 0; r < RB; ++r)
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int kt = base + 64 * u + lane, c = cv[u];
-                const unsigned long long m = __ballot(c != 0);
-                if (c) row_list[(size_t)row * n_kt + cnt + __popcll(m & below)] = (kt << 1) | (c == 2 ? 1 : 0);
-                cnt += __popcll(m);
+                for (int u = 0; u < 4; ++u) {
+                    const int row = row0 + 16 * r, kt = base + 64 * u + lane;
+                    cv[r][u] = (row < n_qb && kt < n_kt) ? cls[(size_t)row * n_kt + kt] : 0;
+                }
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                const int row = row0 + 16 * r;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int kt = base + 64 * u + lane, c = cv[r][u];
+                    const unsigned long long m = __ballot(c != 0);
+                    if (c) row_list[(size_t)row * n_kt + cnt[r] + __popcll(m & below)] = (kt << 1) | (c == 2 ? 1 : 0);
+                    cnt[r] += __popcll(m);
+                }
             }
         }
-        if (lane == 0) {
-            s_cnt[row] = cnt;
-            row_cnt[row] = cnt;
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int row = row0 + 16 * r;
+            if (lane == 0 && row < n_qb) {
+                s_cnt[row] = cnt[r];
+                row_cnt[row] = cnt[r];
+            }
         }
     }
     __syncthreads();
-    // orders: rank = number of heavier entries (ties by index)
-    for (int i = tid; i < n_qb; i += 1024) {
-        const int c = s_cnt[i];
-        int rank = 0;
-        for (int j = 0; j < n_qb; ++j) {
-            const int cj = s_cnt[j];
-            rank += (cj > c) || (cj == c && j < i);
+    // orders: rank = number of heavier entries (ties by index); query blocks on
+    // threads 0-511, key tiles on 512-1023, four entries per LDS read
+    {
+        const bool rows = tid < 512;
+        const int* arr = rows ? s_cnt : s_kbw;
+        const int n_e = rows ? n_qb : n_kb;
+        for (int i = tid & 511; i < n_e; i += 512) {
+            const int c = arr[i];
+            int rank = 0, j = 0;
+#pragma unroll 4
+            for (; j + 4 <= n_e; j += 4) {
+                const i32x4 c4 = *(const i32x4*)(arr + j);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) rank += (c4[e] > c) || (c4[e] == c && j + e < i);
+            }
+            for (; j < n_e; ++j) rank += (arr[j] > c) || (arr[j] == c && j < i);
+            if (rows) {
+                row_order[rank] = i;
+            } else {
+                s_kbo[rank] = i;
+                kb_order[rank] = i;
+            }
         }
-        row_order[rank] = i;
-    }
-    for (int i = tid; i < n_kb; i += 1024) {
-        const int c = s_kbw[i];
-        int rank = 0;
-        for (int j = 0; j < n_kb; ++j) {
-            const int cj = s_kbw[j];
-            rank += (cj > c) || (cj == c && j < i);
-        }
-        s_kbo[rank] = i;
-        kb_order[rank] = i;
     }
     unsigned long long pairs = 0;
     for (int i = tid; i < n_pb; i += 1024) pairs += pair_part[i];
@@ -606,8 +656,8 @@ __global__ __launch_bounds__(kNodeThreads) void trees_meta_keys_kernel(TreeJobsD
     const TreeJobDev& jb = J.j[blockIdx.x];
     __shared__ int s_err;
     if (threadIdx.x == 0) s_err = 0;
-    meta_nodes_body(jb.len, jb.par, jb.n, jb.T, jb.start, jb.off, jb.hend, s_err, jb.ws);
-    meta_tokens_body(jb.len, jb.n, jb.T, jb.pos_offset, jb.start, jb.off, jb.hend, jb.pos, jb.node_of, jb.horizon,
+    const NodeView v = meta_nodes_body(jb.len, jb.par, jb.n, jb.T, jb.start, jb.off, jb.hend, s_err, jb.ws);
+    meta_tokens_body(v.len, jb.n, jb.T, jb.pos_offset, v.start, v.off, v.hend, jb.pos, jb.node_of, jb.horizon,
                      jb.n_past, jb.key_lo, jb.key_hi);
     for (int j = threadIdx.x; j < jb.n_past; j += kNodeThreads) {   // gateway keys: bias 0 or -inf
         const float b = jb.bias[j];
