@@ -292,6 +292,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
     const int n_work = (*a.n_items) * a.hkv;
     const RowOffsX qro = row_offsx(col, half);   // this lane's query row in the Q / dO blocks
     const TrOffsX tro = tr_offsx(lane);
+    QBlockStager stg;
+    stg.init(a, bw);
 
     for (int w_id = blockIdx.x; w_id < n_work; w_id += gridDim.x) {
         // Workgroup-uniform values (the integer divisions run on the VALU):
@@ -311,6 +313,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
         const bool split = tt_kb_items(qlo, qhi, qch) > 1;
         int q_start, q_stop;
         tt_kb_item_range(qlo, qhi, qch, chunk, q_start, q_stop);
+        // the first query block's direct loads go out before the item's V and
+        // K loads (stage 0 was last read before the previous item's final
+        // barrier)
+        const int q_top = (q_stop > q_start) ? ((q_stop - 1) / TT_BQB) * TT_BQB : 0;
+        const int n_steps = (q_stop > q_start) ? ((q_top - q_start) / TT_BQB + 1) * a.rep : 0;
+        if (n_steps > 0) stg.begin(a, bw, q_top, g * a.rep, st[0]);
 
         // V rows of the tile's 128 keys go to LDS (read as MFMA operands every
         // step); K of the lane's key stays in registers. Keys past the end alias
@@ -354,14 +362,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
 
         // Query blocks are walked from the top of the range down, so items whose
         // ranges end at the same subtree end read the same rows at the same time.
-        const int q_top = (q_stop > q_start) ? ((q_stop - 1) / TT_BQB) * TT_BQB : 0;
-        const int n_steps = (q_stop > q_start) ? ((q_top - q_start) / TT_BQB + 1) * a.rep : 0;
-        QBlockStager stg;
-        stg.init(a, bw);
         // step s covers query block q0 of q head g*rep + hh; (q0, hh) of the next
         // step are kept incrementally
         int q0 = q_top, hh = 0;
-        if (n_steps > 0) stg.begin(a, bw, q0, g * a.rep, st[0]);
         for (int s = 0; s < n_steps; ++s) {
             KvStage& S = st[s & 1];
             stg.commit(a, S);
