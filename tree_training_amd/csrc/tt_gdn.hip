@@ -21,7 +21,9 @@
 //    one launch per tree level so a node's parent state (in the caller's
 //    node_states buffer) is complete when it starts; each wave holds a
 //    128 x 16 value slice of the state in MFMA accumulators (the delta rule is
-//    independent per value column) and walks the node's chunks.
+//    independent per value column) and walks the node's chunks. Levels of
+//    one or two nodes use gdn_scan_rows_kernel instead (eight workgroups per
+//    pair, each wave a 32 x 16 slice), which gives the same bits.
 // fp32 end to end: the prep on fp32 MFMA (v_mfma_f32_32x32x2_f32) and the
 // vector ALUs, the scans on v_mfma_f32_16x16x4_f32.
 #include "tt_gdn_common.h"
@@ -456,21 +458,33 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         }
         __syncthreads();
 
-        // V' = U - W S and q^ S: 8 row tiles of S x 4 steps, for both token tiles.
+        // V' = U - W S and q^ S over the 128 state rows as four partial sums of
+        // two row tiles each, added in order: the partition of the row layout's
+        // waves (gdn_scan_rows_kernel), so both layouts give the same bits.
 #pragma unroll
-        for (int rb = 0; rb < 8; ++rb) {
+        for (int w4 = 0; w4 < 4; ++w4) {
+            f32x4 pv[2] = {}, pq[2] = {};
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const int rb = 2 * w4 + r;
+#pragma unroll
+                for (int tb = 0; tb < 2; ++tb) {
+                    const int ro = (16 * tb + c16) * RS + 16 * rb + g4;
+                    const f32x4 qv = *(const f32x4*)&L.Q[ro];
+                    if constexpr (!TRUNC) {
+                        const f32x4 wv = *(const f32x4*)&L.W[ro];
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) pv[tb] = mfma16_f32(-wv[v], S[rb][v], pv[tb]);
+                    }
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) pq[tb] = mfma16_f32(qv[v], S[rb][v], pq[tb]);
+                    __builtin_amdgcn_sched_barrier(0);   // operand reads one step ahead at most (registers)
+                }
+            }
 #pragma unroll
             for (int tb = 0; tb < 2; ++tb) {
-                const int ro = (16 * tb + c16) * RS + 16 * rb + g4;
-                const f32x4 qv = *(const f32x4*)&L.Q[ro];
-                if constexpr (!TRUNC) {
-                    const f32x4 wv = *(const f32x4*)&L.W[ro];
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) vp[tb] = mfma16_f32(-wv[v], S[rb][v], vp[tb]);
-                }
-#pragma unroll
-                for (int v = 0; v < 4; ++v) qs[tb] = mfma16_f32(qv[v], S[rb][v], qs[tb]);
-                __builtin_amdgcn_sched_barrier(0);   // operand reads one step ahead at most (registers)
+                if constexpr (!TRUNC) vp[tb] += pv[tb];
+                qs[tb] += pq[tb];
             }
         }
         if (chunk_vp) {
@@ -518,6 +532,165 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     float* sp = states + ((size_t)node * p.hv + h) * GD * GD + jt;
 #pragma unroll
     for (int rb = 0; rb < 8; ++rb) store_t16(sp + 16 * rb * GD, lane, S[rb]);
+}
+
+// Row layout of the level scans, for levels of few nodes (the exact rule
+// only): a workgroup takes 16 value columns of one (node, v head), eight
+// workgroups per pair, and its wave w the state rows 32w .. 32w+31 of them.
+// The products over the state rows (W S and q^ S) are summed over the four
+// waves through LDS, in wave order; every wave then updates its own rows. A
+// chunk costs each wave about a quarter of the column layout's MFMAs, for
+// four times the workgroups: a level with few nodes runs a serial chain of
+// chunks on a mostly idle chip, and that chain gets shorter.
+constexpr int ROWS_COLS = 16;
+constexpr int kRowsSplit = GD / ROWS_COLS;
+__device__ __forceinline__ void rows_block(const GdnDev& p, int& h, int& c0) {
+    const int bx = blockIdx.x;
+    int cs;
+    if ((p.hv & 7) == 0) {   // the eight column blocks of a head on one XCD (same L2)
+        h = ((bx >> 6) << 3) | (bx & 7);
+        cs = (bx >> 3) & 7;
+    } else {
+        h = bx >> 3;
+        cs = bx & 7;
+    }
+    c0 = ROWS_COLS * cs;
+}
+
+struct ScanRowsLds {
+    ScanLds T;
+    f32x4 P[4][2][2][64];   // per wave: its partial W S and q^ S, both token tiles, lane-major
+};
+
+// As gdn_scan_cols_kernel (exact rule), in the row layout: wave w holds the
+// 32 x 16 slice S[32w .., c0 ..] in two 16 x 16 accumulator tiles.
+template <typename TIn>
+__global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_scan_rows_kernel(GdnDev p, int lvl_begin, float* __restrict__ ws,
+                                                      TIn* __restrict__ out, float* __restrict__ states,
+                                                      float* __restrict__ chunk_sin, float* __restrict__ chunk_vp) {
+    __shared__ __attribute__((aligned(16))) ScanRowsLds L;
+    const int node = p.level_nodes[lvl_begin + blockIdx.y];
+    if (node < 0 || node >= p.n_nodes) return;
+    int h, cb;
+    rows_block(p, h, cb);
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, c16 = lane & 15, g4 = 4 * (lane >> 4);
+    const int j = cb + c16;                                               // this lane's value column
+    const int rb0 = 2 * wave;                                             // the wave's first row tile
+    const int start = p.node_start[node], len = p.node_len[node], chunk0 = p.node_chunk0[node];
+    int par = p.parent[node];
+    if (start < 0 || len < 0 || start > p.n_tokens - len) return;        // malformed node: skipped
+    if (chunk0 < 0 || chunk0 > p.n_chunks - tt_cdiv(len, GC)) return;
+    if (par >= node || par < -1) par = -1;                               // parents precede children
+
+    const float* s0 = par >= 0 ? states + ((size_t)par * p.hv + h) * GD * GD
+                               : (p.init ? p.init + (size_t)h * GD * GD : nullptr);
+    f32x4 S[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) S[r] = s0 ? load_t16(s0 + cb + 16 * (rb0 + r) * GD, lane) : (f32x4){};
+
+    const int n_ch = tt_cdiv(len, GC);
+    ScanAhead<TIn> nx;
+    {
+        const float* cw = ws + ((size_t)chunk0 * p.hv + h) * kWsChunk;
+        scan_fetch_rows<TIn, true>(p, cw, start, min(GC, len), h, nx);
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) nx.x[tb] = load_t16(cw + kWsU + 16 * tb * GD + cb, lane);
+    }
+    for (int ci = 0; ci < n_ch; ++ci) {
+        const int c0 = GC * ci, Lc = min(GC, len - c0);
+        const size_t ch = (size_t)(chunk0 + ci) * p.hv + h;
+        if (chunk_sin) {
+            float* sp = chunk_sin + ch * GD * GD + cb;
+#pragma unroll
+            for (int r = 0; r < 2; ++r) store_t16(sp + 16 * (rb0 + r) * GD, lane, S[r]);
+        }
+        __syncthreads();   // readers of the previous chunk's tiles and partials are done
+        scan_stage_rows<TIn, true, false>(p, nx, L.T.Q, L.T.K, L.T.W, L.T.A, L.T.G);
+        f32x4 vp[2], qs[2], pv[2], pq[2];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            vp[tb] = nx.x[tb];
+            pv[tb] = pq[tb] = (f32x4){};
+        }
+        if (ci + 1 < n_ch) {
+            const float* cw = ws + (ch + p.hv) * kWsChunk;
+            scan_fetch_rows<TIn, true>(p, cw, start + c0 + GC, min(GC, len - c0 - GC), h, nx);
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) nx.x[tb] = load_t16(cw + kWsU + 16 * tb * GD + cb, lane);
+        }
+        __syncthreads();
+
+        // this wave's rows of -W S and q^ S
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) {
+                const int ro = (16 * tb + c16) * RS + 16 * (rb0 + r) + g4;
+                const f32x4 wv = *(const f32x4*)&L.T.W[ro];
+                const f32x4 qv = *(const f32x4*)&L.T.Q[ro];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    pv[tb] = mfma16_f32(-wv[v], S[r][v], pv[tb]);
+                    pq[tb] = mfma16_f32(qv[v], S[r][v], pq[tb]);
+                }
+            }
+        }
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            L.P[wave][0][tb][lane] = pv[tb];
+            L.P[wave][1][tb][lane] = pq[tb];
+        }
+        __syncthreads();
+        // V' = U - W S and q^ S, the partials summed in wave order
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            qs[tb] = (f32x4){};
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                vp[tb] += L.P[w][0][tb][lane];
+                qs[tb] += L.P[w][1][tb][lane];
+            }
+        }
+        if (chunk_vp && wave == 0) {
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) store_t16(chunk_vp + ch * GC * GD + 16 * tb * GD + cb, lane, vp[tb]);
+        }
+        // O = e^G (q^ S) + A V': waves 0 and 1 take one token tile each
+        if (wave < 2) {
+            const int tb = wave;
+            f32x4 o;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) o[v] = qs[tb][v] * expf(L.T.G[16 * tb + g4 + v]);
+#pragma unroll
+            for (int tb2 = 0; tb2 < 2; ++tb2) {
+                const f32x4 av = *(const f32x4*)&L.T.A[(16 * tb + c16) * MS + 16 * tb2 + g4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) o = mfma16_f32(av[v], vp[tb2][v], o);
+            }
+            if (out) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int i = 16 * tb + g4 + v;
+                    if (i < Lc) out[((int64_t)(start + c0 + i) * p.hv + h) * GD + j] = (TIn)o[v];
+                }
+            }
+        }
+        // S <- e^{G_L} S + k~^T V' on this wave's rows
+        const float el = expf(L.T.G[GC - 1]);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            S[r] *= el;
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    S[r] = mfma16_f32(L.T.K[(16 * tb + g4 + v) * RS + 16 * (rb0 + r) + c16], vp[tb][v], S[r]);
+        }
+    }
+
+    float* sp = states + ((size_t)node * p.hv + h) * GD * GD + cb;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) store_t16(sp + 16 * (rb0 + r) * GD, lane, S[r]);
 }
 
 // ----------------------------------------------------------------------------
@@ -628,22 +801,31 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         if (ci > 0) fetch(ci - 1, nx);
         __syncthreads();
 
-        // dV' = A^T dO + k~ dS
+        // dV' = A^T dO + k~ dS as four partial sums added in order, partial w4
+        // holding the A^T dO term of token tiles (w4 / 2, w4 % 2) and the
+        // state rows 32 w4 .. +31: the partition of the row layout's waves
+        // (gdn_rscan_rows_kernel), so both layouts give the same bits.
         f32x4 dv[2];
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
             dv[tb] = (f32x4){};
 #pragma unroll
-            for (int tb2 = 0; tb2 < 2; ++tb2)
+            for (int w4 = 0; w4 < 4; ++w4) {
+                f32x4 pd = {};
+                if (tb == (w4 >> 1)) {
 #pragma unroll
-                for (int v = 0; v < 4; ++v)
-                    dv[tb] = mfma16_f32(L.A[(16 * tb2 + g4 + v) * MS + 16 * tb + c16], dov[tb2][v], dv[tb]);
+                    for (int v = 0; v < 4; ++v)
+                        pd = mfma16_f32(L.A[(16 * (w4 & 1) + g4 + v) * MS + 16 * tb + c16], dov[w4 & 1][v], pd);
+                }
 #pragma unroll
-            for (int rb = 0; rb < 8; ++rb) {
-                const f32x4 kv = *(const f32x4*)&L.K[(16 * tb + c16) * RS + 16 * rb + g4];
+                for (int r = 0; r < 2; ++r) {
+                    const int rb = 2 * w4 + r;
+                    const f32x4 kv = *(const f32x4*)&L.K[(16 * tb + c16) * RS + 16 * rb + g4];
 #pragma unroll
-                for (int v = 0; v < 4; ++v) dv[tb] = mfma16_f32(kv[v], dS[rb][v], dv[tb]);
-                __builtin_amdgcn_sched_barrier(0);
+                    for (int v = 0; v < 4; ++v) pd = mfma16_f32(kv[v], dS[rb][v], pd);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                dv[tb] += pd;
             }
         }
 #pragma unroll
@@ -694,6 +876,132 @@ __global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     float* sp = node_dsin + ((size_t)node * p.hv + h) * GD * GD + jt;
 #pragma unroll
     for (int rb = 0; rb < 8; ++rb) store_t16(sp + 16 * rb * GD, lane, dS[rb]);
+}
+
+struct RscanRowsLds {
+    RscanLds T;
+    f32x4 P[4][2][64];   // per wave: its partial dV', both token tiles, lane-major
+};
+
+// As gdn_rscan_cols_kernel (exact rule), in the row layout of
+// gdn_scan_rows_kernel: wave w holds dS[32w .., c0 ..]. dV' = A^T dO + k~ dS
+// is summed over the waves' rows through LDS, in wave order (wave w also adds
+// the A^T dO term of token tiles (w / 2, w % 2)); every wave then updates its
+// rows of dS.
+template <typename TIn>
+__global__ __launch_bounds__(GT) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_rscan_rows_kernel(
+        GdnDev p, int lvl_begin, const float* __restrict__ ws, const TIn* __restrict__ d_o, int64_t do_st,
+        int64_t do_sh, float* __restrict__ chunk_dso, float* __restrict__ chunk_dvp, float* __restrict__ node_dsin) {
+    __shared__ __attribute__((aligned(16))) RscanRowsLds L;
+    const int node = p.level_nodes[lvl_begin + blockIdx.y];
+    if (node < 0 || node >= p.n_nodes) return;
+    int h, cb;
+    rows_block(p, h, cb);
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, c16 = lane & 15, g4 = 4 * (lane >> 4);
+    const int j = cb + c16;
+    const int rb0 = 2 * wave;
+    const int start = p.node_start[node], len = p.node_len[node], chunk0 = p.node_chunk0[node];
+    if (start < 0 || len < 1 || start > p.n_tokens - len) return;        // malformed node: skipped
+    if (chunk0 < 0 || chunk0 > p.n_chunks - tt_cdiv(len, GC)) return;
+
+    f32x4 dS[2];
+    if (p.d_states && (!p.d_states_last || node == p.n_nodes - 1)) {
+        const float* sp = p.d_states + ((size_t)(p.d_states_last ? 0 : node) * p.hv + h) * GD * GD + cb;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) dS[r] = load_t16(sp + 16 * (rb0 + r) * GD, lane);
+    } else {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) dS[r] = (f32x4){};
+    }
+    {
+        const int c_lo = max(p.child_off[node], 0), c_hi = min(p.child_off[node + 1], p.n_nodes);
+        for (int ci = c_lo; ci < c_hi; ++ci) {
+            const int child = p.child[ci];
+            if (child <= node || child >= p.n_nodes) continue;          // children follow their parent
+            const float* sp = node_dsin + ((size_t)child * p.hv + h) * GD * GD + cb;
+#pragma unroll
+            for (int r = 0; r < 2; ++r) dS[r] += load_t16(sp + 16 * (rb0 + r) * GD, lane);
+        }
+    }
+
+    const int n_ch = tt_cdiv(len, GC);
+    auto fetch = [&](int ci, ScanAhead<TIn>& x) {
+        const int c0 = GC * ci, Lc = min(GC, len - c0);
+        const float* cw = ws + ((size_t)(chunk0 + ci) * p.hv + h) * kWsChunk;
+        scan_fetch_rows<TIn, true>(p, cw, start + c0, Lc, h, x);
+        const TIn* base = d_o + (int64_t)(start + c0) * do_st + (int64_t)h * do_sh + j;
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {   // dO[token 16 tb + 4 (l >> 4) + v][j], zero past the chunk
+                const int i = 16 * tb + g4 + v;
+                x.x[tb][v] = i < Lc ? (float)base[(int64_t)i * do_st] : 0.0f;
+            }
+    };
+    ScanAhead<TIn> nx;
+    fetch(n_ch - 1, nx);
+    const int atb = wave >> 1, atb2 = wave & 1;   // this wave's A^T dO term
+    for (int ci = n_ch - 1; ci >= 0; --ci) {
+        const size_t chn = (size_t)(chunk0 + ci) * p.hv + h;
+        {
+            float* sp = chunk_dso + chn * GD * GD + cb;
+#pragma unroll
+            for (int r = 0; r < 2; ++r) store_t16(sp + 16 * (rb0 + r) * GD, lane, dS[r]);
+        }
+        __syncthreads();   // readers of the previous chunk's tiles and partials are done
+        scan_stage_rows<TIn, true, true>(p, nx, L.T.Q, L.T.K, L.T.W, L.T.A, L.T.G);
+        const f32x4 dov[2] = {nx.x[0], nx.x[1]};
+        if (ci > 0) fetch(ci - 1, nx);
+        __syncthreads();
+
+        f32x4 pd[2];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            pd[tb] = (f32x4){};
+            if (tb == atb) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    pd[tb] = mfma16_f32(L.T.A[(16 * atb2 + g4 + v) * MS + 16 * tb + c16], dov[atb2][v], pd[tb]);
+            }
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const f32x4 kv = *(const f32x4*)&L.T.K[(16 * tb + c16) * RS + 16 * (rb0 + r) + g4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) pd[tb] = mfma16_f32(kv[v], dS[r][v], pd[tb]);
+            }
+            L.P[wave][tb][lane] = pd[tb];
+        }
+        __syncthreads();
+        f32x4 dv[2];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            dv[tb] = (f32x4){};
+#pragma unroll
+            for (int w = 0; w < 4; ++w) dv[tb] += L.P[w][tb][lane];
+        }
+        if (wave == 0) {
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) store_t16(chunk_dvp + chn * GC * GD + 16 * tb * GD + cb, lane, dv[tb]);
+        }
+
+        // dS <- e^{G_L} dS + (e^G q^)^T dO - W^T dV' on this wave's rows
+        const float el = expf(L.T.G[GC - 1]);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            dS[r] *= el;
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int ro = (16 * tb + g4 + v) * RS + 16 * (rb0 + r) + c16;
+                    dS[r] = mfma16_f32(L.T.Q[ro], dov[tb][v], dS[r]);
+                    dS[r] = mfma16_f32(-L.T.W[ro], dv[tb][v], dS[r]);
+                }
+        }
+    }
+    float* sp = node_dsin + ((size_t)node * p.hv + h) * GD * GD + cb;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) store_t16(sp + 16 * (rb0 + r) * GD, lane, dS[r]);
 }
 
 // Gradient of the initial state: the sum over the roots, in node order (the
@@ -1297,14 +1605,32 @@ template <typename TIn, bool TRUNC>
 void launch_prep(const GdnDev& d, float* prep, hipStream_t s) {
     hipLaunchKernelGGL((gdn_prep_kernel<TIn, TRUNC>), dim3(d.n_chunks, d.hv), dim3(GT), 0, s, d, prep);
 }
+// A level of n nodes runs in the row layout (exact rule) when the column
+// layout would leave most of the chip idle: at most TT_GDN_ROWS_MAX_PAIRS
+// (node, v head) pairs, two column workgroups each. On the 16K agent tree (32
+// v heads) 64 pairs (levels of one or two nodes) timed best: 5.60 -> 5.40 ms
+// per step, against 5.43 ms for 128 and for 256.
+#ifndef TT_GDN_ROWS_MAX_PAIRS
+#define TT_GDN_ROWS_MAX_PAIRS 64
+#endif
+template <bool TRUNC>
+bool use_rows(const GdnDev& d, int n) {
+    return !TRUNC && (int64_t)n * d.hv <= TT_GDN_ROWS_MAX_PAIRS;
+}
+
 template <typename TIn, bool TRUNC>
 void launch_scan(const GdnDev& d, int b, int n, float* prep, TIn* out, float* states, float* sin, float* vp,
                  hipStream_t s) {
     // grid (v head x column block, node): all heads of a level's first
     // (longest) nodes are dispatched first
-    for (int b0 = 0; b0 < n; b0 += kMaxGridY)
-        hipLaunchKernelGGL((gdn_scan_cols_kernel<TIn, TRUNC>), dim3(d.hv * kScanSplit, min(kMaxGridY, n - b0)),
-                           dim3(GT), 0, s, d, b + b0, prep, out, states, sin, vp);
+    for (int b0 = 0; b0 < n; b0 += kMaxGridY) {
+        if (use_rows<TRUNC>(d, n))
+            hipLaunchKernelGGL((gdn_scan_rows_kernel<TIn>), dim3(d.hv * kRowsSplit, min(kMaxGridY, n - b0)),
+                               dim3(GT), 0, s, d, b + b0, prep, out, states, sin, vp);
+        else
+            hipLaunchKernelGGL((gdn_scan_cols_kernel<TIn, TRUNC>), dim3(d.hv * kScanSplit, min(kMaxGridY, n - b0)),
+                               dim3(GT), 0, s, d, b + b0, prep, out, states, sin, vp);
+    }
 }
 
 // The forward: chunk terms (prep; TRUNC: plus the node-level U, W), then one
@@ -1435,9 +1761,15 @@ static int gdn_bwd_run(const GdnDev& d, const int32_t* level_offsets, int n_leve
     for (int l = n_levels - 1; l >= 0; --l) {
         const int b = level_offsets[l], n = level_offsets[l + 1] - b;
         if (n <= 0) continue;
-        for (int b0 = 0; b0 < n; b0 += kMaxGridY)
-            hipLaunchKernelGGL((gdn_rscan_cols_kernel<TIn, TRUNC>), dim3(d.hv * kScanSplit, min(kMaxGridY, n - b0)),
-                               dim3(GT), 0, s, d, b + b0, w.prep, d_o, do_st, do_sh, w.dso, w.dvp, w.dsn);
+        for (int b0 = 0; b0 < n; b0 += kMaxGridY) {
+            if (use_rows<TRUNC>(d, n))
+                hipLaunchKernelGGL((gdn_rscan_rows_kernel<TIn>), dim3(d.hv * kRowsSplit, min(kMaxGridY, n - b0)),
+                                   dim3(GT), 0, s, d, b + b0, w.prep, d_o, do_st, do_sh, w.dso, w.dvp, w.dsn);
+            else
+                hipLaunchKernelGGL((gdn_rscan_cols_kernel<TIn, TRUNC>),
+                                   dim3(d.hv * kScanSplit, min(kMaxGridY, n - b0)), dim3(GT), 0, s, d, b + b0,
+                                   w.prep, d_o, do_st, do_sh, w.dso, w.dvp, w.dsn);
+        }
         if (hipGetLastError() != hipSuccess) return TT_E_HIP;
     }
     if (d.d_init) {
