@@ -168,6 +168,8 @@ typedef struct tt_attn_problem {
     size_t plan_bytes;
     int64_t det_slots;      /* tt_attn_bwd with TT_BWD_DETERMINISTIC: the partial-sum slots to reserve,
                                from tt_attn_det_slots for the tree; 0: the bound that holds for any tree */
+    int64_t split_tiles;    /* tt_attn_bwd: the split key tiles the fp32 split sums hold, from
+                               tt_attn_split_tiles for the tree; 0: every key tile */
 } tt_attn_problem;
 
 /* o: [n_q, Hq, head_dim] contiguous, problem dtype; lse: [Hq, n_q] float32
@@ -214,6 +216,17 @@ int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* ws, size_t 
  * Only the TT_BWD_DKDV part depends on the bit. */
 size_t tt_attn_bwd_workspace_bytes(const tt_attn_problem* p);
 
+/* Host only (no device work): the split_tiles a DFS pre-order forest needs:
+ * its 128-key tiles whose visible query range spans more than W queries (see
+ * above), whose fp32 dK/dV sums take 2 * 128 * Hkv * 512 bytes of the
+ * workspace each (14 tiles, 14 MiB, on the 16K agent tree; with split_tiles =
+ * 0 every key tile is counted: 128 MiB there). A split_tiles below what the
+ * plan needs never writes past the workspace: the tiles beyond it get NaN
+ * gradients (dk, dv; the gateway accumulators in deterministic mode).
+ * Same arguments, visibility and errors as tt_attn_det_slots below. */
+int tt_attn_split_tiles(const int32_t* node_len, const int32_t* parent, int n_nodes, const float* past_bias,
+                        int n_past, int64_t* tiles);
+
 /* Host only (no device work): the det_slots a DFS pre-order forest needs,
  * from node_len/parent [n_nodes] and the gateway bias past_bias [n_past]
  * (0 or -inf per gateway key, host memory; NULL: every gateway key visible),
@@ -237,10 +250,11 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
  * TT_NOALLOC_SCRATCH_MB MiB that the library holds on each GPU it runs on
  * until the process ends (the current device's, hipGetDevice; `stream` must
  * belong to it). A problem whose tt_attn_bwd_workspace_bytes exceeds it
- * returns TT_E_WORKSPACE (either dtype needs 128 * Hq * n_q + 1024 * Hkv * (n_q +
- * n_past) bytes, plus the dQ key-split partials of small bf16 problems: about
- * 8K keys at Hq = 32, Hkv = 8). The call allocates and
- * frees nothing (no hipMalloc, no hipMemsetAsync: what must start at zero is
+ * returns TT_E_WORKSPACE (either dtype needs 4 * Hq * n_q bytes plus the
+ * split sums, 1 MiB per split tile at Hkv = 8, plus the dQ key-split
+ * partials of small bf16 problems: with split_tiles from tt_attn_split_tiles,
+ * 16 MiB on the 16K agent tree and 70 MiB on the 48K rollout tree). The call
+ * allocates and frees nothing (no hipMalloc, no hipMemsetAsync: what must start at zero is
  * cleared by a kernel). Every call on one GPU uses that GPU's one scratch
  * array, which keeps the last call's contents: calls that overlap on one GPU
  * (other streams, other threads) race and must not be issued; a TT_BWD_*
@@ -249,7 +263,7 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
  * device address (hipGetSymbolAddress, once per device, cached): make that
  * first call outside stream capture, e.g. an ordinary warm-up call before a
  * graph is captured; later calls make no such lookup. */
-#define TT_NOALLOC_SCRATCH_MB 64
+#define TT_NOALLOC_SCRATCH_MB 96
 size_t tt_noalloc_scratch_bytes(void);
 int tt_attn_bwd_noalloc(const tt_attn_problem* p, const void* o, const float* lse, tt_tensor d_o,
                         void* dq, void* dk, void* dv, float* dk_past_acc, float* dv_past_acc, void* stream);

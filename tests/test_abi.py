@@ -163,17 +163,44 @@ def test_bwd_parts_validation():
 
 
 def test_bwd_noalloc_validation():
-    """The no-allocation backward: a 64 MiB scratch, null problems rejected,
+    """The no-allocation backward: a 96 MiB scratch, null problems rejected,
     and a problem whose workspace exceeds the scratch refused on the host
     (no HIP call: these run without a GPU)."""
     lib = _lib.lib()
-    assert lib.tt_noalloc_scratch_bytes() == 64 << 20
+    assert lib.tt_noalloc_scratch_bytes() == 96 << 20
     d_o = _lib.TTTensor(16, 32 * 128, 128)
     V = ctypes.c_void_p(16)
     assert lib.tt_attn_bwd_noalloc(None, V, V, d_o, V, V, V, None, None, None) == _lib.TT_E_ARG
     big = _problem(n_q=40000)
     assert lib.tt_attn_bwd_workspace_bytes(ctypes.byref(big)) > lib.tt_noalloc_scratch_bytes()
     assert lib.tt_attn_bwd_noalloc(ctypes.byref(big), V, V, d_o, V, V, V, None, None, None) == _lib.TT_E_WORKSPACE
+
+
+@pytest.mark.parametrize("n_q,n_past", [(100, 0), (16318, 0), (5300, 300)])
+def test_bwd_split_tiles_workspace(n_q, n_past):
+    """The fp32 split sums take one dK and one dV block of 128 keys x Hkv x
+    128 floats per split key tile the problem says it holds (split_tiles), or
+    per key tile with split_tiles = 0; a negative count is an argument error."""
+    lib = _lib.lib()
+    n_kb = -(-(n_q + n_past) // 128)
+    tile = 2 * 128 * 8 * 128 * 4
+    full = _problem(n_q=n_q, n_past=n_past)
+    some = _problem(n_q=n_q, n_past=n_past, split_tiles=3)
+    assert lib.tt_attn_bwd_workspace_bytes(ctypes.byref(full)) - \
+        lib.tt_attn_bwd_workspace_bytes(ctypes.byref(some)) == (n_kb - 3) * tile
+    det = _problem(n_q=n_q, n_past=n_past, split_tiles=3, bwd_parts=_lib.TT_BWD_DETERMINISTIC, det_slots=2)
+    assert lib.tt_attn_bwd_workspace_bytes(ctypes.byref(det)) - \
+        lib.tt_attn_bwd_workspace_bytes(ctypes.byref(some)) == 2 * tile
+    bad = _problem(n_q=n_q, n_past=n_past, split_tiles=-1, plan_bytes=lib.tt_plan_bytes(n_q, n_q + n_past),
+                   k_past=_lib.TTTensor(16, 8 * 128, 128), v_past=_lib.TTTensor(16, 8 * 128, 128))
+    assert lib.tt_attn_bwd_workspace_bytes(ctypes.byref(bad)) == 0
+    d_o = _lib.TTTensor(16, 32 * 128, 128)
+    V = ctypes.c_void_p(16)
+    assert lib.tt_attn_bwd(ctypes.byref(bad), V, V, d_o, V, V, V, None, None, V, 1 << 40, None) == _lib.TT_E_ARG
+    # the 16K agent tree's 14 split tiles fit the no-allocation scratch
+    if n_q == 16318:
+        tree = _problem(n_q=n_q, split_tiles=14)
+        assert lib.tt_attn_bwd_workspace_bytes(ctypes.byref(tree)) < lib.tt_noalloc_scratch_bytes()
 
 
 def _tree_job(**kw):
@@ -465,25 +492,25 @@ def test_ce_rows_validation():
     assert call(args(ldg=500)) == _lib.TT_E_ARG
 
 
-def _det_slots(lens, par, bias=None):
+def _det_slots(lens, par, bias=None, fn="tt_attn_det_slots"):
     import numpy as np
     nl, pa = np.asarray(lens, np.int32), np.asarray(par, np.int32)
     b = None if bias is None else np.ascontiguousarray(bias, np.float32)
     out = ctypes.c_int64(-1)
-    rc = _lib.lib().tt_attn_det_slots(nl.ctypes.data, pa.ctypes.data, len(nl),
-                                      None if b is None else b.ctypes.data, 0 if b is None else len(b),
-                                      ctypes.byref(out))
+    rc = getattr(_lib.lib(), fn)(nl.ctypes.data, pa.ctypes.data, len(nl),
+                                 None if b is None else b.ctypes.data, 0 if b is None else len(b), ctypes.byref(out))
     return rc, out.value
 
 
 def test_det_slots_match_visibility_windows():
-    """tt_attn_det_slots (host only) against the dK/dV work-item rule applied
-    to the oracle's dense visibility: per 128-key tile the union of its keys'
-    visible queries is a range [lo, hi); a range longer than the window W
-    (half the largest power of two <= n_q, clamped to [256, 4096]) is one work
-    item per W-aligned window it touches, others one item; the slots are the
-    items beyond each tile's first. Forests with long nodes, with and without
-    a gateway (bias 0 = seen by every query, -inf = by none)."""
+    """tt_attn_det_slots and tt_attn_split_tiles (host only) against the dK/dV
+    work-item rule applied to the oracle's dense visibility: per 128-key tile
+    the union of its keys' visible queries is a range [lo, hi); a range longer
+    than the window W (half the largest power of two <= n_q, clamped to
+    [256, 4096]) is one work item per W-aligned window it touches (a split
+    tile), others one item; the slots are the items beyond each tile's first.
+    Forests with long nodes, with and without a gateway (bias 0 = seen by
+    every query, -inf = by none)."""
     import numpy as np
     from oracle.tree_meta import mask_from_horizon, meta_closed_form
     from tree_training_amd import workloads
@@ -500,7 +527,7 @@ def test_det_slots_match_visibility_windows():
                 cols = np.concatenate([np.repeat((bias == 0)[None, :], T, axis=0), mask], axis=1)
             half = (1 << (T.bit_length() - 1)) // 2
             W = min(4096, max(256, half))
-            want = 0
+            want = want_split = 0
             for kb in range(0, cols.shape[1], 128):
                 rows = np.nonzero(cols[:, kb:kb + 128].any(axis=1))[0]
                 if len(rows) == 0:
@@ -509,9 +536,13 @@ def test_det_slots_match_visibility_windows():
                 assert len(rows) == hi - lo        # one contiguous range
                 if hi - lo > W:
                     want += (hi - 1) // W - lo // W
+                    want_split += 1
             rc, got = _det_slots(lens, par, bias)
             assert rc == _lib.TT_OK
             assert got == want, (seed, n_past, got, want)
+            rc, got = _det_slots(lens, par, bias, "tt_attn_split_tiles")
+            assert rc == _lib.TT_OK
+            assert got == want_split, (seed, n_past, got, want_split)
     # the workloads: far below the topology-free bound n_kb * floor((n_q - 1) / W)
     for (lens, par), n_past in ((workloads.agent_tree(0), 0), (workloads.agent_tree(0), 4096),
                                 (workloads.rollout_tree(0), 0)):
@@ -521,9 +552,10 @@ def test_det_slots_match_visibility_windows():
         assert rc == _lib.TT_OK and 0 < got < -(-(T + n_past) // 128) * ((T - 1) // W) / 2
 
 
-def test_det_slots_rejects_bad_topology():
-    assert _det_slots([5, 0], [-1, 0])[0] == _lib.TT_E_ARG        # empty node
-    assert _det_slots([5, 5], [-1, 1])[0] == _lib.TT_E_ARG        # parent not before the node
-    assert _det_slots([5, 5], [-1, -2])[0] == _lib.TT_E_ARG
-    assert _det_slots([], [])[0] == _lib.TT_E_ARG
-    assert _det_slots([5, 5], [-1, 0])[1] == 0
+@pytest.mark.parametrize("fn", ["tt_attn_det_slots", "tt_attn_split_tiles"])
+def test_det_slots_rejects_bad_topology(fn):
+    assert _det_slots([5, 0], [-1, 0], fn=fn)[0] == _lib.TT_E_ARG        # empty node
+    assert _det_slots([5, 5], [-1, 1], fn=fn)[0] == _lib.TT_E_ARG        # parent not before the node
+    assert _det_slots([5, 5], [-1, -2], fn=fn)[0] == _lib.TT_E_ARG
+    assert _det_slots([], [], fn=fn)[0] == _lib.TT_E_ARG
+    assert _det_slots([5, 5], [-1, 0], fn=fn)[1] == 0

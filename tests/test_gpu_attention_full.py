@@ -389,3 +389,75 @@ def test_attention_deterministic_undersized_slots_poison_not_overrun():
         bad = torch.isnan(b.float()).any(dim=2).any(dim=1)
         assert bad.any() and not bad.all()
         assert torch.equal(a[~bad], b[~bad])
+
+
+def _last_split_tile(lens, par, n_q):
+    """Highest-numbered 128-key tile with more than one dK/dV work item (own
+    key j is seen by queries [j, subtree end of its node); numpy restatement
+    of the work-item window rule)."""
+    start = np.concatenate([[0], np.cumsum(lens)[:-1]])
+    end = start + np.asarray(lens)
+    for u in range(len(lens) - 1, 0, -1):
+        if par[u] >= 0:
+            end[par[u]] = max(end[par[u]], end[u])
+    hi_key = np.repeat(end, lens)
+    half = (1 << (n_q.bit_length() - 1)) // 2
+    qch = min(max(half, 256), 4096)
+    last = -1
+    for kb in range(-(-n_q // 128)):
+        lo, hi = 128 * kb, int(hi_key[128 * kb:128 * kb + 128].max())
+        if hi - lo > qch and (hi - 1) // qch - lo // qch + 1 > 1:
+            last = kb
+    return last
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp32"])
+def test_attention_split_tiles_exact_and_undersized(dt):
+    """The fp32 split sums sized from the tree (tt_attn_split_tiles, one
+    128-key block per split key tile, compacted by the plan's split ranks)
+    against the default workspace (a block for every key tile): the
+    deterministic backward is bitwise equal, the default one equal to its
+    atomics' rounding. A split_tiles one below the tree's count writes nothing
+    past the workspace: exactly the keys of the last split tile (in key order)
+    get NaN dk/dv, every other key's gradients are unchanged."""
+    from tree_training_amd.attention import attn_backward, attn_forward
+    from tree_training_amd.meta import KeyPlan, TreeMetaDevice
+    lens, par = [2048, 300, 900, 700], [-1, 0, 0, 2]
+    T = sum(lens)
+    bf = torch.bfloat16 if dt == "bf16" else torch.float32
+    g = torch.Generator(device=DEV).manual_seed(5)
+    q, k, v, do = (torch.randn(T, h, D, device=DEV, generator=g, dtype=bf) for h in (HQ, HKV, HKV, HQ))
+    view = lambda x: x[None].transpose(1, 2)
+    plan = KeyPlan(TreeMetaDevice(lens, par, device=DEV).horizon, None, topo=(lens, par))
+    need = plan.split_tiles()
+    assert need == int(plan.plan[:28].view(torch.int32)[6].item()) >= 2
+    kb_last = _last_split_tile(lens, par, T)
+    print(f"split_tiles {need}, last split tile {kb_last}, {dt}", flush=True)
+    o, lse = attn_forward(view(q), view(k), view(v), plan, D ** -0.5)
+    run = lambda det: attn_backward(view(q), view(k), view(v), plan, D ** -0.5, o, lse, do[None],
+                                    deterministic=det)
+    exact = {det: run(det) for det in (True, False)}
+    plan._split = 0                       # a block for every key tile
+    full = {det: run(det) for det in (True, False)}
+    plan._split = need - 1
+    short = {det: run(det) for det in (True, False)}
+    torch.cuda.synchronize()
+    bar = 2e-2 if dt == "bf16" else 1e-5
+    want_bad = torch.zeros(T, dtype=torch.bool, device=DEV)
+    want_bad[128 * kb_last:128 * kb_last + 128] = True
+    for det in (True, False):
+        for name, a, b, c in zip(("dq", "dk", "dv"), exact[det], full[det], short[det]):
+            assert torch.isfinite(a.float()).all(), (det, name)
+            if det:
+                assert torch.equal(a, b), (det, name)
+            else:
+                assert _max_rel(a.float(), b.float()) < bar, (det, name)
+            if name == "dq":
+                assert torch.equal(a, c) if det else _max_rel(a.float(), c.float()) < bar, (det, name)
+                continue
+            bad = torch.isnan(c.float()).any(dim=2).any(dim=1)
+            assert torch.equal(bad, want_bad), (det, name)
+            if det:
+                assert torch.equal(a[~bad], c[~bad]), (det, name)
+            else:
+                assert _max_rel(a[~bad].float(), c[~bad].float()) < bar, (det, name)

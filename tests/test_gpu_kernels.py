@@ -205,10 +205,14 @@ def _plan_expected_fast(lo, hi, n_q):
     kb_order = sorted(range(n_kb), key=lambda i: (-(qhi[i] - qlo[i]), i))
     half = (1 << (n_q.bit_length() - 1)) // 2 if n_q >= 2 else 0
     qch = 4096 if half > 4096 else max(half, 256)
-    items = [1 if qhi[k] - qlo[k] <= qch else (qhi[k] - 1) // qch - qlo[k] // qch + 1 for k in kb_order]
-    kb_base = np.concatenate([[0], np.cumsum(items)])
+    n_items = lambda k: 1 if qhi[k] - qlo[k] <= qch else (qhi[k] - 1) // qch - qlo[k] // qch + 1
+    kb_base = np.concatenate([[0], np.cumsum([n_items(k) for k in kb_order])])
+    # split tiles (more than one work item) ranked in key order
+    split = np.array([n_items(k) > 1 for k in range(n_kb)], bool)
+    srank = np.where(split, np.cumsum(split) - 1, -1)
     return dict(P=int(np.clip(b - a, 0, None).sum()), n_qb=n_qb, n_kt=n_kt, n_kb=n_kb, rows=rows,
-                row_order=row_order, qlo=qlo, qhi=qhi, kb_order=kb_order, kb_base=kb_base)
+                row_order=row_order, qlo=qlo, qhi=qhi, kb_order=kb_order, kb_base=kb_base, kb_srank=srank,
+                n_split=int(split.sum()))
 
 
 def _plan_decode(buf, n_q, n_keys):
@@ -222,12 +226,13 @@ def _plan_decode(buf, n_q, n_keys):
     qlo = i32(o, n_kb); o += 4 * n_kb
     qhi = i32(o, n_kb); o += 4 * n_kb
     kb_order = i32(o, n_kb); o += 4 * n_kb
-    kb_base = i32(o, n_kb + 1)
-    hdr = i32(8, 4)
+    kb_base = i32(o, n_kb + 1); o += 4 * (n_kb + 1)
+    kb_srank = i32(o, n_kb)
+    hdr = i32(8, 5)
     return dict(P=int(np.frombuffer(buf, np.uint64, 1, 0)[0]), n_qb=int(hdr[0]), n_kt=int(hdr[1]),
-                n_kb=int(hdr[2]), n_items=int(hdr[3]),
+                n_kb=int(hdr[2]), n_items=int(hdr[3]), n_split=int(hdr[4]),
                 rows=[list(row_list[q, :row_cnt[q]]) for q in range(n_qb)], row_order=list(row_order),
-                qlo=qlo, qhi=qhi, kb_order=list(kb_order), kb_base=kb_base)
+                qlo=qlo, qhi=qhi, kb_order=list(kb_order), kb_base=kb_base, kb_srank=kb_srank)
 
 
 def test_build_trees_matches_separate_calls():
@@ -260,9 +265,9 @@ def test_build_trees_matches_separate_calls():
         n_q, n_keys = plan.n_q, plan.n_keys
         a = _plan_decode(plan.plan.cpu().numpy().tobytes(), n_q, n_keys)
         b = _plan_decode(p2.plan.cpu().numpy().tobytes(), n_q, n_keys)
-        for k in ("P", "n_qb", "n_kt", "n_kb", "n_items", "rows", "row_order", "kb_order"):
+        for k in ("P", "n_qb", "n_kt", "n_kb", "n_items", "n_split", "rows", "row_order", "kb_order"):
             assert a[k] == b[k], (i, k)
-        for k in ("qlo", "qhi", "kb_base"):
+        for k in ("qlo", "qhi", "kb_base", "kb_srank"):
             assert np.array_equal(a[k], b[k]), (i, k)
         st = int(meta.status.item())
         want = int(m2.status.item()) | int(p2.status.item())
@@ -307,11 +312,13 @@ def test_plan_matches_numpy(case):
         assert np.array_equal(m.pos.cpu().numpy(), ref["pos"])
         assert np.array_equal(m.horizon.cpu().numpy(), ref["horizon"])
         assert exp["n_qb"] > 2048 and exp["n_kb"] > 2048 and n_q > 65536
-    for k in ("P", "n_qb", "n_kt", "n_kb", "rows", "row_order", "kb_order"):
+    for k in ("P", "n_qb", "n_kt", "n_kb", "n_split", "rows", "row_order", "kb_order"):
         assert got[k] == exp[k], k
-    for k in ("qlo", "qhi", "kb_base"):
+    for k in ("qlo", "qhi", "kb_base", "kb_srank"):
         assert np.array_equal(got[k], exp[k]), k
     assert got["n_items"] == exp["kb_base"][-1]
+    if bias is None:   # the host count (tt_attn_split_tiles) is the plan's
+        assert KeyPlan(m.horizon, topo=(lens, par)).split_tiles() == max(exp["n_split"], 1)
 
 
 # --------------------------------------------------------------------------- attention

@@ -104,6 +104,32 @@ def test_noalloc_backward_matches_workspace_backward(dtype):
                 assert _rel(a, b) < bar, (name, _rel(a, b))
 
 
+def test_noalloc_agent_tree_with_exact_split_tiles():
+    """The 16K agent tree (16,318 tokens, bf16, 32/8 heads) fits the scratch
+    once its split sums are sized from the tree (tt_attn_split_tiles): the
+    no-allocation backward against tt_attn_bwd with the same problem."""
+    lens, par = workloads.agent_tree(0)
+    print(f"noalloc agent tree T={sum(lens)}", flush=True)
+    c = _case(lens, par, 0, torch.bfloat16, seed=44)
+    from tree_training_amd.meta import KeyPlan
+    plan = KeyPlan(c["keep"][0].horizon, topo=(lens, par))
+    c["pb"].s.split_tiles = plan.split_tiles()
+    lib = _lib.lib()
+    need = lib.tt_attn_bwd_workspace_bytes(ctypes.byref(c["pb"].s))
+    assert c["pb"].s.split_tiles >= 1 and 0 < need <= lib.tt_noalloc_scratch_bytes()
+    c["pb"].s.split_tiles = 0
+    assert lib.tt_attn_bwd_workspace_bytes(ctypes.byref(c["pb"].s)) > lib.tt_noalloc_scratch_bytes()
+    c["pb"].s.split_tiles = plan.split_tiles()
+    ref = _bwd(c, noalloc=False)
+    got = _bwd(c, noalloc=True)
+    for name, a, b in zip(("dq", "dk", "dv"), got, ref):
+        assert torch.isfinite(a.float()).all(), name
+        if name == "dq":
+            assert torch.equal(a, b), name
+        else:
+            assert _rel(a, b) < 2e-2, (name, _rel(a, b))
+
+
 def test_noalloc_rejects_problems_beyond_the_scratch():
     """A problem whose workspace exceeds the scratch array returns
     TT_E_WORKSPACE and launches nothing (outputs untouched)."""

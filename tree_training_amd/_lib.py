@@ -29,13 +29,13 @@ TT_STATUS_BAD_PARENT = 2
 TT_STATUS_BAD_TOTAL = 4
 TT_STATUS_BAD_BIAS = 8
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # Every symbol include/tree_attn.h declares, for the export check.
 EXPORTS = (
     "tt_abi_version", "tt_strerror", "tt_meta_workspace_bytes", "tt_meta_build", "tt_keys_build",
     "tt_meta_dense_mask", "tt_plan_bytes", "tt_plan_build", "tt_attn_fwd_workspace_bytes", "tt_attn_fwd",
-    "tt_attn_bwd_workspace_bytes", "tt_attn_det_slots", "tt_attn_bwd", "tt_gdn_workspace_bytes", "tt_gdn_tree_fwd",
+    "tt_attn_bwd_workspace_bytes", "tt_attn_det_slots", "tt_attn_split_tiles", "tt_attn_bwd", "tt_gdn_workspace_bytes", "tt_gdn_tree_fwd",
     "tt_gdn_bwd_workspace_bytes", "tt_gdn_tree_bwd", "tt_gdn_saved_bytes", "tt_gdn_tree_fwd_save",
     "tt_gdn_bwd_saved_workspace_bytes", "tt_gdn_tree_bwd_saved", "tt_tree_conv_fwd", "tt_tree_conv_bwd_workspace_bytes",
     "tt_tree_conv_bwd", "tt_qk_prologue_fwd", "tt_qk_prologue_bwd_workspace_bytes", "tt_qk_prologue_bwd", "tt_ce_rows",
@@ -64,7 +64,7 @@ class TTAttnProblem(ctypes.Structure):
         ("scale", ctypes.c_float), ("bwd_parts", ctypes.c_int32),
         ("q", TTTensor), ("k", TTTensor), ("v", TTTensor), ("k_past", TTTensor), ("v_past", TTTensor),
         ("key_lo", ctypes.c_void_p), ("key_hi", ctypes.c_void_p), ("plan", ctypes.c_void_p),
-        ("plan_bytes", ctypes.c_size_t), ("det_slots", ctypes.c_int64),
+        ("plan_bytes", ctypes.c_size_t), ("det_slots", ctypes.c_int64), ("split_tiles", ctypes.c_int64),
     ]
 
 
@@ -128,6 +128,7 @@ def _declare(lib):
         "tt_attn_fwd": (ctypes.c_int, [ctypes.POINTER(TTAttnProblem), P, P, P, SZ, VP]),
         "tt_attn_bwd_workspace_bytes": (SZ, [ctypes.POINTER(TTAttnProblem)]),
         "tt_attn_det_slots": (ctypes.c_int, [P, P, I32, P, I32, ctypes.POINTER(ctypes.c_int64)]),
+        "tt_attn_split_tiles": (ctypes.c_int, [P, P, I32, P, I32, ctypes.POINTER(ctypes.c_int64)]),
         "tt_attn_bwd": (ctypes.c_int, [ctypes.POINTER(TTAttnProblem), P, P, TTTensor, P, P, P, P, P, P, SZ,
                                        VP]),
         "tt_gdn_workspace_bytes": (SZ, [ctypes.POINTER(TTGdnProblem)]),

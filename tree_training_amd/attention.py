@@ -127,6 +127,7 @@ def attn_backward(q, k, v, plan: KeyPlan, scale: float, o, lse, d_o, k_past=None
     det = TT_BWD_DETERMINISTIC if deterministic else 0
     pb = _Problem(q, k, v, k_past, v_past, plan, scale)
     pb.s.bwd_parts = det
+    pb.s.split_tiles = plan.split_tiles()
     if det:
         pb.s.det_slots = plan.det_slots()
     dev = q.device

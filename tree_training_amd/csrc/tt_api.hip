@@ -9,7 +9,7 @@
 
 namespace {
 
-constexpr int kAbiVersion = 8;
+constexpr int kAbiVersion = 9;
 constexpr int64_t kMaxTokStride = int64_t(1) << 23;   // elements (bf16; half that for fp32)
 inline int64_t max_tok_stride(int dtype) { return dtype == TT_DTYPE_BF16 ? kMaxTokStride : kMaxTokStride / 2; }
 
@@ -70,6 +70,7 @@ int make_dev(const tt_attn_problem* p, AttnDev* a) {
     a->kb_qhi = reinterpret_cast<const int32_t*>(base + L.kb_qhi);
     a->kb_order = reinterpret_cast<const int32_t*>(base + L.kb_order);
     a->kb_base = reinterpret_cast<const int32_t*>(base + L.kb_base);
+    a->kb_srank = reinterpret_cast<const int32_t*>(base + L.kb_srank);
     a->n_items = reinterpret_cast<const int32_t*>(base) + 5;
     return TT_OK;
 }
@@ -202,8 +203,13 @@ int tt_attn_fwd(const tt_attn_problem* p, void* o, float* lse, void* ws, size_t 
 static size_t delta_bytes(const tt_attn_problem* p) {
     return ((size_t)p->n_heads_q * (size_t)p->n_q * sizeof(float) + 255) & ~(size_t)255;
 }
+// Split key tiles the split sums hold: the caller's exact count, else every
+// key tile.
+static int64_t split_cap(const tt_attn_problem* p) {
+    return p->split_tiles > 0 ? p->split_tiles : (int64_t)tt_cdiv(p->n_q + p->n_past, TT_BKB);
+}
 static size_t split_rows_bytes(const tt_attn_problem* p) {
-    return (size_t)(p->n_q + p->n_past) * (size_t)p->n_heads_kv * 128 * sizeof(float);
+    return (size_t)split_cap(p) * TT_BKB * (size_t)p->n_heads_kv * 128 * sizeof(float);
 }
 // Slots of the deterministic mode: the caller's exact count, else the bound.
 static int64_t det_slot_count(const tt_attn_problem* p) {
@@ -215,7 +221,7 @@ static size_t det_slot_bytes(const tt_attn_problem* p) {
 
 size_t tt_attn_bwd_workspace_bytes(const tt_attn_problem* p) {
     if (!p || p->n_q < 1 || p->n_heads_q < 1 || p->n_heads_kv < 1 || p->n_past < 0) return 0;
-    if ((int64_t)p->n_q + p->n_past > 0x3fffffff || p->det_slots < 0) return 0;
+    if ((int64_t)p->n_q + p->n_past > 0x3fffffff || p->det_slots < 0 || p->split_tiles < 0) return 0;
     size_t b = delta_bytes(p) + 2 * split_rows_bytes(p);
     if (p->bwd_parts & TT_BWD_DETERMINISTIC) b += 2 * det_slot_bytes(p);
     return b + split_part_bytes(p);
@@ -228,7 +234,7 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
     if (rc != TT_OK) return rc;
     if (!o || !lse || !d_o.ptr || !dq || !dk || !dv || !ws) return TT_E_ARG;
     if ((dk_past_acc == nullptr) != (dv_past_acc == nullptr)) return TT_E_ARG;
-    if (p->det_slots < 0) return TT_E_ARG;
+    if (p->det_slots < 0 || p->split_tiles < 0) return TT_E_ARG;
     if (ws_bytes < tt_attn_bwd_workspace_bytes(p)) return TT_E_WORKSPACE;
     const int64_t gran = p->dtype == TT_DTYPE_BF16 ? 8 : 4;
     const size_t ealign = 16;
@@ -254,6 +260,7 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
     b.det = (p->bwd_parts & TT_BWD_DETERMINISTIC) ? 1 : 0;
     b.dk_ws = b.dv_ws = b.dk_slot = b.dv_slot = b.dq_part = nullptr;
     b.det_cap = b.det ? det_slot_count(p) : 0;
+    b.split_cap = split_cap(p);
     b.n_split = key_splits(p);
     {
         uint8_t* w = reinterpret_cast<uint8_t*>(ws) + delta_bytes(p);
@@ -274,9 +281,15 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
     return tt_bwd_f32_launch(a, b, (hipStream_t)stream);
 }
 
-int tt_attn_det_slots(const int32_t* node_len, const int32_t* parent, int n_nodes, const float* past_bias,
-                      int n_past, int64_t* slots) {
-    if (!node_len || !parent || !slots || n_nodes < 1 || n_past < 0) return TT_E_ARG;
+}  // extern "C"
+
+// Visible query range [lo, hi) of every 128-key tile of a DFS pre-order
+// forest (own key j: queries [j, subtree end of its node); a visible gateway
+// key: every query), as the device's metadata, keys and plan passes derive
+// it; n_q = the forest's tokens. TT_OK or TT_E_ARG.
+static int tree_tile_ranges(const int32_t* node_len, const int32_t* parent, int n_nodes, const float* past_bias,
+                            int n_past, int& n_q, std::vector<int>& lo, std::vector<int>& hi) {
+    if (!node_len || !parent || n_nodes < 1 || n_past < 0) return TT_E_ARG;
     // subtree end per node: in DFS pre-order a node's subtree is the run of
     // nodes after it, so children (later nodes) fold into their parents
     std::vector<int64_t> start(n_nodes), end(n_nodes);
@@ -290,8 +303,10 @@ int tt_attn_det_slots(const int32_t* node_len, const int32_t* parent, int n_node
     }
     for (int u = n_nodes - 1; u > 0; --u)
         if (parent[u] >= 0 && end[u] > end[parent[u]]) end[parent[u]] = end[u];
-    const int n_q = (int)T, n_keys = n_past + n_q, n_kb = tt_cdiv(n_keys, TT_BKB), qch = tt_qch(n_q);
-    std::vector<int> lo(n_kb, n_q), hi(n_kb, 0);
+    n_q = (int)T;
+    const int n_kb = tt_cdiv(n_past + n_q, TT_BKB);
+    lo.assign(n_kb, n_q);
+    hi.assign(n_kb, 0);
     for (int j = 0; j < n_past; ++j)
         if (!past_bias || past_bias[j] == 0.0f) {
             lo[j / TT_BKB] = 0;
@@ -303,12 +318,38 @@ int tt_attn_det_slots(const int32_t* node_len, const int32_t* parent, int n_node
             lo[kb] = std::min(lo[kb], (int)t);
             hi[kb] = std::max(hi[kb], (int)end[u]);
         }
+    for (int kb = 0; kb < n_kb; ++kb)
+        if (lo[kb] >= hi[kb]) lo[kb] = hi[kb] = 0;   // a tile no query sees
+    return TT_OK;
+}
+
+extern "C" {
+
+int tt_attn_det_slots(const int32_t* node_len, const int32_t* parent, int n_nodes, const float* past_bias,
+                      int n_past, int64_t* slots) {
+    if (!slots) return TT_E_ARG;
+    int n_q = 0;
+    std::vector<int> lo, hi;
+    const int rc = tree_tile_ranges(node_len, parent, n_nodes, past_bias, n_past, n_q, lo, hi);
+    if (rc != TT_OK) return rc;
+    const int qch = tt_qch(n_q);
     int64_t extra = 0;
-    for (int kb = 0; kb < n_kb; ++kb) {
-        const bool any = lo[kb] < hi[kb];
-        extra += tt_kb_items(any ? lo[kb] : 0, any ? hi[kb] : 0, qch) - 1;
-    }
+    for (size_t kb = 0; kb < lo.size(); ++kb) extra += tt_kb_items(lo[kb], hi[kb], qch) - 1;
     *slots = extra;
+    return TT_OK;
+}
+
+int tt_attn_split_tiles(const int32_t* node_len, const int32_t* parent, int n_nodes, const float* past_bias,
+                        int n_past, int64_t* tiles) {
+    if (!tiles) return TT_E_ARG;
+    int n_q = 0;
+    std::vector<int> lo, hi;
+    const int rc = tree_tile_ranges(node_len, parent, n_nodes, past_bias, n_past, n_q, lo, hi);
+    if (rc != TT_OK) return rc;
+    const int qch = tt_qch(n_q);
+    int64_t n = 0;
+    for (size_t kb = 0; kb < lo.size(); ++kb) n += tt_kb_items(lo[kb], hi[kb], qch) > 1;
+    *tiles = n;
     return TT_OK;
 }
 

@@ -553,12 +553,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
         // Epilogue: rows of dk/dv = this wave's keys, columns = d (as the bf16 pass).
         const bool det_split = split && bw.det;
-        // a later item whose slot lies beyond the workspace writes nothing (its
-        // tile's gradients become NaN in the finalize)
-        const bool det_skip = det_split && chunk > 0 && (int64_t)(item - lo_r - 1) >= bw.det_cap;
+        // a split tile's rows in the split sums (first items) and a later item's
+        // slot: one that lies beyond the workspace writes nothing (the tile's
+        // gradients become NaN in the finalize)
+        const SplitRows sr = split ? split_rows(a, bw, kb) : SplitRows{0, false};
+        const bool det_skip = det_split && (chunk > 0 ? (int64_t)(item - lo_r - 1) >= bw.det_cap : !sr.ok);
         float* const sk = chunk == 0 ? bw.dk_ws : bw.dk_slot;
         float* const sv = chunk == 0 ? bw.dv_ws : bw.dv_slot;
-        const int64_t srow = chunk == 0 ? 0 : (int64_t)(item - lo_r - 1) * TT_BKB - kb * TT_BKB;
+        const int64_t srow = chunk == 0 ? sr.row0 : (int64_t)(item - lo_r - 1) * TT_BKB - kb * TT_BKB;
         const int kbase = kb * TT_BKB + wave * 32;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -584,8 +586,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                         }
                     }
                 } else if (split) {
-                    atomicAdd(bw.dk_ws + widx, gk);
-                    atomicAdd(bw.dv_ws + widx, gv);
+                    if (sr.ok) {
+                        const size_t cidx = ((size_t)(sr.row0 + key) * a.hkv + g) * D + d;
+                        atomicAdd(bw.dk_ws + cidx, gk);
+                        atomicAdd(bw.dv_ws + cidx, gv);
+                    }
                 } else {
                     const size_t idx = ((size_t)(key - a.n_past) * a.hkv + g) * D + d;
                     ((float*)bw.dk)[idx] = gk;

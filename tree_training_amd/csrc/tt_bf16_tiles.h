@@ -420,18 +420,32 @@ __device__ __forceinline__ void store_out4(void* base, size_t idx, const f32x4& 
     }
 }
 
-// Split key tiles: zero the fp32 sums of their own keys before the dK/dV pass
-// (split gateway keys add straight into the caller's fp32 accumulators) ...
-// (16-byte vectors: the workspace and the gateway accumulators are 16-byte
-// aligned and rows are 128 floats)
-// The zeroing of key tile kb, kv head g by one workgroup: the fp32 sums of its
-// own keys, if its query range is split.
+// Split key tiles sum their dK/dV in fp32 rows of the workspace, compacted:
+// the tile of split rank r (plan kb_srank) owns rows 128 r .. 128 r + 127, so
+// key `key` of tile kb sits in row split_row(...) + key. A tile whose rank is
+// beyond the rows the workspace holds (split_cap) writes nothing there, and
+// its keys' gradients become NaN in the finalize.
+struct SplitRows {
+    int64_t row0;   // row of key 0 of the tile's run (rows 128 r - 128 kb + key)
+    bool ok;        // the tile is split and its rows fit the workspace
+};
+__device__ __forceinline__ SplitRows split_rows(const AttnDev& a, const BwdDev& bw, int kb) {
+    const int r = a.kb_srank[kb];
+    return {((int64_t)r - kb) * TT_BKB, r >= 0 && (int64_t)r < bw.split_cap};
+}
+
+// Zero the fp32 sums of a split tile's own keys before the dK/dV pass (split
+// gateway keys add straight into the caller's fp32 accumulators; 16-byte
+// vectors: the workspace and the gateway accumulators are 16-byte aligned and
+// rows are 128 floats), by one workgroup per (key tile kb, kv head g).
 __device__ __forceinline__ void split_zero_tile(const AttnDev& a, const BwdDev& bw, int kb, int g) {
     if (tt_kb_items(a.kb_qlo[kb], a.kb_qhi[kb], tt_qch(a.n_q)) <= 1) return;
+    const SplitRows sr = split_rows(a, bw, kb);
+    if (!sr.ok) return;
     const int k_first = max(kb * TT_BKB, a.n_past), k_end = min(kb * TT_BKB + TT_BKB, a.n_keys);
     for (int e = threadIdx.x; e < (k_end - k_first) * (D / 4); e += 256) {
         const int key = k_first + e / (D / 4);
-        const size_t idx = ((size_t)key * a.hkv + g) * D + 4 * (e % (D / 4));
+        const size_t idx = ((size_t)(sr.row0 + key) * a.hkv + g) * D + 4 * (e % (D / 4));
         *(f32x4*)(bw.dk_ws + idx) = (f32x4){};
         *(f32x4*)(bw.dv_ws + idx) = (f32x4){};
     }
@@ -447,14 +461,17 @@ __global__ __launch_bounds__(256) void bwd_split_zero_kernel(AttnDev a, BwdDev b
 // paid once rather than four times in a row.
 template <typename TOut>
 __device__ __forceinline__ void split_convert_quarter(const AttnDev& a, const BwdDev& bw, int kb, int g, int qt) {
+    const SplitRows sr = split_rows(a, bw, kb);
     const int k_first = max(kb * TT_BKB + 32 * qt, a.n_past), k_end = min(kb * TT_BKB + 32 * qt + 32, a.n_keys);
     const int n = (k_end - k_first) * (D / 4);
+    const float qnan = __int_as_float(0x7fc00000);   // by its bits (built without NaN semantics)
     f32x4 gk[4], gv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int e = threadIdx.x + 256 * i;
-        if (e < n) {
-            const size_t widx = ((size_t)(k_first + e / (D / 4)) * a.hkv + g) * D + 4 * (e % (D / 4));
+        gk[i] = gv[i] = (f32x4){qnan, qnan, qnan, qnan};
+        if (e < n && sr.ok) {
+            const size_t widx = ((size_t)(sr.row0 + k_first + e / (D / 4)) * a.hkv + g) * D + 4 * (e % (D / 4));
             gk[i] = *(const f32x4*)(bw.dk_ws + widx);
             gv[i] = *(const f32x4*)(bw.dv_ws + widx);
         }
@@ -489,13 +506,20 @@ __global__ __launch_bounds__(256) void bwd_split_finalize_det_kernel(AttnDev a, 
     if (m <= 1) return;
     const int k_first = kb * TT_BKB, k_end = min(kb * TT_BKB + TT_BKB, a.n_keys);
     const int64_t slot0 = (int64_t)(a.kb_base[rank] - rank) * TT_BKB;   // slot rows of the tile's second item
-    // slots the workspace lacks (a det_slots below the tree's count): the
-    // work items wrote none, and the tile's gradients are NaN
-    const bool lacks = (int64_t)(a.kb_base[rank] - rank) + (m - 1) > bw.det_cap;
+    const SplitRows sr = split_rows(a, bw, kb);
+    // rows or slots the workspace lacks (split_tiles or det_slots below the
+    // tree's count): the work items wrote none there, and the tile's
+    // gradients are NaN
+    const bool lacks = !sr.ok || (int64_t)(a.kb_base[rank] - rank) + (m - 1) > bw.det_cap;
     for (int e = threadIdx.x; e < (k_end - k_first) * (D / 4); e += 256) {
         const int key = k_first + e / (D / 4), d = 4 * (e % (D / 4));
         const size_t widx = ((size_t)key * a.hkv + g) * D + d;
-        f32x4 gk = *(const f32x4*)(bw.dk_ws + widx), gv = *(const f32x4*)(bw.dv_ws + widx);
+        const size_t cidx = ((size_t)(sr.row0 + key) * a.hkv + g) * D + d;
+        f32x4 gk = {}, gv = {};
+        if (!lacks) {
+            gk = *(const f32x4*)(bw.dk_ws + cidx);
+            gv = *(const f32x4*)(bw.dv_ws + cidx);
+        }
         for (int c = 1; c < (lacks ? 1 : m); ++c) {
             const size_t sidx = ((size_t)(slot0 + (int64_t)(c - 1) * TT_BKB + key - k_first) * a.hkv + g) * D + d;
             gk += *(const f32x4*)(bw.dk_slot + sidx);

@@ -22,6 +22,7 @@ struct AttnDev {
     const int32_t* kb_qhi;
     const int32_t* kb_order;  // plan: key tiles, widest range first
     const int32_t* kb_base;   // plan: first dK/dV work item per key tile (kb_order order)
+    const int32_t* kb_srank;  // plan: rank of each key tile among the split ones (-1: not split)
     const int32_t* n_items;   // plan: number of dK/dV work items
     int n_q, n_past, n_keys, hq, hkv, rep, n_qb, n_kt, n_kb;
     float scale;
@@ -37,8 +38,9 @@ struct BwdDev {
     float* dk_acc;            // [n_past, hkv, 128] fp32 (+=), may be null
     float* dv_acc;
     float* delta;             // workspace [hq, n_q]: rowsum(dO * O)
-    float* dk_ws;             // workspace [n_keys, hkv, 128] fp32: split key tiles' dK
-    float* dv_ws;             // workspace [n_keys, hkv, 128] fp32: split key tiles' dV
+    float* dk_ws;             // workspace [split_cap * 128, hkv, 128] fp32: split key tiles' dK, tile of
+    float* dv_ws;             //   split rank r in rows 128 r .. 128 r + 127; the same for dV
+    int64_t split_cap;        // split tiles the workspace holds (tiles beyond write nothing; their keys get NaN)
     float* dk_slot;           // deterministic mode: [tt_det_slots, 128, hkv, 128] fp32, chunks >= 1
     float* dv_slot;           //   of split key tiles (null otherwise)
     int64_t det_cap;          // deterministic mode: slots the workspace holds (tiles beyond get NaN)

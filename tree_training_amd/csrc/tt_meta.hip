@@ -409,12 +409,44 @@ __global__ __launch_bounds__(256) void plan_orders_kernel(const int32_t* __restr
         plan_kb_order(kb_qlo, kb_qhi, n_kb, blockIdx.x - nb_ro, kb_order);
 }
 
+// Rank of every key tile among the split ones (more than one dK/dV work
+// item), in key order, -1 for the others, and their count in the plan header;
+// run by a whole workgroup of 1024 threads.
+__device__ __forceinline__ void plan_split_ranks(const int32_t* __restrict__ kb_qlo,
+                                                 const int32_t* __restrict__ kb_qhi, int n_kb, int qch,
+                                                 int32_t* __restrict__ kb_srank, uint8_t* __restrict__ plan) {
+    __shared__ int s_w[16];
+    __shared__ int s_c;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if (tid == 0) s_c = 0;
+    __syncthreads();
+    for (int base = 0; base < n_kb; base += 1024) {
+        const int kb = base + tid;
+        const int f = (kb < n_kb && tt_kb_items(kb_qlo[kb], kb_qhi[kb], qch) > 1) ? 1 : 0;
+        const unsigned long long m = __ballot(f);
+        if (lane == 0) s_w[wave] = __popcll(m);
+        __syncthreads();
+        int before = s_c;
+        for (int w = 0; w < wave; ++w) before += s_w[w];
+        if (kb < n_kb) kb_srank[kb] = f ? before + __popcll(m & ((1ull << lane) - 1)) : -1;
+        __syncthreads();
+        if (tid == 0) {
+            int tot = 0;
+            for (int w = 0; w < 16; ++w) tot += s_w[w];
+            s_c += tot;
+        }
+        __syncthreads();
+    }
+    if (tid == 0) reinterpret_cast<int32_t*>(plan)[6] = s_c;
+}
+
 // Plan pass 4: the dK/dV work-item offsets of the ordered key tiles, then the
-// header (pairs P, n_qb, n_kt, n_kb, n_items).
+// header (pairs P, n_qb, n_kt, n_kb, n_items, n_split) and the split ranks.
 __global__ __launch_bounds__(1024) void plan_kb_base_kernel(const int32_t* __restrict__ kb_qlo,
                                                             const int32_t* __restrict__ kb_qhi,
                                                             const int32_t* __restrict__ kb_order, int n_kb,
                                                             int qch, int32_t* __restrict__ kb_base,
+                                                            int32_t* __restrict__ kb_srank,
                                                             const unsigned long long* __restrict__ pair_part,
                                                             int n_pb, int n_qb, int n_kt, uint8_t* __restrict__ plan) {
     __shared__ unsigned long long s_pairs;
@@ -459,6 +491,7 @@ __global__ __launch_bounds__(1024) void plan_kb_base_kernel(const int32_t* __res
         hdr[4] = n_kb;
         hdr[5] = s_carry;
     }
+    plan_split_ranks(kb_qlo, kb_qhi, n_kb, qch, kb_srank, plan);
 }
 
 // Plan passes 2-4 in one workgroup (plans of up to kFinishMax query blocks and
@@ -472,7 +505,8 @@ __device__ __forceinline__ void plan_finish_body(const uint8_t* __restrict__ cls
                                                  const unsigned long long* __restrict__ pair_part, int n_pb,
                                                  int32_t* __restrict__ row_cnt, int32_t* __restrict__ row_list,
                                                  int32_t* __restrict__ row_order, int32_t* __restrict__ kb_order,
-                                                 int32_t* __restrict__ kb_base, uint8_t* __restrict__ plan) {
+                                                 int32_t* __restrict__ kb_base, int32_t* __restrict__ kb_srank,
+                                                 uint8_t* __restrict__ plan) {
     __shared__ __attribute__((aligned(16))) int s_cnt[kFinishMax];
     __shared__ int s_kbo[kFinishMax];
     __shared__ __attribute__((aligned(16))) int s_kbw[kFinishMax];   // query range width of each key tile
@@ -587,6 +621,7 @@ __device__ __forceinline__ void plan_finish_body(const uint8_t* __restrict__ cls
         hdr[4] = n_kb;
         hdr[5] = s_carry;
     }
+    plan_split_ranks(kb_qlo, kb_qhi, n_kb, qch, kb_srank, plan);
 }
 
 __global__ __launch_bounds__(1024) void plan_finish_kernel(const uint8_t* __restrict__ cls, int n_qb, int n_kt,
@@ -596,9 +631,10 @@ __global__ __launch_bounds__(1024) void plan_finish_kernel(const uint8_t* __rest
                                                            int32_t* __restrict__ row_cnt, int32_t* __restrict__ row_list,
                                                            int32_t* __restrict__ row_order,
                                                            int32_t* __restrict__ kb_order,
-                                                           int32_t* __restrict__ kb_base, uint8_t* __restrict__ plan) {
+                                                           int32_t* __restrict__ kb_base, int32_t* __restrict__ kb_srank,
+                                                           uint8_t* __restrict__ plan) {
     plan_finish_body(cls, n_qb, n_kt, kb_qlo, kb_qhi, n_kb, qch, pair_part, n_pb, row_cnt, row_list, row_order,
-                     kb_order, kb_base, plan);
+                     kb_order, kb_base, kb_srank, plan);
 }
 
 // ---------------------------------------------------------------------------
@@ -632,7 +668,7 @@ static_assert(sizeof(TreeJobsDev) <= 3072, "the jobs travel as one kernel argume
 
 struct PlanPtrs {
     PlanLayout L;
-    int32_t *row_cnt, *row_order, *row_list, *kb_qlo, *kb_qhi, *kb_order, *kb_base;
+    int32_t *row_cnt, *row_order, *row_list, *kb_qlo, *kb_qhi, *kb_order, *kb_base, *kb_srank;
     uint8_t* cls;
     unsigned long long* pair_part;
     int nb_cls, nb_kv;
@@ -644,6 +680,7 @@ struct PlanPtrs {
         kb_qhi = reinterpret_cast<int32_t*>(base + L.kb_qhi);
         kb_order = reinterpret_cast<int32_t*>(base + L.kb_order);
         kb_base = reinterpret_cast<int32_t*>(base + L.kb_base);
+        kb_srank = reinterpret_cast<int32_t*>(base + L.kb_srank);
         cls = base + L.cls;
         pair_part = reinterpret_cast<unsigned long long*>(base + L.pair_part);
         nb_cls = tt_cdiv(L.n_qb * L.n_kt, 4);
@@ -687,7 +724,7 @@ __global__ __launch_bounds__(1024) void trees_plan_finish_kernel(TreeJobsDev J) 
     const TreeJobDev& jb = J.j[blockIdx.x];
     const PlanPtrs P(jb.plan, jb.T, jb.n_past + jb.T);
     plan_finish_body(P.cls, P.L.n_qb, P.L.n_kt, P.kb_qlo, P.kb_qhi, P.L.n_kb, tt_qch(jb.T), P.pair_part, P.L.n_pb,
-                     P.row_cnt, P.row_list, P.row_order, P.kb_order, P.kb_base, jb.plan);
+                     P.row_cnt, P.row_list, P.row_order, P.kb_order, P.kb_base, P.kb_srank, jb.plan);
 }
 
 }  // namespace
@@ -781,6 +818,7 @@ int tt_plan_build_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys,
     int32_t* kb_qhi = reinterpret_cast<int32_t*>(base + L.kb_qhi);
     int32_t* kb_order = reinterpret_cast<int32_t*>(base + L.kb_order);
     int32_t* kb_base = reinterpret_cast<int32_t*>(base + L.kb_base);
+    int32_t* kb_srank = reinterpret_cast<int32_t*>(base + L.kb_srank);
     uint8_t* cls = base + L.cls;
     unsigned long long* pair_part = reinterpret_cast<unsigned long long*>(base + L.pair_part);
     const int nb_cls = tt_cdiv(L.n_qb * L.n_kt, 4), nb_kv = tt_cdiv(L.n_kb, 4);
@@ -788,7 +826,8 @@ int tt_plan_build_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys,
                        n_q, L.n_qb, L.n_kt, L.n_kb, nb_cls, nb_kv, cls, kb_qlo, kb_qhi, pair_part);
     if (L.n_qb <= kFinishMax && L.n_kb <= kFinishMax) {
         hipLaunchKernelGGL(plan_finish_kernel, dim3(1), dim3(1024), 0, s, cls, L.n_qb, L.n_kt, kb_qlo, kb_qhi, L.n_kb,
-                           tt_qch(n_q), pair_part, L.n_pb, row_cnt, row_list, row_order, kb_order, kb_base, base);
+                           tt_qch(n_q), pair_part, L.n_pb, row_cnt, row_list, row_order, kb_order, kb_base, kb_srank,
+                           base);
         return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
     }
     hipLaunchKernelGGL(plan_compact_kernel, dim3(tt_cdiv(L.n_qb, 4)), dim3(256), 0, s, cls, L.n_qb, L.n_kt,
@@ -797,6 +836,6 @@ int tt_plan_build_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys,
     hipLaunchKernelGGL(plan_orders_kernel, dim3(nb_ro + tt_cdiv(L.n_kb, 256)), dim3(256), 0, s, row_cnt, L.n_qb,
                        nb_ro, kb_qlo, kb_qhi, L.n_kb, row_order, kb_order);
     hipLaunchKernelGGL(plan_kb_base_kernel, dim3(1), dim3(1024), 0, s, kb_qlo, kb_qhi, kb_order, L.n_kb, tt_qch(n_q),
-                       kb_base, pair_part, L.n_pb, L.n_qb, L.n_kt, base);
+                       kb_base, kb_srank, pair_part, L.n_pb, L.n_qb, L.n_kt, base);
     return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
 }

@@ -201,7 +201,7 @@ def _build_batch(specs, dev):
         kp.device, kp.n_q, kp.n_past, kp.n_keys = dev, T, P, T + P
         kp.key_lo, kp.key_hi, kp.status = keys[0], keys[1], status
         kp.plan_bytes, kp.plan, kp._bias = plan_bytes[j], plan, bias
-        kp._topo, kp._bias_src, kp._det = (nl, pa), pb, None
+        kp._topo, kp._bias_src, kp._det, kp._split = (nl, pa), pb, None, None
         out.append((meta, kp))
     check(lib().tt_trees_build(jobs, n, _stream(dev)), "tt_trees_build")
     return out
@@ -213,9 +213,9 @@ class KeyPlan:
     def __init__(self, horizon: torch.Tensor, past_bias: Optional[torch.Tensor] = None,
                  validate: bool = False, topo=None):
         """``topo``: the forest's host ``(node_len, parent)``, from which
-        ``det_slots`` sizes the deterministic backward's workspace exactly."""
+        ``det_slots`` and ``split_tiles`` size the backward's workspace exactly."""
         dev = horizon.device
-        self._topo, self._bias_src, self._det = topo, past_bias, None
+        self._topo, self._bias_src, self._det, self._split = topo, past_bias, None, None
         n_q = int(horizon.numel())
         n_past = 0 if past_bias is None else int(past_bias.numel())
         if past_bias is not None:
@@ -237,25 +237,40 @@ class KeyPlan:
             if s:
                 raise ValueError(f"gateway bias must be 0 or -inf (status bits {s:#x})")
 
+    def _tree_count(self, fn: str) -> int:
+        """``fn`` (tt_attn_det_slots / tt_attn_split_tiles) on the topology and
+        the host copy of the gateway bias."""
+        nl = np.ascontiguousarray(self._topo[0], dtype=np.int32)
+        pa = np.ascontiguousarray(self._topo[1], dtype=np.int32)
+        bias = None
+        if self._bias_src is not None:
+            bias = np.ascontiguousarray(torch.as_tensor(self._bias_src).detach().float().cpu().numpy())
+        out = ctypes.c_int64(0)
+        check(getattr(lib(), fn)(nl.ctypes.data, pa.ctypes.data, len(nl),
+                                 bias.ctypes.data if bias is not None else None, self.n_past, ctypes.byref(out)), fn)
+        return int(out.value)
+
     def det_slots(self) -> int:
         """Partial-sum slots of the deterministic backward for this tree
         (``tt_attn_det_slots``, host arithmetic on the topology; a gateway bias
         held on the device is copied once). 0 — the tree-independent bound —
         when the plan was built without its topology."""
         if self._det is None:
-            self._det = 0
-            if self._topo is not None:
-                nl = np.ascontiguousarray(self._topo[0], dtype=np.int32)
-                pa = np.ascontiguousarray(self._topo[1], dtype=np.int32)
-                bias = None
-                if self._bias_src is not None:
-                    bias = np.ascontiguousarray(torch.as_tensor(self._bias_src).detach().float().cpu().numpy())
-                out = ctypes.c_int64(0)
-                check(lib().tt_attn_det_slots(nl.ctypes.data, pa.ctypes.data, len(nl),
-                                              bias.ctypes.data if bias is not None else None, self.n_past,
-                                              ctypes.byref(out)), "tt_attn_det_slots")
-                self._det = int(out.value)
+            self._det = self._tree_count("tt_attn_det_slots") if self._topo is not None else 0
         return self._det
+
+    def split_tiles(self) -> int:
+        """Key tiles whose dK/dV the backward sums in fp32 rows of its
+        workspace (``tt_attn_split_tiles``, host arithmetic on the topology;
+        at least 1, since 0 asks for every key tile). 0 — every key tile —
+        when the plan was built without its topology, or when the gateway bias
+        is held on the device only (reading it back would wait for the device
+        on every backward)."""
+        if self._split is None:
+            on_dev = self._bias_src is not None and torch.as_tensor(self._bias_src).device.type != "cpu"
+            known = self._topo is not None and not on_dev
+            self._split = max(self._tree_count("tt_attn_split_tiles"), 1) if known else 0
+        return self._split
 
     def visible_pairs(self) -> int:
         """Visible (query, key) pairs per head, P (synchronises)."""
