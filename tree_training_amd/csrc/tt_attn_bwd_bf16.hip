@@ -313,6 +313,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
         const bool split = tt_kb_items(qlo, qhi, qch) > 1;
         int q_start, q_stop;
         tt_kb_item_range(qlo, qhi, qch, chunk, q_start, q_stop);
+        // a tile of gateway keys that no query sees adds nothing anywhere
+        if (q_stop <= q_start && kb * TT_BKB + TT_BKB <= a.n_past) continue;
         // the first query block's direct loads go out before the item's V and
         // K loads (stage 0 was last read before the previous item's final
         // barrier)

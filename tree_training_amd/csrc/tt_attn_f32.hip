@@ -451,6 +451,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         const bool split = tt_kb_items(qlo, qhi, qch) > 1;
         int q_start, q_stop;
         tt_kb_item_range(qlo, qhi, qch, chunk, q_start, q_stop);
+        // a tile of gateway keys that no query sees adds nothing anywhere
+        if (q_stop <= q_start && kb * TT_BKB + TT_BKB <= a.n_past) continue;
 
         {   // V rows of the tile's 128 keys (keys past the end alias the last key)
             const int dc = 4 * (threadIdx.x & 31), r0 = threadIdx.x >> 5;
