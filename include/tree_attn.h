@@ -247,9 +247,10 @@ int tt_attn_bwd(const tt_attn_problem* p, const void* o, const float* lse, tt_te
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). Same arguments, results and validation as
  * tt_attn_bwd, without ws / ws_bytes: the workspace is a scratch array of
- * TT_NOALLOC_SCRATCH_MB MiB that the library holds on each GPU it runs on
- * until the process ends (the current device's, hipGetDevice; `stream` must
- * belong to it). A problem whose tt_attn_bwd_workspace_bytes exceeds it
+ * TT_NOALLOC_SCRATCH_MB MiB on each GPU, taken by the first call on that GPU
+ * (the array's code object loads on first use: a process that never calls
+ * this entry point never holds it) and held until the process ends (the
+ * current device's, hipGetDevice; `stream` must belong to it). A problem whose tt_attn_bwd_workspace_bytes exceeds it
  * returns TT_E_WORKSPACE (either dtype needs 4 * Hq * n_q bytes plus the
  * split sums, 1 MiB per split tile at Hkv = 8, plus the dQ key-split
  * partials of small bf16 problems: with split_tiles from tt_attn_split_tiles,

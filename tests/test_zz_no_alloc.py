@@ -130,6 +130,61 @@ def test_noalloc_agent_tree_with_exact_split_tiles():
             assert _rel(a, b) < 2e-2, (name, _rel(a, b))
 
 
+_FIRST_CALL_PROBE = r"""
+import ctypes, torch
+from tree_training_amd import _lib
+from tree_training_amd.attention import _Problem, attn_forward
+from tree_training_amd.meta import KeyPlan, TreeMetaDevice
+dev = torch.device("cuda", 0)
+lens, par, HQ, HKV, D = [300, 200, 100], [-1, 0, 0], 32, 8, 128
+T = sum(lens)
+g = torch.Generator(device=dev).manual_seed(0)
+q = torch.randn(1, HQ, T, D, device=dev, generator=g, dtype=torch.bfloat16)
+k = torch.randn(1, HKV, T, D, device=dev, generator=g, dtype=torch.bfloat16)
+plan = KeyPlan(TreeMetaDevice(lens, par, device=dev).horizon)
+o, lse = attn_forward(q, k, k, plan, D ** -0.5)
+pb = _Problem(q, k, k, None, None, plan, D ** -0.5)
+do = torch.randn(T, HQ, D, device=dev, generator=g, dtype=torch.bfloat16)
+out = [torch.empty(T, h, D, device=dev, dtype=torch.bfloat16) for h in (HQ, HKV, HKV)]
+torch.cuda.synchronize()
+lib = _lib.lib()
+P = lambda t: ctypes.c_void_p(t.data_ptr())
+st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+free = [torch.cuda.mem_get_info(dev)[0]]
+lib.tt_noalloc_scratch_bytes()
+free.append(torch.cuda.mem_get_info(dev)[0])
+for _ in range(2):
+    _lib.check(lib.tt_attn_bwd_noalloc(ctypes.byref(pb.s), P(o), P(lse), _lib.TTTensor(do.data_ptr(), HQ * D, D),
+                                       *map(P, out), None, None, st), "tt_attn_bwd_noalloc")
+    torch.cuda.synchronize()
+    free.append(torch.cuda.mem_get_info(dev)[0])
+print("FREE", *free)
+"""
+
+
+def test_noalloc_scratch_reserved_on_first_call():
+    """The scratch array lives in a translation unit of its own, whose code
+    object HIP loads on first use: in a fresh process that has run the
+    library's other kernels, device memory is taken only by the first
+    tt_attn_bwd_noalloc call (>= the scratch size), and not again by the
+    second (a process that never calls it never holds the scratch)."""
+    import os
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("noalloc first-call probe (subprocess)", flush=True)
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_PROBE], cwd=root, capture_output=True, text=True,
+                       timeout=240, env=dict(os.environ, PYTHONPATH=root))
+    assert r.returncode == 0, r.stderr[-2000:]
+    line = [ln for ln in r.stdout.splitlines() if ln.startswith("FREE")][-1]
+    f0, f1, f2, f3 = map(int, line.split()[1:])
+    MiB = 1 << 20
+    print(f"taken: host query {(f0 - f1) / MiB:.1f} MiB, first call {(f1 - f2) / MiB:.1f} MiB, "
+          f"second call {(f2 - f3) / MiB:.1f} MiB", flush=True)
+    assert f0 - f1 < 4 * MiB
+    assert f1 - f2 >= _lib.lib().tt_noalloc_scratch_bytes()
+    assert abs(f2 - f3) < 4 * MiB
+
+
 def test_noalloc_rejects_problems_beyond_the_scratch():
     """A problem whose workspace exceeds the scratch array returns
     TT_E_WORKSPACE and launches nothing (outputs untouched)."""
