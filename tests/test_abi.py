@@ -241,6 +241,15 @@ def test_trees_build_job_count():
     assert ctypes.sizeof(_lib.TTTreeJob) == 144
 
 
+def test_binding_struct_sizes_match_the_header():
+    """The ctypes structs have the sizes tt_api.hip asserts for the header's
+    structs (a field missing on either side changes the size)."""
+    sizes = dict(TTTensor=24, TTAttnProblem=200, TTGdnProblem=240, TTConvProblem=72, TTPrologueProblem=120,
+                 TTTreeJob=144)
+    for name, n in sizes.items():
+        assert ctypes.sizeof(getattr(_lib, name)) == n, name
+
+
 def test_meta_and_plan_validation():
     lib = _lib.lib()
     V = ctypes.c_void_p(16)

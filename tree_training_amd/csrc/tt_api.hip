@@ -134,6 +134,9 @@ int tt_plan_build(const int32_t* key_lo, const int32_t* key_hi, int32_t n_keys, 
 }
 
 static_assert(sizeof(tt_tree_job) == 144, "tt_tree_job layout (bindings mirror it)");
+static_assert(sizeof(tt_tensor) == 24 && sizeof(tt_attn_problem) == 200 && sizeof(tt_gdn_problem) == 240 &&
+                  sizeof(tt_conv_problem) == 72 && sizeof(tt_prologue_problem) == 120,
+              "problem struct layouts (the ctypes bindings mirror them)");
 
 int tt_trees_build(const tt_tree_job* jobs, int32_t n_jobs, void* stream) {
     if (!jobs || n_jobs < 1 || n_jobs > TT_TREE_JOBS_MAX) return TT_E_ARG;
