@@ -210,9 +210,25 @@ def _plan_expected_fast(lo, hi, n_q):
     # split tiles (more than one work item) ranked in key order
     split = np.array([n_items(k) > 1 for k in range(n_kb)], bool)
     srank = np.where(split, np.cumsum(split) - 1, -1)
+    # work items as (tile rank, chunk): tile order, or, from 512 items on,
+    # window-major (top query window first; a window's items in tile order)
+    total = int(kb_base[-1])
+    wm = total >= 512
+    if not wm:
+        items = [(r, c) for r, k in enumerate(kb_order) for c in range(n_items(k))]
+    else:
+        items = []
+        for w in range((n_q - 1) // qch, -1, -1):
+            for r, k in enumerate(kb_order):
+                if n_items(k) > 1:
+                    if qlo[k] // qch <= w <= (qhi[k] - 1) // qch:
+                        items.append((r, w - qlo[k] // qch))
+                elif ((qhi[k] - 1) // qch if qhi[k] > qlo[k] else 0) == w:
+                    items.append((r, 0))
+    assert len(items) == total
     return dict(P=int(np.clip(b - a, 0, None).sum()), n_qb=n_qb, n_kt=n_kt, n_kb=n_kb, rows=rows,
                 row_order=row_order, qlo=qlo, qhi=qhi, kb_order=kb_order, kb_base=kb_base, kb_srank=srank,
-                n_split=int(split.sum()))
+                n_split=int(split.sum()), kb_item=np.array(items, np.int32).reshape(-1, 2), window_major=int(wm))
 
 
 def _plan_decode(buf, n_q, n_keys):
@@ -227,12 +243,14 @@ def _plan_decode(buf, n_q, n_keys):
     qhi = i32(o, n_kb); o += 4 * n_kb
     kb_order = i32(o, n_kb); o += 4 * n_kb
     kb_base = i32(o, n_kb + 1); o += 4 * (n_kb + 1)
-    kb_srank = i32(o, n_kb)
-    hdr = i32(8, 5)
+    kb_srank = i32(o, n_kb); o += 4 * n_kb
+    o = (o + 7) & ~7
+    hdr = i32(8, 6)
+    kb_item = i32(o, 2 * int(hdr[3])).reshape(-1, 2)
     return dict(P=int(np.frombuffer(buf, np.uint64, 1, 0)[0]), n_qb=int(hdr[0]), n_kt=int(hdr[1]),
-                n_kb=int(hdr[2]), n_items=int(hdr[3]), n_split=int(hdr[4]),
+                n_kb=int(hdr[2]), n_items=int(hdr[3]), n_split=int(hdr[4]), window_major=int(hdr[5]),
                 rows=[list(row_list[q, :row_cnt[q]]) for q in range(n_qb)], row_order=list(row_order),
-                qlo=qlo, qhi=qhi, kb_order=list(kb_order), kb_base=kb_base, kb_srank=kb_srank)
+                qlo=qlo, qhi=qhi, kb_order=list(kb_order), kb_base=kb_base, kb_srank=kb_srank, kb_item=kb_item)
 
 
 def test_build_trees_matches_separate_calls():
@@ -265,9 +283,10 @@ def test_build_trees_matches_separate_calls():
         n_q, n_keys = plan.n_q, plan.n_keys
         a = _plan_decode(plan.plan.cpu().numpy().tobytes(), n_q, n_keys)
         b = _plan_decode(p2.plan.cpu().numpy().tobytes(), n_q, n_keys)
-        for k in ("P", "n_qb", "n_kt", "n_kb", "n_items", "n_split", "rows", "row_order", "kb_order"):
+        for k in ("P", "n_qb", "n_kt", "n_kb", "n_items", "n_split", "window_major", "rows", "row_order",
+                  "kb_order"):
             assert a[k] == b[k], (i, k)
-        for k in ("qlo", "qhi", "kb_base", "kb_srank"):
+        for k in ("qlo", "qhi", "kb_base", "kb_srank", "kb_item"):
             assert np.array_equal(a[k], b[k]), (i, k)
         st = int(meta.status.item())
         want = int(m2.status.item()) | int(p2.status.item())
@@ -275,13 +294,14 @@ def test_build_trees_matches_separate_calls():
         assert (st == TT_STATUS_BAD_BIAS) == (i == len(specs) - 2), (i, st)
 
 
-@pytest.mark.parametrize("case", ["forest", "agent16k", "gateway", "rollout270k"])
+@pytest.mark.parametrize("case", ["forest", "agent16k", "gateway", "rollout48k", "rollout270k"])
 def test_plan_matches_numpy(case):
     """Every field of the device tile plan equals the numpy restatement
     (bit-exact: it is index work). Up to 2048 query blocks and key tiles the
     plan's last passes run as one workgroup; the 270K-token rollout (2112 of
     each, and more than 65536 tokens for the metadata) takes the multi-launch
-    paths."""
+    paths. The rollout trees' work items (1,128 and more) are listed
+    window-major, the others' in tile order."""
     from tree_training_amd.meta import KeyPlan
     bias = None
     if case == "forest":
@@ -290,6 +310,8 @@ def test_plan_matches_numpy(case):
         lens, par = workloads.agent_tree(0)
     elif case == "rollout270k":
         lens, par = [8192] + [1024] * 256, [-1] + [0] * 256
+    elif case == "rollout48k":
+        lens, par = workloads.rollout_tree(0)
     else:
         lens, par = [700, 500, 300], [-1, 0, 0]
         vis = np.random.default_rng(3).random(1300) < 0.7
@@ -312,11 +334,12 @@ def test_plan_matches_numpy(case):
         assert np.array_equal(m.pos.cpu().numpy(), ref["pos"])
         assert np.array_equal(m.horizon.cpu().numpy(), ref["horizon"])
         assert exp["n_qb"] > 2048 and exp["n_kb"] > 2048 and n_q > 65536
-    for k in ("P", "n_qb", "n_kt", "n_kb", "n_split", "rows", "row_order", "kb_order"):
+    for k in ("P", "n_qb", "n_kt", "n_kb", "n_split", "window_major", "rows", "row_order", "kb_order"):
         assert got[k] == exp[k], k
-    for k in ("qlo", "qhi", "kb_base", "kb_srank"):
+    for k in ("qlo", "qhi", "kb_base", "kb_srank", "kb_item"):
         assert np.array_equal(got[k], exp[k]), k
     assert got["n_items"] == exp["kb_base"][-1]
+    assert exp["window_major"] == (case.startswith("rollout"))
     if bias is None:   # the host count (tt_attn_split_tiles) is the plan's
         assert KeyPlan(m.horizon, topo=(lens, par)).split_tiles() == max(exp["n_split"], 1)
 

@@ -71,6 +71,7 @@ int make_dev(const tt_attn_problem* p, AttnDev* a) {
     a->kb_order = reinterpret_cast<const int32_t*>(base + L.kb_order);
     a->kb_base = reinterpret_cast<const int32_t*>(base + L.kb_base);
     a->kb_srank = reinterpret_cast<const int32_t*>(base + L.kb_srank);
+    a->kb_item = reinterpret_cast<const int2*>(base + L.kb_item);
     a->n_items = reinterpret_cast<const int32_t*>(base) + 5;
     return TT_OK;
 }

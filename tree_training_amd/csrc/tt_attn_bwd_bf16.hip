@@ -300,13 +300,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
         // readfirstlane keeps them, and everything derived from them, scalar.
         const int g = __builtin_amdgcn_readfirstlane(w_id % a.hkv);
         const int item = __builtin_amdgcn_readfirstlane(w_id / a.hkv);
-        int lo_r = 0, hi_r = a.n_kb - 1;        // last tile rank whose first item <= item
-        while (lo_r < hi_r) {
-            const int mid = (lo_r + hi_r + 1) >> 1;
-            if (a.kb_base[mid] <= item) lo_r = mid; else hi_r = mid - 1;
-        }
+        const int2 rc = a.kb_item[item];           // (tile rank, chunk): the plan's item order
+        const int lo_r = __builtin_amdgcn_readfirstlane(rc.x);
+        const int chunk = __builtin_amdgcn_readfirstlane(rc.y);
         const int kb = __builtin_amdgcn_readfirstlane(a.kb_order[lo_r]);
-        const int chunk = __builtin_amdgcn_readfirstlane(item - a.kb_base[lo_r]);
+        // a later item's slot: the tile's items before it that are not its
+        // first, after those of the tiles ranked before it
+        const int64_t slot = (int64_t)a.kb_base[lo_r] - lo_r + chunk - 1;
         const int qlo = __builtin_amdgcn_readfirstlane(a.kb_qlo[kb]);
         const int qhi = __builtin_amdgcn_readfirstlane(a.kb_qhi[kb]);
         const int qch = tt_qch(a.n_q);
@@ -467,18 +467,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_DKDV_WAV
 
         // Epilogue: rows of dk/dv = this wave's keys, columns = d. In the
         // deterministic mode a split tile's first item stores its partial sums
-        // in the fp32 rows and each later item in its own slot (item - rank - 1
-        // counts the items before it that are not the first of their tile);
-        // the finalize pass adds them in item order.
+        // in the fp32 rows and each later item in its own slot (`slot` above);
+        // the finalize pass adds them in chunk order.
         const bool det_split = split && bw.det;
         // a split tile's rows in the split sums (first items) and a later item's
         // slot: one that lies beyond the workspace writes nothing (the tile's
         // gradients become NaN in the finalize)
         const SplitRows sr = split ? split_rows(a, bw, kb) : SplitRows{0, false};
-        const bool det_skip = det_split && (chunk > 0 ? (int64_t)(item - lo_r - 1) >= bw.det_cap : !sr.ok);
+        const bool det_skip = det_split && (chunk > 0 ? slot >= bw.det_cap : !sr.ok);
         float* const sk = chunk == 0 ? bw.dk_ws : bw.dk_slot;
         float* const sv = chunk == 0 ? bw.dv_ws : bw.dv_slot;
-        const int64_t srow = chunk == 0 ? sr.row0 : (int64_t)(item - lo_r - 1) * TT_BKB - kb * TT_BKB;
+        const int64_t srow = chunk == 0 ? sr.row0 : slot * TT_BKB - kb * TT_BKB;
         const int kbase = kb * TT_BKB + wave * 32;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {

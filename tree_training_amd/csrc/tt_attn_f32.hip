@@ -438,13 +438,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     for (int w_id = blockIdx.x; w_id < n_work; w_id += gridDim.x) {
         const int g = __builtin_amdgcn_readfirstlane(w_id % a.hkv);
         const int item = __builtin_amdgcn_readfirstlane(w_id / a.hkv);
-        int lo_r = 0, hi_r = a.n_kb - 1;        // last tile rank whose first item <= item
-        while (lo_r < hi_r) {
-            const int mid = (lo_r + hi_r + 1) >> 1;
-            if (a.kb_base[mid] <= item) lo_r = mid; else hi_r = mid - 1;
-        }
+        const int2 rc = a.kb_item[item];           // (tile rank, chunk): the plan's item order
+        const int lo_r = __builtin_amdgcn_readfirstlane(rc.x);
+        const int chunk = __builtin_amdgcn_readfirstlane(rc.y);
         const int kb = __builtin_amdgcn_readfirstlane(a.kb_order[lo_r]);
-        const int chunk = __builtin_amdgcn_readfirstlane(item - a.kb_base[lo_r]);
+        // a later item's slot: the tile's items before it that are not its
+        // first, after those of the tiles ranked before it
+        const int64_t slot = (int64_t)a.kb_base[lo_r] - lo_r + chunk - 1;
         const int qlo = __builtin_amdgcn_readfirstlane(a.kb_qlo[kb]);
         const int qhi = __builtin_amdgcn_readfirstlane(a.kb_qhi[kb]);
         const int qch = tt_qch(a.n_q);
@@ -559,10 +559,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         // slot: one that lies beyond the workspace writes nothing (the tile's
         // gradients become NaN in the finalize)
         const SplitRows sr = split ? split_rows(a, bw, kb) : SplitRows{0, false};
-        const bool det_skip = det_split && (chunk > 0 ? (int64_t)(item - lo_r - 1) >= bw.det_cap : !sr.ok);
+        const bool det_skip = det_split && (chunk > 0 ? slot >= bw.det_cap : !sr.ok);
         float* const sk = chunk == 0 ? bw.dk_ws : bw.dk_slot;
         float* const sv = chunk == 0 ? bw.dv_ws : bw.dv_slot;
-        const int64_t srow = chunk == 0 ? sr.row0 : (int64_t)(item - lo_r - 1) * TT_BKB - kb * TT_BKB;
+        const int64_t srow = chunk == 0 ? sr.row0 : slot * TT_BKB - kb * TT_BKB;
         const int kbase = kb * TT_BKB + wave * 32;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {

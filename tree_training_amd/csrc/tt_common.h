@@ -83,7 +83,8 @@ __host__ __device__ inline void tt_kb_item_range(int qlo, int qhi, int qch, int 
 
 // Plan buffer layout. Header (bytes): [0,8) uint64 visible pairs per head;
 // int32 at 8: n_qb, 12: n_kt, 16: n_kb, 20: n_items (dK/dV work items), 24:
-// n_split (key tiles of more than one work item).
+// n_split (key tiles of more than one work item), 28: 1 when kb_item is
+// window-major.
 // Then int32 arrays:
 //   row_cnt[n_qb]           non-empty key tiles per query block
 //   row_order[n_qb]         query blocks by decreasing tile count
@@ -93,12 +94,16 @@ __host__ __device__ inline void tt_kb_item_range(int qlo, int qhi, int qch, int 
 //   kb_base[n_kb + 1]       first work item of each key tile, in kb_order order
 //   kb_srank[n_kb]          rank of each key tile among the split ones, in key
 //                           order (-1: not split): its rows in the split sums
-// and a byte array cls[n_qb * n_kt] (tile classes, build scratch).
+// then int2 kb_item[n_items] (8-byte aligned; room for n_kb * query windows):
+// (tile rank in kb_order, chunk) of each dK/dV work item in the order the
+// persistent grid takes them, and a byte array cls[n_qb * n_kt] (tile
+// classes, build scratch).
 #define TT_PLAN_HDR 64
 struct PlanLayout {
     int n_qb, n_kt, n_kb;
     int n_pb;   // 256-key blocks of the pair count
-    size_t row_cnt, row_order, row_list, kb_qlo, kb_qhi, kb_order, kb_base, kb_srank, pair_part, cls, total;
+    size_t row_cnt, row_order, row_list, kb_qlo, kb_qhi, kb_order, kb_base, kb_srank, kb_item, pair_part, cls,
+        total;
     __host__ __device__ PlanLayout(int n_q, int n_keys) {
         n_qb = tt_cdiv(n_q, TT_BQ);
         n_kt = tt_cdiv(n_keys, TT_BK);
@@ -114,6 +119,7 @@ struct PlanLayout {
         kb_base = o;   o += 4 * ((size_t)n_kb + 1);
         kb_srank = o;  o += 4 * (size_t)n_kb;
         o = (o + 7) & ~(size_t)7;
+        kb_item = o;   o += 8 * (size_t)n_kb * ((n_q - 1) / tt_qch(n_q) + 1);
         pair_part = o; o += 8 * (size_t)n_pb;
         cls = o;       o += (size_t)n_qb * n_kt;
         total = (o + 255) & ~(size_t)255;

@@ -23,6 +23,7 @@ struct AttnDev {
     const int32_t* kb_order;  // plan: key tiles, widest range first
     const int32_t* kb_base;   // plan: first dK/dV work item per key tile (kb_order order)
     const int32_t* kb_srank;  // plan: rank of each key tile among the split ones (-1: not split)
+    const int2* kb_item;      // plan: (tile rank, chunk) of each dK/dV work item, in the order they are taken
     const int32_t* n_items;   // plan: number of dK/dV work items
     int n_q, n_past, n_keys, hq, hkv, rep, n_qb, n_kt, n_kb;
     float scale;

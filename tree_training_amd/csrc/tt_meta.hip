@@ -440,13 +440,75 @@ __device__ __forceinline__ void plan_split_ranks(const int32_t* __restrict__ kb_
     if (tid == 0) reinterpret_cast<int32_t*>(plan)[6] = s_c;
 }
 
+// The dK/dV work items in the order the persistent grid takes them, as (tile
+// rank, chunk) pairs. A tree with at least kWindowMajorItems items lists them
+// window-major: every key tile's item in the top query window, then the next
+// window down, each window's items in tile order (widest range first). The
+// workgroups resident on an XCD (one kv head's items) then walk the same
+// query rows at once and share their Q / dO in L2; with tile order (a tile's
+// items together, widest tile first) they walk a dozen windows at once on the
+// 48K rollout tree. Smaller trees keep tile order, which balances their few
+// long items better. Run by a whole workgroup of 1024 threads once kb_base is
+// final; n_items = kb_base[n_kb]. Header int32 7: 1 when window-major.
+constexpr int kWindowMajorItems = 512;
+__device__ __forceinline__ void plan_item_list(const int32_t* __restrict__ kb_qlo,
+                                               const int32_t* __restrict__ kb_qhi,
+                                               const int32_t* __restrict__ kb_order,
+                                               const int32_t* __restrict__ kb_base, int n_kb, int n_q, int qch,
+                                               int2* __restrict__ kb_item, uint8_t* __restrict__ plan) {
+    __shared__ int s_w[16];
+    __shared__ int s_c;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const bool wm = kb_base[n_kb] >= kWindowMajorItems;
+    if (!wm) {
+        for (int r = tid; r < n_kb; r += 1024) {
+            const int b = kb_base[r], m = kb_base[r + 1] - b;
+            for (int c = 0; c < m; ++c) kb_item[b + c] = make_int2(r, c);
+        }
+    } else {
+        if (tid == 0) s_c = 0;
+        __syncthreads();
+        for (int w = (n_q - 1) / qch; w >= 0; --w) {
+            for (int base = 0; base < n_kb; base += 1024) {
+                const int r = base + tid;
+                int f = 0, chunk = 0;
+                if (r < n_kb) {
+                    const int kb = kb_order[r], lo = kb_qlo[kb], hi = kb_qhi[kb];
+                    if (tt_kb_items(lo, hi, qch) > 1) {   // one item per window it touches
+                        f = lo / qch <= w && w <= (hi - 1) / qch;
+                        chunk = w - lo / qch;
+                    } else {                              // its one item, in its top window
+                        f = (hi > lo ? (hi - 1) / qch : 0) == w;
+                    }
+                }
+                const unsigned long long m = __ballot(f);
+                if (lane == 0) s_w[wave] = __popcll(m);
+                __syncthreads();
+                int before = s_c;
+                for (int x = 0; x < wave; ++x) before += s_w[x];
+                if (f) kb_item[before + __popcll(m & ((1ull << lane) - 1))] = make_int2(r, chunk);
+                __syncthreads();
+                if (tid == 0) {
+                    int tot = 0;
+                    for (int x = 0; x < 16; ++x) tot += s_w[x];
+                    s_c += tot;
+                }
+                __syncthreads();
+            }
+        }
+    }
+    if (tid == 0) reinterpret_cast<int32_t*>(plan)[7] = wm ? 1 : 0;
+}
+
 // Plan pass 4: the dK/dV work-item offsets of the ordered key tiles, then the
-// header (pairs P, n_qb, n_kt, n_kb, n_items, n_split) and the split ranks.
+// header (pairs P, n_qb, n_kt, n_kb, n_items, n_split), the split ranks and
+// the work-item list.
 __global__ __launch_bounds__(1024) void plan_kb_base_kernel(const int32_t* __restrict__ kb_qlo,
                                                             const int32_t* __restrict__ kb_qhi,
                                                             const int32_t* __restrict__ kb_order, int n_kb,
                                                             int qch, int32_t* __restrict__ kb_base,
-                                                            int32_t* __restrict__ kb_srank,
+                                                            int32_t* __restrict__ kb_srank, int2* __restrict__ kb_item,
+                                                            int n_q,
                                                             const unsigned long long* __restrict__ pair_part,
                                                             int n_pb, int n_qb, int n_kt, uint8_t* __restrict__ plan) {
     __shared__ unsigned long long s_pairs;
@@ -492,6 +554,7 @@ __global__ __launch_bounds__(1024) void plan_kb_base_kernel(const int32_t* __res
         hdr[5] = s_carry;
     }
     plan_split_ranks(kb_qlo, kb_qhi, n_kb, qch, kb_srank, plan);
+    plan_item_list(kb_qlo, kb_qhi, kb_order, kb_base, n_kb, n_q, qch, kb_item, plan);
 }
 
 // Plan passes 2-4 in one workgroup (plans of up to kFinishMax query blocks and
@@ -506,7 +569,7 @@ __device__ __forceinline__ void plan_finish_body(const uint8_t* __restrict__ cls
                                                  int32_t* __restrict__ row_cnt, int32_t* __restrict__ row_list,
                                                  int32_t* __restrict__ row_order, int32_t* __restrict__ kb_order,
                                                  int32_t* __restrict__ kb_base, int32_t* __restrict__ kb_srank,
-                                                 uint8_t* __restrict__ plan) {
+                                                 int2* __restrict__ kb_item, int n_q, uint8_t* __restrict__ plan) {
     __shared__ __attribute__((aligned(16))) int s_cnt[kFinishMax];
     __shared__ int s_kbo[kFinishMax];
     __shared__ __attribute__((aligned(16))) int s_kbw[kFinishMax];   // query range width of each key tile
@@ -622,6 +685,7 @@ __device__ __forceinline__ void plan_finish_body(const uint8_t* __restrict__ cls
         hdr[5] = s_carry;
     }
     plan_split_ranks(kb_qlo, kb_qhi, n_kb, qch, kb_srank, plan);
+    plan_item_list(kb_qlo, kb_qhi, kb_order, kb_base, n_kb, n_q, qch, kb_item, plan);
 }
 
 __global__ __launch_bounds__(1024) void plan_finish_kernel(const uint8_t* __restrict__ cls, int n_qb, int n_kt,
@@ -632,9 +696,10 @@ __global__ __launch_bounds__(1024) void plan_finish_kernel(const uint8_t* __rest
                                                            int32_t* __restrict__ row_order,
                                                            int32_t* __restrict__ kb_order,
                                                            int32_t* __restrict__ kb_base, int32_t* __restrict__ kb_srank,
+                                                           int2* __restrict__ kb_item, int n_q,
                                                            uint8_t* __restrict__ plan) {
     plan_finish_body(cls, n_qb, n_kt, kb_qlo, kb_qhi, n_kb, qch, pair_part, n_pb, row_cnt, row_list, row_order,
-                     kb_order, kb_base, kb_srank, plan);
+                     kb_order, kb_base, kb_srank, kb_item, n_q, plan);
 }
 
 // ---------------------------------------------------------------------------
@@ -669,6 +734,7 @@ static_assert(sizeof(TreeJobsDev) <= 3072, "the jobs travel as one kernel argume
 struct PlanPtrs {
     PlanLayout L;
     int32_t *row_cnt, *row_order, *row_list, *kb_qlo, *kb_qhi, *kb_order, *kb_base, *kb_srank;
+    int2* kb_item;
     uint8_t* cls;
     unsigned long long* pair_part;
     int nb_cls, nb_kv;
@@ -681,6 +747,7 @@ struct PlanPtrs {
         kb_order = reinterpret_cast<int32_t*>(base + L.kb_order);
         kb_base = reinterpret_cast<int32_t*>(base + L.kb_base);
         kb_srank = reinterpret_cast<int32_t*>(base + L.kb_srank);
+        kb_item = reinterpret_cast<int2*>(base + L.kb_item);
         cls = base + L.cls;
         pair_part = reinterpret_cast<unsigned long long*>(base + L.pair_part);
         nb_cls = tt_cdiv(L.n_qb * L.n_kt, 4);
@@ -724,7 +791,7 @@ __global__ __launch_bounds__(1024) void trees_plan_finish_kernel(TreeJobsDev J) 
     const TreeJobDev& jb = J.j[blockIdx.x];
     const PlanPtrs P(jb.plan, jb.T, jb.n_past + jb.T);
     plan_finish_body(P.cls, P.L.n_qb, P.L.n_kt, P.kb_qlo, P.kb_qhi, P.L.n_kb, tt_qch(jb.T), P.pair_part, P.L.n_pb,
-                     P.row_cnt, P.row_list, P.row_order, P.kb_order, P.kb_base, P.kb_srank, jb.plan);
+                     P.row_cnt, P.row_list, P.row_order, P.kb_order, P.kb_base, P.kb_srank, P.kb_item, jb.T, jb.plan);
 }
 
 }  // namespace
@@ -819,6 +886,7 @@ int tt_plan_build_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys,
     int32_t* kb_order = reinterpret_cast<int32_t*>(base + L.kb_order);
     int32_t* kb_base = reinterpret_cast<int32_t*>(base + L.kb_base);
     int32_t* kb_srank = reinterpret_cast<int32_t*>(base + L.kb_srank);
+    int2* kb_item = reinterpret_cast<int2*>(base + L.kb_item);
     uint8_t* cls = base + L.cls;
     unsigned long long* pair_part = reinterpret_cast<unsigned long long*>(base + L.pair_part);
     const int nb_cls = tt_cdiv(L.n_qb * L.n_kt, 4), nb_kv = tt_cdiv(L.n_kb, 4);
@@ -827,7 +895,7 @@ int tt_plan_build_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys,
     if (L.n_qb <= kFinishMax && L.n_kb <= kFinishMax) {
         hipLaunchKernelGGL(plan_finish_kernel, dim3(1), dim3(1024), 0, s, cls, L.n_qb, L.n_kt, kb_qlo, kb_qhi, L.n_kb,
                            tt_qch(n_q), pair_part, L.n_pb, row_cnt, row_list, row_order, kb_order, kb_base, kb_srank,
-                           base);
+                           kb_item, n_q, base);
         return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
     }
     hipLaunchKernelGGL(plan_compact_kernel, dim3(tt_cdiv(L.n_qb, 4)), dim3(256), 0, s, cls, L.n_qb, L.n_kt,
@@ -836,6 +904,6 @@ int tt_plan_build_impl(const int32_t* key_lo, const int32_t* key_hi, int n_keys,
     hipLaunchKernelGGL(plan_orders_kernel, dim3(nb_ro + tt_cdiv(L.n_kb, 256)), dim3(256), 0, s, row_cnt, L.n_qb,
                        nb_ro, kb_qlo, kb_qhi, L.n_kb, row_order, kb_order);
     hipLaunchKernelGGL(plan_kb_base_kernel, dim3(1), dim3(1024), 0, s, kb_qlo, kb_qhi, kb_order, L.n_kb, tt_qch(n_q),
-                       kb_base, kb_srank, pair_part, L.n_pb, L.n_qb, L.n_kt, base);
+                       kb_base, kb_srank, kb_item, n_q, pair_part, L.n_pb, L.n_qb, L.n_kt, base);
     return hipGetLastError() == hipSuccess ? TT_OK : TT_E_HIP;
 }
