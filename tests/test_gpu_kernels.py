@@ -435,6 +435,33 @@ def test_attention_parity(case, dtype):
         check_close(name, ref, got, tol)
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_attention_random_forests(seed):
+    """Seeded random cases against the fp64 oracle: irregular forests (1-3
+    roots, depth up to 6, node lengths up to a drawn maximum, at most 2,500
+    tokens), half of them under a gateway of up to 600 keys with a drawn
+    visible share, either dtype, the backward in one call or in parts, with
+    and without TT_BWD_DETERMINISTIC."""
+    rng = np.random.default_rng(1000 + seed)
+    while True:
+        lens, par = workloads.random_forest(int(rng.integers(0, 10**6)), n_roots=(1, int(rng.integers(1, 4))),
+                                            max_depth=int(rng.integers(1, 7)), max_branch=int(rng.integers(1, 5)),
+                                            node_len=(1, int(rng.integers(2, 400))))
+        if sum(lens) <= 2500:
+            break
+    dtype = torch.bfloat16 if rng.random() < 0.6 else torch.float32
+    Lp = int(rng.integers(1, 600)) if rng.random() < 0.5 else 0
+    past_vis = [bool(x) for x in (rng.random(Lp) < rng.random())] if Lp else None
+    det = bool(rng.random() < 0.3)
+    parts = [(0,), (3, 4), (1, 2, 4)][int(rng.integers(0, 3))]
+    say(f"attention random forest seed={seed}: T={sum(lens)} nodes={len(lens)} Lp={Lp} dtype={dtype} det={det} "
+        f"parts={parts}")
+    res = _run(lens, par, dtype, seed=seed, past_vis=past_vis, parts=parts, deterministic=det)
+    for name, (ref, got) in res.items():
+        if name != "lse":
+            check_close(name, ref, got, TOL[dtype])
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
 @pytest.mark.parametrize("shape", ["short", "split"])
 def test_attention_gateway(dtype, shape):
