@@ -73,6 +73,37 @@ def test_gdn_fp32_matches_oracle(case):
     assert _rel(st, st_ref) < 1e-5, case
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_gdn_random_forests_match_oracle(seed):
+    """Seeded random forests (1-3 roots, node lengths up to a drawn maximum of
+    at most 150 tokens, at most 900 tokens), 1-4 q/k heads with one or two v
+    heads each, simple or realistic gates, exact or reference semantics:
+    float32 outputs and node states against the float64 oracle, < 1e-5."""
+    rng = np.random.default_rng(2000 + seed)
+    while True:
+        lens, par = random_forest(int(rng.integers(0, 10**6)), n_roots=(1, int(rng.integers(1, 4))),
+                                  max_depth=int(rng.integers(1, 6)), max_branch=int(rng.integers(1, 4)),
+                                  node_len=(1, int(rng.integers(2, 150))))
+        if sum(lens) <= 900:
+            break
+    T = sum(lens)
+    Hk = int(rng.choice([1, 2, 4]))
+    Hv = Hk * int(rng.choice([1, 2]))
+    mode = "reference" if rng.random() < 0.4 else "exact"
+    real = bool(rng.random() < 0.5)
+    print(f"gdn random forest seed={seed}: T={T} nodes={len(lens)} Hk={Hk} Hv={Hv} {mode} realistic={real}",
+          flush=True)
+    q, k, v, g, beta = _inputs(T, Hk, Hv, 3000 + seed, realistic_gates=real)
+    dev = torch.device("cuda", 0)
+    t = lambda x: torch.from_numpy(x).to(dev)
+    o, st = gdn_tree_forward(t(q), t(k), t(v), t(g), t(beta), GdnTree(lens, par, dev),
+                             reference_truncated=mode == "reference")
+    torch.cuda.synchronize()
+    o_ref, st_ref = ogdn.gdn_tree(q, k, v, g, beta, lens, par, mode=mode)
+    assert _rel(o.cpu().numpy(), o_ref) < 1e-5
+    assert _rel(st.cpu().numpy(), st_ref) < 1e-5
+
+
 @pytest.mark.parametrize("case", ["forest_multi_chunk", "c1_heads"])
 def test_gdn_bf16_matches_oracle(case):
     c = CASES[case]
