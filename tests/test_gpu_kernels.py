@@ -210,12 +210,26 @@ def _plan_expected_fast(lo, hi, n_q):
     # split tiles (more than one work item) ranked in key order
     split = np.array([n_items(k) > 1 for k in range(n_kb)], bool)
     srank = np.where(split, np.cumsum(split) - 1, -1)
-    # work items as (tile rank, chunk): tile order, or, from 512 items on,
+    # work items as (tile rank, chunk): up to 4096 items sorted by length
+    # (descending), then query window (descending), rank, chunk; above that
     # window-major (top query window first; a window's items in tile order)
     total = int(kb_base[-1])
-    wm = total >= 512
+    wm = total > 4096
     if not wm:
-        items = [(r, c) for r, k in enumerate(kb_order) for c in range(n_items(k))]
+        keyed = []
+        for r, k in enumerate(kb_order):
+            m = n_items(k)
+            for c in range(m):
+                if qhi[k] <= qlo[k]:
+                    q0 = q1 = 0
+                elif m == 1:
+                    q0, q1 = (qlo[k] // 32) * 32, qhi[k]
+                else:
+                    w = qlo[k] // qch + c
+                    q0, q1 = max((qlo[k] // 32) * 32, w * qch), min(qhi[k], (w + 1) * qch)
+                w = qlo[k] // qch + c if m > 1 else ((qhi[k] - 1) // qch if qhi[k] > qlo[k] else 0)
+                keyed.append((-min(max(q1 - q0, 0), 4096), -w, r, c))
+        items = [(r, c) for _, _, r, c in sorted(keyed)]
     else:
         items = []
         for w in range((n_q - 1) // qch, -1, -1):
@@ -228,7 +242,7 @@ def _plan_expected_fast(lo, hi, n_q):
     assert len(items) == total
     return dict(P=int(np.clip(b - a, 0, None).sum()), n_qb=n_qb, n_kt=n_kt, n_kb=n_kb, rows=rows,
                 row_order=row_order, qlo=qlo, qhi=qhi, kb_order=kb_order, kb_base=kb_base, kb_srank=srank,
-                n_split=int(split.sum()), kb_item=np.array(items, np.int32).reshape(-1, 2), window_major=int(wm))
+                n_split=int(split.sum()), kb_item=np.array(items, np.int32).reshape(-1, 2), item_order=2 if wm else 1)
 
 
 def _plan_decode(buf, n_q, n_keys):
@@ -248,7 +262,7 @@ def _plan_decode(buf, n_q, n_keys):
     hdr = i32(8, 6)
     kb_item = i32(o, 2 * int(hdr[3])).reshape(-1, 2)
     return dict(P=int(np.frombuffer(buf, np.uint64, 1, 0)[0]), n_qb=int(hdr[0]), n_kt=int(hdr[1]),
-                n_kb=int(hdr[2]), n_items=int(hdr[3]), n_split=int(hdr[4]), window_major=int(hdr[5]),
+                n_kb=int(hdr[2]), n_items=int(hdr[3]), n_split=int(hdr[4]), item_order=int(hdr[5]),
                 rows=[list(row_list[q, :row_cnt[q]]) for q in range(n_qb)], row_order=list(row_order),
                 qlo=qlo, qhi=qhi, kb_order=list(kb_order), kb_base=kb_base, kb_srank=kb_srank, kb_item=kb_item)
 
@@ -283,7 +297,7 @@ def test_build_trees_matches_separate_calls():
         n_q, n_keys = plan.n_q, plan.n_keys
         a = _plan_decode(plan.plan.cpu().numpy().tobytes(), n_q, n_keys)
         b = _plan_decode(p2.plan.cpu().numpy().tobytes(), n_q, n_keys)
-        for k in ("P", "n_qb", "n_kt", "n_kb", "n_items", "n_split", "window_major", "rows", "row_order",
+        for k in ("P", "n_qb", "n_kt", "n_kb", "n_items", "n_split", "item_order", "rows", "row_order",
                   "kb_order"):
             assert a[k] == b[k], (i, k)
         for k in ("qlo", "qhi", "kb_base", "kb_srank", "kb_item"):
@@ -300,8 +314,8 @@ def test_plan_matches_numpy(case):
     (bit-exact: it is index work). Up to 2048 query blocks and key tiles the
     plan's last passes run as one workgroup; the 270K-token rollout (2112 of
     each, and more than 65536 tokens for the metadata) takes the multi-launch
-    paths. The rollout trees' work items (1,128 and more) are listed
-    window-major, the others' in tile order."""
+    paths. The dK/dV work items are sorted by length, then query window, up
+    to 4096 of them (the 270K tree's are listed window-major)."""
     from tree_training_amd.meta import KeyPlan
     bias = None
     if case == "forest":
@@ -334,12 +348,12 @@ def test_plan_matches_numpy(case):
         assert np.array_equal(m.pos.cpu().numpy(), ref["pos"])
         assert np.array_equal(m.horizon.cpu().numpy(), ref["horizon"])
         assert exp["n_qb"] > 2048 and exp["n_kb"] > 2048 and n_q > 65536
-    for k in ("P", "n_qb", "n_kt", "n_kb", "n_split", "window_major", "rows", "row_order", "kb_order"):
+    for k in ("P", "n_qb", "n_kt", "n_kb", "n_split", "item_order", "rows", "row_order", "kb_order"):
         assert got[k] == exp[k], k
     for k in ("qlo", "qhi", "kb_base", "kb_srank", "kb_item"):
         assert np.array_equal(got[k], exp[k]), k
     assert got["n_items"] == exp["kb_base"][-1]
-    assert exp["window_major"] == (case.startswith("rollout"))
+    assert exp["item_order"] == (2 if case == "rollout270k" else 1)
     if bias is None:   # the host count (tt_attn_split_tiles) is the plan's
         assert KeyPlan(m.horizon, topo=(lens, par)).split_tiles() == max(exp["n_split"], 1)
 

@@ -441,29 +441,64 @@ __device__ __forceinline__ void plan_split_ranks(const int32_t* __restrict__ kb_
 }
 
 // The dK/dV work items in the order the persistent grid takes them, as (tile
-// rank, chunk) pairs. A tree with at least kWindowMajorItems items lists them
-// window-major: every key tile's item in the top query window, then the next
-// window down, each window's items in tile order (widest range first). The
-// workgroups resident on an XCD (one kv head's items) then walk the same
-// query rows at once and share their Q / dO in L2; with tile order (a tile's
-// items together, widest tile first) they walk a dozen windows at once on the
-// 48K rollout tree. Smaller trees keep tile order, which balances their few
-// long items better. Run by a whole workgroup of 1024 threads once kb_base is
-// final; n_items = kb_base[n_kb]. Header int32 7: 1 when window-major.
-constexpr int kWindowMajorItems = 512;
+// rank, chunk) pairs. Up to kSortItems items: longest item first (its query
+// range), ties by query window from the top, then by tile rank: the longest
+// items start first (a longest-processing-time schedule over the resident
+// workgroups), and the workgroups of an XCD (one kv head's items) that start
+// together walk the same query window and share its Q / dO in L2. Sorted as
+// packed 64-bit keys, a bitonic sort in LDS. Above kSortItems (trees of
+// hundreds of thousands of tokens) the list is window-major: every key tile's
+// item of the top window, then the next window down, each window's items in
+// tile order. Run by a whole workgroup of 1024 threads once kb_base is final;
+// n_items = kb_base[n_kb]. Header int32 7: 1 sorted by length, 2 window-major.
+constexpr int kSortItems = 4096;
 __device__ __forceinline__ void plan_item_list(const int32_t* __restrict__ kb_qlo,
                                                const int32_t* __restrict__ kb_qhi,
                                                const int32_t* __restrict__ kb_order,
                                                const int32_t* __restrict__ kb_base, int n_kb, int n_q, int qch,
                                                int2* __restrict__ kb_item, uint8_t* __restrict__ plan) {
+    __shared__ unsigned long long s_key[kSortItems];
     __shared__ int s_w[16];
     __shared__ int s_c;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const bool wm = kb_base[n_kb] >= kWindowMajorItems;
-    if (!wm) {
+    const int n_items = kb_base[n_kb];
+    if (n_items <= kSortItems) {
+        // key: (4096 - length) | (4095 - window) | rank | chunk, 13 + 12 + 12 + 12 bits
+        // (n_kb <= n_items, and the windows number at most n_q / 256 + 1 <= n_items / 2 + 1)
+        int n = 1;
+        while (n < n_items) n <<= 1;
+        for (int i = tid; i < n; i += 1024) s_key[i] = ~0ull;
+        __syncthreads();
         for (int r = tid; r < n_kb; r += 1024) {
-            const int b = kb_base[r], m = kb_base[r + 1] - b;
-            for (int c = 0; c < m; ++c) kb_item[b + c] = make_int2(r, c);
+            const int kb = kb_order[r], lo = kb_qlo[kb], hi = kb_qhi[kb], b = kb_base[r];
+            const int m = tt_kb_items(lo, hi, qch);
+            for (int c = 0; c < m; ++c) {
+                int q0, q1;
+                tt_kb_item_range(lo, hi, qch, c, q0, q1);
+                const int len = min(max(q1 - q0, 0), 4096);
+                const int w = min(m > 1 ? lo / qch + c : (hi > lo ? (hi - 1) / qch : 0), 4095);
+                s_key[b + c] = ((unsigned long long)(4096 - len) << 36) | ((unsigned long long)(4095 - w) << 24) |
+                               ((unsigned long long)r << 12) | (unsigned long long)c;
+            }
+        }
+        __syncthreads();
+        for (int k = 2; k <= n; k <<= 1)
+            for (int j = k >> 1; j > 0; j >>= 1) {
+                for (int i = tid; i < n; i += 1024) {
+                    const int p = i ^ j;
+                    if (p > i) {
+                        const unsigned long long x = s_key[i], y = s_key[p];
+                        if ((x > y) == ((i & k) == 0)) {
+                            s_key[i] = y;
+                            s_key[p] = x;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        for (int i = tid; i < n_items; i += 1024) {
+            const unsigned long long key = s_key[i];
+            kb_item[i] = make_int2((int)((key >> 12) & 4095), (int)(key & 4095));
         }
     } else {
         if (tid == 0) s_c = 0;
@@ -497,7 +532,7 @@ __device__ __forceinline__ void plan_item_list(const int32_t* __restrict__ kb_ql
             }
         }
     }
-    if (tid == 0) reinterpret_cast<int32_t*>(plan)[7] = wm ? 1 : 0;
+    if (tid == 0) reinterpret_cast<int32_t*>(plan)[7] = n_items <= kSortItems ? 1 : 2;
 }
 
 // Plan pass 4: the dK/dV work-item offsets of the ordered key tiles, then the
