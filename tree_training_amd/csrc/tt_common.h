@@ -83,8 +83,8 @@ __host__ __device__ inline void tt_kb_item_range(int qlo, int qhi, int qch, int 
 
 // Plan buffer layout. Header (bytes): [0,8) uint64 visible pairs per head;
 // int32 at 8: n_qb, 12: n_kt, 16: n_kb, 20: n_items (dK/dV work items), 24:
-// n_split (key tiles of more than one work item), 28: 1 when kb_item is
-// window-major.
+// n_split (key tiles of more than one work item), 28: kb_item's order (1:
+// longest item first, ties by query window; 2: window-major).
 // Then int32 arrays:
 //   row_cnt[n_qb]           non-empty key tiles per query block
 //   row_order[n_qb]         query blocks by decreasing tile count
